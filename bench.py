@@ -1,0 +1,238 @@
+"""Decode benchmark of the quantised-MoE hot path on one MI355X.
+
+Workload (one decode step = one token through one routed MoE block at
+Qwen3-30B-A3B shape): D 2048, 128 experts, top-8 softmax routing with
+renormalisation, expert width 768, Q6_K experts, f32 router, batch 1.  Each
+token has its own seeded N(0,1) residual.  To keep "HBM GB/s" honest the
+tokens cycle through --layers distinct copies of the layer's 128 experts
+(48 copies = the 23.8 GB of Q6_K experts a 48-layer model keeps resident), so
+consecutive tokens never re-read an expert from the 256 MB last-level cache.
+
+Timed region: K tokens launched back to back on one stream (HIP graphs of up
+to --graph tokens, replayed), bracketed by synchronisation.  value = tokens/s.
+
+roofline: the dominant kernel is the gate/up launch (phase 2).  Its average
+duration is measured with HIP events around each launch over
+--roofline-tokens tokens; algorithmic bytes per launch = top-8 x (gate + up)
+packed Q6_K bytes = 8 x 2 x 1,290,240 = 20,643,840 B.
+
+cpu_baseline: the reference's own kernels (oracle/_ref, AVX-512 tier when the
+host has it) running the same block through ref_moe.c on the host cores, on a
+bounded sample of tokens over 128 distinct random-code experts.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+D, E, K, DE = 2048, 128, 8, 768
+Q6_K = 14
+MAT_BYTES = DE * D // 256 * 210          # one packed Q6_K matrix: 1,290,240 B
+EXPERT_BYTES = 3 * MAT_BYTES             # 3,870,720 B
+TOKEN_BYTES = K * EXPERT_BYTES           # 30,965,760 B per token-layer
+GATEUP_BYTES = K * 2 * MAT_BYTES         # 20,643,840 B per gate/up launch
+DOWN_BYTES = K * MAT_BYTES               # 10,321,920 B per down launch
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_weights(torch, dev, layers, seed):
+    """Random-code Q6_K experts already in the packed tile layout: random code
+    bytes, modest f16 block scales in each matrix's scale plane."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    n_mats = layers * E * 3
+    W = torch.empty((n_mats, MAT_BYTES), dtype=torch.uint8, device=dev)
+    units = MAT_BYTES - (MAT_BYTES // 210) * 2          # 208-byte units, then the f16 scale plane
+    chunk = 256
+    for m0 in range(0, n_mats, chunk):
+        m1 = min(n_mats, m0 + chunk)
+        W[m0:m1].random_(0, 256, generator=g)
+        d = (torch.randn((m1 - m0, (MAT_BYTES - units) // 2), generator=g, device=dev) * 2e-3).to(torch.float16)
+        W[m0:m1, units:] = d.view(torch.uint8)
+    return W
+
+
+def cpu_baseline(args, threads):
+    """Reference kernels on the host (oracle/_ref), bounded sample."""
+    import numpy as np
+
+    import oracle
+    from tests.synth import random_code_rows
+    if oracle.ref is None:
+        return None
+    rng = np.random.default_rng(3)
+    experts = []
+    for _ in range(E):
+        experts.append((random_code_rows(rng, Q6_K, DE, D), random_code_rows(rng, Q6_K, DE, D),
+                        random_code_rows(rng, Q6_K, D, DE)))
+    host = oracle.MoeHost(D=D, de=DE, E=E, k=K, expert_dt=Q6_K, ffn_norm=np.ones(D, np.float32),
+                          router_w=(rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32), experts=experts)
+    hs = rng.standard_normal((64, D)).astype(np.float32)
+    out = {}
+    for nthr in sorted({1, threads}):
+        handle = oracle.ref.refmoe_new(nthr)
+        host.run_ref(handle, hs[0])            # warm
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < args.cpu_seconds / 2 or n < 8:
+            host.run_ref(handle, hs[n % 64])
+            n += 1
+        dt = time.perf_counter() - t0
+        oracle.ref.refmoe_free(handle)
+        out[nthr] = (n / dt, n)
+    tier = oracle.ref.refmoe_tier().decode()
+    best = out[threads]
+    return {"value": round(best[0], 2), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"{best[1]} tokens of the same block (128 distinct random-code Q6_K experts, 495 MB) "
+                      f"through the reference's {tier} tier + pool on {threads} threads",
+            "single_thread_tok_s": round(out[1][0], 2), "gpu_over_cpu": None}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10000, help="timed tokens")
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--layers", type=int, default=48, help="distinct layer copies cycled by the tokens")
+    ap.add_argument("--graph", type=int, default=100, help="tokens per captured HIP graph (0 = eager launches)")
+    ap.add_argument("--roofline-tokens", type=int, default=1000)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
+              "multi-GPU runs are not part of it", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import tierlm_amd
+    from tierlm_amd import MoeBlock
+    from tierlm_amd import quant as hq
+
+    dev = torch.device("cuda", 0)
+    hq.init(0)
+    assert hq.selftest_failures() == 0, "HIP self-test failures"
+    L = args.layers
+    log(f"bench: allocating {L} x {E} Q6_K experts ({L * E * EXPERT_BYTES / 1e9:.1f} GB)")
+    W = make_weights(torch, dev, L, seed=1)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    router_w = torch.randn((E, D), generator=gen, device=dev) / float(np.sqrt(D))
+    ffn_norm = torch.ones(D, device=dev)
+    blocks = []
+    base = W.data_ptr()
+    for layer in range(L):
+        ptrs = [base + ((layer * E + e) * 3 + j) * MAT_BYTES for e in range(E) for j in range(3)]
+        blocks.append(MoeBlock(D=D, de=DE, E=E, k=K, expert_dt=Q6_K, ffn_norm=ffn_norm, router_w=router_w,
+                               expert_ptrs=ptrs, router=0, eps=1e-6, device=dev))
+    total = args.warmup + args.steps
+    H = torch.randn((max(total, args.roofline_tokens), D), generator=gen, device=dev)
+    torch.cuda.synchronize()
+
+    def run_tokens(t0, t1):
+        for t in range(t0, t1):
+            blocks[t % L](H[t])
+
+    graphs = []
+    if args.graph > 0:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            run_tokens(0, min(args.graph, total))          # warm the launch path before capture
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+
+        def capture(t0, t1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                run_tokens(t0, t1)
+            return g
+        G = args.graph
+        warm_chunks = [(t, min(t + G, args.warmup)) for t in range(0, args.warmup, G)]
+        timed_chunks = [(t, min(t + G, total)) for t in range(args.warmup, total, G)]
+        log(f"bench: capturing {len(warm_chunks) + len(timed_chunks)} graphs of <= {G} tokens")
+        warm_graphs = [capture(*c) for c in warm_chunks]
+        graphs = [capture(*c) for c in timed_chunks]
+        torch.cuda.synchronize()
+        for g in warm_graphs:
+            g.replay()
+    else:
+        run_tokens(0, args.warmup)
+    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    if graphs:
+        for g in graphs:
+            g.replay()
+    else:
+        run_tokens(args.warmup, total)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tok_s = args.steps / elapsed
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    # roofline pass: HIP events around each launch, eager, same token stream pattern
+    R = args.roofline_tokens
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(R)]
+    Hr = torch.randn((R, D), generator=gen, device=dev)
+    torch.cuda.synchronize()
+    for t in range(R):
+        b, h = blocks[t % L], Hr[t]
+        ev[t][0].record()
+        b.phase(1, h)
+        ev[t][1].record()
+        b.phase(2, h)
+        ev[t][2].record()
+        b.phase(3, h)
+        ev[t][3].record()
+    torch.cuda.synchronize()
+    ph = np.array([[ev[t][i].elapsed_time(ev[t][i + 1]) for i in range(3)] for t in range(R)]) * 1e3  # us
+    skip = min(20, R // 10)
+    p1, p2, p3 = (float(np.mean(ph[skip:, i])) for i in range(3))
+    gu_gbs = GATEUP_BYTES / (p2 * 1e-6) / 1e9
+    dn_gbs = DOWN_BYTES / (p3 * 1e-6) / 1e9
+    expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
+    log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); phases router {p1:.2f} us, "
+        f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down {p3:.2f} us ({dn_gbs:.0f} GB/s)")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        log(f"bench: cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(args, threads)
+        if cpu:
+            cpu["gpu_over_cpu"] = round(tok_s / cpu["value"], 1)
+
+    line = {
+        "metric": "decode tok/s batch-1, Qwen3-30B-A3B shape; expert GEMV HBM GB/s vs peak",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8xu6->int32 (Q6_K x Q8_K), f32 chain", "data": "synthetic",
+        "config": {"workload": "single routed MoE block at Qwen3-30B-A3B shape (D 2048, 128 experts top-8 softmax+renorm, "
+                               "expert width 768, Q6_K random-code experts, f32 router), batch-1 decode, "
+                               f"one token per step, {L} resident layer copies cycled",
+                   "tokens_timed": args.steps, "graph_tokens": args.graph, "layers_resident": L,
+                   "expert_bytes_per_token": TOKEN_BYTES},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_moe_gateup (gate+up of top-8 experts, SwiGLU, h quantisation)",
+                     "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(p2, 3),
+                     "down_kernel_GBps": round(dn_gbs, 1), "down_avg_launch_us": round(p3, 3),
+                     "router_avg_launch_us": round(p1, 3),
+                     "expert_gemv_GBps": round(expert_gbs, 1), "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

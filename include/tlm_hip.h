@@ -1,0 +1,177 @@
+/* tlm_hip.h - HIP (gfx950 / MI355X) kernel tier for tierlm's quantised-MoE
+ * decode path, behind a plain C ABI.
+ *
+ * Conventions shared with the reference library:
+ *   - dtype codes are tlm_dtype values (src/lib/tlm_quant.h:31-42):
+ *     F32 0, Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14, Q8_K 15;
+ *   - fallible calls return 0 or a negative TLM_E* code
+ *     (src/lib/tlm_platform.h:24-35) and leave a message for
+ *     tlm_hip_errmsg(), thread-local like tlm_errmsg();
+ *   - numerics follow src/lib/tlm_quant.h:113-128: exact int32 block sums and
+ *     one fmaf per block (two for Q4_K/Q5_K) in ascending block order from +0,
+ *     so every integer-format result has the bits of the reference's scalar
+ *     kernel.
+ *
+ * Pointers named *_dev, W, act, y, x, h, ids, w, workspace are device
+ * pointers (hipMalloc'd or from any allocator of the same device); `stream`
+ * is a hipStream_t passed as void* (NULL = the null stream).  Calls enqueue
+ * work and return; results are ready after tlm_hip_sync(stream).  No entry
+ * point allocates device memory except tlm_hip_malloc and tlm_hip_init (which
+ * sizes the staging area behind tlm_kern_hip_fill's host-pointer entries).
+ *
+ * Threading: one caller thread per stream.  The host-pointer entries of
+ * tlm_kern_hip_fill are serialised internally, so pool workers may call them
+ * concurrently.
+ */
+#ifndef TLM_HIP_H
+#define TLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TLM_HIP_OK = 0, TLM_HIP_EIO = -1, TLM_HIP_ENOMEM = -2, TLM_HIP_EINVAL = -3,
+    TLM_HIP_EFORMAT = -4, TLM_HIP_ERANGE = -5, TLM_HIP_ENOTFOUND = -6,
+    TLM_HIP_EUNSUP = -7, TLM_HIP_EBUSY = -8
+};
+
+/* ---- lifetime / tier ----------------------------------------------------
+ * tlm_hip_init replaces tlm_quant_init (src/lib/tlm_quant.c:1069-1088) for the
+ * hip tier: it selects `device`, allocates the staging area, and runs the
+ * start-up self-test of every HIP kernel against the library's built-in
+ * scalar rule on fixed data (src/lib/tlm_quant.c:950-1056).  A kernel that
+ * fails is counted and its dtype is refused by the host-pointer tier entries.
+ * Idempotent for the same device.  TLM_HIP_EUNSUP when no GPU is present. */
+int         tlm_hip_init(int device);
+void        tlm_hip_shutdown(void);
+/* "hip" after a successful init, else "none" (src/lib/tlm_quant.h:87-88). */
+const char *tlm_hip_tier(void);
+/* src/lib/tlm_quant.h:131-134 */
+int         tlm_hip_selftest_failures(void);
+/* src/lib/tlm_platform.h:36 (thread-local message of the last failure) */
+const char *tlm_hip_errmsg(void);
+
+/* ---- device memory (the reference's tlm_alloc_aligned,
+ *      src/lib/tlm_platform.h:55-56, for device buffers) ------------------ */
+int tlm_hip_malloc(void **dptr, size_t bytes);
+int tlm_hip_free(void *dptr);
+int tlm_hip_memcpy_h2d(void *dst_dev, const void *src_host, size_t bytes, void *stream);
+int tlm_hip_memcpy_d2h(void *dst_host, const void *src_dev, size_t bytes, void *stream);
+int tlm_hip_sync(void *stream);
+
+/* ---- activations --------------------------------------------------------
+ * src/lib/tlm_quant.h:71-74 / src/lib/tlm_quant.c:689-707, on device memory:
+ * kind TLM Q8_K (292-byte blocks), Q8_0 (36-byte a8 blocks) or F32 (copy).
+ * dst must be 4-byte aligned and tlm_hip_qact_bytes(kind, n) long. */
+size_t tlm_hip_qact_bytes(int kind, int64_t n);
+int    tlm_hip_quantize_act(int kind, const float *x, int64_t n, void *dst, void *stream);
+
+/* ---- matvec on the reference byte layout --------------------------------
+ * src/lib/tlm_quant.h:76-85: y[r] = dot(W row r, act) for r in [r0, r1),
+ * W row-major with stride row_bytes, any base byte offset.  A bad dtype or n
+ * NaN-fills y[r0..r1) on device and returns TLM_HIP_EINVAL. */
+int tlm_hip_matvec_rows(int dt, const void *W, size_t row_bytes, const void *act, float *y,
+                        int64_t n, int64_t r0, int64_t r1, void *stream);
+
+/* ---- packed (tile) layout for device-resident weights -------------------
+ * The packet payload stays in the reference's byte layout on disk and in host
+ * RAM (src/lib/tlm_store.h:10-11); after it reaches HBM it is packed once into
+ * a tile layout whose every load is a 16-byte aligned vector load.  Packing
+ * keeps every byte (no padding beyond the last 16-row tile) and is
+ * bit-preserving, so the packed GEMV returns the reference's bits.
+ * Q4_K and Q5_K blocks are already 16-byte aligned: their packed layout is the
+ * plain layout with tightly packed rows. */
+size_t tlm_hip_packed_bytes(int dt, int64_t rows, int64_t n);
+int    tlm_hip_pack(int dt, const void *src, size_t row_bytes, int64_t rows, int64_t n,
+                    void *dst, void *stream);
+/* y[0..rows) for a packed matrix (one launch). */
+int    tlm_hip_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const void *act,
+                             float *y, void *stream);
+
+/* ---- segment job: several matvecs in one launch --------------------------
+ * Mirrors mv_job / mv_exec (src/lib/tlm_model.c:175-222): every output row is
+ * computed by exactly one work-group, so batching never changes a bit. */
+typedef struct {
+    int32_t     dt;        /* weight dtype */
+    int32_t     packed;    /* 1 = tlm_hip_pack layout, 0 = plain rows (row_bytes) */
+    const void *W;
+    uint64_t    row_bytes; /* plain layout only */
+    const void *act;       /* tlm_hip_quantize_act output of the dtype's kind */
+    float      *y;
+    int64_t     n, rows;
+} tlm_hip_seg;
+#define TLM_HIP_MAX_SEGS 136   /* MAX_SEGS, src/lib/tlm_model.c:41-42 */
+int tlm_hip_mv_job(const tlm_hip_seg *segs, int nseg, void *stream);
+
+/* ---- one routed MoE block ------------------------------------------------
+ * src/lib/tlm_model.c:940-1055 (with run_batch :900-938, route :798-839):
+ *   xb = rmsnorm(h, ffn_norm); logits = router xb; (ids, w) = route(logits);
+ *   for each rank r: h_r = silu(gate_r xb) * (up_r xb); eo_r = down_r h_r;
+ *   ffn = sum_r w_r * eo_r in ascending rank order (+ shared expert);
+ *   h += ffn.
+ * Every expert is resident (packed) in HBM: experts[3*e + {0,1,2}] point to
+ * expert e's packed gate [de x D], up [de x D] and down [D x de].
+ * Numerics: router logits, integer block sums, gate/up/down rows, the
+ * activation quantisation and the combine order are the reference's; silu /
+ * softmax use the device expf and rmsnorm sums squares in double in a tree,
+ * so those stages agree with the reference to ~1 ulp. */
+typedef struct {
+    int64_t D, de, ds;         /* d_model, expert width, shared width (0 = none) */
+    int32_t E, k, router;      /* experts, top-k (<= 32), router kind 0/1/2 */
+    float   routed_scale, eps;
+    int32_t expert_dt, shared_dt;
+    const float   *ffn_norm;         /* [D] */
+    const float   *router_w;         /* [E x D] f32 rows */
+    const float   *router_bias;      /* [E] or NULL */
+    const uint8_t *mask;             /* [E] 1 = pruned, or NULL */
+    const void *const *experts;      /* device array of 3*E packed matrix pointers */
+    const void *sg, *su, *sd;        /* packed shared gate/up [ds x D], down [D x ds] */
+    const float   *shared_gate_inp;  /* [D] or NULL */
+} tlm_hip_moe_desc;
+
+/* Bytes of caller-owned device workspace one layer call needs. */
+size_t tlm_hip_moe_workspace_bytes(const tlm_hip_moe_desc *d);
+/* h[D] += MoE(h).  ids[k] / w[k] (device, may be NULL) receive the routing.
+ * workspace: tlm_hip_moe_workspace_bytes(d) bytes, 256-byte aligned; calls
+ * on different streams need different workspaces. */
+int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w,
+                      void *workspace, void *stream);
+/* The same block as its launches, one per call, for callers that interleave
+ * other work or time each launch (the reference's moe() is likewise route,
+ * then the gate/up job, then the down job + combine, src/lib/tlm_model.c:972,
+ * 921, 937-1050):
+ *   phase 1: rmsnorm + router logits (+ activation quantisation)
+ *   phase 2: routing + gate/up + SwiGLU + h quantisation
+ *   phase 3: down + rank-order combine + residual update.
+ * Phases must run in order on one stream.  Re-running phase 2 reproduces the
+ * same bits; re-running phase 3 adds the FFN output to h once more. */
+int tlm_hip_moe_layer_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w,
+                            void *workspace, void *stream);
+
+/* ---- reference tier ABI --------------------------------------------------
+ * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a
+ * name and two tables of TLM_QK_COUNT = 10 function pointers indexed F32,
+ * F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K, MXFP4, FP8, Q8_K).  tlm_kern_hip_fill
+ * overwrites the F32, Q8_0, Q4_K, Q5_K, Q6_K and Q8_K entries with
+ * host-pointer kernels that stage through device memory and returns how many
+ * entries it filled; 0 when tlm_hip_init has not succeeded.  This is the
+ * correctness / self-test path; the device-resident calls above are the fast
+ * path. */
+typedef float (*tlm_hip_qdot_fn)(const void *wrow, const void *act, int64_t n, const float *aux);
+typedef void  (*tlm_hip_qmv_fn)(const void *W, size_t row_bytes, const void *act, float *y,
+                                int64_t n, int64_t nrows);
+typedef struct {
+    const char     *name;
+    tlm_hip_qdot_fn dot[10];
+    tlm_hip_qmv_fn  mv[10];
+} tlm_hip_quant_kernels;
+int tlm_kern_hip_fill(tlm_hip_quant_kernels *k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,101 @@
+"""The C-ABI library loads and exports every function include/tlm_hip.h
+declares, and the ctypes structure layouts equal the C compiler's (no GPU
+compute calls here)."""
+import ctypes as C
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HDR = os.path.join(ROOT, "include", "tlm_hip.h")
+
+
+def declared_functions():
+    src = open(HDR).read()
+    src = re.sub(r"/\*.*?\*/", " ", src, flags=re.S)
+    names = re.findall(r"\b(tlm_\w+)\s*\(", src)
+    typedefs = set(re.findall(r"\(\*\s*(tlm_\w+)\)", src))
+    return sorted(set(names) - typedefs)
+
+
+def test_library_exports_every_declared_symbol():
+    from tierlm_amd import lib
+    out = subprocess.run(["nm", "-D", "--defined-only", lib._name], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (\w+)$", out, flags=re.M))
+    decl = declared_functions()
+    assert len(decl) >= 20
+    missing = [n for n in decl if n not in exported]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header():
+    from tierlm_amd import EXPORTS
+    assert sorted(EXPORTS) == declared_functions()
+
+
+def test_struct_layouts_match_c():
+    from tierlm_amd._lib import MoeDesc, QuantKernels, Seg
+    prog = r'''
+#include <stdio.h>
+#include <stddef.h>
+#include "tlm_hip.h"
+#define O(T, f) printf(#T "." #f " %zu\n", offsetof(T, f))
+int main(void) {
+  printf("seg %zu\nmoe %zu\nqk %zu\n", sizeof(tlm_hip_seg), sizeof(tlm_hip_moe_desc), sizeof(tlm_hip_quant_kernels));
+  O(tlm_hip_seg, W); O(tlm_hip_seg, row_bytes); O(tlm_hip_seg, act); O(tlm_hip_seg, y); O(tlm_hip_seg, rows);
+  O(tlm_hip_moe_desc, E); O(tlm_hip_moe_desc, routed_scale); O(tlm_hip_moe_desc, expert_dt);
+  O(tlm_hip_moe_desc, ffn_norm); O(tlm_hip_moe_desc, experts); O(tlm_hip_moe_desc, shared_gate_inp);
+  O(tlm_hip_quant_kernels, dot); O(tlm_hip_quant_kernels, mv);
+  return 0;
+}'''
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "p.c")
+        open(c, "w").write(prog)
+        exe = os.path.join(d, "p")
+        subprocess.run(["gcc", "-std=c11", "-I" + os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        vals = dict(line.rsplit(" ", 1) for line in subprocess.run([exe], capture_output=True, text=True,
+                                                                   check=True).stdout.splitlines())
+    vals = {k: int(v) for k, v in vals.items()}
+    assert vals["seg"] == C.sizeof(Seg)
+    assert vals["moe"] == C.sizeof(MoeDesc)
+    assert vals["qk"] == C.sizeof(QuantKernels)
+    for k, v in vals.items():
+        if "." not in k:
+            continue
+        t, f = k.split(".")
+        cls = {"tlm_hip_seg": Seg, "tlm_hip_moe_desc": MoeDesc, "tlm_hip_quant_kernels": QuantKernels}[t]
+        assert getattr(cls, f).offset == v, k
+
+
+def test_tier_before_init_and_without_gpu():
+    """Without a device the tier stays "none" and fill reports 0 entries."""
+    import torch
+
+    from tierlm_amd import lib, quant
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert quant.tier() == "none"
+    k, got = quant.kernel_table()
+    assert got == 0
+    assert lib.tlm_hip_init(0) == -7          # TLM_EUNSUP: no HIP device
+    assert b"no HIP device" in lib.tlm_hip_errmsg()
+
+
+def test_host_checks_reject_bad_arguments_without_launching():
+    """Argument validation happens on the host, before any launch."""
+    from tierlm_amd import lib
+    from tierlm_amd._lib import MoeDesc
+    d = MoeDesc()
+    d.E, d.k, d.D, d.de = 0, 8, 2048, 768
+    assert lib.tlm_hip_moe_layer(C.byref(d), C.c_void_p(16), None, None, C.c_void_p(256), None) == -3
+    assert lib.tlm_hip_moe_layer_phase(C.byref(d), 4, C.c_void_p(16), None, None, C.c_void_p(256), None) == -3
+    assert lib.tlm_hip_packed_bytes(14, 768, 2048) == 768 * 8 * 210
+    assert lib.tlm_hip_packed_bytes(14, 37, 256) == 48 * 210        # last tile padded to 16 rows
+    assert lib.tlm_hip_packed_bytes(14, 16, 100) == 0
+    assert lib.tlm_hip_qact_bytes(15, 257) == 584
+    assert lib.tlm_hip_qact_bytes(8, 33) == 72
+    assert lib.tlm_hip_quantize_act(15, None, 256, None, None) == -3
+    assert lib.tlm_hip_quantize_act(15, None, 0, None, None) == 0     # n <= 0 is a no-op

@@ -1,0 +1,88 @@
+"""ctypes binding of libtlm_hip.so (include/tlm_hip.h).
+
+The library is the product: nothing in this package computes a result on the
+CPU.  Importing fails with a clear error when the library has not been built
+(``python -c "import __graft_entry__ as g; g.build()"``).
+"""
+import ctypes as C
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtlm_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"tierlm_amd: {LIB_PATH} is not built; run __graft_entry__.build() "
+        "(hipcc --offload-arch=gfx950) first")
+
+lib = C.CDLL(LIB_PATH)
+
+vp, i32, i64, sz, f32 = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
+
+
+class Seg(C.Structure):
+    """tlm_hip_seg"""
+    _fields_ = [("dt", C.c_int32), ("packed", C.c_int32), ("W", vp), ("row_bytes", C.c_uint64),
+                ("act", vp), ("y", vp), ("n", C.c_int64), ("rows", C.c_int64)]
+
+
+class MoeDesc(C.Structure):
+    """tlm_hip_moe_desc"""
+    _fields_ = [("D", C.c_int64), ("de", C.c_int64), ("ds", C.c_int64),
+                ("E", C.c_int32), ("k", C.c_int32), ("router", C.c_int32),
+                ("routed_scale", C.c_float), ("eps", C.c_float),
+                ("expert_dt", C.c_int32), ("shared_dt", C.c_int32),
+                ("ffn_norm", vp), ("router_w", vp), ("router_bias", vp), ("mask", vp),
+                ("experts", vp), ("sg", vp), ("su", vp), ("sd", vp), ("shared_gate_inp", vp)]
+
+
+QDOT = C.CFUNCTYPE(C.c_float, vp, vp, C.c_int64, vp)
+QMV = C.CFUNCTYPE(None, vp, C.c_size_t, vp, vp, C.c_int64, C.c_int64)
+
+
+class QuantKernels(C.Structure):
+    """tlm_hip_quant_kernels (layout of the reference's tlm_quant_kernels)."""
+    _fields_ = [("name", C.c_char_p), ("dot", QDOT * 10), ("mv", QMV * 10)]
+
+
+_SIGS = {
+    "tlm_hip_init": (i32, [i32]),
+    "tlm_hip_shutdown": (None, []),
+    "tlm_hip_tier": (C.c_char_p, []),
+    "tlm_hip_selftest_failures": (i32, []),
+    "tlm_hip_errmsg": (C.c_char_p, []),
+    "tlm_hip_malloc": (i32, [C.POINTER(vp), sz]),
+    "tlm_hip_free": (i32, [vp]),
+    "tlm_hip_memcpy_h2d": (i32, [vp, vp, sz, vp]),
+    "tlm_hip_memcpy_d2h": (i32, [vp, vp, sz, vp]),
+    "tlm_hip_sync": (i32, [vp]),
+    "tlm_hip_qact_bytes": (sz, [i32, i64]),
+    "tlm_hip_quantize_act": (i32, [i32, vp, i64, vp, vp]),
+    "tlm_hip_matvec_rows": (i32, [i32, vp, sz, vp, vp, i64, i64, i64, vp]),
+    "tlm_hip_packed_bytes": (sz, [i32, i64, i64]),
+    "tlm_hip_pack": (i32, [i32, vp, sz, i64, i64, vp, vp]),
+    "tlm_hip_matvec_packed": (i32, [i32, vp, i64, i64, vp, vp, vp]),
+    "tlm_hip_mv_job": (i32, [C.POINTER(Seg), i32, vp]),
+    "tlm_hip_moe_workspace_bytes": (sz, [C.POINTER(MoeDesc)]),
+    "tlm_hip_moe_layer": (i32, [C.POINTER(MoeDesc), vp, vp, vp, vp, vp]),
+    "tlm_hip_moe_layer_phase": (i32, [C.POINTER(MoeDesc), i32, vp, vp, vp, vp, vp]),
+    "tlm_kern_hip_fill": (i32, [C.POINTER(QuantKernels)]),
+}
+
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+EXPORTS = tuple(_SIGS)
+
+
+class HipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"tlm_hip error {code}: {msg}")
+        self.code = code
+
+
+def check(rc):
+    if rc != 0:
+        raise HipError(rc, (lib.tlm_hip_errmsg() or b"").decode(errors="replace"))
+    return rc

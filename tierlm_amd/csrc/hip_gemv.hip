@@ -1,0 +1,389 @@
+/* hip_gemv.hip - quantised GEMV (decode matvec) kernels for gfx950.
+ *
+ * Numerics (src/lib/tlm_quant.h:113-128): per (row, block) an exact int32
+ * isum (and msum for Q4_K/Q5_K); per row the float chain
+ *     acc = fmaf(d_w * d_a, (float)isum, acc)  [; acc = fmaf(-(dmin_w * d_a), (float)msum, acc)]
+ * over blocks in ascending order from +0, run by one thread.  Integer sums are
+ * order-free, so they are split over lanes freely; the float chain never is.
+ * F32 rows: lane i mod 32 accumulates with fmaf in element order, then the
+ * fixed reduce32 tree (src/lib/tlm_quant.c:721-738).
+ *
+ * Two layouts:
+ *   plain  - the reference's row-major bytes, any stride / base offset
+ *            (the drop-in tlm_matvec_rows path).  One lane per block,
+ *            byte-granular weight reads.
+ *   packed - tile layout produced on device by launch_pack (see
+ *            packed_bytes): rows grouped in tiles of 16; the tile's rows are
+ *            contiguous per block column, and the f16 scale of Q6_K / Q8_0
+ *            blocks moves to a side region so every remaining weight read is
+ *            a 16-byte aligned vector load.  This is the HBM-bandwidth path.
+ */
+#include "tlm_hip_internal.h"
+#include "tlm_hip_items.h"
+
+#include <math.h>
+
+namespace {
+
+/* ======================================================================
+ * plain layout
+ * ==================================================================== */
+__device__ __forceinline__ uint32_t ld_u8(const uint8_t *p) { return *p; }
+__device__ __forceinline__ uint32_t ld_u16u(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+/* Integer sums of one plain block (any alignment) against a 4-byte aligned
+ * activation block - the per-element rules of src/lib/tlm_quant.c:778-902. */
+template <int DT>
+__device__ void plain_block(const uint8_t *w, const uint8_t *a, int32_t &is, int32_t &ms) {
+    is = 0;
+    ms = 0;
+    const int8_t *x = (const int8_t *)(a + 4);
+    if constexpr (DT == DT_Q8_0) {
+        for (int i = 0; i < 32; i++) is += (int32_t)(int8_t)w[2 + i] * x[i];
+    } else if constexpr (DT == DT_Q8_K) {
+        for (int i = 0; i < 256; i++) is += (int32_t)(int8_t)w[4 + i] * x[i];
+    } else if constexpr (DT == DT_Q6_K) {
+        const int16_t *bs = (const int16_t *)(a + 260);
+        for (int g = 0; g < 16; g++) {
+            int32_t gs = 0;
+            for (int k = 0; k < 16; k++) {
+                int e = 16 * g + k, h = e >> 7, q = (e >> 5) & 3, l = e & 31;
+                uint32_t nib = w[64 * h + 32 * (q & 1) + l];
+                nib = (q & 2) ? (nib >> 4) : (nib & 15u);
+                uint32_t hi = (w[128 + 32 * h + l] >> (2 * q)) & 3u;
+                gs += (int32_t)(nib | (hi << 4)) * x[e];
+            }
+            is += (int32_t)(int8_t)w[192 + g] * (gs - 32 * (int32_t)bs[g]);
+        }
+    } else {   /* Q4_K / Q5_K */
+        constexpr bool Q5 = DT == DT_Q5_K;
+        const uint8_t *qs = w + (Q5 ? 48 : 16), *s12 = w + 4;
+        const int16_t *bs = (const int16_t *)(a + 260);
+        for (int sb = 0; sb < 8; sb++) {
+            int c = sb >> 1, hb = sb & 1;
+            uint32_t sc, mn;
+            if (sb < 4) { sc = s12[sb] & 63u; mn = s12[4 + sb] & 63u; }
+            else {
+                sc = (s12[sb + 4] & 15u) | ((uint32_t)(s12[sb - 4] >> 6) << 4);
+                mn = ((uint32_t)s12[sb + 4] >> 4) | ((uint32_t)(s12[sb] >> 6) << 4);
+            }
+            int32_t s = 0;
+            for (int l = 0; l < 32; l++) {
+                uint32_t code = hb ? (qs[32 * c + l] >> 4) : (qs[32 * c + l] & 15u);
+                if (Q5) code |= ((w[16 + l] >> (2 * c + hb)) & 1u) << 4;
+                s += (int32_t)code * x[32 * sb + l];
+            }
+            is += (int32_t)sc * s;
+            ms += (int32_t)mn * ((int32_t)bs[2 * sb] + (int32_t)bs[2 * sb + 1]);
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void plain_scales(const uint8_t *w, const uint8_t *a, float &dA, float &dM) {
+    float da = *(const float *)a;
+    if constexpr (DT == DT_Q6_K) { dA = f16_to_f32(ld_u16u(w + 208)) * da; dM = 0.0f; }
+    else if constexpr (DT == DT_Q8_0) { dA = f16_to_f32(ld_u16u(w)) * da; dM = 0.0f; }
+    else if constexpr (DT == DT_Q8_K) {
+        uint32_t u = ld_u16u(w) | (ld_u16u(w + 2) << 16);
+        dA = __uint_as_float(u) * da;
+        dM = 0.0f;
+    } else { dA = f16_to_f32(ld_u16u(w)) * da; dM = f16_to_f32(ld_u16u(w + 2)) * da; }
+}
+
+/* One wave per row, 4 rows per work-group.  Lanes take blocks lane, lane+64,
+ * ...; the chain runs in every lane (same values) over shuffled block results
+ * in ascending order. */
+template <int DT>
+__global__ __launch_bounds__(256) void k_mv_plain_int(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                      const uint8_t *__restrict__ act, float *__restrict__ y,
+                                                      int64_t n, int64_t r0, int64_t r1) {
+    constexpr int BV = DT == DT_Q8_0 ? 32 : 256;
+    constexpr int AB = DT == DT_Q8_0 ? 36 : 292;
+    constexpr int WB = DT == DT_Q8_0 ? 34 : DT == DT_Q4_K ? 144 : DT == DT_Q5_K ? 176 : DT == DT_Q6_K ? 210 : 292;
+    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = r0 + (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= r1) return;
+    const uint8_t *w = W + (size_t)row * row_bytes;
+    const int64_t nb = n / BV;
+    float acc = 0.0f;
+    for (int64_t base = 0; base < nb; base += 64) {
+        int64_t b = base + lane;
+        int32_t is = 0, ms = 0;
+        float dA = 0.0f, dM = 0.0f;
+        if (b < nb) {
+            plain_block<DT>(w + (size_t)b * WB, act + (size_t)b * AB, is, ms);
+            plain_scales<DT>(w + (size_t)b * WB, act + (size_t)b * AB, dA, dM);
+        }
+        float fis = (float)is, fms = (float)ms;
+        int cnt = (int)(nb - base < 64 ? nb - base : 64);
+        for (int j = 0; j < cnt; j++) {
+            acc = fmaf(__shfl(dA, j, 64), __shfl(fis, j, 64), acc);
+            if (AFF) acc = fmaf(-__shfl(dM, j, 64), __shfl(fms, j, 64), acc);
+        }
+    }
+    if (lane == 0) y[row] = acc;
+}
+
+/* F32 row dot with the reference lane order: lanes 0..31 of a half-wave own
+ * elements i = lane mod 32; two rows per wave, 8 rows per work-group. */
+template <bool ALIGNED>
+__global__ __launch_bounds__(256) void k_mv_f32(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                const float *__restrict__ x, float *__restrict__ y,
+                                                int64_t n, int64_t r0, int64_t r1) {
+    const int lane = threadIdx.x & 31;
+    const int64_t row = r0 + (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const bool live = row < r1;
+    float r = 0.0f;
+    if (live) {
+        const uint8_t *w = W + (size_t)row * row_bytes;
+        for (int64_t i = lane; i < n; i += 32) {
+            float wv;
+            if (ALIGNED) wv = ((const float *)w)[i];
+            else {
+                const uint8_t *p = w + 4 * i;
+                wv = __uint_as_float(ld_u16u(p) | (ld_u16u(p + 2) << 16));
+            }
+            r = fmaf(wv, x[i], r);
+        }
+    }
+    /* reduce32: s16[l] = r[l] + r[l+16]; s8; s4; (s4[0]+s4[2]) + (s4[1]+s4[3]) */
+    float s = r + __shfl_down(r, 16, 32);
+    s = s + __shfl_down(s, 8, 32);
+    s = s + __shfl_down(s, 4, 32);
+    float a = s + __shfl_down(s, 2, 32);           /* lane 0: s4[0] + s4[2]; lane 1: s4[1] + s4[3] */
+    float res = a + __shfl_down(a, 1, 32);
+    if (live && lane == 0) y[row] = res;
+}
+
+__global__ void k_nan_fill(float *y, int64_t count) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) y[i] = __uint_as_float(0x7FC00000u);
+}
+
+/* ======================================================================
+ * packed layout
+ *
+ *   T  = ceil(rows / 16) tiles, nb blocks per row, unit index
+ *        u(t, b, i) = (t * nb + b) * 16 + i    (i = row within the tile)
+ *   Q6_K: 208-byte unit ql|qh|sc at u*208; f16 d at T*nb*16*208 + u*2
+ *   Q8_0: 32-byte codes at u*32;            f16 d at T*nb*16*32  + u*2
+ *   Q4_K / Q5_K / Q8_K: whole block at u*block_bytes
+ *   F32: plain rows of n floats
+ * Rows past `rows` in the last tile are zero.
+ * ==================================================================== */
+__global__ void k_pack(int dt, const uint8_t *__restrict__ src, size_t row_bytes, int64_t rows, int nb,
+                       int64_t T, uint8_t *__restrict__ dst) {
+    int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   /* one thread per unit */
+    int64_t units = T * nb * TILE_ROWS;
+    if (u >= units) return;
+    int i = (int)(u % TILE_ROWS);
+    int64_t tb = u / TILE_ROWS;
+    int b = (int)(tb % nb);
+    int64_t t = tb / nb;
+    int64_t r = t * TILE_ROWS + i;
+    const int bb = dt_block_bytes(dt);
+    const uint8_t *s = r < rows ? src + (size_t)r * row_bytes + (size_t)b * bb : nullptr;
+    if (dt == DT_Q6_K) {
+        uint8_t *o = dst + u * 208;
+        for (int k = 0; k < 208; k++) o[k] = s ? s[k] : 0;
+        uint8_t *od = dst + units * 208 + u * 2;
+        od[0] = s ? s[208] : 0;
+        od[1] = s ? s[209] : 0;
+    } else if (dt == DT_Q8_0) {
+        uint8_t *o = dst + u * 32;
+        for (int k = 0; k < 32; k++) o[k] = s ? s[2 + k] : 0;
+        uint8_t *od = dst + units * 32 + u * 2;
+        od[0] = s ? s[0] : 0;
+        od[1] = s ? s[1] : 0;
+    } else {
+        uint8_t *o = dst + u * bb;
+        for (int k = 0; k < bb; k++) o[k] = s ? s[k] : 0;
+    }
+}
+
+__global__ void k_pack_f32(const uint8_t *__restrict__ src, size_t row_bytes, int64_t rows, int64_t n,
+                           float *__restrict__ dst) {
+    int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= rows * n) return;
+    int64_t r = e / n, c = e % n;
+    const uint8_t *p = src + (size_t)r * row_bytes + 4 * c;
+    dst[e] = __uint_as_float(ld_u16u(p) | (ld_u16u(p + 2) << 16));
+}
+
+}  // namespace
+
+/* ---- packed GEMV kernel --------------------------------------------------
+ * Work-group = 4 waves, one 16-row tile; block columns are chunked by NBC so
+ * LDS stays bounded for long rows.  Per chunk every wave computes items
+ * (b, i) with LPI lanes each and parks (isum, msum, dA, dM) in LDS; then 16
+ * threads extend their row's float chain over the chunk in block order.
+ * The activation is staged once per work-group (all blocks). */
+#define PK_NBC 64
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ Wp, int64_t rows, int nb,
+                                                   const uint8_t *__restrict__ act, float *__restrict__ y) {
+    using F = Packed<DT>;
+    constexpr int LPI = F::LPI, IPW = 64 / LPI;          /* items per wave pass */
+    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int kind = dt_act_kind(DT);
+    const XLds X = stage_act(kind, act, nb, lds);
+    const int cap = nb < PK_NBC ? nb : PK_NBC;
+    int32_t *l_is = (int32_t *)(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15));
+    int32_t *l_ms = l_is + cap * TILE_ROWS;
+    float *l_da = (float *)(l_ms + cap * TILE_ROWS);
+    float *l_dm = l_da + cap * TILE_ROWS;
+    __syncthreads();
+
+    const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS, t = blockIdx.x;
+    const int64_t units = T * nb * TILE_ROWS;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q = lane % LPI, slot = lane / LPI;
+    float acc = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += cap) {
+        const int nbc = nb - b0 < cap ? nb - b0 : cap;
+        const int nitems = nbc * TILE_ROWS;
+        for (int it = wave * IPW + slot; it - slot < nitems; it += 4 * IPW) {
+            const bool live = it < nitems;
+            const int bl = live ? it / TILE_ROWS : 0, i = it % TILE_ROWS, b = b0 + bl;
+            int32_t is = 0, ms = 0;
+            float dA = 0.0f, dM = 0.0f;
+            if (live) {
+                const int64_t u = ((int64_t)t * nb + b) * TILE_ROWS + i;
+                F::item(Wp, units, u, b, q, X, is, ms, dA, dM);
+                if (q == 0) {
+                    l_is[bl * TILE_ROWS + i] = is;
+                    l_da[bl * TILE_ROWS + i] = dA;
+                    if (AFF) { l_ms[bl * TILE_ROWS + i] = ms; l_dm[bl * TILE_ROWS + i] = dM; }
+                }
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < TILE_ROWS) {
+            const int i = threadIdx.x;
+            for (int bl = 0; bl < nbc; bl++) {
+                acc = fmaf(l_da[bl * TILE_ROWS + i], (float)l_is[bl * TILE_ROWS + i], acc);
+                if (AFF) acc = fmaf(-l_dm[bl * TILE_ROWS + i], (float)l_ms[bl * TILE_ROWS + i], acc);
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x < TILE_ROWS) {
+        const int64_t r = t * TILE_ROWS + threadIdx.x;
+        if (r < rows) y[r] = acc;
+    }
+}
+
+static size_t packed_lds_bytes(int dt, int nb) {
+    int cap = nb < PK_NBC ? nb : PK_NBC;
+    return ((stage_bytes(dt_act_kind(dt), nb) + 15) & ~(size_t)15) + (size_t)cap * TILE_ROWS * 16;
+}
+
+/* ======================================================================
+ * host launchers
+ * ==================================================================== */
+int launch_nan_fill(float *y, int64_t count, hipStream_t s) {
+    if (count <= 0) return TLM_HIP_OK;
+    hipLaunchKernelGGL(k_nan_fill, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, y, count);
+    return tlmh_check(hipGetLastError(), "nan_fill launch");
+}
+
+int launch_matvec_plain(int dt, const void *W, size_t row_bytes, const void *act, float *y, int64_t n,
+                        int64_t r0, int64_t r1, hipStream_t s) {
+    int bv = dt_block_values(dt);
+    if (bv == 0 || n < 0 || n % bv || (dt != DT_F32 && !dt_int_ok(dt))) {
+        if (y && r1 > r0) launch_nan_fill(y + r0, r1 - r0, s);
+        return tlmh_seterr(TLM_HIP_EINVAL, "matvec_rows: bad dtype %d or n=%lld", dt, (long long)n);
+    }
+    if (r1 <= r0) return TLM_HIP_OK;
+    if (!W || !act || !y) return tlmh_seterr(TLM_HIP_EINVAL, "matvec_rows: NULL pointer");
+    if ((uintptr_t)act & 3u) return tlmh_seterr(TLM_HIP_EINVAL, "matvec_rows: activation must be 4-byte aligned");
+    const uint8_t *w = (const uint8_t *)W;
+    const uint8_t *a = (const uint8_t *)act;
+    int64_t rows = r1 - r0;
+    if (dt == DT_F32) {
+        bool al = ((uintptr_t)W % 4 == 0) && (row_bytes % 4 == 0);
+        dim3 g((unsigned)((rows + 7) / 8));
+        if (al) hipLaunchKernelGGL(k_mv_f32<true>, g, dim3(256), 0, s, w, row_bytes, (const float *)a, y, n, r0, r1);
+        else hipLaunchKernelGGL(k_mv_f32<false>, g, dim3(256), 0, s, w, row_bytes, (const float *)a, y, n, r0, r1);
+        return tlmh_check(hipGetLastError(), "matvec f32 launch");
+    }
+    dim3 g((unsigned)((rows + 3) / 4)), blk(256);
+    switch (dt) {
+    case DT_Q8_0: hipLaunchKernelGGL(k_mv_plain_int<DT_Q8_0>, g, blk, 0, s, w, row_bytes, a, y, n, r0, r1); break;
+    case DT_Q4_K: hipLaunchKernelGGL(k_mv_plain_int<DT_Q4_K>, g, blk, 0, s, w, row_bytes, a, y, n, r0, r1); break;
+    case DT_Q5_K: hipLaunchKernelGGL(k_mv_plain_int<DT_Q5_K>, g, blk, 0, s, w, row_bytes, a, y, n, r0, r1); break;
+    case DT_Q6_K: hipLaunchKernelGGL(k_mv_plain_int<DT_Q6_K>, g, blk, 0, s, w, row_bytes, a, y, n, r0, r1); break;
+    case DT_Q8_K: hipLaunchKernelGGL(k_mv_plain_int<DT_Q8_K>, g, blk, 0, s, w, row_bytes, a, y, n, r0, r1); break;
+    }
+    return tlmh_check(hipGetLastError(), "matvec launch");
+}
+
+size_t packed_bytes(int dt, int64_t rows, int64_t n) {
+    int bv = dt_block_values(dt);
+    if (bv == 0 || rows < 0 || n < 0 || n % bv) return 0;
+    if (dt == DT_F32) return (size_t)rows * (size_t)n * 4;
+    if (!dt_int_ok(dt)) return 0;
+    int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    return (size_t)T * (size_t)(n / bv) * TILE_ROWS * (size_t)dt_block_bytes(dt);
+}
+
+int launch_pack(int dt, const void *src, size_t row_bytes, int64_t rows, int64_t n, void *dst, hipStream_t s) {
+    size_t pb = packed_bytes(dt, rows, n);
+    if (pb == 0 && rows > 0 && n > 0) return tlmh_seterr(TLM_HIP_EINVAL, "pack: bad dtype %d or n=%lld", dt, (long long)n);
+    if (pb == 0) return TLM_HIP_OK;
+    if (!src || !dst) return tlmh_seterr(TLM_HIP_EINVAL, "pack: NULL pointer");
+    if ((uintptr_t)dst & 15u) return tlmh_seterr(TLM_HIP_EINVAL, "pack: destination must be 16-byte aligned");
+    if (dt == DT_F32) {
+        int64_t e = rows * n;
+        hipLaunchKernelGGL(k_pack_f32, dim3((unsigned)((e + 255) / 256)), dim3(256), 0, s, (const uint8_t *)src,
+                           row_bytes, rows, n, (float *)dst);
+    } else {
+        int nb = (int)(n / dt_block_values(dt));
+        int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS, units = T * nb * TILE_ROWS;
+        hipLaunchKernelGGL(k_pack, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, dt, (const uint8_t *)src,
+                           row_bytes, rows, nb, T, (uint8_t *)dst);
+    }
+    return tlmh_check(hipGetLastError(), "pack launch");
+}
+
+int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, float *y, hipStream_t s) {
+    if (packed_bytes(dt, rows, n) == 0 && rows > 0 && n > 0)
+        return tlmh_seterr(TLM_HIP_EINVAL, "matvec_packed: bad dtype %d or n=%lld", dt, (long long)n);
+    if (rows <= 0) return TLM_HIP_OK;
+    if (!Wp || !act || !y) return tlmh_seterr(TLM_HIP_EINVAL, "matvec_packed: NULL pointer");
+    if ((uintptr_t)act & 3u) return tlmh_seterr(TLM_HIP_EINVAL, "matvec_packed: activation must be 4-byte aligned");
+    if (dt == DT_F32) return launch_matvec_plain(dt, Wp, (size_t)n * 4, act, y, n, 0, rows, s);
+    if ((uintptr_t)Wp & 15u) return tlmh_seterr(TLM_HIP_EINVAL, "matvec_packed: weights must be 16-byte aligned");
+    int nb = (int)(n / dt_block_values(dt));
+    if (stage_bytes(dt_act_kind(dt), nb) > 40 * 1024)
+        return tlmh_seterr(TLM_HIP_EUNSUP, "matvec_packed: n=%lld exceeds the staged-activation limit", (long long)n);
+    if (n == 0) return launch_matvec_plain(dt, Wp, 0, act, y, 0, 0, rows, s);
+    int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    size_t lds = packed_lds_bytes(dt, nb);
+    dim3 g((unsigned)T), blk(256);
+    const uint8_t *w = (const uint8_t *)Wp, *a = (const uint8_t *)act;
+    switch (dt) {
+    case DT_Q8_0: hipLaunchKernelGGL(k_mv_packed<DT_Q8_0>, g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q4_K: hipLaunchKernelGGL(k_mv_packed<DT_Q4_K>, g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q5_K: hipLaunchKernelGGL(k_mv_packed<DT_Q5_K>, g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q6_K: hipLaunchKernelGGL(k_mv_packed<DT_Q6_K>, g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q8_K: hipLaunchKernelGGL(k_mv_packed<DT_Q8_K>, g, blk, lds, s, w, rows, nb, a, y); break;
+    }
+    return tlmh_check(hipGetLastError(), "matvec_packed launch");
+}
+
+int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s) {
+    if (nseg < 0 || nseg > TLM_HIP_MAX_SEGS || (nseg > 0 && !segs))
+        return tlmh_seterr(TLM_HIP_EINVAL, "mv_job: bad segment count %d", nseg);
+    for (int i = 0; i < nseg; i++) {
+        const tlm_hip_seg *g = &segs[i];
+        int rc = g->packed ? launch_matvec_packed(g->dt, g->W, g->rows, g->n, g->act, g->y, s)
+                           : launch_matvec_plain(g->dt, g->W, (size_t)g->row_bytes, g->act, g->y, g->n, 0, g->rows, s);
+        if (rc) return rc;
+    }
+    return TLM_HIP_OK;
+}

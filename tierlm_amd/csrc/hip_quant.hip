@@ -1,0 +1,139 @@
+/* hip_quant.hip - activation quantisers on device (Q8_K and the 36-byte Q8_0
+ * activation "a8"), bit-exact with src/lib/tlm_quant.c:458-506.
+ *
+ * Q8_K: one wave64 per 256-value block, 4 values per lane.  amax is a wave
+ * max (order-free, exact); d = amax/127 and id = 127/amax are IEEE divisions;
+ * codes use the same magic-constant RNE; bsums are integer sums of 16 codes
+ * (4 lanes) - so every byte equals the reference's.
+ * a8: 8 lanes per 32-value block, 8 blocks per wave. */
+#include "tlm_hip_internal.h"
+
+#include <math.h>
+
+namespace {
+
+/* Flags and amax of the lanes in a group of `width` lanes (power of two,
+ * aligned); every lane of the group receives the result. */
+template <int WIDTH>
+__device__ __forceinline__ void group_amax(float &amax, int &nan, int &inf) {
+#pragma unroll
+    for (int m = 1; m < WIDTH; m <<= 1) {
+        float o = __shfl_xor(amax, m, 64);
+        amax = o > amax ? o : amax;
+        nan |= __shfl_xor(nan, m, 64);
+        inf |= __shfl_xor(inf, m, 64);
+    }
+}
+
+/* The shared per-block rule (src/lib/tlm_quant.c:458-478) for this lane's 4
+ * values; returns the block scale d and writes 4 codes packed in a dword. */
+template <int WIDTH>
+__device__ __forceinline__ float act_rule(const float v[4], const bool ok[4], uint32_t &codes) {
+    float amax = 0.0f;
+    int nan = 0, inf = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (!ok[j]) continue;
+        float a = fabsf(v[j]);
+        if (a != a) nan = 1;
+        else if (a == INFINITY) inf = 1;
+        else if (a > amax) amax = a;
+    }
+    group_amax<WIDTH>(amax, nan, inf);
+    codes = 0;
+    if (nan || inf) return nan ? __uint_as_float(0x7FC00000u) : INFINITY;
+    if (!(amax > 0.0f)) return 0.0f;
+    float d = amax / 127.0f;
+    if (amax >= 0x1p-100f) {
+        float id = 127.0f / amax;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (ok[j]) codes |= (uint32_t)(uint8_t)(int8_t)rne_clamp(v[j] * id, -127, 127) << (8 * j);
+    } else {
+        double id = 127.0 / (double)amax;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (ok[j]) codes |= (uint32_t)(uint8_t)(int8_t)rne_clamp((float)((double)v[j] * id), -127, 127) << (8 * j);
+    }
+    return d;
+}
+
+__device__ __forceinline__ int byte_sum(uint32_t c) {
+    return (int)(int8_t)(c & 0xFF) + (int)(int8_t)((c >> 8) & 0xFF) + (int)(int8_t)((c >> 16) & 0xFF) +
+           (int)(int8_t)(c >> 24);
+}
+
+/* grid: ceil(nblocks / 4) work-groups of 4 waves; one wave per block. */
+__global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int64_t n,
+                                                   uint8_t *__restrict__ dst, int64_t nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblocks) return;
+    float v[4];
+    bool ok[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int64_t i = b * 256 + 4 * lane + j;
+        ok[j] = i < n;
+        v[j] = ok[j] ? x[i] : 0.0f;
+    }
+    uint32_t codes;
+    float d = act_rule<64>(v, ok, codes);
+    uint8_t *blk = dst + b * 292;
+    if (lane == 0) *(float *)blk = d;
+    *(uint32_t *)(blk + 4 + 4 * lane) = codes;
+    int s = byte_sum(codes);
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((lane & 3) == 0) *(int16_t *)(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
+}
+
+/* grid: ceil(nblocks / 32) work-groups of 4 waves; 8 lanes per block. */
+__global__ __launch_bounds__(256) void k_quant_a8(const float *__restrict__ x, int64_t n,
+                                                  uint8_t *__restrict__ dst, int64_t nblocks) {
+    const int lane = threadIdx.x & 63, sub = lane & 7;
+    const int64_t b = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    /* every lane of a group of 8 takes part in the shuffles, so the group
+     * exits together */
+    const bool live = b < nblocks;
+    float v[4];
+    bool ok[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int64_t i = b * 32 + 4 * sub + j;
+        ok[j] = live && i < n;
+        v[j] = ok[j] ? x[i] : 0.0f;
+    }
+    uint32_t codes;
+    float d = act_rule<8>(v, ok, codes);
+    if (!live) return;
+    uint8_t *blk = dst + b * 36;
+    if (sub == 0) *(float *)blk = d;
+    *(uint32_t *)(blk + 4 + 4 * sub) = codes;
+}
+
+__global__ void k_copy_f32(const float *__restrict__ x, int64_t n, float *__restrict__ y) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = x[i];
+}
+
+}  // namespace
+
+int launch_quantize_act(int kind, const float *x, int64_t n, void *dst, hipStream_t s) {
+    if (n <= 0) return TLM_HIP_OK;   /* src/lib/tlm_quant.c:700 */
+    if (!x || !dst) return tlmh_seterr(TLM_HIP_EINVAL, "quantize_act: NULL pointer");
+    if (((uintptr_t)dst & 3u) || ((uintptr_t)x & 3u))
+        return tlmh_seterr(TLM_HIP_EINVAL, "quantize_act: x and dst must be 4-byte aligned");
+    if (kind == DT_Q8_K) {
+        int64_t nb = (n + 255) / 256;
+        hipLaunchKernelGGL(k_quant_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, n, (uint8_t *)dst, nb);
+    } else if (kind == DT_Q8_0) {
+        int64_t nb = (n + 31) / 32;
+        hipLaunchKernelGGL(k_quant_a8, dim3((unsigned)((nb + 31) / 32)), dim3(256), 0, s, x, n, (uint8_t *)dst, nb);
+    } else if (kind == DT_F32) {
+        hipLaunchKernelGGL(k_copy_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, (float *)dst);
+    } else {
+        return tlmh_seterr(TLM_HIP_EINVAL, "quantize_act: unsupported activation kind %d", kind);
+    }
+    return tlmh_check(hipGetLastError(), "quantize_act launch");
+}

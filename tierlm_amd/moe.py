@@ -1,0 +1,51 @@
+"""One routed MoE block on device (src/lib/tlm_model.c:940-1055) through
+tlm_hip_moe_layer.
+
+``MoeBlock`` owns nothing but the small device tables the C call needs (the
+packed-expert pointer table and the workspace); weights are device tensors
+the caller keeps alive.  Expert e's packed gate / up / down pointers sit at
+table entries 3e, 3e+1, 3e+2.
+"""
+import ctypes as C
+
+import torch
+
+from ._lib import MoeDesc, check, lib
+from .quant import stream
+
+
+class MoeBlock:
+    def __init__(self, *, D, de, E, k, expert_dt, ffn_norm, router_w, expert_ptrs,
+                 router=0, routed_scale=1.0, eps=1e-6, router_bias=None, mask=None,
+                 ds=0, shared_dt=0, shared=None, shared_gate_inp=None, device="cuda"):
+        self.keep = [ffn_norm, router_w, router_bias, mask, shared, shared_gate_inp]
+        assert len(expert_ptrs) == 3 * E
+        self.table = torch.tensor(list(expert_ptrs), dtype=torch.int64, device=device)
+        sg, su, sd = shared if shared is not None else (None, None, None)
+
+        def p(t):
+            return t.data_ptr() if t is not None else None
+
+        self.desc = MoeDesc(D, de, ds, E, k, router, routed_scale, eps, expert_dt, shared_dt,
+                            p(ffn_norm), p(router_w), p(router_bias), p(mask), self.table.data_ptr(),
+                            p(sg), p(su), p(sd), p(shared_gate_inp))
+        nbytes = int(lib.tlm_hip_moe_workspace_bytes(C.byref(self.desc)))
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        self.ids = torch.zeros(max(k, 1), dtype=torch.int32, device=device)
+        self.w = torch.zeros(max(k, 1), dtype=torch.float32, device=device)
+
+    def __call__(self, h):
+        """h (f32 device [D]) += MoE(h); routing lands in self.ids / self.w."""
+        check(lib.tlm_hip_moe_layer(C.byref(self.desc), C.c_void_p(h.data_ptr()),
+                                    C.c_void_p(self.ids.data_ptr()), C.c_void_p(self.w.data_ptr()),
+                                    C.c_void_p(self.workspace.data_ptr()), stream()))
+        return h
+
+    def phase(self, ph, h):
+        check(lib.tlm_hip_moe_layer_phase(C.byref(self.desc), ph, C.c_void_p(h.data_ptr()),
+                                          C.c_void_p(self.ids.data_ptr()), C.c_void_p(self.w.data_ptr()),
+                                          C.c_void_p(self.workspace.data_ptr()), stream()))
+
+    def set_expert_ptrs(self, expert_ptrs):
+        """Point the block at another set of packed experts (same geometry)."""
+        self.table.copy_(torch.tensor(list(expert_ptrs), dtype=torch.int64))
