@@ -12,9 +12,10 @@ Timed region: K tokens launched back to back on one stream (HIP graphs of up
 to --graph tokens, replayed), bracketed by synchronisation.  value = tokens/s.
 
 roofline: the dominant kernel is the gate/up launch (phase 2).  Its average
-duration is measured with HIP events around each launch over
---roofline-tokens tokens; algorithmic bytes per launch = top-8 x (gate + up)
-packed Q6_K bytes = 8 x 2 x 1,290,240 = 20,643,840 B.
+duration is measured with HIP events around a graph of --roofline-tokens
+back-to-back phase-2 launches (cycling the layer copies), divided by the
+count; algorithmic bytes per launch = top-8 x (gate + up) packed Q6_K bytes =
+8 x 2 x 1,290,240 = 20,643,840 B.
 
 cpu_baseline: the reference's own kernels (oracle/_ref, AVX-512 tier when the
 host has it) running the same block through ref_moe.c on the host cores, on a
@@ -102,7 +103,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--layers", type=int, default=48, help="distinct layer copies cycled by the tokens")
     ap.add_argument("--graph", type=int, default=100, help="tokens per captured HIP graph (0 = eager launches)")
-    ap.add_argument("--roofline-tokens", type=int, default=1000)
+    ap.add_argument("--roofline-tokens", type=int, default=960, help="launches per phase in the roofline graphs")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -180,30 +181,46 @@ def main():
     tok_s = args.steps / elapsed
     ms_per_step = elapsed * 1e3 / args.steps
 
-    # roofline pass: HIP events around each launch, eager, same token stream pattern
+    # roofline pass: per phase, one HIP graph of R launches of that phase
+    # alone, each on the next layer copy (so weights stream from HBM), replayed
+    # between two events on the stream it runs on; average launch = elapsed / R
+    # (kernel time plus the graph's dispatch gap between dependent launches)
     R = args.roofline_tokens
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(R)]
-    Hr = torch.randn((R, D), generator=gen, device=dev)
+    hr = torch.randn(D, generator=gen, device=dev)
+    for b in blocks:                       # every workspace holds a routed token
+        b(hr.clone())
     torch.cuda.synchronize()
-    for t in range(R):
-        b, h = blocks[t % L], Hr[t]
-        ev[t][0].record()
-        b.phase(1, h)
-        ev[t][1].record()
-        b.phase(2, h)
-        ev[t][2].record()
-        b.phase(3, h)
-        ev[t][3].record()
-    torch.cuda.synchronize()
-    ph = np.array([[ev[t][i].elapsed_time(ev[t][i + 1]) for i in range(3)] for t in range(R)]) * 1e3  # us
-    skip = min(20, R // 10)
-    p1, p2, p3 = (float(np.mean(ph[skip:, i])) for i in range(3))
+    ph = []
+    for p in range(1, 5):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            blocks[0].phase(p, hr)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for t in range(R):
+                blocks[t % L].phase(p, hr)
+        g.replay()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(3):
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            g.replay()
+            ev1.record()
+            ev1.synchronize()
+            us = ev0.elapsed_time(ev1) * 1e3 / R
+            best = us if best is None else min(best, us)
+        ph.append(best)
+        del g
+    p1, p2, p3, p4 = ph
     gu_gbs = GATEUP_BYTES / (p2 * 1e-6) / 1e9
     dn_gbs = DOWN_BYTES / (p3 * 1e-6) / 1e9
     expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
-    log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); phases router {p1:.2f} us, "
-        f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down {p3:.2f} us ({dn_gbs:.0f} GB/s)")
-
+    log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); per launch: router {p1:.2f} us, "
+        f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down {p3:.2f} us ({dn_gbs:.0f} GB/s), combine {p4:.2f} us")
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
@@ -224,10 +241,12 @@ def main():
                    "expert_bytes_per_token": TOKEN_BYTES},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_moe_gateup (gate+up of top-8 experts, SwiGLU, h quantisation)",
+                     "kernel": "k_moe_gateup (routing + gate/up of the top-8 experts + SwiGLU)",
                      "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(p2, 3),
                      "down_kernel_GBps": round(dn_gbs, 1), "down_avg_launch_us": round(p3, 3),
-                     "router_avg_launch_us": round(p1, 3),
+                     "router_avg_launch_us": round(p1, 3), "combine_avg_launch_us": round(p4, 3),
+                     "timing": "HIP events around a graph of R back-to-back launches of the phase (R = roofline_launches), / R",
+                     "roofline_launches": R,
                      "expert_gemv_GBps": round(expert_gbs, 1), "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
     }

@@ -226,47 +226,39 @@ template <int DT>
 __global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ Wp, int64_t rows, int nb,
                                                    const uint8_t *__restrict__ act, float *__restrict__ y) {
     using F = Packed<DT>;
-    constexpr int LPI = F::LPI, IPW = 64 / LPI;          /* items per wave pass */
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
+    constexpr int IPL = 4;                                  /* items in flight per lane */
     extern __shared__ __align__(16) uint8_t lds[];
     const int kind = dt_act_kind(DT);
     const XLds X = stage_act(kind, act, nb, lds);
     const int cap = nb < PK_NBC ? nb : PK_NBC;
-    int32_t *l_is = (int32_t *)(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15));
-    int32_t *l_ms = l_is + cap * TILE_ROWS;
-    float *l_da = (float *)(l_ms + cap * TILE_ROWS);
-    float *l_dm = l_da + cap * TILE_ROWS;
+    const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * TILE_ROWS);
     __syncthreads();
 
     const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS, t = blockIdx.x;
     const int64_t units = T * nb * TILE_ROWS;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int q = lane % LPI, slot = lane / LPI;
+    const int round_items = (int)(blockDim.x / F::LPI) * IPL;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += cap) {
         const int nbc = nb - b0 < cap ? nb - b0 : cap;
         const int nitems = nbc * TILE_ROWS;
-        for (int it = wave * IPW + slot; it - slot < nitems; it += 4 * IPW) {
-            const bool live = it < nitems;
-            const int bl = live ? it / TILE_ROWS : 0, i = it % TILE_ROWS, b = b0 + bl;
-            int32_t is = 0, ms = 0;
-            float dA = 0.0f, dM = 0.0f;
-            if (live) {
-                const int64_t u = ((int64_t)t * nb + b) * TILE_ROWS + i;
-                F::item(Wp, units, u, b, q, X, is, ms, dA, dM);
-                if (q == 0) {
-                    l_is[bl * TILE_ROWS + i] = is;
-                    l_da[bl * TILE_ROWS + i] = dA;
-                    if (AFF) { l_ms[bl * TILE_ROWS + i] = ms; l_dm[bl * TILE_ROWS + i] = dM; }
-                }
-            }
+        for (int base = 0; base < nitems; base += round_items) {
+            auto map = [&](int it, const uint8_t *&W, int64_t &un, int64_t &u, int &b, int &pk) {
+                const int g = base + it, bl = g / TILE_ROWS, i = g % TILE_ROWS;
+                W = Wp;
+                un = units;
+                b = b0 + bl;
+                u = ((int64_t)t * nb + b) * TILE_ROWS + i;
+                pk = g;
+            };
+            run_items<DT, IPL>(nitems - base, map, [&]() { return X; }, park);
         }
         __syncthreads();
         if (threadIdx.x < TILE_ROWS) {
             const int i = threadIdx.x;
             for (int bl = 0; bl < nbc; bl++) {
-                acc = fmaf(l_da[bl * TILE_ROWS + i], (float)l_is[bl * TILE_ROWS + i], acc);
-                if (AFF) acc = fmaf(-l_dm[bl * TILE_ROWS + i], (float)l_ms[bl * TILE_ROWS + i], acc);
+                acc = fmaf(park.da[bl * TILE_ROWS + i], (float)park.is[bl * TILE_ROWS + i], acc);
+                if (AFF) acc = fmaf(-park.dm[bl * TILE_ROWS + i], (float)park.ms[bl * TILE_ROWS + i], acc);
             }
         }
         __syncthreads();

@@ -1,27 +1,33 @@
-/* hip_moe.hip - one routed MoE block on device in three launches
+/* hip_moe.hip - one routed MoE block on device in four launches
  * (src/lib/tlm_model.c:940-1055, run_batch :900-938, route :798-839).
  *
- *   K1 moe_router   ceil(E/8) work-groups.  Each recomputes xb = rmsnorm(h)
- *                   (same tree, so the same bits in every group) and 8 router
- *                   rows in the reference's f32 lane order.  Group 0 also
- *                   publishes xb, quantises it for the experts and for the
- *                   shared expert, evaluates the shared sigmoid gate, and
- *                   clears the arrival counters used by K2 and K3.
+ *   K1 moe_router   one wave per work-group, two router rows each.  Every
+ *                   group recomputes xb = rmsnorm(h) (same tree, same bits),
+ *                   then its rows in the reference's f32 lane order; group b
+ *                   also quantises activation block b of xb for the experts
+ *                   (and the shared expert) and group 0 publishes xb and the
+ *                   shared sigmoid gate.
  *   K2 moe_gateup   one group per (rank, 16-row tile) of gate and up, then the
- *                   shared expert's tiles.  Every group routes (softmax, top-k,
- *                   renormalise) from the logits itself - identical in all
- *                   groups - so routing needs no launch or counter of its own.
- *                   A group computes its 16 gate rows and 16 up rows,
- *                   h = silu(g) * u, and the last group to finish a
- *                   quantisation block of h (256 or 32 values) quantises it.
- *   K3 moe_down     one group per (rank, 16-row tile) of down, then shared.
- *                   The last group to finish a tile combines the tile's rows
- *                   in ascending rank order, adds the gated shared output and
- *                   updates the residual h.
- *
- * Integer sums, per-row fma chains, activation quantisation and the combine
- * order are the reference's; expf and rmsnorm's double sum of squares are
- * the device's (to about an ulp). */
+ *                   shared expert's tiles.  Every group routes (softmax, top-k
+ *                   by rank counting, renormalise) from the logits itself -
+ *                   the same bits in every group - so no group waits on
+ *                   another; each wave then puts all its weight loads in
+ *                   flight, copies the activation into its own LDS while they
+ *                   land, computes, and the group writes h = silu(g) * u for
+ *                   its 16 rows.
+ *   K3 moe_down     one group per (rank, 16-row tile) of down, then shared;
+ *                   wave w owns block column(s) w: it puts its weight loads in
+ *                   flight, quantises its block(s) of h (the reference's
+ *                   activation rule) into LDS, computes; the group then runs
+ *                   the 16 row chains and writes the rows.
+ *   K4 moe_combine  ffn = sum_r w_r * eo_r in ascending rank order (+ gated
+ *                   shared output), h += ffn.
+ * No launch hands data between its own work-groups, so no cross-XCD cache
+ * maintenance is needed inside a kernel.  The kernels are instantiated per
+ * (expert dtype, shared dtype) so each holds one or two item paths only: the
+ * four launches then fit the instruction cache together.  Integer sums,
+ * per-row fma chains, activation quantisation and the combine order are the
+ * reference's; expf and rmsnorm's double sum of squares are the device's. */
 #include "tlm_hip_internal.h"
 #include "tlm_hip_items.h"
 
@@ -31,518 +37,647 @@ namespace {
 
 constexpr int MAXK = 32;          /* top-k bound of this implementation */
 constexpr int MAXE = 256;         /* expert-count bound (4 per lane of one wave) */
+constexpr int NWAVE = 4;          /* waves per group in K2 */
+constexpr int PARK_MAX = 512;     /* parked items per matrix chunk in K2 */
+constexpr int NONE = -1;          /* "no shared expert" instantiation */
 
-/* ---- workspace layout (256-byte aligned regions) ------------------------- */
+__host__ __device__ constexpr int bvals(int kind) { return kind == DT_Q8_K ? 256 : 32; }
+
+/* ---- workspace layout (256-byte aligned regions), computed on the host and
+ * passed to every kernel --------------------------------------------------- */
 struct WsLayout {
-    size_t xb, xe, xs, logits, route, hh, hq, eo, so, cnt_h, cnt_t, total;
-    int64_t nqe, nqs;             /* quantisation blocks of h per rank / for shared */
+    size_t xb, xe, xs, logits, route, hh, eo, so, total;
 };
 
 __host__ __device__ inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-__host__ __device__ inline WsLayout ws_layout(const tlm_hip_moe_desc &d) {
+inline WsLayout ws_layout(const tlm_hip_moe_desc &d) {
     WsLayout L;
     const int ek = dt_act_kind(d.expert_dt), sk = d.ds > 0 ? dt_act_kind(d.shared_dt) : DT_Q8_K;
-    const int ebv = ek == DT_Q8_K ? 256 : 32, sbv = sk == DT_Q8_K ? 256 : 32;
     size_t o = 0;
     L.xb = o;     o += al256((size_t)d.D * 4);
-    L.xe = o;     o += al256(act_bytes(ek, d.D));
-    L.xs = o;     o += al256(act_bytes(sk, d.D));
+    /* activations of xb in the split (LDS) layout, whole blocks */
+    L.xe = o;     o += al256(stage_bytes(ek, (int)((d.D + bvals(ek) - 1) / bvals(ek))));
+    L.xs = o;     o += al256(stage_bytes(sk, (int)((d.D + bvals(sk) - 1) / bvals(sk))));
     L.logits = o; o += al256((size_t)d.E * 4);
-    L.route = o;  o += 512;                        /* ids[32] int32, w[32] f32, sgate, ... */
+    L.route = o;  o += 512;                        /* ids int32[32] at +0, w f32[32] at +128, sgate at +256 */
     L.hh = o;     o += al256((size_t)(d.k * d.de + d.ds) * 4);
-    L.nqe = (d.de + ebv - 1) / ebv;
-    L.nqs = d.ds > 0 ? (d.ds + sbv - 1) / sbv : 0;
-    L.hq = o;     o += al256(act_bytes(ek, d.de) * (size_t)d.k + (d.ds > 0 ? act_bytes(sk, d.ds) : 0));
     L.eo = o;     o += al256((size_t)d.k * d.D * 4);
     L.so = o;     o += al256((size_t)d.D * 4);
-    L.cnt_h = o;  o += al256((size_t)(d.k * L.nqe + L.nqs) * 4);
-    L.cnt_t = o;  o += al256((size_t)((d.D + TILE_ROWS - 1) / TILE_ROWS) * 4);
     L.total = o;
     return L;
 }
 
-/* route region: ids at +0 (int32[32]), w at +128 (f32[32]), shared gate at +256 */
 __device__ __forceinline__ int32_t *ws_ids(uint8_t *ws, const WsLayout &L) { return (int32_t *)(ws + L.route); }
 __device__ __forceinline__ float *ws_w(uint8_t *ws, const WsLayout &L) { return (float *)(ws + L.route + 128); }
 __device__ __forceinline__ float *ws_sgate(uint8_t *ws, const WsLayout &L) { return (float *)(ws + L.route + 256); }
-/* quantised h of rank r (r == k: shared) */
-__host__ __device__ __forceinline__ size_t hq_off(const tlm_hip_moe_desc &d, const WsLayout &L, int r) {
-    return L.hq + act_bytes(dt_act_kind(d.expert_dt), d.de) * (size_t)r;
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-/* ---- block-wide helpers --------------------------------------------------- */
-__device__ double block_sum_d(double v, double *scratch) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    if ((threadIdx.x & 63) == 0) scratch[wave] = v;
-    __syncthreads();
-    double s = 0.0;
-    for (int i = 0; i < nw; i++) s += scratch[i];
-    __syncthreads();
-    return s;
-}
-
-/* xb = rmsnorm(h) * w into LDS (src/lib/tlm_model.c:164-169): sum of squares
- * in double (a fixed tree here), r = 1/sqrtf(mean + eps), (x * r) * w. */
-__device__ void rmsnorm_lds(const float *__restrict__ h, const float *__restrict__ nw, int64_t D, float eps,
-                            float *xb, double *scratch) {
-    double ss = 0.0;
-    for (int64_t i = threadIdx.x; i < D; i += blockDim.x) {
-        double v = (double)h[i];
-        ss += v * v;
+/* max / or over aligned groups of WIDTH lanes (2, 4, 8, 16 or 64), uniform in the group */
+template <int WIDTH> __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+    uint32_t o;
+    if (WIDTH >= 2) { o = dpp_u32<DPP_XOR1>(v); v = o > v ? o : v; }
+    if (WIDTH >= 4) { o = dpp_u32<DPP_XOR2>(v); v = o > v ? o : v; }
+    if (WIDTH >= 8) { o = dpp_u32<DPP_HALF_MIRROR>(v); v = o > v ? o : v; }
+    if (WIDTH >= 16) { o = dpp_u32<DPP_MIRROR>(v); v = o > v ? o : v; }
+    if (WIDTH == 64) {
+        const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+        const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+        const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+        v = ab > cd ? ab : cd;
     }
-    ss = block_sum_d(ss, scratch);
-    const float r = 1.0f / sqrtf((float)(ss / (double)D) + eps);
-    for (int64_t i = threadIdx.x; i < D; i += blockDim.x) xb[i] = h[i] * r * nw[i];
-    __syncthreads();
+    return v;
+}
+template <int WIDTH> __device__ __forceinline__ uint32_t group_or_u32(uint32_t v) {
+    if (WIDTH >= 2) v |= dpp_u32<DPP_XOR1>(v);
+    if (WIDTH >= 4) v |= dpp_u32<DPP_XOR2>(v);
+    if (WIDTH >= 8) v |= dpp_u32<DPP_HALF_MIRROR>(v);
+    if (WIDTH >= 16) v |= dpp_u32<DPP_MIRROR>(v);
+    if (WIDTH == 64)
+        v = ((uint32_t)__builtin_amdgcn_readlane((int)v, 0) | (uint32_t)__builtin_amdgcn_readlane((int)v, 16)) |
+            ((uint32_t)__builtin_amdgcn_readlane((int)v, 32) | (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return v;
 }
 
-/* One activation block of `cnt` <= block values from `x` into the quantised
- * layout at dst, by one wave (rule of src/lib/tlm_quant.c:458-506). */
-__device__ void quant_block_wave(int kind, const float *x, int cnt, uint8_t *dst) {
-    const int lane = threadIdx.x & 63;
-    const bool q8k = kind == DT_Q8_K;
-    const int width = q8k ? 64 : 8;
-    const bool mine = q8k || lane < 8;
-    const int sub = q8k ? lane : (lane & 7);
-    float v[4];
-    bool ok[4];
+/* ---- activation rule (src/lib/tlm_quant.c:458-478) for this lane's 4 values
+ * of a block spread over WIDTH lanes: d, and the 4 codes packed in a dword --- */
+template <int WIDTH>
+__device__ __forceinline__ float act_rule4(f32x4 v, bool ok, uint32_t &codes) {
+    /* |v| as bits: for non-negative floats the unsigned order is the float
+     * order; above 0x7F800000 is NaN, equal is infinity */
+    uint32_t am = 0, fl = 0;
+#pragma unroll
     for (int j = 0; j < 4; j++) {
-        int i = 4 * sub + j;
-        ok[j] = mine && i < cnt;
-        v[j] = ok[j] ? x[i] : 0.0f;
+        const uint32_t b = ok ? (__float_as_uint(v[j]) & 0x7FFFFFFFu) : 0u;
+        fl |= (b > 0x7F800000u ? 1u : 0u) | (b == 0x7F800000u ? 2u : 0u);
+        const uint32_t f = b < 0x7F800000u ? b : 0u;
+        am = f > am ? f : am;
     }
-    float amax = 0.0f;
-    int nan = 0, inf = 0;
-    for (int j = 0; j < 4; j++) {
-        if (!ok[j]) continue;
-        float a = fabsf(v[j]);
-        if (a != a) nan = 1;
-        else if (a == INFINITY) inf = 1;
-        else if (a > amax) amax = a;
+    am = group_max_u32<WIDTH>(am);
+    fl = group_or_u32<WIDTH>(fl);
+    const float amax = __uint_as_float(am);
+    codes = 0;
+    if (fl) return (fl & 1u) ? __uint_as_float(0x7FC00000u) : INFINITY;
+    if (!(amax > 0.0f) || !ok) return amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float d = amax / 127.0f;
+    if (amax >= 0x1p-100f) {
+        const float id = 127.0f / amax;
+#pragma unroll
+        for (int j = 0; j < 4; j++) codes |= (uint32_t)(uint8_t)(int8_t)rne_clamp(v[j] * id, -127, 127) << (8 * j);
+    } else {
+        const double id = 127.0 / (double)amax;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            codes |= (uint32_t)(uint8_t)(int8_t)rne_clamp((float)((double)v[j] * id), -127, 127) << (8 * j);
     }
-    for (int m = 1; m < 64; m <<= 1) {
-        if (m >= width) break;
-        float o = __shfl_xor(amax, m, 64);
-        amax = o > amax ? o : amax;
-        nan |= __shfl_xor(nan, m, 64);
-        inf |= __shfl_xor(inf, m, 64);
-    }
-    uint32_t codes = 0;
-    float d;
-    if (nan || inf) d = nan ? __uint_as_float(0x7FC00000u) : INFINITY;
-    else if (!(amax > 0.0f)) d = 0.0f;
-    else {
-        d = amax / 127.0f;
-        if (amax >= 0x1p-100f) {
-            float id = 127.0f / amax;
-            for (int j = 0; j < 4; j++)
-                if (ok[j]) codes |= (uint32_t)(uint8_t)(int8_t)rne_clamp(v[j] * id, -127, 127) << (8 * j);
-        } else {
-            double id = 127.0 / (double)amax;
-            for (int j = 0; j < 4; j++)
-                if (ok[j]) codes |= (uint32_t)(uint8_t)(int8_t)rne_clamp((float)((double)v[j] * id), -127, 127) << (8 * j);
+    return d;
+}
+
+__device__ __forceinline__ int byte_sum(uint32_t c) {
+    return (int)(int8_t)(c & 0xFF) + (int)(int8_t)((c >> 8) & 0xFF) + (int)(int8_t)((c >> 16) & 0xFF) +
+           (int)(int8_t)(c >> 24);
+}
+
+/* Quantise one block (values v of this lane, `ok` = lane inside the block)
+ * into the split layout at (q, bs, d) of block index b: Q8_K uses all 64
+ * lanes, a8 the 8 lanes of a group. */
+template <class QP, class BP, class DP>
+__device__ __forceinline__ void quant_block_to(int kind, f32x4 v, bool ok, int sub, QP q, BP bs, DP dd, int b) {
+    uint32_t codes;
+    if (kind == DT_Q8_K) {
+        const float d = act_rule4<64>(v, ok, codes);
+        q[b * 64 + sub] = codes;
+        int s = byte_sum(codes);
+        s += (int)dpp_u32<DPP_XOR1>((uint32_t)s);
+        s += (int)dpp_u32<DPP_XOR2>((uint32_t)s);
+        if ((sub & 3) == 0) bs[b * 16 + (sub >> 2)] = (int16_t)s;
+        if (sub == 0) dd[b] = d;
+    } else {
+        const float d = act_rule4<8>(v, ok, codes);
+        if (ok) {
+            q[b * 8 + sub] = codes;
+            if (sub == 0) dd[b] = d;
         }
-    }
-    if (mine) {
-        if (sub == 0) *(float *)dst = d;
-        *(uint32_t *)(dst + 4 + 4 * sub) = codes;
-    }
-    if (q8k) {
-        int s = (int)(int8_t)(codes & 0xFF) + (int)(int8_t)((codes >> 8) & 0xFF) +
-                (int)(int8_t)((codes >> 16) & 0xFF) + (int)(int8_t)(codes >> 24);
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        if ((lane & 3) == 0) *(int16_t *)(dst + 260 + 2 * (lane >> 2)) = (int16_t)s;
     }
 }
 
-/* ---- routing by one wave (src/lib/tlm_model.c:776-839) ------------------- */
-/* larger value wins; equal values -> lower id; be < 0 means "none yet" */
-__device__ __forceinline__ bool better(float v, int e, float bv, int be) {
-    return be < 0 || v > bv || (v == bv && e < be);
+/* ---- routing by the group (src/lib/tlm_model.c:776-839) --------------------
+ * 256 threads; thread t owns expert t.  Every valid entry (unmasked, selection
+ * value not NaN) gets a 64-bit key: the order-preserving bits of its value,
+ * then ~index.  Keys are distinct and "larger key" is exactly the reference's
+ * "larger value, ties to the lower index", so an entry's rank (the number of
+ * larger keys) is its position in the reference's top-k; ranks 0..k-1 are
+ * written directly.  With fewer than k valid entries the reference's fallback
+ * (lowest unmasked unused index, else 0) fills the remaining ranks. */
+struct RouteLds {
+    unsigned long long key[MAXE];
+    float p[MAXE];
+    int cnt[MAXE];
+    double red[NWAVE];
+    float redf[NWAVE];
+    int redi[NWAVE];
+    int ids[MAXK];
+    float w[MAXK];
+};
+
+__device__ __forceinline__ uint32_t ord_bits(float f) {
+    const uint32_t b = __float_as_uint(f + 0.0f);   /* -0 -> +0: equal values, equal keys */
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-/* ids[0..k) by repeated arg-max over unmasked, non-NaN, unused entries;
- * lane l owns experts l, l+64, l+128, l+192. */
-__device__ void topk_wave(const float *v, const uint8_t *mask, int E, int k, int *ids) {
-    const int lane = threadIdx.x & 63;
-    uint32_t taken = 0;
-    for (int r = 0; r < k; r++) {
-        float bv = 0.0f;
-        int be = -1;
-        for (int j = 0; j < 4; j++) {
-            int e = lane + 64 * j;
-            if (e >= E || ((taken >> j) & 1u) || (mask && mask[e])) continue;
-            float x = v[e];
-            if (x != x) continue;
-            if (better(x, e, bv, be)) { bv = x; be = e; }
-        }
-        for (int m = 32; m >= 1; m >>= 1) {
-            float ov = __shfl_xor(bv, m, 64);
-            int oe = __shfl_xor(be, m, 64);
-            if (oe >= 0 && better(ov, oe, bv, be)) { bv = ov; be = oe; }
-        }
-        if (be < 0) {   /* nothing finite left: lowest unmasked unused id, else 0 */
-            int cand = 1 << 30;
-            for (int j = 0; j < 4; j++) {
-                int e = lane + 64 * j;
-                if (e >= E || ((taken >> j) & 1u) || (mask && mask[e])) continue;
-                cand = e < cand ? e : cand;
-            }
-            for (int m = 32; m >= 1; m >>= 1) {
-                int o = __shfl_xor(cand, m, 64);
-                cand = o < cand ? o : cand;
-            }
-            be = cand == (1 << 30) ? 0 : cand;
-        }
-        if ((be & 63) == lane) taken |= 1u << (be >> 6);
-        if (lane == 0) ids[r] = be;
+/* ids / weights land in R->ids[0..k), R->w[0..k), readable by every thread. */
+__device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, LAS RouteLds *R) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, E = d.E, k = d.k;
+    const bool sig = d.router == 2;
+    const bool in = t < E;
+    const bool unmasked = in && !(d.mask && d.mask[t]);
+    const float l = in ? logits[t] : 0.0f;
+    const float bias = (sig && in && d.router_bias) ? d.router_bias[t] : 0.0f;
+    float p;
+    if (sig) {   /* sigmoid score = weight; bias for selection only */
+        p = 1.0f / (1.0f + expf(-l));
+    } else {     /* softmax over the routable experts */
+        float m = wave_max_f32((unmasked && l > -INFINITY) ? l : -INFINITY);
+        if (lane == 0) R->redf[wave] = m;
+        __syncthreads();
+        float mx = R->redf[0];
+#pragma unroll
+        for (int q = 1; q < NWAVE; q++) mx = R->redf[q] > mx ? R->redf[q] : mx;
+        const bool off = !unmasked || l != l || mx == -INFINITY;
+        const float x = off ? 0.0f : expf(l - mx);
+        const double s = wave_sum_f64((double)x);
+        if (lane == 0) R->red[wave] = s;
+        __syncthreads();
+        const double st = (R->red[0] + R->red[1]) + (R->red[2] + R->red[3]);
+        const float inv = st > 0.0 ? (float)(1.0 / st) : 0.0f;
+        p = x * inv;
     }
-}
-
-/* ids, w into LDS; p is LDS scratch of 2*MAXE floats. */
-__device__ void route_wave(const tlm_hip_moe_desc &d, const float *logits, int *ids, float *w, float *p) {
-    const int lane = threadIdx.x & 63, E = d.E, k = d.k;
-    const uint8_t *mask = d.mask;
-    if (d.router == 2) {   /* sigmoid; bias for selection only; renormalise; scale */
-        for (int j = 0; j < 4; j++) {
-            int e = lane + 64 * j;
-            if (e < E) {
-                float s = 1.0f / (1.0f + expf(-logits[e]));
-                p[e] = s;
-                p[MAXE + e] = s + (d.router_bias ? d.router_bias[e] : 0.0f);
-            }
+    const float sel = sig ? p + bias : p;
+    const bool valid = unmasked && sel == sel;
+    const unsigned long long key =
+        valid ? ((unsigned long long)ord_bits(sel) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)t) : 0ull;
+    R->key[t] = key;
+    R->p[t] = p;
+    const int nv_wave = __builtin_popcountll(__ballot(valid));   /* whole wave active here */
+    if (lane == 0) R->redi[wave] = nv_wave;
+    __syncthreads();
+    const int nvalid = (R->redi[0] + R->redi[1]) + (R->redi[2] + R->redi[3]);
+    /* rank = #larger keys; with E <= 128 two threads split the scan of one entry */
+    const bool split = E <= 128;
+    const int e = split ? (t & 127) : t, hE = (E + 1) >> 1;
+    const int f0 = (split && t >= 128) ? hE : 0, f1 = (split && t < 128) ? hE : E;
+    const unsigned long long ke = e < E ? R->key[e] : 0ull;
+    int c = 0;
+    if (ke != 0ull) {
+#pragma unroll 8
+        for (int f = f0; f < f1; f++) c += R->key[f] > ke ? 1 : 0;
+    }
+    R->cnt[t] = c;
+    __syncthreads();
+    if (in && key != 0ull) {
+        const int rank = split ? R->cnt[t] + R->cnt[t + 128] : c;
+        if (rank < k) { R->ids[rank] = t; R->w[rank] = p; }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        if (nvalid < k) {
+            if (lane == 0)
+                for (int r = nvalid; r < k; r++) {
+                    int pick = -1;
+                    for (int f = 0; f < E && pick < 0; f++) {
+                        if (d.mask && d.mask[f]) continue;
+                        bool used = false;
+                        for (int q = 0; q < r; q++) used = used || R->ids[q] == f;
+                        if (!used) pick = f;
+                    }
+                    pick = pick < 0 ? 0 : pick;
+                    R->ids[r] = pick;
+                    R->w[r] = R->p[pick];
+                }
+            wave_sync();
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        topk_wave(p + MAXE, mask, E, k, ids);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        if (lane == 0) {
+        /* renormalise in rank order (double sum), then scale */
+        float wr = lane < k ? R->w[lane] : 0.0f;
+        if (d.router != 1) {
             double s = 0.0;
-            for (int r = 0; r < k; r++) s += (double)p[ids[r]];
-            float inv = (float)(1.0 / (s + 1e-20));
-            for (int r = 0; r < k; r++) w[r] = p[ids[r]] * inv * d.routed_scale;
+            for (int r = 0; r < k; r++) s += (double)rdlane_f32(wr, r);
+            if (sig || s > 0.0) wr *= (float)(1.0 / (sig ? s + 1e-20 : s));
         }
-        return;
-    }
-    /* softmax over routable experts, then top-k (router 0 renormalises) */
-    float mx = -INFINITY;
-    for (int j = 0; j < 4; j++) {
-        int e = lane + 64 * j;
-        if (e < E && !(mask && mask[e]) && logits[e] > mx) mx = logits[e];
-    }
-    for (int m = 32; m >= 1; m >>= 1) {
-        float o = __shfl_xor(mx, m, 64);
-        mx = o > mx ? o : mx;
-    }
-    double s = 0.0;
-    float pv[4];
-    for (int j = 0; j < 4; j++) {
-        int e = lane + 64 * j;
-        pv[j] = 0.0f;
-        if (e < E) {
-            float l = logits[e];
-            bool off = (mask && mask[e]) || l != l || mx == -INFINITY;
-            pv[j] = off ? 0.0f : expf(l - mx);
-            s += (double)pv[j];
-        }
-    }
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-    const float inv = s > 0.0 ? (float)(1.0 / s) : 0.0f;
-    for (int j = 0; j < 4; j++) {
-        int e = lane + 64 * j;
-        if (e < E) p[e] = pv[j] * inv;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    topk_wave(p, mask, E, k, ids);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane == 0) {
-        for (int r = 0; r < k; r++) w[r] = p[ids[r]];
-        if (d.router == 0) {
-            double t = 0.0;
-            for (int r = 0; r < k; r++) t += (double)w[r];
-            if (t > 0.0) {
-                float it = (float)(1.0 / t);
-                for (int r = 0; r < k; r++) w[r] *= it;
-            }
-        }
-        if (d.routed_scale != 1.0f)
-            for (int r = 0; r < k; r++) w[r] *= d.routed_scale;
-    }
-}
-
-/* ---- tile GEMV inside a fused kernel --------------------------------------
- * Items (b, i) of tile t of a packed matrix spread over the group's waves;
- * results parked in LDS arrays indexed b * 16 + i. */
-template <int DT>
-__device__ void tile_items(const uint8_t *Wp, int64_t rows, int nb, int64_t t, const XLds &X, int32_t *l_is,
-                           int32_t *l_ms, float *l_da, float *l_dm) {
-    using F = Packed<DT>;
-    constexpr int LPI = F::LPI, IPW = 64 / LPI;
-    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS, units = T * nb * TILE_ROWS;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    const int q = lane % LPI, slot = lane / LPI, nitems = nb * TILE_ROWS;
-    for (int it = wave * IPW + slot; it - slot < nitems; it += nw * IPW) {
-        if (it < nitems) {
-            const int b = it / TILE_ROWS, i = it % TILE_ROWS;
-            int32_t is, ms;
-            float dA, dM;
-            F::item(Wp, units, (t * nb + b) * TILE_ROWS + i, b, q, X, is, ms, dA, dM);
-            if (q == 0) {
-                l_is[it] = is;
-                l_da[it] = dA;
-                if (AFF) { l_ms[it] = ms; l_dm[it] = dM; }
-            }
-        }
-    }
-}
-
-__device__ void tile_items_dt(int dt, const uint8_t *Wp, int64_t rows, int nb, int64_t t, const XLds &X,
-                              int32_t *l_is, int32_t *l_ms, float *l_da, float *l_dm) {
-    switch (dt) {
-    case DT_Q6_K: tile_items<DT_Q6_K>(Wp, rows, nb, t, X, l_is, l_ms, l_da, l_dm); break;
-    case DT_Q8_0: tile_items<DT_Q8_0>(Wp, rows, nb, t, X, l_is, l_ms, l_da, l_dm); break;
-    case DT_Q4_K: tile_items<DT_Q4_K>(Wp, rows, nb, t, X, l_is, l_ms, l_da, l_dm); break;
-    case DT_Q5_K: tile_items<DT_Q5_K>(Wp, rows, nb, t, X, l_is, l_ms, l_da, l_dm); break;
-    default: break;
-    }
-}
-
-/* Row i's float chain over the nb parked blocks, ascending. */
-__device__ __forceinline__ float tile_chain(int dt, int nb, int i, const int32_t *l_is, const int32_t *l_ms,
-                                            const float *l_da, const float *l_dm) {
-    const bool aff = dt == DT_Q4_K || dt == DT_Q5_K;
-    float acc = 0.0f;
-    for (int b = 0; b < nb; b++) {
-        acc = fmaf(l_da[b * TILE_ROWS + i], (float)l_is[b * TILE_ROWS + i], acc);
-        if (aff) acc = fmaf(-l_dm[b * TILE_ROWS + i], (float)l_ms[b * TILE_ROWS + i], acc);
-    }
-    return acc;
-}
-
-/* LDS for one matrix's parked items */
-__host__ __device__ inline size_t park_bytes(int nb) { return (size_t)nb * TILE_ROWS * 16; }
-
-/* Arrival at a counter: returns true in every thread of the group for the
- * group that completes the count, which also re-arms the counter to 0 so the
- * launch can run again.  Release before the increment, acquire after. */
-__device__ bool arrive_last(int32_t *cnt, int need, int *s_flag) {
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        int old = atomicAdd(cnt, 1);
-        int last = old == need - 1;
-        if (last) atomicExch(cnt, 0);
-        *s_flag = last;
+        if (sig || d.routed_scale != 1.0f) wr *= d.routed_scale;
+        if (lane < k) R->w[lane] = wr;
     }
     __syncthreads();
-    const bool last = *s_flag != 0;
-    if (last) __threadfence();
-    return last;
 }
 
 /* ======================================================================
- * K1: rmsnorm + router + activation quantisation + counter reset
+ * K1: rmsnorm + router + activation quantisation (one wave per group)
  * ==================================================================== */
-__global__ __launch_bounds__(256) void k_moe_router(tlm_hip_moe_desc d, const float *__restrict__ h, uint8_t *ws) {
+constexpr int RCH = 16;            /* router values per lane per pipelined chunk */
+constexpr int RCHV = 32 * RCH;     /* values of one row per chunk */
+
+/* Chunk at c0 of a router row: lane hl takes elements c0 + hl + 32j.  D is a
+ * multiple of 32, so a chunk is either full or, as the row's last, holds
+ * whole 32-value groups; TAIL loads clamp into the row and fma_chunk skips
+ * the groups past D. */
+template <bool TAIL>
+__device__ __forceinline__ void load_chunk(float (&v)[RCH], const GAS float *wr, int64_t c0, int hl, int64_t D) {
+    const GAS float *p = wr + c0 + hl;
+#pragma unroll
+    for (int j = 0; j < RCH; j++) v[j] = (!TAIL || c0 + 32 * j < D) ? p[32 * j] : 0.0f;
+}
+
+template <bool TAIL>
+__device__ __forceinline__ float fma_chunk(const float (&v)[RCH], const LAS float *xb, int64_t c0, int hl,
+                                           int64_t D, float r) {
+    const LAS float *x = xb + c0 + hl;
+#pragma unroll
+    for (int j = 0; j < RCH; j++)
+        if (!TAIL || c0 + 32 * j < D) r = fmaf(v[j], x[32 * j], r);
+    return r;
+}
+
+__global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
+                                                   uint8_t *ws) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const WsLayout L = ws_layout(d);
-    float *xb = (float *)lds;
-    double *scratch = (double *)(lds + al256((size_t)d.D * 4));
-    rmsnorm_lds(h, d.ffn_norm, d.D, d.eps, xb, scratch);
+    const int lane = threadIdx.x, hl = lane & 31;
+    const int64_t D = d.D;
+    const int64_t row = (int64_t)blockIdx.x * 2 + (lane >> 5);
+    const bool live = row < d.E;
+    const GAS float *wr = (const GAS float *)d.router_w + (live ? row : 0) * D;
+    const GAS f32x4 *h4 = (const GAS f32x4 *)hptr, *n4 = (const GAS f32x4 *)d.ffn_norm;
+    const int64_t nfull = D / RCHV, ctail = nfull * RCHV;
 
-    /* router rows, 8 per group: lane i mod 32 + reduce32 (src/lib/tlm_quant.c:724-738) */
-    const int hl = threadIdx.x & 31;
-    const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-    float r = 0.0f;
-    if (row < d.E) {
-        const float *wr = d.router_w + row * d.D;
-        for (int64_t i = hl; i < d.D; i += 32) r = fmaf(wr[i], xb[i], r);
-    }
-    float s = r + __shfl_down(r, 16, 32);
-    s = s + __shfl_down(s, 8, 32);
-    s = s + __shfl_down(s, 4, 32);
-    float a = s + __shfl_down(s, 2, 32);
-    float res = a + __shfl_down(a, 1, 32);
-    if (row < d.E && hl == 0) ((float *)(ws + L.logits))[row] = res;
+    /* the first full chunk and the partial last chunk in flight before the norm */
+    float va[RCH], vb[RCH], vt[RCH];
+    if (nfull > 0) load_chunk<false>(va, wr, 0, hl, D);
+    if (ctail < D) load_chunk<true>(vt, wr, ctail, hl, D);
 
-    if (blockIdx.x != 0) return;
-    float *gxb = (float *)(ws + L.xb);
-    for (int64_t i = threadIdx.x; i < d.D; i += blockDim.x) gxb[i] = xb[i];
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int ek = dt_act_kind(d.expert_dt), ebv = ek == DT_Q8_K ? 256 : 32;
-    for (int64_t b = wave; b < (d.D + ebv - 1) / ebv; b += nw) {
-        int64_t rest = d.D - b * ebv;
-        quant_block_wave(ek, xb + b * ebv, rest >= ebv ? ebv : (int)rest, ws + L.xe + b * (ebv == 256 ? 292 : 36));
-    }
-    if (d.ds > 0) {
-        const int sk = dt_act_kind(d.shared_dt), sbv = sk == DT_Q8_K ? 256 : 32;
-        for (int64_t b = wave; b < (d.D + sbv - 1) / sbv; b += nw) {
-            int64_t rest = d.D - b * sbv;
-            quant_block_wave(sk, xb + b * sbv, rest >= sbv ? sbv : (int)rest, ws + L.xs + b * (sbv == 256 ? 292 : 36));
+    /* rmsnorm (src/lib/tlm_model.c:164-169): sum of squares in double, lane
+     * then wave tree; x and the norm weights parked in LDS (16-byte copies) */
+    LAS f32x4 *xb4 = (LAS f32x4 *)lds;
+    LAS f32x4 *xw4 = xb4 + D / 4;
+    constexpr int NV = 8;   /* 16-byte loads of h and of the weights per lane per batch */
+    const int D4 = (int)(D / 4);
+    double ss = 0.0;
+    for (int c = lane; c < D4; c += 64 * NV) {
+        f32x4 hv[NV], nv[NV];
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int cc = c + 64 * j;
+            if (cc < D4) { hv[j] = h4[cc]; nv[j] = n4[cc]; }
         }
-        if (threadIdx.x == 0) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int cc = c + 64 * j;
+            if (cc < D4) {
+#pragma unroll
+                for (int t = 0; t < 4; t++) ss += (double)hv[j][t] * (double)hv[j][t];
+                xb4[cc] = hv[j];
+                xw4[cc] = nv[j];
+            }
+        }
+    }
+    ss = wave_sum_f64(ss);
+    const float rn = 1.0f / sqrtf((float)(ss / (double)D) + d.eps);
+    wave_sync();
+    for (int c = lane; c < D4; c += 64) {
+        const f32x4 x = xb4[c], w = xw4[c];
+        f32x4 o;
+#pragma unroll
+        for (int t = 0; t < 4; t++) o[t] = x[t] * rn * w[t];
+        xb4[c] = o;
+    }
+    wave_sync();
+    const LAS float *xb = (const LAS float *)lds;
+
+    /* router row: element i -> lane i mod 32, fmaf in element order, then the
+     * reduce32 tree (src/lib/tlm_quant.c:724-738); full chunks double-buffered */
+    float r = 0.0f;
+    int64_t c = 0;
+    for (; c + 1 < nfull; c += 2) {
+        load_chunk<false>(vb, wr, (c + 1) * RCHV, hl, D);
+        r = fma_chunk<false>(va, xb, c * RCHV, hl, D, r);
+        if (c + 2 < nfull) load_chunk<false>(va, wr, (c + 2) * RCHV, hl, D);
+        r = fma_chunk<false>(vb, xb, (c + 1) * RCHV, hl, D, r);
+    }
+    if (c < nfull) r = fma_chunk<false>(va, xb, c * RCHV, hl, D, r);
+    if (ctail < D) r = fma_chunk<true>(vt, xb, ctail, hl, D, r);
+    /* lane 0 of each half ends with ((r0 + r16) + (r8 + r24)) + ...: the
+     * reference's pairing (i, i+16), (i, i+8), (i, i+4), (i, i+2), (i, i+1);
+     * row_shl:n hands lane i the value of lane i+n */
+    float s = r + __shfl_xor(r, 16, 64);
+    s = s + dpp_f32<0x108>(s);
+    s = s + dpp_f32<0x104>(s);
+    s = s + dpp_f32<DPP_XOR2>(s);
+    const float res = s + dpp_f32<DPP_XOR1>(s);
+    if (live && hl == 0) ((GAS float *)(ws + L.logits))[row] = res;
+
+    /* group b quantises activation block b for the experts / shared expert
+     * into the split layout the gate/up launch copies straight into LDS */
+    const int b = blockIdx.x;
+    for (int which = 0; which < (d.ds > 0 ? 2 : 1); which++) {
+        const int kind = dt_act_kind(which ? d.shared_dt : d.expert_dt), bv = bvals(kind);
+        const int nb = (int)(D >> (kind == DT_Q8_K ? 8 : 5));   /* D is a multiple of the block */
+        if (b >= nb) continue;
+        GAS uint8_t *base = (GAS uint8_t *)(ws + (which ? L.xs : L.xe));
+        const int sub = kind == DT_Q8_K ? lane : (lane & 7);
+        const bool ok = (kind == DT_Q8_K || lane < 8) && (int64_t)b * bv + 4 * sub < D;
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (ok) v = *(const LAS f32x4 *)(xb + (int64_t)b * bv + 4 * sub);
+        quant_block_to(kind, v, ok, sub, (GAS uint32_t *)base, (GAS int16_t *)(base + nb * 256),
+                       (GAS float *)(base + nb * bv + (kind == DT_Q8_K ? nb * 32 : 0)), b);
+    }
+    if (b == 0) {
+        GAS f32x4 *gxb = (GAS f32x4 *)(ws + L.xb);
+        for (int64_t c = lane; c < D / 4; c += 64) gxb[c] = xb4[c];
+        if (d.ds > 0) {
             float g = 1.0f;
             if (d.shared_gate_inp) {   /* sequential float dot (src/lib/tlm_model.c:1043-1046) */
+                LAS float *gi = (LAS float *)xw4;   /* the norm weights are no longer needed */
+                for (int64_t i = lane; i < D; i += 64) gi[i] = ((const GAS float *)d.shared_gate_inp)[i];
+                wave_sync();
                 float acc = 0.0f;
-                for (int64_t i = 0; i < d.D; i++) acc += d.shared_gate_inp[i] * xb[i];
+                if (lane == 0)
+                    for (int64_t i = 0; i < D; i++) acc += gi[i] * xb[i];
                 g = 1.0f / (1.0f + expf(-acc));
             }
-            *ws_sgate(ws, L) = g;
+            if (lane == 0) *(GAS float *)ws_sgate(ws, L) = g;
         }
     }
-    int32_t *ch = (int32_t *)(ws + L.cnt_h);
-    for (int64_t i = threadIdx.x; i < d.k * L.nqe + L.nqs; i += blockDim.x) ch[i] = 0;
-    int32_t *ct = (int32_t *)(ws + L.cnt_t);
-    for (int64_t i = threadIdx.x; i < (d.D + TILE_ROWS - 1) / TILE_ROWS; i += blockDim.x) ct[i] = 0;
+}
+
+inline int router_groups(const tlm_hip_moe_desc &d) {
+    int64_t g = (d.E + 1) / 2;
+    const int ek = dt_act_kind(d.expert_dt);
+    const int64_t ge = (d.D + bvals(ek) - 1) / bvals(ek);
+    if (ge > g) g = ge;
+    if (d.ds > 0) {
+        const int sk = dt_act_kind(d.shared_dt);
+        const int64_t gs = (d.D + bvals(sk) - 1) / bvals(sk);
+        if (gs > g) g = gs;
+    }
+    return (int)g;
+}
+
+/* Wave-private copy of a split-layout activation into LDS (16-byte loads,
+ * all of a pass in flight first). */
+__device__ XLds wave_stage(int kind, const uint8_t *__restrict__ act, int nb, uint8_t *area_g) {
+    constexpr int SC = 4;
+    const int lane = threadIdx.x & 63;
+    const GAS u32x4 *a = (const GAS u32x4 *)act;
+    LAS u32x4 *area = (LAS u32x4 *)area_g;
+    const int n16 = (int)((stage_bytes(kind, nb) + 15) / 16);
+    for (int c0 = 0; c0 < n16; c0 += 64 * SC) {
+        u32x4 v[SC];
+#pragma unroll
+        for (int j = 0; j < SC; j++) {
+            const int c = c0 + lane + 64 * j;
+            if (c < n16) v[j] = a[c];
+        }
+#pragma unroll
+        for (int j = 0; j < SC; j++) {
+            const int c = c0 + lane + 64 * j;
+            if (c < n16) area[c] = v[j];
+        }
+    }
+    wave_sync();
+    return xlds_at(kind, nb, area_g);
 }
 
 /* ======================================================================
- * K2: route + gate/up + SwiGLU + h quantisation
+ * K2: route + gate/up + SwiGLU
  * grid: k * de/16 expert tiles (rank-major), then ds/16 shared tiles
+ * LDS: NWAVE wave-private activation copies, then the park of the chunk.
  * ==================================================================== */
-__global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, int32_t *ids_out, float *w_out, uint8_t *ws) {
+template <int DT>
+__device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const uint8_t *uW, const uint8_t *act,
+                            int64_t F, int64_t t, float *hh, uint8_t *lds) {
+    using Fm = Packed<DT>;
+    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
+    constexpr int IPL = DT == DT_Q8_0 ? 8 : 4;
+    constexpr int kind = DT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
+    const int nb = (int)(d.D / Fm::BV);
+    const int wave = threadIdx.x >> 6;
+    const size_t xstride = (stage_bytes(kind, nb) + 15) & ~(size_t)15;
+    uint8_t *xarea = lds + xstride * wave;
+    const int cb = nb < PARK_MAX / TILE_ROWS / 2 ? nb : PARK_MAX / TILE_ROWS / 2;   /* blocks per chunk */
+    const Park park = park_at(lds + xstride * NWAVE, 2 * cb * TILE_ROWS);
+    const int64_t T = F / TILE_ROWS, units = T * nb * TILE_ROWS;
+    const int slots = (int)blockDim.x / Fm::LPI;
+    bool staged = false;
+    XLds X = xlds_at(kind, nb, xarea);
+    float accg = 0.0f, accu = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += cb) {
+        const int nbc = nb - b0 < cb ? nb - b0 : cb;
+        const int per = nbc * TILE_ROWS, nitems = 2 * per;
+        for (int base = 0; base < nitems; base += slots * IPL) {
+            auto map = [&](int it, const uint8_t *&W, int64_t &un, int64_t &u, int &b, int &pk) {
+                const int g = base + it, m = g >= per, rem = g - m * per;
+                W = m ? uW : gW;
+                un = units;
+                b = b0 + rem / TILE_ROWS;
+                u = (t * nb + b) * TILE_ROWS + rem % TILE_ROWS;
+                pk = g;
+            };
+            auto stage = [&]() {
+                if (!staged) { X = wave_stage(kind, act, nb, xarea); staged = true; }
+                return X;
+            };
+            run_items<DT, IPL>(nitems - base, map, stage, park);
+        }
+        __syncthreads();
+        if (threadIdx.x < TILE_ROWS) {
+            const int i = threadIdx.x;
+            for (int bl = 0; bl < nbc; bl++) {
+                accg = fmaf(park.da[bl * TILE_ROWS + i], (float)park.is[bl * TILE_ROWS + i], accg);
+                if (AFF) accg = fmaf(-park.dm[bl * TILE_ROWS + i], (float)park.ms[bl * TILE_ROWS + i], accg);
+                const int j = per + bl * TILE_ROWS + i;
+                accu = fmaf(park.da[j], (float)park.is[j], accu);
+                if (AFF) accu = fmaf(-park.dm[j], (float)park.ms[j], accu);
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x < TILE_ROWS)
+        hh[t * TILE_ROWS + threadIdx.x] = accg / (1.0f + expf(-accg)) * accu;   /* silu(g) * u (tlm_model.c:171, 927) */
+}
+
+template <int EDT, int SDT>
+__global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout L, int32_t *ids_out, float *w_out,
+                                                    uint8_t *ws) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int s_ids[MAXK];
-    __shared__ float s_w[MAXK];
-    __shared__ float s_p[2 * MAXE];
-    __shared__ int s_flag;
-    const WsLayout L = ws_layout(d);
+    __shared__ RouteLds s_route;
+    const int te = (int)(d.de / TILE_ROWS), nexp = d.k * te;
+    const bool shared = SDT != NONE && (int)blockIdx.x >= nexp;
+    if constexpr (SDT != NONE) {
+        if (shared) {
+            const int t = (int)blockIdx.x - nexp;
+            float *hh = (float *)(ws + L.hh) + (size_t)d.k * d.de;
+            gateup_tile<SDT>(d, (const uint8_t *)d.sg, (const uint8_t *)d.su, ws + L.xs, d.ds, t, hh, lds);
+            return;
+        }
+    }
+    const int r = (int)blockIdx.x / te, t = (int)blockIdx.x - r * te;
+    LAS RouteLds *R = (LAS RouteLds *)&s_route;
+    route_group(d, (const GAS float *)(ws + L.logits), R);
+    if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
+        const int q = threadIdx.x;
+        ws_ids(ws, L)[q] = R->ids[q];
+        ws_w(ws, L)[q] = R->w[q];
+        if (ids_out) ids_out[q] = R->ids[q];
+        if (w_out) w_out[q] = R->w[q];
+    }
+    const int e = R->ids[r];
+    float *hh = (float *)(ws + L.hh) + (size_t)r * d.de;
+    gateup_tile<EDT>(d, (const uint8_t *)d.experts[3 * e + 0], (const uint8_t *)d.experts[3 * e + 1], ws + L.xe,
+                     d.de, t, hh, lds);
+}
 
-    const int64_t te = d.de / TILE_ROWS, nexp = (int64_t)d.k * te;
-    const bool shared = (int64_t)blockIdx.x >= nexp;
-    const int dt = shared ? d.shared_dt : d.expert_dt;
-    const int kind = dt_act_kind(dt);
-    const int64_t F = shared ? d.ds : d.de;
-    const int r = shared ? d.k : (int)(blockIdx.x / te);
-    const int64_t t = shared ? (int64_t)blockIdx.x - nexp : (int64_t)blockIdx.x % te;
-    const int nb = (int)(d.D / dt_block_values(dt));
-
-    const XLds X = stage_act(kind, ws + (shared ? L.xs : L.xe), nb, lds);
-    const size_t off = (stage_bytes(kind, nb) + 15) & ~(size_t)15;
-    int32_t *g_is = (int32_t *)(lds + off), *g_ms = g_is + nb * TILE_ROWS;
-    float *g_da = (float *)(g_ms + nb * TILE_ROWS), *g_dm = g_da + nb * TILE_ROWS;
-    int32_t *u_is = (int32_t *)(g_dm + nb * TILE_ROWS), *u_ms = u_is + nb * TILE_ROWS;
-    float *u_da = (float *)(u_ms + nb * TILE_ROWS), *u_dm = u_da + nb * TILE_ROWS;
-
-    if (!shared && threadIdx.x < 64) {
-        route_wave(d, (const float *)(ws + L.logits), s_ids, s_w, s_p);
-        if (blockIdx.x == 0 && threadIdx.x == 0) {
-            for (int q = 0; q < d.k; q++) {
-                ws_ids(ws, L)[q] = s_ids[q];
-                ws_w(ws, L)[q] = s_w[q];
-                if (ids_out) ids_out[q] = s_ids[q];
-                if (w_out) w_out[q] = s_w[q];
+/* ======================================================================
+ * K3: down.  Group = (rank, 16-row tile); wave w owns block column(s)
+ * c = w*CPW .. w*CPW+CPW-1 (CPW = 64 / (16*LPI): 1 for the 256-value
+ * formats, 2 for Q8_0): one item per lane, its own activation block(s).
+ * ==================================================================== */
+template <int DT>
+__device__ void down_tile(const tlm_hip_moe_desc &d, const uint8_t *W, const float *hsrc, int64_t F, int64_t t,
+                          float *out, uint8_t *lds) {
+    using Fm = Packed<DT>;
+    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
+    constexpr int kind = DT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
+    constexpr int BV = Fm::BV, CPW = 64 / (TILE_ROWS * Fm::LPI);
+    const int nb = (int)(F / BV);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int q = lane % Fm::LPI, slot = lane / Fm::LPI;               /* slot: 16*CPW items per wave */
+    const int64_t T = (d.D + TILE_ROWS - 1) / TILE_ROWS, units = T * nb * TILE_ROWS;
+    /* LDS: the whole activation (split layout) shared by the waves, then the park */
+    uint8_t *xarea = lds;
+    const XLds X = xlds_at(kind, nb, xarea);
+    const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), nb * TILE_ROWS);
+    LAS uint32_t *qx = (LAS uint32_t *)xarea;
+    LAS int16_t *bsx = (LAS int16_t *)(xarea + nb * 256);
+    LAS float *dx = (LAS float *)(xarea + nb * BV + (kind == DT_Q8_K ? nb * 32 : 0));
+    const GAS float *hg = (const GAS float *)hsrc;
+    for (int c0 = wave * CPW; c0 < nb; c0 += nw * CPW) {
+        const int b = c0 + slot / TILE_ROWS, i = slot % TILE_ROWS;
+        const bool live = b < nb;
+        typename Fm::Raw raw;
+        if (live) raw = Fm::load(W, units, (t * nb + b) * TILE_ROWS + i, q);
+        /* quantise this wave's block(s) of h while the loads are in flight */
+        if (kind == DT_Q8_K) {
+            const f32x4 v = *(const GAS f32x4 *)(hg + (int64_t)c0 * 256 + 4 * lane);
+            quant_block_to(kind, v, true, lane, qx, bsx, dx, c0);
+        } else {
+            const int bq = c0 + (lane >> 3), sub = lane & 7;
+            const bool ok = (lane >> 3) < CPW && bq < nb;
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (ok) v = *(const GAS f32x4 *)(hg + (int64_t)bq * 32 + 4 * sub);
+            quant_block_to(kind, v, ok, sub, qx, bsx, dx, bq);
+        }
+        wave_sync();
+        if (live) {
+            int32_t is, ms;
+            float dA, dM;
+            Fm::compute(raw, X, b, q, is, ms, dA, dM);
+            if (q == 0) {
+                park.is[b * TILE_ROWS + i] = is;
+                park.da[b * TILE_ROWS + i] = dA;
+                if (AFF) { park.ms[b * TILE_ROWS + i] = ms; park.dm[b * TILE_ROWS + i] = dM; }
             }
         }
     }
     __syncthreads();
-
-    const uint8_t *gW, *uW;
-    if (shared) {
-        gW = (const uint8_t *)d.sg;
-        uW = (const uint8_t *)d.su;
-    } else {
-        const int e = s_ids[r];
-        gW = (const uint8_t *)d.experts[3 * e + 0];
-        uW = (const uint8_t *)d.experts[3 * e + 1];
-    }
-    tile_items_dt(dt, gW, F, nb, t, X, g_is, g_ms, g_da, g_dm);
-    tile_items_dt(dt, uW, F, nb, t, X, u_is, u_ms, u_da, u_dm);
-    __syncthreads();
-
-    float *hh = (float *)(ws + L.hh) + (size_t)r * d.de;
     if (threadIdx.x < TILE_ROWS) {
-        const int i = threadIdx.x;
-        float g = tile_chain(dt, nb, i, g_is, g_ms, g_da, g_dm);
-        float u = tile_chain(dt, nb, i, u_is, u_ms, u_da, u_dm);
-        hh[t * TILE_ROWS + i] = g / (1.0f + expf(-g)) * u;   /* silu(g) * u (src/lib/tlm_model.c:171, 927) */
+        const int64_t row = t * TILE_ROWS + threadIdx.x;
+        float acc = park_chain<AFF>(park, nb, threadIdx.x);
+        if (row < d.D) out[row] = acc;
     }
+}
 
-    /* the group that completes a quantisation block of h quantises it */
-    const int qbv = kind == DT_Q8_K ? 256 : 32;
-    const int64_t qb = (t * TILE_ROWS) / qbv;
-    const int64_t qend = (qb + 1) * qbv < F ? (qb + 1) * qbv : F;
-    const int need = (int)((qend - qb * qbv + TILE_ROWS - 1) / TILE_ROWS);
-    int32_t *cnt = (int32_t *)(ws + L.cnt_h) + (shared ? (int64_t)d.k * L.nqe : (int64_t)r * L.nqe) + qb;
-    if (arrive_last(cnt, need, &s_flag) && threadIdx.x < 64)
-        quant_block_wave(kind, hh + qb * qbv, (int)(qend - qb * qbv),
-                         ws + hq_off(d, L, r) + (size_t)qb * (qbv == 256 ? 292 : 36));
+template <int EDT, int SDT>
+__global__ __launch_bounds__(1024) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, uint8_t *ws) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int TD = (int)(d.D / TILE_ROWS), nexp = d.k * TD;
+    if constexpr (SDT != NONE) {
+        if ((int)blockIdx.x >= nexp) {
+            const int t = (int)blockIdx.x - nexp;
+            down_tile<SDT>(d, (const uint8_t *)d.sd, (const float *)(ws + L.hh) + (size_t)d.k * d.de, d.ds, t,
+                           (float *)(ws + L.so), lds);
+            return;
+        }
+    }
+    const int r = (int)blockIdx.x / TD, t = (int)blockIdx.x - r * TD;
+    int e = ws_ids(ws, L)[r];
+    if (e < 0 || e >= d.E) e = 0;   /* only reachable if phase 3 runs before any phase 2 */
+    down_tile<EDT>(d, (const uint8_t *)d.experts[3 * e + 2], (const float *)(ws + L.hh) + (size_t)r * d.de, d.de, t,
+                   (float *)(ws + L.eo) + (size_t)r * d.D, lds);
 }
 
 /* ======================================================================
- * K3: down + rank-order combine + residual
- * grid: k * D/16 expert tiles (rank-major), then D/16 shared tiles
+ * K4: rank-order combine + residual (src/lib/tlm_model.c:1029-1050)
  * ==================================================================== */
-__global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, float *__restrict__ h, uint8_t *ws) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int s_flag;
-    const WsLayout L = ws_layout(d);
-    const int64_t TD = (d.D + TILE_ROWS - 1) / TILE_ROWS, nexp = (int64_t)d.k * TD;
-    const bool shared = (int64_t)blockIdx.x >= nexp;
-    const int dt = shared ? d.shared_dt : d.expert_dt;
-    const int kind = dt_act_kind(dt);
-    const int64_t F = shared ? d.ds : d.de;
-    const int r = shared ? d.k : (int)(blockIdx.x / TD);
-    const int64_t t = shared ? (int64_t)blockIdx.x - nexp : (int64_t)blockIdx.x % TD;
-    const int nb = (int)(F / dt_block_values(dt));
-
-    const XLds X = stage_act(kind, ws + hq_off(d, L, r), nb, lds);
-    const size_t off = (stage_bytes(kind, nb) + 15) & ~(size_t)15;
-    int32_t *l_is = (int32_t *)(lds + off), *l_ms = l_is + nb * TILE_ROWS;
-    float *l_da = (float *)(l_ms + nb * TILE_ROWS), *l_dm = l_da + nb * TILE_ROWS;
-    __syncthreads();
-
-    int e = shared ? 0 : ws_ids(ws, L)[r];
-    if (e < 0 || e >= d.E) e = 0;   /* only reachable if phase 3 runs before any phase 2 */
-    const uint8_t *W = shared ? (const uint8_t *)d.sd : (const uint8_t *)d.experts[3 * e + 2];
-    tile_items_dt(dt, W, d.D, nb, t, X, l_is, l_ms, l_da, l_dm);
-    __syncthreads();
-    float *out = shared ? (float *)(ws + L.so) : (float *)(ws + L.eo) + (size_t)r * d.D;
-    if (threadIdx.x < TILE_ROWS) {
-        const int64_t row = t * TILE_ROWS + threadIdx.x;
-        float v = tile_chain(dt, nb, threadIdx.x, l_is, l_ms, l_da, l_dm);
-        if (row < d.D) out[row] = v;
-    }
-    const int need = d.k + (d.ds > 0 ? 1 : 0);
-    if (!arrive_last((int32_t *)(ws + L.cnt_t) + t, need, &s_flag) || threadIdx.x >= TILE_ROWS) return;
-
-    /* combine in ascending rank order (src/lib/tlm_model.c:1029-1050) */
-    const int64_t row = t * TILE_ROWS + threadIdx.x;
+__global__ __launch_bounds__(256) void k_moe_combine(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h, uint8_t *ws) {
+    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (row >= d.D) return;
-    const float *eo = (const float *)(ws + L.eo);
-    const float *w = ws_w(ws, L);
-    float ffn = 0.0f;
-    for (int q = 0; q < d.k; q++) {
-        float c = w[q] * eo[(size_t)q * d.D + row];
-        ffn += c;
+    const GAS float *eo = (const GAS float *)(ws + L.eo);
+    const GAS float *w = (const GAS float *)ws_w(ws, L);
+    /* every load first (one round trip), then the sums in rank order */
+    float ev[MAXK], wv[MAXK];
+#pragma unroll
+    for (int q = 0; q < MAXK; q++) {
+        if (q < d.k) {
+            ev[q] = eo[(size_t)q * d.D + row];
+            wv[q] = w[q];
+        }
     }
-    if (d.ds > 0) ffn += *ws_sgate(ws, L) * ((const float *)(ws + L.so))[row];
-    h[row] += ffn;
+    const float hv = h[row];
+    const float so = d.ds > 0 ? ((const GAS float *)(ws + L.so))[row] : 0.0f;
+    const float sg = d.ds > 0 ? *(const GAS float *)ws_sgate(ws, L) : 0.0f;
+    float ffn = 0.0f;
+#pragma unroll
+    for (int q = 0; q < MAXK; q++) {
+        if (q < d.k) {
+            const float c = wv[q] * ev[q];
+            ffn += c;
+        }
+    }
+    if (d.ds > 0) ffn += sg * so;
+    h[row] = hv + ffn;
 }
+
+/* ---- instantiation table: [expert dtype][shared dtype or none] --------------- */
+typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *);
+typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, uint8_t *);
+
+inline int dt_slot(int dt) { return dt == DT_Q6_K ? 0 : dt == DT_Q8_0 ? 1 : dt == DT_Q4_K ? 2 : dt == DT_Q5_K ? 3 : -1; }
+
+#define ROW(K, E) {K<E, NONE>, K<E, DT_Q6_K>, K<E, DT_Q8_0>, K<E, DT_Q4_K>, K<E, DT_Q5_K>}
+const gateup_fn GU[4][5] = {ROW(k_moe_gateup, DT_Q6_K), ROW(k_moe_gateup, DT_Q8_0), ROW(k_moe_gateup, DT_Q4_K),
+                            ROW(k_moe_gateup, DT_Q5_K)};
+const down_fn DN[4][5] = {ROW(k_moe_down, DT_Q6_K), ROW(k_moe_down, DT_Q8_0), ROW(k_moe_down, DT_Q4_K),
+                          ROW(k_moe_down, DT_Q5_K)};
+#undef ROW
 
 }  // namespace
 
 size_t moe_workspace_bytes(const tlm_hip_moe_desc *d) { return d ? ws_layout(*d).total : 0; }
 
-static bool moe_dt_ok(int dt) { return dt == DT_Q6_K || dt == DT_Q8_0 || dt == DT_Q4_K || dt == DT_Q5_K; }
+static bool moe_dt_ok(int dt) { return dt_slot(dt) >= 0; }
 
 int launch_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w, void *ws, hipStream_t s) {
     return launch_moe_phase(d, 0, h, ids, w, ws, s);
 }
 
-/* phase 0 = all three launches */
+static size_t x_area(int kind, int nb) { return (stage_bytes(kind, nb) + 15) & ~(size_t)15; }
+
+/* phase 0 = all launches; 1 router, 2 gate/up, 3 down, 4 combine */
 int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
                      hipStream_t s) {
-    if (phase < 0 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
+    if (phase < 0 || phase > 4) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
     if (!d || !h || !ws) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL argument");
     if ((uintptr_t)ws & 255u) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: workspace must be 256-byte aligned");
     if (d->E <= 0 || d->E > MAXE || d->k <= 0 || d->k > MAXK || d->k > d->E)
@@ -555,6 +690,7 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     if (d->D <= 0 || d->D % TILE_ROWS || d->D % ebv || d->de <= 0 || d->de % TILE_ROWS || d->de % ebv)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: D=%lld de=%lld must be multiples of 16 and of the block",
                            (long long)d->D, (long long)d->de);
+    if (d->ds < 0) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: ds=%lld", (long long)d->ds);
     if (d->ds > 0) {
         const int sbv = dt_block_values(d->shared_dt);
         if (d->ds % TILE_ROWS || d->ds % sbv || d->D % sbv)
@@ -563,27 +699,41 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
         if (!d->sg || !d->su || !d->sd) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: shared matrices missing");
     }
     if (!d->ffn_norm || !d->router_w || !d->experts) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL weights");
+    if (((uintptr_t)h | (uintptr_t)d->ffn_norm) & 15u)
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: h and ffn_norm must be 16-byte aligned");
     const int ek = dt_act_kind(d->expert_dt), sk = d->ds > 0 ? dt_act_kind(d->shared_dt) : ek;
     const int nbe = (int)(d->D / ebv), nbde = (int)(d->de / ebv);
-    const int nbs = d->ds > 0 ? (int)(d->D / dt_block_values(d->shared_dt)) : 0;
-    const int nbsd = d->ds > 0 ? (int)(d->ds / dt_block_values(d->shared_dt)) : 0;
-    size_t lds1 = al256((size_t)d->D * 4) + 64;
-    size_t lds2e = ((stage_bytes(ek, nbe) + 15) & ~(size_t)15) + 2 * park_bytes(nbe);
-    size_t lds2s = d->ds > 0 ? ((stage_bytes(sk, nbs) + 15) & ~(size_t)15) + 2 * park_bytes(nbs) : 0;
-    size_t lds3e = ((stage_bytes(ek, nbde) + 15) & ~(size_t)15) + park_bytes(nbde);
-    size_t lds3s = d->ds > 0 ? ((stage_bytes(sk, nbsd) + 15) & ~(size_t)15) + park_bytes(nbsd) : 0;
+    const int sbv = d->ds > 0 ? dt_block_values(d->shared_dt) : ebv;
+    const int nbs = (int)(d->D / sbv), nbsd = d->ds > 0 ? (int)(d->ds / sbv) : 0;
+    auto park2 = [](int nb) { int cb = nb < PARK_MAX / TILE_ROWS / 2 ? nb : PARK_MAX / TILE_ROWS / 2; return park_bytes(2 * cb * TILE_ROWS); };
+    /* K3 waves: one per CPW block columns (CPW = 4 / LPI), at most 16; wider
+     * matrices loop over their columns */
+    auto waves3 = [](int dt, int nb) { const int cpw = dt == DT_Q8_0 ? 2 : 1; return (nb + cpw - 1) / cpw; };
+    int w3 = waves3(d->expert_dt, nbde);
+    if (d->ds > 0 && waves3(d->shared_dt, nbsd) > w3) w3 = waves3(d->shared_dt, nbsd);
+    if (w3 > 16) w3 = 16;
+    size_t lds1 = al256((size_t)d->D * 8);          /* x and the norm weights */
+    size_t lds2e = NWAVE * x_area(ek, nbe) + park2(nbe);
+    size_t lds2s = d->ds > 0 ? NWAVE * x_area(sk, nbs) + park2(nbs) : 0;
+    size_t lds3e = x_area(ek, nbde) + park_bytes(nbde * TILE_ROWS);
+    size_t lds3s = d->ds > 0 ? x_area(sk, nbsd) + park_bytes(nbsd * TILE_ROWS) : 0;
     size_t lds2 = lds2e > lds2s ? lds2e : lds2s, lds3 = lds3e > lds3s ? lds3e : lds3s;
-    if (lds1 > 60 * 1024 || lds2 > 60 * 1024 || lds3 > 60 * 1024)
+    if (lds1 > 64 * 1024 || lds2 > 64 * 1024 || lds3 > 64 * 1024)
         return tlmh_seterr(TLM_HIP_EUNSUP, "moe_layer: D=%lld / de=%lld exceed the LDS staging limit",
                            (long long)d->D, (long long)d->de);
     uint8_t *w8 = (uint8_t *)ws;
     const tlm_hip_moe_desc dv = *d;
-    const unsigned g1 = (unsigned)((d->E + 7) / 8);
+    const WsLayout L = ws_layout(*d);
+    const int es = dt_slot(d->expert_dt), ss = d->ds > 0 ? 1 + dt_slot(d->shared_dt) : 0;
+    const gateup_fn gu = GU[es][ss];
+    const down_fn dn = DN[es][ss];
+    const unsigned g1 = (unsigned)router_groups(*d);
     const unsigned g2 = (unsigned)(d->k * (d->de / TILE_ROWS) + (d->ds > 0 ? d->ds / TILE_ROWS : 0));
     const unsigned g3 = (unsigned)((d->k + (d->ds > 0 ? 1 : 0)) * (d->D / TILE_ROWS));
-    if (phase == 0 || phase == 1)
-        hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(256), lds1, s, dv, (const float *)h, w8);
-    if (phase == 0 || phase == 2) hipLaunchKernelGGL(k_moe_gateup, dim3(g2), dim3(256), lds2, s, dv, ids, w, w8);
-    if (phase == 0 || phase == 3) hipLaunchKernelGGL(k_moe_down, dim3(g3), dim3(256), lds3, s, dv, h, w8);
+    const unsigned g4 = (unsigned)((d->D + 255) / 256);
+    if (phase == 0 || phase == 1) hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8);
+    if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8);
+    if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(64 * w3), lds3, s, dv, L, w8);
+    if (phase == 0 || phase == 4) hipLaunchKernelGGL(k_moe_combine, dim3(g4), dim3(256), 0, s, dv, L, h, w8);
     return tlmh_check(hipGetLastError(), "moe_layer launch");
 }

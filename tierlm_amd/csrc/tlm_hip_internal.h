@@ -57,18 +57,76 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
 /* Round half to even via 1.5*2^23, clamp to [lo, hi], NaN -> 0
  * (src/lib/tlm_quant.c:233-243).  Built with -ffp-contract=off. */
 __device__ __forceinline__ int rne_clamp(float v, int lo, int hi) {
-    if (v != v) return 0;
-    if (v <= (float)lo) return lo;
-    if (v >= (float)hi) return hi;
+    /* branch-free: the clamped bounds are integers, which the magic-number
+     * rounding returns unchanged */
+    const float t = v != v ? 0.0f : fminf(fmaxf(v, (float)lo), (float)hi);
     const float magic = 12582912.0f;
-    return (int)((v + magic) - magic);
+    return (int)((t + magic) - magic);
 }
+
+/* Address-space qualified pointers.  Pointers that travel through structs,
+ * tables or lambdas lose their address space and compile to flat_* accesses,
+ * which count against both the vector-memory and the LDS wait counters; the
+ * hot loops therefore name global (1) and LDS (3) explicitly. */
+#define GAS __attribute__((address_space(1)))
+#define LAS __attribute__((address_space(3)))
+/* plain clang vectors: loadable through qualified pointers (HIP's uint4 is not) */
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 /* 4 x int8 dot with int32 accumulate (v_dot4_i32_i8): exact. */
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 __device__ __forceinline__ int wave_lane() { return (int)__lane_id(); }
 
+/* ---- wave reductions over DPP -------------------------------------------
+ * Within each 16-lane row: xor-1 and xor-2 quad permutes, then the half-row
+ * and row mirrors (lane i <-> 7-i, i <-> 15-i) pair whole quads and halves,
+ * so every lane ends with its row's value; the four rows are then combined
+ * from lanes 0, 16, 32, 48 through readlane, which leaves the result uniform.
+ * A DPP move costs one VALU op, against an LDS round trip for a shuffle. */
+enum { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+template <int CTRL> __device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = dpp_u32<CTRL>((uint32_t)b), hi = dpp_u32<CTRL>((uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ float rdlane_f32(float v, int l) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), l));
+}
+__device__ __forceinline__ double rdlane_f64(double v, int l) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+/* max over the wave (no NaN inputs) */
+__device__ __forceinline__ float wave_max_f32(float v) {
+    float o;
+    o = dpp_f32<DPP_XOR1>(v);        v = o > v ? o : v;
+    o = dpp_f32<DPP_XOR2>(v);        v = o > v ? o : v;
+    o = dpp_f32<DPP_HALF_MIRROR>(v); v = o > v ? o : v;
+    o = dpp_f32<DPP_MIRROR>(v);      v = o > v ? o : v;
+    const float a = rdlane_f32(v, 0), b = rdlane_f32(v, 16), c = rdlane_f32(v, 32), d = rdlane_f32(v, 48);
+    const float ab = b > a ? b : a, cd = d > c ? d : c;
+    return cd > ab ? cd : ab;
+}
+/* sum over the wave, fixed tree: ((row0 + row1) + (row2 + row3)) */
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_f64<DPP_XOR1>(v);
+    v += dpp_f64<DPP_XOR2>(v);
+    v += dpp_f64<DPP_HALF_MIRROR>(v);
+    v += dpp_f64<DPP_MIRROR>(v);
+    return (rdlane_f64(v, 0) + rdlane_f64(v, 16)) + (rdlane_f64(v, 32) + rdlane_f64(v, 48));
+}
 /* ---- launchers (defined in the .hip files) ------------------------------ */
 int launch_quantize_act(int kind, const float *x, int64_t n, void *dst, hipStream_t s);
 int launch_matvec_plain(int dt, const void *W, size_t row_bytes, const void *act, float *y,
