@@ -191,7 +191,7 @@ def main():
         b(hr.clone())
     torch.cuda.synchronize()
     ph = []
-    for p in range(1, 5):
+    for p in range(1, 4):
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -215,12 +215,12 @@ def main():
             best = us if best is None else min(best, us)
         ph.append(best)
         del g
-    p1, p2, p3, p4 = ph
+    p1, p2, p3 = ph
     gu_gbs = GATEUP_BYTES / (p2 * 1e-6) / 1e9
     dn_gbs = DOWN_BYTES / (p3 * 1e-6) / 1e9
     expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
     log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); per launch: router {p1:.2f} us, "
-        f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down {p3:.2f} us ({dn_gbs:.0f} GB/s), combine {p4:.2f} us")
+        f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down+combine {p3:.2f} us ({dn_gbs:.0f} GB/s)")
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
@@ -243,8 +243,8 @@ def main():
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "k_moe_gateup (routing + gate/up of the top-8 experts + SwiGLU)",
                      "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(p2, 3),
-                     "down_kernel_GBps": round(dn_gbs, 1), "down_avg_launch_us": round(p3, 3),
-                     "router_avg_launch_us": round(p1, 3), "combine_avg_launch_us": round(p4, 3),
+                     "down_combine_GBps": round(dn_gbs, 1), "down_combine_avg_launch_us": round(p3, 3),
+                     "router_avg_launch_us": round(p1, 3),
                      "timing": "HIP events around a graph of R back-to-back launches of the phase (R = roofline_launches), / R",
                      "roofline_launches": R,
                      "expert_gemv_GBps": round(expert_gbs, 1), "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4)},

@@ -146,10 +146,9 @@ int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *
  * 921, 937-1050):
  *   phase 1: rmsnorm + router logits + activation quantisation
  *   phase 2: routing + gate/up + SwiGLU
- *   phase 3: h quantisation + down
- *   phase 4: rank-order combine + residual update.
- * Phases must run in order on one stream.  Re-running phases 1-3 reproduces
- * the same bits; re-running phase 4 adds the FFN output to h once more. */
+ *   phase 3: h quantisation + down + rank-order combine + residual update.
+ * Phases must run in order on one stream.  Re-running phases 1-2 reproduces
+ * the same bits; re-running phase 3 adds the FFN output to h once more. */
 int tlm_hip_moe_layer_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w,
                             void *workspace, void *stream);
 

@@ -91,7 +91,7 @@ def test_host_checks_reject_bad_arguments_without_launching():
     d = MoeDesc()
     d.E, d.k, d.D, d.de = 0, 8, 2048, 768
     assert lib.tlm_hip_moe_layer(C.byref(d), C.c_void_p(16), None, None, C.c_void_p(256), None) == -3
-    assert lib.tlm_hip_moe_layer_phase(C.byref(d), 5, C.c_void_p(16), None, None, C.c_void_p(256), None) == -3
+    assert lib.tlm_hip_moe_layer_phase(C.byref(d), 4, C.c_void_p(16), None, None, C.c_void_p(256), None) == -3
     assert lib.tlm_hip_packed_bytes(14, 768, 2048) == 768 * 8 * 210
     assert lib.tlm_hip_packed_bytes(14, 37, 256) == 48 * 210        # last tile padded to 16 rows
     assert lib.tlm_hip_packed_bytes(14, 16, 100) == 0

@@ -1,4 +1,4 @@
-/* hip_moe.hip - one routed MoE block on device in four launches
+/* hip_moe.hip - one routed MoE block on device in three launches
  * (src/lib/tlm_model.c:940-1055, run_batch :900-938, route :798-839).
  *
  *   K1 moe_router   one wave per work-group, two router rows each.  Every
@@ -15,19 +15,16 @@
  *                   flight, copies the activation into its own LDS while they
  *                   land, computes, and the group writes h = silu(g) * u for
  *                   its 16 rows.
- *   K3 moe_down     one group per (rank, 16-row tile) of down, then shared;
- *                   wave w owns block column(s) w: it puts its weight loads in
- *                   flight, quantises its block(s) of h (the reference's
- *                   activation rule) into LDS, computes; the group then runs
- *                   the 16 row chains and writes the rows.
- *   K4 moe_combine  ffn = sum_r w_r * eo_r in ascending rank order (+ gated
- *                   shared output), h += ffn.
+ *   K3 moe_down     one group per 8 rows of D: quantises every rank's h (the
+ *                   reference's activation rule) into LDS while its down-row
+ *                   loads are in flight, computes, and adds
+ *                   sum_r w_r * out_r (+ gate * shared) to h in rank order.
  * No launch hands data between its own work-groups, so no cross-XCD cache
  * maintenance is needed inside a kernel.  The kernels are instantiated per
- * (expert dtype, shared dtype) so each holds one or two item paths only: the
- * four launches then fit the instruction cache together.  Integer sums,
- * per-row fma chains, activation quantisation and the combine order are the
- * reference's; expf and rmsnorm's double sum of squares are the device's. */
+ * (expert dtype, shared dtype) so each holds one or two item paths only.
+ * Integer sums, per-row fma chains, activation quantisation and the combine
+ * order are the reference's; expf and rmsnorm's double sum of squares are the
+ * device's. */
 #include "tlm_hip_internal.h"
 #include "tlm_hip_items.h"
 
@@ -46,7 +43,7 @@ __host__ __device__ constexpr int bvals(int kind) { return kind == DT_Q8_K ? 256
 /* ---- workspace layout (256-byte aligned regions), computed on the host and
  * passed to every kernel --------------------------------------------------- */
 struct WsLayout {
-    size_t xb, xe, xs, logits, route, hh, eo, so, total;
+    size_t xb, xe, xs, logits, route, hh, total;
 };
 
 __host__ __device__ inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -62,8 +59,6 @@ inline WsLayout ws_layout(const tlm_hip_moe_desc &d) {
     L.logits = o; o += al256((size_t)d.E * 4);
     L.route = o;  o += 512;                        /* ids int32[32] at +0, w f32[32] at +128, sgate at +256 */
     L.hh = o;     o += al256((size_t)(d.k * d.de + d.ds) * 4);
-    L.eo = o;     o += al256((size_t)d.k * d.D * 4);
-    L.so = o;     o += al256((size_t)d.D * 4);
     L.total = o;
     return L;
 }
@@ -107,7 +102,7 @@ template <int WIDTH> __device__ __forceinline__ uint32_t group_or_u32(uint32_t v
 /* ---- activation rule (src/lib/tlm_quant.c:458-478) for this lane's 4 values
  * of a block spread over WIDTH lanes: d, and the 4 codes packed in a dword --- */
 template <int WIDTH>
-__device__ __forceinline__ float act_rule4(f32x4 v, bool ok, uint32_t &codes) {
+__device__ __attribute__((noinline)) float act_rule4(f32x4 v, bool ok, uint32_t &codes) {
     /* |v| as bits: for non-negative floats the unsigned order is the float
      * order; above 0x7F800000 is NaN, equal is infinity */
     uint32_t am = 0, fl = 0;
@@ -166,6 +161,80 @@ __device__ __forceinline__ void quant_block_to(int kind, f32x4 v, bool ok, int s
     }
 }
 
+/* Codes of 16 values for a block whose amax is below 2^-100, where 127/amax
+ * is taken in double (src/lib/tlm_quant.c:466-471).  Out of line: it is never
+ * reached by ordinary activations, and a call waits for every load in flight. */
+__device__ __attribute__((noinline)) u32x4 tiny_codes16(f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3, float amax) {
+    const double id = 127.0 / (double)amax;
+    const f32x4 v[4] = {v0, v1, v2, v3};
+    u32x4 c = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int t = 0; t < 16; t++)
+        c[t >> 2] |= (uint32_t)(uint8_t)(int8_t)rne_clamp((float)((double)v[t >> 2][t & 3] * id), -127, 127)
+                     << (8 * (t & 3));
+    return c;
+}
+
+/* The activation rule with 16 contiguous values per lane and a block spread
+ * over WIDTH lanes of one DPP row (16 for Q8_K, 2 for a8).  Returns d and
+ * the 16 codes packed in c[0..3]. */
+template <int WIDTH>
+__device__ __forceinline__ float act_rule16(const f32x4 (&v)[4], bool ok, u32x4 &c) {
+    uint32_t am = 0, fl = 0;
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+        const uint32_t b = ok ? (__float_as_uint(v[t >> 2][t & 3]) & 0x7FFFFFFFu) : 0u;
+        fl |= (b > 0x7F800000u ? 1u : 0u) | (b == 0x7F800000u ? 2u : 0u);
+        const uint32_t f = b < 0x7F800000u ? b : 0u;
+        am = f > am ? f : am;
+    }
+    am = group_max_u32<WIDTH>(am);
+    fl = group_or_u32<WIDTH>(fl);
+    const float amax = __uint_as_float(am);
+    c = u32x4{0u, 0u, 0u, 0u};
+    if (fl) return (fl & 1u) ? __uint_as_float(0x7FC00000u) : INFINITY;
+    if (!(amax > 0.0f) || !ok) return amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float d = amax / 127.0f;
+    if (amax >= 0x1p-100f) {
+        const float id = 127.0f / amax;
+#pragma unroll
+        for (int t = 0; t < 16; t++)
+            c[t >> 2] |= (uint32_t)(uint8_t)(int8_t)rne_clamp(v[t >> 2][t & 3] * id, -127, 127) << (8 * (t & 3));
+    } else {
+        c = tiny_codes16(v[0], v[1], v[2], v[3], amax);
+    }
+    return d;
+}
+
+/* Quantise block b (this lane: values 16*sub..16*sub+15) into the split
+ * layout (q codes, bs bsums, dd scales).  Q8_K: 16 lanes per block, and a
+ * lane's 16 codes are exactly bsum group sub; a8: 2 lanes per block. */
+__device__ __forceinline__ void quant16_to(int kind, const f32x4 (&v)[4], bool ok, int sub, LAS uint8_t *q,
+                                           LAS int16_t *bs, LAS float *dd, int b) {
+    u32x4 c;
+    if (kind == DT_Q8_K) {
+        const float d = act_rule16<16>(v, ok, c);
+        if (ok) {
+            *(LAS u32x4 *)(q + b * 256 + 16 * sub) = c;
+            bs[b * 16 + sub] = (int16_t)(byte_sum(c.x) + byte_sum(c.y) + byte_sum(c.z) + byte_sum(c.w));
+            if (sub == 0) dd[b] = d;
+        }
+    } else {
+        const float d = act_rule16<2>(v, ok, c);
+        if (ok) {
+            *(LAS u32x4 *)(q + b * 32 + 16 * sub) = c;
+            if (sub == 0) dd[b] = d;
+        }
+    }
+}
+
+__device__ __attribute__((noinline)) void quant16_to_ool(int kind, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3, bool ok,
+                                                        int sub, LAS uint8_t *q, LAS int16_t *bs, LAS float *dd,
+                                                        int b) {
+    const f32x4 v[4] = {v0, v1, v2, v3};
+    quant16_to(kind, v, ok, sub, q, bs, dd, b);
+}
+
 /* ---- routing by the group (src/lib/tlm_model.c:776-839) --------------------
  * 256 threads; thread t owns expert t.  Every valid entry (unmasked, selection
  * value not NaN) gets a 64-bit key: the order-preserving bits of its value,
@@ -190,8 +259,11 @@ __device__ __forceinline__ uint32_t ord_bits(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-/* ids / weights land in R->ids[0..k), R->w[0..k), readable by every thread. */
-__device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, LAS RouteLds *R) {
+/* ids / weights land in R->ids[0..k), R->w[0..k), readable by every thread.
+ * stash() runs in every thread before a group barrier, once the softmax is
+ * done: a place for LDS writes of values loaded at kernel entry. */
+template <class Stash>
+__device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, LAS RouteLds *R, Stash stash) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, E = d.E, k = d.k;
     const bool sig = d.router == 2;
     const bool in = t < E;
@@ -223,6 +295,7 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
         valid ? ((unsigned long long)ord_bits(sel) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)t) : 0ull;
     R->key[t] = key;
     R->p[t] = p;
+    stash();
     const int nv_wave = __builtin_popcountll(__ballot(valid));   /* whole wave active here */
     if (lane == 0) R->redi[wave] = nv_wave;
     __syncthreads();
@@ -312,9 +385,13 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
     const GAS f32x4 *h4 = (const GAS f32x4 *)hptr, *n4 = (const GAS f32x4 *)d.ffn_norm;
     const int64_t nfull = D / RCHV, ctail = nfull * RCHV;
 
-    /* the first full chunk and the partial last chunk in flight before the norm */
-    float va[RCH], vb[RCH], vt[RCH];
-    if (nfull > 0) load_chunk<false>(va, wr, 0, hl, D);
+    /* the first four full chunks (2048 values of the row) and the partial
+     * last chunk in flight before the norm */
+    float v0[RCH], v1[RCH], v2[RCH], v3[RCH], vt[RCH];
+    if (nfull > 0) load_chunk<false>(v0, wr, 0, hl, D);
+    if (nfull > 1) load_chunk<false>(v1, wr, RCHV, hl, D);
+    if (nfull > 2) load_chunk<false>(v2, wr, 2 * RCHV, hl, D);
+    if (nfull > 3) load_chunk<false>(v3, wr, 3 * RCHV, hl, D);
     if (ctail < D) load_chunk<true>(vt, wr, ctail, hl, D);
 
     /* rmsnorm (src/lib/tlm_model.c:164-169): sum of squares in double, lane
@@ -356,16 +433,25 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
     const LAS float *xb = (const LAS float *)lds;
 
     /* router row: element i -> lane i mod 32, fmaf in element order, then the
-     * reduce32 tree (src/lib/tlm_quant.c:724-738); full chunks double-buffered */
+     * reduce32 tree (src/lib/tlm_quant.c:724-738); each buffer is refilled
+     * four chunks ahead as soon as it is consumed */
     float r = 0.0f;
-    int64_t c = 0;
-    for (; c + 1 < nfull; c += 2) {
-        load_chunk<false>(vb, wr, (c + 1) * RCHV, hl, D);
-        r = fma_chunk<false>(va, xb, c * RCHV, hl, D, r);
-        if (c + 2 < nfull) load_chunk<false>(va, wr, (c + 2) * RCHV, hl, D);
-        r = fma_chunk<false>(vb, xb, (c + 1) * RCHV, hl, D, r);
+    for (int64_t c = 0; c < nfull; c += 4) {
+        r = fma_chunk<false>(v0, xb, c * RCHV, hl, D, r);
+        if (c + 4 < nfull) load_chunk<false>(v0, wr, (c + 4) * RCHV, hl, D);
+        if (c + 1 < nfull) {
+            r = fma_chunk<false>(v1, xb, (c + 1) * RCHV, hl, D, r);
+            if (c + 5 < nfull) load_chunk<false>(v1, wr, (c + 5) * RCHV, hl, D);
+        }
+        if (c + 2 < nfull) {
+            r = fma_chunk<false>(v2, xb, (c + 2) * RCHV, hl, D, r);
+            if (c + 6 < nfull) load_chunk<false>(v2, wr, (c + 6) * RCHV, hl, D);
+        }
+        if (c + 3 < nfull) {
+            r = fma_chunk<false>(v3, xb, (c + 3) * RCHV, hl, D, r);
+            if (c + 7 < nfull) load_chunk<false>(v3, wr, (c + 7) * RCHV, hl, D);
+        }
     }
-    if (c < nfull) r = fma_chunk<false>(va, xb, c * RCHV, hl, D, r);
     if (ctail < D) r = fma_chunk<true>(vt, xb, ctail, hl, D, r);
     /* lane 0 of each half ends with ((r0 + r16) + (r8 + r24)) + ...: the
      * reference's pairing (i, i+16), (i, i+8), (i, i+4), (i, i+2), (i, i+1);
@@ -524,7 +610,16 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
     }
     const int r = (int)blockIdx.x / te, t = (int)blockIdx.x - r * te;
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
-    route_group(d, (const GAS float *)(ws + L.logits), R);
+    /* every expert's gate / up matrix, loaded with the logits and parked in
+     * LDS during routing, so the chosen one costs no extra round trip */
+    __shared__ const uint8_t *s_gate[MAXE], *s_up[MAXE];
+    const int tid = threadIdx.x;
+    const uint8_t *tg = tid < d.E ? (const uint8_t *)d.experts[3 * tid + 0] : nullptr;
+    const uint8_t *tu = tid < d.E ? (const uint8_t *)d.experts[3 * tid + 1] : nullptr;
+    route_group(d, (const GAS float *)(ws + L.logits), R, [&]() {
+        s_gate[tid] = tg;
+        s_up[tid] = tu;
+    });
     if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
         const int q = threadIdx.x;
         ws_ids(ws, L)[q] = R->ids[q];
@@ -534,124 +629,173 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
     }
     const int e = R->ids[r];
     float *hh = (float *)(ws + L.hh) + (size_t)r * d.de;
-    gateup_tile<EDT>(d, (const uint8_t *)d.experts[3 * e + 0], (const uint8_t *)d.experts[3 * e + 1], ws + L.xe,
-                     d.de, t, hh, lds);
+    gateup_tile<EDT>(d, s_gate[e], s_up[e], ws + L.xe, d.de, t, hh, lds);
 }
 
 /* ======================================================================
- * K3: down.  Group = (rank, 16-row tile); wave w owns block column(s)
- * c = w*CPW .. w*CPW+CPW-1 (CPW = 64 / (16*LPI): 1 for the 256-value
- * formats, 2 for Q8_0): one item per lane, its own activation block(s).
+ * K3: down + rank-order combine + residual (src/lib/tlm_model.c:921-937,
+ * 1029-1050).  Group = 8 rows of D for every rank (and the shared expert):
+ * it quantises all ranks' h itself (the reference's activation rule, one
+ * block per wave or 8 blocks per wave for Q8_0), streams the ranks' down rows
+ * for its 8 rows, and finishes h[row] += sum_r w_r * out_r (+ gate * shared)
+ * in rank order, so no launch or group waits for another's rows.
  * ==================================================================== */
-template <int DT>
-__device__ void down_tile(const tlm_hip_moe_desc &d, const uint8_t *W, const float *hsrc, int64_t F, int64_t t,
-                          float *out, uint8_t *lds) {
+constexpr int DROWS = 8;   /* rows of D per K3 group: half a packed tile */
+
+/* Rows row0..row0+7 of nmat matrices F wide (matrix r = wptr(r), activation
+ * r = hsrc + r*F); parks (matrix, block, row) results at
+ * ((r * nb + b) << 3) + i.  xarea: the activations of all matrices in the split
+ * layout; pre() runs once the activation loads are out (all threads call it);
+ * the group synchronises before the first compute. */
+template <int DT, class WPtr, class Pre>
+__device__ void down_rows(int nmat, WPtr wptr, Pre pre, const float *hsrc, int64_t F, int64_t D, int64_t row0,
+                          uint8_t *xarea, Park park) {
     using Fm = Packed<DT>;
-    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
     constexpr int kind = DT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
-    constexpr int BV = Fm::BV, CPW = 64 / (TILE_ROWS * Fm::LPI);
-    const int nb = (int)(F / BV);
+    constexpr int BV = Fm::BV, IPL = DT == DT_Q8_0 ? 8 : 4;
+    constexpr int LPB = kind == DT_Q8_K ? 16 : 2;  /* lanes per activation block, 16 values each */
+    constexpr int BPW = 64 / LPB;                   /* activation blocks per wave per pass */
+    constexpr int QB = 2;                           /* passes whose loads go out first */
+    const int nb = (int)(F / BV), nq = nmat * nb, nitems = nq * DROWS;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    const int q = lane % Fm::LPI, slot = lane / Fm::LPI;               /* slot: 16*CPW items per wave */
-    const int64_t T = (d.D + TILE_ROWS - 1) / TILE_ROWS, units = T * nb * TILE_ROWS;
-    /* LDS: the whole activation (split layout) shared by the waves, then the park */
-    uint8_t *xarea = lds;
-    const XLds X = xlds_at(kind, nb, xarea);
-    const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), nb * TILE_ROWS);
-    LAS uint32_t *qx = (LAS uint32_t *)xarea;
-    LAS int16_t *bsx = (LAS int16_t *)(xarea + nb * 256);
-    LAS float *dx = (LAS float *)(xarea + nb * BV + (kind == DT_Q8_K ? nb * 32 : 0));
+    const int slots = (int)blockDim.x / Fm::LPI;
+    const int64_t units = (D / TILE_ROWS) * nb * TILE_ROWS;
+    const int64_t t = row0 / TILE_ROWS, i0 = row0 % TILE_ROWS;
+    const XLds X = xlds_at(kind, nq, xarea);
+    LAS uint8_t *qx = (LAS uint8_t *)xarea;
+    LAS int16_t *bsx = (LAS int16_t *)(xarea + nq * 256);
+    LAS float *dx = (LAS float *)(xarea + nq * BV + (kind == DT_Q8_K ? nq * 32 : 0));
     const GAS float *hg = (const GAS float *)hsrc;
-    for (int c0 = wave * CPW; c0 < nb; c0 += nw * CPW) {
-        const int b = c0 + slot / TILE_ROWS, i = slot % TILE_ROWS;
-        const bool live = b < nb;
-        typename Fm::Raw raw;
-        if (live) raw = Fm::load(W, units, (t * nb + b) * TILE_ROWS + i, q);
-        /* quantise this wave's block(s) of h while the loads are in flight */
-        if (kind == DT_Q8_K) {
-            const f32x4 v = *(const GAS f32x4 *)(hg + (int64_t)c0 * 256 + 4 * lane);
-            quant_block_to(kind, v, true, lane, qx, bsx, dx, c0);
-        } else {
-            const int bq = c0 + (lane >> 3), sub = lane & 7;
-            const bool ok = (lane >> 3) < CPW && bq < nb;
-            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (ok) v = *(const GAS f32x4 *)(hg + (int64_t)bq * 32 + 4 * sub);
-            quant_block_to(kind, v, ok, sub, qx, bsx, dx, bq);
+    /* activation block of pass m for this lane (blocks of all matrices are
+     * contiguous in h: block j starts at value j * BV); the lane takes values
+     * 16*sub..16*sub+15 of it */
+    const int sub = lane % LPB;
+    auto qblock = [&](int m) { return (wave + nw * m) * BPW + lane / LPB; };
+    auto qload = [&](int m, f32x4 (&v)[4]) {
+        const int j = qblock(m);
+        if (j < nq) {
+            const GAS f32x4 *src = (const GAS f32x4 *)(hg + (int64_t)j * BV + 16 * sub);
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = src[u];
         }
-        wave_sync();
-        if (live) {
-            int32_t is, ms;
-            float dA, dM;
-            Fm::compute(raw, X, b, q, is, ms, dA, dM);
-            if (q == 0) {
-                park.is[b * TILE_ROWS + i] = is;
-                park.da[b * TILE_ROWS + i] = dA;
-                if (AFF) { park.ms[b * TILE_ROWS + i] = ms; park.dm[b * TILE_ROWS + i] = dM; }
+    };
+    f32x4 hv[QB][4];
+#pragma unroll
+    for (int m = 0; m < QB; m++) qload(m, hv[m]);
+    pre();   /* with the activation loads in flight */
+    auto quant = [&](int m, const f32x4 (&v)[4]) { quant16_to(kind, v, qblock(m) < nq, sub, qx, bsx, dx, qblock(m)); };
+    for (int base = 0; base < nitems; base += slots * IPL) {
+        auto map = [&](int it, const uint8_t *&W, int64_t &un, int64_t &u, int &b, int &pk) {
+            const int g = base + it, i = g & (DROWS - 1), j = g >> 3;
+            const int r = j / nb, blk = j - r * nb;
+            W = wptr(r);
+            un = units;
+            u = (t * nb + blk) * TILE_ROWS + i0 + i;
+            b = j;
+            pk = g;
+        };
+        auto stage = [&]() {
+            if (base == 0) {
+#pragma unroll
+                for (int m = 0; m < QB; m++) quant(m, hv[m]);
+                for (int m = QB; (wave + nw * m) * BPW < nq; m++) {   /* wider than QB passes */
+                    f32x4 v[4];
+                    qload(m, v);
+                    quant16_to_ool(kind, v[0], v[1], v[2], v[3], qblock(m) < nq, sub, qx, bsx, dx, qblock(m));
+                }
+                __syncthreads();
             }
-        }
+            return X;
+        };
+        run_items<DT, IPL>(nitems - base, map, stage, park);
     }
-    __syncthreads();
-    if (threadIdx.x < TILE_ROWS) {
-        const int64_t row = t * TILE_ROWS + threadIdx.x;
-        float acc = park_chain<AFF>(park, nb, threadIdx.x);
-        if (row < d.D) out[row] = acc;
+}
+
+/* Row i's result for matrix r: the block chain in ascending order. */
+template <int DT>
+__device__ __forceinline__ float down_chain(const Park &k, int r, int nb, int i) {
+    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const int p = ((r * nb + b) << 3) + i;
+        acc = fmaf(k.da[p], (float)k.is[p], acc);
+        if (AFF) acc = fmaf(-k.dm[p], (float)k.ms[p], acc);
     }
+    return acc;
+}
+
+__host__ __device__ inline size_t down_lds_part(int kind, int nq) {
+    return ((stage_bytes(kind, nq) + 15) & ~(size_t)15) + park_bytes(nq * DROWS);
 }
 
 template <int EDT, int SDT>
-__global__ __launch_bounds__(1024) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, uint8_t *ws) {
+__global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h,
+                                                  uint8_t *ws) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const int TD = (int)(d.D / TILE_ROWS), nexp = d.k * TD;
+    constexpr int ek = EDT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
+    const int k = d.k;
+    const int64_t row0 = (int64_t)blockIdx.x * DROWS;
+    const int nbe = (int)(d.de / Packed<EDT>::BV);
+    /* rank t's expert id (thread t < k), clamped so that a stray call before
+     * any routing still reads valid memory, and expert t's down matrix (t < E):
+     * both reach LDS once the activation loads are in flight */
+    __shared__ const uint8_t *s_tab[MAXE];
+    __shared__ int s_eid[MAXK];
+    __shared__ float s_w[MAXK];
+    __shared__ float s_out[(MAXK + 1) * DROWS];
+    const int tid = threadIdx.x;
+    const int eid = tid < k ? ((const GAS int32_t *)ws_ids(ws, L))[tid] : 0;
+    const uint8_t *tab = tid < d.E ? (const uint8_t *)d.experts[3 * tid + 2] : nullptr;   /* down matrices */
+    /* the combine's inputs, loaded before anything waits; w reaches LDS only
+     * after the rows are done, so no wave stalls on it early */
+    const float wl = tid < k ? ((const GAS float *)ws_w(ws, L))[tid] : 0.0f;
+    float hv = 0.0f, sg = 0.0f;
+    if (tid < DROWS) {
+        hv = h[row0 + tid];
+        if (SDT != NONE) sg = *(const GAS float *)ws_sgate(ws, L);
+    }
+    auto table = [&]() {
+        if (tid < d.E) s_tab[tid] = tab;
+        if (tid < k) s_eid[tid] = (eid < 0 || eid >= d.E) ? 0 : eid;
+        __syncthreads();
+    };
+    const Park pe = park_at(lds + ((stage_bytes(ek, k * nbe) + 15) & ~(size_t)15), k * nbe * DROWS);
+    down_rows<EDT>(k, [&](int r) { return s_tab[s_eid[r]]; }, table, (const float *)(ws + L.hh), d.de, d.D, row0, lds,
+                   pe);
+    Park ps = pe;
+    int nbs = 0;
     if constexpr (SDT != NONE) {
-        if ((int)blockIdx.x >= nexp) {
-            const int t = (int)blockIdx.x - nexp;
-            down_tile<SDT>(d, (const uint8_t *)d.sd, (const float *)(ws + L.hh) + (size_t)d.k * d.de, d.ds, t,
-                           (float *)(ws + L.so), lds);
-            return;
-        }
+        constexpr int sk = SDT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
+        nbs = (int)(d.ds / Packed<SDT>::BV);
+        uint8_t *xs = lds + down_lds_part(ek, k * nbe);
+        ps = park_at(xs + ((stage_bytes(sk, nbs) + 15) & ~(size_t)15), nbs * DROWS);
+        down_rows<SDT>(1, [&](int) { return (const uint8_t *)d.sd; }, []() {},
+                       (const float *)(ws + L.hh) + (size_t)k * d.de, d.ds, d.D, row0, xs, ps);
     }
-    const int r = (int)blockIdx.x / TD, t = (int)blockIdx.x - r * TD;
-    int e = ws_ids(ws, L)[r];
-    if (e < 0 || e >= d.E) e = 0;   /* only reachable if phase 3 runs before any phase 2 */
-    down_tile<EDT>(d, (const uint8_t *)d.experts[3 * e + 2], (const float *)(ws + L.hh) + (size_t)r * d.de, d.de, t,
-                   (float *)(ws + L.eo) + (size_t)r * d.D, lds);
-}
-
-/* ======================================================================
- * K4: rank-order combine + residual (src/lib/tlm_model.c:1029-1050)
- * ==================================================================== */
-__global__ __launch_bounds__(256) void k_moe_combine(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h, uint8_t *ws) {
-    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= d.D) return;
-    const GAS float *eo = (const GAS float *)(ws + L.eo);
-    const GAS float *w = (const GAS float *)ws_w(ws, L);
-    /* every load first (one round trip), then the sums in rank order */
-    float ev[MAXK], wv[MAXK];
-#pragma unroll
-    for (int q = 0; q < MAXK; q++) {
-        if (q < d.k) {
-            ev[q] = eo[(size_t)q * d.D + row];
-            wv[q] = w[q];
-        }
+    __syncthreads();
+    /* row chains, one thread per (matrix, row); then the rank-order sum */
+    const int nm = k + (SDT != NONE ? 1 : 0);
+    for (int t = tid; t < nm * DROWS; t += blockDim.x) {
+        const int r = t >> 3, i = t & (DROWS - 1);
+        if constexpr (SDT != NONE) s_out[t] = r < k ? down_chain<EDT>(pe, r, nbe, i) : down_chain<SDT>(ps, 0, nbs, i);
+        else s_out[t] = down_chain<EDT>(pe, r, nbe, i);
     }
-    const float hv = h[row];
-    const float so = d.ds > 0 ? ((const GAS float *)(ws + L.so))[row] : 0.0f;
-    const float sg = d.ds > 0 ? *(const GAS float *)ws_sgate(ws, L) : 0.0f;
-    float ffn = 0.0f;
-#pragma unroll
-    for (int q = 0; q < MAXK; q++) {
-        if (q < d.k) {
-            const float c = wv[q] * ev[q];
+    if (tid < k) s_w[tid] = wl;
+    __syncthreads();
+    if (tid < DROWS) {
+        float ffn = 0.0f;
+        for (int r = 0; r < k; r++) {
+            const float c = s_w[r] * s_out[r * DROWS + tid];
             ffn += c;
         }
+        if constexpr (SDT != NONE) ffn += sg * s_out[k * DROWS + tid];
+        h[row0 + tid] = hv + ffn;
     }
-    if (d.ds > 0) ffn += sg * so;
-    h[row] = hv + ffn;
 }
 
 /* ---- instantiation table: [expert dtype][shared dtype or none] --------------- */
 typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *);
-typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, uint8_t *);
+typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *);
 
 inline int dt_slot(int dt) { return dt == DT_Q6_K ? 0 : dt == DT_Q8_0 ? 1 : dt == DT_Q4_K ? 2 : dt == DT_Q5_K ? 3 : -1; }
 
@@ -674,10 +818,10 @@ int launch_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w
 
 static size_t x_area(int kind, int nb) { return (stage_bytes(kind, nb) + 15) & ~(size_t)15; }
 
-/* phase 0 = all launches; 1 router, 2 gate/up, 3 down, 4 combine */
+/* phase 0 = all launches; 1 router, 2 gate/up, 3 down + combine */
 int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
                      hipStream_t s) {
-    if (phase < 0 || phase > 4) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
+    if (phase < 0 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
     if (!d || !h || !ws) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL argument");
     if ((uintptr_t)ws & 255u) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: workspace must be 256-byte aligned");
     if (d->E <= 0 || d->E > MAXE || d->k <= 0 || d->k > MAXK || d->k > d->E)
@@ -706,21 +850,15 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const int sbv = d->ds > 0 ? dt_block_values(d->shared_dt) : ebv;
     const int nbs = (int)(d->D / sbv), nbsd = d->ds > 0 ? (int)(d->ds / sbv) : 0;
     auto park2 = [](int nb) { int cb = nb < PARK_MAX / TILE_ROWS / 2 ? nb : PARK_MAX / TILE_ROWS / 2; return park_bytes(2 * cb * TILE_ROWS); };
-    /* K3 waves: one per CPW block columns (CPW = 4 / LPI), at most 16; wider
-     * matrices loop over their columns */
-    auto waves3 = [](int dt, int nb) { const int cpw = dt == DT_Q8_0 ? 2 : 1; return (nb + cpw - 1) / cpw; };
-    int w3 = waves3(d->expert_dt, nbde);
-    if (d->ds > 0 && waves3(d->shared_dt, nbsd) > w3) w3 = waves3(d->shared_dt, nbsd);
-    if (w3 > 16) w3 = 16;
     size_t lds1 = al256((size_t)d->D * 8);          /* x and the norm weights */
     size_t lds2e = NWAVE * x_area(ek, nbe) + park2(nbe);
     size_t lds2s = d->ds > 0 ? NWAVE * x_area(sk, nbs) + park2(nbs) : 0;
-    size_t lds3e = x_area(ek, nbde) + park_bytes(nbde * TILE_ROWS);
-    size_t lds3s = d->ds > 0 ? x_area(sk, nbsd) + park_bytes(nbsd * TILE_ROWS) : 0;
-    size_t lds2 = lds2e > lds2s ? lds2e : lds2s, lds3 = lds3e > lds3s ? lds3e : lds3s;
+    /* K3: every rank's activation and parked rows, then the shared expert's */
+    size_t lds3 = down_lds_part(ek, d->k * nbde) + (d->ds > 0 ? down_lds_part(sk, nbsd) : 0);
+    size_t lds2 = lds2e > lds2s ? lds2e : lds2s;
     if (lds1 > 64 * 1024 || lds2 > 64 * 1024 || lds3 > 64 * 1024)
-        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_layer: D=%lld / de=%lld exceed the LDS staging limit",
-                           (long long)d->D, (long long)d->de);
+        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_layer: D=%lld / k*de=%lld exceed the LDS staging limit",
+                           (long long)d->D, (long long)(d->k * d->de));
     uint8_t *w8 = (uint8_t *)ws;
     const tlm_hip_moe_desc dv = *d;
     const WsLayout L = ws_layout(*d);
@@ -729,11 +867,9 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const down_fn dn = DN[es][ss];
     const unsigned g1 = (unsigned)router_groups(*d);
     const unsigned g2 = (unsigned)(d->k * (d->de / TILE_ROWS) + (d->ds > 0 ? d->ds / TILE_ROWS : 0));
-    const unsigned g3 = (unsigned)((d->k + (d->ds > 0 ? 1 : 0)) * (d->D / TILE_ROWS));
-    const unsigned g4 = (unsigned)((d->D + 255) / 256);
+    const unsigned g3 = (unsigned)(d->D / DROWS);
     if (phase == 0 || phase == 1) hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8);
     if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8);
-    if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(64 * w3), lds3, s, dv, L, w8);
-    if (phase == 0 || phase == 4) hipLaunchKernelGGL(k_moe_combine, dim3(g4), dim3(256), 0, s, dv, L, h, w8);
+    if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(256), lds3, s, dv, L, h, w8);
     return tlmh_check(hipGetLastError(), "moe_layer launch");
 }

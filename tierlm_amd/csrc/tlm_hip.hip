@@ -138,7 +138,7 @@ int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *
 
 int tlm_hip_moe_layer_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *workspace,
                             void *stream) {
-    if (phase < 1 || phase > 4) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_phase: phase %d not in 1..4", phase);
+    if (phase < 1 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_phase: phase %d not in 1..3", phase);
     return launch_moe_phase(d, phase, h, ids, w, workspace, (hipStream_t)stream);
 }
 
