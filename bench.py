@@ -38,6 +38,10 @@ TOKEN_BYTES = K * EXPERT_BYTES           # 30,965,760 B per token-layer
 GATEUP_BYTES = K * 2 * MAT_BYTES         # 20,643,840 B per gate/up launch
 DOWN_BYTES = K * MAT_BYTES               # 10,321,920 B per down launch
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per gate/up launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (KiB per dispatch), each
+# scaled by its reading for a 256 MiB device copy (factors 1.99976 and 1.0); the run and its
+# figures: profiles/moe_block_qwen3_30b_hbm_traffic.md
+GATEUP_TRAFFIC_BYTES = 20918804
 
 
 def log(msg):
@@ -106,6 +110,9 @@ def main():
     ap.add_argument("--roofline-tokens", type=int, default=960, help="launches per phase in the roofline graphs")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-check-mib", type=int, default=0,
+                    help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
+                         "of known size, the scale for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -221,6 +228,16 @@ def main():
     expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
     log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); per launch: router {p1:.2f} us, "
         f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down+combine {p3:.2f} us ({dn_gbs:.0f} GB/s)")
+    if args.copy_check_mib > 0:
+        nbytes = args.copy_check_mib << 20
+        src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: copy check {args.copy_check_mib} MiB done")
+        del src, dst
+
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
@@ -240,7 +257,8 @@ def main():
                    "tokens_timed": args.steps, "graph_tokens": args.graph, "layers_resident": L,
                    "expert_bytes_per_token": TOKEN_BYTES},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled by a 256 MiB copy",
                      "kernel": "k_moe_gateup (routing + gate/up of the top-8 experts + SwiGLU)",
                      "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(p2, 3),
                      "down_combine_GBps": round(dn_gbs, 1), "down_combine_avg_launch_us": round(p3, 3),

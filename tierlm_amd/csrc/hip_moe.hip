@@ -734,7 +734,14 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int ek = EDT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
     const int k = d.k;
-    const int64_t row0 = (int64_t)blockIdx.x * DROWS;
+    /* Work-groups go to the 8 XCDs round-robin by id, so groups g and g + 8
+     * share an XCD (and its L2): they take the two halves of one packed tile,
+     * whose rows meet inside shared cache lines.  Ids of a last incomplete
+     * run of 16 map straight. */
+    const int g = blockIdx.x, ng = (int)gridDim.x;
+    const int g16 = g & ~15;
+    const int64_t row0 = g16 + 16 <= ng ? ((int64_t)(g16 >> 1) + (g & 7)) * TILE_ROWS + ((g >> 3) & 1) * DROWS
+                                        : (int64_t)g * DROWS;
     const int nbe = (int)(d.de / Packed<EDT>::BV);
     /* rank t's expert id (thread t < k), clamped so that a stray call before
      * any routing still reads valid memory, and expert t's down matrix (t < E):
