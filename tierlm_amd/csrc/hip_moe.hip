@@ -73,6 +73,13 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+/* Kernel arguments are read through the scalar cache, and the compiler
+ * fetches each field where it is first used: every such batch is a full
+ * round trip before the next dependent load can go out.  Naming the fields a
+ * kernel needs at its entry makes it fetch them all at once, with one wait. */
+template <class T> __device__ __forceinline__ void arg_now(T v) { asm volatile("" ::"s"(v)); }
+template <class... T> __device__ __forceinline__ void args_now(T... v) { (arg_now(v), ...); }
+
 /* max / or over aligned groups of WIDTH lanes (2, 4, 8, 16 or 64), uniform in the group */
 template <int WIDTH> __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
     uint32_t o;
@@ -102,7 +109,7 @@ template <int WIDTH> __device__ __forceinline__ uint32_t group_or_u32(uint32_t v
 /* ---- activation rule (src/lib/tlm_quant.c:458-478) for this lane's 4 values
  * of a block spread over WIDTH lanes: d, and the 4 codes packed in a dword --- */
 template <int WIDTH>
-__device__ __attribute__((noinline)) float act_rule4(f32x4 v, bool ok, uint32_t &codes) {
+__device__ __forceinline__ float act_rule4(f32x4 v, bool ok, uint32_t &codes) {
     /* |v| as bits: for non-negative floats the unsigned order is the float
      * order; above 0x7F800000 is NaN, equal is infinity */
     uint32_t am = 0, fl = 0;
@@ -206,23 +213,28 @@ __device__ __forceinline__ float act_rule16(const f32x4 (&v)[4], bool ok, u32x4 
     return d;
 }
 
+__device__ __forceinline__ void st16(LAS uint8_t *p, u32x4 v) { *(LAS u32x4 *)p = v; }
+__device__ __forceinline__ void st16(GAS uint8_t *p, u32x4 v) { *(GAS u32x4 *)p = v; }
+
 /* Quantise block b (this lane: values 16*sub..16*sub+15) into the split
- * layout (q codes, bs bsums, dd scales).  Q8_K: 16 lanes per block, and a
- * lane's 16 codes are exactly bsum group sub; a8: 2 lanes per block. */
-__device__ __forceinline__ void quant16_to(int kind, const f32x4 (&v)[4], bool ok, int sub, LAS uint8_t *q,
-                                           LAS int16_t *bs, LAS float *dd, int b) {
+ * layout (q codes, bs bsums, dd scales; LDS or global).  Q8_K: 16 lanes per
+ * block, and a lane's 16 codes are exactly bsum group sub; a8: 2 lanes per
+ * block. */
+template <class QP, class BP, class DP>
+__device__ __forceinline__ void quant16_to(int kind, const f32x4 (&v)[4], bool ok, int sub, QP q, BP bs, DP dd,
+                                           int b) {
     u32x4 c;
     if (kind == DT_Q8_K) {
         const float d = act_rule16<16>(v, ok, c);
         if (ok) {
-            *(LAS u32x4 *)(q + b * 256 + 16 * sub) = c;
+            st16(q + b * 256 + 16 * sub, c);
             bs[b * 16 + sub] = (int16_t)(byte_sum(c.x) + byte_sum(c.y) + byte_sum(c.z) + byte_sum(c.w));
             if (sub == 0) dd[b] = d;
         }
     } else {
         const float d = act_rule16<2>(v, ok, c);
         if (ok) {
-            *(LAS u32x4 *)(q + b * 32 + 16 * sub) = c;
+            st16(q + b * 32 + 16 * sub, c);
             if (sub == 0) dd[b] = d;
         }
     }
@@ -267,9 +279,9 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, E = d.E, k = d.k;
     const bool sig = d.router == 2;
     const bool in = t < E;
-    const bool unmasked = in && !(d.mask && d.mask[t]);
+    const bool unmasked = in && !(d.mask && ((const GAS uint8_t *)d.mask)[t]);
     const float l = in ? logits[t] : 0.0f;
-    const float bias = (sig && in && d.router_bias) ? d.router_bias[t] : 0.0f;
+    const float bias = (sig && in && d.router_bias) ? ((const GAS float *)d.router_bias)[t] : 0.0f;
     float p;
     if (sig) {   /* sigmoid score = weight; bias for selection only */
         p = 1.0f / (1.0f + expf(-l));
@@ -307,7 +319,7 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
     const unsigned long long ke = e < E ? R->key[e] : 0ull;
     int c = 0;
     if (ke != 0ull) {
-#pragma unroll 8
+#pragma unroll 16
         for (int f = f0; f < f1; f++) c += R->key[f] > ke ? 1 : 0;
     }
     R->cnt[t] = c;
@@ -377,6 +389,8 @@ __device__ __forceinline__ float fma_chunk(const float (&v)[RCH], const LAS floa
 __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
                                                    uint8_t *ws) {
     extern __shared__ __align__(16) uint8_t lds[];
+    args_now(d.D, d.E, d.eps, d.router_w, d.ffn_norm, d.ds, d.expert_dt, d.shared_dt, d.shared_gate_inp, L.logits,
+             L.xb, L.xe, L.xs, L.route, hptr, ws, blockDim.x, gridDim.x);
     const int lane = threadIdx.x, hl = lane & 31;
     const int64_t D = d.D;
     const int64_t row = (int64_t)blockIdx.x * 2 + (lane >> 5);
@@ -400,34 +414,71 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
     LAS f32x4 *xw4 = xb4 + D / 4;
     constexpr int NV = 8;   /* 16-byte loads of h and of the weights per lane per batch */
     const int D4 = (int)(D / 4);
-    double ss = 0.0;
-    for (int c = lane; c < D4; c += 64 * NV) {
+    if (D4 <= 64 * NV) {
+        /* one batch (D <= 2048): normalise in registers, write x once */
         f32x4 hv[NV], nv[NV];
 #pragma unroll
         for (int j = 0; j < NV; j++) {
-            const int cc = c + 64 * j;
+            const int cc = lane + 64 * j;
             if (cc < D4) { hv[j] = h4[cc]; nv[j] = n4[cc]; }
         }
+        double ss = 0.0;
 #pragma unroll
-        for (int j = 0; j < NV; j++) {
-            const int cc = c + 64 * j;
-            if (cc < D4) {
+        for (int j = 0; j < NV; j++)
+            if (lane + 64 * j < D4) {
 #pragma unroll
                 for (int t = 0; t < 4; t++) ss += (double)hv[j][t] * (double)hv[j][t];
-                xb4[cc] = hv[j];
-                xw4[cc] = nv[j];
+            }
+        ss = wave_sum_f64(ss);
+        const float rn = 1.0f / sqrtf((float)(ss / (double)D) + d.eps);
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int cc = lane + 64 * j;
+            if (cc < D4) {
+                f32x4 o;
+#pragma unroll
+                for (int t = 0; t < 4; t++) o[t] = hv[j][t] * rn * nv[j][t];
+                xb4[cc] = o;
             }
         }
-    }
-    ss = wave_sum_f64(ss);
-    const float rn = 1.0f / sqrtf((float)(ss / (double)D) + d.eps);
-    wave_sync();
-    for (int c = lane; c < D4; c += 64) {
-        const f32x4 x = xb4[c], w = xw4[c];
-        f32x4 o;
+    } else {
+        /* wider: h and the weights parked in LDS, normalised in batches */
+        double ss = 0.0;
+        for (int c = lane; c < D4; c += 64 * NV) {
+            f32x4 hv[NV], nv[NV];
 #pragma unroll
-        for (int t = 0; t < 4; t++) o[t] = x[t] * rn * w[t];
-        xb4[c] = o;
+            for (int j = 0; j < NV; j++) {
+                const int cc = c + 64 * j;
+                if (cc < D4) { hv[j] = h4[cc]; nv[j] = n4[cc]; }
+            }
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const int cc = c + 64 * j;
+                if (cc < D4) {
+#pragma unroll
+                    for (int t = 0; t < 4; t++) ss += (double)hv[j][t] * (double)hv[j][t];
+                    xb4[cc] = hv[j];
+                    xw4[cc] = nv[j];
+                }
+            }
+        }
+        ss = wave_sum_f64(ss);
+        const float rn = 1.0f / sqrtf((float)(ss / (double)D) + d.eps);
+        wave_sync();
+        for (int c = lane; c < D4; c += 64 * NV) {
+            f32x4 x[NV], w[NV];
+#pragma unroll
+            for (int j = 0; j < NV; j++)
+                if (c + 64 * j < D4) { x[j] = xb4[c + 64 * j]; w[j] = xw4[c + 64 * j]; }
+#pragma unroll
+            for (int j = 0; j < NV; j++)
+                if (c + 64 * j < D4) {
+                    f32x4 o;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) o[t] = x[j][t] * rn * w[j][t];
+                    xb4[c + 64 * j] = o;
+                }
+        }
     }
     wave_sync();
     const LAS float *xb = (const LAS float *)lds;
@@ -466,13 +517,14 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
     /* group b quantises activation block b for the experts / shared expert
      * into the split layout the gate/up launch copies straight into LDS */
     const int b = blockIdx.x;
+#pragma unroll 1
     for (int which = 0; which < (d.ds > 0 ? 2 : 1); which++) {
         const int kind = dt_act_kind(which ? d.shared_dt : d.expert_dt), bv = bvals(kind);
         const int nb = (int)(D >> (kind == DT_Q8_K ? 8 : 5));   /* D is a multiple of the block */
         if (b >= nb) continue;
         GAS uint8_t *base = (GAS uint8_t *)(ws + (which ? L.xs : L.xe));
-        const int sub = kind == DT_Q8_K ? lane : (lane & 7);
-        const bool ok = (kind == DT_Q8_K || lane < 8) && (int64_t)b * bv + 4 * sub < D;
+        const int sub = kind == DT_Q8_K ? lane : (lane & 7);   /* 4 values per lane */
+        const bool ok = kind == DT_Q8_K || lane < 8;
         f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
         if (ok) v = *(const LAS f32x4 *)(xb + (int64_t)b * bv + 4 * sub);
         quant_block_to(kind, v, ok, sub, (GAS uint32_t *)base, (GAS int16_t *)(base + nb * 256),
@@ -598,6 +650,9 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
                                                     uint8_t *ws) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ RouteLds s_route;
+    args_now(d.D, d.de, d.ds, d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, d.experts, L.logits, L.route,
+             L.hh, L.xe, ids_out, w_out, ws, blockDim.x, gridDim.x);
+    if constexpr (SDT != NONE) args_now(d.sg, d.su, L.xs);
     const int te = (int)(d.de / TILE_ROWS), nexp = d.k * te;
     const bool shared = SDT != NONE && (int)blockIdx.x >= nexp;
     if constexpr (SDT != NONE) {
@@ -614,8 +669,9 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
      * LDS during routing, so the chosen one costs no extra round trip */
     __shared__ const uint8_t *s_gate[MAXE], *s_up[MAXE];
     const int tid = threadIdx.x;
-    const uint8_t *tg = tid < d.E ? (const uint8_t *)d.experts[3 * tid + 0] : nullptr;
-    const uint8_t *tu = tid < d.E ? (const uint8_t *)d.experts[3 * tid + 1] : nullptr;
+    const GAS uint64_t *xt = (const GAS uint64_t *)d.experts;
+    const uint8_t *tg = tid < d.E ? (const uint8_t *)xt[3 * tid + 0] : nullptr;
+    const uint8_t *tu = tid < d.E ? (const uint8_t *)xt[3 * tid + 1] : nullptr;
     route_group(d, (const GAS float *)(ws + L.logits), R, [&]() {
         s_gate[tid] = tg;
         s_up[tid] = tu;
@@ -732,6 +788,8 @@ template <int EDT, int SDT>
 __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h,
                                                   uint8_t *ws) {
     extern __shared__ __align__(16) uint8_t lds[];
+    args_now(d.D, d.de, d.ds, d.E, d.k, d.experts, L.route, L.hh, h, ws, blockDim.x, gridDim.x);
+    if constexpr (SDT != NONE) args_now(d.sd);
     constexpr int ek = EDT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
     const int k = d.k;
     /* Work-groups go to the 8 XCDs round-robin by id, so groups g and g + 8
@@ -752,7 +810,7 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
     __shared__ float s_out[(MAXK + 1) * DROWS];
     const int tid = threadIdx.x;
     const int eid = tid < k ? ((const GAS int32_t *)ws_ids(ws, L))[tid] : 0;
-    const uint8_t *tab = tid < d.E ? (const uint8_t *)d.experts[3 * tid + 2] : nullptr;   /* down matrices */
+    const uint8_t *tab = tid < d.E ? (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * tid + 2] : nullptr;
     /* the combine's inputs, loaded before anything waits; w reaches LDS only
      * after the rows are done, so no wave stalls on it early */
     const float wl = tid < k ? ((const GAS float *)ws_w(ws, L))[tid] : 0.0f;
