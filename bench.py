@@ -228,6 +228,26 @@ def main():
     expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
     log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); per launch: router {p1:.2f} us, "
         f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down+combine {p3:.2f} us ({dn_gbs:.0f} GB/s)")
+    # on-box streaming-read reference: this library's packed Q6_K GEMV over a ~2 GB span of
+    # the resident expert bytes read as one 2048-wide matrix (values irrelevant)
+    srows = (2 << 30) // 1680 // 16 * 16
+    sbytes = hq.packed_bytes(Q6_K, srows, D)
+    xs = hq.quantize_act(hq.Q8_K, torch.randn(D, generator=gen, device=dev))
+    ys = torch.empty(srows, dtype=torch.float32, device=dev)
+    hq.matvec_packed(Q6_K, W, srows, D, xs, ys)
+    torch.cuda.synchronize()
+    stream_us = None
+    for _ in range(5):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        hq.matvec_packed(Q6_K, W, srows, D, xs, ys)
+        ev1.record()
+        ev1.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3
+        stream_us = us if stream_us is None else min(stream_us, us)
+    stream_gbs = sbytes / (stream_us * 1e-6) / 1e9
+    log(f"bench: streaming GEMV over {sbytes / 1e9:.2f} GB: {stream_gbs:.0f} GB/s")
+
     if args.copy_check_mib > 0:
         nbytes = args.copy_check_mib << 20
         src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
@@ -265,7 +285,9 @@ def main():
                      "router_avg_launch_us": round(p1, 3),
                      "timing": "HIP events around a graph of R back-to-back launches of the phase (R = roofline_launches), / R",
                      "roofline_launches": R,
-                     "expert_gemv_GBps": round(expert_gbs, 1), "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4)},
+                     "expert_gemv_GBps": round(expert_gbs, 1), "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4),
+                     "stream_read_peak_GBps": round(stream_gbs, 1),
+                     "stream_read_kernel": "k_mv_packed<Q6_K> over ~2 GB of resident expert bytes, one launch (best of 5)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
