@@ -107,6 +107,17 @@ typedef struct {
 #define TLM_HIP_MAX_SEGS 136   /* MAX_SEGS, src/lib/tlm_model.c:41-42 */
 int tlm_hip_mv_job(const tlm_hip_seg *segs, int nseg, void *stream);
 
+/* ---- many tokens through one packed matrix (prefill) ------------------------
+ * The reference's prefill runs the decode step once per token
+ * (src/lib/tlm_model.c:1105-1113), i.e. tlm_matvec_rows per token.  This
+ * streams a packed matrix once for all ntok tokens (int8 MFMA) and returns,
+ * for every token t and row r, exactly the decode result:
+ *   Y[t * rows + r] == tlm_hip_matvec_packed(dt, Wp, rows, n, act_t, .)[r]
+ * act: ntok activation vectors in the reference layout (Q8_K blocks,
+ * n/256 * 292 bytes each, consecutive, 4-byte aligned).  dt: Q6_K. */
+int tlm_hip_matmul_tokens(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok,
+                          float *Y, void *stream);
+
 /* ---- one routed MoE block ------------------------------------------------
  * src/lib/tlm_model.c:940-1055 (with run_batch :900-938, route :798-839):
  *   xb = rmsnorm(h, ffn_norm); logits = router xb; (ids, w) = route(logits);

@@ -1,0 +1,78 @@
+"""Many tokens through one packed matrix (int8 MFMA) vs the decode dot.
+
+The reference's prefill is the decode step per token (src/lib/tlm_model.c:
+1105-1113), so every (token, row) output must carry the decode kernel's bits:
+the token-batched kernel is checked bit for bit against the packed GEMV run
+token by token (itself bit-exact with the oracle, test_hip_gemv.py), and a
+sample against the oracle directly.  Shapes cover token counts around the
+32-token tile, rows around the 16-row tile and the 128-row group, the edge
+weight patterns of the reference's matvec tests, and poisoned activations."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.synth import random_code_rows
+from tests.test_hip_gemv import make_wrow, same
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(hip, dev, dt, rows, n, ntok, seed, wmode=None, poison=False):
+    rng = np.random.default_rng(seed)
+    if wmode is None:
+        W = random_code_rows(rng, dt, rows, n)
+    else:
+        W = np.stack([make_wrow(rng, dt, n, wmode if wmode >= 0 else int(rng.integers(0, 5))) for _ in range(rows)])
+    rb = W.shape[1]
+    X = (rng.standard_normal((ntok, n)) * rng.choice([0.1, 1.0, 30.0], size=(ntok, 1))).astype(np.float32)
+    if poison and ntok > 3:
+        X[1] = 0.0
+        X[2, 5] = np.nan
+        X[3, n - 1] = np.inf
+    Wd = torch.from_numpy(W.reshape(-1)).to(dev)
+    Wp = hip.pack(dt, Wd, rb, rows, n)
+    act = hip.quantize_act(hip.Q8_K, torch.from_numpy(X.reshape(-1)).to(dev))
+    Y = hip.matmul_tokens(dt, Wp, rows, n, act, ntok)
+    ab = oracle.qact_bytes(oracle.Q8_K, n)
+    want = torch.empty((ntok, rows), dtype=torch.float32, device=dev)
+    for t in range(ntok):
+        hip.matvec_packed(dt, Wp, rows, n, act[t * ab:(t + 1) * ab], want[t])
+    torch.cuda.synchronize()
+    got, want = Y.cpu().numpy(), want.cpu().numpy()
+    ok = same(got, want)
+    assert ok.all(), f"{(~ok).sum()} of {ok.size} outputs differ; first at {np.argwhere(~ok)[0]}"
+    return W, X, got
+
+
+@pytest.mark.parametrize("rows,n,ntok", [(768, 2048, 32), (768, 2048, 1), (100, 512, 33), (2048, 768, 45),
+                                         (130, 256, 64), (16, 256, 7)])
+def test_tokmm_q6k_matches_decode(hip, dev, rows, n, ntok):
+    run_case(hip, dev, oracle.Q6_K, rows, n, ntok, seed=rows * 7 + ntok)
+
+
+@pytest.mark.parametrize("wmode", [1, 2, 3, 4, -1])
+def test_tokmm_q6k_edge_weights(hip, dev, wmode):
+    run_case(hip, dev, oracle.Q6_K, 48, 512, 19, seed=100 + wmode, wmode=wmode)
+
+
+def test_tokmm_q6k_poisoned_tokens(hip, dev):
+    run_case(hip, dev, oracle.Q6_K, 96, 1024, 40, seed=7, poison=True)
+
+
+def test_tokmm_q6k_vs_oracle(hip, dev):
+    W, X, got = run_case(hip, dev, oracle.Q6_K, 64, 512, 9, seed=3, wmode=3)
+    for t in range(X.shape[0]):
+        act = oracle.quantize_act(oracle.Q8_K, X[t])
+        want = oracle.matvec_rows(oracle.Q6_K, W, W.shape[1], act, 512, 0, 64)
+        assert same(got[t], want).all(), t
+
+
+def test_tokmm_rejects_bad_arguments(hip, dev):
+    from tierlm_amd._lib import HipError
+    Wp = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    act = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    with pytest.raises(HipError):
+        hip.matmul_tokens(oracle.Q6_K, Wp, 16, 100, act, 2)      # n not a multiple of 256
+    with pytest.raises(HipError):
+        hip.matmul_tokens(oracle.Q8_0, Wp, 16, 256, act, 2)      # dtype without a token kernel

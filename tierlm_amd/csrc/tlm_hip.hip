@@ -126,6 +126,11 @@ int tlm_hip_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const
     return launch_matvec_packed(dt, Wp, rows, n, act, y, (hipStream_t)stream);
 }
 
+int tlm_hip_matmul_tokens(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok,
+                          float *Y, void *stream) {
+    return launch_tokmm(dt, Wp, rows, n, act, ntok, Y, (hipStream_t)stream);
+}
+
 int tlm_hip_mv_job(const tlm_hip_seg *segs, int nseg, void *stream) {
     return launch_mv_job(segs, nseg, (hipStream_t)stream);
 }

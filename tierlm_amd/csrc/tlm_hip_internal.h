@@ -137,6 +137,8 @@ int launch_pack(int dt, const void *src, size_t row_bytes, int64_t rows, int64_t
 int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, float *y,
                          hipStream_t s);
 int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s);
+int launch_tokmm(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok, float *Y,
+                 hipStream_t s);
 size_t moe_workspace_bytes(const tlm_hip_moe_desc *d);
 int launch_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w, void *ws, hipStream_t s);
 int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,

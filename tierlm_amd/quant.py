@@ -101,6 +101,15 @@ def matvec_packed(dt, Wp, rows, n, act, y=None):
     return y
 
 
+def matmul_tokens(dt, Wp, rows, n, act, ntok, Y=None):
+    """Y[t, r] = packed row r . token t's activation (act: ntok consecutive
+    activation vectors); the decode result for every token."""
+    if Y is None:
+        Y = torch.empty((ntok, rows), dtype=torch.float32, device=Wp.device)
+    check(lib.tlm_hip_matmul_tokens(dt, _ptr(Wp), rows, n, _ptr(act), ntok, _ptr(Y), stream()))
+    return Y
+
+
 def mv_job(segs):
     """segs: list of dicts with dt, packed, W, row_bytes, act, y, n, rows (tensors)."""
     arr = (Seg * max(len(segs), 1))()
