@@ -163,6 +163,18 @@ int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *
 int tlm_hip_moe_layer_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w,
                             void *workspace, void *stream);
 
+/* ---- prefill: T tokens through the routed MoE block ---------------------------
+ * src/lib/tlm_model.c:1105-1113 runs the decode step once per token; the MoE
+ * block has no cross-token terms, so this gives every token exactly the
+ * result of tlm_hip_moe_layer on it: h[t*D .. t*D+D) += MoE(h_t), routing in
+ * ids / w [T*k] (either may be NULL).  Tokens are bucketed by expert and each
+ * expert's rows stream once per 32 of its tokens (int8 MFMA).  Routed Q6_K
+ * experts, no shared expert.  workspace: tlm_hip_moe_prefill_workspace_bytes
+ * bytes, 256-byte aligned. */
+size_t tlm_hip_moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T);
+int tlm_hip_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w,
+                        void *workspace, void *stream);
+
 /* ---- reference tier ABI --------------------------------------------------
  * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a
  * name and two tables of TLM_QK_COUNT = 10 function pointers indexed F32,

@@ -63,6 +63,8 @@ _SIGS = {
     "tlm_hip_matvec_packed": (i32, [i32, vp, i64, i64, vp, vp, vp]),
     "tlm_hip_mv_job": (i32, [C.POINTER(Seg), i32, vp]),
     "tlm_hip_matmul_tokens": (i32, [i32, vp, i64, i64, vp, i64, vp, vp]),
+    "tlm_hip_moe_prefill_workspace_bytes": (sz, [C.POINTER(MoeDesc), i64]),
+    "tlm_hip_moe_prefill": (i32, [C.POINTER(MoeDesc), vp, i64, vp, vp, vp, vp]),
     "tlm_hip_moe_workspace_bytes": (sz, [C.POINTER(MoeDesc)]),
     "tlm_hip_moe_layer": (i32, [C.POINTER(MoeDesc), vp, vp, vp, vp, vp]),
     "tlm_hip_moe_layer_phase": (i32, [C.POINTER(MoeDesc), i32, vp, vp, vp, vp, vp]),

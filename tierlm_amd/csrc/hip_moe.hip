@@ -23,10 +23,11 @@
  * maintenance is needed inside a kernel.  The kernels are instantiated per
  * (expert dtype, shared dtype) so each holds one or two item paths only.
  * Integer sums, per-row fma chains, activation quantisation and the combine
- * order are the reference's; expf and rmsnorm's double sum of squares are the
- * device's. */
+ * order are the reference's; e^x (double exp rounded to float) and rmsnorm's
+ * double sum of squares (a tree) are the device's. */
 #include "tlm_hip_internal.h"
 #include "tlm_hip_items.h"
+#include "tlm_hip_mfma.h"
 
 #include <math.h>
 
@@ -284,7 +285,7 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
     const float bias = (sig && in && d.router_bias) ? ((const GAS float *)d.router_bias)[t] : 0.0f;
     float p;
     if (sig) {   /* sigmoid score = weight; bias for selection only */
-        p = 1.0f / (1.0f + expf(-l));
+        p = 1.0f / (1.0f + exp_rn(-l));
     } else {     /* softmax over the routable experts */
         float m = wave_max_f32((unmasked && l > -INFINITY) ? l : -INFINITY);
         if (lane == 0) R->redf[wave] = m;
@@ -293,7 +294,7 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
 #pragma unroll
         for (int q = 1; q < NWAVE; q++) mx = R->redf[q] > mx ? R->redf[q] : mx;
         const bool off = !unmasked || l != l || mx == -INFINITY;
-        const float x = off ? 0.0f : expf(l - mx);
+        const float x = off ? 0.0f : exp_rn(l - mx);
         const double s = wave_sum_f64((double)x);
         if (lane == 0) R->red[wave] = s;
         __syncthreads();
@@ -386,11 +387,15 @@ __device__ __forceinline__ float fma_chunk(const float (&v)[RCH], const LAS floa
     return r;
 }
 
+/* blockIdx.y = token (prefill): its residual at hptr + y * D, its workspace at
+ * ws + y * tstride; a decode launch has one token. */
 __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
-                                                   uint8_t *ws) {
+                                                   uint8_t *ws, size_t tstride) {
     extern __shared__ __align__(16) uint8_t lds[];
     args_now(d.D, d.E, d.eps, d.router_w, d.ffn_norm, d.ds, d.expert_dt, d.shared_dt, d.shared_gate_inp, L.logits,
-             L.xb, L.xe, L.xs, L.route, hptr, ws, blockDim.x, gridDim.x);
+             L.xb, L.xe, L.xs, L.route, hptr, ws, tstride, blockDim.x, gridDim.x);
+    hptr += (size_t)blockIdx.y * d.D;
+    ws += (size_t)blockIdx.y * tstride;
     const int lane = threadIdx.x, hl = lane & 31;
     const int64_t D = d.D;
     const int64_t row = (int64_t)blockIdx.x * 2 + (lane >> 5);
@@ -542,7 +547,7 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
                 float acc = 0.0f;
                 if (lane == 0)
                     for (int64_t i = 0; i < D; i++) acc += gi[i] * xb[i];
-                g = 1.0f / (1.0f + expf(-acc));
+                g = 1.0f / (1.0f + exp_rn(-acc));
             }
             if (lane == 0) *(GAS float *)ws_sgate(ws, L) = g;
         }
@@ -642,7 +647,7 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
         __syncthreads();
     }
     if (threadIdx.x < TILE_ROWS)
-        hh[t * TILE_ROWS + threadIdx.x] = accg / (1.0f + expf(-accg)) * accu;   /* silu(g) * u (tlm_model.c:171, 927) */
+        hh[t * TILE_ROWS + threadIdx.x] = accg / (1.0f + exp_rn(-accg)) * accu;   /* silu(g) * u (tlm_model.c:171, 927) */
 }
 
 template <int EDT, int SDT>
@@ -858,6 +863,232 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
     }
 }
 
+/* ======================================================================
+ * Prefill: T tokens through the block at once (src/lib/tlm_model.c:1105-1113
+ * runs the decode step per token; the MoE block has no cross-token terms, so
+ * batching keeps every token's bits).  K1 runs per token (blockIdx.y); each
+ * token routes as in K2; (token, rank) pairs are bucketed by expert into
+ * slots; each expert's gate / up / down rows stream once per 32 of its slots
+ * through the int8 MFMA tile; the combine runs per token in rank order.
+ * ==================================================================== */
+struct PfLayout {
+    size_t tok;        /* T per-token decode workspaces (stride tstride) */
+    size_t pair_e;     /* int32 [T*k]: expert of (token, rank) */
+    size_t pair_w;     /* f32 [T*k]: its routing weight */
+    size_t pair_pos;   /* int32 [T*k]: position in its expert's slot run */
+    size_t slot_of;    /* int32 [T*k]: slot of (token, rank) */
+    size_t slot_tok;   /* int32 [T*k]: token of slot */
+    size_t tiles;      /* int32 [MT][3]: expert (-1 unused), first slot, slots */
+    size_t hbuf;       /* f32 [T*k][de]: silu(g) * u per slot */
+    size_t hq;         /* [T*k] split-layout Q8_K of hbuf rows, stride hq_stride */
+    size_t out;        /* f32 [T*k][D]: down output per slot */
+    size_t tstride, hq_stride, total;
+    int64_t T;
+    int MT;
+};
+
+inline PfLayout pf_layout(const tlm_hip_moe_desc &d, int64_t T) {
+    PfLayout P;
+    const WsLayout L = ws_layout(d);
+    const size_t pairs = (size_t)T * d.k;
+    size_t o = 0;
+    P.T = T;
+    P.MT = (int)(pairs / tokmm::TM_TOK + d.E);
+    P.tstride = L.total;
+    P.hq_stride = al256(stage_bytes(DT_Q8_K, (int)(d.de / 256)));
+    P.tok = o;      o += P.tstride * T;
+    P.pair_e = o;   o += al256(pairs * 4);
+    P.pair_w = o;   o += al256(pairs * 4);
+    P.pair_pos = o; o += al256(pairs * 4);
+    P.slot_of = o;  o += al256(pairs * 4);
+    P.slot_tok = o; o += al256(pairs * 4);
+    P.tiles = o;    o += al256((size_t)P.MT * 12);
+    P.hbuf = o;     o += al256(pairs * d.de * 4);
+    P.hq = o;       o += P.hq_stride * pairs;
+    P.out = o;      o += al256(pairs * d.D * 4);
+    P.total = o;
+    return P;
+}
+
+__global__ __launch_bounds__(256) void k_pf_route(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws,
+                                                  int32_t *ids_out, float *w_out) {
+    __shared__ RouteLds s_route;
+    args_now(d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, L.logits, P.tok, P.tstride, P.pair_e,
+             P.pair_w, ws, ids_out, w_out);
+    const int t = blockIdx.x;
+    const uint8_t *wst = ws + P.tok + (size_t)t * P.tstride;
+    LAS RouteLds *R = (LAS RouteLds *)&s_route;
+    route_group(d, (const GAS float *)(wst + L.logits), R, []() {});
+    if ((int)threadIdx.x < d.k) {
+        const int q = threadIdx.x;
+        const size_t pr = (size_t)t * d.k + q;
+        ((GAS int32_t *)(ws + P.pair_e))[pr] = R->ids[q];
+        ((GAS float *)(ws + P.pair_w))[pr] = R->w[q];
+        if (ids_out) ids_out[pr] = R->ids[q];
+        if (w_out) w_out[pr] = R->w[q];
+    }
+}
+
+/* One group: slots grouped by expert (order within an expert is free - every
+ * slot is computed on its own), and the tile table of 32-slot runs. */
+__global__ __launch_bounds__(256) void k_pf_bucket(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
+    __shared__ int s_cnt[MAXE], s_off[MAXE], s_toff[MAXE], s_scan[256];
+    args_now(d.E, d.k, P.T, P.MT, P.pair_e, P.pair_pos, P.slot_of, P.slot_tok, P.tiles, ws);
+    const int tid = threadIdx.x, E = d.E;
+    const int npair = (int)(P.T * d.k);
+    const GAS int32_t *pe = (const GAS int32_t *)(ws + P.pair_e);
+    GAS int32_t *ppos = (GAS int32_t *)(ws + P.pair_pos);
+    if (tid < MAXE) s_cnt[tid] = 0;
+    __syncthreads();
+    for (int p = tid; p < npair; p += 256) {
+        int e = pe[p];
+        e = (e < 0 || e >= E) ? 0 : e;
+        ppos[p] = atomicAdd(&s_cnt[e], 1);
+    }
+    __syncthreads();
+    /* exclusive scans of slot counts and tile counts over the experts */
+    const int c = tid < E ? s_cnt[tid] : 0;
+    const int nt = (c + tokmm::TM_TOK - 1) / tokmm::TM_TOK;
+    for (int pass = 0; pass < 2; pass++) {
+        int v = pass == 0 ? c : nt;
+        s_scan[tid] = v;
+        __syncthreads();
+        for (int off = 1; off < 256; off <<= 1) {
+            const int o = tid >= off ? s_scan[tid - off] : 0;
+            __syncthreads();
+            v += o;
+            s_scan[tid] = v;
+            __syncthreads();
+        }
+        if (tid < E) (pass == 0 ? s_off : s_toff)[tid] = v - (pass == 0 ? c : nt);
+        __syncthreads();
+    }
+    const int tiles_used = s_scan[255];
+    GAS int32_t *slot_of = (GAS int32_t *)(ws + P.slot_of);
+    GAS int32_t *slot_tok = (GAS int32_t *)(ws + P.slot_tok);
+    for (int p = tid; p < npair; p += 256) {
+        int e = pe[p];
+        e = (e < 0 || e >= E) ? 0 : e;
+        const int slot = s_off[e] + ppos[p];
+        slot_of[p] = slot;
+        slot_tok[slot] = p / d.k;
+    }
+    GAS int32_t *tiles = (GAS int32_t *)(ws + P.tiles);
+    if (tid < E) {
+        for (int q = 0; q < nt; q++) {
+            const int ti = s_toff[tid] + q;
+            tiles[3 * ti] = tid;
+            tiles[3 * ti + 1] = s_off[tid] + tokmm::TM_TOK * q;
+            tiles[3 * ti + 2] = c - tokmm::TM_TOK * q < tokmm::TM_TOK ? c - tokmm::TM_TOK * q : tokmm::TM_TOK;
+        }
+    }
+    for (int ti = tiles_used + tid; ti < P.MT; ti += 256) tiles[3 * ti] = -1;
+}
+
+/* Rows of gate and up (each wave: 32 rows x up to 32 slots of one expert),
+ * then h = silu(g) * u per (slot, row). */
+__global__ __launch_bounds__(256) void k_pf_gateup(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws) {
+    __shared__ float s_da[4][tokmm::TM_TOK];
+    args_now(d.D, d.de, d.experts, L.xe, P.tok, P.tstride, P.tiles, P.slot_tok, P.hbuf, ws);
+    const GAS int32_t *tl = (const GAS int32_t *)(ws + P.tiles) + 3 * blockIdx.y;
+    const int e = tl[0];
+    if (e < 0) return;
+    const int s0 = tl[1], n = tl[2];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, half = lane >> 5;
+    const int64_t rows = d.de, row = (int64_t)blockIdx.x * 128 + wave * 32 + j;
+    const int64_t rr = row < rows ? row : rows - 1;
+    const int nb = (int)(d.D / 256);
+    const int64_t units = (rows / TILE_ROWS) * nb * TILE_ROWS;
+    const int64_t ubase = (rr / TILE_ROWS) * nb * TILE_ROWS + rr % TILE_ROWS;
+    const int slot = s0 + (j < n ? j : n - 1);
+    const int tok = ((const GAS int32_t *)(ws + P.slot_tok))[slot];
+    const GAS uint8_t *arow = (const GAS uint8_t *)(ws + P.tok + (size_t)tok * P.tstride + L.xe);
+    const GAS uint64_t *xt = (const GAS uint64_t *)d.experts;
+    const uint8_t *wg = (const uint8_t *)xt[3 * e], *wu = (const uint8_t *)xt[3 * e + 1];
+    float accg[16], accu[16];
+    tokmm::tile_q6k<true>(wg, units, ubase, nb, arow, (LAS float *)s_da[wave], j, half, accg);
+    tokmm::tile_q6k<true>(wu, units, ubase, nb, arow, (LAS float *)s_da[wave], j, half, accu);
+    if (row < rows) {
+        GAS float *hb = (GAS float *)(ws + P.hbuf);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int i = 8 * (v >> 2) + 4 * half + (v & 3);
+            if (i < n) hb[(size_t)(s0 + i) * rows + row] = accg[v] / (1.0f + exp_rn(-accg[v])) * accu[v];
+        }
+    }
+}
+
+/* Quantise h of every slot (src/lib/tlm_quant.c:458-478): one wave per block. */
+__global__ __launch_bounds__(64) void k_pf_hquant(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
+    args_now(d.de, P.hbuf, P.hq, P.hq_stride, ws);
+    const int b = blockIdx.x, lane = threadIdx.x;
+    const size_t slot = blockIdx.y;
+    const int nbd = (int)(d.de / 256);
+    const f32x4 v = *(const GAS f32x4 *)((const GAS float *)(ws + P.hbuf) + slot * d.de + (size_t)b * 256 + 4 * lane);
+    GAS uint8_t *q = (GAS uint8_t *)(ws + P.hq + slot * P.hq_stride);
+    quant_block_to(DT_Q8_K, v, true, lane, (GAS uint32_t *)q, (GAS int16_t *)(q + nbd * 256),
+                   (GAS float *)(q + nbd * 288), b);
+}
+
+/* Rows of down (each wave: 32 rows x up to 32 slots of one expert). */
+__global__ __launch_bounds__(256) void k_pf_down(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
+    __shared__ float s_da[4][tokmm::TM_TOK];
+    args_now(d.D, d.de, d.experts, P.tiles, P.hq, P.hq_stride, P.out, ws);
+    const GAS int32_t *tl = (const GAS int32_t *)(ws + P.tiles) + 3 * blockIdx.y;
+    const int e = tl[0];
+    if (e < 0) return;
+    const int s0 = tl[1], n = tl[2];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, half = lane >> 5;
+    const int64_t rows = d.D, row = (int64_t)blockIdx.x * 128 + wave * 32 + j;
+    const int64_t rr = row < rows ? row : rows - 1;
+    const int nb = (int)(d.de / 256);
+    const int64_t units = (rows / TILE_ROWS) * nb * TILE_ROWS;
+    const int64_t ubase = (rr / TILE_ROWS) * nb * TILE_ROWS + rr % TILE_ROWS;
+    const int slot = s0 + (j < n ? j : n - 1);
+    const GAS uint8_t *arow = (const GAS uint8_t *)(ws + P.hq + (size_t)slot * P.hq_stride);
+    const uint8_t *wd = (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * e + 2];
+    float acc[16];
+    tokmm::tile_q6k<true>(wd, units, ubase, nb, arow, (LAS float *)s_da[wave], j, half, acc);
+    if (row < rows) {
+        GAS float *out = (GAS float *)(ws + P.out);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int i = 8 * (v >> 2) + 4 * half + (v & 3);
+            if (i < n) out[(size_t)(s0 + i) * rows + row] = acc[v];
+        }
+    }
+}
+
+/* h[t] += sum_r w_r * out[slot(t, r)] in rank order (src/lib/tlm_model.c:1029-1050). */
+__global__ __launch_bounds__(256) void k_pf_combine(tlm_hip_moe_desc d, PfLayout P, float *__restrict__ h,
+                                                    uint8_t *ws) {
+    args_now(d.D, d.k, P.pair_w, P.slot_of, P.out, h, ws);
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y;
+    if (row >= d.D) return;
+    const GAS float *pw = (const GAS float *)(ws + P.pair_w) + (size_t)t * d.k;
+    const GAS int32_t *so = (const GAS int32_t *)(ws + P.slot_of) + (size_t)t * d.k;
+    const GAS float *out = (const GAS float *)(ws + P.out);
+    float ev[MAXK], wv[MAXK];
+#pragma unroll
+    for (int q = 0; q < MAXK; q++) {
+        if (q < d.k) {
+            wv[q] = pw[q];
+            ev[q] = out[(size_t)so[q] * d.D + row];
+        }
+    }
+    const float hv = h[(size_t)t * d.D + row];
+    float ffn = 0.0f;
+#pragma unroll
+    for (int q = 0; q < MAXK; q++) {
+        if (q < d.k) {
+            const float c = wv[q] * ev[q];
+            ffn += c;
+        }
+    }
+    h[(size_t)t * d.D + row] = hv + ffn;
+}
+
 /* ---- instantiation table: [expert dtype][shared dtype or none] --------------- */
 typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *);
 typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *);
@@ -883,10 +1114,8 @@ int launch_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w
 
 static size_t x_area(int kind, int nb) { return (stage_bytes(kind, nb) + 15) & ~(size_t)15; }
 
-/* phase 0 = all launches; 1 router, 2 gate/up, 3 down + combine */
-int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
-                     hipStream_t s) {
-    if (phase < 0 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
+/* descriptor checks shared by the decode and prefill launches */
+static int moe_check(const tlm_hip_moe_desc *d, const float *h, const void *ws) {
     if (!d || !h || !ws) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL argument");
     if ((uintptr_t)ws & 255u) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: workspace must be 256-byte aligned");
     if (d->E <= 0 || d->E > MAXE || d->k <= 0 || d->k > MAXK || d->k > d->E)
@@ -910,6 +1139,17 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     if (!d->ffn_norm || !d->router_w || !d->experts) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL weights");
     if (((uintptr_t)h | (uintptr_t)d->ffn_norm) & 15u)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: h and ffn_norm must be 16-byte aligned");
+    if ((size_t)d->D * 8 > 64 * 1024)
+        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_layer: D=%lld exceeds the LDS staging limit", (long long)d->D);
+    return TLM_HIP_OK;
+}
+
+/* phase 0 = all launches; 1 router, 2 gate/up, 3 down + combine */
+int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
+                     hipStream_t s) {
+    if (phase < 0 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
+    if (int rc = moe_check(d, h, ws)) return rc;
+    const int ebv = dt_block_values(d->expert_dt);
     const int ek = dt_act_kind(d->expert_dt), sk = d->ds > 0 ? dt_act_kind(d->shared_dt) : ek;
     const int nbe = (int)(d->D / ebv), nbde = (int)(d->de / ebv);
     const int sbv = d->ds > 0 ? dt_block_values(d->shared_dt) : ebv;
@@ -933,8 +1173,41 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const unsigned g1 = (unsigned)router_groups(*d);
     const unsigned g2 = (unsigned)(d->k * (d->de / TILE_ROWS) + (d->ds > 0 ? d->ds / TILE_ROWS : 0));
     const unsigned g3 = (unsigned)(d->D / DROWS);
-    if (phase == 0 || phase == 1) hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8);
+    if (phase == 0 || phase == 1)
+        hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8, (size_t)0);
     if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8);
     if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(256), lds3, s, dv, L, h, w8);
     return tlmh_check(hipGetLastError(), "moe_layer launch");
+}
+
+size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T) {
+    return (d && T > 0) ? pf_layout(*d, T).total : 0;
+}
+
+/* T tokens: K1 per token, routing per token, bucketing, gate/up + SwiGLU,
+ * h quantisation, down, combine. */
+int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
+                       hipStream_t s) {
+    if (int rc = moe_check(d, h, ws)) return rc;
+    if (T <= 0 || T > 65536) return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld outside 1..65536", (long long)T);
+    if (d->expert_dt != DT_Q6_K || d->ds > 0)
+        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_prefill: routed Q6_K experts without a shared expert only "
+                           "(expert dtype %d, ds %lld)", d->expert_dt, (long long)d->ds);
+    const tlm_hip_moe_desc dv = *d;
+    const WsLayout L = ws_layout(*d);
+    const PfLayout P = pf_layout(*d, T);
+    uint8_t *w8 = (uint8_t *)ws;
+    const unsigned g1 = (unsigned)router_groups(*d);
+    const size_t lds1 = al256((size_t)d->D * 8);
+    hipLaunchKernelGGL(k_moe_router, dim3(g1, (unsigned)T), dim3(64), lds1, s, dv, L, (const float *)h, w8 + P.tok,
+                       P.tstride);
+    hipLaunchKernelGGL(k_pf_route, dim3((unsigned)T), dim3(256), 0, s, dv, L, P, w8, ids, w);
+    hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(256), 0, s, dv, P, w8);
+    hipLaunchKernelGGL(k_pf_gateup, dim3((unsigned)((d->de + 127) / 128), (unsigned)P.MT), dim3(256), 0, s, dv, L, P,
+                       w8);
+    hipLaunchKernelGGL(k_pf_hquant, dim3((unsigned)(d->de / 256), (unsigned)(T * d->k)), dim3(64), 0, s, dv, P, w8);
+    hipLaunchKernelGGL(k_pf_down, dim3((unsigned)((d->D + 127) / 128), (unsigned)P.MT), dim3(256), 0, s, dv, P, w8);
+    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((d->D + 255) / 256), (unsigned)T), dim3(256), 0, s, dv, P, h,
+                       w8);
+    return tlmh_check(hipGetLastError(), "moe_prefill launch");
 }

@@ -126,6 +126,15 @@ int tlm_hip_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const
     return launch_matvec_packed(dt, Wp, rows, n, act, y, (hipStream_t)stream);
 }
 
+size_t tlm_hip_moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T) {
+    return moe_prefill_workspace_bytes(d, T);
+}
+
+int tlm_hip_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *workspace,
+                        void *stream) {
+    return launch_moe_prefill(d, h, T, ids, w, workspace, (hipStream_t)stream);
+}
+
 int tlm_hip_matmul_tokens(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok,
                           float *Y, void *stream) {
     return launch_tokmm(dt, Wp, rows, n, act, ntok, Y, (hipStream_t)stream);

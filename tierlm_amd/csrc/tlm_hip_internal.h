@@ -64,6 +64,14 @@ __device__ __forceinline__ int rne_clamp(float v, int lo, int hi) {
     return (int)((t + magic) - magic);
 }
 
+/* e^x for the routing softmax / sigmoid and SiLU: exp in double, rounded
+ * once to float - the correctly rounded expf except where the true value lies
+ * within ~2^-52 relative of a float rounding midpoint.  The reference calls
+ * libm's expf, itself within 0.502 ulp, so the two agree except in rare
+ * near-midpoint cases (a float-only device exp is within about 1 ulp and
+ * disagrees far more often). */
+__device__ __forceinline__ float exp_rn(float x) { return (float)exp((double)x); }
+
 /* Address-space qualified pointers.  Pointers that travel through structs,
  * tables or lambdas lose their address space and compile to flat_* accesses,
  * which count against both the vector-memory and the LDS wait counters; the
@@ -137,6 +145,9 @@ int launch_pack(int dt, const void *src, size_t row_bytes, int64_t rows, int64_t
 int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, float *y,
                          hipStream_t s);
 int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s);
+size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T);
+int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
+                       hipStream_t s);
 int launch_tokmm(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok, float *Y,
                  hipStream_t s);
 size_t moe_workspace_bytes(const tlm_hip_moe_desc *d);

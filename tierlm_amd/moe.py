@@ -46,6 +46,24 @@ class MoeBlock:
                                           C.c_void_p(self.ids.data_ptr()), C.c_void_p(self.w.data_ptr()),
                                           C.c_void_p(self.workspace.data_ptr()), stream()))
 
+    def prefill(self, h, ids=None, w=None):
+        """h (f32 device [T, D]): every token's residual += MoE(token), as
+        __call__ would give it one token at a time; routing in ids / w [T, k]
+        when given.  The prefill workspace is kept per token count."""
+        T = h.shape[0]
+        ws = self._pf_ws.get(T) if hasattr(self, "_pf_ws") else None
+        if ws is None:
+            nbytes = int(lib.tlm_hip_moe_prefill_workspace_bytes(C.byref(self.desc), T))
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=h.device)
+            self._pf_ws = getattr(self, "_pf_ws", {})
+            self._pf_ws[T] = ws
+
+        def p(t):
+            return C.c_void_p(t.data_ptr()) if t is not None else None
+        check(lib.tlm_hip_moe_prefill(C.byref(self.desc), C.c_void_p(h.data_ptr()), T, p(ids), p(w),
+                                      C.c_void_p(ws.data_ptr()), stream()))
+        return h
+
     def set_expert_ptrs(self, expert_ptrs):
         """Point the block at another set of packed experts (same geometry)."""
         self.table.copy_(torch.tensor(list(expert_ptrs), dtype=torch.int64))
