@@ -65,6 +65,47 @@ def make_weights(torch, dev, layers, seed):
     return W
 
 
+PREFILL_T = 512
+INT8_PEAK_TOPS = 5000.0                  # MI355X dense int8 MFMA
+
+
+def prefill_bench(torch, dev, W, router_w, ffn_norm, gen):
+    """One 512-token chunk through the same block (layer copy 0's 128
+    experts): router, routing, tokens bucketed per expert, grouped gate/up +
+    SwiGLU and down on int8 MFMA, combine.  Algorithmic bytes = all 128
+    experts once (every expert gets tokens at this size); int8 ops = 2 x
+    tokens x top-8 x 3 x 768 x 2048."""
+    from tierlm_amd import MoeBlock
+    ptrs = [W.data_ptr() + (e * 3 + j) * MAT_BYTES for e in range(E) for j in range(3)]
+    blk = MoeBlock(D=D, de=DE, E=E, k=K, expert_dt=Q6_K, ffn_norm=ffn_norm, router_w=router_w, expert_ptrs=ptrs,
+                   router=0, eps=1e-6, device=dev)
+    H0 = torch.randn((PREFILL_T, D), generator=gen, device=dev)
+    h = H0.clone()
+    blk.prefill(h)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(5):
+        h.copy_(H0)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        blk.prefill(h)
+        ev1.record()
+        ev1.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3
+        best = us if best is None else min(best, us)
+    nbytes = E * EXPERT_BYTES
+    ops = 2.0 * PREFILL_T * K * 3 * DE * D
+    log(f"bench: prefill {PREFILL_T} tokens: {best:.1f} us ({PREFILL_T / best * 1e6:.0f} tok/s), "
+        f"experts {nbytes / best / 1e3:.0f} GB/s, int8 {ops / best / 1e6:.1f} TOP/s")
+    return {"tokens": PREFILL_T, "us": round(best, 1), "tok_s": round(PREFILL_T / best * 1e6, 1),
+            "expert_bytes": nbytes, "expert_GBps": round(nbytes / best / 1e3, 1),
+            "hbm_frac": round(nbytes / best / 1e3 / HBM_PEAK_GBS, 4), "int8_ops": ops,
+            "int8_TOPs": round(ops / best / 1e6, 2), "mfma_util": round(ops / best / 1e6 / INT8_PEAK_TOPS, 4),
+            "timing": "HIP events around one tlm_hip_moe_prefill call (best of 5)",
+            "workload": "512-token chunk, Qwen3-30B-A3B-shape block, 128 random-code Q6_K experts, "
+                        "tokens routed by the seeded f32 router and bucketed per expert"}
+
+
 def cpu_baseline(args, threads):
     """Reference kernels on the host (oracle/_ref), bounded sample."""
     import numpy as np
@@ -110,6 +151,7 @@ def main():
     ap.add_argument("--roofline-tokens", type=int, default=960, help="launches per phase in the roofline graphs")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill measurement")
     ap.add_argument("--copy-check-mib", type=int, default=0,
                     help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
                          "of known size, the scale for HBM byte counters")
@@ -258,6 +300,8 @@ def main():
         log(f"bench: copy check {args.copy_check_mib} MiB done")
         del src, dst
 
+    prefill = None if args.no_prefill else prefill_bench(torch, dev, W, router_w, ffn_norm, gen)
+
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
@@ -289,6 +333,7 @@ def main():
                      "stream_read_peak_GBps": round(stream_gbs, 1),
                      "stream_read_kernel": "k_mv_packed<Q6_K> over ~2 GB of resident expert bytes, one launch (best of 5)"},
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
 
