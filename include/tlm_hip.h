@@ -16,8 +16,9 @@
  * pointers (hipMalloc'd or from any allocator of the same device); `stream`
  * is a hipStream_t passed as void* (NULL = the null stream).  Calls enqueue
  * work and return; results are ready after tlm_hip_sync(stream).  No entry
- * point allocates device memory except tlm_hip_malloc and tlm_hip_init (which
- * sizes the staging area behind tlm_kern_hip_fill's host-pointer entries).
+ * point allocates device memory except tlm_hip_malloc, tlm_hip_init (which
+ * sizes the staging area behind tlm_kern_hip_fill's host-pointer entries) and
+ * tlm_hip_store_open (the slot arena and its staging buffers).
  *
  * Threading: one caller thread per stream.  The host-pointer entries of
  * tlm_kern_hip_fill are serialised internally, so pool workers may call them
@@ -174,6 +175,100 @@ int tlm_hip_moe_layer_phase(const tlm_hip_moe_desc *d, int phase, float *h, int3
 size_t tlm_hip_moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T);
 int tlm_hip_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w,
                         void *workspace, void *stream);
+
+/* ---- expert slot cache in HBM -------------------------------------------------
+ * The reference's routed-expert cache (src/lib/tlm_store.h:24-97; policy
+ * src/lib/tlm_store.c:139-740) with its slots in HBM: equal slots allocated
+ * once, FREE -> LOADING -> READY, every selection counted, counts halved
+ * every 16 ticks, victims by lowest (count, last use) among unreferenced,
+ * unpinned READY slots (a FREE slot first), pins by compiler flag / heat /
+ * warm count up to pin_frac of the slots, and hints that only take FREE or
+ * count-0 slots, bounded in flight so top_k slots stay free for demand.
+ * The same calls give the same slots, return codes and counters as the
+ * reference.
+ *
+ * A slot holds one expert's gate, up and down in the tlm_hip_pack layout
+ * (the moe block's expert table points into slots); bytes_read counts
+ * payload bytes copied into HBM.  Loads run on the store's own stream:
+ * payload -> pinned staging (or straight from the payload when it already
+ * lies in page-locked memory) -> DMA -> pack.  Each expert's payload is the
+ * reference's EXPERT packet payload (gate | up | down at item_off,
+ * src/lib/tlm_packet.h:39-54, rows of tlm_row_bytes), read from `payload`
+ * (host memory the caller keeps alive until close) or, when NULL, written by
+ * the `fetch` callback into staging on the store's loader thread. */
+typedef struct tlm_hip_store tlm_hip_store;
+
+typedef struct {
+    uint16_t    layer;
+    uint16_t    flags;        /* bit0 compiler pin, bit1 pruned (src/lib/tlm_store.c:43-44) */
+    uint32_t    id;
+    int32_t     dtype;        /* Q8_0, Q4_K, Q5_K or Q6_K */
+    float       heat;         /* manifest heat (src/lib/tlm_packet.h:80) */
+    uint32_t    seed;         /* warm-sidecar count (src/lib/tlm_store.c:306-340) */
+    uint32_t    item_off[3];  /* gate, up, down inside the payload */
+    uint64_t    payload_len;
+    const void *payload;      /* host bytes, or NULL: use fetch */
+} tlm_hip_expert_src;
+
+/* Write expert (layer, id)'s payload_len payload bytes to dst; 0 or TLM_E*.
+ * Runs on the store's loader thread. */
+typedef int (*tlm_hip_fetch_fn)(void *user, int layer, int id, void *dst, uint64_t len);
+
+typedef struct {
+    int64_t          d_model, d_expert;  /* gate / up [d_expert x d_model], down [d_model x d_expert] */
+    int32_t          top_k;              /* demand reserve for hints (src/lib/tlm_store.c:406) */
+    int32_t          prefetch;           /* accept hints (tlm_store_opts.prefetch) */
+    double           pin_frac;           /* tlm_store_opts.pin_frac */
+    uint64_t         budget_bytes;       /* HBM for slots, rounded down to whole slots (>= 1) */
+    tlm_hip_fetch_fn fetch;
+    void            *fetch_user;
+} tlm_hip_store_opts;
+
+typedef struct {
+    int32_t     slot;      /* >= 0: acquired (release it); -1: not acquired */
+    const void *mats[3];   /* device: packed gate, up, down inside the slot */
+} tlm_hip_expert_ref;
+
+typedef struct {           /* tlm_store_stats, src/lib/tlm_store.h:66-70 */
+    uint64_t hits, misses, prefetch_issued, prefetch_used, prefetch_dropped;
+    uint64_t bytes_read, evictions, wait_ns;
+    int32_t  slots, pinned, in_use;
+} tlm_hip_store_stats;
+
+/* tlm_store_open (src/lib/tlm_store.h:42-46) over n expert sources; pruned
+ * sources are left out.  Needs tlm_hip_init. */
+int      tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store_opts *o,
+                            tlm_hip_store **out);
+/* Waits for loads in flight; then frees the slots. */
+void     tlm_hip_store_close(tlm_hip_store *s);
+int      tlm_hip_store_n_slots(const tlm_hip_store *s);
+uint64_t tlm_hip_store_slot_bytes(const tlm_hip_store *s);
+/* src/lib/tlm_store.h:48-50: pin the hottest experts; loads them synchronously. */
+int      tlm_hip_store_warm(tlm_hip_store *s);
+/* src/lib/tlm_store.h:52-54, 78-83: every out[i] with slot >= 0 holds a
+ * reference (release it whatever the return code); mats are valid device
+ * addresses at once, their contents after a wait.  Does not block, except
+ * when a miss finds no victim while an unreferenced load is still in flight
+ * (a caller that waits on the device runs ahead of its loads): it then waits
+ * for that load rather than fail with TLM_HIP_EBUSY. */
+int      tlm_hip_store_acquire(tlm_hip_store *s, int layer, const int *ids, int k, tlm_hip_expert_ref *out);
+/* src/lib/tlm_store.h:55-56: block the host until READY; 0, or the load's
+ * error (TLM_E*, e.g. the fetch callback's). */
+int      tlm_hip_store_wait(tlm_hip_store *s, tlm_hip_expert_ref *ref);
+/* Device-side wait: work enqueued on `stream` after this call runs after the
+ * expert's load; the host blocks only until the load has been queued. */
+int      tlm_hip_store_stream_wait(tlm_hip_store *s, const tlm_hip_expert_ref *ref, void *stream);
+int      tlm_hip_store_is_ready(tlm_hip_store *s, const tlm_hip_expert_ref *ref);
+/* src/lib/tlm_store.h:58-59.  `stream`: where the work reading the slot was
+ * enqueued; the slot is not overwritten before that work has finished. */
+void     tlm_hip_store_release(tlm_hip_store *s, tlm_hip_expert_ref *ref, void *stream);
+/* src/lib/tlm_store.h:60-62, 71-77: advisory hints. */
+void     tlm_hip_store_prefetch(tlm_hip_store *s, int layer, const int *ids, int k);
+/* src/lib/tlm_store.h:63-64: once per generated token. */
+void     tlm_hip_store_tick(tlm_hip_store *s);
+/* Block until no load is queued or in flight. */
+int      tlm_hip_store_drain(tlm_hip_store *s);
+void     tlm_hip_store_get_stats(tlm_hip_store *s, tlm_hip_store_stats *out);
 
 /* ---- reference tier ABI --------------------------------------------------
  * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a

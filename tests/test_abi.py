@@ -37,7 +37,7 @@ def test_python_binding_covers_header():
 
 
 def test_struct_layouts_match_c():
-    from tierlm_amd._lib import MoeDesc, QuantKernels, Seg
+    from tierlm_amd._lib import ExpertRef, ExpertSrc, MoeDesc, QuantKernels, Seg, StoreOpts, StoreStats
     prog = r'''
 #include <stdio.h>
 #include <stddef.h>
@@ -49,6 +49,13 @@ int main(void) {
   O(tlm_hip_moe_desc, E); O(tlm_hip_moe_desc, routed_scale); O(tlm_hip_moe_desc, expert_dt);
   O(tlm_hip_moe_desc, ffn_norm); O(tlm_hip_moe_desc, experts); O(tlm_hip_moe_desc, shared_gate_inp);
   O(tlm_hip_quant_kernels, dot); O(tlm_hip_quant_kernels, mv);
+  printf("src %zu\nopts %zu\nref %zu\nstats %zu\n", sizeof(tlm_hip_expert_src), sizeof(tlm_hip_store_opts),
+         sizeof(tlm_hip_expert_ref), sizeof(tlm_hip_store_stats));
+  O(tlm_hip_expert_src, id); O(tlm_hip_expert_src, dtype); O(tlm_hip_expert_src, item_off);
+  O(tlm_hip_expert_src, payload_len); O(tlm_hip_expert_src, payload);
+  O(tlm_hip_store_opts, top_k); O(tlm_hip_store_opts, pin_frac); O(tlm_hip_store_opts, fetch);
+  O(tlm_hip_store_opts, fetch_user); O(tlm_hip_expert_ref, mats);
+  O(tlm_hip_store_stats, wait_ns); O(tlm_hip_store_stats, slots); O(tlm_hip_store_stats, in_use);
   return 0;
 }'''
     with tempfile.TemporaryDirectory() as d:
@@ -62,11 +69,15 @@ int main(void) {
     assert vals["seg"] == C.sizeof(Seg)
     assert vals["moe"] == C.sizeof(MoeDesc)
     assert vals["qk"] == C.sizeof(QuantKernels)
+    for name, cls in (("src", ExpertSrc), ("opts", StoreOpts), ("ref", ExpertRef), ("stats", StoreStats)):
+        assert vals[name] == C.sizeof(cls), name
     for k, v in vals.items():
         if "." not in k:
             continue
         t, f = k.split(".")
-        cls = {"tlm_hip_seg": Seg, "tlm_hip_moe_desc": MoeDesc, "tlm_hip_quant_kernels": QuantKernels}[t]
+        cls = {"tlm_hip_seg": Seg, "tlm_hip_moe_desc": MoeDesc, "tlm_hip_quant_kernels": QuantKernels,
+               "tlm_hip_expert_src": ExpertSrc, "tlm_hip_store_opts": StoreOpts, "tlm_hip_expert_ref": ExpertRef,
+               "tlm_hip_store_stats": StoreStats}[t]
         assert getattr(cls, f).offset == v, k
 
 

@@ -35,6 +35,35 @@ class MoeDesc(C.Structure):
                 ("experts", vp), ("sg", vp), ("su", vp), ("sd", vp), ("shared_gate_inp", vp)]
 
 
+class ExpertSrc(C.Structure):
+    """tlm_hip_expert_src"""
+    _fields_ = [("layer", C.c_uint16), ("flags", C.c_uint16), ("id", C.c_uint32), ("dtype", C.c_int32),
+                ("heat", C.c_float), ("seed", C.c_uint32), ("item_off", C.c_uint32 * 3),
+                ("payload_len", C.c_uint64), ("payload", vp)]
+
+
+FETCH = C.CFUNCTYPE(C.c_int, vp, C.c_int, C.c_int, vp, C.c_uint64)
+
+
+class StoreOpts(C.Structure):
+    """tlm_hip_store_opts"""
+    _fields_ = [("d_model", C.c_int64), ("d_expert", C.c_int64), ("top_k", C.c_int32), ("prefetch", C.c_int32),
+                ("pin_frac", C.c_double), ("budget_bytes", C.c_uint64), ("fetch", FETCH), ("fetch_user", vp)]
+
+
+class ExpertRef(C.Structure):
+    """tlm_hip_expert_ref"""
+    _fields_ = [("slot", C.c_int32), ("mats", vp * 3)]
+
+
+class StoreStats(C.Structure):
+    """tlm_hip_store_stats"""
+    _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("prefetch_issued", C.c_uint64),
+                ("prefetch_used", C.c_uint64), ("prefetch_dropped", C.c_uint64), ("bytes_read", C.c_uint64),
+                ("evictions", C.c_uint64), ("wait_ns", C.c_uint64), ("slots", C.c_int32), ("pinned", C.c_int32),
+                ("in_use", C.c_int32)]
+
+
 QDOT = C.CFUNCTYPE(C.c_float, vp, vp, C.c_int64, vp)
 QMV = C.CFUNCTYPE(None, vp, C.c_size_t, vp, vp, C.c_int64, C.c_int64)
 
@@ -69,6 +98,20 @@ _SIGS = {
     "tlm_hip_moe_layer": (i32, [C.POINTER(MoeDesc), vp, vp, vp, vp, vp]),
     "tlm_hip_moe_layer_phase": (i32, [C.POINTER(MoeDesc), i32, vp, vp, vp, vp, vp]),
     "tlm_kern_hip_fill": (i32, [C.POINTER(QuantKernels)]),
+    "tlm_hip_store_open": (i32, [C.POINTER(ExpertSrc), i32, C.POINTER(StoreOpts), C.POINTER(vp)]),
+    "tlm_hip_store_close": (None, [vp]),
+    "tlm_hip_store_n_slots": (i32, [vp]),
+    "tlm_hip_store_slot_bytes": (C.c_uint64, [vp]),
+    "tlm_hip_store_warm": (i32, [vp]),
+    "tlm_hip_store_acquire": (i32, [vp, i32, C.POINTER(C.c_int), i32, C.POINTER(ExpertRef)]),
+    "tlm_hip_store_wait": (i32, [vp, C.POINTER(ExpertRef)]),
+    "tlm_hip_store_stream_wait": (i32, [vp, C.POINTER(ExpertRef), vp]),
+    "tlm_hip_store_is_ready": (i32, [vp, C.POINTER(ExpertRef)]),
+    "tlm_hip_store_release": (None, [vp, C.POINTER(ExpertRef), vp]),
+    "tlm_hip_store_prefetch": (None, [vp, i32, C.POINTER(C.c_int), i32]),
+    "tlm_hip_store_tick": (None, [vp]),
+    "tlm_hip_store_drain": (i32, [vp]),
+    "tlm_hip_store_get_stats": (None, [vp, C.POINTER(StoreStats)]),
 }
 
 for _name, (_res, _args) in _SIGS.items():

@@ -1,0 +1,720 @@
+/* hip_store.hip - the routed-expert slot cache moved into HBM
+ * (tlm_hip_store_*; the reference's RAM cache is src/lib/tlm_store.c).
+ *
+ * Policy - slot lifecycle FREE -> LOADING -> READY, hits referenced before
+ * misses choose victims, victims by lowest (decayed selection count, last
+ * use), halving every 16 ticks, pins, and the hint rules - is the reference's
+ * (src/lib/tlm_store.c:139-740); the same operation scripts give the same
+ * slots and counters (tests/test_hip_store.py).  What changes is where the
+ * bytes live and how they get there:
+ *
+ *   - one hipMalloc arena of equal slots; a slot holds an expert's gate, up
+ *     and down in the packed tile layout the MoE kernels read;
+ *   - a load is host payload -> pinned staging (a loader thread copies, or
+ *     calls the fetch callback; a payload already in pinned memory is DMA'd
+ *     straight from where it lies) -> one DMA into a device staging buffer
+ *     on the store's side stream -> three pack kernels into the slot -> an
+ *     event per slot.  The caller's compute stream never blocks on a copy;
+ *   - READY is published when the host sees the slot's event complete;
+ *     tlm_hip_store_stream_wait lets a stream wait for a LOADING slot on the
+ *     device instead;
+ *   - release records an event on the caller's stream; the next load into
+ *     that slot waits for it on the side stream, so a slot is never
+ *     overwritten while kernels enqueued before the release still read it.
+ *
+ * Threading: one mutex guards the policy state; the loader thread takes it
+ * only to pick up jobs and to publish a submitted load. */
+#include "tlm_hip_internal.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <chrono>
+#include <condition_variable>
+#include <deque>
+#include <mutex>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+int tlmh_current_device(void);
+
+namespace {
+
+enum { S_FREE = 0, S_LOADING = 1, S_READY = 2 };
+enum { K_DEMAND = 0, K_HINT = 1, K_PIN = 2 };
+constexpr int DECAY_TICKS = 16;      /* tlm_store.c:41 */
+constexpr int HINT_BACKLOG = 4;      /* tlm_store.c:42 */
+constexpr int HINT_INFLIGHT = 16;    /* tlm_store.c:43 */
+constexpr int NSTAGE = 3;            /* staging buffers: fill, DMA and pack overlap */
+constexpr size_t MAT_ALIGN = 256;
+
+struct Expert {
+    tlm_hip_expert_src src;
+    size_t off[3];          /* packed gate / up / down inside a slot */
+    int64_t rows[3], n[3];
+    bool pinned_src;        /* payload lies in page-locked host memory */
+    uint32_t freq = 0;
+    int slot = -1;
+};
+
+struct Slot {
+    int state = S_FREE, ex = -1, refs = 0, pinned = 0, hinted = 0, demand = 0, err = 0;
+    uint64_t last = 0;
+    uint64_t gen = 0;           /* bumped by every start_load */
+    bool submitted = false;     /* `loaded` recorded for generation gen */
+    bool reads_pending = false; /* `released` recorded since the last load took it */
+    hipEvent_t loaded = nullptr, released = nullptr;
+};
+
+struct Job {
+    int v, e;
+    uint64_t gen;
+};
+
+uint64_t key_of(int layer, int id) { return ((uint64_t)(uint32_t)layer << 32) | (uint32_t)id; }
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int64_t now_ns() {
+    return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+}  // namespace
+
+struct tlm_hip_store {
+    std::mutex mu;
+    std::condition_variable cv;
+    int device = -1;
+    hipStream_t side = nullptr;
+    tlm_hip_store_opts o{};
+    std::vector<Expert> ex;
+    std::unordered_map<uint64_t, int> index;
+    int n_slots = 0, reserve = 1;
+    size_t slot_bytes = 0, stage_bytes = 0;
+    uint8_t *arena = nullptr;
+    std::vector<Slot> sl;
+    uint8_t *stage_host[NSTAGE] = {}, *stage_dev[NSTAGE] = {};
+    hipEvent_t stage_free[NSTAGE] = {};
+    int stage_next = 0;                 /* loader thread only */
+    std::deque<Job> jobs;
+    int unsubmitted = 0;                /* LOADING slots whose job has not been submitted */
+    std::thread loader;
+    bool stop = false;
+    uint64_t clock = 0, ticks = 0;
+    int loading = 0, demand_loading = 0, hint_loading = 0, n_pinned = 0;
+    tlm_hip_store_stats st{};
+
+    int find(int layer, int id) const {
+        if (layer < 0 || id < 0) return -1;
+        auto it = index.find(key_of(layer, id));
+        return it == index.end() ? -1 : it->second;
+    }
+
+    /* ---- policy (all with mu held) ------------------------------------ */
+    void fail_slot(int v, int err) {            /* tlm_store.c:139-158 */
+        Slot &s = sl[v];
+        if (s.ex >= 0 && ex[s.ex].slot == v) ex[s.ex].slot = -1;
+        if (s.state == S_LOADING) {
+            loading--;
+            if (s.demand) demand_loading--;
+            else hint_loading--;
+            if (!s.submitted) unsubmitted--;
+        }
+        s.state = S_FREE;
+        if (s.pinned) n_pinned--;
+        s.pinned = s.hinted = s.demand = 0;
+        s.last = 0;
+        s.submitted = false;
+        if (s.refs > 0) {
+            s.err = err;
+        } else {
+            s.err = 0;
+            s.ex = -1;
+        }
+        cv.notify_all();
+    }
+
+    void start_load(int v, int e, int kind) {   /* tlm_store.c:162-189 */
+        Slot &s = sl[v];
+        if (s.state == S_READY && s.ex >= 0) {
+            ex[s.ex].slot = -1;
+            st.evictions++;
+        }
+        loading++;
+        s.state = S_LOADING;
+        s.ex = e;
+        ex[e].slot = v;
+        s.refs = kind == K_HINT ? 0 : 1;
+        s.pinned = kind == K_PIN;
+        if (s.pinned) n_pinned++;
+        s.hinted = kind == K_HINT;
+        s.demand = kind != K_HINT;
+        if (s.demand) demand_loading++;
+        else hint_loading++;
+        s.err = 0;
+        s.last = kind == K_HINT ? 0 : clock;
+        s.gen++;
+        s.submitted = false;
+        unsubmitted++;
+        jobs.push_back(Job{v, e, s.gen});
+        cv.notify_all();
+    }
+
+    void complete(int v) {                      /* the publish step, tlm_store.c:273-282 */
+        Slot &s = sl[v];
+        s.state = S_READY;
+        loading--;
+        if (s.demand) demand_loading--;
+        else hint_loading--;
+        st.bytes_read += ex[s.ex].src.payload_len;
+        cv.notify_all();
+    }
+
+    /* LOADING -> READY once the slot's event has completed on the device */
+    void refresh(int v) {
+        Slot &s = sl[v];
+        if (s.state != S_LOADING || !s.submitted) return;
+        hipError_t q = hipEventQuery(s.loaded);
+        if (q == hipSuccess) complete(v);
+        else if (q != hipErrorNotReady) fail_slot(v, tlmh_check(q, "store: load"));
+    }
+    void refresh_all() {
+        for (int v = 0; v < n_slots; v++) refresh(v);
+    }
+
+    int pick_victim(int kind) const {           /* tlm_store.c:196-214 */
+        int best = -1;
+        uint32_t bf = 0;
+        uint64_t bl = 0;
+        for (int i = 0; i < n_slots; i++) {
+            const Slot &s = sl[i];
+            if (s.refs > 0 || s.pinned) continue;
+            if (s.state == S_FREE) return i;
+            if (s.state != S_READY) continue;
+            uint32_t f = ex[s.ex].freq;
+            if (kind == K_HINT && f > 0) continue;
+            if (best < 0 || f < bf || (f == bf && s.last < bl)) {
+                best = i;
+                bf = f;
+                bl = s.last;
+            }
+        }
+        return best;
+    }
+
+    void take_ref(int v, uint64_t stamp, tlm_hip_expert_ref *r) {   /* tlm_store.c:216-234 */
+        Slot &s = sl[v];
+        s.refs++;
+        s.last = stamp;
+        if (s.hinted) {
+            s.hinted = 0;
+            st.prefetch_used++;
+        }
+        if (s.state == S_LOADING && !s.demand) {
+            s.demand = 1;
+            hint_loading--;
+            demand_loading++;
+        }
+        r->slot = v;
+        const Expert &x = ex[s.ex];
+        for (int m = 0; m < 3; m++) r->mats[m] = arena + (size_t)v * slot_bytes + x.off[m];
+    }
+
+    void drop_ref(int v) {                      /* tlm_store.c:236-246 */
+        Slot &s = sl[v];
+        if (s.refs <= 0) return;
+        if (--s.refs == 0 && s.state == S_FREE) {
+            s.err = 0;
+            s.ex = -1;
+        }
+    }
+
+    /* ---- the loader thread ------------------------------------------------ */
+    int run_job(const Job &j) {
+        const Expert &x = ex[j.e];
+        const int i = stage_next;
+        stage_next = (stage_next + 1) % NSTAGE;
+        int rc = tlmh_check(hipEventSynchronize(stage_free[i]), "store: staging buffer");
+        if (rc) return rc;
+        const void *src = x.src.payload;
+        const uint64_t len = x.src.payload_len;
+        if (!x.pinned_src) {
+            if (src) {
+                memcpy(stage_host[i], src, len);
+            } else {
+                rc = o.fetch(o.fetch_user, x.src.layer, (int)x.src.id, stage_host[i], len);
+                if (rc) return rc < 0 ? rc : TLM_HIP_EIO;
+            }
+            src = stage_host[i];
+        }
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            Slot &s = sl[j.v];
+            if (s.gen != j.gen || s.state != S_LOADING) return TLM_HIP_OK;   /* superseded */
+            if (s.reads_pending) {   /* kernels enqueued before the last release still read the slot */
+                rc = tlmh_check(hipStreamWaitEvent(side, s.released, 0), "store: wait for release");
+                if (rc) return rc;
+                s.reads_pending = false;
+            }
+        }
+        rc = tlmh_check(hipMemcpyAsync(stage_dev[i], src, len, hipMemcpyHostToDevice, side), "store: DMA");
+        uint8_t *base = arena + (size_t)j.v * slot_bytes;
+        const int dt = x.src.dtype;
+        for (int m = 0; m < 3 && !rc; m++)
+            rc = launch_pack(dt, stage_dev[i] + x.src.item_off[m], (size_t)(x.n[m] / dt_block_values(dt)) *
+                             (size_t)dt_block_bytes(dt), x.rows[m], x.n[m], base + x.off[m], side);
+        if (!rc) rc = tlmh_check(hipEventRecord(sl[j.v].loaded, side), "store: record load");
+        int rc2 = tlmh_check(hipEventRecord(stage_free[i], side), "store: record staging");
+        return rc ? rc : rc2;
+    }
+
+    void loader_main() {
+        (void)hipSetDevice(device);
+        for (;;) {
+            Job j;
+            {
+                std::unique_lock<std::mutex> lk(mu);
+                cv.wait(lk, [&] { return stop || !jobs.empty(); });
+                if (jobs.empty()) return;
+                j = jobs.front();
+                jobs.pop_front();
+            }
+            int rc = run_job(j);
+            std::lock_guard<std::mutex> lk(mu);
+            Slot &s = sl[j.v];
+            if (s.gen != j.gen || s.state != S_LOADING) continue;
+            if (rc) {
+                fail_slot(j.v, rc);
+            } else {
+                s.submitted = true;
+                unsubmitted--;
+                cv.notify_all();
+            }
+        }
+    }
+
+    /* A demand miss found no victim while some unreferenced, unpinned slot is
+     * still LOADING (a caller that waits on the device runs ahead of the
+     * loads): block until one such load has finished, as the reference's
+     * read would have by then.  false when there is none (then: EBUSY). */
+    bool wait_unreferenced_load(std::unique_lock<std::mutex> &lk) {
+        int v = -1;
+        for (int i = 0; i < n_slots && v < 0; i++)
+            if (sl[i].state == S_LOADING && sl[i].refs == 0 && !sl[i].pinned) v = i;
+        if (v < 0) return false;
+        const int64_t t0 = now_ns();
+        const uint64_t gen = sl[v].gen;
+        cv.wait(lk, [&] { return sl[v].gen != gen || sl[v].state != S_LOADING || sl[v].submitted; });
+        if (sl[v].gen == gen && sl[v].state == S_LOADING) {
+            hipEvent_t ev = sl[v].loaded;
+            lk.unlock();
+            (void)hipEventSynchronize(ev);
+            lk.lock();
+            refresh(v);
+        }
+        st.wait_ns += (uint64_t)(now_ns() - t0);
+        return true;
+    }
+
+    /* wait (mu held through lk) until no job is queued or unsubmitted */
+    void drain_jobs(std::unique_lock<std::mutex> &lk) {
+        cv.wait(lk, [&] { return unsubmitted == 0 && jobs.empty(); });
+    }
+
+    void destroy() {
+        if (loader.joinable()) {
+            {
+                std::unique_lock<std::mutex> lk(mu);
+                drain_jobs(lk);
+                stop = true;
+                cv.notify_all();
+            }
+            loader.join();
+        }
+        if (side) (void)hipStreamSynchronize(side);
+        for (Slot &s : sl) {
+            if (s.loaded) (void)hipEventDestroy(s.loaded);
+            if (s.released) (void)hipEventDestroy(s.released);
+        }
+        for (int i = 0; i < NSTAGE; i++) {
+            if (stage_free[i]) (void)hipEventDestroy(stage_free[i]);
+            if (stage_host[i]) (void)hipHostFree(stage_host[i]);
+            if (stage_dev[i]) (void)hipFree(stage_dev[i]);
+        }
+        if (arena) (void)hipFree(arena);
+        if (side) (void)hipStreamDestroy(side);
+    }
+};
+
+namespace {
+
+struct PinCand {
+    int e, cp;
+    float heat;
+    uint32_t seed;
+    uint16_t layer;
+    uint32_t id;
+};
+
+/* tlm_store.c:516-523: compiler pins, heat, sidecar count, (layer, id) */
+bool pin_before(const PinCand &x, const PinCand &y) {
+    if (x.cp != y.cp) return x.cp > y.cp;
+    if (x.heat != y.heat) return x.heat > y.heat;
+    if (x.seed != y.seed) return x.seed > y.seed;
+    if (x.layer != y.layer) return x.layer < y.layer;
+    return x.id < y.id;
+}
+
+bool host_pinned(const void *p) {
+    hipPointerAttribute_t a;
+    hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();   /* an unknown (pageable) pointer is not an error here */
+        return false;
+    }
+    return a.type == hipMemoryTypeHost;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store_opts *o, tlm_hip_store **out) {
+    if (!out) return tlmh_seterr(TLM_HIP_EINVAL, "store open: NULL out");
+    *out = nullptr;
+    if (!o || n < 0 || (n > 0 && !src)) return tlmh_seterr(TLM_HIP_EINVAL, "store open: bad arguments");
+    const int dev = tlmh_current_device();
+    if (dev < 0) return tlmh_seterr(TLM_HIP_EUNSUP, "store open: tlm_hip_init has not run");
+    const int64_t D = o->d_model, de = o->d_expert;
+    if (D <= 0 || de <= 0) return tlmh_seterr(TLM_HIP_EINVAL, "store open: d_model %lld, d_expert %lld",
+                                              (long long)D, (long long)de);
+    tlm_hip_store *s = new (std::nothrow) tlm_hip_store;
+    if (!s) return tlmh_seterr(TLM_HIP_ENOMEM, "store open: out of memory");
+    s->device = dev;
+    s->o = *o;
+    s->reserve = o->top_k > 0 ? std::min(o->top_k, 1024) : 1;   /* tlm_store.c:406 */
+    for (int i = 0; i < n; i++) {
+        const tlm_hip_expert_src &x = src[i];
+        if (x.flags & 2u) continue;   /* pruned (tlm_store.c:429) */
+        const int dt = x.dtype;
+        if (dt != DT_Q8_0 && dt != DT_Q4_K && dt != DT_Q5_K && dt != DT_Q6_K) {
+            delete s;
+            return tlmh_seterr(TLM_HIP_EUNSUP, "store open: expert %u:%u dtype %d", x.layer, x.id, dt);
+        }
+        const int bv = dt_block_values(dt);
+        if (D % bv || de % bv) {
+            delete s;
+            return tlmh_seterr(TLM_HIP_EINVAL, "store open: d_model / d_expert not multiples of %d", bv);
+        }
+        Expert e;
+        e.src = x;
+        e.rows[0] = e.rows[1] = de;
+        e.n[0] = e.n[1] = D;
+        e.rows[2] = D;
+        e.n[2] = de;
+        size_t at = 0;
+        for (int m = 0; m < 3; m++) {
+            const uint64_t raw = (uint64_t)(e.n[m] / bv) * dt_block_bytes(dt) * (uint64_t)e.rows[m];
+            if ((uint64_t)x.item_off[m] + raw > x.payload_len) {
+                delete s;
+                return tlmh_seterr(TLM_HIP_EFORMAT, "store open: expert %u:%u item %d overruns its payload",
+                                   x.layer, x.id, m);
+            }
+            e.off[m] = at;
+            at += align_up(packed_bytes(dt, e.rows[m], e.n[m]), MAT_ALIGN);
+        }
+        if (!x.payload && !o->fetch) {
+            delete s;
+            return tlmh_seterr(TLM_HIP_EINVAL, "store open: expert %u:%u has no payload and no fetch", x.layer, x.id);
+        }
+        e.pinned_src = x.payload && host_pinned(x.payload);
+        s->slot_bytes = std::max(s->slot_bytes, at);
+        s->stage_bytes = std::max(s->stage_bytes, (size_t)x.payload_len);
+        const uint64_t k = key_of(x.layer, (int)x.id);
+        if (s->index.count(k)) {
+            delete s;
+            return tlmh_seterr(TLM_HIP_EFORMAT, "store open: duplicate expert %u:%u", x.layer, x.id);
+        }
+        s->index[k] = (int)s->ex.size();
+        s->ex.push_back(e);
+    }
+    int rc = TLM_HIP_OK;
+    if (!s->ex.empty()) {   /* tlm_store.c:449-457: whole slots, at least one, at most one per expert */
+        uint64_t ns = o->budget_bytes / s->slot_bytes;
+        ns = std::max<uint64_t>(ns, 1);
+        ns = std::min<uint64_t>(ns, s->ex.size());
+        s->n_slots = (int)ns;
+        s->sl.resize(ns);
+        rc = tlmh_check(hipMalloc((void **)&s->arena, ns * s->slot_bytes), "store: slot arena");
+        for (size_t v = 0; v < ns && !rc; v++) {
+            rc = tlmh_check(hipEventCreateWithFlags(&s->sl[v].loaded, hipEventDisableTiming), "store: event");
+            if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->sl[v].released, hipEventDisableTiming), "store: event");
+        }
+        if (!rc) rc = tlmh_check(hipStreamCreateWithFlags(&s->side, hipStreamNonBlocking), "store: side stream");
+        for (int i = 0; i < NSTAGE && !rc; i++) {
+            rc = tlmh_check(hipHostMalloc((void **)&s->stage_host[i], s->stage_bytes, hipHostMallocDefault),
+                            "store: pinned staging");
+            if (!rc) rc = tlmh_check(hipMalloc((void **)&s->stage_dev[i], s->stage_bytes), "store: device staging");
+            if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->stage_free[i], hipEventDisableTiming), "store: event");
+        }
+        if (!rc) s->loader = std::thread([s] { s->loader_main(); });
+    }
+    if (rc) {
+        s->destroy();
+        delete s;
+        return rc;
+    }
+    *out = s;
+    return TLM_HIP_OK;
+}
+
+void tlm_hip_store_close(tlm_hip_store *s) {
+    if (!s) return;
+    s->destroy();
+    delete s;
+}
+
+int tlm_hip_store_n_slots(const tlm_hip_store *s) { return s ? s->n_slots : 0; }
+uint64_t tlm_hip_store_slot_bytes(const tlm_hip_store *s) { return s ? s->slot_bytes : 0; }
+
+/* tlm_store.c:525-583 */
+int tlm_hip_store_warm(tlm_hip_store *s) {
+    if (!s) return tlmh_seterr(TLM_HIP_EINVAL, "store warm: NULL");
+    if (s->n_slots == 0) return TLM_HIP_OK;
+    double frac = s->o.pin_frac;
+    if (!(frac > 0.0)) return TLM_HIP_OK;
+    if (frac > 0.9) frac = 0.9;
+    int target = (int)floor(frac * s->n_slots);
+    if (target > s->n_slots - 1) target = s->n_slots - 1;
+    if (target <= 0) return TLM_HIP_OK;
+    std::unique_lock<std::mutex> lk(s->mu);
+    std::vector<PinCand> c;
+    for (int i = 0; i < (int)s->ex.size(); i++) {
+        const tlm_hip_expert_src &x = s->ex[i].src;
+        const int cp = (x.flags & 1u) != 0;
+        if (!cp && !(x.heat > 0.0f) && x.seed == 0) continue;
+        c.push_back(PinCand{i, cp, x.heat, x.seed, x.layer, x.id});
+    }
+    std::stable_sort(c.begin(), c.end(), pin_before);
+    int pinned = s->n_pinned, rc = TLM_HIP_OK;
+    std::vector<int> mine;
+    for (size_t i = 0; i < c.size() && pinned < target; i++) {
+        int e = c[i].e, v = s->ex[e].slot;
+        if (v >= 0) {
+            if (!s->sl[v].pinned) {
+                s->sl[v].pinned = 1;
+                s->n_pinned++;
+                pinned++;
+            }
+            continue;
+        }
+        v = s->pick_victim(K_PIN);
+        if (v < 0) break;
+        s->start_load(v, e, K_PIN);
+        mine.push_back(v);
+        pinned++;
+    }
+    for (int v : mine) {
+        Slot &sl = s->sl[v];
+        while (sl.state == S_LOADING) {
+            if (!sl.submitted) {
+                s->cv.wait(lk);
+                continue;
+            }
+            hipEvent_t ev = sl.loaded;
+            lk.unlock();
+            (void)hipEventSynchronize(ev);
+            lk.lock();
+            s->refresh(v);
+        }
+        if (sl.state != S_READY && rc == TLM_HIP_OK)
+            rc = tlmh_seterr(sl.err ? sl.err : TLM_HIP_EIO, "store warm: pinned expert failed to load");
+        s->drop_ref(v);
+    }
+    return rc;
+}
+
+/* tlm_store.c:586-640 */
+int tlm_hip_store_acquire(tlm_hip_store *s, int layer, const int *ids, int k, tlm_hip_expert_ref *out) {
+    if (!s || k < 0 || (k > 0 && (!ids || !out))) return tlmh_seterr(TLM_HIP_EINVAL, "store acquire: bad arguments");
+    int rc = TLM_HIP_OK;
+    std::unique_lock<std::mutex> lk(s->mu);
+    s->refresh_all();
+    const uint64_t stamp = ++s->clock;
+    for (int i = 0; i < k; i++) {
+        out[i].slot = -1;
+        out[i].mats[0] = out[i].mats[1] = out[i].mats[2] = nullptr;
+        const int e = s->find(layer, ids[i]);
+        if (e < 0) {
+            if (rc == TLM_HIP_OK)
+                rc = tlmh_seterr(TLM_HIP_ENOTFOUND, "store: layer %d expert %d has no packet (absent or pruned)",
+                                 layer, ids[i]);
+            continue;
+        }
+        if (s->ex[e].freq < UINT32_MAX) s->ex[e].freq++;
+    }
+    for (int i = 0; i < k; i++) {   /* hits first: a miss never evicts this step's hit */
+        const int e = s->find(layer, ids[i]);
+        if (e < 0 || s->ex[e].slot < 0) continue;
+        s->take_ref(s->ex[e].slot, stamp, &out[i]);
+        s->st.hits++;
+    }
+    for (int i = 0; i < k; i++) {
+        if (out[i].slot >= 0) continue;
+        const int e = s->find(layer, ids[i]);
+        if (e < 0) continue;
+        if (s->ex[e].slot >= 0) {   /* repeated id, placed earlier in this pass */
+            s->take_ref(s->ex[e].slot, stamp, &out[i]);
+            s->st.hits++;
+            continue;
+        }
+        int v = s->pick_victim(K_DEMAND);
+        while (v < 0 && s->wait_unreferenced_load(lk)) v = s->pick_victim(K_DEMAND);
+        if (v < 0) {
+            if (rc == TLM_HIP_OK)
+                rc = tlmh_seterr(TLM_HIP_EBUSY, "store: all %d slots are referenced or pinned; the slot budget "
+                                 "must hold at least top_k unpinned slots", s->n_slots);
+            continue;
+        }
+        s->st.misses++;
+        s->start_load(v, e, K_DEMAND);
+        const Expert &x = s->ex[e];
+        out[i].slot = v;
+        for (int m = 0; m < 3; m++) out[i].mats[m] = s->arena + (size_t)v * s->slot_bytes + x.off[m];
+    }
+    return rc;
+}
+
+static int wait_status(tlm_hip_store *s, int v) {
+    const Slot &sl = s->sl[v];
+    if (sl.state == S_READY) return TLM_HIP_OK;
+    const int rc = sl.err ? sl.err : TLM_HIP_EIO;
+    if (sl.ex >= 0)
+        return tlmh_seterr(rc, "store: layer %u expert %u could not be loaded", s->ex[sl.ex].src.layer,
+                           s->ex[sl.ex].src.id);
+    return tlmh_seterr(rc, "store: expert could not be loaded");
+}
+
+/* tlm_store.c:642-671: blocks the host until the slot is READY */
+int tlm_hip_store_wait(tlm_hip_store *s, tlm_hip_expert_ref *ref) {
+    if (!s || !ref) return tlmh_seterr(TLM_HIP_EINVAL, "store wait: NULL argument");
+    if (ref->slot < 0 || ref->slot >= s->n_slots) return tlmh_seterr(TLM_HIP_EINVAL, "store wait: expert was not acquired");
+    const int v = ref->slot;
+    std::unique_lock<std::mutex> lk(s->mu);
+    int64_t t0 = 0;
+    Slot &sl = s->sl[v];
+    s->refresh(v);
+    while (sl.state == S_LOADING) {
+        if (!t0) t0 = now_ns();
+        if (!sl.submitted) {
+            s->cv.wait(lk);
+            continue;
+        }
+        hipEvent_t ev = sl.loaded;
+        lk.unlock();
+        (void)hipEventSynchronize(ev);
+        lk.lock();
+        s->refresh(v);
+    }
+    if (t0) s->st.wait_ns += (uint64_t)(now_ns() - t0);
+    return wait_status(s, v);
+}
+
+/* The device-side wait: work enqueued on `stream` after this call runs after
+ * the slot's load.  The host blocks only until the load has been submitted. */
+int tlm_hip_store_stream_wait(tlm_hip_store *s, const tlm_hip_expert_ref *ref, void *stream) {
+    if (!s || !ref) return tlmh_seterr(TLM_HIP_EINVAL, "store stream wait: NULL argument");
+    if (ref->slot < 0 || ref->slot >= s->n_slots)
+        return tlmh_seterr(TLM_HIP_EINVAL, "store stream wait: expert was not acquired");
+    const int v = ref->slot;
+    std::unique_lock<std::mutex> lk(s->mu);
+    Slot &sl = s->sl[v];
+    s->refresh(v);
+    s->cv.wait(lk, [&] { return sl.state != S_LOADING || sl.submitted; });
+    if (sl.state == S_LOADING)
+        return tlmh_check(hipStreamWaitEvent((hipStream_t)stream, sl.loaded, 0), "store: stream wait");
+    return wait_status(s, v);
+}
+
+int tlm_hip_store_is_ready(tlm_hip_store *s, const tlm_hip_expert_ref *ref) {
+    if (!s || !ref || ref->slot < 0 || ref->slot >= s->n_slots) return 0;
+    std::lock_guard<std::mutex> lk(s->mu);
+    s->refresh(ref->slot);
+    return s->sl[ref->slot].state == S_READY;
+}
+
+/* tlm_store.c:681-692, plus the device-side ordering: the slot is not
+ * overwritten before the work enqueued on `stream` up to now has finished */
+void tlm_hip_store_release(tlm_hip_store *s, tlm_hip_expert_ref *ref, void *stream) {
+    if (!s || !ref) return;
+    if (ref->slot >= 0 && ref->slot < s->n_slots) {
+        std::lock_guard<std::mutex> lk(s->mu);
+        Slot &sl = s->sl[ref->slot];
+        if (sl.refs > 0 && hipEventRecord(sl.released, (hipStream_t)stream) == hipSuccess) sl.reads_pending = true;
+        s->drop_ref(ref->slot);
+    }
+    ref->slot = -1;
+    ref->mats[0] = ref->mats[1] = ref->mats[2] = nullptr;
+}
+
+/* tlm_store.c:694-718 */
+void tlm_hip_store_prefetch(tlm_hip_store *s, int layer, const int *ids, int k) {
+    if (!s || !s->o.prefetch || !ids || k <= 0) return;
+    std::lock_guard<std::mutex> lk(s->mu);
+    s->refresh_all();
+    int cap = s->n_slots - s->n_pinned - s->reserve;
+    if (cap > HINT_INFLIGHT) cap = HINT_INFLIGHT;
+    for (int i = 0; i < k; i++) {
+        const int e = s->find(layer, ids[i]);
+        if (e < 0 || s->ex[e].slot >= 0) continue;
+        if (s->demand_loading > HINT_BACKLOG || s->hint_loading >= cap) {
+            s->st.prefetch_dropped++;
+            continue;
+        }
+        const int v = s->pick_victim(K_HINT);
+        if (v < 0) {
+            s->st.prefetch_dropped++;
+            continue;
+        }
+        s->start_load(v, e, K_HINT);
+        s->st.prefetch_issued++;
+    }
+}
+
+/* tlm_store.c:720-726 */
+void tlm_hip_store_tick(tlm_hip_store *s) {
+    if (!s) return;
+    std::lock_guard<std::mutex> lk(s->mu);
+    if (++s->ticks % DECAY_TICKS == 0)
+        for (Expert &x : s->ex) x.freq >>= 1;
+}
+
+/* Every queued load submitted and finished (READY or failed). */
+int tlm_hip_store_drain(tlm_hip_store *s) {
+    if (!s) return tlmh_seterr(TLM_HIP_EINVAL, "store drain: NULL");
+    std::unique_lock<std::mutex> lk(s->mu);
+    s->drain_jobs(lk);
+    lk.unlock();
+    int rc = s->side ? tlmh_check(hipStreamSynchronize(s->side), "store drain") : TLM_HIP_OK;
+    lk.lock();
+    s->refresh_all();
+    return rc;
+}
+
+/* tlm_store.c:728-740 */
+void tlm_hip_store_get_stats(tlm_hip_store *s, tlm_hip_store_stats *out) {
+    if (!out) return;
+    memset(out, 0, sizeof *out);
+    if (!s) return;
+    std::lock_guard<std::mutex> lk(s->mu);
+    *out = s->st;
+    out->slots = s->n_slots;
+    out->pinned = s->n_pinned;
+    for (const Slot &sl : s->sl) out->in_use += sl.refs > 0;
+}
+
+}  // extern "C"

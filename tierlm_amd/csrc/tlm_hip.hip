@@ -42,6 +42,8 @@ static uint8_t *g_stage = nullptr;      /* device staging for host-pointer entri
 static size_t g_stage_bytes = 0;
 static hipStream_t g_stage_stream = nullptr;
 
+int tlmh_current_device(void) { return g_device; }
+
 extern "C" {
 
 const char *tlm_hip_errmsg(void) { return g_err; }
