@@ -164,6 +164,12 @@ int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *
 int tlm_hip_moe_layer_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w,
                             void *workspace, void *stream);
 
+/* Routing alone: route() of src/lib/tlm_model.c:798-839 after rmsnorm and
+ * the router, ids[k] / w[k] (device) exactly as tlm_hip_moe_layer routes the
+ * same h.  The expert matrices are not read. */
+int tlm_hip_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, float *w, void *workspace,
+                      void *stream);
+
 /* ---- prefill: T tokens through the routed MoE block ---------------------------
  * src/lib/tlm_model.c:1105-1113 runs the decode step once per token; the MoE
  * block has no cross-token terms, so this gives every token exactly the
@@ -269,6 +275,27 @@ void     tlm_hip_store_tick(tlm_hip_store *s);
 /* Block until no load is queued or in flight. */
 int      tlm_hip_store_drain(tlm_hip_store *s);
 void     tlm_hip_store_get_stats(tlm_hip_store *s, tlm_hip_store_stats *out);
+
+/* One routed MoE block with its experts in the cache: moe() of
+ * src/lib/tlm_model.c:960-1055 with tlm_store_acquire, the router lookahead
+ * (:844-877, issued at :988-991) and the releases.  Routes on device, reads
+ * the routing back (one round trip, shared with the hints), acquires the k
+ * experts, issues each hint's ids as prefetch hints, points the routed
+ * entries of d->experts (a writable device table of 3*E pointers) at the
+ * slots, makes `stream` wait for loads still in flight, runs the block
+ * (h += MoE(h), as tlm_hip_moe_layer) and releases.  ids_host / w_host (may
+ * be NULL) receive the routing.  On an error h is unchanged and every
+ * reference is released.  A hint: layer `layer`'s block descriptor with
+ * k = the number of experts to hint (lookahead_k, <= 32), and a workspace of
+ * its own; at most 7 hints. */
+typedef struct {
+    const tlm_hip_moe_desc *desc;
+    int32_t                 layer;
+    void                   *workspace;
+} tlm_hip_moe_hint;
+int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int layer, float *h,
+                            int32_t *ids_host, float *w_host, const tlm_hip_moe_hint *hints, int n_hints,
+                            void *workspace, void *stream);
 
 /* ---- reference tier ABI --------------------------------------------------
  * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a

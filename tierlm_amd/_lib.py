@@ -64,6 +64,11 @@ class StoreStats(C.Structure):
                 ("in_use", C.c_int32)]
 
 
+class MoeHint(C.Structure):
+    """tlm_hip_moe_hint"""
+    _fields_ = [("desc", C.POINTER(MoeDesc)), ("layer", C.c_int32), ("workspace", vp)]
+
+
 QDOT = C.CFUNCTYPE(C.c_float, vp, vp, C.c_int64, vp)
 QMV = C.CFUNCTYPE(None, vp, C.c_size_t, vp, vp, C.c_int64, C.c_int64)
 
@@ -112,6 +117,8 @@ _SIGS = {
     "tlm_hip_store_tick": (None, [vp]),
     "tlm_hip_store_drain": (i32, [vp]),
     "tlm_hip_store_get_stats": (None, [vp, C.POINTER(StoreStats)]),
+    "tlm_hip_moe_route": (i32, [C.POINTER(MoeDesc), vp, vp, vp, vp, vp]),
+    "tlm_hip_moe_layer_store": (i32, [C.POINTER(MoeDesc), vp, i32, vp, vp, vp, C.POINTER(MoeHint), i32, vp, vp]),
 }
 
 for _name, (_res, _args) in _SIGS.items():

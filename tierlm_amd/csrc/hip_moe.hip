@@ -929,6 +929,25 @@ __global__ __launch_bounds__(256) void k_pf_route(tlm_hip_moe_desc d, WsLayout L
     }
 }
 
+/* Routing alone for one token (route(), src/lib/tlm_model.c:798-839) from the
+ * logits the router launch left in the workspace: ids / w into the
+ * workspace's route area (where the gate/up launch puts the same values) and,
+ * when given, to ids_out / w_out. */
+__global__ __launch_bounds__(256) void k_moe_route(tlm_hip_moe_desc d, WsLayout L, uint8_t *ws, int32_t *ids_out,
+                                                   float *w_out) {
+    __shared__ RouteLds s_route;
+    args_now(d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, L.logits, L.route, ws, ids_out, w_out);
+    LAS RouteLds *R = (LAS RouteLds *)&s_route;
+    route_group(d, (const GAS float *)(ws + L.logits), R, []() {});
+    if ((int)threadIdx.x < d.k) {
+        const int q = threadIdx.x;
+        ws_ids(ws, L)[q] = R->ids[q];
+        ws_w(ws, L)[q] = R->w[q];
+        if (ids_out) ids_out[q] = R->ids[q];
+        if (w_out) w_out[q] = R->w[q];
+    }
+}
+
 /* One group: slots grouped by expert (order within an expert is free - every
  * slot is computed on its own), and the tile table of 32-slot runs. */
 __global__ __launch_bounds__(256) void k_pf_bucket(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
@@ -1112,6 +1131,8 @@ int launch_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w
     return launch_moe_phase(d, 0, h, ids, w, ws, s);
 }
 
+size_t moe_route_offset(const tlm_hip_moe_desc *d) { return ws_layout(*d).route; }
+
 static size_t x_area(int kind, int nb) { return (stage_bytes(kind, nb) + 15) & ~(size_t)15; }
 
 /* descriptor checks shared by the decode and prefill launches */
@@ -1178,6 +1199,14 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8);
     if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(256), lds3, s, dv, L, h, w8);
     return tlmh_check(hipGetLastError(), "moe_layer launch");
+}
+
+/* The router launch, then routing alone: ids / w (k each) in the workspace's
+ * route area (moe_route_offset: ids int32 at +0, w f32 at +128). */
+int launch_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, float *w, void *ws, hipStream_t s) {
+    if (int rc = launch_moe_phase(d, 1, (float *)h, nullptr, nullptr, ws, s)) return rc;
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, s, *d, ws_layout(*d), (uint8_t *)ws, ids, w);
+    return tlmh_check(hipGetLastError(), "moe_route launch");
 }
 
 size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T) {

@@ -50,6 +50,9 @@ constexpr int HINT_BACKLOG = 4;      /* tlm_store.c:42 */
 constexpr int HINT_INFLIGHT = 16;    /* tlm_store.c:43 */
 constexpr int NSTAGE = 3;            /* staging buffers: fill, DMA and pack overlap */
 constexpr size_t MAT_ALIGN = 256;
+constexpr int MAX_HINTS = 7;         /* lookahead layers per tlm_hip_moe_layer_store call */
+constexpr int ROUTE_BYTES = 256;     /* ids int32[32] at +0, w f32[32] at +128 (moe_route_offset) */
+constexpr int MOE_MAXK = 32;
 
 struct Expert {
     tlm_hip_expert_src src;
@@ -107,6 +110,7 @@ struct tlm_hip_store {
     uint64_t clock = 0, ticks = 0;
     int loading = 0, demand_loading = 0, hint_loading = 0, n_pinned = 0;
     tlm_hip_store_stats st{};
+    uint8_t *route_host = nullptr;      /* pinned: routing results of tlm_hip_moe_layer_store */
 
     int find(int layer, int id) const {
         if (layer < 0 || id < 0) return -1;
@@ -346,6 +350,7 @@ struct tlm_hip_store {
             if (stage_dev[i]) (void)hipFree(stage_dev[i]);
         }
         if (arena) (void)hipFree(arena);
+        if (route_host) (void)hipHostFree(route_host);
         if (side) (void)hipStreamDestroy(side);
     }
 };
@@ -461,6 +466,8 @@ int tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store
             if (!rc) rc = tlmh_check(hipMalloc((void **)&s->stage_dev[i], s->stage_bytes), "store: device staging");
             if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->stage_free[i], hipEventDisableTiming), "store: event");
         }
+        if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->route_host, ROUTE_BYTES * (1 + MAX_HINTS),
+                                               hipHostMallocDefault), "store: routing scratch");
         if (!rc) s->loader = std::thread([s] { s->loader_main(); });
     }
     if (rc) {
@@ -715,6 +722,96 @@ void tlm_hip_store_get_stats(tlm_hip_store *s, tlm_hip_store_stats *out) {
     out->slots = s->n_slots;
     out->pinned = s->n_pinned;
     for (const Slot &sl : s->sl) out->in_use += sl.refs > 0;
+}
+
+
+}  // extern "C"
+
+/* ---- one MoE block through the cache -------------------------------------- */
+namespace {
+
+constexpr int TS_MAX = 3 * MOE_MAXK;
+
+struct TableSet {
+    int32_t n;
+    int32_t idx[TS_MAX];
+    const void *ptr[TS_MAX];
+};
+
+/* table[idx[i]] = ptr[i]: the routed experts' gate / up / down entries */
+__global__ __launch_bounds__(128) void k_table_set(const void **table, TableSet t) {
+    const int i = threadIdx.x;
+    if (i < t.n) table[t.idx[i]] = t.ptr[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+/* moe() with the store, src/lib/tlm_model.c:960-1055: route, acquire the
+ * routed experts, issue the lookahead hints (:988-991, lookahead() :844-877),
+ * run the block once every expert's load has landed, release. */
+int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int layer, float *h, int32_t *ids_host,
+                            float *w_host, const tlm_hip_moe_hint *hints, int n_hints, void *workspace,
+                            void *stream) {
+    if (!d || !s || !h || !workspace || n_hints < 0 || n_hints > MAX_HINTS || (n_hints > 0 && !hints))
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: bad arguments");
+    if (d->k <= 0 || d->k > MOE_MAXK) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: k=%d", d->k);
+    for (int i = 0; i < n_hints; i++)
+        if (!hints[i].desc || !hints[i].workspace || hints[i].workspace == workspace)
+            return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: hint %d needs its own descriptor and workspace", i);
+    hipStream_t st = (hipStream_t)stream;
+    /* every route first (the hints read the same residual, before this
+     * block's update), then one round trip for all of them */
+    int rc = launch_moe_route(d, h, nullptr, nullptr, workspace, st);
+    if (rc) return rc;
+    HIPCHK(hipMemcpyAsync(s->route_host, (uint8_t *)workspace + moe_route_offset(d), ROUTE_BYTES,
+                          hipMemcpyDeviceToHost, st));
+    for (int i = 0; i < n_hints; i++) {
+        if ((rc = launch_moe_route(hints[i].desc, h, nullptr, nullptr, hints[i].workspace, st))) return rc;
+        HIPCHK(hipMemcpyAsync(s->route_host + ROUTE_BYTES * (1 + i),
+                              (uint8_t *)hints[i].workspace + moe_route_offset(hints[i].desc), ROUTE_BYTES,
+                              hipMemcpyDeviceToHost, st));
+    }
+    HIPCHK(hipStreamSynchronize(st));
+    const int k = d->k;
+    int ids[MOE_MAXK];
+    float w[MOE_MAXK];
+    memcpy(ids, s->route_host, sizeof(int) * k);
+    memcpy(w, s->route_host + 128, sizeof(float) * k);
+    if (ids_host) memcpy(ids_host, ids, sizeof(int) * k);
+    if (w_host) memcpy(w_host, w, sizeof(float) * k);
+    for (int r = 0; r < k; r++)   /* the table write below indexes 3 * id + m */
+        if (ids[r] < 0 || ids[r] >= d->E)
+            return tlmh_seterr(TLM_HIP_EIO, "moe_layer_store: routing produced expert %d of %d", ids[r], d->E);
+
+    tlm_hip_expert_ref refs[MOE_MAXK];
+    auto release_all = [&] {
+        for (int r = 0; r < k; r++) tlm_hip_store_release(s, &refs[r], stream);
+    };
+    rc = tlm_hip_store_acquire(s, layer, ids, k, refs);
+    if (rc) {
+        release_all();
+        return rc;
+    }
+    /* hints only now that this block's experts hold references (:988-990) */
+    for (int i = 0; i < n_hints; i++)
+        tlm_hip_store_prefetch(s, hints[i].layer, (const int *)(s->route_host + ROUTE_BYTES * (1 + i)),
+                               hints[i].desc->k);
+    TableSet t{};
+    for (int r = 0; r < k; r++)
+        for (int m = 0; m < 3; m++) {
+            t.idx[t.n] = 3 * ids[r] + m;
+            t.ptr[t.n] = refs[r].mats[m];
+            t.n++;
+        }
+    hipLaunchKernelGGL(k_table_set, dim3(1), dim3(128), 0, st, (const void **)d->experts, t);
+    rc = tlmh_check(hipGetLastError(), "moe_layer_store: table");
+    for (int r = 0; r < k && !rc; r++) rc = tlm_hip_store_stream_wait(s, &refs[r], stream);
+    if (!rc) rc = launch_moe_phase(d, 2, h, nullptr, nullptr, workspace, st);
+    if (!rc) rc = launch_moe_phase(d, 3, h, nullptr, nullptr, workspace, st);
+    release_all();
+    return rc;
 }
 
 }  // extern "C"

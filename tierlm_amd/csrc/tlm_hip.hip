@@ -152,6 +152,11 @@ int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *
     return launch_moe_layer(d, h, ids, w, workspace, (hipStream_t)stream);
 }
 
+int tlm_hip_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, float *w, void *workspace,
+                      void *stream) {
+    return launch_moe_route(d, h, ids, w, workspace, (hipStream_t)stream);
+}
+
 int tlm_hip_moe_layer_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *workspace,
                             void *stream) {
     if (phase < 1 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_phase: phase %d not in 1..3", phase);

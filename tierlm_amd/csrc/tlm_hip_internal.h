@@ -154,5 +154,7 @@ size_t moe_workspace_bytes(const tlm_hip_moe_desc *d);
 int launch_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w, void *ws, hipStream_t s);
 int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
                      hipStream_t s);
+int launch_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, float *w, void *ws, hipStream_t s);
+size_t moe_route_offset(const tlm_hip_moe_desc *d);
 
 #endif

@@ -10,7 +10,7 @@ import ctypes as C
 
 import torch
 
-from ._lib import MoeDesc, check, lib
+from ._lib import MoeDesc, MoeHint, check, lib
 from .quant import stream
 
 
@@ -63,6 +63,42 @@ class MoeBlock:
         check(lib.tlm_hip_moe_prefill(C.byref(self.desc), C.c_void_p(h.data_ptr()), T, p(ids), p(w),
                                       C.c_void_p(ws.data_ptr()), stream()))
         return h
+
+    def route(self, h, ids=None, w=None):
+        """Routing alone (device ids / w of k entries), as __call__ routes h."""
+        ids = self.ids if ids is None else ids
+        w = self.w if w is None else w
+        check(lib.tlm_hip_moe_route(C.byref(self.desc), C.c_void_p(h.data_ptr()), C.c_void_p(ids.data_ptr()),
+                                    C.c_void_p(w.data_ptr()), C.c_void_p(self.workspace.data_ptr()), stream()))
+        return ids, w
+
+    def step_store(self, store, layer, h, hints=()):
+        """h += MoE(h) with the experts taken from ``store`` (a HipStore over
+        this block's geometry): the block's expert table is rewritten for the
+        routed experts.  hints: (block, layer, k) lookahead tuples - the
+        block's router predicts k experts of that layer.  Returns the routing
+        (ids, w) as host lists."""
+        n = len(hints)
+        arr = (MoeHint * max(n, 1))()
+        self._hint_keep = []
+        for i, (blk, hl, hk) in enumerate(hints):
+            dsc = MoeDesc.from_buffer_copy(blk.desc)
+            dsc.k = hk
+            ws = blk._hint_ws(dsc)
+            self._hint_keep.append((dsc, ws))
+            arr[i] = MoeHint(C.pointer(dsc), hl, C.c_void_p(ws.data_ptr()))
+        ids = (C.c_int32 * self.desc.k)()
+        w = (C.c_float * self.desc.k)()
+        check(lib.tlm_hip_moe_layer_store(C.byref(self.desc), store.h, layer, C.c_void_p(h.data_ptr()), ids, w, arr,
+                                          n, C.c_void_p(self.workspace.data_ptr()), stream()))
+        return list(ids), list(w)
+
+    def _hint_ws(self, dsc):
+        """the workspace this block's router uses when it predicts for a hint"""
+        nbytes = int(lib.tlm_hip_moe_workspace_bytes(C.byref(dsc)))
+        if getattr(self, "_hws", None) is None or self._hws.numel() < nbytes:
+            self._hws = torch.empty(nbytes, dtype=torch.uint8, device=self.workspace.device)
+        return self._hws
 
     def set_expert_ptrs(self, expert_ptrs):
         """Point the block at another set of packed experts (same geometry)."""
