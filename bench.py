@@ -106,6 +106,102 @@ def prefill_bench(torch, dev, W, router_w, ffn_norm, gen):
                         "tokens routed by the seeded f32 router and bucketed per expert"}
 
 
+def host_payloads(torch, n_experts, seed):
+    """n_experts Q6_K expert payloads in the reference's packet layout (gate |
+    up | down rows of 1680 / 1680 / 630 bytes, random codes, finite f16 block
+    scales) in one page-locked host buffer; returns (buffer, payload bytes)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    plen = EXPERT_BYTES
+    buf = torch.empty(n_experts * plen, dtype=torch.uint8, pin_memory=True)
+    nbl = plen // 210
+    for e in range(n_experts):
+        blocks = rng.integers(0, 256, size=(nbl, 210), dtype=np.uint8)
+        blocks[:, 208:210] = (rng.standard_normal((nbl, 1)) * 2e-3).astype(np.float16).view(np.uint8)
+        buf[e * plen:(e + 1) * plen].copy_(torch.from_numpy(blocks.reshape(-1)))
+    return buf, plen
+
+
+def slot_cache_bench(torch, dev, router_w, ffn_norm, gen, tokens):
+    """The expert slot cache in HBM (tlm_hip_store_*): (1) fill rate - all 128
+    experts of the block loaded into empty slots (pinned host payloads ->
+    DMA -> pack), against one plain pinned host-to-device copy of the same
+    bytes; (2) decode through the cache (tlm_hip_moe_layer_store) with every
+    expert resident, and with half of them (64 slots: misses stream over
+    PCIe)."""
+    from tierlm_amd import MoeBlock
+    from tierlm_amd.store import HipStore
+    buf, plen = host_payloads(torch, E, seed=7)
+    off = [0, MAT_BYTES, 2 * MAT_BYTES]
+    srcs = [{"layer": 0, "id": e, "dtype": Q6_K, "item_off": off, "payload": buf[e * plen:(e + 1) * plen]}
+            for e in range(E)]
+    out = {"payload_bytes": plen, "experts": E}
+
+    dst = torch.empty(E * plen, dtype=torch.uint8, device=dev)
+    best = None
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dst.copy_(buf, non_blocking=True)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    out["h2d_copy_GBps"] = round(E * plen / best / 1e9, 2)
+    del dst
+
+    def make_store(slots):
+        return HipStore(srcs, d_model=D, d_expert=DE, top_k=K, budget_bytes=slots * (EXPERT_BYTES + 768),
+                        prefetch=0)
+
+    best = None
+    for _ in range(3):
+        st = make_store(E)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for b in range(E // K):
+            rc, g = st.acquire(0, list(range(b * K, (b + 1) * K)))
+            assert rc == 0
+            for j in range(K):
+                st.release(g, j)
+        st.settle()
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+        assert st.stats()["misses"] == E
+        st.close()
+    out["fill_GBps"] = round(E * plen / best / 1e9, 2)
+    out["fill_us_per_expert"] = round(best / E * 1e6, 1)
+
+    dummy = torch.zeros(EXPERT_BYTES, dtype=torch.uint8, device=dev)
+    blk = MoeBlock(D=D, de=DE, E=E, k=K, expert_dt=Q6_K, ffn_norm=ffn_norm, router_w=router_w,
+                   expert_ptrs=[dummy.data_ptr()] * (3 * E), router=0, eps=1e-6, device=dev)
+    for slots, name in ((E, "resident"), (E // 2, "half")):
+        st = make_store(slots)
+        H = torch.randn((tokens + 20, D), generator=gen, device=dev)
+        for t in range(20):                      # warm: fill what fits
+            blk.step_store(st, 0, H[t].clone())
+            st.tick()
+        s0 = st.stats()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(20, 20 + tokens):
+            blk.step_store(st, 0, H[t])
+            st.tick()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        s1 = st.stats()
+        miss = (s1["misses"] - s0["misses"]) / tokens
+        out[name] = {"slots": st.n_slots(), "tok_s": round(tokens / dt, 1), "us_per_token": round(dt / tokens * 1e6, 1),
+                     "misses_per_token": round(miss, 2),
+                     "miss_GBps": round(miss * plen * tokens / dt / 1e9, 2)}
+        st.close()
+        log(f"bench: slot cache {name} ({out[name]['slots']} slots): {out[name]['tok_s']:.0f} tok/s, "
+            f"{miss:.2f} misses/token")
+    log(f"bench: slot fill {out['fill_GBps']} GB/s ({out['fill_us_per_expert']} us/expert), "
+        f"plain pinned H2D copy {out['h2d_copy_GBps']} GB/s")
+    out["timing"] = "host wall clock around the calls, synchronised (the cache path reads routing back per token)"
+    return out
+
+
 def cpu_baseline(args, threads):
     """Reference kernels on the host (oracle/_ref), bounded sample."""
     import numpy as np
@@ -152,6 +248,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill measurement")
+    ap.add_argument("--no-store", action="store_true", help="skip the expert slot cache measurement")
+    ap.add_argument("--store-tokens", type=int, default=400, help="tokens per slot-cache decode measurement")
     ap.add_argument("--copy-check-mib", type=int, default=0,
                     help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
                          "of known size, the scale for HBM byte counters")
@@ -301,6 +399,7 @@ def main():
         del src, dst
 
     prefill = None if args.no_prefill else prefill_bench(torch, dev, W, router_w, ffn_norm, gen)
+    slot_cache = None if args.no_store else slot_cache_bench(torch, dev, router_w, ffn_norm, gen, args.store_tokens)
 
     cpu = None
     if not args.no_cpu:
@@ -334,6 +433,7 @@ def main():
                      "stream_read_kernel": "k_mv_packed<Q6_K> over ~2 GB of resident expert bytes, one launch (best of 5)"},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "slot_cache": slot_cache,
     }
     print(json.dumps(line), flush=True)
 

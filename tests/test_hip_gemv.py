@@ -265,3 +265,33 @@ def test_mv_job_segments(hip, dev):
     torch.cuda.synchronize()
     for s, want in zip(segs, wants):
         assert np.all(same(s["y"].cpu().numpy(), want))
+
+
+def pack_layout_host(dt, W, rows, n):
+    """The packed tile layout written out in numpy: unit u = (t*nb + b)*16 + i
+    holds row t*16 + i, block b (Q6_K bytes 0..207, Q8_0 codes, other formats
+    the whole block), rows past the matrix as zeros; Q6_K / Q8_0 then carry an
+    f16 d plane of 2 bytes per unit."""
+    bv, bb = oracle.BLOCK[dt]
+    nb = n // bv
+    T = (rows + 15) // 16
+    blocks = np.zeros((T * 16, nb, bb), np.uint8)
+    blocks[:rows] = W.reshape(rows, nb, bb)
+    units = blocks.reshape(T, 16, nb, bb).transpose(0, 2, 1, 3).reshape(-1, bb)
+    if dt == oracle.Q6_K:
+        return np.concatenate([units[:, :208].reshape(-1), units[:, 208:210].reshape(-1)])
+    if dt == oracle.Q8_0:
+        return np.concatenate([units[:, 2:34].reshape(-1), units[:, 0:2].reshape(-1)])
+    return units.reshape(-1)
+
+
+@pytest.mark.parametrize("dt", [oracle.Q8_0, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K, oracle.Q8_K])
+@pytest.mark.parametrize("rows,n,offset", [(16, 256, 0), (37, 512, 1), (130, 768, 6), (1, 256, 3)])
+def test_pack_layout(hip, dev, dt, rows, n, offset):
+    rng = np.random.default_rng(rows * 7 + dt)
+    W = rng.integers(0, 256, size=(rows, oracle.row_bytes(dt, n)), dtype=np.uint8)
+    raw = np.concatenate([np.full(offset, 0xEE, np.uint8), W.reshape(-1)])
+    Wd = torch.from_numpy(raw).to(dev)
+    out = hip.pack(dt, Wd[offset:], W.shape[1], rows, n).cpu().numpy()
+    want = pack_layout_host(dt, W, rows, n)
+    assert np.array_equal(out[:want.size], want)

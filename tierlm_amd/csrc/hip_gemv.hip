@@ -173,33 +173,79 @@ __global__ void k_nan_fill(float *y, int64_t count) {
  *   F32: plain rows of n floats
  * Rows past `rows` in the last tile are zero.
  * ==================================================================== */
-__global__ void k_pack(int dt, const uint8_t *__restrict__ src, size_t row_bytes, int64_t rows, int nb,
-                       int64_t T, uint8_t *__restrict__ dst) {
-    int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   /* one thread per unit */
-    int64_t units = T * nb * TILE_ROWS;
-    if (u >= units) return;
-    int i = (int)(u % TILE_ROWS);
-    int64_t tb = u / TILE_ROWS;
-    int b = (int)(tb % nb);
-    int64_t t = tb / nb;
-    int64_t r = t * TILE_ROWS + i;
+/* One work-group per (16-row tile, chunk of cb block columns).  The tile's
+ * source - 16 row pieces of cb * block_bytes contiguous bytes - is loaded into
+ * LDS with aligned dword loads (the dwords holding the piece: never outside
+ * the piece's pages), so the reads stream whether src is device memory or
+ * page-locked host memory read over PCIe; then the chunk's units (contiguous
+ * in the packed layout) and d values are written with coalesced dword stores.
+ * Unit u = (t*nb + b)*16 + i holds row t*16 + i, block b: Q6_K bytes 0..207,
+ * Q8_0 codes 2..33, other formats the whole block; Q6_K and Q8_0 keep their
+ * f16 d in a plane after the units.  Rows past the matrix pack as zeros. */
+__global__ __launch_bounds__(256) void k_pack(int dt, const uint8_t *__restrict__ src, size_t row_bytes, int64_t rows,
+                                             int nb, int cb, int rstride, uint8_t *__restrict__ dst) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int64_t t = blockIdx.x, T = gridDim.x;
+    const int b0 = (int)blockIdx.y * cb;
+    const int ncb = nb - b0 < cb ? nb - b0 : cb;
     const int bb = dt_block_bytes(dt);
-    const uint8_t *s = r < rows ? src + (size_t)r * row_bytes + (size_t)b * bb : nullptr;
-    if (dt == DT_Q6_K) {
-        uint8_t *o = dst + u * 208;
-        for (int k = 0; k < 208; k++) o[k] = s ? s[k] : 0;
-        uint8_t *od = dst + units * 208 + u * 2;
-        od[0] = s ? s[208] : 0;
-        od[1] = s ? s[209] : 0;
-    } else if (dt == DT_Q8_0) {
-        uint8_t *o = dst + u * 32;
-        for (int k = 0; k < 32; k++) o[k] = s ? s[2 + k] : 0;
-        uint8_t *od = dst + units * 32 + u * 2;
-        od[0] = s ? s[0] : 0;
-        od[1] = s ? s[1] : 0;
-    } else {
-        uint8_t *o = dst + u * bb;
-        for (int k = 0; k < bb; k++) o[k] = s ? s[k] : 0;
+    const int U = dt == DT_Q6_K ? 208 : dt == DT_Q8_0 ? 32 : bb;   /* unit bytes, a multiple of 4 */
+    const int skip = dt == DT_Q8_0 ? 2 : 0;                          /* f16 d leads a Q8_0 block */
+    const int dpos = dt == DT_Q6_K ? 208 : 0;                        /* where d sits in the block */
+    const bool plane = dt == DT_Q6_K || dt == DT_Q8_0;
+    const int piece = ncb * bb, dmax = (piece + 6) / 4 + 1;
+    const int tid = threadIdx.x;
+    auto head_of = [&](int i) -> int {
+        return (int)(((uintptr_t)src + (size_t)(t * TILE_ROWS + i) * row_bytes + (size_t)b0 * bb) & 3u);
+    };
+    /* eight loads in flight per thread before any is stored: over PCIe each
+     * is a round trip of microseconds */
+    constexpr int BATCH = 8;
+    for (int base = tid; base < TILE_ROWS * dmax; base += 256 * BATCH) {
+        uint32_t v[BATCH];
+        int at[BATCH];
+#pragma unroll
+        for (int q = 0; q < BATCH; q++) {
+            const int idx = base + 256 * q;
+            at[q] = -1;
+            const int i = idx / dmax, w = idx - i * dmax;
+            const int64_t r = t * TILE_ROWS + i;
+            if (idx < TILE_ROWS * dmax && r < rows) {
+                const uint8_t *p = src + (size_t)r * row_bytes + (size_t)b0 * bb;
+                const int head = (int)((uintptr_t)p & 3u);
+                if (4 * w < head + piece) {
+                    v[q] = *(const uint32_t *)(p - head + 4 * w);
+                    at[q] = i * rstride + 4 * w;
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < BATCH; q++)
+            if (at[q] >= 0) *(uint32_t *)(lds + at[q]) = v[q];
+    }
+    __syncthreads();
+    const int64_t units = T * nb * TILE_ROWS, u0 = (t * nb + b0) * TILE_ROWS;
+    const int n1 = ncb * TILE_ROWS * (U / 4), n2 = plane ? ncb * TILE_ROWS / 2 : 0;
+    for (int o = tid; o < n1 + n2; o += 256) {
+        if (o < n1) {
+            const int lu = o / (U / 4), k = (o - lu * (U / 4)) * 4;
+            const int i = lu % TILE_ROWS, bl = lu / TILE_ROWS;
+            uint32_t v = 0;
+            if (t * TILE_ROWS + i < rows) {
+                const uint8_t *q = lds + i * rstride + head_of(i) + bl * bb + skip + k;
+                v = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
+            }
+            *(uint32_t *)(dst + (u0 + lu) * U + k) = v;
+        } else {
+            const int lu = 2 * (o - n1), i = lu % TILE_ROWS, bl = lu / TILE_ROWS;
+            uint32_t v = 0;
+            for (int h = 0; h < 2; h++)
+                if (t * TILE_ROWS + i + h < rows) {
+                    const uint8_t *q = lds + (i + h) * rstride + head_of(i + h) + bl * bb + dpos;
+                    v |= ((uint32_t)q[0] | ((uint32_t)q[1] << 8)) << (16 * h);
+                }
+            *(uint32_t *)(dst + units * U + 2 * (u0 + lu)) = v;
+        }
     }
 }
 
@@ -334,10 +380,14 @@ int launch_pack(int dt, const void *src, size_t row_bytes, int64_t rows, int64_t
         hipLaunchKernelGGL(k_pack_f32, dim3((unsigned)((e + 255) / 256)), dim3(256), 0, s, (const uint8_t *)src,
                            row_bytes, rows, n, (float *)dst);
     } else {
-        int nb = (int)(n / dt_block_values(dt));
-        int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS, units = T * nb * TILE_ROWS;
-        hipLaunchKernelGGL(k_pack, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, dt, (const uint8_t *)src,
-                           row_bytes, rows, nb, T, (uint8_t *)dst);
+        const int nb = (int)(n / dt_block_values(dt)), bb = dt_block_bytes(dt);
+        const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS;
+        const int cb = 2040 / bb < nb ? 2040 / bb : nb;                 /* <= 2040 source bytes per row piece */
+        const int rstride = (cb * bb + 8 + 3) & ~3;                    /* piece + alignment head + tail */
+        if (T > 0x7FFFFFFF) return tlmh_seterr(TLM_HIP_EINVAL, "pack: %lld rows", (long long)rows);
+        hipLaunchKernelGGL(k_pack, dim3((unsigned)T, (unsigned)((nb + cb - 1) / cb)), dim3(256),
+                           (size_t)TILE_ROWS * rstride, s, dt, (const uint8_t *)src, row_bytes, rows, nb, cb, rstride,
+                           (uint8_t *)dst);
     }
     return tlmh_check(hipGetLastError(), "pack launch");
 }

@@ -10,17 +10,19 @@
  *
  *   - one hipMalloc arena of equal slots; a slot holds an expert's gate, up
  *     and down in the packed tile layout the MoE kernels read;
- *   - a load is host payload -> pinned staging (a loader thread copies, or
- *     calls the fetch callback; a payload already in pinned memory is DMA'd
- *     straight from where it lies) -> one DMA into a device staging buffer
- *     on the store's side stream -> three pack kernels into the slot -> an
- *     event per slot.  The caller's compute stream never blocks on a copy;
+ *   - a load is three pack kernels on the store's own stream that read the
+ *     payload over PCIe straight from page-locked host memory - where it
+ *     lies, or a staging buffer the loader thread first copies a pageable
+ *     payload into (or the fetch callback fills) - and write the slot; then
+ *     an event per slot.  The caller's stream never blocks on a load;
  *   - READY is published when the host sees the slot's event complete;
  *     tlm_hip_store_stream_wait lets a stream wait for a LOADING slot on the
  *     device instead;
- *   - release records an event on the caller's stream; the next load into
- *     that slot waits for it on the side stream, so a slot is never
- *     overwritten while kernels enqueued before the release still read it.
+ *   - release only notes the caller's stream; the first load that evicts a
+ *     released slot records one event on that stream (shared by every such
+ *     load until the next release) and the slot's packs wait for it, so a
+ *     slot is never overwritten while kernels enqueued before its release
+ *     still read it, and all-hit steps make no runtime calls for it.
  *
  * Threading: one mutex guards the policy state; the loader thread takes it
  * only to pick up jobs and to publish a submitted load. */
@@ -48,7 +50,8 @@ enum { K_DEMAND = 0, K_HINT = 1, K_PIN = 2 };
 constexpr int DECAY_TICKS = 16;      /* tlm_store.c:41 */
 constexpr int HINT_BACKLOG = 4;      /* tlm_store.c:42 */
 constexpr int HINT_INFLIGHT = 16;    /* tlm_store.c:43 */
-constexpr int NSTAGE = 3;            /* staging buffers: fill, DMA and pack overlap */
+constexpr int NSTAGE = 3;            /* staging buffers for pageable payloads */
+constexpr int NLOAD = 2;             /* load streams: consecutive loads overlap */
 constexpr size_t MAT_ALIGN = 256;
 constexpr int MAX_HINTS = 7;         /* lookahead layers per tlm_hip_moe_layer_store call */
 constexpr int ROUTE_BYTES = 256;     /* ids int32[32] at +0, w f32[32] at +128 (moe_route_offset) */
@@ -58,7 +61,8 @@ struct Expert {
     tlm_hip_expert_src src;
     size_t off[3];          /* packed gate / up / down inside a slot */
     int64_t rows[3], n[3];
-    bool pinned_src;        /* payload lies in page-locked host memory */
+    const void *dev_src;    /* the payload's device-visible address when it lies in page-locked
+                               host memory, else NULL (copied through staging) */
     uint32_t freq = 0;
     int slot = -1;
 };
@@ -68,13 +72,15 @@ struct Slot {
     uint64_t last = 0;
     uint64_t gen = 0;           /* bumped by every start_load */
     bool submitted = false;     /* `loaded` recorded for generation gen */
-    bool reads_pending = false; /* `released` recorded since the last load took it */
-    hipEvent_t loaded = nullptr, released = nullptr;
+    bool reads_pending = false; /* released since the last load took it: kernels may still read it */
+    hipStream_t rel_stream = nullptr;
+    hipEvent_t loaded = nullptr;
 };
 
 struct Job {
     int v, e;
     uint64_t gen;
+    int rel;                    /* release point the packs wait for, or -1 */
 };
 
 uint64_t key_of(int layer, int id) { return ((uint64_t)(uint32_t)layer << 32) | (uint32_t)id; }
@@ -92,7 +98,8 @@ struct tlm_hip_store {
     std::mutex mu;
     std::condition_variable cv;
     int device = -1;
-    hipStream_t side = nullptr;
+    hipStream_t lstream[NLOAD] = {};     /* load streams, used in turn */
+    int lnext = 0;                       /* loader thread only */
     tlm_hip_store_opts o{};
     std::vector<Expert> ex;
     std::unordered_map<uint64_t, int> index;
@@ -100,8 +107,9 @@ struct tlm_hip_store {
     size_t slot_bytes = 0, stage_bytes = 0;
     uint8_t *arena = nullptr;
     std::vector<Slot> sl;
-    uint8_t *stage_host[NSTAGE] = {}, *stage_dev[NSTAGE] = {};
-    hipEvent_t stage_free[NSTAGE] = {};
+    uint8_t *stage_host[NSTAGE] = {};   /* page-locked staging for pageable payloads */
+    const uint8_t *stage_dev[NSTAGE] = {};  /* their device-visible addresses */
+    hipEvent_t stage_packed[NSTAGE] = {};
     int stage_next = 0;                 /* loader thread only */
     std::deque<Job> jobs;
     int unsubmitted = 0;                /* LOADING slots whose job has not been submitted */
@@ -111,6 +119,14 @@ struct tlm_hip_store {
     int loading = 0, demand_loading = 0, hint_loading = 0, n_pinned = 0;
     tlm_hip_store_stats st{};
     uint8_t *route_host = nullptr;      /* pinned: routing results of tlm_hip_moe_layer_store */
+    /* release points: an event recorded on a release stream when a load first
+     * needs one, shared by every load that needs a point on that stream
+     * before the next release; reused once no queued load waits for it */
+    std::vector<hipEvent_t> rel_ev;
+    std::vector<int> rel_users;
+    int rel_cur = -1;
+    hipStream_t rel_cur_stream = nullptr;
+    uint64_t release_seq = 0, rel_cur_seq = 0;
 
     int find(int layer, int id) const {
         if (layer < 0 || id < 0) return -1;
@@ -164,8 +180,47 @@ struct tlm_hip_store {
         s.gen++;
         s.submitted = false;
         unsubmitted++;
-        jobs.push_back(Job{v, e, s.gen});
+        int rel = -1;
+        if (s.reads_pending) {
+            rel = release_point(s.rel_stream);
+            s.reads_pending = false;
+        }
+        jobs.push_back(Job{v, e, s.gen, rel});
         cv.notify_all();
+    }
+
+    /* An event on `stream` after every release so far (the slot's readers
+     * were all enqueued before it).  Recording it here, at the first load
+     * that needs it, rather than at each release keeps all-hit steps free of
+     * runtime calls.  -1 if no event could be recorded: then the stream is
+     * drained on the host instead. */
+    int release_point(hipStream_t stream) {
+        if (rel_cur >= 0 && rel_cur_stream == stream && rel_cur_seq == release_seq) {
+            rel_users[rel_cur]++;
+            return rel_cur;
+        }
+        int idx = -1;
+        for (int i = 0; i < (int)rel_ev.size() && idx < 0; i++)
+            if (rel_users[i] == 0) idx = i;
+        if (idx < 0) {
+            hipEvent_t ev;
+            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+                (void)hipStreamSynchronize(stream);
+                return -1;
+            }
+            rel_ev.push_back(ev);
+            rel_users.push_back(0);
+            idx = (int)rel_ev.size() - 1;
+        }
+        if (hipEventRecord(rel_ev[idx], stream) != hipSuccess) {
+            (void)hipStreamSynchronize(stream);
+            return -1;
+        }
+        rel_cur = idx;
+        rel_cur_stream = stream;
+        rel_cur_seq = release_seq;
+        rel_users[idx] = 1;
+        return idx;
     }
 
     void complete(int v) {                      /* the publish step, tlm_store.c:273-282 */
@@ -238,42 +293,52 @@ struct tlm_hip_store {
     }
 
     /* ---- the loader thread ------------------------------------------------ */
+    /* The pack kernels read the payload straight from page-locked host
+     * memory over PCIe (the caller's, or the staging buffer a pageable
+     * payload is first copied into) and write the slot: one pass, no DMA
+     * engine, no cross-stream dependency. */
     int run_job(const Job &j) {
         const Expert &x = ex[j.e];
-        const int i = stage_next;
-        stage_next = (stage_next + 1) % NSTAGE;
-        int rc = tlmh_check(hipEventSynchronize(stage_free[i]), "store: staging buffer");
-        if (rc) return rc;
-        const void *src = x.src.payload;
-        const uint64_t len = x.src.payload_len;
-        if (!x.pinned_src) {
-            if (src) {
-                memcpy(stage_host[i], src, len);
-            } else {
-                rc = o.fetch(o.fetch_user, x.src.layer, (int)x.src.id, stage_host[i], len);
-                if (rc) return rc < 0 ? rc : TLM_HIP_EIO;
-            }
-            src = stage_host[i];
-        }
+        int rc = TLM_HIP_OK;
+        hipStream_t packs = lstream[lnext];
+        lnext = (lnext + 1) % NLOAD;
         {
             std::lock_guard<std::mutex> lk(mu);
-            Slot &s = sl[j.v];
-            if (s.gen != j.gen || s.state != S_LOADING) return TLM_HIP_OK;   /* superseded */
-            if (s.reads_pending) {   /* kernels enqueued before the last release still read the slot */
-                rc = tlmh_check(hipStreamWaitEvent(side, s.released, 0), "store: wait for release");
+            if (j.rel >= 0) {   /* kernels enqueued before the slot's release may still read it */
+                rc = tlmh_check(hipStreamWaitEvent(packs, rel_ev[j.rel], 0), "store: wait for release");
+                rel_users[j.rel]--;
                 if (rc) return rc;
-                s.reads_pending = false;
             }
+            const Slot &s = sl[j.v];
+            if (s.gen != j.gen || s.state != S_LOADING) return TLM_HIP_OK;   /* superseded */
         }
-        rc = tlmh_check(hipMemcpyAsync(stage_dev[i], src, len, hipMemcpyHostToDevice, side), "store: DMA");
+        const uint8_t *src = (const uint8_t *)x.dev_src;
+        int i = -1;
+        if (!src) {
+            i = stage_next;
+            stage_next = (stage_next + 1) % NSTAGE;
+            /* the staging buffer is free once the packs that read it have run */
+            if ((rc = tlmh_check(hipEventSynchronize(stage_packed[i]), "store: staging buffer"))) return rc;
+            if (x.src.payload) {
+                memcpy(stage_host[i], x.src.payload, x.src.payload_len);
+            } else {
+                rc = o.fetch(o.fetch_user, x.src.layer, (int)x.src.id, stage_host[i], x.src.payload_len);
+                if (rc) return rc < 0 ? rc : TLM_HIP_EIO;
+            }
+            src = stage_dev[i];
+        }
         uint8_t *base = arena + (size_t)j.v * slot_bytes;
         const int dt = x.src.dtype;
         for (int m = 0; m < 3 && !rc; m++)
-            rc = launch_pack(dt, stage_dev[i] + x.src.item_off[m], (size_t)(x.n[m] / dt_block_values(dt)) *
-                             (size_t)dt_block_bytes(dt), x.rows[m], x.n[m], base + x.off[m], side);
-        if (!rc) rc = tlmh_check(hipEventRecord(sl[j.v].loaded, side), "store: record load");
-        int rc2 = tlmh_check(hipEventRecord(stage_free[i], side), "store: record staging");
-        return rc ? rc : rc2;
+            rc = launch_pack(dt, src + x.src.item_off[m], (size_t)(x.n[m] / dt_block_values(dt)) *
+                             (size_t)dt_block_bytes(dt), x.rows[m], x.n[m], base + x.off[m], packs);
+        if (!rc) rc = tlmh_check(hipEventRecord(sl[j.v].loaded, packs), "store: record load");
+        if (rc) (void)hipStreamSynchronize(packs);   /* no half-done load may race a later one into the slot */
+        if (i >= 0) {
+            const int rc2 = tlmh_check(hipEventRecord(stage_packed[i], packs), "store: record staging");
+            if (!rc) rc = rc2;
+        }
+        return rc;
     }
 
     void loader_main() {
@@ -339,19 +404,19 @@ struct tlm_hip_store {
             }
             loader.join();
         }
-        if (side) (void)hipStreamSynchronize(side);
-        for (Slot &s : sl) {
+        for (hipStream_t q : lstream)
+            if (q) (void)hipStreamSynchronize(q);
+        for (Slot &s : sl)
             if (s.loaded) (void)hipEventDestroy(s.loaded);
-            if (s.released) (void)hipEventDestroy(s.released);
-        }
+        for (hipEvent_t ev : rel_ev) (void)hipEventDestroy(ev);
         for (int i = 0; i < NSTAGE; i++) {
-            if (stage_free[i]) (void)hipEventDestroy(stage_free[i]);
+            if (stage_packed[i]) (void)hipEventDestroy(stage_packed[i]);
             if (stage_host[i]) (void)hipHostFree(stage_host[i]);
-            if (stage_dev[i]) (void)hipFree(stage_dev[i]);
         }
         if (arena) (void)hipFree(arena);
         if (route_host) (void)hipHostFree(route_host);
-        if (side) (void)hipStreamDestroy(side);
+        for (hipStream_t q : lstream)
+            if (q) (void)hipStreamDestroy(q);
     }
 };
 
@@ -374,14 +439,17 @@ bool pin_before(const PinCand &x, const PinCand &y) {
     return x.id < y.id;
 }
 
-bool host_pinned(const void *p) {
+/* The device-visible address of a host pointer into page-locked memory that
+ * is mapped for the device, else NULL (pageable memory: copied through
+ * staging). */
+const void *device_view(const void *p) {
     hipPointerAttribute_t a;
     hipError_t e = hipPointerGetAttributes(&a, p);
     if (e != hipSuccess) {
         (void)hipGetLastError();   /* an unknown (pageable) pointer is not an error here */
-        return false;
+        return nullptr;
     }
-    return a.type == hipMemoryTypeHost;
+    return a.type == hipMemoryTypeHost ? a.devicePointer : nullptr;
 }
 
 }  // namespace
@@ -436,7 +504,7 @@ int tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store
             delete s;
             return tlmh_seterr(TLM_HIP_EINVAL, "store open: expert %u:%u has no payload and no fetch", x.layer, x.id);
         }
-        e.pinned_src = x.payload && host_pinned(x.payload);
+        e.dev_src = x.payload ? device_view(x.payload) : nullptr;
         s->slot_bytes = std::max(s->slot_bytes, at);
         s->stage_bytes = std::max(s->stage_bytes, (size_t)x.payload_len);
         const uint64_t k = key_of(x.layer, (int)x.id);
@@ -457,14 +525,16 @@ int tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store
         rc = tlmh_check(hipMalloc((void **)&s->arena, ns * s->slot_bytes), "store: slot arena");
         for (size_t v = 0; v < ns && !rc; v++) {
             rc = tlmh_check(hipEventCreateWithFlags(&s->sl[v].loaded, hipEventDisableTiming), "store: event");
-            if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->sl[v].released, hipEventDisableTiming), "store: event");
         }
-        if (!rc) rc = tlmh_check(hipStreamCreateWithFlags(&s->side, hipStreamNonBlocking), "store: side stream");
+        for (int q = 0; q < NLOAD && !rc; q++)
+            rc = tlmh_check(hipStreamCreateWithFlags(&s->lstream[q], hipStreamNonBlocking), "store: load stream");
         for (int i = 0; i < NSTAGE && !rc; i++) {
-            rc = tlmh_check(hipHostMalloc((void **)&s->stage_host[i], s->stage_bytes, hipHostMallocDefault),
+            rc = tlmh_check(hipHostMalloc((void **)&s->stage_host[i], s->stage_bytes, hipHostMallocMapped),
                             "store: pinned staging");
-            if (!rc) rc = tlmh_check(hipMalloc((void **)&s->stage_dev[i], s->stage_bytes), "store: device staging");
-            if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->stage_free[i], hipEventDisableTiming), "store: event");
+            void *dp = nullptr;
+            if (!rc) rc = tlmh_check(hipHostGetDevicePointer(&dp, s->stage_host[i], 0), "store: staging address");
+            s->stage_dev[i] = (const uint8_t *)dp;
+            if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->stage_packed[i], hipEventDisableTiming), "store: event");
         }
         if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->route_host, ROUTE_BYTES * (1 + MAX_HINTS),
                                                hipHostMallocDefault), "store: routing scratch");
@@ -661,7 +731,11 @@ void tlm_hip_store_release(tlm_hip_store *s, tlm_hip_expert_ref *ref, void *stre
     if (ref->slot >= 0 && ref->slot < s->n_slots) {
         std::lock_guard<std::mutex> lk(s->mu);
         Slot &sl = s->sl[ref->slot];
-        if (sl.refs > 0 && hipEventRecord(sl.released, (hipStream_t)stream) == hipSuccess) sl.reads_pending = true;
+        if (sl.refs > 0) {
+            sl.reads_pending = true;
+            sl.rel_stream = (hipStream_t)stream;
+            s->release_seq++;
+        }
         s->drop_ref(ref->slot);
     }
     ref->slot = -1;
@@ -706,7 +780,9 @@ int tlm_hip_store_drain(tlm_hip_store *s) {
     std::unique_lock<std::mutex> lk(s->mu);
     s->drain_jobs(lk);
     lk.unlock();
-    int rc = s->side ? tlmh_check(hipStreamSynchronize(s->side), "store drain") : TLM_HIP_OK;
+    int rc = TLM_HIP_OK;
+    for (hipStream_t q : s->lstream)
+        if (q && !rc) rc = tlmh_check(hipStreamSynchronize(q), "store drain");
     lk.lock();
     s->refresh_all();
     return rc;
