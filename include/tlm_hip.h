@@ -297,6 +297,67 @@ int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int lay
                             int32_t *ids_host, float *w_host, const tlm_hip_moe_hint *hints, int n_hints,
                             void *workspace, void *stream);
 
+/* ---- compiled model stores: manifest + packet files -----------------------
+ * Reader of the reference's store format (src/lib/tlm_packet.h:8-151,
+ * src/lib/tlm_packet.c:8-34): tlm_manifest_load's checks (one valid layout,
+ * header CRC32C, packet-table SHA-256, record ranges, order, no overlapping
+ * extents), tlm_packet_read's header / length / CRC checks with the replica
+ * fallback, and tensor-directory lookup. */
+enum { TLM_HIP_PK_DENSE = 1, TLM_HIP_PK_EXPERT = 2, TLM_HIP_PK_BUNDLE = 3, TLM_HIP_PK_MTP = 4,
+       TLM_HIP_PK_EMBED = 5, TLM_HIP_PK_TABLE = 6, TLM_HIP_PK_META = 7, TLM_HIP_PK_TOKEN = 8 };
+#define TLM_HIP_LAYER_NONE 0xFFFFu
+
+typedef struct {            /* tlm_packet_loc, src/lib/tlm_packet.h:70-81 */
+    uint16_t type, layer;
+    uint32_t id;
+    uint8_t  drive, replica_drive;   /* 0xFF = no replica */
+    uint16_t flags;                  /* bit0 pinned at load, bit1 pruned */
+    uint64_t offset, replica_offset, total_len;
+    uint32_t crc32c;
+    float    heat;
+} tlm_hip_packet_loc;
+
+typedef struct {            /* tlm_model_geom, src/lib/tlm_packet.h:84-95 */
+    char     arch[32];
+    uint32_t n_layers, d_model, n_heads, n_kv_heads, head_dim;
+    uint32_t vocab, n_experts, top_k, d_expert, n_shared, d_shared;
+    uint32_t max_ctx, router;
+    float    rope_theta, norm_eps, routed_scale;
+    uint32_t mtp_layers, rope_scale;
+    float    rope_factor, rope_beta_fast, rope_beta_slow;
+    uint32_t rope_orig_len;
+} tlm_hip_model_geom;
+
+typedef struct {            /* tlm_tensor_ref, src/lib/tlm_packet.h:59-66 */
+    char     name[48];
+    uint32_t dtype, ndim;
+    uint64_t shape[2], offset, nbytes;
+} tlm_hip_tensor_ref;
+
+typedef struct tlm_hip_manifest tlm_hip_manifest;
+/* src/lib/tlm_packet.h:127 (tlm_manifest_load) */
+int  tlm_hip_manifest_load(const char *path, tlm_hip_manifest **out);
+void tlm_hip_manifest_free(tlm_hip_manifest *m);
+const tlm_hip_model_geom *tlm_hip_manifest_geom(const tlm_hip_manifest *m);
+const char *tlm_hip_manifest_name(const tlm_hip_manifest *m);
+int  tlm_hip_manifest_n_packets(const tlm_hip_manifest *m);
+const tlm_hip_packet_loc *tlm_hip_manifest_packet(const tlm_hip_manifest *m, int i);
+/* src/lib/tlm_packet.h:129-130 (tlm_manifest_find): binary search */
+const tlm_hip_packet_loc *tlm_hip_manifest_find(const tlm_hip_manifest *m, int type, int layer, uint32_t id);
+/* src/lib/tlm_packet.h:132: <drive dir>/<name>.tlmp */
+const char *tlm_hip_manifest_drive_path(const tlm_hip_manifest *m, int i);
+/* src/lib/tlm_packet.h:164-165 (tlm_packet_read): buf holds loc->total_len
+ * bytes; the payload is at buf + *payload_off, *payload_len bytes. */
+int  tlm_hip_packet_read(tlm_hip_manifest *m, const tlm_hip_packet_loc *loc, void *buf, uint64_t *payload_off,
+                         uint64_t *payload_len);
+/* dtype and gate / up / down item offsets of a packet header (tlm_packet_hdr) */
+int  tlm_hip_packet_header(const void *buf, uint32_t *dtype, uint32_t item_off[3]);
+/* src/lib/tlm_packet.h:141 (tlm_dir_find): TLM_HIP_ENOTFOUND if absent */
+int  tlm_hip_dir_find(const void *payload, uint64_t len, const char *name, tlm_hip_tensor_ref *out);
+/* the format's checksums: CRC32C (src/lib/tlm_platform.h crc32c), SHA-256 */
+uint32_t tlm_hip_crc32c(uint32_t crc, const void *p, size_t n);
+void     tlm_hip_sha256(const void *p, size_t n, uint8_t out[32]);
+
 /* ---- reference tier ABI --------------------------------------------------
  * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a
  * name and two tables of TLM_QK_COUNT = 10 function pointers indexed F32,

@@ -37,7 +37,8 @@ def test_python_binding_covers_header():
 
 
 def test_struct_layouts_match_c():
-    from tierlm_amd._lib import ExpertRef, ExpertSrc, MoeDesc, QuantKernels, Seg, StoreOpts, StoreStats
+    from tierlm_amd._lib import (ExpertRef, ExpertSrc, ModelGeom, MoeDesc, PacketLoc, QuantKernels, Seg, StoreOpts,
+                                 StoreStats, TensorRef)
     prog = r'''
 #include <stdio.h>
 #include <stddef.h>
@@ -56,6 +57,11 @@ int main(void) {
   O(tlm_hip_store_opts, top_k); O(tlm_hip_store_opts, pin_frac); O(tlm_hip_store_opts, fetch);
   O(tlm_hip_store_opts, fetch_user); O(tlm_hip_expert_ref, mats);
   O(tlm_hip_store_stats, wait_ns); O(tlm_hip_store_stats, slots); O(tlm_hip_store_stats, in_use);
+  printf("loc %zu\ngeom %zu\ntref %zu\n", sizeof(tlm_hip_packet_loc), sizeof(tlm_hip_model_geom),
+         sizeof(tlm_hip_tensor_ref));
+  O(tlm_hip_packet_loc, flags); O(tlm_hip_packet_loc, offset); O(tlm_hip_packet_loc, crc32c); O(tlm_hip_packet_loc, heat);
+  O(tlm_hip_model_geom, router); O(tlm_hip_model_geom, rope_theta); O(tlm_hip_model_geom, rope_orig_len);
+  O(tlm_hip_tensor_ref, dtype); O(tlm_hip_tensor_ref, shape); O(tlm_hip_tensor_ref, nbytes);
   return 0;
 }'''
     with tempfile.TemporaryDirectory() as d:
@@ -69,7 +75,8 @@ int main(void) {
     assert vals["seg"] == C.sizeof(Seg)
     assert vals["moe"] == C.sizeof(MoeDesc)
     assert vals["qk"] == C.sizeof(QuantKernels)
-    for name, cls in (("src", ExpertSrc), ("opts", StoreOpts), ("ref", ExpertRef), ("stats", StoreStats)):
+    for name, cls in (("src", ExpertSrc), ("opts", StoreOpts), ("ref", ExpertRef), ("stats", StoreStats),
+                      ("loc", PacketLoc), ("geom", ModelGeom), ("tref", TensorRef)):
         assert vals[name] == C.sizeof(cls), name
     for k, v in vals.items():
         if "." not in k:
@@ -77,7 +84,8 @@ int main(void) {
         t, f = k.split(".")
         cls = {"tlm_hip_seg": Seg, "tlm_hip_moe_desc": MoeDesc, "tlm_hip_quant_kernels": QuantKernels,
                "tlm_hip_expert_src": ExpertSrc, "tlm_hip_store_opts": StoreOpts, "tlm_hip_expert_ref": ExpertRef,
-               "tlm_hip_store_stats": StoreStats}[t]
+               "tlm_hip_store_stats": StoreStats, "tlm_hip_packet_loc": PacketLoc, "tlm_hip_model_geom": ModelGeom,
+               "tlm_hip_tensor_ref": TensorRef}[t]
         assert getattr(cls, f).offset == v, k
 
 

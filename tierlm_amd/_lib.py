@@ -69,6 +69,30 @@ class MoeHint(C.Structure):
     _fields_ = [("desc", C.POINTER(MoeDesc)), ("layer", C.c_int32), ("workspace", vp)]
 
 
+class PacketLoc(C.Structure):
+    """tlm_hip_packet_loc"""
+    _fields_ = [("type", C.c_uint16), ("layer", C.c_uint16), ("id", C.c_uint32), ("drive", C.c_uint8),
+                ("replica_drive", C.c_uint8), ("flags", C.c_uint16), ("offset", C.c_uint64),
+                ("replica_offset", C.c_uint64), ("total_len", C.c_uint64), ("crc32c", C.c_uint32),
+                ("heat", C.c_float)]
+
+
+class ModelGeom(C.Structure):
+    """tlm_hip_model_geom"""
+    _fields_ = [("arch", C.c_char * 32)] + [(n, C.c_uint32) for n in (
+        "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "vocab", "n_experts", "top_k", "d_expert",
+        "n_shared", "d_shared", "max_ctx", "router")] + [
+        ("rope_theta", C.c_float), ("norm_eps", C.c_float), ("routed_scale", C.c_float),
+        ("mtp_layers", C.c_uint32), ("rope_scale", C.c_uint32), ("rope_factor", C.c_float),
+        ("rope_beta_fast", C.c_float), ("rope_beta_slow", C.c_float), ("rope_orig_len", C.c_uint32)]
+
+
+class TensorRef(C.Structure):
+    """tlm_hip_tensor_ref"""
+    _fields_ = [("name", C.c_char * 48), ("dtype", C.c_uint32), ("ndim", C.c_uint32), ("shape", C.c_uint64 * 2),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64)]
+
+
 QDOT = C.CFUNCTYPE(C.c_float, vp, vp, C.c_int64, vp)
 QMV = C.CFUNCTYPE(None, vp, C.c_size_t, vp, vp, C.c_int64, C.c_int64)
 
@@ -118,6 +142,19 @@ _SIGS = {
     "tlm_hip_store_drain": (i32, [vp]),
     "tlm_hip_store_get_stats": (None, [vp, C.POINTER(StoreStats)]),
     "tlm_hip_moe_route": (i32, [C.POINTER(MoeDesc), vp, vp, vp, vp, vp]),
+    "tlm_hip_manifest_load": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "tlm_hip_manifest_free": (None, [vp]),
+    "tlm_hip_manifest_geom": (C.POINTER(ModelGeom), [vp]),
+    "tlm_hip_manifest_name": (C.c_char_p, [vp]),
+    "tlm_hip_manifest_n_packets": (i32, [vp]),
+    "tlm_hip_manifest_packet": (C.POINTER(PacketLoc), [vp, i32]),
+    "tlm_hip_manifest_find": (C.POINTER(PacketLoc), [vp, i32, i32, C.c_uint32]),
+    "tlm_hip_manifest_drive_path": (C.c_char_p, [vp, i32]),
+    "tlm_hip_packet_read": (i32, [vp, C.POINTER(PacketLoc), vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "tlm_hip_packet_header": (i32, [vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    "tlm_hip_dir_find": (i32, [vp, C.c_uint64, C.c_char_p, C.POINTER(TensorRef)]),
+    "tlm_hip_crc32c": (C.c_uint32, [C.c_uint32, vp, sz]),
+    "tlm_hip_sha256": (None, [vp, sz, vp]),
     "tlm_hip_moe_layer_store": (i32, [C.POINTER(MoeDesc), vp, i32, vp, vp, vp, C.POINTER(MoeHint), i32, vp, vp]),
 }
 
