@@ -358,6 +358,33 @@ int  tlm_hip_dir_find(const void *payload, uint64_t len, const char *name, tlm_h
 uint32_t tlm_hip_crc32c(uint32_t crc, const void *p, size_t n);
 void     tlm_hip_sha256(const void *p, size_t n, uint8_t out[32]);
 
+/* ---- the whole decode step on the device -----------------------------------
+ * tlm_model_open / tlm_model_step / tlm_model_prefill and tierlm bench's
+ * greedy loop (src/lib/tlm_model.h:60-125, src/lib/tlm_model.c:486-600,
+ * 1058-1113, src/bin/tierlm.c:702-729) for a compiled store: the model is
+ * loaded into HBM (every weight packed, every expert resident, an f32 KV cache
+ * of max_ctx positions) and each step runs embedding, attention (rmsnorm,
+ * q/k/v, qk-norm, RoPE / YaRN, KV append, softmax attention, o, residual),
+ * the MoE block, the final norm, lm_head and the greedy argmax on one stream.
+ * Dense-FFN layers, MTP heads and head_dim above 256 are not supported
+ * (TLM_HIP_EUNSUP).  Needs tlm_hip_init. */
+typedef struct tlm_hip_model tlm_hip_model;
+typedef struct {
+    int32_t max_ctx;     /* KV positions; 0 = the store's max_ctx, else 4096 (tlm_kv_new) */
+} tlm_hip_model_opts;
+int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
+void tlm_hip_model_close(tlm_hip_model *M);
+const tlm_hip_model_geom *tlm_hip_model_geom_of(const tlm_hip_model *M);
+int  tlm_hip_model_kv_len(const tlm_hip_model *M);
+int  tlm_hip_model_kv_capacity(const tlm_hip_model *M);
+void tlm_hip_model_reset(tlm_hip_model *M);   /* tlm_kv_reset */
+/* tlm_model_step: logits (host, vocab floats) and next (the greedy token)
+ * may each be NULL. */
+int  tlm_hip_model_step(tlm_hip_model *M, int token, float *logits, int32_t *next);
+/* prefill the prompt, then n_gen greedy tokens into out; between steps the
+ * token stays on the device. */
+int  tlm_hip_model_generate(tlm_hip_model *M, const int32_t *prompt, int n_prompt, int n_gen, int32_t *out);
+
 /* ---- reference tier ABI --------------------------------------------------
  * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a
  * name and two tables of TLM_QK_COUNT = 10 function pointers indexed F32,

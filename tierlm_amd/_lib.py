@@ -153,6 +153,14 @@ _SIGS = {
     "tlm_hip_packet_read": (i32, [vp, C.POINTER(PacketLoc), vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "tlm_hip_packet_header": (i32, [vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     "tlm_hip_dir_find": (i32, [vp, C.c_uint64, C.c_char_p, C.POINTER(TensorRef)]),
+    "tlm_hip_model_open": (i32, [C.c_char_p, vp, C.POINTER(vp)]),
+    "tlm_hip_model_close": (None, [vp]),
+    "tlm_hip_model_geom_of": (C.POINTER(ModelGeom), [vp]),
+    "tlm_hip_model_kv_len": (i32, [vp]),
+    "tlm_hip_model_kv_capacity": (i32, [vp]),
+    "tlm_hip_model_reset": (None, [vp]),
+    "tlm_hip_model_step": (i32, [vp, i32, vp, C.POINTER(C.c_int32)]),
+    "tlm_hip_model_generate": (i32, [vp, C.POINTER(C.c_int32), i32, i32, C.POINTER(C.c_int32)]),
     "tlm_hip_crc32c": (C.c_uint32, [C.c_uint32, vp, sz]),
     "tlm_hip_sha256": (None, [vp, sz, vp]),
     "tlm_hip_moe_layer_store": (i32, [C.POINTER(MoeDesc), vp, i32, vp, vp, vp, C.POINTER(MoeHint), i32, vp, vp]),
