@@ -202,6 +202,65 @@ def slot_cache_bench(torch, dev, router_w, ffn_norm, gen, tokens):
     return out
 
 
+C1_STORE = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
+C1_TIERLM = os.path.join(ROOT, "oracle", "_ref", "bin", "tierlm")
+
+
+def c1_prompt():
+    x, out, m = 42, [], (1 << 64) - 1
+    for _ in range(64):
+        x ^= (x << 13) & m
+        x ^= x >> 7
+        x ^= (x << 17) & m
+        out.append(x % 4096)
+    return out
+
+
+def c1_bench(reps):
+    """The whole decode step on the 4-layer synthetic model (the reference's
+    compiled store, oracle/make_c1.sh): 64-token prompt, 64 greedy tokens, as
+    `tierlm bench --prompt-len 64 -n 64`; decode tok/s = 63 / decode time.
+    Beside it the reference's own runtime on the host cores, same store."""
+    import subprocess
+    from tierlm_amd.model import Model
+    m = Model(C1_STORE, max_ctx=256)
+    prompt = c1_prompt()
+    m.reset()
+    m.generate(prompt, 64)                        # warm
+    pre = dec = None
+    for _ in range(reps):
+        m.reset()
+        t0 = time.perf_counter()
+        m.generate(prompt, 1)
+        t1 = time.perf_counter()
+        m.reset()
+        t2 = time.perf_counter()
+        toks = m.generate(prompt, 64)
+        t3 = time.perf_counter()
+        p, d = t1 - t0, (t3 - t2) - (t1 - t0)
+        pre = p if pre is None else min(pre, p)
+        dec = d if dec is None else min(dec, d)
+    m.close()
+    out = {"prefill_tok_s": round(64 / pre, 1), "decode_tok_s": round(63 / dec, 1),
+           "decode_us_per_token": round(dec / 63 * 1e6, 1), "tokens_head": toks[:4],
+           "timing": "host wall clock around tlm_hip_model_generate (prefill 64, then 63 decode steps), best of "
+                     f"{reps}; eager launches"}
+    if os.path.exists(C1_TIERLM):
+        r = subprocess.run([C1_TIERLM, "bench", C1_STORE, "--prompt-len", "64", "-n", "64", "--cache", "1G"],
+                           capture_output=True, text=True, timeout=120)
+        line = r.stdout.splitlines()[0] if r.stdout else ""
+        try:
+            ref_dec = float(line.split("decode 64 tokens in")[1].split("(")[1].split(" tok/s")[0])
+            ref_pre = float(line.split("prompt 64 tokens in")[1].split("(")[1].split(" tok/s")[0])
+            out["reference_cpu"] = {"prefill_tok_s": ref_pre, "decode_tok_s": ref_dec, "threads": os.cpu_count(),
+                                    "kind": "reference", "command": "tierlm bench --prompt-len 64 -n 64 --cache 1G"}
+        except (IndexError, ValueError):
+            out["reference_cpu"] = None
+    log(f"bench: C1 whole step: prefill {out['prefill_tok_s']:.0f} tok/s, decode {out['decode_tok_s']:.0f} tok/s "
+        f"({out['decode_us_per_token']:.1f} us/token); reference CPU {out.get('reference_cpu')}")
+    return out
+
+
 def cpu_baseline(args, threads):
     """Reference kernels on the host (oracle/_ref), bounded sample."""
     import numpy as np
@@ -249,6 +308,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill measurement")
     ap.add_argument("--no-store", action="store_true", help="skip the expert slot cache measurement")
+    ap.add_argument("--no-c1", action="store_true", help="skip the whole-step synthetic model measurement")
     ap.add_argument("--store-tokens", type=int, default=400, help="tokens per slot-cache decode measurement")
     ap.add_argument("--copy-check-mib", type=int, default=0,
                     help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
@@ -368,10 +428,12 @@ def main():
     expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
     log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); per launch: router {p1:.2f} us, "
         f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down+combine {p3:.2f} us ({dn_gbs:.0f} GB/s)")
-    # on-box streaming-read reference: this library's packed Q6_K GEMV over a ~2 GB span of
-    # the resident expert bytes read as one 2048-wide matrix (values irrelevant)
-    srows = (2 << 30) // 1680 // 16 * 16
+    # on-box streaming-read reference: this library's packed Q6_K GEMV over a span of up to
+    # 2 GiB of the resident expert bytes read as one 2048-wide matrix (values irrelevant); the
+    # span never exceeds the buffer it reads
+    srows = min(2 << 30, W.numel()) // 1680 // 16 * 16
     sbytes = hq.packed_bytes(Q6_K, srows, D)
+    assert 0 < sbytes <= W.numel(), (sbytes, W.numel())
     xs = hq.quantize_act(hq.Q8_K, torch.randn(D, generator=gen, device=dev))
     ys = torch.empty(srows, dtype=torch.float32, device=dev)
     hq.matvec_packed(Q6_K, W, srows, D, xs, ys)
@@ -400,6 +462,7 @@ def main():
 
     prefill = None if args.no_prefill else prefill_bench(torch, dev, W, router_w, ffn_norm, gen)
     slot_cache = None if args.no_store else slot_cache_bench(torch, dev, router_w, ffn_norm, gen, args.store_tokens)
+    c1 = None if args.no_c1 or not os.path.exists(C1_STORE) else c1_bench(3)
 
     cpu = None
     if not args.no_cpu:
@@ -434,6 +497,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "slot_cache": slot_cache,
+        "c1_whole_step": c1,
     }
     print(json.dumps(line), flush=True)
 

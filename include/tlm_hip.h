@@ -371,6 +371,8 @@ void     tlm_hip_sha256(const void *p, size_t n, uint8_t out[32]);
 typedef struct tlm_hip_model tlm_hip_model;
 typedef struct {
     int32_t max_ctx;     /* KV positions; 0 = the store's max_ctx, else 4096 (tlm_kv_new) */
+    int32_t eager;       /* 1: launch each step's kernels directly; 0: replay the step as a HIP graph
+                            captured at first use (the position and tokens live in device memory) */
 } tlm_hip_model_opts;
 int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
 void tlm_hip_model_close(tlm_hip_model *M);

@@ -105,3 +105,21 @@ def test_c1_context_and_token_errors(c1):
     with pytest.raises(HipError):
         c1.generate(prompt_tokens() * 4, 10)   # 256 + 9 > max_ctx 256 (TLM_ERANGE)
     assert c1.kv_len() == 0
+
+
+@needs_c1
+def test_c1_graph_replays_equal_eager_steps(hip, c1):
+    """Every replay of the captured step graph gives the eager launches' bits
+    (logits at each of 40 positions, with host work between replays)."""
+    from tierlm_amd.model import Model
+    eager = Model(C1, max_ctx=256, eager=True)
+    try:
+        c1.reset()
+        eager.reset()
+        toks = prompt_tokens()[:30] + greedy_tokens()[:10]
+        for pos, t in enumerate(toks):
+            a, na = c1.step(t)
+            b, nb = eager.step(t)
+            assert na == nb and np.array_equal(a.view(np.uint32), b.view(np.uint32)), pos
+    finally:
+        eager.close()

@@ -58,9 +58,12 @@ __device__ float block_max_f32(float v, float *red) {
 }
 
 /* ---- embedding row (tlm_dequantize_row, src/lib/tlm_quant.c:629-660) -------- */
+/* The step's position and token live in device memory (st[0] = pos, seq[pos]
+ * = the token), so one captured graph serves every position. */
 __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, size_t row_bytes, int dt,
-                                              const int32_t *__restrict__ tok, int D, float *__restrict__ h) {
-    const uint8_t *row = embd + (size_t)tok[0] * row_bytes;
+                                              const int32_t *__restrict__ seq, const int32_t *__restrict__ st, int D,
+                                              float *__restrict__ h) {
+    const uint8_t *row = embd + (size_t)seq[st[0]] * row_bytes;
     for (int i = threadIdx.x + blockIdx.x * blockDim.x; i < D; i += blockDim.x * gridDim.x) {
         if (dt == DT_F32) {
             h[i] = ((const float *)row)[i];
@@ -89,12 +92,13 @@ __global__ __launch_bounds__(NT) void k_rmsnorm(const float *__restrict__ x, con
  * layer's caches (head-major [KV][max_ctx][hd]). */
 __global__ __launch_bounds__(64) void k_qk_rope(float *__restrict__ q, float *__restrict__ kx,
                                                 const float *__restrict__ vx, const float *__restrict__ q_norm,
-                                                const float *__restrict__ k_norm, const float *__restrict__ cs,
-                                                const float *__restrict__ sn, float *__restrict__ kc,
-                                                float *__restrict__ vc, int H, int hd, int pos, int max_ctx,
-                                                float eps) {
+                                                const float *__restrict__ k_norm, const float *__restrict__ cs_all,
+                                                const float *__restrict__ sn_all, float *__restrict__ kc,
+                                                float *__restrict__ vc, int H, int hd, const int32_t *__restrict__ st,
+                                                int max_ctx, float eps) {
     __shared__ float s_v[256];
-    const int b = blockIdx.x, lane = threadIdx.x, half = hd >> 1;
+    const int b = blockIdx.x, lane = threadIdx.x, half = hd >> 1, pos = st[0];
+    const float *cs = cs_all + (size_t)pos * half, *sn = sn_all + (size_t)pos * half;
     const bool is_q = b < H;
     float *v = is_q ? q + (size_t)b * hd : kx + (size_t)(b - H) * hd;
     const float *nw = is_q ? q_norm : k_norm;
@@ -131,13 +135,22 @@ __global__ __launch_bounds__(64) void k_qk_rope(float *__restrict__ q, float *__
 
 /* ---- attention core, one group per head (src/lib/tlm_model.c:683-719) --------
  * kc / vc: this layer's caches, head-major [KV][max_ctx][hd]; scores: H x
- * max_ctx floats of scratch. */
+ * max_ctx floats of scratch.  The reference's order is kept: each score is
+ * one thread's dot product in ascending i, and each output element one
+ * thread's sum over positions in ascending t.  V goes through LDS in chunks
+ * of ATT_TC positions (coalesced loads), so that ordered sum runs on LDS
+ * reads instead of a global round trip per position. */
+constexpr int ATT_TC = 32;
+
 __global__ __launch_bounds__(NT) void k_attn(const float *__restrict__ q, const float *__restrict__ kc,
                                              const float *__restrict__ vc, float *__restrict__ scores,
-                                             float *__restrict__ att, int H, int KV, int hd, int max_ctx, int T) {
-    __shared__ float s_q[256];
+                                             float *__restrict__ att, int H, int KV, int hd, int max_ctx,
+                                             const int32_t *__restrict__ st) {
+    __shared__ __align__(16) float s_q[256];
+    __shared__ __align__(16) float s_v[ATT_TC * 256];
     __shared__ double s_red[NT / 64];
     __shared__ float s_redf[NT / 64];
+    const int T = st[0] + 1;
     const int h = blockIdx.x, tid = threadIdx.x, kvh = h / (H / KV);
     const float *K = kc + (size_t)kvh * max_ctx * hd, *V = vc + (size_t)kvh * max_ctx * hd;
     float *s = scores + (size_t)h * max_ctx;
@@ -146,9 +159,15 @@ __global__ __launch_bounds__(NT) void k_attn(const float *__restrict__ q, const 
     const float scale = 1.0f / sqrtf((float)hd);
     float mx = -INFINITY;
     for (int t = tid; t < T; t += NT) {
-        const float *kt = K + (size_t)t * hd;
+        const f32x4 *kt = (const f32x4 *)(K + (size_t)t * hd);   /* hd % 32 == 0: 16-byte rows */
         float d = 0.0f;
-        for (int i = 0; i < hd; i++) d += s_q[i] * kt[i];
+        for (int i4 = 0; i4 < hd / 4; i4++) {
+            const f32x4 k4 = kt[i4];
+            d += s_q[4 * i4] * k4.x;
+            d += s_q[4 * i4 + 1] * k4.y;
+            d += s_q[4 * i4 + 2] * k4.z;
+            d += s_q[4 * i4 + 3] * k4.w;
+        }
         d *= scale;   /* scale after the dot, before the max */
         s[t] = d;
         if (d > mx) mx = d;
@@ -163,14 +182,20 @@ __global__ __launch_bounds__(NT) void k_attn(const float *__restrict__ q, const 
     sum = block_sum_f64(sum, s_red);
     const float inv = (float)(1.0 / sum);
     __syncthreads();   /* every p stored */
-    for (int i = tid; i < hd; i += NT) {
-        float o = 0.0f;
-        for (int t = 0; t < T; t++) {
-            const float p = s[t] * inv;
-            o += p * V[(size_t)t * hd + i];
-        }
-        att[(size_t)h * hd + i] = o;
+    float o = 0.0f;
+    for (int t0 = 0; t0 < T; t0 += ATT_TC) {
+        const int tn = T - t0 < ATT_TC ? T - t0 : ATT_TC;
+        const int n4 = tn * hd / 4;
+        for (int e = tid; e < n4; e += NT) ((f32x4 *)s_v)[e] = ((const f32x4 *)(V + (size_t)t0 * hd))[e];
+        __syncthreads();
+        if (tid < hd)
+            for (int t = 0; t < tn; t++) {
+                const float p = s[t0 + t] * inv;
+                o += p * s_v[t * hd + tid];
+            }
+        __syncthreads();   /* the chunk is read before the next one overwrites it */
     }
+    if (tid < hd) att[(size_t)h * hd + tid] = o;
 }
 
 __global__ __launch_bounds__(NT) void k_add(float *__restrict__ h, const float *__restrict__ y, int n) {
@@ -179,7 +204,8 @@ __global__ __launch_bounds__(NT) void k_add(float *__restrict__ h, const float *
 }
 
 /* greedy: the first maximum, NaN skipped, 0 if none (src/lib/tlm_model.c:1139-1146) */
-__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ l, int n, int32_t *__restrict__ out) {
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ l, int n, int32_t *__restrict__ seq,
+                                                 const int32_t *__restrict__ st) {
     __shared__ float s_v[1024];
     __shared__ int s_i[1024];
     float bv = 0.0f;
@@ -207,7 +233,11 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ l, in
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) out[0] = s_i[0] < 0 ? 0 : s_i[0];
+    if (threadIdx.x == 0) seq[st[0] + 1] = s_i[0] < 0 ? 0 : s_i[0];   /* the next step's token */
+}
+
+__global__ void k_advance(int32_t *st) {
+    if (threadIdx.x == 0) st[0] += 1;
 }
 
 struct DevMat {
@@ -239,9 +269,11 @@ struct tlm_hip_model {
     float *h = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
     float *logits = nullptr;
     uint8_t *act = nullptr, *act2 = nullptr, *moe_ws = nullptr;
-    int32_t *tok = nullptr, *ids = nullptr;
+    int32_t *st = nullptr, *seq = nullptr, *ids = nullptr;   /* st[0] = position; seq[max_ctx + 1] tokens */
     float *w = nullptr;
     int32_t *host_tok = nullptr;   /* pinned */
+    hipGraphExec_t graph[2] = {nullptr, nullptr};   /* step without / with logits, captured at first use */
+    bool graph_failed[2] = {false, false};
 
     void *dalloc(size_t n) {
         void *p = nullptr;
@@ -251,6 +283,8 @@ struct tlm_hip_model {
     }
     ~tlm_hip_model() {
         if (stream) (void)hipStreamSynchronize(stream);
+        for (hipGraphExec_t g : graph)
+            if (g) (void)hipGraphExecDestroy(g);
         for (void *p : allocs) (void)hipFree(p);
         if (host_tok) (void)hipHostFree(host_tok);
         if (stream) (void)hipStreamDestroy(stream);
@@ -381,6 +415,7 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
     if (max_ctx <= 0) max_ctx = g.max_ctx > 0 ? (int)g.max_ctx : 4096;
     if (g.max_ctx > 0 && max_ctx > (int)g.max_ctx) max_ctx = (int)g.max_ctx;
     M->max_ctx = max_ctx;
+    M->graph_failed[0] = M->graph_failed[1] = o && o->eager;
     const int64_t D = g.d_model, hd = g.head_dim, H = g.n_heads, KV = g.n_kv_heads, E = g.n_experts;
     const int64_t de = g.d_expert, ds = g.n_shared > 0 ? g.d_shared : 0;
 
@@ -554,15 +589,18 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
     size_t ws = 0;
     for (const Layer &Ly : M->L) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
     M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
-    M->tok = (int32_t *)M->dalloc(16);
+    M->st = (int32_t *)M->dalloc(16);
+    M->seq = (int32_t *)M->dalloc(((size_t)max_ctx + 1) * 4);
     M->ids = (int32_t *)M->dalloc(32 * 4);
     M->w = (float *)M->dalloc(32 * 4);
     for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->h, (void *)M->xb, (void *)M->xb2,
                     (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits, (void *)M->act,
-                    (void *)M->act2, (void *)M->moe_ws, (void *)M->tok, (void *)M->ids, (void *)M->w})
+                    (void *)M->act2, (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
+                    (void *)M->w})
         if (!p) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the KV cache / scratch");
     if ((rc = tlmh_check(hipHostMalloc((void **)&M->host_tok, 64, hipHostMallocDefault), "model: pinned scratch")))
         return rc;
+    if ((rc = tlmh_check(hipMemset(M->st, 0, 16), "model: position"))) return rc;
     return tlmh_check(hipStreamSynchronize(M->stream), "model: load");
 }
 
@@ -573,14 +611,16 @@ int matvec(tlm_hip_model *M, const DevMat &W, const float *x, uint8_t *act, floa
     return rc;
 }
 
-/* tlm_model_step, src/lib/tlm_model.c:1058-1103: token in M->tok (device) */
-int step(tlm_hip_model *M, bool want_logits) {
+/* tlm_model_step, src/lib/tlm_model.c:1058-1103, enqueued: the token is
+ * seq[pos], pos = st[0]; with logits, the greedy next token goes to
+ * seq[pos + 1]; st[0] advances.  Every argument is the same at every position
+ * (the step is captured once as a graph). */
+int enqueue_step(tlm_hip_model *M, bool want_logits) {
     const tlm_hip_model_geom &g = M->g;
     const int D = (int)g.d_model, hd = (int)g.head_dim, H = (int)g.n_heads, KV = (int)g.n_kv_heads;
-    const int pos = M->kv_len, half = hd / 2;
     hipStream_t s = M->stream;
     hipLaunchKernelGGL(k_embed, dim3((D + NT - 1) / NT), dim3(NT), 0, s, M->embd, M->embd_row, M->embd_dt,
-                       (const int32_t *)M->tok, D, M->h);
+                       (const int32_t *)M->seq, (const int32_t *)M->st, D, M->h);
     int rc = tlmh_check(hipGetLastError(), "model: embed");
     for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
         const Layer &Ly = M->L[l];
@@ -594,11 +634,11 @@ int step(tlm_hip_model *M, bool want_logits) {
         if (rc) break;
         const size_t lbase = (size_t)l * KV * M->max_ctx * hd;
         hipLaunchKernelGGL(k_qk_rope, dim3(H + KV), dim3(64), 0, s, M->q, M->kx, (const float *)M->vx, Ly.q_norm,
-                           Ly.k_norm, (const float *)(M->cs + (size_t)pos * half),
-                           (const float *)(M->sn + (size_t)pos * half), M->kc + lbase, M->vc + lbase, H, hd, pos,
-                           M->max_ctx, g.norm_eps);
+                           Ly.k_norm, (const float *)M->cs, (const float *)M->sn, M->kc + lbase, M->vc + lbase, H,
+                           hd, (const int32_t *)M->st, M->max_ctx, g.norm_eps);
         hipLaunchKernelGGL(k_attn, dim3(H), dim3(NT), 0, s, (const float *)M->q, (const float *)(M->kc + lbase),
-                           (const float *)(M->vc + lbase), M->scores, M->att, H, KV, hd, M->max_ctx, pos + 1);
+                           (const float *)(M->vc + lbase), M->scores, M->att, H, KV, hd, M->max_ctx,
+                           (const int32_t *)M->st);
         rc = tlmh_check(hipGetLastError(), "model: attention");
         if (!rc) rc = matvec(M, Ly.o, M->att, M->act2, M->xb2);
         if (rc) break;
@@ -607,15 +647,41 @@ int step(tlm_hip_model *M, bool want_logits) {
         rc = launch_moe_layer(&Ly.moe, M->h, M->ids, M->w, M->moe_ws, s);
     }
     if (rc) return rc;
-    M->kv_len = pos + 1;
     if (want_logits) {   /* tlm_model.c:1087-1095, then the greedy argmax */
         hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(NT), 0, s, (const float *)M->h, M->out_norm, D, g.norm_eps,
                            M->xb);
         rc = matvec(M, M->lm_head, M->xb, M->act, M->logits);
         if (rc) return rc;
-        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, (const float *)M->logits, (int)g.vocab, M->tok);
-        rc = tlmh_check(hipGetLastError(), "model: logits");
+        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, (const float *)M->logits, (int)g.vocab, M->seq,
+                           (const int32_t *)M->st);
     }
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, M->st);
+    return tlmh_check(hipGetLastError(), "model: step");
+}
+
+/* One step (the caller checked the context): the captured graph of the kind,
+ * captured at first use; eager launches if capture is unavailable. */
+int step(tlm_hip_model *M, bool want_logits) {
+    const int k = want_logits ? 1 : 0;
+    if (!M->graph[k] && !M->graph_failed[k]) {
+        hipGraph_t gr = nullptr;
+        int rc = tlmh_check(hipStreamBeginCapture(M->stream, hipStreamCaptureModeThreadLocal), "model: capture");
+        if (!rc) {
+            const int rc_enq = enqueue_step(M, want_logits);
+            rc = tlmh_check(hipStreamEndCapture(M->stream, &gr), "model: capture");
+            if (!rc) rc = rc_enq;
+        }
+        if (!rc) rc = tlmh_check(hipGraphInstantiate(&M->graph[k], gr, nullptr, nullptr, 0), "model: instantiate");
+        if (gr) (void)hipGraphDestroy(gr);
+        if (rc) {
+            M->graph[k] = nullptr;
+            M->graph_failed[k] = true;
+            (void)hipGetLastError();
+        }
+    }
+    int rc = M->graph[k] ? tlmh_check(hipGraphLaunch(M->graph[k], M->stream), "model: step graph")
+                         : enqueue_step(M, want_logits);
+    if (!rc) M->kv_len++;
     return rc;
 }
 
@@ -647,7 +713,11 @@ const tlm_hip_model_geom *tlm_hip_model_geom_of(const tlm_hip_model *M) { return
 int tlm_hip_model_kv_len(const tlm_hip_model *M) { return M ? M->kv_len : 0; }
 int tlm_hip_model_kv_capacity(const tlm_hip_model *M) { return M ? M->max_ctx : 0; }
 void tlm_hip_model_reset(tlm_hip_model *M) {
-    if (M) M->kv_len = 0;
+    if (!M) return;
+    M->kv_len = 0;
+    M->host_tok[2] = 0;
+    (void)hipMemcpyAsync(M->st, M->host_tok + 2, 4, hipMemcpyHostToDevice, M->stream);
+    (void)hipStreamSynchronize(M->stream);
 }
 
 /* tlm_model_step: one token; logits (host, vocab floats) and the greedy next
@@ -656,50 +726,42 @@ int tlm_hip_model_step(tlm_hip_model *M, int token, float *logits, int32_t *next
     if (!M) return tlmh_seterr(TLM_HIP_EINVAL, "model step: NULL");
     if (token < 0 || (uint32_t)token >= M->g.vocab) return tlmh_seterr(TLM_HIP_EINVAL, "token %d out of range", token);
     if (M->kv_len >= M->max_ctx) return tlmh_seterr(TLM_HIP_ERANGE, "context full (%d tokens)", M->max_ctx);
+    const int pos = M->kv_len;
     M->host_tok[0] = token;
-    int rc = tlmh_check(hipMemcpyAsync(M->tok, M->host_tok, 4, hipMemcpyHostToDevice, M->stream), "model: token");
+    int rc = tlmh_check(hipMemcpyAsync(M->seq + pos, M->host_tok, 4, hipMemcpyHostToDevice, M->stream), "model: token");
     if (!rc) rc = step(M, logits || next);
     if (!rc && logits)
         rc = tlmh_check(hipMemcpyAsync(logits, M->logits, (size_t)M->g.vocab * 4, hipMemcpyDeviceToHost, M->stream),
                         "model: logits");
-    if (!rc && next) rc = tlmh_check(hipMemcpyAsync(M->host_tok + 1, M->tok, 4, hipMemcpyDeviceToHost, M->stream),
-                                     "model: next token");
+    if (!rc && next)
+        rc = tlmh_check(hipMemcpyAsync(M->host_tok + 1, M->seq + pos + 1, 4, hipMemcpyDeviceToHost, M->stream),
+                        "model: next token");
     if (!rc) rc = tlmh_check(hipStreamSynchronize(M->stream), "model: step");
     if (!rc && next) *next = M->host_tok[1];
     return rc;
 }
 
 /* tlm_model_prefill (src/lib/tlm_model.c:1105-1113) then n_gen greedy tokens
- * (tierlm bench's loop, src/bin/tierlm.c:720-729): the next token never
- * leaves the device between steps; out receives the n_gen tokens. */
+ * (tierlm bench's loop, src/bin/tierlm.c:720-729): the prompt is written to
+ * the device once, each step's token is read there and each greedy token is
+ * written there by the previous step; out receives the n_gen tokens. */
 int tlm_hip_model_generate(tlm_hip_model *M, const int32_t *prompt, int n_prompt, int n_gen, int32_t *out) {
     if (!M || !prompt || n_prompt <= 0 || n_gen < 0 || (n_gen > 0 && !out))
         return tlmh_seterr(TLM_HIP_EINVAL, "model generate: bad arguments");
-    if (M->kv_len + n_prompt + (n_gen > 0 ? n_gen - 1 : 0) > M->max_ctx)
+    const int pos0 = M->kv_len;
+    if ((int64_t)pos0 + n_prompt + (n_gen > 0 ? n_gen - 1 : 0) > M->max_ctx)
         return tlmh_seterr(TLM_HIP_ERANGE, "model generate: %d + %d tokens exceed the context (%d)", n_prompt, n_gen,
                            M->max_ctx);
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || (uint32_t)prompt[i] >= M->g.vocab)
             return tlmh_seterr(TLM_HIP_EINVAL, "token %d out of range", prompt[i]);
-    int32_t *dev_out = n_gen > 0 ? (int32_t *)M->dalloc((size_t)n_gen * 4) : nullptr;
-    if (n_gen > 0 && !dev_out) return tlmh_seterr(TLM_HIP_ENOMEM, "model generate: out of device memory");
-    int rc = TLM_HIP_OK;
-    for (int i = 0; i < n_prompt && !rc; i++) {
-        rc = tlmh_check(hipMemcpyAsync(M->tok, prompt + i, 4, hipMemcpyHostToDevice, M->stream), "model: token");
-        if (!rc) rc = tlmh_check(hipStreamSynchronize(M->stream), "model: token");   /* prompt is pageable */
-        if (!rc) rc = step(M, i == n_prompt - 1);
-    }
-    for (int gi = 0; gi < n_gen && !rc; gi++) {
-        rc = tlmh_check(hipMemcpyAsync(dev_out + gi, M->tok, 4, hipMemcpyDeviceToDevice, M->stream), "model: token");
-        if (!rc && gi + 1 < n_gen) rc = step(M, true);
-    }
+    int rc = tlmh_check(hipMemcpy(M->seq + pos0, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice), "model: prompt");
+    for (int i = 0; i < n_prompt && !rc; i++) rc = step(M, i == n_prompt - 1);
+    for (int gi = 1; gi < n_gen && !rc; gi++) rc = step(M, true);
     if (!rc && n_gen > 0)
-        rc = tlmh_check(hipMemcpyAsync(out, dev_out, (size_t)n_gen * 4, hipMemcpyDeviceToHost, M->stream), "model: out");
+        rc = tlmh_check(hipMemcpyAsync(out, M->seq + pos0 + n_prompt, (size_t)n_gen * 4, hipMemcpyDeviceToHost,
+                                       M->stream), "model: out");
     if (!rc) rc = tlmh_check(hipStreamSynchronize(M->stream), "model: generate");
-    if (dev_out) {
-        M->allocs.pop_back();
-        (void)hipFree(dev_out);
-    }
     return rc;
 }
 

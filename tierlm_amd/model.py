@@ -10,12 +10,12 @@ from ._lib import check, lib
 
 class ModelOpts(C.Structure):
     """tlm_hip_model_opts"""
-    _fields_ = [("max_ctx", C.c_int32)]
+    _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32)]
 
 
 class Model:
-    def __init__(self, manifest_path, max_ctx=0):
-        self.opts = ModelOpts(max_ctx)
+    def __init__(self, manifest_path, max_ctx=0, eager=False):
+        self.opts = ModelOpts(max_ctx, int(eager))
         h = C.c_void_p()
         check(lib.tlm_hip_model_open(str(manifest_path).encode(), C.byref(self.opts), C.byref(h)))
         self.h = h
