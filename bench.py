@@ -244,7 +244,7 @@ def c1_bench(reps):
     out = {"prefill_tok_s": round(64 / pre, 1), "decode_tok_s": round(63 / dec, 1),
            "decode_us_per_token": round(dec / 63 * 1e6, 1), "tokens_head": toks[:4],
            "timing": "host wall clock around tlm_hip_model_generate (prefill 64, then 63 decode steps), best of "
-                     f"{reps}; eager launches"}
+                     f"{reps}; each step one replay of a captured HIP graph"}
     if os.path.exists(C1_TIERLM):
         r = subprocess.run([C1_TIERLM, "bench", C1_STORE, "--prompt-len", "64", "-n", "64", "--cache", "1G"],
                            capture_output=True, text=True, timeout=120)

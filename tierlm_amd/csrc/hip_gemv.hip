@@ -20,6 +20,7 @@
  */
 #include "tlm_hip_internal.h"
 #include "tlm_hip_items.h"
+#include "tlm_hip_act.h"
 
 #include <math.h>
 
@@ -315,6 +316,177 @@ __global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ W
     }
 }
 
+/* rmsnorm of x (when w is given) then the activation quantiser of kind,
+ * written straight into the LDS layout that stage_act fills from a quantised
+ * vector: r = 1 / sqrtf(mean(x^2) + eps) with the sum of squares in double
+ * (per thread, then a fixed tree), values x * r * w (rmsnorm,
+ * src/lib/tlm_model.c:164-169, then the quantiser of
+ * src/lib/tlm_quant.c:458-506); without w, x itself is quantised.  Thread mapping: Q8_K, one
+ * wave per 256-value block, 4 values per lane; a8, 8 lanes per 32-value
+ * block.  The first NQ_IT passes keep x and w in registers between the sum
+ * and the quantiser.  Every thread takes part; the caller synchronises. */
+constexpr int NQ_IT = 4;
+
+static __device__ __forceinline__ XLds stage_norm_act(int kind, const float *__restrict__ x,
+                                                      const float *__restrict__ w, float eps, int nb, uint8_t *lds_g) {
+    __shared__ double red[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (int)blockDim.x >> 6;
+    const bool k8 = kind == DT_Q8_K;
+    const int bv = k8 ? 256 : 32, n = nb * bv;
+    const int per = k8 ? nw : (int)blockDim.x / 8;   /* blocks per pass */
+    const int nit = (nb + per - 1) / per;
+    const int myb = k8 ? wave : tid / 8, off = 4 * (k8 ? lane : (tid & 7));
+    const bool plain = w == nullptr;
+    const GAS f32x4 *x4 = (const GAS f32x4 *)x, *w4 = (const GAS f32x4 *)w;
+    f32x4 xv[NQ_IT], wv[NQ_IT];
+#pragma unroll
+    for (int it = 0; it < NQ_IT; it++) {
+        const int b = it * per + myb;
+        if (b < nb) {
+            xv[it] = x4[(b * bv + off) / 4];
+            if (!plain) wv[it] = w4[(b * bv + off) / 4];
+        }
+    }
+    float r = 1.0f;
+    if (!plain) {
+        double ss = 0.0;
+#pragma unroll
+        for (int it = 0; it < NQ_IT; it++)
+            if (it * per + myb < nb)
+                for (int j = 0; j < 4; j++) ss += (double)xv[it][j] * (double)xv[it][j];
+        for (int it = NQ_IT; it < nit; it++) {
+            const int b = it * per + myb;
+            if (b < nb) {
+                const f32x4 a = x4[(b * bv + off) / 4];
+                for (int j = 0; j < 4; j++) ss += (double)a[j] * (double)a[j];
+            }
+        }
+        ss = wave_sum_f64(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = 0.0;
+        for (int i = 0; i < nw; i++) ss += red[i];
+        r = 1.0f / sqrtf((float)(ss / (double)n) + eps);
+    }
+    LAS uint8_t *lds = (LAS uint8_t *)lds_g;
+    LAS uint32_t *q32 = (LAS uint32_t *)lds;
+    LAS int16_t *bs16 = (LAS int16_t *)(lds + nb * 256);
+    LAS float *dl = (LAS float *)(lds + (k8 ? nb * 288 : nb * 32));
+    auto quant = [&](int b, const f32x4 &a, const f32x4 &ww) {
+        const bool live = b < nb;
+        float v[4];
+        bool ok[4];
+        for (int j = 0; j < 4; j++) {
+            ok[j] = live;
+            v[j] = !live ? 0.0f : plain ? a[j] : a[j] * r * ww[j];
+        }
+        uint32_t codes;
+        if (k8) {
+            const float d = act_rule<64>(v, ok, codes);
+            int sm = byte_sum(codes);
+            sm += __shfl_xor(sm, 1, 64);
+            sm += __shfl_xor(sm, 2, 64);
+            if (live) {
+                q32[b * 64 + lane] = codes;
+                if (lane == 0) dl[b] = d;
+                if ((lane & 3) == 0) bs16[b * 16 + (lane >> 2)] = (int16_t)sm;
+            }
+        } else {
+            const float d = act_rule<8>(v, ok, codes);
+            if (live) {
+                q32[b * 8 + (tid & 7)] = codes;
+                if ((tid & 7) == 0) dl[b] = d;
+            }
+        }
+    };
+#pragma unroll
+    for (int it = 0; it < NQ_IT; it++)
+        if (it < nit) quant(it * per + myb, xv[it], wv[it]);
+    for (int it = NQ_IT; it < nit; it++) {
+        const int b = it * per + myb;
+        f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f}, ww = a;
+        if (b < nb) {
+            a = x4[(b * bv + off) / 4];
+            if (!plain) ww = w4[(b * bv + off) / 4];
+        }
+        quant(b, a, ww);
+    }
+    return xlds_at(kind, nb, lds_g);
+}
+
+/* The same tile for up to MV_SEGS matrices of one dtype and width in one
+ * launch (segment s owns tiles [tile_end[s-1], tile_end[s])), all taking the
+ * same activation; accum: y[r] += acc instead of y[r] = acc (the reference's
+ * residual update h += W x, tlm_model.c:762, adds the finished product). */
+template <int DT>
+__global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
+    using F = Packed<DT>;
+    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
+    constexpr int IPL = 4;
+    extern __shared__ __align__(16) uint8_t lds[];
+    int s = 0;
+    while (s + 1 < sg.n && (int64_t)blockIdx.x >= sg.tile_end[s]) s++;
+    const uint8_t *Wp = sg.W[s];
+    const int64_t rows = sg.rows[s], t = (int64_t)blockIdx.x - (s ? sg.tile_end[s - 1] : 0);
+    float *y = sg.y[s];
+    const int kind = dt_act_kind(DT);
+    XLds X = xlds_at(kind, nb, lds);
+    if (!sg.nx) {
+        stage_act(kind, act, nb, lds);
+        __syncthreads();
+    }
+    const int cap = nb < PK_NBC ? nb : PK_NBC;
+    const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * TILE_ROWS);
+    bool staged = !sg.nx;
+    /* the activation from rmsnorm once the first weight loads are out */
+    auto stage = [&]() {
+        if (!staged) {
+            stage_norm_act(kind, sg.nx, sg.nw, sg.eps, nb, lds);
+            __syncthreads();
+            staged = true;
+        }
+        return X;
+    };
+    const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    const int64_t units = T * nb * TILE_ROWS;
+    const int round_items = (int)(blockDim.x / F::LPI) * IPL;
+    float acc = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += cap) {
+        const int nbc = nb - b0 < cap ? nb - b0 : cap;
+        const int nitems = nbc * TILE_ROWS;
+        for (int base = 0; base < nitems; base += round_items) {
+            auto map = [&](int it, const uint8_t *&W, int64_t &un, int64_t &u, int &b, int &pk) {
+                const int g = base + it, bl = g / TILE_ROWS, i = g % TILE_ROWS;
+                W = Wp;
+                un = units;
+                b = b0 + bl;
+                u = ((int64_t)t * nb + b) * TILE_ROWS + i;
+                pk = g;
+            };
+            run_items<DT, IPL>(nitems - base, map, stage, park);
+        }
+        __syncthreads();
+        if (threadIdx.x < TILE_ROWS) {
+            const int i = threadIdx.x;
+            for (int bl = 0; bl < nbc; bl++) {
+                acc = fmaf(park.da[bl * TILE_ROWS + i], (float)park.is[bl * TILE_ROWS + i], acc);
+                if (AFF) acc = fmaf(-park.dm[bl * TILE_ROWS + i], (float)park.ms[bl * TILE_ROWS + i], acc);
+            }
+        }
+        __syncthreads();
+    }
+    const int64_t r = t * TILE_ROWS + threadIdx.x;
+    if (threadIdx.x < TILE_ROWS && r < rows) y[r] = sg.accum ? y[r] + acc : acc;
+    if (sg.keys && threadIdx.x < 64) {   /* lanes 0..15 hold the tile's rows */
+        unsigned long long key = threadIdx.x < TILE_ROWS && r < rows ? argmax_key(acc, (uint32_t)r) : 0ull;
+        for (int o = 8; o > 0; o >>= 1) {
+            const unsigned long long other = __shfl_xor(key, o, 64);
+            key = other > key ? other : key;
+        }
+        if (threadIdx.x == 0) sg.keys[t] = key;
+    }
+}
+
 static size_t packed_lds_bytes(int dt, int nb) {
     int cap = nb < PK_NBC ? nb : PK_NBC;
     return ((stage_bytes(dt_act_kind(dt), nb) + 15) & ~(size_t)15) + (size_t)cap * TILE_ROWS * 16;
@@ -416,6 +588,50 @@ int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const 
     case DT_Q8_K: hipLaunchKernelGGL(k_mv_packed<DT_Q8_K>, g, blk, lds, s, w, rows, nb, a, y); break;
     }
     return tlmh_check(hipGetLastError(), "matvec_packed launch");
+}
+
+int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows, float *const *y, int nseg, int accum,
+                   const void *act, hipStream_t s, const MvNorm *norm, unsigned long long *keys) {
+    if (nseg < 1 || nseg > MV_SEGS) return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: %d segments", nseg);
+    if (packed_bytes(dt, 1, n) == 0 || dt == DT_F32 || n <= 0 || n % dt_block_values(dt))
+        return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: dtype %d, n=%lld", dt, (long long)n);
+    if (norm ? (!norm->x || ((uintptr_t)norm->x & 15u) || ((uintptr_t)norm->w & 15u))
+             : (!act || ((uintptr_t)act & 3u)))
+        return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: activation");
+    if (keys && (nseg != 1 || ((uintptr_t)keys & 7u) || rows[0] > 0x7FFFFFFF))
+        return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: greedy key needs one segment");
+    const int nb = (int)(n / dt_block_values(dt));
+    if (stage_bytes(dt_act_kind(dt), nb) > 40 * 1024)
+        return tlmh_seterr(TLM_HIP_EUNSUP, "mv_segs: n=%lld exceeds the staged-activation limit", (long long)n);
+    MvSegs sg{};
+    sg.n = nseg;
+    sg.accum = accum;
+    sg.nx = norm ? norm->x : nullptr;
+    sg.nw = norm ? norm->w : nullptr;
+    sg.eps = norm ? norm->eps : 0.0f;
+    sg.keys = keys;
+    int64_t end = 0;
+    for (int i = 0; i < nseg; i++) {
+        if (!W[i] || !y[i] || rows[i] <= 0 || ((uintptr_t)W[i] & 15u))
+            return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: segment %d", i);
+        sg.W[i] = (const uint8_t *)W[i];
+        sg.rows[i] = rows[i];
+        sg.y[i] = y[i];
+        end += (rows[i] + TILE_ROWS - 1) / TILE_ROWS;
+        sg.tile_end[i] = end;
+    }
+    const size_t lds = packed_lds_bytes(dt, nb);
+    const dim3 g((unsigned)end), blk(256);
+    const uint8_t *a = (const uint8_t *)act;
+    switch (dt) {
+    case DT_Q8_0: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q8_0>, g, blk, lds, s, sg, nb, a); break;
+    case DT_Q4_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q4_K>, g, blk, lds, s, sg, nb, a); break;
+    case DT_Q5_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q5_K>, g, blk, lds, s, sg, nb, a); break;
+    case DT_Q6_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q6_K>, g, blk, lds, s, sg, nb, a); break;
+    case DT_Q8_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q8_K>, g, blk, lds, s, sg, nb, a); break;
+    default: return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: dtype %d", dt);
+    }
+    return tlmh_check(hipGetLastError(), "mv_segs launch");
 }
 
 int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s) {

@@ -16,6 +16,7 @@
  * of sequential double sums, and e^x is exp in double rounded to float; the
  * reference's greedy tokens are reproduced exactly. */
 #include "tlm_hip_internal.h"
+#include "tlm_hip_act.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -42,21 +43,6 @@ __device__ double block_sum_f64(double v, double *red) {
     return s;
 }
 
-/* max over non-NaN values (a NaN never compares greater), -inf if none */
-__device__ float block_max_f32(float v, float *red) {
-    for (int o = 32; o > 0; o >>= 1) {
-        const float u = __shfl_xor(v, o);
-        v = u > v ? u : v;
-    }
-    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float m = -INFINITY;
-    for (int i = 0; i < nw; i++) m = red[i] > m ? red[i] : m;
-    return m;
-}
-
 /* ---- embedding row (tlm_dequantize_row, src/lib/tlm_quant.c:629-660) -------- */
 /* The step's position and token live in device memory (st[0] = pos, seq[pos]
  * = the token), so one captured graph serves every position. */
@@ -75,169 +61,288 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
     }
 }
 
-/* ---- rmsnorm over one vector: out = x * r * w, r = 1 / sqrtf(mean(x^2) + eps) */
-__global__ __launch_bounds__(NT) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, int n,
-                                                float eps, float *__restrict__ out) {
-    __shared__ double red[NT / 64];
-    double ss = 0.0;
-    for (int i = threadIdx.x; i < n; i += NT) ss += (double)x[i] * (double)x[i];
-    ss = block_sum_f64(ss, red);
-    const float r = 1.0f / sqrtf((float)(ss / (double)n) + eps);
-    for (int i = threadIdx.x; i < n; i += NT) out[i] = x[i] * r * w[i];
-}
+/* ---- attention for one query head, everything it needs fused ---------------
+ * (src/lib/tlm_model.c:743-756 with attn_heads :683-719): the head's q-norm
+ * and RoPE, the k-norm and RoPE of its key head and the KV append (written by
+ * the first query head of each key head; the others take the new key and
+ * value from their own copy), scores, softmax and P.V in the reference's
+ * order, the output stored to att.  Each score is one thread's dot product in
+ * ascending i, each output element one thread's sum over positions in
+ * ascending t.
+ *
+ * Cache layout (per layer and key head): keys dimension-major, K[i][t] at
+ * i * max_ctx + t, so that the lanes of a score pass (one position each)
+ * read consecutive words for every i; values position-major, V[t][i], so
+ * that a chunk of positions is one contiguous run.
+ *
+ * Latency, not bandwidth, sets this kernel's time (one group per head), so
+ * it is arranged around the memory counter, which retires loads in issue
+ * order: every load goes out at entry, unconditionally (indices clamped) and
+ * in the order the values are consumed - head vectors, norm weights and
+ * RoPE factors, then the first pass's key column per thread (HD <= 128) and
+ * the first V chunk (ATT_VF floats) - and no global store precedes a barrier
+ * (a barrier waits for the group's stores): the KV append goes last.  The
+ * probabilities stay in LDS (dynamic, max_ctx floats) when SPL, else in the
+ * head's global scratch row; they are scaled by 1/sum in place (the
+ * reference's p = s[t] * inv).  The ordered sums go 16 positions per group
+ * (four 16-byte probability reads, sixteen fixed-offset value reads, then
+ * the adds); the last group of a chunk reads whole (the probability row is padded to 16, a chunk holds a
+ * multiple of 16 positions) and masks its adds.  Later V chunks load into
+ * registers while the previous one is summed.  q_norm / k_norm are read only
+ * when has_qn / has_kn. */
+constexpr int ATT_VF = 8192;                 /* floats of V per LDS chunk (32 KB) */
+constexpr int ATT_PF = ATT_VF / 4 / NT;      /* 16-byte V loads per thread per chunk */
+constexpr int ATT_LDS_POS = 4096;            /* contexts whose probabilities fit in LDS */
+constexpr int ATT_PU = 16;                   /* positions per group in the ordered sums */
 
-/* ---- per head: qk-norm, RoPE, KV append (src/lib/tlm_model.c:743-753) -------
- * One wave per head; blocks [0, H) take the query heads, [H, H + KV) the key
- * heads, which also store k (after RoPE) and v at position pos of this
- * layer's caches (head-major [KV][max_ctx][hd]). */
-__global__ __launch_bounds__(64) void k_qk_rope(float *__restrict__ q, float *__restrict__ kx,
-                                                const float *__restrict__ vx, const float *__restrict__ q_norm,
-                                                const float *__restrict__ k_norm, const float *__restrict__ cs_all,
-                                                const float *__restrict__ sn_all, float *__restrict__ kc,
-                                                float *__restrict__ vc, int H, int hd, const int32_t *__restrict__ st,
-                                                int max_ctx, float eps) {
-    __shared__ float s_v[256];
-    const int b = blockIdx.x, lane = threadIdx.x, half = hd >> 1, pos = st[0];
-    const float *cs = cs_all + (size_t)pos * half, *sn = sn_all + (size_t)pos * half;
-    const bool is_q = b < H;
-    float *v = is_q ? q + (size_t)b * hd : kx + (size_t)(b - H) * hd;
-    const float *nw = is_q ? q_norm : k_norm;
-    float e[4];   /* hd <= 256 */
-    for (int k = 0; k < 4; k++) e[k] = lane + 64 * k < hd ? v[lane + 64 * k] : 0.0f;
-    if (nw) {   /* rmsnorm over the head, in place (tlm_model.c:743-746) */
-        double ss = 0.0;
-        for (int k = 0; k < 4; k++) ss += (double)e[k] * (double)e[k];
-        ss = wave_sum_f64(ss);
-        const float r = 1.0f / sqrtf((float)(ss / (double)hd) + eps);
-        for (int k = 0; k < 4; k++)
-            if (lane + 64 * k < hd) e[k] = e[k] * r * nw[lane + 64 * k];
-    }
-    for (int k = 0; k < 4; k++)
-        if (lane + 64 * k < hd) s_v[lane + 64 * k] = e[k];
+/* max over non-NaN values (a NaN never compares greater), -inf if none */
+__device__ float block_max_dpp(float v, float *red) {
+    v = wave_max_f32(v);
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     __syncthreads();
-    /* NeoX pairs (j, j + hd/2): a' = a cs - b sn, b' = b cs + a sn (rope(), :721-728) */
-    for (int j = lane; j < half; j += 64) {
-        const float a = s_v[j], c = s_v[j + half];
-        const float x0 = a * cs[j] - c * sn[j], x1 = c * cs[j] + a * sn[j];
-        v[j] = x0;
-        v[j + half] = x1;
-        if (!is_q) {
-            float *kd = kc + ((size_t)(b - H) * max_ctx + pos) * hd;
-            kd[j] = x0;
-            kd[j + half] = x1;
-        }
-    }
-    if (!is_q) {
-        float *vd = vc + ((size_t)(b - H) * max_ctx + pos) * hd;
-        for (int i = lane; i < hd; i += 64) vd[i] = vx[(size_t)(b - H) * hd + i];
-    }
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float m = -INFINITY;
+    for (int i = 0; i < nw; i++) m = red[i] > m ? red[i] : m;
+    return m;
 }
 
-/* ---- attention core, one group per head (src/lib/tlm_model.c:683-719) --------
- * kc / vc: this layer's caches, head-major [KV][max_ctx][hd]; scores: H x
- * max_ctx floats of scratch.  The reference's order is kept: each score is
- * one thread's dot product in ascending i, and each output element one
- * thread's sum over positions in ascending t.  V goes through LDS in chunks
- * of ATT_TC positions (coalesced loads), so that ordered sum runs on LDS
- * reads instead of a global round trip per position. */
-constexpr int ATT_TC = 32;
-
-__global__ __launch_bounds__(NT) void k_attn(const float *__restrict__ q, const float *__restrict__ kc,
-                                             const float *__restrict__ vc, float *__restrict__ scores,
-                                             float *__restrict__ att, int H, int KV, int hd, int max_ctx,
-                                             const int32_t *__restrict__ st) {
-    __shared__ __align__(16) float s_q[256];
-    __shared__ __align__(16) float s_v[ATT_TC * 256];
+template <int HD, bool SPL>
+__global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, const float *__restrict__ kx,
+                                                   const float *__restrict__ vx, const float *__restrict__ q_norm,
+                                                   const float *__restrict__ k_norm, int has_qn, int has_kn,
+                                                   const float *__restrict__ cs_all, const float *__restrict__ sn_all,
+                                                   float *__restrict__ kc, float *__restrict__ vc,
+                                                   float *__restrict__ scores, float *__restrict__ att, int H,
+                                                   int KV, int max_ctx, const int32_t *__restrict__ st, float eps) {
+    constexpr int HALF = HD / 2, H4 = HD / 4;
+    constexpr int VC = (ATT_VF / HD) & ~(ATT_PU - 1);   /* V positions per chunk */
+    constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;     /* elements / pairs per lane */
+    constexpr bool KPRE = HD <= 128;
+    extern __shared__ __align__(16) float s_dyn[];
+    __shared__ __align__(16) float s_q[HD], s_k[HD], s_vn[HD];
+    __shared__ __align__(16) float s_v[ATT_VF];
     __shared__ double s_red[NT / 64];
     __shared__ float s_redf[NT / 64];
-    const int T = st[0] + 1;
-    const int h = blockIdx.x, tid = threadIdx.x, kvh = h / (H / KV);
-    const float *K = kc + (size_t)kvh * max_ctx * hd, *V = vc + (size_t)kvh * max_ctx * hd;
-    float *s = scores + (size_t)h * max_ctx;
-    for (int i = tid; i < hd; i += NT) s_q[i] = q[(size_t)h * hd + i];
-    __syncthreads();
-    const float scale = 1.0f / sqrtf((float)hd);
-    float mx = -INFINITY;
-    for (int t = tid; t < T; t += NT) {
-        const f32x4 *kt = (const f32x4 *)(K + (size_t)t * hd);   /* hd % 32 == 0: 16-byte rows */
-        float d = 0.0f;
-        for (int i4 = 0; i4 < hd / 4; i4++) {
-            const f32x4 k4 = kt[i4];
-            d += s_q[4 * i4] * k4.x;
-            d += s_q[4 * i4 + 1] * k4.y;
-            d += s_q[4 * i4 + 2] * k4.z;
-            d += s_q[4 * i4 + 3] * k4.w;
+    const int pos = st[0], T = pos + 1;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = h / (H / KV);
+    const float *K = kc + (size_t)kvh * max_ctx * HD, *V = vc + (size_t)kvh * max_ctx * HD;
+
+    /* 1. wave 0: the query head, wave 1: the key head, wave 2: the value
+     *    head (the others load the query head too and drop it) */
+    const float *hv = wave == 1 ? kx + (size_t)kvh * HD : wave == 2 ? vx + (size_t)kvh * HD : q + (size_t)h * HD;
+    const float *nwp = wave == 1 ? k_norm : q_norm;
+    float e[KE], nw[KE], cv[KH], sv[KH];
+#pragma unroll
+    for (int k = 0; k < KE; k++) e[k] = hv[min(lane + 64 * k, HD - 1)];
+#pragma unroll
+    for (int k = 0; k < KE; k++) nw[k] = nwp[min(lane + 64 * k, HD - 1)];
+#pragma unroll
+    for (int k = 0; k < KH; k++) {
+        cv[k] = cs_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
+        sv[k] = sn_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
+    }
+    /* 2. the first pass's key columns and the first V chunk */
+    float kr[KPRE ? HD : 1];
+    if constexpr (KPRE) {
+        const float *kt = K + min(tid, pos);
+#pragma unroll
+        for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
+    }
+    f32x4 pv[ATT_PF];
+    auto vload = [&](int t0) {
+        const int n4 = (T - t0 < VC ? T - t0 : VC) * H4;
+        const f32x4 *src = (const f32x4 *)(V + (size_t)t0 * HD);
+#pragma unroll
+        for (int j = 0; j < ATT_PF; j++) pv[j] = src[min(tid + NT * j, n4 - 1)];
+    };
+    vload(0);
+
+    /* norm (tlm_model.c:743-746) and RoPE (rope(), :721-728: pairs (j, j + HD/2)) */
+    if (wave < 3) {
+        float *v = wave == 0 ? s_q : wave == 1 ? s_k : s_vn;
+        if (wave < 2 && (wave == 0 ? has_qn : has_kn)) {
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < KE; k++)
+                if (lane + 64 * k < HD) ss += (double)e[k] * (double)e[k];
+            ss = wave_sum_f64(ss);
+            const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
+#pragma unroll
+            for (int k = 0; k < KE; k++) e[k] = e[k] * r * nw[k];
         }
-        d *= scale;   /* scale after the dot, before the max */
-        s[t] = d;
+#pragma unroll
+        for (int k = 0; k < KE; k++)
+            if (lane + 64 * k < HD) v[lane + 64 * k] = e[k];
+        if (wave < 2) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int k = 0; k < KH; k++) {
+                const int j = lane + 64 * k;
+                if (j < HALF) {
+                    const float a = v[j], c = v[j + HALF];
+                    v[j] = a * cv[k] - c * sv[k];
+                    v[j + HALF] = c * cv[k] + a * sv[k];
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    /* scores (scale after the dot, before the max) */
+    float *sp;
+    if constexpr (SPL) sp = s_dyn;
+    else sp = scores + (size_t)h * max_ctx;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float mx = -INFINITY;
+    const f32x4 *q4 = (const f32x4 *)s_q;
+    for (int t = tid; t < T; t += NT) {
+        float d = 0.0f;
+        if (KPRE && t < NT) {
+            if (t == pos) {   /* the new key, from this group's copy */
+#pragma unroll
+                for (int i4 = 0; i4 < H4; i4++) {
+                    const f32x4 k4 = ((const f32x4 *)s_k)[i4];
+                    kr[4 * i4] = k4.x;
+                    kr[4 * i4 + 1] = k4.y;
+                    kr[4 * i4 + 2] = k4.z;
+                    kr[4 * i4 + 3] = k4.w;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < HD / 16; c++) {   /* q in batches of 16 */
+                f32x4 qb[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) qb[u] = q4[4 * c + u];
+#pragma unroll
+                for (int u = 0; u < 16; u++) d += qb[u / 4][u % 4] * kr[16 * c + u];
+            }
+        } else if (t == pos) {
+#pragma unroll
+            for (int i = 0; i < HD; i++) d += s_q[i] * s_k[i];
+        } else {
+            const float *kt = K + t;
+#pragma unroll 16
+            for (int i = 0; i < HD; i++) d += s_q[i] * kt[(size_t)i * max_ctx];
+        }
+        d *= scale;
+        sp[t] = d;
         if (d > mx) mx = d;
     }
-    mx = block_max_f32(mx, s_redf);
+    mx = block_max_dpp(mx, s_redf);
     double sum = 0.0;
     for (int t = tid; t < T; t += NT) {
-        const float p = exp_rn(s[t] - mx);
-        s[t] = p;
+        const float p = exp_rn(sp[t] - mx);
+        sp[t] = p;
         sum += (double)p;
     }
     sum = block_sum_f64(sum, s_red);
     const float inv = (float)(1.0 / sum);
-    __syncthreads();   /* every p stored */
+    for (int t = tid; t < T; t += NT) sp[t] = sp[t] * inv;
+
+    /* P.V, chunk by chunk */
     float o = 0.0f;
-    for (int t0 = 0; t0 < T; t0 += ATT_TC) {
-        const int tn = T - t0 < ATT_TC ? T - t0 : ATT_TC;
-        const int n4 = tn * hd / 4;
-        for (int e = tid; e < n4; e += NT) ((f32x4 *)s_v)[e] = ((const f32x4 *)(V + (size_t)t0 * hd))[e];
-        __syncthreads();
-        if (tid < hd)
-            for (int t = 0; t < tn; t++) {
-                const float p = s[t0 + t] * inv;
-                o += p * s_v[t * hd + tid];
+    for (int t0 = 0; t0 < T; t0 += VC) {
+        const int tn = T - t0 < VC ? T - t0 : VC;
+#pragma unroll
+        for (int j = 0; j < ATT_PF; j++) {   /* registers -> LDS (whole buffer); row pos from this group's copy */
+            const int e4 = tid + NT * j;
+            const f32x4 nv = ((const f32x4 *)s_vn)[e4 % H4];
+            ((f32x4 *)s_v)[e4] = t0 + e4 / H4 == pos ? nv : pv[j];
+        }
+        __syncthreads();   /* every p stored (first pass) and the chunk in LDS */
+        if (t0 + VC < T) vload(t0 + VC);
+        if (tid < HD) {
+            const float *pc = sp + t0;   /* t0: a multiple of VC, itself of 16 */
+            const float *vcol = s_v + tid;
+            const int ng = (tn + ATT_PU - 1) / ATT_PU;
+#pragma unroll 1
+            for (int g = 0; g < ng; g++) {
+                f32x4 p4[ATT_PU / 4];
+                float vr[ATT_PU];
+                const float *pg = pc + g * ATT_PU;
+#pragma unroll
+                for (int u = 0; u < ATT_PU / 4; u++) {
+                    if constexpr (SPL) p4[u] = *(const f32x4 *)(pg + 4 * u);   /* LDS: 16-byte aligned */
+                    else p4[u] = f32x4{pg[4 * u], pg[4 * u + 1], pg[4 * u + 2], pg[4 * u + 3]};
+                }
+#pragma unroll
+                for (int u = 0; u < ATT_PU; u++) vr[u] = vcol[(g * ATT_PU + u) * HD];
+                if (g + 1 < ng) {
+#pragma unroll
+                    for (int u = 0; u < ATT_PU; u++) o += p4[u / 4][u % 4] * vr[u];
+                } else {
+                    const int lim = tn - g * ATT_PU;
+#pragma unroll
+                    for (int u = 0; u < ATT_PU; u++) {
+                        const float a = o + p4[u / 4][u % 4] * vr[u];
+                        o = u < lim ? a : o;
+                    }
+                }
             }
+        }
         __syncthreads();   /* the chunk is read before the next one overwrites it */
     }
-    if (tid < hd) att[(size_t)h * hd + tid] = o;
-}
-
-__global__ __launch_bounds__(NT) void k_add(float *__restrict__ h, const float *__restrict__ y, int n) {
-    const int i = blockIdx.x * NT + threadIdx.x;
-    if (i < n) h[i] += y[i];
-}
-
-/* greedy: the first maximum, NaN skipped, 0 if none (src/lib/tlm_model.c:1139-1146) */
-__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ l, int n, int32_t *__restrict__ seq,
-                                                 const int32_t *__restrict__ st) {
-    __shared__ float s_v[1024];
-    __shared__ int s_i[1024];
-    float bv = 0.0f;
-    int bi = -1;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float v = l[i];
-        if (v != v) continue;
-        if (bi < 0 || v > bv) {
-            bv = v;
-            bi = i;
+    if (tid < HD) att[(size_t)h * HD + tid] = o;
+    if (h % (H / KV) == 0)   /* the KV append, after the last barrier */
+        for (int i = tid; i < HD; i += NT) {
+            kc[((size_t)kvh * HD + i) * max_ctx + pos] = s_k[i];
+            vc[((size_t)kvh * max_ctx + pos) * HD + i] = s_vn[i];
         }
+}
+
+/* host: launch for the model's head width (a multiple of 32, at most 256) */
+int launch_attn(int hd, int H, int KV, int max_ctx, const float *q, const float *kx, const float *vx,
+                const float *q_norm, const float *k_norm, const float *cs, const float *sn, float *kc, float *vc,
+                float *scores, float *att, const int32_t *st, float eps, hipStream_t s) {
+    const bool spl = max_ctx <= ATT_LDS_POS;
+    const int has_qn = q_norm != nullptr, has_kn = k_norm != nullptr;
+    if (!q_norm) q_norm = q;   /* read (clamped) and dropped */
+    if (!k_norm) k_norm = q;
+    const size_t dyn = spl ? (size_t)(max_ctx + ATT_PU) * 4 : 0;   /* the last group reads whole */
+#define TLM_ATT(W)                                                                                                \
+    case W:                                                                                                       \
+        if (spl)                                                                                                  \
+            hipLaunchKernelGGL((k_attn_fused<W, true>), dim3(H), dim3(NT), dyn, s, q, kx, vx, q_norm, k_norm,     \
+                               has_qn, has_kn, cs, sn, kc, vc, scores, att, H, KV, max_ctx, st, eps);             \
+        else                                                                                                      \
+            hipLaunchKernelGGL((k_attn_fused<W, false>), dim3(H), dim3(NT), 0, s, q, kx, vx, q_norm, k_norm,      \
+                               has_qn, has_kn, cs, sn, kc, vc, scores, att, H, KV, max_ctx, st, eps);             \
+        break;
+    switch (hd) {
+        TLM_ATT(32) TLM_ATT(64) TLM_ATT(96) TLM_ATT(128) TLM_ATT(160) TLM_ATT(192) TLM_ATT(224) TLM_ATT(256)
+    default: return tlmh_seterr(TLM_HIP_EUNSUP, "model: head width %d", hd);
     }
-    s_v[threadIdx.x] = bv;
-    s_i[threadIdx.x] = bi;
-    __syncthreads();
-    for (int w = 512; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) {
-            const float ov = s_v[threadIdx.x + w];
-            const int oi = s_i[threadIdx.x + w];
-            const int mi = s_i[threadIdx.x];
-            if (oi >= 0 && (mi < 0 || ov > s_v[threadIdx.x] || (ov == s_v[threadIdx.x] && oi < mi))) {
-                s_v[threadIdx.x] = ov;
-                s_i[threadIdx.x] = oi;
-            }
+#undef TLM_ATT
+    return tlmh_check(hipGetLastError(), "model: attention");
+}
+
+/* end of a step: with the lm_head tiles' greedy keys (argmax_key of their
+ * rows), the maximum decodes to the reference's argmax (src/lib/tlm_model.c:
+ * 1139-1146: first maximum, NaN skipped, 0 if none), the next step's token,
+ * stored at seq[pos + 1]; the position advances. */
+__global__ __launch_bounds__(1024) void k_advance(int32_t *st, int32_t *seq, const unsigned long long *keys,
+                                                  int nkeys) {
+    __shared__ unsigned long long red[16];
+    const int pos = st[0];
+    if (keys) {
+        unsigned long long k = 0ull;
+        for (int i = threadIdx.x; i < nkeys; i += blockDim.x) k = keys[i] > k ? keys[i] : k;
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long other = __shfl_xor(k, o, 64);
+            k = other > k ? other : k;
         }
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
         __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w = 1; w < (int)(blockDim.x >> 6); w++) k = red[w] > k ? red[w] : k;
+            seq[pos + 1] = argmax_index(k);
+        }
     }
-    if (threadIdx.x == 0) seq[st[0] + 1] = s_i[0] < 0 ? 0 : s_i[0];   /* the next step's token */
-}
-
-__global__ void k_advance(int32_t *st) {
-    if (threadIdx.x == 0) st[0] += 1;
+    if (threadIdx.x == 0) st[0] = pos + 1;
 }
 
 struct DevMat {
@@ -266,10 +371,11 @@ struct tlm_hip_model {
     const float *out_norm = nullptr;
     DevMat lm_head;
     float *kc = nullptr, *vc = nullptr, *cs = nullptr, *sn = nullptr, *scores = nullptr;
-    float *h = nullptr, *xb = nullptr, *xb2 = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
+    float *h = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
     float *logits = nullptr;
-    uint8_t *act = nullptr, *act2 = nullptr, *moe_ws = nullptr;
+    uint8_t *moe_ws = nullptr;
     int32_t *st = nullptr, *seq = nullptr, *ids = nullptr;   /* st[0] = position; seq[max_ctx + 1] tokens */
+    unsigned long long *keys = nullptr;                      /* greedy key per lm_head tile */
     float *w = nullptr;
     int32_t *host_tok = nullptr;   /* pinned */
     hipGraphExec_t graph[2] = {nullptr, nullptr};   /* step without / with logits, captured at first use */
@@ -574,18 +680,13 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
     const size_t per = (size_t)g.n_layers * KV * (size_t)max_ctx * hd;
     M->kc = (float *)M->dalloc(per * 4);
     M->vc = (float *)M->dalloc(per * 4);
-    M->scores = (float *)M->dalloc((size_t)H * max_ctx * 4);
+    M->scores = (float *)M->dalloc(((size_t)H * max_ctx + 16) * 4);   /* attention reads a row in groups of 16 */
     M->h = (float *)M->dalloc((size_t)D * 4);
-    M->xb = (float *)M->dalloc((size_t)D * 4);
-    M->xb2 = (float *)M->dalloc((size_t)D * 4);
     M->q = (float *)M->dalloc((size_t)H * hd * 4);
     M->kx = (float *)M->dalloc((size_t)KV * hd * 4);
     M->vx = (float *)M->dalloc((size_t)KV * hd * 4);
     M->att = (float *)M->dalloc((size_t)H * hd * 4);
     M->logits = (float *)M->dalloc((size_t)g.vocab * 4);
-    const int64_t amax = D > H * hd ? D : H * hd;
-    M->act = (uint8_t *)M->dalloc(act_bytes(DT_Q8_K, amax) + act_bytes(DT_Q8_0, amax) + 64);
-    M->act2 = (uint8_t *)M->dalloc(act_bytes(DT_Q8_K, amax) + act_bytes(DT_Q8_0, amax) + 64);
     size_t ws = 0;
     for (const Layer &Ly : M->L) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
     M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
@@ -593,22 +694,16 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
     M->seq = (int32_t *)M->dalloc(((size_t)max_ctx + 1) * 4);
     M->ids = (int32_t *)M->dalloc(32 * 4);
     M->w = (float *)M->dalloc(32 * 4);
-    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->h, (void *)M->xb, (void *)M->xb2,
-                    (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits, (void *)M->act,
-                    (void *)M->act2, (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
-                    (void *)M->w})
+    M->keys = (unsigned long long *)M->dalloc(((size_t)g.vocab + TILE_ROWS - 1) / TILE_ROWS * 8);
+    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->h,
+                    (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
+                    (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
+                    (void *)M->w, (void *)M->keys})
         if (!p) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the KV cache / scratch");
     if ((rc = tlmh_check(hipHostMalloc((void **)&M->host_tok, 64, hipHostMallocDefault), "model: pinned scratch")))
         return rc;
     if ((rc = tlmh_check(hipMemset(M->st, 0, 16), "model: position"))) return rc;
     return tlmh_check(hipStreamSynchronize(M->stream), "model: load");
-}
-
-/* one matrix-vector job with the activation of x quantised for the matrix's kind */
-int matvec(tlm_hip_model *M, const DevMat &W, const float *x, uint8_t *act, float *y) {
-    int rc = launch_quantize_act(dt_act_kind(W.dt), x, W.n, act, M->stream);
-    if (!rc) rc = launch_matvec_packed(W.dt, W.p, W.rows, W.n, act, y, M->stream);
-    return rc;
 }
 
 /* tlm_model_step, src/lib/tlm_model.c:1058-1103, enqueued: the token is
@@ -624,38 +719,46 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
     int rc = tlmh_check(hipGetLastError(), "model: embed");
     for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
         const Layer &Ly = M->L[l];
-        /* attention(), tlm_model.c:730-763 */
-        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(NT), 0, s, (const float *)M->h, Ly.attn_norm, D, g.norm_eps,
-                           M->xb);
-        rc = launch_quantize_act(dt_act_kind(Ly.q.dt), M->xb, D, M->act, s);
-        if (!rc) rc = launch_matvec_packed(Ly.q.dt, Ly.q.p, Ly.q.rows, Ly.q.n, M->act, M->q, s);
-        if (!rc) rc = launch_matvec_packed(Ly.k.dt, Ly.k.p, Ly.k.rows, Ly.k.n, M->act, M->kx, s);
-        if (!rc) rc = launch_matvec_packed(Ly.v.dt, Ly.v.p, Ly.v.rows, Ly.v.n, M->act, M->vx, s);
+        /* attention(), tlm_model.c:730-763: q | k | v in one launch whose
+         * groups each normalise and quantise h themselves, the fused head
+         * kernel, o added into h */
+        const MvNorm an{M->h, Ly.attn_norm, g.norm_eps};
+        const void *W3[3] = {Ly.q.p, Ly.k.p, Ly.v.p};
+        const int64_t R3[3] = {Ly.q.rows, Ly.k.rows, Ly.v.rows};
+        float *const Y3[3] = {M->q, M->kx, M->vx};
+        if (Ly.q.dt == Ly.k.dt && Ly.q.dt == Ly.v.dt) {
+            rc = launch_mv_segs(Ly.q.dt, D, W3, R3, Y3, 3, 0, nullptr, s, &an);
+        } else {
+            for (int m = 0; m < 3 && !rc; m++) {
+                const DevMat &Wm = m == 0 ? Ly.q : m == 1 ? Ly.k : Ly.v;
+                rc = launch_mv_segs(Wm.dt, D, &W3[m], &R3[m], &Y3[m], 1, 0, nullptr, s, &an);
+            }
+        }
         if (rc) break;
         const size_t lbase = (size_t)l * KV * M->max_ctx * hd;
-        hipLaunchKernelGGL(k_qk_rope, dim3(H + KV), dim3(64), 0, s, M->q, M->kx, (const float *)M->vx, Ly.q_norm,
-                           Ly.k_norm, (const float *)M->cs, (const float *)M->sn, M->kc + lbase, M->vc + lbase, H,
-                           hd, (const int32_t *)M->st, M->max_ctx, g.norm_eps);
-        hipLaunchKernelGGL(k_attn, dim3(H), dim3(NT), 0, s, (const float *)M->q, (const float *)(M->kc + lbase),
-                           (const float *)(M->vc + lbase), M->scores, M->att, H, KV, hd, M->max_ctx,
-                           (const int32_t *)M->st);
-        rc = tlmh_check(hipGetLastError(), "model: attention");
-        if (!rc) rc = matvec(M, Ly.o, M->att, M->act2, M->xb2);
-        if (rc) break;
-        hipLaunchKernelGGL(k_add, dim3((D + NT - 1) / NT), dim3(NT), 0, s, M->h, (const float *)M->xb2, D);
+        rc = launch_attn(hd, H, KV, M->max_ctx, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm, M->cs, M->sn,
+                         M->kc + lbase, M->vc + lbase, M->scores, M->att, (const int32_t *)M->st, g.norm_eps, s);
+        /* o: every group quantises the attention output itself */
+        const MvNorm ao{M->att, nullptr, 0.0f};
+        const void *Wo = Ly.o.p;
+        const int64_t Ro = Ly.o.rows;
+        float *const Yo = M->h;
+        if (!rc) rc = launch_mv_segs(Ly.o.dt, (int64_t)H * hd, &Wo, &Ro, &Yo, 1, 1, nullptr, s, &ao);
         /* moe(), tlm_model.c:940-1055 */
-        rc = launch_moe_layer(&Ly.moe, M->h, M->ids, M->w, M->moe_ws, s);
+        if (!rc) rc = launch_moe_layer(&Ly.moe, M->h, M->ids, M->w, M->moe_ws, s);
     }
     if (rc) return rc;
-    if (want_logits) {   /* tlm_model.c:1087-1095, then the greedy argmax */
-        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(NT), 0, s, (const float *)M->h, M->out_norm, D, g.norm_eps,
-                           M->xb);
-        rc = matvec(M, M->lm_head, M->xb, M->act, M->logits);
+    const int nkeys = (int)((g.vocab + TILE_ROWS - 1) / TILE_ROWS);
+    if (want_logits) {   /* tlm_model.c:1087-1095 (norm in the lm_head's groups), the greedy key */
+        const MvNorm on{M->h, M->out_norm, g.norm_eps};
+        const void *Wl = M->lm_head.p;
+        const int64_t Rl = M->lm_head.rows;
+        float *const Yl = M->logits;
+        rc = launch_mv_segs(M->lm_head.dt, D, &Wl, &Rl, &Yl, 1, 0, nullptr, s, &on, M->keys);
         if (rc) return rc;
-        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, (const float *)M->logits, (int)g.vocab, M->seq,
-                           (const int32_t *)M->st);
     }
-    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, M->st);
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(want_logits ? 1024 : 64), 0, s, M->st, M->seq,
+                       want_logits ? (const unsigned long long *)M->keys : nullptr, nkeys);
     return tlmh_check(hipGetLastError(), "model: step");
 }
 

@@ -145,6 +145,40 @@ int launch_pack(int dt, const void *src, size_t row_bytes, int64_t rows, int64_t
 int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, float *y,
                          hipStream_t s);
 int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s);
+/* up to MV_SEGS packed matrices of one dtype and width n in one launch, one
+ * shared activation; accum: y += W x.  With nx set, every group computes the
+ * activation itself, quantising rmsnorm(nx) * nw (eps), or nx itself when nw
+ * is null, instead of reading act; with
+ * keys set (one segment), group t also stores the greedy key of its rows
+ * (the maximum of argmax_key) at keys[t]. */
+#define MV_SEGS 4
+struct MvSegs {
+    const uint8_t *W[MV_SEGS];
+    int64_t rows[MV_SEGS], tile_end[MV_SEGS];
+    float *y[MV_SEGS];
+    const float *nx, *nw;
+    unsigned long long *keys;
+    float eps;
+    int n, accum;
+};
+struct MvNorm {
+    const float *x, *w;
+    float eps;
+};
+int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows, float *const *y, int nseg, int accum,
+                   const void *act, hipStream_t s, const MvNorm *norm = nullptr, unsigned long long *keys = nullptr);
+/* greedy key of logit v at index i: larger value first, then lower index; 0
+ * for NaN (skipped), so the maximum over a vector decodes to the reference's
+ * argmax (first maximum, NaN skipped, 0 if none) - argmax_index */
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t i) {
+    if (v != v) return 0ull;
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);   /* -0 == +0 */
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - i);
+}
+__host__ __device__ inline int argmax_index(unsigned long long key) {
+    return key ? (int)(0xFFFFFFFFu - (uint32_t)key) : 0;
+}
 size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T);
 int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
                        hipStream_t s);
