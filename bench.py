@@ -206,43 +206,16 @@ C1_STORE = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
 C1_TIERLM = os.path.join(ROOT, "oracle", "_ref", "bin", "tierlm")
 
 
-def c1_prompt():
-    x, out, m = 42, [], (1 << 64) - 1
-    for _ in range(64):
-        x ^= (x << 13) & m
-        x ^= x >> 7
-        x ^= (x << 17) & m
-        out.append(x % 4096)
-    return out
-
-
 def c1_bench(reps):
     """The whole decode step on the 4-layer synthetic model (the reference's
     compiled store, oracle/make_c1.sh): 64-token prompt, 64 greedy tokens, as
     `tierlm bench --prompt-len 64 -n 64`; decode tok/s = 63 / decode time.
     Beside it the reference's own runtime on the host cores, same store."""
     import subprocess
-    from tierlm_amd.model import Model
-    m = Model(C1_STORE, max_ctx=256)
-    prompt = c1_prompt()
-    m.reset()
-    m.generate(prompt, 64)                        # warm
-    pre = dec = None
-    for _ in range(reps):
-        m.reset()
-        t0 = time.perf_counter()
-        m.generate(prompt, 1)
-        t1 = time.perf_counter()
-        m.reset()
-        t2 = time.perf_counter()
-        toks = m.generate(prompt, 64)
-        t3 = time.perf_counter()
-        p, d = t1 - t0, (t3 - t2) - (t1 - t0)
-        pre = p if pre is None else min(pre, p)
-        dec = d if dec is None else min(dec, d)
-    m.close()
-    out = {"prefill_tok_s": round(64 / pre, 1), "decode_tok_s": round(63 / dec, 1),
-           "decode_us_per_token": round(dec / 63 * 1e6, 1), "tokens_head": toks[:4],
+    from tierlm_amd.model import bench as model_bench
+    r = model_bench(C1_STORE, 64, 64, reps, max_ctx=256)
+    out = {"prefill_tok_s": r["prefill_tok_s"], "decode_tok_s": r["decode_tok_s"],
+           "decode_us_per_token": r["decode_us_per_token"], "tokens_head": r["tokens"][:4],
            "timing": "host wall clock around tlm_hip_model_generate (prefill 64, then 63 decode steps), best of "
                      f"{reps}; each step one replay of a captured HIP graph"}
     if os.path.exists(C1_TIERLM):

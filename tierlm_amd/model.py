@@ -1,7 +1,14 @@
 """The whole decode step on the device (tlm_hip_model_*; the reference's
 tlm_model_step / tlm_model_prefill, src/lib/tlm_model.c:1058-1113) for a
-compiled store, through ctypes.  Computes nothing itself."""
+compiled store, through ctypes.  Computes nothing itself.
+
+    python -m tierlm_amd.model STORE.tlmm [--prompt-len 64] [-n 64] [--eager]
+
+times the device the way `tierlm bench` times the host runtime
+(src/bin/tierlm.c:702-735): a pseudo-random prompt, prefill, then greedy
+tokens; decode tok/s = (n - 1) / decode time."""
 import ctypes as C
+import time
 
 import numpy as np
 
@@ -50,3 +57,61 @@ class Model:
         out = (C.c_int32 * max(n, 1))()
         check(lib.tlm_hip_model_generate(self.h, p, len(prompt), n, out))
         return list(out[:n])
+
+
+def bench_prompt(n, vocab, seed=42):
+    """tierlm bench's prompt: xorshift64 from the seed, each token mod vocab
+    (src/bin/tierlm.c:711-715)."""
+    x, out, m = seed, [], (1 << 64) - 1
+    for _ in range(n):
+        x ^= (x << 13) & m
+        x ^= x >> 7
+        x ^= (x << 17) & m
+        out.append(x % vocab)
+    return out
+
+
+def bench(path, prompt_len=64, n=64, reps=3, eager=False, max_ctx=0):
+    """Best of reps: prefill time (generate(prompt, 1)) and decode time (the
+    n - 1 further steps of generate(prompt, n)), host wall clock around the
+    calls; tokens stay on the device between steps."""
+    m = Model(path, max_ctx=max_ctx or prompt_len + n + 1, eager=eager)
+    try:
+        prompt = bench_prompt(prompt_len, m.geom.vocab)
+        m.reset()
+        toks = m.generate(prompt, n)            # warm (and graph capture)
+        pre = dec = None
+        for _ in range(reps):
+            m.reset()
+            t0 = time.perf_counter()
+            m.generate(prompt, 1)
+            t1 = time.perf_counter()
+            m.reset()
+            t2 = time.perf_counter()
+            toks = m.generate(prompt, n)
+            t3 = time.perf_counter()
+            p, d = t1 - t0, (t3 - t2) - (t1 - t0)
+            pre = p if pre is None else min(pre, p)
+            dec = d if dec is None else min(dec, d)
+    finally:
+        m.close()
+    return {"prefill_tok_s": round(prompt_len / pre, 1), "decode_tok_s": round((n - 1) / dec, 1),
+            "decode_us_per_token": round(dec / (n - 1) * 1e6, 1), "tokens": toks}
+
+
+if __name__ == "__main__":
+    import argparse
+
+    from .quant import init
+    ap = argparse.ArgumentParser(prog="python -m tierlm_amd.model")
+    ap.add_argument("store")
+    ap.add_argument("--prompt-len", type=int, default=64)
+    ap.add_argument("-n", type=int, default=64)
+    ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--eager", action="store_true", help="launch kernels directly instead of replaying a graph")
+    a = ap.parse_args()
+    init(0)
+    r = bench(a.store, a.prompt_len, a.n, a.reps, a.eager)
+    print(f"bench {a.store}: prompt {a.prompt_len} tokens ({r['prefill_tok_s']:.1f} tok/s), decode {a.n} tokens "
+          f"({r['decode_tok_s']:.1f} tok/s, {r['decode_us_per_token']:.1f} us/token){' eager' if a.eager else ''}",
+          flush=True)
