@@ -256,8 +256,8 @@ __device__ __attribute__((noinline)) void quant16_to_ool(int kind, f32x4 v0, f32
  * larger keys) is its position in the reference's top-k; ranks 0..k-1 are
  * written directly.  With fewer than k valid entries the reference's fallback
  * (lowest unmasked unused index, else 0) fills the remaining ranks. */
-struct RouteLds {
-    unsigned long long key[MAXE];
+struct __align__(16) RouteLds {
+    unsigned long long key[MAXE];   /* entries t >= E hold 0 (never larger) */
     float p[MAXE];
     int cnt[MAXE];
     double red[NWAVE];
@@ -272,11 +272,14 @@ __device__ __forceinline__ uint32_t ord_bits(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-/* ids / weights land in R->ids[0..k), R->w[0..k), readable by every thread.
- * stash() runs in every thread before a group barrier, once the softmax is
- * done: a place for LDS writes of values loaded at kernel entry. */
+/* ids land in R->ids[0..k) and, with weights, the renormalised weights in
+ * R->w[0..k), readable by every thread (without weights R->w holds the
+ * unnormalised probabilities).  stash() runs in every thread before a group
+ * barrier, once the softmax is done: a place for LDS writes of values loaded
+ * at kernel entry. */
 template <class Stash>
-__device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, LAS RouteLds *R, Stash stash) {
+__device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, LAS RouteLds *R, Stash stash,
+                            bool weights = true) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, E = d.E, k = d.k;
     const bool sig = d.router == 2;
     const bool in = t < E;
@@ -313,15 +316,27 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
     if (lane == 0) R->redi[wave] = nv_wave;
     __syncthreads();
     const int nvalid = (R->redi[0] + R->redi[1]) + (R->redi[2] + R->redi[3]);
-    /* rank = #larger keys; with E <= 128 two threads split the scan of one entry */
+    /* rank = #larger keys; with E <= 128 two threads split the scan of one
+     * entry, each over a fixed 64 entries (two keys per 16-byte read; the
+     * zero keys past E never count) */
     const bool split = E <= 128;
-    const int e = split ? (t & 127) : t, hE = (E + 1) >> 1;
-    const int f0 = (split && t >= 128) ? hE : 0, f1 = (split && t < 128) ? hE : E;
+    const int e = split ? (t & 127) : t;
     const unsigned long long ke = e < E ? R->key[e] : 0ull;
     int c = 0;
     if (ke != 0ull) {
+        if (split) {
+            const LAS u32x4 *kp = (const LAS u32x4 *)(R->key + (t >= 128 ? 64 : 0));
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                const u32x4 w = kp[j];
+                const unsigned long long a = ((unsigned long long)w.y << 32) | w.x;
+                const unsigned long long b = ((unsigned long long)w.w << 32) | w.z;
+                c += (a > ke ? 1 : 0) + (b > ke ? 1 : 0);
+            }
+        } else {
 #pragma unroll 16
-        for (int f = f0; f < f1; f++) c += R->key[f] > ke ? 1 : 0;
+            for (int f = 0; f < E; f++) c += R->key[f] > ke ? 1 : 0;
+        }
     }
     R->cnt[t] = c;
     __syncthreads();
@@ -330,7 +345,8 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
         if (rank < k) { R->ids[rank] = t; R->w[rank] = p; }
     }
     __syncthreads();
-    if (wave == 0) {
+    if (nvalid < k || weights) {   /* uniform over the group */
+      if (wave == 0) {
         if (nvalid < k) {
             if (lane == 0)
                 for (int r = nvalid; r < k; r++) {
@@ -347,17 +363,19 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
                 }
             wave_sync();
         }
-        /* renormalise in rank order (double sum), then scale */
-        float wr = lane < k ? R->w[lane] : 0.0f;
-        if (d.router != 1) {
-            double s = 0.0;
-            for (int r = 0; r < k; r++) s += (double)rdlane_f32(wr, r);
-            if (sig || s > 0.0) wr *= (float)(1.0 / (sig ? s + 1e-20 : s));
+        if (weights) {   /* renormalise in rank order (double sum), then scale */
+            float wr = lane < k ? R->w[lane] : 0.0f;
+            if (d.router != 1) {
+                double s = 0.0;
+                for (int r = 0; r < k; r++) s += (double)rdlane_f32(wr, r);
+                if (sig || s > 0.0) wr *= (float)(1.0 / (sig ? s + 1e-20 : s));
+            }
+            if (sig || d.routed_scale != 1.0f) wr *= d.routed_scale;
+            if (lane < k) R->w[lane] = wr;
         }
-        if (sig || d.routed_scale != 1.0f) wr *= d.routed_scale;
-        if (lane < k) R->w[lane] = wr;
+      }
+      __syncthreads();
     }
-    __syncthreads();
 }
 
 /* ======================================================================
@@ -677,10 +695,15 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
     const GAS uint64_t *xt = (const GAS uint64_t *)d.experts;
     const uint8_t *tg = tid < d.E ? (const uint8_t *)xt[3 * tid + 0] : nullptr;
     const uint8_t *tu = tid < d.E ? (const uint8_t *)xt[3 * tid + 1] : nullptr;
-    route_group(d, (const GAS float *)(ws + L.logits), R, [&]() {
-        s_gate[tid] = tg;
-        s_up[tid] = tu;
-    });
+    /* only group 0 publishes the weights (for the down launch); the others
+     * need their expert's id alone */
+    route_group(
+        d, (const GAS float *)(ws + L.logits), R,
+        [&]() {
+            s_gate[tid] = tg;
+            s_up[tid] = tu;
+        },
+        blockIdx.x == 0);
     if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
         const int q = threadIdx.x;
         ws_ids(ws, L)[q] = R->ids[q];
