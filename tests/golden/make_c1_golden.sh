@@ -5,6 +5,10 @@
 #                   xorshift(42) prompt (tierlm run --print-tokens)
 #   c1_oracle.jsonl its top-10 logits at every position of prompt + the first
 #                   63 greedy tokens, teacher-forced (tierlm oracle)
+#   c1_greedy_long.txt  320 greedy tokens after the same prompt (positions up
+#                   to 383: several attention chunks and score passes)
+#   c1_oracle_long.jsonl  top-10 logits at every position of prompt + the
+#                   first 319 of those tokens, teacher-forced
 # Run here, where the reference's tools are built; the fixtures are data.
 set -e
 HERE=$(cd "$(dirname "$0")" && pwd)
@@ -22,3 +26,6 @@ print(','.join(map(str, out)))")
 echo "f2fb519981d61a8626b130207ac434f1  $HERE/c1_greedy.txt" | md5sum -c -
 GEN=$(tr ' ' ',' < "$HERE/c1_greedy.txt" | cut -d, -f1-63)
 "$B/tierlm" oracle "$C1/c1.tlmm" --tokens "$PROMPT,$GEN" --cache 1G 2>/dev/null > "$HERE/c1_oracle.jsonl"
+"$B/tierlm" run "$C1/c1.tlmm" --tokens "$PROMPT" -n 320 --print-tokens --cache 1G 2>/dev/null > "$HERE/c1_greedy_long.txt"
+GENL=$(tr ' ' ',' < "$HERE/c1_greedy_long.txt" | cut -d, -f1-319)
+"$B/tierlm" oracle "$C1/c1.tlmm" --tokens "$PROMPT,$GENL" --cache 1G 2>/dev/null > "$HERE/c1_oracle_long.jsonl"

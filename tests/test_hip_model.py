@@ -1,16 +1,26 @@
-"""The whole decode step on the device (tlm_hip_model_*) on the 4-layer
-synthetic model as the reference's own compiler writes it (oracle/make_c1.sh:
-D 512, 8/2 heads x 64, 32 experts top-4 Q6_K, Q8_0 dense, f32 router, one
-shared expert, vocabulary 4096), against the reference's own runtime on the
-same store (tests/golden/make_c1_golden.sh):
+"""The whole decode step on the device (tlm_hip_model_*) on synthetic models
+as the reference's own compiler writes them, against the reference's own
+runtime on the same stores:
 
+* C1 (oracle/make_c1.sh, tests/golden/make_c1_golden.sh): D 512, 8/2 heads x
+  64, qk-norm, 32 experts top-4 Q6_K, softmax router, one shared expert, Q8_0
+  dense, vocabulary 4096;
+* C2S (oracle/make_c2s.sh, tests/golden/make_c2s_golden.sh): D 256, 4/2 heads
+  x 128, no qk-norm, YaRN RoPE, 16 experts top-2 Q4_K under the sigmoid
+  router (selection bias, routed scale 2.5), no shared expert, vocabulary
+  2048.
+
+Checks:
 * teacher-forced, every position of prompt + generated tokens: the top-10
   logits of `tierlm oracle` (ids identical, values within 1e-5 relative; most
   are bit-identical - the integer paths are exact and the rest runs in the
   reference's order);
-* free-running greedy decode of 64 tokens after the 64-token xorshift(42)
-  prompt: the reference's tokens exactly (`tierlm run --print-tokens`,
-  md5 f2fb5199...)."""
+* free-running greedy decode after the 64-token xorshift(42) prompt: the
+  reference's tokens exactly (`tierlm run --print-tokens`; C1's 64 tokens
+  md5 f2fb5199...);
+* C1 over 383 positions (320 greedy tokens), with the probabilities in LDS
+  (max_ctx 512) and in global scratch (max_ctx 5000): several V chunks and a
+  second score pass, teacher-forced and free-running."""
 import json
 import os
 
@@ -21,22 +31,49 @@ pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 C1 = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
+C2S = os.path.join(ROOT, "oracle", "_ref", "c2s", "c2s.tlmm")
 GOLD = os.path.join(ROOT, "tests", "golden")
 needs_c1 = pytest.mark.skipif(not os.path.exists(C1), reason="oracle/_ref/c1 not built (oracle/make_c1.sh)")
+needs_c2s = pytest.mark.skipif(not os.path.exists(C2S), reason="oracle/_ref/c2s not built (oracle/make_c2s.sh)")
 
 
-def prompt_tokens():
+def prompt_tokens(vocab=4096):
     x, out, m = 42, [], (1 << 64) - 1
     for _ in range(64):   # src/bin/tierlm.c:711-715
         x ^= (x << 13) & m
         x ^= x >> 7
         x ^= (x << 17) & m
-        out.append(x % 4096)
+        out.append(x % vocab)
     return out
 
 
-def greedy_tokens():
-    return [int(t) for t in open(os.path.join(GOLD, "c1_greedy.txt")).read().split()]
+def greedy_tokens(name="c1_greedy.txt"):
+    return [int(t) for t in open(os.path.join(GOLD, name)).read().split()]
+
+
+def teacher_forced(model, oracle_file, tokens):
+    """Step through tokens; at every position the top-10 ids must be the
+    reference's and each value within 1e-5 relative; returns (bit-identical
+    count, total)."""
+    oracle_rows = [json.loads(line) for line in open(os.path.join(GOLD, oracle_file))]
+    assert len(oracle_rows) == len(tokens)
+    model.reset()
+    exact = total = 0
+    worst = 0.0
+    for pos, tok in enumerate(tokens):
+        lg, nxt = model.step(tok)
+        want = oracle_rows[pos]["topk"]
+        got_ids = np.argsort(-lg, kind="stable")[:10]
+        assert [int(i) for i in got_ids] == [w[0] for w in want], f"pos {pos}"
+        for wid, wv in want:
+            wv = np.float32(wv)
+            d = abs(float(lg[wid]) - float(wv))
+            assert d <= 1e-5 * max(1.0, abs(float(wv))), f"pos {pos} id {wid}: {lg[wid]!r} vs {wv!r}"
+            exact += lg[wid] == wv
+            worst = max(worst, d)
+            total += 1
+        assert nxt == want[0][0]
+    return exact, total, worst
 
 
 @pytest.fixture(scope="module")
@@ -49,26 +86,48 @@ def c1(hip):
 
 @needs_c1
 def test_c1_teacher_forced_top10_logits(c1):
-    oracle_rows = [json.loads(line) for line in open(os.path.join(GOLD, "c1_oracle.jsonl"))]
     tokens = prompt_tokens() + greedy_tokens()[:63]
-    assert len(oracle_rows) == len(tokens) == 127
-    c1.reset()
-    exact = worst = 0
-    total = 0
-    for pos, tok in enumerate(tokens):
-        lg, nxt = c1.step(tok)
-        want = oracle_rows[pos]["topk"]
-        got_ids = np.argsort(-lg, kind="stable")[:10]
-        assert [int(i) for i in got_ids] == [w[0] for w in want], f"pos {pos}"
-        for wid, wv in want:
-            wv = np.float32(wv)
-            d = abs(float(lg[wid]) - float(wv))
-            assert d <= 1e-5 * max(1.0, abs(float(wv))), f"pos {pos} id {wid}: {lg[wid]!r} vs {wv!r}"
-            exact += lg[wid] == wv
-            worst = max(worst, d)
-            total += 1
-        assert nxt == want[0][0]
+    assert len(tokens) == 127
+    exact, total, worst = teacher_forced(c1, "c1_oracle.jsonl", tokens)
     assert exact >= total // 2, f"only {exact} of {total} top-10 logits bit-identical (worst {worst:.3g})"
+
+
+@needs_c1
+@pytest.mark.parametrize("max_ctx", [512, 5000])
+def test_c1_long_context(hip, max_ctx):
+    """383 positions: with HD 64 a V chunk holds 128 positions and a score
+    pass 256, so this runs 3 chunks and 2 passes; max_ctx 5000 keeps the
+    probabilities in global scratch instead of LDS."""
+    from tierlm_amd.model import Model
+    m = Model(C1, max_ctx=max_ctx)
+    try:
+        gen = greedy_tokens("c1_greedy_long.txt")
+        assert len(gen) == 320
+        exact, total, worst = teacher_forced(m, "c1_oracle_long.jsonl", prompt_tokens() + gen[:319])
+        assert exact >= total // 2, f"only {exact} of {total} top-10 logits bit-identical (worst {worst:.3g})"
+        m.reset()
+        assert m.generate(prompt_tokens(), 320) == gen
+        assert m.kv_len() == 64 + 319
+    finally:
+        m.close()
+
+
+@needs_c2s
+def test_c2s_teacher_forced_and_greedy(hip):
+    """Head width 128, no qk-norm, YaRN, sigmoid routing with bias and
+    routed scale, Q4_K experts, no shared expert."""
+    from tierlm_amd.model import Model
+    m = Model(C2S, max_ctx=256)
+    try:
+        g = m.geom
+        assert (g.head_dim, g.n_heads, g.n_kv_heads, g.top_k, g.n_shared, g.vocab) == (128, 4, 2, 2, 0, 2048)
+        gen = greedy_tokens("c2s_greedy.txt")
+        exact, total, worst = teacher_forced(m, "c2s_oracle.jsonl", prompt_tokens(2048) + gen[:63])
+        assert exact >= total // 2, f"only {exact} of {total} top-10 logits bit-identical (worst {worst:.3g})"
+        m.reset()
+        assert m.generate(prompt_tokens(2048), 64) == gen
+    finally:
+        m.close()
 
 
 @needs_c1
