@@ -380,6 +380,22 @@ const tlm_hip_model_geom *tlm_hip_model_geom_of(const tlm_hip_model *M);
 int  tlm_hip_model_kv_len(const tlm_hip_model *M);
 int  tlm_hip_model_kv_capacity(const tlm_hip_model *M);
 void tlm_hip_model_reset(tlm_hip_model *M);   /* tlm_kv_reset */
+/* A random-init model of geometry g built directly in HBM, for measuring the
+ * decode step at shapes whose compiled stores are too large to write or ship
+ * (the role `tlmc synth` + `tlmc compile` play for the reference,
+ * src/bin/tlmc.c:270-330): block bytes from a counter-based hash of seed with
+ * finite scale fields, weights of about the spread of N(0, 0.02); norms 1;
+ * router f32 of variance 1/d_model; embedding and lm_head as dense_dt / Q8_0.
+ * Its outputs are not the reference synthesiser's: parity is established on
+ * compiled stores (tlm_hip_model_open).  Needs tlm_hip_init. */
+typedef struct {
+    int32_t  expert_dt, dense_dt;   /* Q4_K, Q5_K, Q6_K or Q8_0 (dtype codes above) */
+    int32_t  qk_norm;               /* 1: q_norm / k_norm present */
+    int32_t  reserved;
+    uint64_t seed;
+} tlm_hip_model_synth_opts;
+int  tlm_hip_model_synth(const tlm_hip_model_geom *g, const tlm_hip_model_synth_opts *so,
+                         const tlm_hip_model_opts *o, tlm_hip_model **out);
 /* tlm_model_step: logits (host, vocab floats) and next (the greedy token)
  * may each be NULL. */
 int  tlm_hip_model_step(tlm_hip_model *M, int token, float *logits, int32_t *next);

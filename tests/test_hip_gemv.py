@@ -147,11 +147,11 @@ def test_matvec_tiles_ranges(hip, dev, dt):
 
 
 @pytest.mark.parametrize("dt", INT)
-@pytest.mark.parametrize("rows,n", [(16, 256), (48, 512), (37, 768), (768, 2048), (2048, 768), (100, 4096)])
+@pytest.mark.parametrize("rows,n", [(16, 256), (48, 512), (37, 768), (768, 2048), (2048, 768), (100, 4096),
+                                    (64, 8192)])
 def test_matvec_packed(hip, dev, dt, rows, n):
-    """Packed tile layout == oracle, including a partial last tile."""
-    if dt == oracle.Q8_0 and n > 4096:
-        pytest.skip("staged activation limit")
+    """Packed tile layout == oracle, including a partial last tile and rows
+    longer than one chunk of blocks (Q8_0: 128 blocks, others 64)."""
     rng = np.random.default_rng(rows * 31 + n + dt)
     W = random_code_rows(rng, dt, rows, n)
     if rows <= 64:

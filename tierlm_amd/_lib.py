@@ -87,6 +87,12 @@ class ModelGeom(C.Structure):
         ("rope_beta_fast", C.c_float), ("rope_beta_slow", C.c_float), ("rope_orig_len", C.c_uint32)]
 
 
+class ModelSynthOpts(C.Structure):
+    """tlm_hip_model_synth_opts"""
+    _fields_ = [("expert_dt", C.c_int32), ("dense_dt", C.c_int32), ("qk_norm", C.c_int32), ("reserved", C.c_int32),
+                ("seed", C.c_uint64)]
+
+
 class TensorRef(C.Structure):
     """tlm_hip_tensor_ref"""
     _fields_ = [("name", C.c_char * 48), ("dtype", C.c_uint32), ("ndim", C.c_uint32), ("shape", C.c_uint64 * 2),
@@ -154,6 +160,7 @@ _SIGS = {
     "tlm_hip_packet_header": (i32, [vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     "tlm_hip_dir_find": (i32, [vp, C.c_uint64, C.c_char_p, C.POINTER(TensorRef)]),
     "tlm_hip_model_open": (i32, [C.c_char_p, vp, C.POINTER(vp)]),
+    "tlm_hip_model_synth": (i32, [C.POINTER(ModelGeom), C.POINTER(ModelSynthOpts), vp, C.POINTER(vp)]),
     "tlm_hip_model_close": (None, [vp]),
     "tlm_hip_model_geom_of": (C.POINTER(ModelGeom), [vp]),
     "tlm_hip_model_kv_len": (i32, [vp]),

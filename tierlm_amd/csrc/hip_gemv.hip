@@ -266,19 +266,34 @@ __global__ void k_pack_f32(const uint8_t *__restrict__ src, size_t row_bytes, in
  * LDS stays bounded for long rows.  Per chunk every wave computes items
  * (b, i) with LPI lanes each and parks (isum, msum, dA, dM) in LDS; then 16
  * threads extend their row's float chain over the chunk in block order.
- * The activation is staged once per work-group (all blocks). */
-#define PK_NBC 64
+ * The activation is staged once per work-group (all blocks).  Items in
+ * flight per lane (IPL) and blocks per chunk (NBC): a round of loads costs
+ * one memory latency, so for wide Q8_0 rows (DEEP: at least 64 blocks) a
+ * lane (5 registers per item) keeps 16 in flight, branch-free, and a chunk
+ * of 128 blocks is one round - a 16-row tile of up to 4096 columns streams in
+ * a single latency; narrower rows keep 4 per lane (a deep round would be
+ * mostly dropped items). */
+template <int DT, bool DEEP> struct MvCfg {
+    static constexpr int IPL = 4, NBC = 64;
+    static constexpr bool CLAMP = false;
+};
+template <> struct MvCfg<DT_Q8_0, true> {
+    static constexpr int IPL = 16, NBC = 128;
+    static constexpr bool CLAMP = true;
+};
+static bool mv_deep(int dt, int nb) { return dt == DT_Q8_0 && nb >= 64; }
+static int mv_nbc(int dt, int nb) { return mv_deep(dt, nb) ? MvCfg<DT_Q8_0, true>::NBC : MvCfg<DT_Q6_K, false>::NBC; }
 
-template <int DT>
+template <int DT, bool DEEP>
 __global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ Wp, int64_t rows, int nb,
                                                    const uint8_t *__restrict__ act, float *__restrict__ y) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    constexpr int IPL = 4;                                  /* items in flight per lane */
+    constexpr int IPL = MvCfg<DT, DEEP>::IPL;                     /* items in flight per lane */
     extern __shared__ __align__(16) uint8_t lds[];
     const int kind = dt_act_kind(DT);
     const XLds X = stage_act(kind, act, nb, lds);
-    const int cap = nb < PK_NBC ? nb : PK_NBC;
+    const int cap = nb < MvCfg<DT, DEEP>::NBC ? nb : MvCfg<DT, DEEP>::NBC;
     const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * TILE_ROWS);
     __syncthreads();
 
@@ -298,16 +313,10 @@ __global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ W
                 u = ((int64_t)t * nb + b) * TILE_ROWS + i;
                 pk = g;
             };
-            run_items<DT, IPL>(nitems - base, map, [&]() { return X; }, park);
+            run_items<DT, IPL, MvCfg<DT, DEEP>::CLAMP>(nitems - base, map, [&]() { return X; }, park);
         }
         __syncthreads();
-        if (threadIdx.x < TILE_ROWS) {
-            const int i = threadIdx.x;
-            for (int bl = 0; bl < nbc; bl++) {
-                acc = fmaf(park.da[bl * TILE_ROWS + i], (float)park.is[bl * TILE_ROWS + i], acc);
-                if (AFF) acc = fmaf(-park.dm[bl * TILE_ROWS + i], (float)park.ms[bl * TILE_ROWS + i], acc);
-            }
-        }
+        if (threadIdx.x < TILE_ROWS) acc = chain_park<AFF>(park, nbc, 0, TILE_ROWS, threadIdx.x, acc);
         __syncthreads();
     }
     if (threadIdx.x < TILE_ROWS) {
@@ -321,44 +330,68 @@ __global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ W
  * vector: r = 1 / sqrtf(mean(x^2) + eps) with the sum of squares in double
  * (per thread, then a fixed tree), values x * r * w (rmsnorm,
  * src/lib/tlm_model.c:164-169, then the quantiser of
- * src/lib/tlm_quant.c:458-506); without w, x itself is quantised.  Thread mapping: Q8_K, one
- * wave per 256-value block, 4 values per lane; a8, 8 lanes per 32-value
- * block.  The first NQ_IT passes keep x and w in registers between the sum
- * and the quantiser.  Every thread takes part; the caller synchronises. */
-constexpr int NQ_IT = 4;
+ * src/lib/tlm_quant.c:458-506); without w, x itself is quantised.  Each lane
+ * takes 16 contiguous values (quant16_to): a Q8_K block spans 16 lanes, an a8
+ * block 2, so one pass of 256 threads covers 4096 values.  The first pass's
+ * x and w are loaded by norm_act_load before the tile's weight loads (loads
+ * retire in issue order: the norm must not wait for the weights), with no
+ * branch around them (lanes past the last block read the last block); later
+ * passes reload.  Every thread takes part; the caller synchronises. */
+struct NormIn {
+    f32x4 xv[4], wv[4];
+};
+struct NormMap {
+    int bv, per, myb, sub;
+    __device__ NormMap(int kind) {
+        const bool k8 = kind == DT_Q8_K;
+        const int lpb = k8 ? 16 : 2;   /* lanes per block */
+        bv = k8 ? 256 : 32;
+        per = (int)blockDim.x / lpb;
+        myb = (int)threadIdx.x / lpb;
+        sub = (int)threadIdx.x % lpb;
+    }
+};
+
+static __device__ __forceinline__ void norm_act_load(int kind, const float *__restrict__ x,
+                                                     const float *__restrict__ w, int nb, NormIn &in) {
+    const NormMap m(kind);
+    const int b = min(m.myb, nb - 1);
+    const GAS f32x4 *x4 = (const GAS f32x4 *)x + (b * m.bv + 16 * m.sub) / 4;
+    const GAS f32x4 *w4 = (const GAS f32x4 *)(w ? w : x) + (b * m.bv + 16 * m.sub) / 4;
+#pragma unroll
+    for (int u = 0; u < 4; u++) in.xv[u] = x4[u];
+#pragma unroll
+    for (int u = 0; u < 4; u++) in.wv[u] = w4[u];
+}
 
 static __device__ __forceinline__ XLds stage_norm_act(int kind, const float *__restrict__ x,
-                                                      const float *__restrict__ w, float eps, int nb, uint8_t *lds_g) {
+                                                      const float *__restrict__ w, float eps, int nb, uint8_t *lds_g,
+                                                      const NormIn &in) {
     __shared__ double red[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (int)blockDim.x >> 6;
-    const bool k8 = kind == DT_Q8_K;
-    const int bv = k8 ? 256 : 32, n = nb * bv;
-    const int per = k8 ? nw : (int)blockDim.x / 8;   /* blocks per pass */
-    const int nit = (nb + per - 1) / per;
-    const int myb = k8 ? wave : tid / 8, off = 4 * (k8 ? lane : (tid & 7));
+    const NormMap m(kind);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)blockDim.x >> 6;
+    const int n = nb * m.bv, nit = (nb + m.per - 1) / m.per;
     const bool plain = w == nullptr;
-    const GAS f32x4 *x4 = (const GAS f32x4 *)x, *w4 = (const GAS f32x4 *)w;
-    f32x4 xv[NQ_IT], wv[NQ_IT];
+    auto ld = [&](const float *p, int b, f32x4 (&v)[4]) {
+        const GAS f32x4 *p4 = (const GAS f32x4 *)p + (b * m.bv + 16 * m.sub) / 4;
 #pragma unroll
-    for (int it = 0; it < NQ_IT; it++) {
-        const int b = it * per + myb;
-        if (b < nb) {
-            xv[it] = x4[(b * bv + off) / 4];
-            if (!plain) wv[it] = w4[(b * bv + off) / 4];
-        }
-    }
+        for (int u = 0; u < 4; u++) v[u] = p4[u];
+    };
     float r = 1.0f;
     if (!plain) {
         double ss = 0.0;
+        if (m.myb < nb)
 #pragma unroll
-        for (int it = 0; it < NQ_IT; it++)
-            if (it * per + myb < nb)
-                for (int j = 0; j < 4; j++) ss += (double)xv[it][j] * (double)xv[it][j];
-        for (int it = NQ_IT; it < nit; it++) {
-            const int b = it * per + myb;
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) ss += (double)in.xv[u][j] * (double)in.xv[u][j];
+        for (int it = 1; it < nit; it++) {
+            const int b = it * m.per + m.myb;
             if (b < nb) {
-                const f32x4 a = x4[(b * bv + off) / 4];
-                for (int j = 0; j < 4; j++) ss += (double)a[j] * (double)a[j];
+                f32x4 a[4];
+                ld(x, b, a);
+                for (int u = 0; u < 4; u++)
+                    for (int j = 0; j < 4; j++) ss += (double)a[u][j] * (double)a[u][j];
             }
         }
         ss = wave_sum_f64(ss);
@@ -369,46 +402,23 @@ static __device__ __forceinline__ XLds stage_norm_act(int kind, const float *__r
         r = 1.0f / sqrtf((float)(ss / (double)n) + eps);
     }
     LAS uint8_t *lds = (LAS uint8_t *)lds_g;
-    LAS uint32_t *q32 = (LAS uint32_t *)lds;
+    const bool k8 = kind == DT_Q8_K;
     LAS int16_t *bs16 = (LAS int16_t *)(lds + nb * 256);
     LAS float *dl = (LAS float *)(lds + (k8 ? nb * 288 : nb * 32));
-    auto quant = [&](int b, const f32x4 &a, const f32x4 &ww) {
-        const bool live = b < nb;
-        float v[4];
-        bool ok[4];
-        for (int j = 0; j < 4; j++) {
-            ok[j] = live;
-            v[j] = !live ? 0.0f : plain ? a[j] : a[j] * r * ww[j];
-        }
-        uint32_t codes;
-        if (k8) {
-            const float d = act_rule<64>(v, ok, codes);
-            int sm = byte_sum(codes);
-            sm += __shfl_xor(sm, 1, 64);
-            sm += __shfl_xor(sm, 2, 64);
-            if (live) {
-                q32[b * 64 + lane] = codes;
-                if (lane == 0) dl[b] = d;
-                if ((lane & 3) == 0) bs16[b * 16 + (lane >> 2)] = (int16_t)sm;
-            }
-        } else {
-            const float d = act_rule<8>(v, ok, codes);
-            if (live) {
-                q32[b * 8 + (tid & 7)] = codes;
-                if ((tid & 7) == 0) dl[b] = d;
-            }
-        }
-    };
+    auto quant = [&](int b, const f32x4 (&a)[4], const f32x4 (&ww)[4]) {
+        f32x4 v[4];
 #pragma unroll
-    for (int it = 0; it < NQ_IT; it++)
-        if (it < nit) quant(it * per + myb, xv[it], wv[it]);
-    for (int it = NQ_IT; it < nit; it++) {
-        const int b = it * per + myb;
-        f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f}, ww = a;
-        if (b < nb) {
-            a = x4[(b * bv + off) / 4];
-            if (!plain) ww = w4[(b * bv + off) / 4];
-        }
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[u][j] = plain ? a[u][j] : a[u][j] * r * ww[u][j];
+        quant16_to(kind, v, b < nb, m.sub, lds, bs16, dl, b);
+    };
+    quant(m.myb, in.xv, in.wv);
+    for (int it = 1; it < nit; it++) {   /* uniform over the group */
+        const int b = it * m.per + m.myb, bc = min(b, nb - 1);
+        f32x4 a[4], ww[4];
+        ld(x, bc, a);
+        ld(plain ? x : w, bc, ww);
         quant(b, a, ww);
     }
     return xlds_at(kind, nb, lds_g);
@@ -418,11 +428,11 @@ static __device__ __forceinline__ XLds stage_norm_act(int kind, const float *__r
  * launch (segment s owns tiles [tile_end[s-1], tile_end[s])), all taking the
  * same activation; accum: y[r] += acc instead of y[r] = acc (the reference's
  * residual update h += W x, tlm_model.c:762, adds the finished product). */
-template <int DT>
+template <int DT, bool DEEP>
 __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    constexpr int IPL = 4;
+    constexpr int IPL = MvCfg<DT, DEEP>::IPL;
     extern __shared__ __align__(16) uint8_t lds[];
     int s = 0;
     while (s + 1 < sg.n && (int64_t)blockIdx.x >= sg.tile_end[s]) s++;
@@ -431,17 +441,20 @@ __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const 
     float *y = sg.y[s];
     const int kind = dt_act_kind(DT);
     XLds X = xlds_at(kind, nb, lds);
+    NormIn nin;
     if (!sg.nx) {
         stage_act(kind, act, nb, lds);
         __syncthreads();
+    } else {
+        norm_act_load(kind, sg.nx, sg.nw, nb, nin);
     }
-    const int cap = nb < PK_NBC ? nb : PK_NBC;
+    const int cap = nb < MvCfg<DT, DEEP>::NBC ? nb : MvCfg<DT, DEEP>::NBC;
     const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * TILE_ROWS);
     bool staged = !sg.nx;
     /* the activation from rmsnorm once the first weight loads are out */
     auto stage = [&]() {
         if (!staged) {
-            stage_norm_act(kind, sg.nx, sg.nw, sg.eps, nb, lds);
+            stage_norm_act(kind, sg.nx, sg.nw, sg.eps, nb, lds, nin);
             __syncthreads();
             staged = true;
         }
@@ -463,16 +476,10 @@ __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const 
                 u = ((int64_t)t * nb + b) * TILE_ROWS + i;
                 pk = g;
             };
-            run_items<DT, IPL>(nitems - base, map, stage, park);
+            run_items<DT, IPL, MvCfg<DT, DEEP>::CLAMP>(nitems - base, map, stage, park);
         }
         __syncthreads();
-        if (threadIdx.x < TILE_ROWS) {
-            const int i = threadIdx.x;
-            for (int bl = 0; bl < nbc; bl++) {
-                acc = fmaf(park.da[bl * TILE_ROWS + i], (float)park.is[bl * TILE_ROWS + i], acc);
-                if (AFF) acc = fmaf(-park.dm[bl * TILE_ROWS + i], (float)park.ms[bl * TILE_ROWS + i], acc);
-            }
-        }
+        if (threadIdx.x < TILE_ROWS) acc = chain_park<AFF>(park, nbc, 0, TILE_ROWS, threadIdx.x, acc);
         __syncthreads();
     }
     const int64_t r = t * TILE_ROWS + threadIdx.x;
@@ -488,7 +495,7 @@ __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const 
 }
 
 static size_t packed_lds_bytes(int dt, int nb) {
-    int cap = nb < PK_NBC ? nb : PK_NBC;
+    const int cap = nb < mv_nbc(dt, nb) ? nb : mv_nbc(dt, nb);
     return ((stage_bytes(dt_act_kind(dt), nb) + 15) & ~(size_t)15) + (size_t)cap * TILE_ROWS * 16;
 }
 
@@ -573,7 +580,7 @@ int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const 
     if (dt == DT_F32) return launch_matvec_plain(dt, Wp, (size_t)n * 4, act, y, n, 0, rows, s);
     if ((uintptr_t)Wp & 15u) return tlmh_seterr(TLM_HIP_EINVAL, "matvec_packed: weights must be 16-byte aligned");
     int nb = (int)(n / dt_block_values(dt));
-    if (stage_bytes(dt_act_kind(dt), nb) > 40 * 1024)
+    if (packed_lds_bytes(dt, nb) > 64 * 1024)
         return tlmh_seterr(TLM_HIP_EUNSUP, "matvec_packed: n=%lld exceeds the staged-activation limit", (long long)n);
     if (n == 0) return launch_matvec_plain(dt, Wp, 0, act, y, 0, 0, rows, s);
     int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS;
@@ -581,11 +588,14 @@ int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const 
     dim3 g((unsigned)T), blk(256);
     const uint8_t *w = (const uint8_t *)Wp, *a = (const uint8_t *)act;
     switch (dt) {
-    case DT_Q8_0: hipLaunchKernelGGL(k_mv_packed<DT_Q8_0>, g, blk, lds, s, w, rows, nb, a, y); break;
-    case DT_Q4_K: hipLaunchKernelGGL(k_mv_packed<DT_Q4_K>, g, blk, lds, s, w, rows, nb, a, y); break;
-    case DT_Q5_K: hipLaunchKernelGGL(k_mv_packed<DT_Q5_K>, g, blk, lds, s, w, rows, nb, a, y); break;
-    case DT_Q6_K: hipLaunchKernelGGL(k_mv_packed<DT_Q6_K>, g, blk, lds, s, w, rows, nb, a, y); break;
-    case DT_Q8_K: hipLaunchKernelGGL(k_mv_packed<DT_Q8_K>, g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q8_0:
+        if (mv_deep(dt, nb)) hipLaunchKernelGGL((k_mv_packed<DT_Q8_0, true>), g, blk, lds, s, w, rows, nb, a, y);
+        else hipLaunchKernelGGL((k_mv_packed<DT_Q8_0, false>), g, blk, lds, s, w, rows, nb, a, y);
+        break;
+    case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed<DT_Q4_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q5_K: hipLaunchKernelGGL((k_mv_packed<DT_Q5_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q6_K: hipLaunchKernelGGL((k_mv_packed<DT_Q6_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
+    case DT_Q8_K: hipLaunchKernelGGL((k_mv_packed<DT_Q8_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
     }
     return tlmh_check(hipGetLastError(), "matvec_packed launch");
 }
@@ -601,7 +611,7 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
     if (keys && (nseg != 1 || ((uintptr_t)keys & 7u) || rows[0] > 0x7FFFFFFF))
         return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: greedy key needs one segment");
     const int nb = (int)(n / dt_block_values(dt));
-    if (stage_bytes(dt_act_kind(dt), nb) > 40 * 1024)
+    if (packed_lds_bytes(dt, nb) > 64 * 1024)
         return tlmh_seterr(TLM_HIP_EUNSUP, "mv_segs: n=%lld exceeds the staged-activation limit", (long long)n);
     MvSegs sg{};
     sg.n = nseg;
@@ -624,11 +634,14 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
     const dim3 g((unsigned)end), blk(256);
     const uint8_t *a = (const uint8_t *)act;
     switch (dt) {
-    case DT_Q8_0: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q8_0>, g, blk, lds, s, sg, nb, a); break;
-    case DT_Q4_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q4_K>, g, blk, lds, s, sg, nb, a); break;
-    case DT_Q5_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q5_K>, g, blk, lds, s, sg, nb, a); break;
-    case DT_Q6_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q6_K>, g, blk, lds, s, sg, nb, a); break;
-    case DT_Q8_K: hipLaunchKernelGGL(k_mv_packed_seg<DT_Q8_K>, g, blk, lds, s, sg, nb, a); break;
+    case DT_Q8_0:
+        if (mv_deep(dt, nb)) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, true>), g, blk, lds, s, sg, nb, a);
+        else hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, false>), g, blk, lds, s, sg, nb, a);
+        break;
+    case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q4_K, false>), g, blk, lds, s, sg, nb, a); break;
+    case DT_Q5_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q5_K, false>), g, blk, lds, s, sg, nb, a); break;
+    case DT_Q6_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q6_K, false>), g, blk, lds, s, sg, nb, a); break;
+    case DT_Q8_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_K, false>), g, blk, lds, s, sg, nb, a); break;
     default: return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: dtype %d", dt);
     }
     return tlmh_check(hipGetLastError(), "mv_segs launch");

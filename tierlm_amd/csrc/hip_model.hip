@@ -16,6 +16,7 @@
  * of sequential double sums, and e^x is exp in double rounded to float; the
  * reference's greedy tokens are reproduced exactly. */
 #include "tlm_hip_internal.h"
+#include <hip/hip_fp16.h>
 #include "tlm_hip_act.h"
 
 #include <math.h>
@@ -502,9 +503,9 @@ int yarn(std::vector<float> &inv_freq, uint32_t head_dim, double theta, double f
     return TLM_HIP_OK;
 }
 
-int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
+/* geometry checks and defaults, context, stream, RoPE tables (M->g set) */
+int prepare(tlm_hip_model *M, const tlm_hip_model_opts *o) {
     tlm_hip_model_geom &g = M->g;
-    g = *tlm_hip_manifest_geom(m);
     /* tlm_model.c:490-498 */
     if (g.n_layers == 0 || g.d_model == 0 || g.n_heads == 0 || g.n_kv_heads == 0 || g.head_dim == 0 ||
         (g.head_dim & 1) || g.n_heads % g.n_kv_heads || g.vocab == 0 || g.top_k > g.n_experts ||
@@ -522,8 +523,7 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
     if (g.max_ctx > 0 && max_ctx > (int)g.max_ctx) max_ctx = (int)g.max_ctx;
     M->max_ctx = max_ctx;
     M->graph_failed[0] = M->graph_failed[1] = o && o->eager;
-    const int64_t D = g.d_model, hd = g.head_dim, H = g.n_heads, KV = g.n_kv_heads, E = g.n_experts;
-    const int64_t de = g.d_expert, ds = g.n_shared > 0 ? g.d_shared : 0;
+    const int64_t hd = g.head_dim;
 
     int rc = tlmh_check(hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking), "model: stream");
     if (rc) return rc;
@@ -551,6 +551,51 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
         M->sn = (float *)b;
     }
     M->L.resize(g.n_layers);
+    return TLM_HIP_OK;
+}
+
+/* KV cache and the step's device state (alloc_scratch, tlm_model.c:402-446) */
+int finish(tlm_hip_model *M) {
+    const tlm_hip_model_geom &g = M->g;
+    const int64_t D = g.d_model, hd = g.head_dim, H = g.n_heads, KV = g.n_kv_heads;
+    const int max_ctx = M->max_ctx;
+    int rc;
+    const size_t per = (size_t)g.n_layers * KV * (size_t)max_ctx * hd;
+    M->kc = (float *)M->dalloc(per * 4);
+    M->vc = (float *)M->dalloc(per * 4);
+    M->scores = (float *)M->dalloc(((size_t)H * max_ctx + 16) * 4);   /* attention reads a row in groups of 16 */
+    M->h = (float *)M->dalloc((size_t)D * 4);
+    M->q = (float *)M->dalloc((size_t)H * hd * 4);
+    M->kx = (float *)M->dalloc((size_t)KV * hd * 4);
+    M->vx = (float *)M->dalloc((size_t)KV * hd * 4);
+    M->att = (float *)M->dalloc((size_t)H * hd * 4);
+    M->logits = (float *)M->dalloc((size_t)g.vocab * 4);
+    size_t ws = 0;
+    for (const Layer &Ly : M->L) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
+    M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
+    M->st = (int32_t *)M->dalloc(16);
+    M->seq = (int32_t *)M->dalloc(((size_t)max_ctx + 1) * 4);
+    M->ids = (int32_t *)M->dalloc(32 * 4);
+    M->w = (float *)M->dalloc(32 * 4);
+    M->keys = (unsigned long long *)M->dalloc(((size_t)g.vocab + TILE_ROWS - 1) / TILE_ROWS * 8);
+    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->h,
+                    (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
+                    (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
+                    (void *)M->w, (void *)M->keys})
+        if (!p) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the KV cache / scratch");
+    if ((rc = tlmh_check(hipHostMalloc((void **)&M->host_tok, 64, hipHostMallocDefault), "model: pinned scratch")))
+        return rc;
+    if ((rc = tlmh_check(hipMemset(M->st, 0, 16), "model: position"))) return rc;
+    return tlmh_check(hipStreamSynchronize(M->stream), "model: load");
+}
+
+int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
+    M->g = *tlm_hip_manifest_geom(m);
+    int rc = prepare(M, o);
+    if (rc) return rc;
+    const tlm_hip_model_geom &g = M->g;
+    const int64_t D = g.d_model, hd = g.head_dim, H = g.n_heads, KV = g.n_kv_heads, E = g.n_experts;
+    const int64_t de = g.d_expert, ds = g.n_shared > 0 ? g.d_shared : 0;
     for (uint32_t l = 0; l < g.n_layers; l++) {   /* load_layer, tlm_model.c:294-341 */
         Packet pk;
         if ((rc = read_packet(m, TLM_HIP_PK_DENSE, (int)l, 0, pk))) return rc;
@@ -676,34 +721,7 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
         if ((rc = dev_upload(M, pk.payload() + t.offset, (size_t)t.nbytes, &p))) return rc;
         M->embd = (const uint8_t *)p;
     }
-    /* KV cache, scratch (alloc_scratch, tlm_model.c:402-446) */
-    const size_t per = (size_t)g.n_layers * KV * (size_t)max_ctx * hd;
-    M->kc = (float *)M->dalloc(per * 4);
-    M->vc = (float *)M->dalloc(per * 4);
-    M->scores = (float *)M->dalloc(((size_t)H * max_ctx + 16) * 4);   /* attention reads a row in groups of 16 */
-    M->h = (float *)M->dalloc((size_t)D * 4);
-    M->q = (float *)M->dalloc((size_t)H * hd * 4);
-    M->kx = (float *)M->dalloc((size_t)KV * hd * 4);
-    M->vx = (float *)M->dalloc((size_t)KV * hd * 4);
-    M->att = (float *)M->dalloc((size_t)H * hd * 4);
-    M->logits = (float *)M->dalloc((size_t)g.vocab * 4);
-    size_t ws = 0;
-    for (const Layer &Ly : M->L) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
-    M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
-    M->st = (int32_t *)M->dalloc(16);
-    M->seq = (int32_t *)M->dalloc(((size_t)max_ctx + 1) * 4);
-    M->ids = (int32_t *)M->dalloc(32 * 4);
-    M->w = (float *)M->dalloc(32 * 4);
-    M->keys = (unsigned long long *)M->dalloc(((size_t)g.vocab + TILE_ROWS - 1) / TILE_ROWS * 8);
-    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->h,
-                    (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
-                    (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
-                    (void *)M->w, (void *)M->keys})
-        if (!p) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the KV cache / scratch");
-    if ((rc = tlmh_check(hipHostMalloc((void **)&M->host_tok, 64, hipHostMallocDefault), "model: pinned scratch")))
-        return rc;
-    if ((rc = tlmh_check(hipMemset(M->st, 0, 16), "model: position"))) return rc;
-    return tlmh_check(hipStreamSynchronize(M->stream), "model: load");
+    return finish(M);
 }
 
 /* tlm_model_step, src/lib/tlm_model.c:1058-1103, enqueued: the token is
@@ -788,6 +806,187 @@ int step(tlm_hip_model *M, bool want_logits) {
     return rc;
 }
 
+/* ---- random-init models (tlm_hip_model_synth) -----------------------------
+ * Counter-based: every byte is a function of (seed, tensor, index), through
+ * the splitmix64 output function (Steele, Lea, Flood, "Fast splittable
+ * pseudorandom number generators", OOPSLA 2014). */
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* n16 x 16 random bytes */
+__global__ __launch_bounds__(NT) void k_synth_bytes(uint8_t *__restrict__ dst, int64_t n16, uint64_t seed) {
+    const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n16) return;
+    const uint64_t a = mix64(seed + 2 * (uint64_t)i), b = mix64(seed + 2 * (uint64_t)i + 1);
+    ((u32x4 *)dst)[i] = u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+}
+
+/* the f16 field at byte off of each bb-byte block: scale * (0.5 + u), u in [0, 1) */
+__global__ __launch_bounds__(NT) void k_synth_scale(uint8_t *__restrict__ rows, int64_t nblocks, int bb, int off,
+                                                    float scale, uint64_t seed) {
+    const int64_t b = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (b >= nblocks) return;
+    const float u = (float)(mix64(seed ^ (uint64_t)b) >> 40) * 0x1p-24f;
+    const __half hv = __float2half(scale * (0.5f + u));
+    *(uint16_t *)(rows + b * bb + off) = *(const uint16_t *)&hv;
+}
+
+/* f32 values bias + scale * U(-sqrt(3), sqrt(3)) (standard deviation scale) */
+__global__ __launch_bounds__(NT) void k_synth_f32(float *__restrict__ dst, int64_t n, uint64_t seed, float scale,
+                                                  float bias) {
+    const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const float u = (float)(mix64(seed ^ (uint64_t)i) >> 40) * 0x1p-24f;
+    dst[i] = bias + scale * 1.7320508f * (2.0f * u - 1.0f);
+}
+
+/* rows of dtype dt in the reference layout: random code bytes, scale fields
+ * giving weights of about the spread of N(0, 0.02) */
+int synth_rows(hipStream_t s, int dt, uint8_t *dst, int64_t rows, int64_t n, uint64_t seed) {
+    const int64_t nb = rows * (n / dt_block_values(dt));
+    const int bb = dt_block_bytes(dt);
+    const int64_t n16 = (nb * bb + 15) / 16;
+    hipLaunchKernelGGL(k_synth_bytes, dim3((unsigned)((n16 + NT - 1) / NT)), dim3(NT), 0, s, dst, n16, seed);
+    const dim3 gb((unsigned)((nb + NT - 1) / NT));
+    const uint64_t s2 = mix64(seed ^ 0x5CA1Eull);
+    switch (dt) {   /* codes uniform: |int8| rms 74, Q6_K code-32 rms 18.5 x int8 scale rms 74, K-quant 6-bit scales */
+    case DT_Q8_0: hipLaunchKernelGGL(k_synth_scale, gb, dim3(NT), 0, s, dst, nb, bb, 0, 2.7e-4f, s2); break;
+    case DT_Q6_K: hipLaunchKernelGGL(k_synth_scale, gb, dim3(NT), 0, s, dst, nb, bb, 208, 1.5e-5f, s2); break;
+    case DT_Q4_K:
+    case DT_Q5_K: {
+        const float sc = dt == DT_Q4_K ? 6.2e-5f : 3.1e-5f;
+        hipLaunchKernelGGL(k_synth_scale, gb, dim3(NT), 0, s, dst, nb, bb, 0, sc, s2);
+        hipLaunchKernelGGL(k_synth_scale, gb, dim3(NT), 0, s, dst, nb, bb, 2, sc, mix64(s2));
+        break;
+    }
+    default: return tlmh_seterr(TLM_HIP_EUNSUP, "model synth: dtype %d", dt);
+    }
+    return tlmh_check(hipGetLastError(), "model synth: rows");
+}
+
+/* a synthetic matrix packed at dst (allocated when null); tmp holds the rows */
+int synth_matrix(tlm_hip_model *M, int dt, int64_t rows, int64_t n, uint64_t seed, uint8_t *tmp, void *dst,
+                 DevMat *out) {
+    const int bv = dt_block_values(dt);
+    if (bv == 0 || !dt_int_ok(dt) || dt == DT_Q8_K || n % bv)
+        return tlmh_seterr(TLM_HIP_EUNSUP, "model synth: matrix dtype %d, %lld columns", dt, (long long)n);
+    out->dt = dt;
+    out->rows = rows;
+    out->n = n;
+    out->p = dst ? dst : M->dalloc(packed_bytes(dt, rows, n));
+    if (!out->p) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
+    int rc = synth_rows(M->stream, dt, tmp, rows, n, seed);
+    if (!rc) rc = launch_pack(dt, tmp, (size_t)(n / bv) * dt_block_bytes(dt), rows, n, out->p, M->stream);
+    return rc;
+}
+
+float *synth_vec(tlm_hip_model *M, int64_t n, uint64_t seed, float scale, float bias) {
+    float *p = (float *)M->dalloc((size_t)n * 4);
+    if (p)
+        hipLaunchKernelGGL(k_synth_f32, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, M->stream, p, n, seed,
+                           scale, bias);
+    return p;
+}
+
+int synth(tlm_hip_model *M, const tlm_hip_model_synth_opts *so, const tlm_hip_model_opts *o) {
+    int rc = prepare(M, o);
+    if (rc) return rc;
+    const tlm_hip_model_geom &g = M->g;
+    const int64_t D = g.d_model, hd = g.head_dim, H = g.n_heads, KV = g.n_kv_heads, E = g.n_experts;
+    const int64_t de = g.d_expert, ds = g.n_shared > 0 ? g.d_shared : 0, V = g.vocab;
+    const int edt = so->expert_dt, ddt = so->dense_dt;
+    if (D % 32) return tlmh_seterr(TLM_HIP_EUNSUP, "model synth: d_model %lld", (long long)D);
+    /* one scratch for the largest matrix's rows */
+    const int64_t mats[][3] = {{ddt, H * hd, D}, {ddt, D, H * hd}, {edt, de, D}, {edt, D, de}, {ddt, V, D},
+                               {edt, ds, D}, {edt, D, ds}};
+    size_t tmpb = (size_t)V * (D / 32) * 34;   /* the embedding rows (Q8_0) */
+    for (const auto &m : mats) {
+        const int bv = dt_block_values((int)m[0]);
+        if (bv == 0 || m[2] % bv)
+            return tlmh_seterr(TLM_HIP_EUNSUP, "model synth: dtype %lld with %lld columns", (long long)m[0],
+                               (long long)m[2]);
+        tmpb = std::max(tmpb, (size_t)m[1] * (size_t)(m[2] / bv) * dt_block_bytes((int)m[0]));
+    }
+    uint8_t *tmp = (uint8_t *)M->dalloc((tmpb + 15) & ~(size_t)15);
+    if (!tmp) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
+    uint64_t tensor = 0;
+    auto next = [&]() { return mix64(so->seed * 0x100000001B3ull + ++tensor); };
+    /* experts: one arena, 256-byte aligned matrices */
+    const size_t pg = (packed_bytes(edt, de, D) + 255) & ~(size_t)255, pd = (packed_bytes(edt, D, de) + 255) & ~(size_t)255;
+    uint8_t *arena = (uint8_t *)M->dalloc((size_t)g.n_layers * E * (2 * pg + pd));
+    if (!arena) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory for the experts");
+    std::vector<const void *> table(3 * E);
+    for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
+        Layer &Ly = M->L[l];
+        Ly.attn_norm = synth_vec(M, D, next(), 0.0f, 1.0f);
+        Ly.ffn_norm = synth_vec(M, D, next(), 0.0f, 1.0f);
+        if (so->qk_norm) {
+            Ly.q_norm = synth_vec(M, hd, next(), 0.0f, 1.0f);
+            Ly.k_norm = synth_vec(M, hd, next(), 0.0f, 1.0f);
+        }
+        if (!Ly.attn_norm || !Ly.ffn_norm || (so->qk_norm && (!Ly.q_norm || !Ly.k_norm)))
+            return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
+        if ((rc = synth_matrix(M, ddt, H * hd, D, next(), tmp, nullptr, &Ly.q)) ||
+            (rc = synth_matrix(M, ddt, KV * hd, D, next(), tmp, nullptr, &Ly.k)) ||
+            (rc = synth_matrix(M, ddt, KV * hd, D, next(), tmp, nullptr, &Ly.v)) ||
+            (rc = synth_matrix(M, ddt, D, H * hd, next(), tmp, nullptr, &Ly.o)))
+            return rc;
+        tlm_hip_moe_desc &d = Ly.moe;
+        d.D = D;
+        d.de = de;
+        d.E = (int32_t)E;
+        d.k = (int32_t)g.top_k;
+        d.router = (int32_t)g.router;
+        d.routed_scale = g.routed_scale;
+        d.eps = g.norm_eps;
+        d.ffn_norm = Ly.ffn_norm;
+        d.router_w = synth_vec(M, E * D, next(), 1.0f / sqrtf((float)D), 0.0f);
+        if (!d.router_w) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
+        d.expert_dt = edt;
+        for (int64_t e = 0; e < E && !rc; e++) {
+            uint8_t *base = arena + ((size_t)l * E + e) * (2 * pg + pd);
+            DevMat dm;
+            if ((rc = synth_matrix(M, edt, de, D, next(), tmp, base, &dm)) ||
+                (rc = synth_matrix(M, edt, de, D, next(), tmp, base + pg, &dm)) ||
+                (rc = synth_matrix(M, edt, D, de, next(), tmp, base + 2 * pg, &dm)))
+                return rc;
+            table[3 * e] = base;
+            table[3 * e + 1] = base + pg;
+            table[3 * e + 2] = base + 2 * pg;
+        }
+        void *tp;
+        if ((rc = dev_upload(M, table.data(), table.size() * sizeof(void *), &tp))) return rc;
+        d.experts = (const void *const *)tp;
+        if (ds > 0) {
+            DevMat sg, su, sd;
+            if ((rc = synth_matrix(M, edt, ds, D, next(), tmp, nullptr, &sg)) ||
+                (rc = synth_matrix(M, edt, ds, D, next(), tmp, nullptr, &su)) ||
+                (rc = synth_matrix(M, edt, D, ds, next(), tmp, nullptr, &sd)))
+                return rc;
+            d.ds = ds;
+            d.shared_dt = edt;
+            d.sg = sg.p;
+            d.su = su.p;
+            d.sd = sd.p;
+        }
+    }
+    M->out_norm = synth_vec(M, D, next(), 0.0f, 1.0f);
+    if (!M->out_norm) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
+    if ((rc = synth_matrix(M, ddt, V, D, next(), tmp, nullptr, &M->lm_head))) return rc;
+    /* embedding rows stay in the reference layout (Q8_0), gathered per token */
+    M->embd_dt = DT_Q8_0;
+    M->embd_row = (size_t)(D / 32) * 34;
+    uint8_t *embd = (uint8_t *)M->dalloc(((size_t)V * M->embd_row + 15) & ~(size_t)15);
+    if (!embd) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
+    if ((rc = synth_rows(M->stream, DT_Q8_0, embd, V, D, next()))) return rc;
+    M->embd = embd;
+    return finish(M);
+}
+
 }  // namespace
 
 extern "C" {
@@ -802,6 +1001,22 @@ int tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, t
     tlm_hip_model *M = new tlm_hip_model;
     rc = load(M, m, o);
     tlm_hip_manifest_free(m);
+    if (rc) {
+        delete M;
+        return rc;
+    }
+    *out = M;
+    return TLM_HIP_OK;
+}
+
+int tlm_hip_model_synth(const tlm_hip_model_geom *g, const tlm_hip_model_synth_opts *so, const tlm_hip_model_opts *o,
+                        tlm_hip_model **out) {
+    if (!g || !so || !out) return tlmh_seterr(TLM_HIP_EINVAL, "model synth: NULL argument");
+    *out = nullptr;
+    if (tlmh_current_device() < 0) return tlmh_seterr(TLM_HIP_EUNSUP, "model synth: tlm_hip_init has not run");
+    tlm_hip_model *M = new tlm_hip_model;
+    M->g = *g;
+    const int rc = synth(M, so, o);
     if (rc) {
         delete M;
         return rc;

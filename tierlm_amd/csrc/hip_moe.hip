@@ -26,6 +26,7 @@
  * order are the reference's; e^x (double exp rounded to float) and rmsnorm's
  * double sum of squares (a tree) are the device's. */
 #include "tlm_hip_internal.h"
+#include "tlm_hip_act.h"
 #include "tlm_hip_items.h"
 #include "tlm_hip_mfma.h"
 
@@ -81,32 +82,6 @@ __device__ __forceinline__ void wave_sync() {
 template <class T> __device__ __forceinline__ void arg_now(T v) { asm volatile("" ::"s"(v)); }
 template <class... T> __device__ __forceinline__ void args_now(T... v) { (arg_now(v), ...); }
 
-/* max / or over aligned groups of WIDTH lanes (2, 4, 8, 16 or 64), uniform in the group */
-template <int WIDTH> __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
-    uint32_t o;
-    if (WIDTH >= 2) { o = dpp_u32<DPP_XOR1>(v); v = o > v ? o : v; }
-    if (WIDTH >= 4) { o = dpp_u32<DPP_XOR2>(v); v = o > v ? o : v; }
-    if (WIDTH >= 8) { o = dpp_u32<DPP_HALF_MIRROR>(v); v = o > v ? o : v; }
-    if (WIDTH >= 16) { o = dpp_u32<DPP_MIRROR>(v); v = o > v ? o : v; }
-    if (WIDTH == 64) {
-        const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-        const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-        const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
-        v = ab > cd ? ab : cd;
-    }
-    return v;
-}
-template <int WIDTH> __device__ __forceinline__ uint32_t group_or_u32(uint32_t v) {
-    if (WIDTH >= 2) v |= dpp_u32<DPP_XOR1>(v);
-    if (WIDTH >= 4) v |= dpp_u32<DPP_XOR2>(v);
-    if (WIDTH >= 8) v |= dpp_u32<DPP_HALF_MIRROR>(v);
-    if (WIDTH >= 16) v |= dpp_u32<DPP_MIRROR>(v);
-    if (WIDTH == 64)
-        v = ((uint32_t)__builtin_amdgcn_readlane((int)v, 0) | (uint32_t)__builtin_amdgcn_readlane((int)v, 16)) |
-            ((uint32_t)__builtin_amdgcn_readlane((int)v, 32) | (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
-    return v;
-}
-
 /* ---- activation rule (src/lib/tlm_quant.c:458-478) for this lane's 4 values
  * of a block spread over WIDTH lanes: d, and the 4 codes packed in a dword --- */
 template <int WIDTH>
@@ -141,11 +116,6 @@ __device__ __forceinline__ float act_rule4(f32x4 v, bool ok, uint32_t &codes) {
     return d;
 }
 
-__device__ __forceinline__ int byte_sum(uint32_t c) {
-    return (int)(int8_t)(c & 0xFF) + (int)(int8_t)((c >> 8) & 0xFF) + (int)(int8_t)((c >> 16) & 0xFF) +
-           (int)(int8_t)(c >> 24);
-}
-
 /* Quantise one block (values v of this lane, `ok` = lane inside the block)
  * into the split layout at (q, bs, d) of block index b: Q8_K uses all 64
  * lanes, a8 the 8 lanes of a group. */
@@ -167,85 +137,6 @@ __device__ __forceinline__ void quant_block_to(int kind, f32x4 v, bool ok, int s
             if (sub == 0) dd[b] = d;
         }
     }
-}
-
-/* Codes of 16 values for a block whose amax is below 2^-100, where 127/amax
- * is taken in double (src/lib/tlm_quant.c:466-471).  Out of line: it is never
- * reached by ordinary activations, and a call waits for every load in flight. */
-__device__ __attribute__((noinline)) u32x4 tiny_codes16(f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3, float amax) {
-    const double id = 127.0 / (double)amax;
-    const f32x4 v[4] = {v0, v1, v2, v3};
-    u32x4 c = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int t = 0; t < 16; t++)
-        c[t >> 2] |= (uint32_t)(uint8_t)(int8_t)rne_clamp((float)((double)v[t >> 2][t & 3] * id), -127, 127)
-                     << (8 * (t & 3));
-    return c;
-}
-
-/* The activation rule with 16 contiguous values per lane and a block spread
- * over WIDTH lanes of one DPP row (16 for Q8_K, 2 for a8).  Returns d and
- * the 16 codes packed in c[0..3]. */
-template <int WIDTH>
-__device__ __forceinline__ float act_rule16(const f32x4 (&v)[4], bool ok, u32x4 &c) {
-    uint32_t am = 0, fl = 0;
-#pragma unroll
-    for (int t = 0; t < 16; t++) {
-        const uint32_t b = ok ? (__float_as_uint(v[t >> 2][t & 3]) & 0x7FFFFFFFu) : 0u;
-        fl |= (b > 0x7F800000u ? 1u : 0u) | (b == 0x7F800000u ? 2u : 0u);
-        const uint32_t f = b < 0x7F800000u ? b : 0u;
-        am = f > am ? f : am;
-    }
-    am = group_max_u32<WIDTH>(am);
-    fl = group_or_u32<WIDTH>(fl);
-    const float amax = __uint_as_float(am);
-    c = u32x4{0u, 0u, 0u, 0u};
-    if (fl) return (fl & 1u) ? __uint_as_float(0x7FC00000u) : INFINITY;
-    if (!(amax > 0.0f) || !ok) return amax > 0.0f ? amax / 127.0f : 0.0f;
-    const float d = amax / 127.0f;
-    if (amax >= 0x1p-100f) {
-        const float id = 127.0f / amax;
-#pragma unroll
-        for (int t = 0; t < 16; t++)
-            c[t >> 2] |= (uint32_t)(uint8_t)(int8_t)rne_clamp(v[t >> 2][t & 3] * id, -127, 127) << (8 * (t & 3));
-    } else {
-        c = tiny_codes16(v[0], v[1], v[2], v[3], amax);
-    }
-    return d;
-}
-
-__device__ __forceinline__ void st16(LAS uint8_t *p, u32x4 v) { *(LAS u32x4 *)p = v; }
-__device__ __forceinline__ void st16(GAS uint8_t *p, u32x4 v) { *(GAS u32x4 *)p = v; }
-
-/* Quantise block b (this lane: values 16*sub..16*sub+15) into the split
- * layout (q codes, bs bsums, dd scales; LDS or global).  Q8_K: 16 lanes per
- * block, and a lane's 16 codes are exactly bsum group sub; a8: 2 lanes per
- * block. */
-template <class QP, class BP, class DP>
-__device__ __forceinline__ void quant16_to(int kind, const f32x4 (&v)[4], bool ok, int sub, QP q, BP bs, DP dd,
-                                           int b) {
-    u32x4 c;
-    if (kind == DT_Q8_K) {
-        const float d = act_rule16<16>(v, ok, c);
-        if (ok) {
-            st16(q + b * 256 + 16 * sub, c);
-            bs[b * 16 + sub] = (int16_t)(byte_sum(c.x) + byte_sum(c.y) + byte_sum(c.z) + byte_sum(c.w));
-            if (sub == 0) dd[b] = d;
-        }
-    } else {
-        const float d = act_rule16<2>(v, ok, c);
-        if (ok) {
-            st16(q + b * 32 + 16 * sub, c);
-            if (sub == 0) dd[b] = d;
-        }
-    }
-}
-
-__device__ __attribute__((noinline)) void quant16_to_ool(int kind, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3, bool ok,
-                                                        int sub, LAS uint8_t *q, LAS int16_t *bs, LAS float *dd,
-                                                        int b) {
-    const f32x4 v[4] = {v0, v1, v2, v3};
-    quant16_to(kind, v, ok, sub, q, bs, dd, b);
 }
 
 /* ---- routing by the group (src/lib/tlm_model.c:776-839) --------------------
@@ -632,7 +523,7 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
     const int slots = (int)blockDim.x / Fm::LPI;
     bool staged = false;
     XLds X = xlds_at(kind, nb, xarea);
-    float accg = 0.0f, accu = 0.0f;
+    float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += cb) {
         const int nbc = nb - b0 < cb ? nb - b0 : cb;
         const int per = nbc * TILE_ROWS, nitems = 2 * per;
@@ -652,20 +543,18 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
             run_items<DT, IPL>(nitems - base, map, stage, park);
         }
         __syncthreads();
-        if (threadIdx.x < TILE_ROWS) {
-            const int i = threadIdx.x;
-            for (int bl = 0; bl < nbc; bl++) {
-                accg = fmaf(park.da[bl * TILE_ROWS + i], (float)park.is[bl * TILE_ROWS + i], accg);
-                if (AFF) accg = fmaf(-park.dm[bl * TILE_ROWS + i], (float)park.ms[bl * TILE_ROWS + i], accg);
-                const int j = per + bl * TILE_ROWS + i;
-                accu = fmaf(park.da[j], (float)park.is[j], accu);
-                if (AFF) accu = fmaf(-park.dm[j], (float)park.ms[j], accu);
-            }
+        /* threads 0-15: the gate rows' chains, 16-31: the up rows' */
+        if (threadIdx.x < 2 * TILE_ROWS) {
+            const int i = threadIdx.x & (TILE_ROWS - 1);
+            acc = chain_park<AFF>(park, nbc, threadIdx.x < TILE_ROWS ? 0 : per, TILE_ROWS, i, acc);
         }
         __syncthreads();
     }
-    if (threadIdx.x < TILE_ROWS)
-        hh[t * TILE_ROWS + threadIdx.x] = accg / (1.0f + exp_rn(-accg)) * accu;   /* silu(g) * u (tlm_model.c:171, 927) */
+    if (threadIdx.x < 64) {   /* wave 0: up value from lane i + 16 */
+        const float up = __shfl_down(acc, TILE_ROWS, 64);
+        if (threadIdx.x < TILE_ROWS)
+            hh[t * TILE_ROWS + threadIdx.x] = acc / (1.0f + exp_rn(-acc)) * up;   /* silu(g) * u (tlm_model.c:171, 927) */
+    }
 }
 
 template <int EDT, int SDT>
@@ -799,13 +688,7 @@ __device__ void down_rows(int nmat, WPtr wptr, Pre pre, const float *hsrc, int64
 template <int DT>
 __device__ __forceinline__ float down_chain(const Park &k, int r, int nb, int i) {
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    float acc = 0.0f;
-    for (int b = 0; b < nb; b++) {
-        const int p = ((r * nb + b) << 3) + i;
-        acc = fmaf(k.da[p], (float)k.is[p], acc);
-        if (AFF) acc = fmaf(-k.dm[p], (float)k.ms[p], acc);
-    }
-    return acc;
+    return chain_park<AFF>(k, nb, (r * nb) << 3, DROWS, i, 0.0f);
 }
 
 __host__ __device__ inline size_t down_lds_part(int kind, int nq) {

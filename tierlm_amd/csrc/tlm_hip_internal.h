@@ -127,6 +127,32 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     const float ab = b > a ? b : a, cd = d > c ? d : c;
     return cd > ab ? cd : ab;
 }
+/* max / or over aligned groups of WIDTH lanes (2, 4, 8, 16 or 64), uniform in the group */
+template <int WIDTH> __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+    uint32_t o;
+    if (WIDTH >= 2) { o = dpp_u32<DPP_XOR1>(v); v = o > v ? o : v; }
+    if (WIDTH >= 4) { o = dpp_u32<DPP_XOR2>(v); v = o > v ? o : v; }
+    if (WIDTH >= 8) { o = dpp_u32<DPP_HALF_MIRROR>(v); v = o > v ? o : v; }
+    if (WIDTH >= 16) { o = dpp_u32<DPP_MIRROR>(v); v = o > v ? o : v; }
+    if (WIDTH == 64) {
+        const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+        const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+        const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+        v = ab > cd ? ab : cd;
+    }
+    return v;
+}
+template <int WIDTH> __device__ __forceinline__ uint32_t group_or_u32(uint32_t v) {
+    if (WIDTH >= 2) v |= dpp_u32<DPP_XOR1>(v);
+    if (WIDTH >= 4) v |= dpp_u32<DPP_XOR2>(v);
+    if (WIDTH >= 8) v |= dpp_u32<DPP_HALF_MIRROR>(v);
+    if (WIDTH >= 16) v |= dpp_u32<DPP_MIRROR>(v);
+    if (WIDTH == 64)
+        v = ((uint32_t)__builtin_amdgcn_readlane((int)v, 0) | (uint32_t)__builtin_amdgcn_readlane((int)v, 16)) |
+            ((uint32_t)__builtin_amdgcn_readlane((int)v, 32) | (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return v;
+}
+
 /* sum over the wave, fixed tree: ((row0 + row1) + (row2 + row3)) */
 __device__ __forceinline__ double wave_sum_f64(double v) {
     v += dpp_f64<DPP_XOR1>(v);

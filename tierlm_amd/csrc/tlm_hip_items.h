@@ -269,13 +269,16 @@ __device__ __forceinline__ static Park park_at(uint8_t *p, int nitems) {
     return k;
 }
 
-/* Items it = slot + SLOTS*j (j < IPL) of a list of nitems.  map(it, W, units,
- * u, b, pk) names the item's packed matrix, its unit, its activation block
- * and its park slot.  Every load is issued first; then stage() runs (it
- * fills the LDS activation while the loads are in flight and returns it);
- * then every compute.  Lanes of an item share `it`, so shuffles stay
- * in-item.  Returns the XLds that stage() produced. */
-template <int DT, int IPL, class Map, class Stage>
+/* Items it = slot + SLOTS*j (j < IPL) of a list of nitems (>= 1).  map(it,
+ * W, units, u, b, pk) names the item's packed matrix, its unit, its
+ * activation block and its park slot.  Every load is issued first; then
+ * stage() runs (it fills the LDS activation while the loads are in flight
+ * and returns it); then every compute.  Lanes of an item share `it`, so
+ * shuffles stay in-item.  Items past the end are skipped, or with CLAMP
+ * load the last item's bytes and are dropped: with many items per lane the
+ * compiler keeps branch-free loads in flight together, where a branch per
+ * item made it wait between them.  Returns the XLds that stage() produced. */
+template <int DT, int IPL, bool CLAMP = false, class Map, class Stage>
 __device__ __forceinline__ XLds run_items(int nitems, Map map, Stage stage, Park park) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
@@ -286,13 +289,19 @@ __device__ __forceinline__ XLds run_items(int nitems, Map map, Stage stage, Park
 #pragma unroll
     for (int j = 0; j < IPL; j++) {
         const int it = slot + slots * j;
-        pk[j] = -1;
-        bb[j] = 0;
-        if (it < nitems) {
-            const uint8_t *W;
-            int64_t units, u;
-            map(it, W, units, u, bb[j], pk[j]);
+        const uint8_t *W;
+        int64_t units, u;
+        if constexpr (CLAMP) {
+            map(it < nitems ? it : nitems - 1, W, units, u, bb[j], pk[j]);
+            if (it >= nitems) pk[j] = -1;
             raw[j] = F::load(W, units, u, q);
+        } else {
+            pk[j] = -1;
+            bb[j] = 0;
+            if (it < nitems) {
+                map(it, W, units, u, bb[j], pk[j]);
+                raw[j] = F::load(W, units, u, q);
+            }
         }
     }
     const XLds X = stage();
@@ -312,14 +321,37 @@ __device__ __forceinline__ XLds run_items(int nitems, Map map, Stage stage, Park
     return X;
 }
 
-/* Row i's float chain over nb parked blocks in ascending order (the reference's
- * per-row fma sequence), park index b * TILE_ROWS + i. */
+/* Row i's float chain continued over nb parked blocks in ascending order:
+ * the reference's per-row fma sequence (acc = fmaf(d_w d_a, isum, acc), then
+ * for Q4_K / Q5_K acc = fmaf(-dmin_w d_a, msum, acc)); park index
+ * o + b * stride + i.  Eight blocks' values are read before their fmas so
+ * the LDS reads overlap; the fma order is unchanged. */
 template <bool AFF>
-__device__ __forceinline__ float park_chain(const Park &k, int nb, int i) {
-    float acc = 0.0f;
-    for (int b = 0; b < nb; b++) {
-        acc = fmaf(k.da[b * TILE_ROWS + i], (float)k.is[b * TILE_ROWS + i], acc);
-        if (AFF) acc = fmaf(-k.dm[b * TILE_ROWS + i], (float)k.ms[b * TILE_ROWS + i], acc);
+__device__ __forceinline__ float chain_park(const Park &k, int nb, int o, int stride, int i, float acc) {
+    int b = 0;
+    for (; b + 8 <= nb; b += 8) {
+        float da[8], dm[8];
+        int32_t is[8], ms[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int p = o + (b + u) * stride + i;
+            da[u] = k.da[p];
+            is[u] = k.is[p];
+            if (AFF) {
+                dm[u] = k.dm[p];
+                ms[u] = k.ms[p];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            acc = fmaf(da[u], (float)is[u], acc);
+            if (AFF) acc = fmaf(-dm[u], (float)ms[u], acc);
+        }
+    }
+    for (; b < nb; b++) {
+        const int p = o + b * stride + i;
+        acc = fmaf(k.da[p], (float)k.is[p], acc);
+        if (AFF) acc = fmaf(-k.dm[p], (float)k.ms[p], acc);
     }
     return acc;
 }

@@ -20,11 +20,38 @@ class ModelOpts(C.Structure):
     _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32)]
 
 
+# Qwen3-30B-A3B: 48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128
+# experts top-8 of width 768, vocabulary 151936, qk-norm, rope theta 1e6
+QWEN3_30B_A3B = dict(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_dim=128, vocab=151936,
+                     n_experts=128, top_k=8, d_expert=768, n_shared=0, d_shared=0, max_ctx=40960, router=0,
+                     rope_theta=1e6, norm_eps=1e-6, routed_scale=1.0)
+
+
 class Model:
     def __init__(self, manifest_path, max_ctx=0, eager=False):
         self.opts = ModelOpts(max_ctx, int(eager))
         h = C.c_void_p()
         check(lib.tlm_hip_model_open(str(manifest_path).encode(), C.byref(self.opts), C.byref(h)))
+        self._bind(h)
+
+    @classmethod
+    def synth(cls, geom, expert_dt=14, dense_dt=8, qk_norm=True, seed=1, max_ctx=0, eager=False):
+        """tlm_hip_model_synth: a random-init model of geometry geom (a dict of
+        tlm_hip_model_geom fields) built in HBM."""
+        from ._lib import ModelGeom, ModelSynthOpts
+        g = ModelGeom()
+        g.arch = b"synthetic"
+        for k, v in geom.items():
+            setattr(g, k, v)
+        so = ModelSynthOpts(expert_dt, dense_dt, int(qk_norm), 0, seed)
+        self = cls.__new__(cls)
+        self.opts = ModelOpts(max_ctx, int(eager))
+        h = C.c_void_p()
+        check(lib.tlm_hip_model_synth(C.byref(g), C.byref(so), C.byref(self.opts), C.byref(h)))
+        self._bind(h)
+        return self
+
+    def _bind(self, h):
         self.h = h
         self.geom = lib.tlm_hip_model_geom_of(h).contents
 
