@@ -234,6 +234,35 @@ def c1_bench(reps):
     return out
 
 
+def c3_bench(reps, ctx):
+    """The whole decode step on a random-init model of the full Qwen3-30B-A3B
+    shape (48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128 experts top-8
+    of width 768, vocabulary 151936; Q6_K experts, Q8_0 dense; every expert
+    resident, 23.8 GB), built in HBM by tlm_hip_model_synth: a 64-token
+    prompt, then greedy tokens up to ctx positions.  The reference has no
+    store of this size here, so no CPU figure sits beside it."""
+    from tierlm_amd.model import QWEN3_30B_A3B, Model, time_model
+    t0 = time.perf_counter()
+    m = Model.synth(QWEN3_30B_A3B, expert_dt=Q6_K, dense_dt=8, seed=1, max_ctx=ctx)
+    built = time.perf_counter() - t0
+    try:
+        r = time_model(m, 64, ctx - 64, reps, warm_n=8)
+        short = time_model(m, 64, 64, reps)
+    finally:
+        m.close()
+    out = {"model": "Qwen3-30B-A3B shape, random init (48 layers, 128 experts top-8, Q6_K experts, Q8_0 dense)",
+           "context": ctx, "prefill_tok_s": r["prefill_tok_s"], "decode_tok_s": r["decode_tok_s"],
+           "decode_ms_per_token": round(r["decode_us_per_token"] / 1e3, 3),
+           "decode_tok_s_first_64": short["decode_tok_s"], "build_s": round(built, 2),
+           "timing": f"host wall clock around tlm_hip_model_generate: prefill 64, then {ctx - 64 - 1} decode steps "
+                     f"to {ctx} positions, best of {reps}; each step one replay of a captured HIP graph",
+           "reference_cpu": None}
+    log(f"bench: Qwen3-30B-A3B-shape model: decode {out['decode_tok_s']:.1f} tok/s to {ctx} positions "
+        f"({out['decode_ms_per_token']:.3f} ms/token; {out['decode_tok_s_first_64']:.1f} tok/s over the first 64), "
+        f"prefill {out['prefill_tok_s']:.1f} tok/s")
+    return out
+
+
 def cpu_baseline(args, threads):
     """Reference kernels on the host (oracle/_ref), bounded sample."""
     import numpy as np
@@ -282,6 +311,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill measurement")
     ap.add_argument("--no-store", action="store_true", help="skip the expert slot cache measurement")
     ap.add_argument("--no-c1", action="store_true", help="skip the whole-step synthetic model measurement")
+    ap.add_argument("--no-c3", action="store_true", help="skip the full Qwen3-30B-A3B-shape model measurement")
+    ap.add_argument("--c3-context", type=int, default=2048, help="positions the full-model decode runs to")
     ap.add_argument("--store-tokens", type=int, default=400, help="tokens per slot-cache decode measurement")
     ap.add_argument("--copy-check-mib", type=int, default=0,
                     help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
@@ -436,6 +467,10 @@ def main():
     prefill = None if args.no_prefill else prefill_bench(torch, dev, W, router_w, ffn_norm, gen)
     slot_cache = None if args.no_store else slot_cache_bench(torch, dev, router_w, ffn_norm, gen, args.store_tokens)
     c1 = None if args.no_c1 or not os.path.exists(C1_STORE) else c1_bench(3)
+    if not args.no_c3:
+        del W                                  # the block's 23.8 GB of experts; the model builds its own
+        torch.cuda.empty_cache()
+    c3 = None if args.no_c3 else c3_bench(1, args.c3_context)
 
     cpu = None
     if not args.no_cpu:
@@ -471,6 +506,7 @@ def main():
         "prefill": prefill,
         "slot_cache": slot_cache,
         "c1_whole_step": c1,
+        "qwen3_30b_a3b_whole_model": c3,
     }
     print(json.dumps(line), flush=True)
 

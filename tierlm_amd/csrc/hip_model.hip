@@ -78,18 +78,19 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
  *
  * Latency, not bandwidth, sets this kernel's time (one group per head), so
  * it is arranged around the memory counter, which retires loads in issue
- * order: every load goes out at entry, unconditionally (indices clamped) and
- * in the order the values are consumed - head vectors, norm weights and
- * RoPE factors, then the first pass's key column per thread (HD <= 128) and
- * the first V chunk (ATT_VF floats) - and no global store precedes a barrier
- * (a barrier waits for the group's stores): the KV append goes last.  The
+ * order: the loads go out unconditionally (indices clamped) in the order the
+ * values are consumed - head vectors, norm weights and RoPE factors and the
+ * first pass's key columns per thread at entry (HD <= 128; later passes load
+ * theirs at once too), the first two V chunks (ATT_VF floats each) once the
+ * scores are done - and no global store precedes a barrier (a barrier waits
+ * for the group's stores): the KV append goes last.  The
  * probabilities stay in LDS (dynamic, max_ctx floats) when SPL, else in the
  * head's global scratch row; they are scaled by 1/sum in place (the
  * reference's p = s[t] * inv).  The ordered sums go 16 positions per group
  * (four 16-byte probability reads, sixteen fixed-offset value reads, then
  * the adds); the last group of a chunk reads whole (the probability row is padded to 16, a chunk holds a
- * multiple of 16 positions) and masks its adds.  Later V chunks load into
- * registers while the previous one is summed.  q_norm / k_norm are read only
+ * multiple of 16 positions) and masks its adds.  Two V chunks wait in
+ * registers while one is summed.  q_norm / k_norm are read only
  * when has_qn / has_kn. */
 constexpr int ATT_VF = 8192;                 /* floats of V per LDS chunk (32 KB) */
 constexpr int ATT_PF = ATT_VF / 4 / NT;      /* 16-byte V loads per thread per chunk */
@@ -151,14 +152,13 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
 #pragma unroll
         for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
     }
-    f32x4 pv[ATT_PF];
-    auto vload = [&](int t0) {
+    f32x4 pa[ATT_PF], pb[ATT_PF];   /* two V chunks in registers */
+    auto vload = [&](int t0, f32x4 (&pv)[ATT_PF]) {
         const int n4 = (T - t0 < VC ? T - t0 : VC) * H4;
         const f32x4 *src = (const f32x4 *)(V + (size_t)t0 * HD);
 #pragma unroll
         for (int j = 0; j < ATT_PF; j++) pv[j] = src[min(tid + NT * j, n4 - 1)];
     };
-    vload(0);
 
     /* norm (tlm_model.c:743-746) and RoPE (rope(), :721-728: pairs (j, j + HD/2)) */
     if (wave < 3) {
@@ -200,9 +200,15 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
     const float scale = 1.0f / sqrtf((float)HD);
     float mx = -INFINITY;
     const f32x4 *q4 = (const f32x4 *)s_q;
-    for (int t = tid; t < T; t += NT) {
+    for (int p0 = 0; p0 < T; p0 += NT) {   /* passes of NT positions, uniform over the group */
+        const int t = p0 + tid;
         float d = 0.0f;
-        if (KPRE && t < NT) {
+        if (KPRE) {
+            if (p0 > 0) {   /* this pass's key columns, all at once (rows clamped to pos) */
+                const float *kt = K + min(t, pos);
+#pragma unroll
+                for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
+            }
             if (t == pos) {   /* the new key, from this group's copy */
 #pragma unroll
                 for (int i4 = 0; i4 < H4; i4++) {
@@ -224,15 +230,19 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
         } else if (t == pos) {
 #pragma unroll
             for (int i = 0; i < HD; i++) d += s_q[i] * s_k[i];
-        } else {
+        } else if (t < T) {
             const float *kt = K + t;
 #pragma unroll 16
             for (int i = 0; i < HD; i++) d += s_q[i] * kt[(size_t)i * max_ctx];
         }
-        d *= scale;
-        sp[t] = d;
-        if (d > mx) mx = d;
+        if (t < T) {
+            d *= scale;
+            sp[t] = d;
+            if (d > mx) mx = d;
+        }
     }
+    vload(0, pa);   /* the key registers are free now; max, exp and sum cover the latency */
+    if (VC < T) vload(VC, pb);
     mx = block_max_dpp(mx, s_redf);
     double sum = 0.0;
     for (int t = tid; t < T; t += NT) {
@@ -244,9 +254,10 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
     const float inv = (float)(1.0 / sum);
     for (int t = tid; t < T; t += NT) sp[t] = sp[t] * inv;
 
-    /* P.V, chunk by chunk */
+    /* P.V, chunk by chunk: the chunk being summed in LDS, the next two in
+     * registers (pa / pb alternate; a freed buffer loads the chunk after next) */
     float o = 0.0f;
-    for (int t0 = 0; t0 < T; t0 += VC) {
+    auto chunk = [&](int t0, f32x4 (&pv)[ATT_PF]) {
         const int tn = T - t0 < VC ? T - t0 : VC;
 #pragma unroll
         for (int j = 0; j < ATT_PF; j++) {   /* registers -> LDS (whole buffer); row pos from this group's copy */
@@ -255,7 +266,7 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
             ((f32x4 *)s_v)[e4] = t0 + e4 / H4 == pos ? nv : pv[j];
         }
         __syncthreads();   /* every p stored (first pass) and the chunk in LDS */
-        if (t0 + VC < T) vload(t0 + VC);
+        if (t0 + 2 * VC < T) vload(t0 + 2 * VC, pv);
         if (tid < HD) {
             const float *pc = sp + t0;   /* t0: a multiple of VC, itself of 16 */
             const float *vcol = s_v + tid;
@@ -286,6 +297,12 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
             }
         }
         __syncthreads();   /* the chunk is read before the next one overwrites it */
+    };
+    for (int t0 = 0;;) {   /* uniform over the group */
+        chunk(t0, pa);
+        if ((t0 += VC) >= T) break;
+        chunk(t0, pb);
+        if ((t0 += VC) >= T) break;
     }
     if (tid < HD) att[(size_t)h * HD + tid] = o;
     if (h % (H / KV) == 0)   /* the KV append, after the last barrier */

@@ -98,32 +98,37 @@ def bench_prompt(n, vocab, seed=42):
     return out
 
 
-def bench(path, prompt_len=64, n=64, reps=3, eager=False, max_ctx=0):
+def time_model(m, prompt_len=64, n=64, reps=3, warm_n=None):
     """Best of reps: prefill time (generate(prompt, 1)) and decode time (the
     n - 1 further steps of generate(prompt, n)), host wall clock around the
     calls; tokens stay on the device between steps."""
-    m = Model(path, max_ctx=max_ctx or prompt_len + n + 1, eager=eager)
-    try:
-        prompt = bench_prompt(prompt_len, m.geom.vocab)
+    prompt = bench_prompt(prompt_len, m.geom.vocab)
+    m.reset()
+    toks = m.generate(prompt, n if warm_n is None else warm_n)   # warm (and graph capture)
+    pre = dec = None
+    for _ in range(reps):
         m.reset()
-        toks = m.generate(prompt, n)            # warm (and graph capture)
-        pre = dec = None
-        for _ in range(reps):
-            m.reset()
-            t0 = time.perf_counter()
-            m.generate(prompt, 1)
-            t1 = time.perf_counter()
-            m.reset()
-            t2 = time.perf_counter()
-            toks = m.generate(prompt, n)
-            t3 = time.perf_counter()
-            p, d = t1 - t0, (t3 - t2) - (t1 - t0)
-            pre = p if pre is None else min(pre, p)
-            dec = d if dec is None else min(dec, d)
-    finally:
-        m.close()
+        t0 = time.perf_counter()
+        m.generate(prompt, 1)
+        t1 = time.perf_counter()
+        m.reset()
+        t2 = time.perf_counter()
+        toks = m.generate(prompt, n)
+        t3 = time.perf_counter()
+        p, d = t1 - t0, (t3 - t2) - (t1 - t0)
+        pre = p if pre is None else min(pre, p)
+        dec = d if dec is None else min(dec, d)
     return {"prefill_tok_s": round(prompt_len / pre, 1), "decode_tok_s": round((n - 1) / dec, 1),
             "decode_us_per_token": round(dec / (n - 1) * 1e6, 1), "tokens": toks}
+
+
+def bench(path, prompt_len=64, n=64, reps=3, eager=False, max_ctx=0):
+    """time_model on a compiled store."""
+    m = Model(path, max_ctx=max_ctx or prompt_len + n + 1, eager=eager)
+    try:
+        return time_model(m, prompt_len, n, reps)
+    finally:
+        m.close()
 
 
 if __name__ == "__main__":
