@@ -3,10 +3,12 @@ tlm_model_step / tlm_model_prefill, src/lib/tlm_model.c:1058-1113) for a
 compiled store, through ctypes.  Computes nothing itself.
 
     python -m tierlm_amd.model STORE.tlmm [--prompt-len 64] [-n 64] [--eager]
+    python -m tierlm_amd.model --synth qwen3-30b-a3b [--layers 48] ...
 
 times the device the way `tierlm bench` times the host runtime
 (src/bin/tierlm.c:702-735): a pseudo-random prompt, prefill, then greedy
-tokens; decode tok/s = (n - 1) / decode time."""
+tokens; decode tok/s = (n - 1) / decode time.  --synth times a random-init
+model of that shape built in HBM (tlm_hip_model_synth) instead of a store."""
 import ctypes as C
 import time
 
@@ -136,14 +138,28 @@ if __name__ == "__main__":
 
     from .quant import init
     ap = argparse.ArgumentParser(prog="python -m tierlm_amd.model")
-    ap.add_argument("store")
+    ap.add_argument("store", nargs="?")
+    ap.add_argument("--synth", choices=["qwen3-30b-a3b"], help="a random-init model of this shape instead of a store")
+    ap.add_argument("--layers", type=int, default=0, help="with --synth: layers (default: the model's)")
     ap.add_argument("--prompt-len", type=int, default=64)
     ap.add_argument("-n", type=int, default=64)
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--eager", action="store_true", help="launch kernels directly instead of replaying a graph")
     a = ap.parse_args()
+    if (a.store is None) == (a.synth is None):
+        ap.error("give a store or --synth")
     init(0)
-    r = bench(a.store, a.prompt_len, a.n, a.reps, a.eager)
-    print(f"bench {a.store}: prompt {a.prompt_len} tokens ({r['prefill_tok_s']:.1f} tok/s), decode {a.n} tokens "
+    if a.synth:
+        geom = dict(QWEN3_30B_A3B, **({"n_layers": a.layers} if a.layers else {}))
+        m = Model.synth(geom, seed=1, max_ctx=a.prompt_len + a.n + 1, eager=a.eager)
+        try:
+            r = time_model(m, a.prompt_len, a.n, a.reps)
+        finally:
+            m.close()
+        name = f"{a.synth} ({geom['n_layers']} layers, random init)"
+    else:
+        r = bench(a.store, a.prompt_len, a.n, a.reps, a.eager)
+        name = a.store
+    print(f"bench {name}: prompt {a.prompt_len} tokens ({r['prefill_tok_s']:.1f} tok/s), decode {a.n} tokens "
           f"({r['decode_tok_s']:.1f} tok/s, {r['decode_us_per_token']:.1f} us/token){' eager' if a.eager else ''}",
           flush=True)
