@@ -38,19 +38,21 @@ def prefill_vs_decode(case, dev, T, seed, scale=1.0):
     return H, got, got_ids
 
 
+@pytest.mark.parametrize("dt", [oracle.Q4_K, oracle.Q5_K, oracle.Q6_K])
 @pytest.mark.parametrize("T", [1, 7, 40, 129])
-def test_prefill_equals_decode_per_token(hip, dev, T):
+def test_prefill_equals_decode_per_token(hip, dev, dt, T):
     """D 512, 16 experts top-4, de 256: at T = 129 some experts hold more than
     32 tokens (two tiles), at T = 1 most hold none."""
-    case = build_moe_case(D=512, de=256, E=16, k=4, ds=0, expert_dt=oracle.Q6_K, seed=60 + T, device=dev,
+    case = build_moe_case(D=512, de=256, E=16, k=4, ds=0, expert_dt=dt, seed=60 + T, device=dev,
                           weights="random_codes")
     prefill_vs_decode(case, dev, T, seed=T)
 
 
-def test_prefill_qwen3_shape_vs_oracle(hip, dev):
+@pytest.mark.parametrize("dt", [oracle.Q5_K, oracle.Q6_K])
+def test_prefill_qwen3_shape_vs_oracle(hip, dev, dt):
     """D 2048, 128 experts top-8, de 768 at 24 tokens: decode bits per token, and
     the oracle's block (routing identical, residual within 1e-5)."""
-    case = build_moe_case(D=2048, de=768, E=128, k=8, ds=0, expert_dt=oracle.Q6_K, seed=9, device=dev,
+    case = build_moe_case(D=2048, de=768, E=128, k=8, ds=0, expert_dt=dt, seed=9, device=dev,
                           weights="random_codes")
     H, got, got_ids = prefill_vs_decode(case, dev, 24, seed=5)
     _, _, got_w = prefill_vs_decode.last
@@ -76,5 +78,9 @@ def test_prefill_rejects_unsupported(hip, dev):
     from tierlm_amd._lib import HipError
     case = build_moe_case(D=256, de=256, E=8, k=2, ds=256, expert_dt=oracle.Q6_K, shared_dt=oracle.Q8_0, seed=1,
                           device=dev, weights="random_codes")
+    with pytest.raises(HipError):
+        case.block.prefill(torch.zeros((4, 256), device=dev))
+    case = build_moe_case(D=256, de=256, E=8, k=2, ds=0, expert_dt=oracle.Q8_0, seed=1, device=dev,
+                          weights="random_codes")
     with pytest.raises(HipError):
         case.block.prefill(torch.zeros((4, 256), device=dev))

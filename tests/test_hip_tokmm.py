@@ -6,7 +6,8 @@ the token-batched kernel is checked bit for bit against the packed GEMV run
 token by token (itself bit-exact with the oracle, test_hip_gemv.py), and a
 sample against the oracle directly.  Shapes cover token counts around the
 32-token tile, rows around the 16-row tile and the 128-row group, the edge
-weight patterns of the reference's matvec tests, and poisoned activations."""
+weight patterns of the reference's matvec tests, and poisoned activations,
+for each weight format with a token kernel (Q4_K, Q5_K, Q6_K)."""
 import numpy as np
 import pytest
 import torch
@@ -45,26 +46,33 @@ def run_case(hip, dev, dt, rows, n, ntok, seed, wmode=None, poison=False):
     return W, X, got
 
 
+KQ = [oracle.Q4_K, oracle.Q5_K, oracle.Q6_K]
+
+
+@pytest.mark.parametrize("dt", KQ)
 @pytest.mark.parametrize("rows,n,ntok", [(768, 2048, 32), (768, 2048, 1), (100, 512, 33), (2048, 768, 45),
                                          (130, 256, 64), (16, 256, 7)])
-def test_tokmm_q6k_matches_decode(hip, dev, rows, n, ntok):
-    run_case(hip, dev, oracle.Q6_K, rows, n, ntok, seed=rows * 7 + ntok)
+def test_tokmm_matches_decode(hip, dev, dt, rows, n, ntok):
+    run_case(hip, dev, dt, rows, n, ntok, seed=rows * 7 + ntok + dt)
 
 
+@pytest.mark.parametrize("dt", KQ)
 @pytest.mark.parametrize("wmode", [1, 2, 3, 4, -1])
-def test_tokmm_q6k_edge_weights(hip, dev, wmode):
-    run_case(hip, dev, oracle.Q6_K, 48, 512, 19, seed=100 + wmode, wmode=wmode)
+def test_tokmm_edge_weights(hip, dev, dt, wmode):
+    run_case(hip, dev, dt, 48, 512, 19, seed=100 + wmode, wmode=wmode)
 
 
-def test_tokmm_q6k_poisoned_tokens(hip, dev):
-    run_case(hip, dev, oracle.Q6_K, 96, 1024, 40, seed=7, poison=True)
+@pytest.mark.parametrize("dt", KQ)
+def test_tokmm_poisoned_tokens(hip, dev, dt):
+    run_case(hip, dev, dt, 96, 1024, 40, seed=7, poison=True)
 
 
-def test_tokmm_q6k_vs_oracle(hip, dev):
-    W, X, got = run_case(hip, dev, oracle.Q6_K, 64, 512, 9, seed=3, wmode=3)
+@pytest.mark.parametrize("dt", KQ)
+def test_tokmm_vs_oracle(hip, dev, dt):
+    W, X, got = run_case(hip, dev, dt, 64, 512, 9, seed=3, wmode=3)
     for t in range(X.shape[0]):
         act = oracle.quantize_act(oracle.Q8_K, X[t])
-        want = oracle.matvec_rows(oracle.Q6_K, W, W.shape[1], act, 512, 0, 64)
+        want = oracle.matvec_rows(dt, W, W.shape[1], act, 512, 0, 64)
         assert same(got[t], want).all(), t
 
 

@@ -910,35 +910,46 @@ __global__ __launch_bounds__(256) void k_pf_bucket(tlm_hip_moe_desc d, PfLayout 
     for (int ti = tiles_used + tid; ti < P.MT; ti += 256) tiles[3 * ti] = -1;
 }
 
-/* Rows of gate and up (each wave: 32 rows x up to 32 slots of one expert),
- * then h = silu(g) * u per (slot, row). */
-__global__ __launch_bounds__(256) void k_pf_gateup(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws) {
-    __shared__ float s_da[4][tokmm::TM_TOK];
+/* Rows of gate and up: 64 rows per group over the tile's (up to 32) slots of
+ * one expert - waves 0-1 stream gate rows, waves 2-3 the same rows of up -
+ * then, through LDS, h = silu(g) * u per (slot, row). */
+template <int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_pf_gateup(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws) {
+    __shared__ __align__(16) uint8_t s_tile[tokmm::tile_lds_bytes<DT>()];
+    static_assert(tokmm::tile_lds_bytes<DT>() >= 2 * 16 * 64 * 4, "exchange area");
     args_now(d.D, d.de, d.experts, L.xe, P.tok, P.tstride, P.tiles, P.slot_tok, P.hbuf, ws);
     const GAS int32_t *tl = (const GAS int32_t *)(ws + P.tiles) + 3 * blockIdx.y;
     const int e = tl[0];
     if (e < 0) return;
     const int s0 = tl[1], n = tl[2];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, half = lane >> 5;
-    const int64_t rows = d.de, row = (int64_t)blockIdx.x * 128 + wave * 32 + j;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, up = wave >> 1;
+    const int64_t rows = d.de, row = (int64_t)blockIdx.x * 64 + (wave & 1) * 32 + (lane & 31);
     const int64_t rr = row < rows ? row : rows - 1;
     const int nb = (int)(d.D / 256);
     const int64_t units = (rows / TILE_ROWS) * nb * TILE_ROWS;
     const int64_t ubase = (rr / TILE_ROWS) * nb * TILE_ROWS + rr % TILE_ROWS;
-    const int slot = s0 + (j < n ? j : n - 1);
+    const int js = (int)threadIdx.x >> 3;                  /* the token this thread stages */
+    const int slot = s0 + (js < n ? js : n - 1);
     const int tok = ((const GAS int32_t *)(ws + P.slot_tok))[slot];
-    const GAS uint8_t *arow = (const GAS uint8_t *)(ws + P.tok + (size_t)tok * P.tstride + L.xe);
+    const GAS uint8_t *x = (const GAS uint8_t *)(ws + P.tok + (size_t)tok * P.tstride + L.xe);
     const GAS uint64_t *xt = (const GAS uint64_t *)d.experts;
-    const uint8_t *wg = (const uint8_t *)xt[3 * e], *wu = (const uint8_t *)xt[3 * e + 1];
-    float accg[16], accu[16];
-    tokmm::tile_q6k<true>(wg, units, ubase, nb, arow, (LAS float *)s_da[wave], j, half, accg);
-    tokmm::tile_q6k<true>(wu, units, ubase, nb, arow, (LAS float *)s_da[wave], j, half, accu);
-    if (row < rows) {
+    const tokmm::Chain ch = tokmm::chain_at<DT>((const uint8_t *)xt[3 * e + up], units, ubase);
+    float acc[16];
+    tokmm::tile_run<DT, true>(ch, nb, x, (LAS uint8_t *)s_tile, acc);
+    /* the tile ended on a barrier: its LDS is free for the up values */
+    LAS float *xch = (LAS float *)s_tile + (wave & 1) * 16 * 64 + lane;
+    if (up) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) xch[64 * v] = acc[v];
+    }
+    __syncthreads();
+    if (!up && row < rows) {
         GAS float *hb = (GAS float *)(ws + P.hbuf);
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int i = 8 * (v >> 2) + 4 * half + (v & 3);
-            if (i < n) hb[(size_t)(s0 + i) * rows + row] = accg[v] / (1.0f + exp_rn(-accg[v])) * accu[v];
+            const float g = acc[v], u = xch[64 * v];
+            if (i < n) hb[(size_t)(s0 + i) * rows + row] = g / (1.0f + exp_rn(-g)) * u;
         }
     }
 }
@@ -955,25 +966,28 @@ __global__ __launch_bounds__(64) void k_pf_hquant(tlm_hip_moe_desc d, PfLayout P
                    (GAS float *)(q + nbd * 288), b);
 }
 
-/* Rows of down (each wave: 32 rows x up to 32 slots of one expert). */
-__global__ __launch_bounds__(256) void k_pf_down(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
-    __shared__ float s_da[4][tokmm::TM_TOK];
+/* Rows of down: 4 waves x 32 rows per group over the tile's slots of one
+ * expert. */
+template <int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_pf_down(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
+    __shared__ __align__(16) uint8_t s_tile[tokmm::tile_lds_bytes<DT>()];
     args_now(d.D, d.de, d.experts, P.tiles, P.hq, P.hq_stride, P.out, ws);
     const GAS int32_t *tl = (const GAS int32_t *)(ws + P.tiles) + 3 * blockIdx.y;
     const int e = tl[0];
     if (e < 0) return;
     const int s0 = tl[1], n = tl[2];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, half = lane >> 5;
-    const int64_t rows = d.D, row = (int64_t)blockIdx.x * 128 + wave * 32 + j;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5;
+    const int64_t rows = d.D, row = (int64_t)blockIdx.x * 128 + wave * 32 + (lane & 31);
     const int64_t rr = row < rows ? row : rows - 1;
     const int nb = (int)(d.de / 256);
     const int64_t units = (rows / TILE_ROWS) * nb * TILE_ROWS;
-    const int64_t ubase = (rr / TILE_ROWS) * nb * TILE_ROWS + rr % TILE_ROWS;
-    const int slot = s0 + (j < n ? j : n - 1);
-    const GAS uint8_t *arow = (const GAS uint8_t *)(ws + P.hq + (size_t)slot * P.hq_stride);
+    const int js = (int)threadIdx.x >> 3;
+    const int slot = s0 + (js < n ? js : n - 1);
+    const GAS uint8_t *x = (const GAS uint8_t *)(ws + P.hq + (size_t)slot * P.hq_stride);
     const uint8_t *wd = (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * e + 2];
+    const tokmm::Chain ch = tokmm::chain_at<DT>(wd, units, (rr / TILE_ROWS) * nb * TILE_ROWS + rr % TILE_ROWS);
     float acc[16];
-    tokmm::tile_q6k<true>(wd, units, ubase, nb, arow, (LAS float *)s_da[wave], j, half, acc);
+    tokmm::tile_run<DT, true>(ch, nb, x, (LAS uint8_t *)s_tile, acc);
     if (row < rows) {
         GAS float *out = (GAS float *)(ws + P.out);
 #pragma unroll
@@ -1125,9 +1139,9 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
                        hipStream_t s) {
     if (int rc = moe_check(d, h, ws)) return rc;
     if (T <= 0 || T > 65536) return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld outside 1..65536", (long long)T);
-    if (d->expert_dt != DT_Q6_K || d->ds > 0)
-        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_prefill: routed Q6_K experts without a shared expert only "
-                           "(expert dtype %d, ds %lld)", d->expert_dt, (long long)d->ds);
+    if (!tokmm::tile_dt(d->expert_dt) || d->ds > 0)
+        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_prefill: routed Q4_K / Q5_K / Q6_K experts without a shared "
+                           "expert only (expert dtype %d, ds %lld)", d->expert_dt, (long long)d->ds);
     const tlm_hip_moe_desc dv = *d;
     const WsLayout L = ws_layout(*d);
     const PfLayout P = pf_layout(*d, T);
@@ -1138,10 +1152,18 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
                        P.tstride);
     hipLaunchKernelGGL(k_pf_route, dim3((unsigned)T), dim3(256), 0, s, dv, L, P, w8, ids, w);
     hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(256), 0, s, dv, P, w8);
-    hipLaunchKernelGGL(k_pf_gateup, dim3((unsigned)((d->de + 127) / 128), (unsigned)P.MT), dim3(256), 0, s, dv, L, P,
-                       w8);
+    const dim3 ggu((unsigned)((d->de + 63) / 64), (unsigned)P.MT), gdn((unsigned)((d->D + 127) / 128), (unsigned)P.MT);
+    switch (d->expert_dt) {
+    case DT_Q4_K: hipLaunchKernelGGL(k_pf_gateup<DT_Q4_K>, ggu, dim3(256), 0, s, dv, L, P, w8); break;
+    case DT_Q5_K: hipLaunchKernelGGL(k_pf_gateup<DT_Q5_K>, ggu, dim3(256), 0, s, dv, L, P, w8); break;
+    default: hipLaunchKernelGGL(k_pf_gateup<DT_Q6_K>, ggu, dim3(256), 0, s, dv, L, P, w8); break;
+    }
     hipLaunchKernelGGL(k_pf_hquant, dim3((unsigned)(d->de / 256), (unsigned)(T * d->k)), dim3(64), 0, s, dv, P, w8);
-    hipLaunchKernelGGL(k_pf_down, dim3((unsigned)((d->D + 127) / 128), (unsigned)P.MT), dim3(256), 0, s, dv, P, w8);
+    switch (d->expert_dt) {
+    case DT_Q4_K: hipLaunchKernelGGL(k_pf_down<DT_Q4_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
+    case DT_Q5_K: hipLaunchKernelGGL(k_pf_down<DT_Q5_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
+    default: hipLaunchKernelGGL(k_pf_down<DT_Q6_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
+    }
     hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((d->D + 255) / 256), (unsigned)T), dim3(256), 0, s, dv, P, h,
                        w8);
     return tlmh_check(hipGetLastError(), "moe_prefill launch");
