@@ -296,6 +296,18 @@ __device__ __forceinline__ float fma_chunk(const float (&v)[RCH], const LAS floa
     return r;
 }
 
+/* The 32 lane partials of a router dot (lanes 0-31 and 32-63 separately):
+ * lane 0 of each half ends with ((r0 + r16) + (r8 + r24)) + ...: the
+ * reference's pairing (i, i+16), (i, i+8), (i, i+4), (i, i+2), (i, i+1)
+ * (src/lib/tlm_quant.c:724-738); row_shl:n hands lane i the value of lane i+n */
+__device__ __forceinline__ float reduce32(float r) {
+    float s = r + __shfl_xor(r, 16, 64);
+    s = s + dpp_f32<0x108>(s);
+    s = s + dpp_f32<0x104>(s);
+    s = s + dpp_f32<DPP_XOR2>(s);
+    return s + dpp_f32<DPP_XOR1>(s);
+}
+
 /* blockIdx.y = token (prefill): its residual at hptr + y * D, its workspace at
  * ws + y * tstride; a decode launch has one token. */
 __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
@@ -418,14 +430,7 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
         }
     }
     if (ctail < D) r = fma_chunk<true>(vt, xb, ctail, hl, D, r);
-    /* lane 0 of each half ends with ((r0 + r16) + (r8 + r24)) + ...: the
-     * reference's pairing (i, i+16), (i, i+8), (i, i+4), (i, i+2), (i, i+1);
-     * row_shl:n hands lane i the value of lane i+n */
-    float s = r + __shfl_xor(r, 16, 64);
-    s = s + dpp_f32<0x108>(s);
-    s = s + dpp_f32<0x104>(s);
-    s = s + dpp_f32<DPP_XOR2>(s);
-    const float res = s + dpp_f32<DPP_XOR1>(s);
+    const float res = reduce32(r);
     if (live && hl == 0) ((GAS float *)(ws + L.logits))[row] = res;
 
     /* group b quantises activation block b for the experts / shared expert
@@ -772,8 +777,10 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
 /* ======================================================================
  * Prefill: T tokens through the block at once (src/lib/tlm_model.c:1105-1113
  * runs the decode step per token; the MoE block has no cross-token terms, so
- * batching keeps every token's bits).  K1 runs per token (blockIdx.y); each
- * token routes as in K2; (token, rank) pairs are bucketed by expert into
+ * batching keeps every token's bits).  Each token is normalised and quantised
+ * by one wave as K1 does it; router logits come 16 tokens x 8 rows per group
+ * in K1's dot order; each token routes as in K2; (token, rank) pairs are
+ * bucketed by expert into
  * slots; each expert's gate / up / down rows stream once per 32 of its slots
  * through the int8 MFMA tile; the combine runs per token in rank order.
  * ==================================================================== */
@@ -814,6 +821,128 @@ inline PfLayout pf_layout(const tlm_hip_moe_desc &d, int64_t T) {
     P.out = o;      o += al256(pairs * d.D * 4);
     P.total = o;
     return P;
+}
+
+/* Per (block b, token) one wave: xb = rmsnorm(h) with the router launch's
+ * lane order and tree (same bits; every wave of a token sums the same
+ * squares), block b of xb published to the token's workspace and quantised
+ * to Q8_K in the split layout.  D is a multiple of 256, so lane l's f32x4
+ * l + 64 b is lane l's part of block b. */
+__global__ __launch_bounds__(64) void k_pf_norm(tlm_hip_moe_desc d, WsLayout L, PfLayout P, const float *__restrict__ h,
+                                                uint8_t *ws) {
+    args_now(d.D, d.eps, d.ffn_norm, L.xb, L.xe, P.tok, P.tstride, h, ws);
+    const int lane = threadIdx.x, b = blockIdx.x;
+    const int64_t D = d.D;
+    const int nb = (int)(D / 256);
+    const GAS f32x4 *h4 = (const GAS f32x4 *)(h + (size_t)blockIdx.y * D);
+    GAS uint8_t *wst = (GAS uint8_t *)(ws + P.tok + (size_t)blockIdx.y * P.tstride);
+    const f32x4 nv = ((const GAS f32x4 *)d.ffn_norm)[lane + 64 * b];
+    constexpr int NV = 8;                  /* 16-byte loads per lane per batch, all in flight at once */
+    double ss = 0.0;
+    f32x4 mine = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 < nb; j0 += NV) {
+        f32x4 hv[NV];
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+            if (j0 + j < nb) hv[j] = h4[lane + 64 * (j0 + j)];
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+            if (j0 + j < nb) {
+#pragma unroll
+                for (int t = 0; t < 4; t++) ss += (double)hv[j][t] * (double)hv[j][t];
+                if (j0 + j == b) mine = hv[j];
+            }
+    }
+    ss = wave_sum_f64(ss);
+    const float rn = 1.0f / sqrtf((float)(ss / (double)D) + d.eps);
+    f32x4 o;
+#pragma unroll
+    for (int t = 0; t < 4; t++) o[t] = mine[t] * rn * nv[t];
+    ((GAS f32x4 *)(wst + L.xb))[lane + 64 * b] = o;
+    GAS uint8_t *xe = wst + L.xe;
+    quant_block_to(DT_Q8_K, o, true, lane, (GAS uint32_t *)xe, (GAS int16_t *)(xe + nb * 256),
+                   (GAS float *)(xe + nb * 288), b);
+}
+
+/* Router logits of 16 tokens x 8 router rows per group: the tokens' xb in
+ * LDS a 512-value chunk at a time, each thread one row's lane (i mod 32) for
+ * all 16 tokens, fmaf in element order, then reduce32 - every (token, row)
+ * dot has the decode launch's order and bits.  The chunk is stored
+ * transposed, [token][lane][m] for element c0 + lane + 32 m (lane rows 80
+ * bytes apart: 16-byte reads of 8 lanes fall on distinct banks), so a lane
+ * reads four of its values at once; the next chunk's values and router
+ * weights are in flight in registers while a chunk computes. */
+constexpr int PFL_ROWS = 8, PFL_TOK = 16, PFL_CH = 512, PFL_M = PFL_CH / 32, PFL_LS = 20;
+__global__ __launch_bounds__(256) void k_pf_logits(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws) {
+    __shared__ __align__(16) float s_x[PFL_TOK * 32 * PFL_LS];
+    args_now(d.D, d.E, d.router_w, L.xb, L.logits, P.tok, P.tstride, P.T, ws);
+    const int tid = threadIdx.x, hl = tid & 31;
+    const int64_t D = d.D, e = (int64_t)blockIdx.x * PFL_ROWS + (tid >> 5);
+    const int t0 = (int)blockIdx.y * PFL_TOK;
+    const GAS float *wr = (const GAS float *)d.router_w + (e < d.E ? e : d.E - 1) * D + hl;
+    /* staging: thread tid loads f32x4 q = tid % 128 (elements 4q..4q+3 of the
+     * chunk) of tokens tid / 128 + 2 k, k = 0..7 */
+    const int sq = tid & 127, st = tid >> 7;
+    const GAS f32x4 *xrow[PFL_TOK / 2];
+#pragma unroll
+    for (int k = 0; k < PFL_TOK / 2; k++) {
+        const int tt = t0 + st + 2 * k < P.T ? t0 + st + 2 * k : (int)P.T - 1;
+        xrow[k] = (const GAS f32x4 *)(ws + P.tok + (size_t)tt * P.tstride + L.xb) + sq;
+    }
+    auto load_x = [&](int64_t c0, int ch, f32x4 (&xv)[PFL_TOK / 2]) {
+#pragma unroll
+        for (int k = 0; k < PFL_TOK / 2; k++) xv[k] = 4 * sq < ch ? xrow[k][c0 / 4] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    auto load_w = [&](int64_t c0, int ch, float (&wv)[PFL_M]) {
+#pragma unroll
+        for (int m = 0; m < PFL_M; m++) wv[m] = 32 * m < ch ? wr[c0 + 32 * m] : 0.0f;
+    };
+    float acc[PFL_TOK];
+#pragma unroll
+    for (int t = 0; t < PFL_TOK; t++) acc[t] = 0.0f;
+    f32x4 xv[PFL_TOK / 2];
+    float wv[PFL_M], wn[PFL_M];
+    int ch = D < PFL_CH ? (int)D : PFL_CH;          /* D is a multiple of 32 */
+    load_x(0, ch, xv);
+    load_w(0, ch, wv);
+    for (int64_t c0 = 0; c0 < D; c0 += PFL_CH) {
+        __syncthreads();                            /* the last chunk is consumed */
+#pragma unroll
+        for (int k = 0; k < PFL_TOK / 2; k++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = 4 * sq + u;           /* element c0 + i -> lane i % 32, m = i / 32 */
+                s_x[((st + 2 * k) * 32 + (i & 31)) * PFL_LS + (i >> 5)] = xv[k][u];
+            }
+        __syncthreads();
+        const int cur = ch;
+        const int64_t c1 = c0 + PFL_CH;
+        if (c1 < D) {
+            ch = D - c1 < PFL_CH ? (int)(D - c1) : PFL_CH;
+            load_x(c1, ch, xv);
+            load_w(c1, ch, wn);
+        }
+        const LAS float *xl = (const LAS float *)s_x + hl * PFL_LS;
+#pragma unroll
+        for (int m4 = 0; m4 < PFL_M / 4; m4++) {
+            if (32 * 4 * m4 >= cur) break;
+#pragma unroll
+            for (int t = 0; t < PFL_TOK; t++) {
+                const f32x4 x4 = *(const LAS f32x4 *)(xl + t * 32 * PFL_LS + 4 * m4);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (32 * (4 * m4 + k) < cur) acc[t] = fmaf(wv[4 * m4 + k], x4[k], acc[t]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < PFL_M; m++) wv[m] = wn[m];
+    }
+#pragma unroll
+    for (int t = 0; t < PFL_TOK; t++) {
+        const float res = reduce32(acc[t]);
+        if (hl == 0 && e < d.E && t0 + t < P.T)
+            ((GAS float *)(ws + P.tok + (size_t)(t0 + t) * P.tstride + L.logits))[e] = res;
+    }
 }
 
 __global__ __launch_bounds__(256) void k_pf_route(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws,
@@ -912,11 +1041,11 @@ __global__ __launch_bounds__(256) void k_pf_bucket(tlm_hip_moe_desc d, PfLayout 
 
 /* Rows of gate and up: 64 rows per group over the tile's (up to 32) slots of
  * one expert - waves 0-1 stream gate rows, waves 2-3 the same rows of up -
- * then, through LDS, h = silu(g) * u per (slot, row). */
+ * then, through LDS, h = silu(g) * u per (slot, row) by all four waves. */
 template <int DT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_pf_gateup(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws) {
     __shared__ __align__(16) uint8_t s_tile[tokmm::tile_lds_bytes<DT>()];
-    static_assert(tokmm::tile_lds_bytes<DT>() >= 2 * 16 * 64 * 4, "exchange area");
+    static_assert(tokmm::tile_lds_bytes<DT>() >= 2 * 32 * 64 * 4, "g / u area");
     args_now(d.D, d.de, d.experts, L.xe, P.tok, P.tstride, P.tiles, P.slot_tok, P.hbuf, ws);
     const GAS int32_t *tl = (const GAS int32_t *)(ws + P.tiles) + 3 * blockIdx.y;
     const int e = tl[0];
@@ -936,20 +1065,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const tokmm::Chain ch = tokmm::chain_at<DT>((const uint8_t *)xt[3 * e + up], units, ubase);
     float acc[16];
     tokmm::tile_run<DT, true>(ch, nb, x, (LAS uint8_t *)s_tile, acc);
-    /* the tile ended on a barrier: its LDS is free for the up values */
-    LAS float *xch = (LAS float *)s_tile + (wave & 1) * 16 * 64 + lane;
-    if (up) {
+    /* the tile ended on a barrier: its LDS takes g and u of the group's 64
+     * rows x 32 slots ([gate|up][slot][row]), then every thread forms 8 of
+     * the h values (slots past the tile's last are skipped) */
+    LAS float *gu = (LAS float *)s_tile;
+    const int rl = (wave & 1) * 32 + (lane & 31);
 #pragma unroll
-        for (int v = 0; v < 16; v++) xch[64 * v] = acc[v];
-    }
+    for (int v = 0; v < 16; v++) gu[(up * 32 + 8 * (v >> 2) + 4 * half + (v & 3)) * 64 + rl] = acc[v];
     __syncthreads();
-    if (!up && row < rows) {
+    const int r2 = threadIdx.x & 63;
+    const int64_t orow = (int64_t)blockIdx.x * 64 + r2;
+    if (orow < rows) {
         GAS float *hb = (GAS float *)(ws + P.hbuf);
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int i = 8 * (v >> 2) + 4 * half + (v & 3);
-            const float g = acc[v], u = xch[64 * v];
-            if (i < n) hb[(size_t)(s0 + i) * rows + row] = g / (1.0f + exp_rn(-g)) * u;
+        for (int q = 0; q < 8; q++) {
+            const int i = 4 * q + (threadIdx.x >> 6);
+            if (i < n) {
+                const float g = gu[i * 64 + r2], u = gu[(32 + i) * 64 + r2];
+                hb[(size_t)(s0 + i) * rows + orow] = g / (1.0f + exp_rn(-g)) * u;
+            }
         }
     }
 }
@@ -1133,7 +1267,8 @@ size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T) {
     return (d && T > 0) ? pf_layout(*d, T).total : 0;
 }
 
-/* T tokens: K1 per token, routing per token, bucketing, gate/up + SwiGLU,
+/* T tokens: norm + quantisation per token, batched router logits, routing per
+ * token, bucketing, gate/up + SwiGLU,
  * h quantisation, down, combine. */
 int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
                        hipStream_t s) {
@@ -1146,10 +1281,10 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
     const WsLayout L = ws_layout(*d);
     const PfLayout P = pf_layout(*d, T);
     uint8_t *w8 = (uint8_t *)ws;
-    const unsigned g1 = (unsigned)router_groups(*d);
-    const size_t lds1 = al256((size_t)d->D * 8);
-    hipLaunchKernelGGL(k_moe_router, dim3(g1, (unsigned)T), dim3(64), lds1, s, dv, L, (const float *)h, w8 + P.tok,
-                       P.tstride);
+    hipLaunchKernelGGL(k_pf_norm, dim3((unsigned)(d->D / 256), (unsigned)T), dim3(64), 0, s, dv, L, P, (const float *)h,
+                       w8);
+    hipLaunchKernelGGL(k_pf_logits, dim3((unsigned)((d->E + PFL_ROWS - 1) / PFL_ROWS), (unsigned)((T + PFL_TOK - 1) / PFL_TOK)),
+                       dim3(256), 0, s, dv, L, P, w8);
     hipLaunchKernelGGL(k_pf_route, dim3((unsigned)T), dim3(256), 0, s, dv, L, P, w8, ids, w);
     hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(256), 0, s, dv, P, w8);
     const dim3 ggu((unsigned)((d->de + 63) / 64), (unsigned)P.MT), gdn((unsigned)((d->D + 127) / 128), (unsigned)P.MT);
