@@ -986,7 +986,7 @@ __global__ __launch_bounds__(256) void k_moe_route(tlm_hip_moe_desc d, WsLayout 
 /* One group: slots grouped by expert (order within an expert is free - every
  * slot is computed on its own), and the tile table of 32-slot runs. */
 __global__ __launch_bounds__(256) void k_pf_bucket(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
-    __shared__ int s_cnt[MAXE], s_off[MAXE], s_toff[MAXE], s_scan[256];
+    __shared__ int s_cnt[MAXE], s_off[MAXE], s_toff[MAXE], s_wc[4], s_wt[4];
     args_now(d.E, d.k, P.T, P.MT, P.pair_e, P.pair_pos, P.slot_of, P.slot_tok, P.tiles, ws);
     const int tid = threadIdx.x, E = d.E;
     const int npair = (int)(P.T * d.k);
@@ -994,38 +994,64 @@ __global__ __launch_bounds__(256) void k_pf_bucket(tlm_hip_moe_desc d, PfLayout 
     GAS int32_t *ppos = (GAS int32_t *)(ws + P.pair_pos);
     if (tid < MAXE) s_cnt[tid] = 0;
     __syncthreads();
-    for (int p = tid; p < npair; p += 256) {
-        int e = pe[p];
-        e = (e < 0 || e >= E) ? 0 : e;
-        ppos[p] = atomicAdd(&s_cnt[e], 1);
+    /* 16 pairs per thread per batch: their loads in flight at once */
+    constexpr int BP = 16;
+    for (int p0 = 0; p0 < npair; p0 += 256 * BP) {
+        int ev[BP];
+#pragma unroll
+        for (int q = 0; q < BP; q++) {
+            const int p = p0 + tid + 256 * q;
+            const int e = p < npair ? pe[p] : 0;
+            ev[q] = (e < 0 || e >= E) ? 0 : e;
+        }
+#pragma unroll
+        for (int q = 0; q < BP; q++) {
+            const int p = p0 + tid + 256 * q;
+            if (p < npair) ppos[p] = atomicAdd(&s_cnt[ev[q]], 1);
+        }
     }
     __syncthreads();
-    /* exclusive scans of slot counts and tile counts over the experts */
+    /* exclusive scans of slot counts and tile counts over the experts: wave
+     * scans, then the wave totals */
     const int c = tid < E ? s_cnt[tid] : 0;
     const int nt = (c + tokmm::TM_TOK - 1) / tokmm::TM_TOK;
-    for (int pass = 0; pass < 2; pass++) {
-        int v = pass == 0 ? c : nt;
-        s_scan[tid] = v;
-        __syncthreads();
-        for (int off = 1; off < 256; off <<= 1) {
-            const int o = tid >= off ? s_scan[tid - off] : 0;
-            __syncthreads();
-            v += o;
-            s_scan[tid] = v;
-            __syncthreads();
-        }
-        if (tid < E) (pass == 0 ? s_off : s_toff)[tid] = v - (pass == 0 ? c : nt);
-        __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6;
+    int ic = c, it = nt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int a = __shfl_up(ic, off, 64), b = __shfl_up(it, off, 64);
+        if (lane >= off) { ic += a; it += b; }
     }
-    const int tiles_used = s_scan[255];
+    if (lane == 63) { s_wc[wave] = ic; s_wt[wave] = it; }
+    __syncthreads();
+    int bc = 0, bt = 0;
+    for (int w = 0; w < wave; w++) { bc += s_wc[w]; bt += s_wt[w]; }
+    if (tid < E) {
+        s_off[tid] = bc + ic - c;
+        s_toff[tid] = bt + it - nt;
+    }
+    const int tiles_used = s_wt[0] + s_wt[1] + s_wt[2] + s_wt[3];
+    __syncthreads();
     GAS int32_t *slot_of = (GAS int32_t *)(ws + P.slot_of);
     GAS int32_t *slot_tok = (GAS int32_t *)(ws + P.slot_tok);
-    for (int p = tid; p < npair; p += 256) {
-        int e = pe[p];
-        e = (e < 0 || e >= E) ? 0 : e;
-        const int slot = s_off[e] + ppos[p];
-        slot_of[p] = slot;
-        slot_tok[slot] = p / d.k;
+    for (int p0 = 0; p0 < npair; p0 += 256 * BP) {
+        int ev[BP], pv[BP];
+#pragma unroll
+        for (int q = 0; q < BP; q++) {
+            const int p = p0 + tid + 256 * q;
+            const int e = p < npair ? pe[p] : 0;
+            ev[q] = (e < 0 || e >= E) ? 0 : e;
+            pv[q] = p < npair ? ppos[p] : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < BP; q++) {
+            const int p = p0 + tid + 256 * q;
+            if (p < npair) {
+                const int slot = s_off[ev[q]] + pv[q];
+                slot_of[p] = slot;
+                slot_tok[slot] = p / d.k;
+            }
+        }
     }
     GAS int32_t *tiles = (GAS int32_t *)(ws + P.tiles);
     if (tid < E) {
@@ -1136,30 +1162,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 __global__ __launch_bounds__(256) void k_pf_combine(tlm_hip_moe_desc d, PfLayout P, float *__restrict__ h,
                                                     uint8_t *ws) {
     args_now(d.D, d.k, P.pair_w, P.slot_of, P.out, h, ws);
-    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    /* four rows per thread (D is a multiple of 256), 16-byte loads */
+    const int64_t r4 = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int t = blockIdx.y;
-    if (row >= d.D) return;
+    if (4 * r4 >= d.D) return;
     const GAS float *pw = (const GAS float *)(ws + P.pair_w) + (size_t)t * d.k;
     const GAS int32_t *so = (const GAS int32_t *)(ws + P.slot_of) + (size_t)t * d.k;
     const GAS float *out = (const GAS float *)(ws + P.out);
-    float ev[MAXK], wv[MAXK];
+    f32x4 ev[MAXK];
+    float wv[MAXK];
 #pragma unroll
     for (int q = 0; q < MAXK; q++) {
         if (q < d.k) {
             wv[q] = pw[q];
-            ev[q] = out[(size_t)so[q] * d.D + row];
+            ev[q] = *(const GAS f32x4 *)(out + (size_t)so[q] * d.D + 4 * r4);
         }
     }
-    const float hv = h[(size_t)t * d.D + row];
-    float ffn = 0.0f;
+    GAS f32x4 *hp = (GAS f32x4 *)(h + (size_t)t * d.D) + r4;
+    const f32x4 hv = *hp;
+    f32x4 o;
 #pragma unroll
-    for (int q = 0; q < MAXK; q++) {
-        if (q < d.k) {
-            const float c = wv[q] * ev[q];
-            ffn += c;
+    for (int c = 0; c < 4; c++) {
+        float ffn = 0.0f;
+#pragma unroll
+        for (int q = 0; q < MAXK; q++) {
+            if (q < d.k) {
+                const float x = wv[q] * ev[q][c];
+                ffn += x;
+            }
         }
+        o[c] = hv[c] + ffn;
     }
-    h[(size_t)t * d.D + row] = hv + ffn;
+    *hp = o;
 }
 
 /* ---- instantiation table: [expert dtype][shared dtype or none] --------------- */
@@ -1299,7 +1333,7 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
     case DT_Q5_K: hipLaunchKernelGGL(k_pf_down<DT_Q5_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
     default: hipLaunchKernelGGL(k_pf_down<DT_Q6_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
     }
-    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((d->D + 255) / 256), (unsigned)T), dim3(256), 0, s, dv, P, h,
+    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((d->D + 1023) / 1024), (unsigned)T), dim3(256), 0, s, dv, P, h,
                        w8);
     return tlmh_check(hipGetLastError(), "moe_prefill launch");
 }
