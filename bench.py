@@ -69,15 +69,37 @@ PREFILL_T = 512
 INT8_PEAK_TOPS = 5000.0                  # MI355X dense int8 MFMA
 
 
-def prefill_bench(torch, dev, W, router_w, ffn_norm, gen):
-    """One 512-token chunk through the same block (layer copy 0's 128
-    experts): router, routing, tokens bucketed per expert, grouped gate/up +
-    SwiGLU and down on int8 MFMA, combine.  Algorithmic bytes = all 128
-    experts once (every expert gets tokens at this size); int8 ops = 2 x
-    tokens x top-8 x 3 x 768 x 2048."""
+Q5_K = 13
+MAT_BYTES_Q5K = DE * D // 256 * 176      # one packed Q5_K matrix: 1,081,344 B
+
+
+def make_weights_q5k(torch, dev, seed):
+    """128 random-code Q5_K experts in the packed layout (whole 176-byte
+    blocks in tile order): random code / scale bytes, modest f16 d and
+    non-negative f16 dmin in each block's first four bytes."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    n_mats = E * 3
+    W = torch.empty((n_mats, MAT_BYTES_Q5K), dtype=torch.uint8, device=dev)
+    W.random_(0, 256, generator=g)
+    units = W.view(n_mats, -1, 176)
+    d = (torch.randn(units.shape[:2], generator=g, device=dev) * 2e-3).to(torch.float16)
+    dm = (torch.randn(units.shape[:2], generator=g, device=dev).abs() * 2e-3).to(torch.float16)
+    units[:, :, 0:2] = d.view(torch.uint8).view(n_mats, -1, 2)
+    units[:, :, 2:4] = dm.view(torch.uint8).view(n_mats, -1, 2)
+    return W
+
+
+def prefill_bench(torch, dev, W, mat_bytes, dt, router_w, ffn_norm, gen):
+    """One 512-token chunk through the block (128 experts of dtype dt, matrix
+    stride mat_bytes in W): per-token norm + quantisation, batched router
+    logits, routing, tokens bucketed per expert, grouped gate/up + SwiGLU and
+    down on int8 MFMA, combine.  Algorithmic bytes = all 128 experts once
+    (every expert gets tokens at this size); int8 ops = 2 x tokens x top-8 x
+    3 x 768 x 2048."""
     from tierlm_amd import MoeBlock
-    ptrs = [W.data_ptr() + (e * 3 + j) * MAT_BYTES for e in range(E) for j in range(3)]
-    blk = MoeBlock(D=D, de=DE, E=E, k=K, expert_dt=Q6_K, ffn_norm=ffn_norm, router_w=router_w, expert_ptrs=ptrs,
+    ptrs = [W.data_ptr() + (e * 3 + j) * mat_bytes for e in range(E) for j in range(3)]
+    blk = MoeBlock(D=D, de=DE, E=E, k=K, expert_dt=dt, ffn_norm=ffn_norm, router_w=router_w, expert_ptrs=ptrs,
                    router=0, eps=1e-6, device=dev)
     H0 = torch.randn((PREFILL_T, D), generator=gen, device=dev)
     h = H0.clone()
@@ -93,16 +115,17 @@ def prefill_bench(torch, dev, W, router_w, ffn_norm, gen):
         ev1.synchronize()
         us = ev0.elapsed_time(ev1) * 1e3
         best = us if best is None else min(best, us)
-    nbytes = E * EXPERT_BYTES
+    nbytes = E * 3 * mat_bytes
     ops = 2.0 * PREFILL_T * K * 3 * DE * D
-    log(f"bench: prefill {PREFILL_T} tokens: {best:.1f} us ({PREFILL_T / best * 1e6:.0f} tok/s), "
+    name = {Q6_K: "Q6_K", Q5_K: "Q5_K"}[dt]
+    log(f"bench: prefill {PREFILL_T} tokens ({name}): {best:.1f} us ({PREFILL_T / best * 1e6:.0f} tok/s), "
         f"experts {nbytes / best / 1e3:.0f} GB/s, int8 {ops / best / 1e6:.1f} TOP/s")
     return {"tokens": PREFILL_T, "us": round(best, 1), "tok_s": round(PREFILL_T / best * 1e6, 1),
             "expert_bytes": nbytes, "expert_GBps": round(nbytes / best / 1e3, 1),
             "hbm_frac": round(nbytes / best / 1e3 / HBM_PEAK_GBS, 4), "int8_ops": ops,
             "int8_TOPs": round(ops / best / 1e6, 2), "mfma_util": round(ops / best / 1e6 / INT8_PEAK_TOPS, 4),
             "timing": "HIP events around one tlm_hip_moe_prefill call (best of 5)",
-            "workload": "512-token chunk, Qwen3-30B-A3B-shape block, 128 random-code Q6_K experts, "
+            "workload": f"512-token chunk, Qwen3-30B-A3B-shape block, 128 random-code {name} experts, "
                         "tokens routed by the seeded f32 router and bucketed per expert"}
 
 
@@ -464,7 +487,12 @@ def main():
         log(f"bench: copy check {args.copy_check_mib} MiB done")
         del src, dst
 
-    prefill = None if args.no_prefill else prefill_bench(torch, dev, W, router_w, ffn_norm, gen)
+    prefill = prefill_q5k = None
+    if not args.no_prefill:
+        prefill = prefill_bench(torch, dev, W, MAT_BYTES, Q6_K, router_w, ffn_norm, gen)
+        W5 = make_weights_q5k(torch, dev, seed=5)
+        prefill_q5k = prefill_bench(torch, dev, W5, MAT_BYTES_Q5K, Q5_K, router_w, ffn_norm, gen)
+        del W5
     slot_cache = None if args.no_store else slot_cache_bench(torch, dev, router_w, ffn_norm, gen, args.store_tokens)
     c1 = None if args.no_c1 or not os.path.exists(C1_STORE) else c1_bench(3)
     if not args.no_c3:
@@ -504,6 +532,7 @@ def main():
                      "stream_read_kernel": "k_mv_packed<Q6_K> over ~2 GB of resident expert bytes, one launch (best of 5)"},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "prefill_q5k": prefill_q5k,
         "slot_cache": slot_cache,
         "c1_whole_step": c1,
         "qwen3_30b_a3b_whole_model": c3,

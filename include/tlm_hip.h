@@ -115,7 +115,9 @@ int tlm_hip_mv_job(const tlm_hip_seg *segs, int nseg, void *stream);
  * for every token t and row r, exactly the decode result:
  *   Y[t * rows + r] == tlm_hip_matvec_packed(dt, Wp, rows, n, act_t, .)[r]
  * act: ntok activation vectors in the reference layout (Q8_K blocks,
- * n/256 * 292 bytes each, consecutive, 4-byte aligned).  dt: Q6_K. */
+ * n/256 * 292 bytes each, consecutive, 4-byte aligned; well-formed, i.e. each
+ * bsum the sum of its 16 codes, as the quantiser writes them).  dt: Q4_K, Q5_K
+ * or Q6_K. */
 int tlm_hip_matmul_tokens(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok,
                           float *Y, void *stream);
 
@@ -175,9 +177,9 @@ int tlm_hip_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, f
  * block has no cross-token terms, so this gives every token exactly the
  * result of tlm_hip_moe_layer on it: h[t*D .. t*D+D) += MoE(h_t), routing in
  * ids / w [T*k] (either may be NULL).  Tokens are bucketed by expert and each
- * expert's rows stream once per 32 of its tokens (int8 MFMA).  Routed Q6_K
- * experts, no shared expert.  workspace: tlm_hip_moe_prefill_workspace_bytes
- * bytes, 256-byte aligned. */
+ * expert's rows stream once per 32 of its tokens (int8 MFMA).  Routed Q4_K,
+ * Q5_K or Q6_K experts, no shared expert (others: TLM_HIP_EUNSUP).
+ * workspace: tlm_hip_moe_prefill_workspace_bytes bytes, 256-byte aligned. */
 size_t tlm_hip_moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T);
 int tlm_hip_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w,
                         void *workspace, void *stream);
