@@ -225,6 +225,99 @@ def slot_cache_bench(torch, dev, router_w, ffn_norm, gen, tokens):
     return out
 
 
+def c5_bench(torch, dev, tokens, cache_gb, pool=64, gamma=0.14, seed=11):
+    """The HBM slot cache at the Qwen3-235B-A22B shape: 94 layers x 128
+    experts (D 4096, expert width 1536, top-8) of Q4_K, 10.6 MB each (127.7 GB
+    in all), served from pinned host memory through tlm_hip_moe_layer_store
+    with the cache capped at cache_gb, the next layer's router predicting its
+    experts (lookahead hints), one router per layer.  Routing heat: sigmoid
+    routing (kind 2) whose selection bias is -gamma * ln(rank + 1) per expert,
+    which puts about Zipf(1.1)'s share of the selections on the hottest
+    experts (the measured share is reported).  Every (layer, expert) has its
+    own slot and is loaded over PCIe on a miss; their payload bytes come from
+    a pool of `pool` distinct random-code payloads (the bytes do not change
+    the traffic), so host memory stays under 1 GB.  A second, short run caps
+    the cache at 8 GB, where most selections miss and stream over PCIe."""
+    import numpy as np
+    from tierlm_amd import MoeBlock
+    from tierlm_amd.store import HipStore
+    L5, D5, DE5, Q4_K = 94, 4096, 1536, 12
+    rg, rd = D5 // 256 * 144, DE5 // 256 * 144          # gate/up and down row bytes
+    off = [0, DE5 * rg, 2 * DE5 * rg]
+    plen = 2 * DE5 * rg + D5 * rd                        # 10,616,832 B
+    rng = np.random.default_rng(seed)
+    buf = torch.empty(pool * plen, dtype=torch.uint8, pin_memory=True)
+    nbl = plen // 144
+    for i in range(pool):
+        blocks = rng.integers(0, 256, size=(nbl, 144), dtype=np.uint8)
+        blocks[:, 0:2] = (rng.standard_normal((nbl, 1)) * 2e-3).astype(np.float16).view(np.uint8)
+        blocks[:, 2:4] = (np.abs(rng.standard_normal((nbl, 1))) * 2e-3).astype(np.float16).view(np.uint8)
+        buf[i * plen:(i + 1) * plen].copy_(torch.from_numpy(blocks.reshape(-1)))
+    srcs = [{"layer": l, "id": e, "dtype": Q4_K, "item_off": off,
+             "payload": buf[((l * E + e) % pool) * plen:((l * E + e) % pool + 1) * plen]}
+            for l in range(L5) for e in range(E)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    ffn_norm = torch.ones(D5, device=dev)
+    bias = torch.tensor(-gamma * np.log(np.arange(E) + 1.0), dtype=torch.float32, device=dev)
+    dummy = torch.zeros(16, dtype=torch.uint8, device=dev)
+    blocks = []
+    for l in range(L5):
+        # each layer's hot experts are a different permutation of the ids
+        perm = torch.randperm(E, generator=g, device=dev)
+        blocks.append(MoeBlock(D=D5, de=DE5, E=E, k=K, expert_dt=Q4_K, ffn_norm=ffn_norm,
+                               router_w=torch.randn((E, D5), generator=g, device=dev) / float(np.sqrt(D5)),
+                               expert_ptrs=[dummy.data_ptr()] * (3 * E), router=2, router_bias=bias[perm].contiguous(),
+                               eps=1e-6, device=dev))
+    H = torch.randn((tokens + 40, D5), generator=g, device=dev)
+
+    def run(cap_gb, ntok, warm):
+        st = HipStore(srcs, d_model=D5, d_expert=DE5, top_k=K, budget_bytes=int(cap_gb * (1 << 30)), prefetch=1)
+        sel = np.zeros((L5, E), np.int64)
+
+        def token(t, count):
+            for l in range(L5):
+                hints = [(blocks[l + 1], l + 1, K)] if l + 1 < L5 else []
+                ids, _ = blocks[l].step_store(st, l, H[t].clone(), hints)
+                if count:
+                    sel[l, ids] += 1
+                st.tick()
+
+        for t in range(warm):                            # fill the cache and reach the heat's steady state
+            token(t, False)
+        s0 = st.stats()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(warm, warm + ntok):
+            token(t, True)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        s1 = st.stats()
+        miss = (s1["misses"] - s0["misses"]) / ntok
+        fs = np.sort(sel, axis=1)[:, ::-1].sum(axis=0)
+        r = {"cache_GB": cap_gb, "slots": st.n_slots(), "tokens": ntok, "warmup_tokens": warm,
+             "tok_s": round(ntok / dt, 2), "ms_per_token": round(dt / ntok * 1e3, 2),
+             "misses_per_token": round(miss, 1), "hit_rate": round(1.0 - miss / (L5 * K), 4),
+             "miss_GBps": round(miss * plen * ntok / dt / 1e9, 2),
+             "heat_top10pct_share": round(float(fs[:13].sum() / fs.sum()), 3)}
+        st.close()
+        log(f"bench: C5 slot cache ({r['slots']} slots, {cap_gb:.0f} GB): {r['tok_s']:.2f} tok/s, "
+            f"{r['misses_per_token']:.1f} misses/token (hit rate {r['hit_rate']:.3f}), {r['miss_GBps']:.1f} GB/s "
+            f"over PCIe, heat top-13 share {r['heat_top10pct_share']}")
+        return r
+
+    out = {"model": "Qwen3-235B-A22B shape MoE stack: 94 layers, D 4096, 128 experts top-8 of width 1536, Q4_K, "
+                    "random codes (127.7 GB of experts)",
+           "expert_bytes": plen, **run(cache_gb, tokens, 40),
+           "heat": f"sigmoid routing, selection bias -{gamma} ln(rank + 1) (a Zipf(1.1)-like heat; Zipf(1.1) puts 0.61 "
+                   "of top-8 selections on the 13 hottest experts)",
+           "timing": "host wall clock around 94 tlm_hip_moe_layer_store calls per token (ctypes, routing read back "
+                     "per layer), after the warm-up tokens"}
+    out["small_cache"] = run(8.0, max(2, tokens // 4), 4)   # misses stream over PCIe
+    del blocks, buf
+    return out
+
+
 C1_STORE = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
 C1_TIERLM = os.path.join(ROOT, "oracle", "_ref", "bin", "tierlm")
 
@@ -337,6 +430,9 @@ def main():
     ap.add_argument("--no-c3", action="store_true", help="skip the full Qwen3-30B-A3B-shape model measurement")
     ap.add_argument("--c3-context", type=int, default=2048, help="positions the full-model decode runs to")
     ap.add_argument("--store-tokens", type=int, default=400, help="tokens per slot-cache decode measurement")
+    ap.add_argument("--no-c5", action="store_true", help="skip the Qwen3-235B-shape slot-cache measurement")
+    ap.add_argument("--c5-tokens", type=int, default=20, help="timed tokens of the Qwen3-235B-shape slot-cache run")
+    ap.add_argument("--c5-cache-gb", type=float, default=64.0, help="slot cache cap of that run (GB)")
     ap.add_argument("--copy-check-mib", type=int, default=0,
                     help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
                          "of known size, the scale for HBM byte counters")
@@ -499,6 +595,15 @@ def main():
         del W                                  # the block's 23.8 GB of experts; the model builds its own
         torch.cuda.empty_cache()
     c3 = None if args.no_c3 else c3_bench(1, args.c3_context)
+    c5 = None
+    if not args.no_c5:
+        torch.cuda.empty_cache()
+        try:
+            c5 = c5_bench(torch, dev, args.c5_tokens, args.c5_cache_gb)
+        except Exception as e:                 # recorded, so the rest of the line still prints
+            c5 = {"error": repr(e)}
+            log(f"bench: C5 slot cache failed: {e!r}")
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
@@ -536,6 +641,7 @@ def main():
         "slot_cache": slot_cache,
         "c1_whole_step": c1,
         "qwen3_30b_a3b_whole_model": c3,
+        "qwen3_235b_a22b_slot_cache": c5,
     }
     print(json.dumps(line), flush=True)
 
