@@ -778,7 +778,7 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
  * Prefill: T tokens through the block at once (src/lib/tlm_model.c:1105-1113
  * runs the decode step per token; the MoE block has no cross-token terms, so
  * batching keeps every token's bits).  Each token is normalised and quantised
- * by one wave as K1 does it; router logits come 16 tokens x 8 rows per group
+ * by one wave as K1 does it; router logits come 8 tokens x 8 rows per group
  * in K1's dot order; each token routes as in K2; (token, rank) pairs are
  * bucketed by expert into
  * slots; each expert's gate / up / down rows stream once per 32 of its slots
@@ -864,15 +864,15 @@ __global__ __launch_bounds__(64) void k_pf_norm(tlm_hip_moe_desc d, WsLayout L, 
                    (GAS float *)(xe + nb * 288), b);
 }
 
-/* Router logits of 16 tokens x 8 router rows per group: the tokens' xb in
+/* Router logits of 8 tokens x 8 router rows per group: the tokens' xb in
  * LDS a 512-value chunk at a time, each thread one row's lane (i mod 32) for
- * all 16 tokens, fmaf in element order, then reduce32 - every (token, row)
+ * all 8 tokens, fmaf in element order, then reduce32 - every (token, row)
  * dot has the decode launch's order and bits.  The chunk is stored
  * transposed, [token][lane][m] for element c0 + lane + 32 m (lane rows 80
  * bytes apart: 16-byte reads of 8 lanes fall on distinct banks), so a lane
  * reads four of its values at once; the next chunk's values and router
  * weights are in flight in registers while a chunk computes. */
-constexpr int PFL_ROWS = 8, PFL_TOK = 16, PFL_CH = 512, PFL_M = PFL_CH / 32, PFL_LS = 20;
+constexpr int PFL_ROWS = 8, PFL_TOK = 8, PFL_CH = 512, PFL_M = PFL_CH / 32, PFL_LS = 20;
 __global__ __launch_bounds__(256) void k_pf_logits(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws) {
     __shared__ __align__(16) float s_x[PFL_TOK * 32 * PFL_LS];
     args_now(d.D, d.E, d.router_w, L.xb, L.logits, P.tok, P.tstride, P.T, ws);
