@@ -79,16 +79,24 @@ class MoeBlock:
         block's router predicts k experts of that layer.  Returns the routing
         (ids, w) as host lists."""
         n = len(hints)
-        arr = (MoeHint * max(n, 1))()
-        self._hint_keep = []
-        for i, (blk, hl, hk) in enumerate(hints):
-            dsc = MoeDesc.from_buffer_copy(blk.desc)
-            dsc.k = hk
-            ws = blk._hint_ws(dsc)
-            self._hint_keep.append((dsc, ws))
-            arr[i] = MoeHint(C.pointer(dsc), hl, C.c_void_p(ws.data_ptr()))
-        ids = (C.c_int32 * self.desc.k)()
-        w = (C.c_float * self.desc.k)()
+        # the hint table is built once per (blocks, layers, k) and kept with
+        # the descriptors and workspaces it points at
+        key = tuple((id(blk), hl, hk) for blk, hl, hk in hints)
+        cache = self.__dict__.setdefault("_hint_cache", {})
+        if key not in cache:
+            arr = (MoeHint * max(n, 1))()
+            keep = []
+            for i, (blk, hl, hk) in enumerate(hints):
+                dsc = MoeDesc.from_buffer_copy(blk.desc)
+                dsc.k = hk
+                ws = blk._hint_ws(dsc)
+                keep.append((blk, dsc, ws))
+                arr[i] = MoeHint(C.pointer(dsc), hl, C.c_void_p(ws.data_ptr()))
+            cache[key] = (arr, keep)
+        arr = cache[key][0]
+        if getattr(self, "_route_out", None) is None:
+            self._route_out = ((C.c_int32 * self.desc.k)(), (C.c_float * self.desc.k)())
+        ids, w = self._route_out
         check(lib.tlm_hip_moe_layer_store(C.byref(self.desc), store.h, layer, C.c_void_p(h.data_ptr()), ids, w, arr,
                                           n, C.c_void_p(self.workspace.data_ptr()), stream()))
         return list(ids), list(w)
