@@ -63,6 +63,37 @@ def test_prefill_qwen3_shape_vs_oracle(hip, dev, dt):
         assert np.all(np.abs(got[t] - want_h) <= tol), t
 
 
+@pytest.mark.parametrize("dt", [oracle.Q5_K, oracle.Q6_K])
+def test_prefill_qwen3_shape_512_tokens(hip, dev, dt):
+    """The benchmarked chunk: 512 tokens through D 2048, 128 experts top-8,
+    de 768 (every expert holds tokens, many hold two 32-slot tiles); routing
+    of every token and the residual of every 8th token carry the decode
+    block's bits."""
+    case = build_moe_case(D=2048, de=768, E=128, k=8, ds=0, expert_dt=dt, seed=13, device=dev,
+                          weights="random_codes")
+    T = 512
+    rng = np.random.default_rng(21)
+    H = rng.standard_normal((T, case.D)).astype(np.float32)
+    h = torch.from_numpy(H.copy()).to(dev)
+    ids = torch.empty((T, case.k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, case.k), dtype=torch.float32, device=dev)
+    case.block.prefill(h, ids, w)
+    torch.cuda.synchronize()
+    got, got_ids, got_w = h.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()
+    counts = np.bincount(got_ids.ravel(), minlength=case.E)
+    assert counts.min() > 0 and (counts > 32).any()          # every expert used, some past one tile
+    for t in range(T):
+        case.block.route(torch.from_numpy(H[t].copy()).to(dev))
+        torch.cuda.synchronize()
+        assert np.array_equal(got_ids[t], case.block.ids.cpu().numpy()[:case.k]), t
+        assert np.array_equal(got_w[t].view(np.uint32), case.block.w.cpu().numpy()[:case.k].view(np.uint32)), t
+    for t in range(0, T, 8):
+        ht = torch.from_numpy(H[t].copy()).to(dev)
+        case.block(ht)
+        torch.cuda.synchronize()
+        assert np.array_equal(got[t].view(np.uint32), ht.cpu().numpy().view(np.uint32)), f"token {t}"
+
+
 @pytest.mark.parametrize("router", [1, 2])
 def test_prefill_routers_and_mask(hip, dev, router):
     mask = np.zeros(16, np.uint8)

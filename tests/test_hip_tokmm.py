@@ -51,7 +51,7 @@ KQ = [oracle.Q4_K, oracle.Q5_K, oracle.Q6_K]
 
 @pytest.mark.parametrize("dt", KQ)
 @pytest.mark.parametrize("rows,n,ntok", [(768, 2048, 32), (768, 2048, 1), (100, 512, 33), (2048, 768, 45),
-                                         (130, 256, 64), (16, 256, 7)])
+                                         (130, 256, 64), (16, 256, 7), (768, 2048, 512)])
 def test_tokmm_matches_decode(hip, dev, dt, rows, n, ntok):
     run_case(hip, dev, dt, rows, n, ntok, seed=rows * 7 + ntok + dt)
 
