@@ -94,6 +94,27 @@ def test_prefill_qwen3_shape_512_tokens(hip, dev, dt):
         assert np.array_equal(got[t].view(np.uint32), ht.cpu().numpy().view(np.uint32)), f"token {t}"
 
 
+def test_prefill_many_tokens(hip, dev):
+    """20000 tokens x top-4 = 80000 (token, rank) slots, more than a grid's y
+    dimension holds: the launches that cover slots put them on x."""
+    case = build_moe_case(D=256, de=256, E=16, k=4, ds=0, expert_dt=oracle.Q6_K, seed=17, device=dev,
+                          weights="random_codes")
+    T = 20000
+    rng = np.random.default_rng(22)
+    H = rng.standard_normal((T, case.D)).astype(np.float32)
+    h = torch.from_numpy(H.copy()).to(dev)
+    ids = torch.empty((T, case.k), dtype=torch.int32, device=dev)
+    case.block.prefill(h, ids)
+    torch.cuda.synchronize()
+    got, got_ids = h.cpu().numpy(), ids.cpu().numpy()
+    for t in list(range(0, T, 997)) + [T - 1]:
+        ht = torch.from_numpy(H[t].copy()).to(dev)
+        case.block(ht)
+        torch.cuda.synchronize()
+        assert np.array_equal(got_ids[t], case.block.ids.cpu().numpy()[:case.k]), t
+        assert np.array_equal(got[t].view(np.uint32), ht.cpu().numpy().view(np.uint32)), f"token {t}"
+
+
 @pytest.mark.parametrize("router", [1, 2])
 def test_prefill_routers_and_mask(hip, dev, router):
     mask = np.zeros(16, np.uint8)

@@ -1117,8 +1117,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 /* Quantise h of every slot (src/lib/tlm_quant.c:458-478): one wave per block. */
 __global__ __launch_bounds__(64) void k_pf_hquant(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
     args_now(d.de, P.hbuf, P.hq, P.hq_stride, ws);
-    const int b = blockIdx.x, lane = threadIdx.x;
-    const size_t slot = blockIdx.y;
+    const int b = blockIdx.y, lane = threadIdx.x;
+    const size_t slot = blockIdx.x;   /* T * k slots: the grid's x (y is capped at 65536) */
     const int nbd = (int)(d.de / 256);
     const f32x4 v = *(const GAS f32x4 *)((const GAS float *)(ws + P.hbuf) + slot * d.de + (size_t)b * 256 + 4 * lane);
     GAS uint8_t *q = (GAS uint8_t *)(ws + P.hq + slot * P.hq_stride);
@@ -1314,6 +1314,9 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
     const tlm_hip_moe_desc dv = *d;
     const WsLayout L = ws_layout(*d);
     const PfLayout P = pf_layout(*d, T);
+    if (P.MT > 65536)   /* the tile grids' y */
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld x k=%d gives %d tiles, more than 65536", (long long)T,
+                           d->k, P.MT);
     uint8_t *w8 = (uint8_t *)ws;
     hipLaunchKernelGGL(k_pf_norm, dim3((unsigned)(d->D / 256), (unsigned)T), dim3(64), 0, s, dv, L, P, (const float *)h,
                        w8);
@@ -1327,7 +1330,7 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
     case DT_Q5_K: hipLaunchKernelGGL(k_pf_gateup<DT_Q5_K>, ggu, dim3(256), 0, s, dv, L, P, w8); break;
     default: hipLaunchKernelGGL(k_pf_gateup<DT_Q6_K>, ggu, dim3(256), 0, s, dv, L, P, w8); break;
     }
-    hipLaunchKernelGGL(k_pf_hquant, dim3((unsigned)(d->de / 256), (unsigned)(T * d->k)), dim3(64), 0, s, dv, P, w8);
+    hipLaunchKernelGGL(k_pf_hquant, dim3((unsigned)(T * d->k), (unsigned)(d->de / 256)), dim3(64), 0, s, dv, P, w8);
     switch (d->expert_dt) {
     case DT_Q4_K: hipLaunchKernelGGL(k_pf_down<DT_Q4_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
     case DT_Q5_K: hipLaunchKernelGGL(k_pf_down<DT_Q5_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
