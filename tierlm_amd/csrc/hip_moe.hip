@@ -308,8 +308,8 @@ __device__ __forceinline__ float reduce32(float r) {
     return s + dpp_f32<DPP_XOR1>(s);
 }
 
-/* blockIdx.y = token (prefill): its residual at hptr + y * D, its workspace at
- * ws + y * tstride; a decode launch has one token. */
+/* blockIdx.y = token: its residual at hptr + y * D, its workspace at
+ * ws + y * tstride (the decode launches have one token). */
 __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
                                                    uint8_t *ws, size_t tstride) {
     extern __shared__ __align__(16) uint8_t lds[];
