@@ -93,7 +93,7 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
  * registers while one is summed.  q_norm / k_norm are read only
  * when has_qn / has_kn. */
 constexpr int ATT_VF = 8192;                 /* floats of V per LDS chunk (32 KB) */
-constexpr int ATT_PF = ATT_VF / 4 / NT;      /* 16-byte V loads per thread per chunk */
+constexpr int ATT_PF = ATT_VF / 4 / 128;     /* 16-byte V loads per producer thread per chunk */
 constexpr int ATT_LDS_POS = 4096;            /* contexts whose probabilities fit in LDS */
 constexpr int ATT_PU = 16;                   /* positions per group in the ordered sums */
 
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
     constexpr bool KPRE = HD <= 128;
     extern __shared__ __align__(16) float s_dyn[];
     __shared__ __align__(16) float s_q[HD], s_k[HD], s_vn[HD];
-    __shared__ __align__(16) float s_v[ATT_VF];
+    __shared__ __align__(16) float s_v[2 * ATT_VF];
     __shared__ double s_red[NT / 64];
     __shared__ float s_redf[NT / 64];
     const int pos = st[0], T = pos + 1;
@@ -152,12 +152,16 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
 #pragma unroll
         for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
     }
-    f32x4 pa[ATT_PF], pb[ATT_PF];   /* two V chunks in registers */
-    auto vload = [&](int t0, f32x4 (&pv)[ATT_PF]) {
+    /* V chunks (VC positions): the producer threads (tid >= 128, waves 2-3)
+     * hold two in registers, loaded two chunks ahead */
+    const int ptid = tid - 128, nch = (T + VC - 1) / VC;
+    f32x4 va[ATT_PF], vb[ATT_PF];
+    auto vload = [&](int c, f32x4 (&pv)[ATT_PF]) {
+        const int t0 = c * VC;
         const int n4 = (T - t0 < VC ? T - t0 : VC) * H4;
         const f32x4 *src = (const f32x4 *)(V + (size_t)t0 * HD);
 #pragma unroll
-        for (int j = 0; j < ATT_PF; j++) pv[j] = src[min(tid + NT * j, n4 - 1)];
+        for (int j = 0; j < ATT_PF; j++) pv[j] = src[min(ptid + 128 * j, n4 - 1)];
     };
 
     /* norm (tlm_model.c:743-746) and RoPE (rope(), :721-728: pairs (j, j + HD/2)) */
@@ -241,8 +245,10 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
             if (d > mx) mx = d;
         }
     }
-    vload(0, pa);   /* the key registers are free now; max, exp and sum cover the latency */
-    if (VC < T) vload(VC, pb);
+    if (tid >= 128) {   /* the key registers are free now; max, exp and sum cover the latency */
+        vload(0, va);
+        if (nch > 1) vload(1, vb);
+    }
     mx = block_max_dpp(mx, s_redf);
     double sum = 0.0;
     for (int t = tid; t < T; t += NT) {
@@ -253,58 +259,112 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
     sum = block_sum_f64(sum, s_red);
     const float inv = (float)(1.0 / sum);
     for (int t = tid; t < T; t += NT) sp[t] = sp[t] * inv;
+    __syncthreads();   /* every p stored before the producers read them */
 
-    /* P.V, chunk by chunk: the chunk being summed in LDS, the next two in
-     * registers (pa / pb alternate; a freed buffer loads the chunk after next) */
-    float o = 0.0f;
-    auto chunk = [&](int t0, f32x4 (&pv)[ATT_PF]) {
-        const int tn = T - t0 < VC ? T - t0 : VC;
+    /* P.V, chunk by chunk, as a pipeline inside the group: the producers
+     * store chunk c + 1 to LDS as the products c = p_t * v_t[i] (the
+     * reference's product, bit for bit) while the consumers (tid < 128, lane
+     * = output element i, and i + 128 when HD = 256) run the ordered sums over
+     * chunk c - one add per position; two LDS buffers, one barrier per chunk.
+     * A producer reads its chunk's probabilities at once (one wait), and the
+     * new row only in the last chunk. */
+    constexpr int CD = (HD + 127) / 128;
+    float o[CD];
 #pragma unroll
-        for (int j = 0; j < ATT_PF; j++) {   /* registers -> LDS (whole buffer); row pos from this group's copy */
-            const int e4 = tid + NT * j;
-            const f32x4 nv = ((const f32x4 *)s_vn)[e4 % H4];
-            ((f32x4 *)s_v)[e4] = t0 + e4 / H4 == pos ? nv : pv[j];
+    for (int m = 0; m < CD; m++) o[m] = 0.0f;
+    float *buf0 = s_v, *buf1 = s_v + ATT_VF;
+    auto produce = [&](int c, const f32x4 (&pv)[ATT_PF], float *buf) {
+        const int t0 = c * VC, tn = T - t0 < VC ? T - t0 : VC;
+        float pt[ATT_PF];
+#pragma unroll
+        for (int j = 0; j < ATT_PF; j++) {
+            const int tl = (ptid + 128 * j) / H4;
+            pt[j] = sp[t0 + min(tl, tn - 1)];
         }
-        __syncthreads();   /* every p stored (first pass) and the chunk in LDS */
-        if (t0 + 2 * VC < T) vload(t0 + 2 * VC, pv);
-        if (tid < HD) {
-            const float *pc = sp + t0;   /* t0: a multiple of VC, itself of 16 */
-            const float *vcol = s_v + tid;
-            const int ng = (tn + ATT_PU - 1) / ATT_PU;
-#pragma unroll 1
-            for (int g = 0; g < ng; g++) {
-                f32x4 p4[ATT_PU / 4];
-                float vr[ATT_PU];
-                const float *pg = pc + g * ATT_PU;
+        if (c == nch - 1) {   /* the chunk holding row pos: this group's copy, and nothing past T */
 #pragma unroll
-                for (int u = 0; u < ATT_PU / 4; u++) {
-                    if constexpr (SPL) p4[u] = *(const f32x4 *)(pg + 4 * u);   /* LDS: 16-byte aligned */
-                    else p4[u] = f32x4{pg[4 * u], pg[4 * u + 1], pg[4 * u + 2], pg[4 * u + 3]};
-                }
+            for (int j = 0; j < ATT_PF; j++) {
+                const int e4 = ptid + 128 * j, tl = e4 / H4;
+                f32x4 v4 = t0 + tl == pos ? ((const f32x4 *)s_vn)[e4 % H4] : pv[j];
+                const float q = tl < tn ? pt[j] : 0.0f;
+                f32x4 cc;
 #pragma unroll
-                for (int u = 0; u < ATT_PU; u++) vr[u] = vcol[(g * ATT_PU + u) * HD];
-                if (g + 1 < ng) {
+                for (int k = 0; k < 4; k++) cc[k] = q * v4[k];
+                ((f32x4 *)buf)[e4] = cc;
+            }
+        } else {
 #pragma unroll
-                    for (int u = 0; u < ATT_PU; u++) o += p4[u / 4][u % 4] * vr[u];
-                } else {
-                    const int lim = tn - g * ATT_PU;
+            for (int j = 0; j < ATT_PF; j++) {
+                f32x4 cc;
 #pragma unroll
-                    for (int u = 0; u < ATT_PU; u++) {
-                        const float a = o + p4[u / 4][u % 4] * vr[u];
-                        o = u < lim ? a : o;
-                    }
-                }
+                for (int k = 0; k < 4; k++) cc[k] = pt[j] * pv[j][k];
+                ((f32x4 *)buf)[ptid + 128 * j] = cc;
             }
         }
-        __syncthreads();   /* the chunk is read before the next one overwrites it */
     };
-    for (int t0 = 0;;) {   /* uniform over the group */
-        chunk(t0, pa);
-        if ((t0 += VC) >= T) break;
-        chunk(t0, pb);
-        if ((t0 += VC) >= T) break;
+    auto consume = [&](int c, const float *buf) {
+        const int t0 = c * VC, tn = T - t0 < VC ? T - t0 : VC;
+        const int ng = (tn + ATT_PU - 1) / ATT_PU;
+        /* group g + 1's products load while group g's ordered sums run;
+         * reads past the chunk's last position stay inside the buffer and
+         * are masked in the last group */
+        float ra[CD][ATT_PU], rb[CD][ATT_PU];
+        auto ld = [&](int g, float (&r)[CD][ATT_PU]) {
+#pragma unroll
+            for (int m = 0; m < CD; m++)
+#pragma unroll
+                for (int u = 0; u < ATT_PU; u++) r[m][u] = buf[(g * ATT_PU + u) * HD + min(tid + 128 * m, HD - 1)];
+        };
+        auto add = [&](int g, const float (&r)[CD][ATT_PU]) {
+            if (g + 1 < ng) {
+#pragma unroll
+                for (int u = 0; u < ATT_PU; u++)
+#pragma unroll
+                    for (int m = 0; m < CD; m++) o[m] += r[m][u];
+            } else {
+                const int lim = tn - g * ATT_PU;
+#pragma unroll
+                for (int u = 0; u < ATT_PU; u++)
+#pragma unroll
+                    for (int m = 0; m < CD; m++) {
+                        const float a = o[m] + r[m][u];
+                        o[m] = u < lim ? a : o[m];
+                    }
+            }
+        };
+        ld(0, ra);
+#pragma unroll 1
+        for (int g = 0; g < ng; g += 2) {
+            if (g + 1 < ng) ld(g + 1, rb);
+            add(g, ra);
+            if (g + 1 >= ng) break;
+            if (g + 2 < ng) ld(g + 2, ra);
+            add(g + 1, rb);
+        }
+    };
+    if (tid >= 128) {
+        produce(0, va, buf0);
+        if (nch > 2) vload(2, va);
     }
-    if (tid < HD) att[(size_t)h * HD + tid] = o;
+    __syncthreads();
+    for (int c = 0; c < nch; c += 2) {   /* uniform over the group; even chunks in va / buf0, odd in vb / buf1 */
+        if (tid < 128) consume(c, buf0);
+        else if (c + 1 < nch) {
+            produce(c + 1, vb, buf1);
+            if (c + 3 < nch) vload(c + 3, vb);
+        }
+        __syncthreads();
+        if (c + 1 >= nch) break;
+        if (tid < 128) consume(c + 1, buf1);
+        else if (c + 2 < nch) {
+            produce(c + 2, va, buf0);
+            if (c + 4 < nch) vload(c + 4, va);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int m = 0; m < CD; m++)
+        if (tid < 128 && tid + 128 * m < HD) att[(size_t)h * HD + tid + 128 * m] = o[m];
     if (h % (H / KV) == 0)   /* the KV append, after the last barrier */
         for (int i = tid; i < HD; i += NT) {
             kc[((size_t)kvh * HD + i) * max_ctx + pos] = s_k[i];
