@@ -86,12 +86,13 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
  * for the group's stores): the KV append goes last.  The
  * probabilities stay in LDS (dynamic, max_ctx floats) when SPL, else in the
  * head's global scratch row; they are scaled by 1/sum in place (the
- * reference's p = s[t] * inv).  The ordered sums go 16 positions per group
- * (four 16-byte probability reads, sixteen fixed-offset value reads, then
- * the adds); the last group of a chunk reads whole (the probability row is padded to 16, a chunk holds a
- * multiple of 16 positions) and masks its adds.  Two V chunks wait in
- * registers while one is summed.  q_norm / k_norm are read only
- * when has_qn / has_kn. */
+ * reference's p = s[t] * inv).  P.V is a pipeline inside the group: waves
+ * 2-3 hold V chunks two ahead in registers and store each chunk to one of
+ * two LDS buffers as the products p_t * v_t[i]; waves 0-1 (one output
+ * element per lane) sum the previous chunk meanwhile, 16 positions per group
+ * of LDS reads, the last group of a chunk read whole (a chunk holds a
+ * multiple of 16 positions) and its adds masked.  q_norm / k_norm are read
+ * only when has_qn / has_kn. */
 constexpr int ATT_VF = 8192;                 /* floats of V per LDS chunk (32 KB) */
 constexpr int ATT_PF = ATT_VF / 4 / 128;     /* 16-byte V loads per producer thread per chunk */
 constexpr int ATT_LDS_POS = 4096;            /* contexts whose probabilities fit in LDS */
