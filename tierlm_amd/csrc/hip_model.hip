@@ -97,6 +97,7 @@ constexpr int ATT_VF = 8192;                 /* floats of V per LDS chunk (32 KB
 constexpr int ATT_PF = ATT_VF / 4 / 128;     /* 16-byte V loads per producer thread per chunk */
 constexpr int ATT_LDS_POS = 4096;            /* contexts whose probabilities fit in LDS */
 constexpr int ATT_PU = 16;                   /* positions per group in the ordered sums */
+constexpr int ATT_SPLIT_MIN = 2 * NT;         /* longest context scored inside the fused launch */
 
 /* max over non-NaN values (a NaN never compares greater), -inf if none */
 __device__ float block_max_dpp(float v, float *red) {
@@ -110,18 +111,130 @@ __device__ float block_max_dpp(float v, float *red) {
     return m;
 }
 
-template <int HD, bool SPL>
+/* Scores of one query head over one slice of NT positions (grid: heads x
+ * max_ctx / NT slices; slices past the current position return): the head's
+ * q (wave 0) and the new key (wave 1) normalised and rotated exactly as the
+ * fused launch does it, then one position per thread - the dot in ascending
+ * i, scaled after the dot - into the head's score row, and the slice's
+ * maximum (non-NaN values, -inf if none) into smax[h * nslice + slice]. */
+template <int HD>
+__global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kx,
+                                                    const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+                                                    int has_qn, int has_kn, const float *__restrict__ cs_all,
+                                                    const float *__restrict__ sn_all, const float *__restrict__ kc,
+                                                    float *__restrict__ scores, float *__restrict__ smax, int H,
+                                                    int KV, int max_ctx, const int32_t *__restrict__ st, float eps) {
+    constexpr int HALF = HD / 2, H4 = HD / 4;
+    constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;
+    constexpr bool KPRE = HD <= 128;
+    __shared__ __align__(16) float s_q[HD], s_k[HD];
+    __shared__ float s_redf[NT / 64];
+    const int pos = st[0], T = pos + 1;
+    const int p0 = (int)blockIdx.y * NT;
+    if (p0 >= T) return;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = h / (H / KV);
+    const float *K = kc + (size_t)kvh * max_ctx * HD;
+    const int t = p0 + tid;
+    const float *hv = wave == 1 ? kx + (size_t)kvh * HD : q + (size_t)h * HD;
+    const float *nwp = wave == 1 ? k_norm : q_norm;
+    float e[KE], nw[KE], cv[KH], sv[KH];
+#pragma unroll
+    for (int k = 0; k < KE; k++) e[k] = hv[min(lane + 64 * k, HD - 1)];
+#pragma unroll
+    for (int k = 0; k < KE; k++) nw[k] = nwp[min(lane + 64 * k, HD - 1)];
+#pragma unroll
+    for (int k = 0; k < KH; k++) {
+        cv[k] = cs_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
+        sv[k] = sn_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
+    }
+    float kr[KPRE ? HD : 1];
+    if constexpr (KPRE) {   /* this slice's key columns, all at once (rows clamped to pos) */
+        const float *kt = K + min(t, pos);
+#pragma unroll
+        for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
+    }
+    if (wave < 2) {   /* norm (tlm_model.c:743-746) and RoPE (rope(), :721-728: pairs (j, j + HD/2)) */
+        float *v = wave == 0 ? s_q : s_k;
+        if (wave == 0 ? has_qn : has_kn) {
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < KE; k++)
+                if (lane + 64 * k < HD) ss += (double)e[k] * (double)e[k];
+            ss = wave_sum_f64(ss);
+            const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
+#pragma unroll
+            for (int k = 0; k < KE; k++) e[k] = e[k] * r * nw[k];
+        }
+#pragma unroll
+        for (int k = 0; k < KE; k++)
+            if (lane + 64 * k < HD) v[lane + 64 * k] = e[k];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < KH; k++) {
+            const int j = lane + 64 * k;
+            if (j < HALF) {
+                const float a = v[j], c = v[j + HALF];
+                v[j] = a * cv[k] - c * sv[k];
+                v[j + HALF] = c * cv[k] + a * sv[k];
+            }
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)HD);
+    const f32x4 *q4 = (const f32x4 *)s_q;
+    float d = 0.0f, mx = -INFINITY;
+    if (KPRE) {
+        if (t == pos) {   /* the new key, from this group's copy */
+#pragma unroll
+            for (int i4 = 0; i4 < H4; i4++) {
+                const f32x4 k4 = ((const f32x4 *)s_k)[i4];
+                kr[4 * i4] = k4.x;
+                kr[4 * i4 + 1] = k4.y;
+                kr[4 * i4 + 2] = k4.z;
+                kr[4 * i4 + 3] = k4.w;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < HD / 16; c++) {   /* q in batches of 16 */
+            f32x4 qb[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) qb[u] = q4[4 * c + u];
+#pragma unroll
+            for (int u = 0; u < 16; u++) d += qb[u / 4][u % 4] * kr[16 * c + u];
+        }
+    } else if (t == pos) {
+#pragma unroll
+        for (int i = 0; i < HD; i++) d += s_q[i] * s_k[i];
+    } else if (t < T) {
+        const float *kt = K + t;
+#pragma unroll 16
+        for (int i = 0; i < HD; i++) d += s_q[i] * kt[(size_t)i * max_ctx];
+    }
+    if (t < T) {
+        d *= scale;
+        scores[(size_t)h * max_ctx + t] = d;
+        if (d > mx) mx = d;
+    }
+    mx = block_max_dpp(mx, s_redf);
+    if (tid == 0) smax[(size_t)h * gridDim.y + blockIdx.y] = mx;
+}
+
+template <int HD, bool SPL, bool SPLIT>
 __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, const float *__restrict__ kx,
                                                    const float *__restrict__ vx, const float *__restrict__ q_norm,
                                                    const float *__restrict__ k_norm, int has_qn, int has_kn,
                                                    const float *__restrict__ cs_all, const float *__restrict__ sn_all,
                                                    float *__restrict__ kc, float *__restrict__ vc,
-                                                   float *__restrict__ scores, float *__restrict__ att, int H,
-                                                   int KV, int max_ctx, const int32_t *__restrict__ st, float eps) {
+                                                   float *__restrict__ scores, const float *__restrict__ smax,
+                                                   float *__restrict__ att, int H, int KV, int max_ctx,
+                                                   const int32_t *__restrict__ st, float eps) {
     constexpr int HALF = HD / 2, H4 = HD / 4;
     constexpr int VC = (ATT_VF / HD) & ~(ATT_PU - 1);   /* V positions per chunk */
     constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;     /* elements / pairs per lane */
-    constexpr bool KPRE = HD <= 128;
+    constexpr bool KPRE = HD <= 128 && !SPLIT;
     extern __shared__ __align__(16) float s_dyn[];
     __shared__ __align__(16) float s_q[HD], s_k[HD], s_vn[HD];
     __shared__ __align__(16) float s_v[2 * ATT_VF];
@@ -146,7 +259,7 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
         cv[k] = cs_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
         sv[k] = sn_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
     }
-    /* 2. the first pass's key columns and the first V chunk */
+    /* 2. without the split launch: the first pass's key columns */
     float kr[KPRE ? HD : 1];
     if constexpr (KPRE) {
         const float *kt = K + min(tid, pos);
@@ -198,62 +311,77 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
     }
     __syncthreads();
 
-    /* scores (scale after the dot, before the max) */
+    /* scores (scale after the dot, before the max): from the split launch
+     * (the head's row and its slices' maxima), or here, a pass of NT
+     * positions at a time */
     float *sp;
     if constexpr (SPL) sp = s_dyn;
     else sp = scores + (size_t)h * max_ctx;
-    const float scale = 1.0f / sqrtf((float)HD);
-    float mx = -INFINITY;
-    const f32x4 *q4 = (const f32x4 *)s_q;
-    for (int p0 = 0; p0 < T; p0 += NT) {   /* passes of NT positions, uniform over the group */
-        const int t = p0 + tid;
-        float d = 0.0f;
-        if (KPRE) {
-            if (p0 > 0) {   /* this pass's key columns, all at once (rows clamped to pos) */
-                const float *kt = K + min(t, pos);
+    const float *sg = SPLIT ? (const float *)(scores + (size_t)h * max_ctx) : (const float *)sp;
+    float mx = -INFINITY;   /* the maximum of non-NaN values, -inf if none */
+    if constexpr (SPLIT) {
+        if (tid >= 128) {   /* the first V chunks go out before the maximum, exp and sum */
+            vload(0, va);
+            if (nch > 1) vload(1, vb);
+        }
+        const int nslice = (max_ctx + NT - 1) / NT, nsl = (T + NT - 1) / NT;
+        for (int i = 0; i < nsl; i++) {
+            const float m = smax[(size_t)h * nslice + i];
+            mx = m > mx ? m : mx;
+        }
+    } else {
+        const float scale = 1.0f / sqrtf((float)HD);
+        const f32x4 *q4 = (const f32x4 *)s_q;
+        for (int p0 = 0; p0 < T; p0 += NT) {   /* passes of NT positions, uniform over the group */
+            const int t = p0 + tid;
+            float d = 0.0f;
+            if (KPRE) {
+                if (p0 > 0) {   /* this pass's key columns, all at once (rows clamped to pos) */
+                    const float *kt = K + min(t, pos);
 #pragma unroll
-                for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
-            }
-            if (t == pos) {   /* the new key, from this group's copy */
-#pragma unroll
-                for (int i4 = 0; i4 < H4; i4++) {
-                    const f32x4 k4 = ((const f32x4 *)s_k)[i4];
-                    kr[4 * i4] = k4.x;
-                    kr[4 * i4 + 1] = k4.y;
-                    kr[4 * i4 + 2] = k4.z;
-                    kr[4 * i4 + 3] = k4.w;
+                    for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
                 }
-            }
+                if (t == pos) {   /* the new key, from this group's copy */
 #pragma unroll
-            for (int c = 0; c < HD / 16; c++) {   /* q in batches of 16 */
-                f32x4 qb[4];
+                    for (int i4 = 0; i4 < H4; i4++) {
+                        const f32x4 k4 = ((const f32x4 *)s_k)[i4];
+                        kr[4 * i4] = k4.x;
+                        kr[4 * i4 + 1] = k4.y;
+                        kr[4 * i4 + 2] = k4.z;
+                        kr[4 * i4 + 3] = k4.w;
+                    }
+                }
 #pragma unroll
-                for (int u = 0; u < 4; u++) qb[u] = q4[4 * c + u];
+                for (int c = 0; c < HD / 16; c++) {   /* q in batches of 16 */
+                    f32x4 qb[4];
 #pragma unroll
-                for (int u = 0; u < 16; u++) d += qb[u / 4][u % 4] * kr[16 * c + u];
-            }
-        } else if (t == pos) {
+                    for (int u = 0; u < 4; u++) qb[u] = q4[4 * c + u];
 #pragma unroll
-            for (int i = 0; i < HD; i++) d += s_q[i] * s_k[i];
-        } else if (t < T) {
-            const float *kt = K + t;
+                    for (int u = 0; u < 16; u++) d += qb[u / 4][u % 4] * kr[16 * c + u];
+                }
+            } else if (t == pos) {
+#pragma unroll
+                for (int i = 0; i < HD; i++) d += s_q[i] * s_k[i];
+            } else if (t < T) {
+                const float *kt = K + t;
 #pragma unroll 16
-            for (int i = 0; i < HD; i++) d += s_q[i] * kt[(size_t)i * max_ctx];
+                for (int i = 0; i < HD; i++) d += s_q[i] * kt[(size_t)i * max_ctx];
+            }
+            if (t < T) {
+                d *= scale;
+                sp[t] = d;
+                if (d > mx) mx = d;
+            }
         }
-        if (t < T) {
-            d *= scale;
-            sp[t] = d;
-            if (d > mx) mx = d;
+        if (tid >= 128) {   /* the key registers are free now; max, exp and sum cover the latency */
+            vload(0, va);
+            if (nch > 1) vload(1, vb);
         }
+        mx = block_max_dpp(mx, s_redf);
     }
-    if (tid >= 128) {   /* the key registers are free now; max, exp and sum cover the latency */
-        vload(0, va);
-        if (nch > 1) vload(1, vb);
-    }
-    mx = block_max_dpp(mx, s_redf);
     double sum = 0.0;
     for (int t = tid; t < T; t += NT) {
-        const float p = exp_rn(sp[t] - mx);
+        const float p = exp_rn(sg[t] - mx);
         sp[t] = p;
         sum += (double)p;
     }
@@ -376,20 +504,34 @@ __global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, 
 /* host: launch for the model's head width (a multiple of 32, at most 256) */
 int launch_attn(int hd, int H, int KV, int max_ctx, const float *q, const float *kx, const float *vx,
                 const float *q_norm, const float *k_norm, const float *cs, const float *sn, float *kc, float *vc,
-                float *scores, float *att, const int32_t *st, float eps, hipStream_t s) {
+                float *scores, float *smax, float *att, const int32_t *st, float eps, hipStream_t s) {
     const bool spl = max_ctx <= ATT_LDS_POS;
     const int has_qn = q_norm != nullptr, has_kn = k_norm != nullptr;
     if (!q_norm) q_norm = q;   /* read (clamped) and dropped */
     if (!k_norm) k_norm = q;
     const size_t dyn = spl ? (size_t)(max_ctx + ATT_PU) * 4 : 0;   /* the last group reads whole */
+    const unsigned nslice = (unsigned)((max_ctx + NT - 1) / NT);
+    /* contexts of at most ATT_SPLIT_MIN positions score inside the fused launch (one or two
+     * passes); longer ones in the split launch, a group per (head, NT positions) */
+    const bool split = max_ctx > ATT_SPLIT_MIN;
 #define TLM_ATT(W)                                                                                                \
     case W:                                                                                                       \
-        if (spl)                                                                                                  \
-            hipLaunchKernelGGL((k_attn_fused<W, true>), dim3(H), dim3(NT), dyn, s, q, kx, vx, q_norm, k_norm,     \
-                               has_qn, has_kn, cs, sn, kc, vc, scores, att, H, KV, max_ctx, st, eps);             \
-        else                                                                                                      \
-            hipLaunchKernelGGL((k_attn_fused<W, false>), dim3(H), dim3(NT), 0, s, q, kx, vx, q_norm, k_norm,      \
-                               has_qn, has_kn, cs, sn, kc, vc, scores, att, H, KV, max_ctx, st, eps);             \
+        if (!split)                                                                                               \
+            hipLaunchKernelGGL((k_attn_fused<W, true, false>), dim3(H), dim3(NT), dyn, s, q, kx, vx, q_norm,      \
+                               k_norm, has_qn, has_kn, cs, sn, kc, vc, scores, smax, att, H, KV, max_ctx, st,     \
+                               eps);                                                                              \
+        else {                                                                                                    \
+            hipLaunchKernelGGL((k_attn_scores<W>), dim3(H, nslice), dim3(NT), 0, s, q, kx, q_norm, k_norm,       \
+                               has_qn, has_kn, cs, sn, kc, scores, smax, H, KV, max_ctx, st, eps);                \
+            if (spl)                                                                                              \
+                hipLaunchKernelGGL((k_attn_fused<W, true, true>), dim3(H), dim3(NT), dyn, s, q, kx, vx, q_norm,   \
+                                   k_norm, has_qn, has_kn, cs, sn, kc, vc, scores, smax, att, H, KV, max_ctx, st, \
+                                   eps);                                                                          \
+            else                                                                                                  \
+                hipLaunchKernelGGL((k_attn_fused<W, false, true>), dim3(H), dim3(NT), 0, s, q, kx, vx, q_norm,   \
+                                   k_norm, has_qn, has_kn, cs, sn, kc, vc, scores, smax, att, H, KV, max_ctx, st, \
+                                   eps);                                                                          \
+        }                                                                                                         \
         break;
     switch (hd) {
         TLM_ATT(32) TLM_ATT(64) TLM_ATT(96) TLM_ATT(128) TLM_ATT(160) TLM_ATT(192) TLM_ATT(224) TLM_ATT(256)
@@ -449,7 +591,7 @@ struct tlm_hip_model {
     size_t embd_row = 0;
     const float *out_norm = nullptr;
     DevMat lm_head;
-    float *kc = nullptr, *vc = nullptr, *cs = nullptr, *sn = nullptr, *scores = nullptr;
+    float *kc = nullptr, *vc = nullptr, *cs = nullptr, *sn = nullptr, *scores = nullptr, *smax = nullptr;
     float *h = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
     float *logits = nullptr;
     uint8_t *moe_ws = nullptr;
@@ -642,6 +784,7 @@ int finish(tlm_hip_model *M) {
     M->kc = (float *)M->dalloc(per * 4);
     M->vc = (float *)M->dalloc(per * 4);
     M->scores = (float *)M->dalloc(((size_t)H * max_ctx + 16) * 4);   /* attention reads a row in groups of 16 */
+    M->smax = (float *)M->dalloc((size_t)H * ((max_ctx + NT - 1) / NT) * 4);   /* per (head, slice) score maxima */
     M->h = (float *)M->dalloc((size_t)D * 4);
     M->q = (float *)M->dalloc((size_t)H * hd * 4);
     M->kx = (float *)M->dalloc((size_t)KV * hd * 4);
@@ -656,7 +799,7 @@ int finish(tlm_hip_model *M) {
     M->ids = (int32_t *)M->dalloc(32 * 4);
     M->w = (float *)M->dalloc(32 * 4);
     M->keys = (unsigned long long *)M->dalloc(((size_t)g.vocab + TILE_ROWS - 1) / TILE_ROWS * 8);
-    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->h,
+    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->smax, (void *)M->h,
                     (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
                     (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
                     (void *)M->w, (void *)M->keys})
@@ -833,7 +976,7 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
         if (rc) break;
         const size_t lbase = (size_t)l * KV * M->max_ctx * hd;
         rc = launch_attn(hd, H, KV, M->max_ctx, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm, M->cs, M->sn,
-                         M->kc + lbase, M->vc + lbase, M->scores, M->att, (const int32_t *)M->st, g.norm_eps, s);
+                         M->kc + lbase, M->vc + lbase, M->scores, M->smax, M->att, (const int32_t *)M->st, g.norm_eps, s);
         /* o: every group quantises the attention output itself */
         const MvNorm ao{M->att, nullptr, 0.0f};
         const void *Wo = Ly.o.p;
