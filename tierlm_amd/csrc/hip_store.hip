@@ -119,6 +119,7 @@ struct tlm_hip_store {
     int loading = 0, demand_loading = 0, hint_loading = 0, n_pinned = 0;
     tlm_hip_store_stats st{};
     uint8_t *route_host = nullptr;      /* pinned: routing results of tlm_hip_moe_layer_store */
+    uint32_t *route_dev = nullptr;      /* route_host as the device addresses it (mapped, coherent) */
     /* release points: an event recorded on a release stream when a load first
      * needs one, shared by every load that needs a point on that stream
      * before the next release; reused once no queued load waits for it */
@@ -536,8 +537,12 @@ int tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store
             s->stage_dev[i] = (const uint8_t *)dp;
             if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->stage_packed[i], hipEventDisableTiming), "store: event");
         }
+        /* mapped and coherent: k_route_export stores the routing straight into it, and the stream
+         * synchronisation that follows makes those stores visible to the host */
         if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->route_host, ROUTE_BYTES * (1 + MAX_HINTS),
-                                               hipHostMallocDefault), "store: routing scratch");
+                                               hipHostMallocMapped | hipHostMallocCoherent), "store: routing scratch");
+        if (!rc) rc = tlmh_check(hipHostGetDevicePointer((void **)&s->route_dev, s->route_host, 0),
+                                 "store: routing scratch address");
         if (!rc) s->loader = std::thread([s] { s->loader_main(); });
     }
     if (rc) {
@@ -815,6 +820,18 @@ struct TableSet {
 };
 
 /* table[idx[i]] = ptr[i]: the routed experts' gate / up / down entries */
+/* Route areas of the block and its hints -> route_host, ROUTE_BYTES each, in one launch (one
+ * dword per thread, vector stores over PCIe) instead of 1 + n_hints device-to-host copies. */
+struct RouteSrc {
+    const uint32_t *src[1 + MAX_HINTS];
+};
+constexpr int ROUTE_DW = ROUTE_BYTES / 4;
+
+__global__ __launch_bounds__(ROUTE_DW * (1 + MAX_HINTS)) void k_route_export(uint32_t *dst, RouteSrc r, int n) {
+    const int i = threadIdx.x / ROUTE_DW, j = threadIdx.x % ROUTE_DW;
+    if (i < n) dst[i * ROUTE_DW + j] = r.src[i][j];
+}
+
 __global__ __launch_bounds__(128) void k_table_set(const void **table, TableSet t) {
     const int i = threadIdx.x;
     if (i < t.n) table[t.idx[i]] = t.ptr[i];
@@ -841,14 +858,18 @@ int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int lay
      * block's update), then one round trip for all of them */
     int rc = launch_moe_route(d, h, nullptr, nullptr, workspace, st);
     if (rc) return rc;
-    HIPCHK(hipMemcpyAsync(s->route_host, (uint8_t *)workspace + moe_route_offset(d), ROUTE_BYTES,
-                          hipMemcpyDeviceToHost, st));
+    RouteSrc rs{};
+    rs.src[0] = (const uint32_t *)((const uint8_t *)workspace + moe_route_offset(d));
     for (int i = 0; i < n_hints; i++) {
         if ((rc = launch_moe_route(hints[i].desc, h, nullptr, nullptr, hints[i].workspace, st))) return rc;
-        HIPCHK(hipMemcpyAsync(s->route_host + ROUTE_BYTES * (1 + i),
-                              (uint8_t *)hints[i].workspace + moe_route_offset(hints[i].desc), ROUTE_BYTES,
-                              hipMemcpyDeviceToHost, st));
+        rs.src[1 + i] = (const uint32_t *)((const uint8_t *)hints[i].workspace + moe_route_offset(hints[i].desc));
     }
+    for (int i = 0; i <= n_hints; i++)
+        if ((uintptr_t)rs.src[i] & 3u)
+            return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: workspace %d is not 4-byte aligned", i);
+    hipLaunchKernelGGL(k_route_export, dim3(1), dim3(ROUTE_DW * (1 + MAX_HINTS)), 0, st, s->route_dev, rs,
+                       1 + n_hints);
+    HIPCHK(hipGetLastError());
     HIPCHK(hipStreamSynchronize(st));
     const int k = d->k;
     int ids[MOE_MAXK];
