@@ -299,11 +299,18 @@ def c5_bench(torch, dev, tokens, cache_gb, pool=64, gamma=0.14, seed=11):
              "tok_s": round(ntok / dt, 2), "ms_per_token": round(dt / ntok * 1e3, 2),
              "misses_per_token": round(miss, 1), "hit_rate": round(1.0 - miss / (L5 * K), 4),
              "miss_GBps": round(miss * plen * ntok / dt / 1e9, 2),
+             # lookahead loads are not misses: they land before the layer asks, but cross PCIe too
+             "prefetch_issued_per_token": round((s1["prefetch_issued"] - s0["prefetch_issued"]) / ntok, 1),
+             "prefetch_used_per_token": round((s1["prefetch_used"] - s0["prefetch_used"]) / ntok, 1),
+             "load_GBps_with_prefetch": round((miss + (s1["prefetch_issued"] - s0["prefetch_issued"]) / ntok)
+                                              * plen * ntok / dt / 1e9, 2),
              "heat_top10pct_share": round(float(fs[:13].sum() / fs.sum()), 3)}
         st.close()
         log(f"bench: C5 slot cache ({r['slots']} slots, {cap_gb:.0f} GB): {r['tok_s']:.2f} tok/s, "
             f"{r['misses_per_token']:.1f} misses/token (hit rate {r['hit_rate']:.3f}), {r['miss_GBps']:.1f} GB/s "
-            f"over PCIe, heat top-13 share {r['heat_top10pct_share']}")
+            f"of misses; lookahead {r['prefetch_issued_per_token']:.1f} loads/token "
+            f"({r['prefetch_used_per_token']:.1f} used); all loads {r['load_GBps_with_prefetch']:.1f} GB/s over PCIe, "
+            f"heat top-13 share {r['heat_top10pct_share']}")
         return r
 
     out = {"model": "Qwen3-235B-A22B shape MoE stack: 94 layers, D 4096, 128 experts top-8 of width 1536, Q4_K, "
