@@ -891,10 +891,6 @@ int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int lay
         release_all();
         return rc;
     }
-    /* hints only now that this block's experts hold references (:988-990) */
-    for (int i = 0; i < n_hints; i++)
-        tlm_hip_store_prefetch(s, hints[i].layer, (const int *)(s->route_host + ROUTE_BYTES * (1 + i)),
-                               hints[i].desc->k);
     TableSet t{};
     for (int r = 0; r < k; r++)
         for (int m = 0; m < 3; m++) {
@@ -907,6 +903,11 @@ int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int lay
     for (int r = 0; r < k && !rc; r++) rc = tlm_hip_store_stream_wait(s, &refs[r], stream);
     if (!rc) rc = launch_moe_phase(d, 2, h, nullptr, nullptr, workspace, st);
     if (!rc) rc = launch_moe_phase(d, 3, h, nullptr, nullptr, workspace, st);
+    /* hints while this block's experts still hold references (:988-990), issued after the block's
+     * launches so that the loader's bookkeeping is off the path to them */
+    for (int i = 0; i < n_hints && !rc; i++)
+        tlm_hip_store_prefetch(s, hints[i].layer, (const int *)(s->route_host + ROUTE_BYTES * (1 + i)),
+                               hints[i].desc->k);
     release_all();
     return rc;
 }
