@@ -71,6 +71,14 @@ int tlm_hip_sync(void *stream);
 size_t tlm_hip_qact_bytes(int kind, int64_t n);
 int    tlm_hip_quantize_act(int kind, const float *x, int64_t n, void *dst, void *stream);
 
+/* ---- the exponential ----------------------------------------------------
+ * y[i] = e^(x[i]) on device memory, bit for bit libm's expf as the reference
+ * calls it (silu / sigmoidf_, src/lib/tlm_model.c:171-172; the routing softmax
+ * :823; the attention softmax :705): the function every softmax, sigmoid and
+ * SiLU of this library evaluates, exposed so a caller can check it against
+ * its own libm. */
+int    tlm_hip_expf(const float *x, float *y, int64_t n, void *stream);
+
 /* ---- matvec on the reference byte layout --------------------------------
  * src/lib/tlm_quant.h:76-85: y[r] = dot(W row r, act) for r in [r0, r1),
  * W row-major with stride row_bytes, any base byte offset.  A bad dtype or n
@@ -375,12 +383,21 @@ typedef struct {
     int32_t max_ctx;     /* KV positions; 0 = the store's max_ctx, else 4096 (tlm_kv_new) */
     int32_t eager;       /* 1: launch each step's kernels directly; 0: replay the step as a HIP graph
                             captured at first use (the position and tokens live in device memory) */
+    int32_t attn_slices; /* attention slices per key head; 0 = automatic (enough groups to cover the
+                            chip at long contexts); 1 = one group per key head, which stores the
+                            output itself */
 } tlm_hip_model_opts;
 int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
 void tlm_hip_model_close(tlm_hip_model *M);
 const tlm_hip_model_geom *tlm_hip_model_geom_of(const tlm_hip_model *M);
 int  tlm_hip_model_kv_len(const tlm_hip_model *M);
 int  tlm_hip_model_kv_capacity(const tlm_hip_model *M);
+/* The routing of the last step: per MoE layer, the top_k expert ids and
+ * weights in rank order (ids and w each n_layers x top_k, host memory) - what
+ * the reference's routing hook receives once per layer per token
+ * (tlm_model_set_route_hook, src/lib/tlm_model.h:63-70, called at
+ * src/lib/tlm_model.c:1053).  Waits for the step. */
+int  tlm_hip_model_routes(tlm_hip_model *M, int32_t *ids, float *w);
 void tlm_hip_model_reset(tlm_hip_model *M);   /* tlm_kv_reset */
 /* A random-init model of geometry g built directly in HBM, for measuring the
  * decode step at shapes whose compiled stores are too large to write or ship

@@ -59,6 +59,8 @@ for _n, _r, _a in [
     ("orc_matvec_rows", None, [i32, vp, sz, vp, vp, i64, i64, i64]),
     ("orc_block_isum", None, [i32, vp, vp, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     ("orc_rmsnorm", None, [vp, vp, vp, i64, f32]), ("orc_silu", f32, [f32]), ("orc_sigmoid", f32, [f32]),
+    ("orc_expf_many", None, [vp, vp, i64]), ("orc_exp2_tab", C.c_uint64, [i32]),
+    ("orc_expf_published_many", None, [vp, vp, i64, i32]),
     ("orc_topk", None, [vp, vp, i32, i32, vp]),
     ("orc_route", None, [i32, vp, vp, vp, i32, i32, f32, vp, vp]),
     ("orc_moe_layer", i32, [C.POINTER(OrcMoeDesc), vp, vp, vp, C.POINTER(OrcMoeTrace)]),
@@ -164,6 +166,22 @@ def block_isum(dt, wblock, ablock):
     a, b = C.c_int32(), C.c_int32()
     orc.orc_block_isum(dt, wblock.ctypes.data, ablock.ctypes.data, C.byref(a), C.byref(b))
     return a.value, b.value
+
+
+def expf(x):
+    """libm's expf over a float32 array (the reference's e^x)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    orc.orc_expf_many(_p(x), _p(y), x.size)
+    return y
+
+
+def expf_published(x, fused=True):
+    """The published expf algorithm restated (orc_expf_published)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    orc.orc_expf_published_many(_p(x), _p(y), x.size, int(fused))
+    return y
 
 
 def rmsnorm(x, w, eps):

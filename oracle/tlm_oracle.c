@@ -574,6 +574,60 @@ void orc_rmsnorm(float *out, const float *x, const float *w, int64_t n, float ep
     for (int64_t i = 0; i < n; i++) out[i] = x[i] * r * w[i];
 }
 
+/* e^x as the reference evaluates it: libm's expf itself (src/lib/tlm_model.c:
+ * 171-172, 705, 806, 823), over a vector */
+void orc_expf_many(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
+/* The published algorithm behind glibc's expf (2.27+; ARM optimized-routines,
+ * math/expf.c, Szabolcs Nagy 2017), restated from its description: x * N/ln 2
+ * = k + r, k rounded to the nearest integer through the 1.5 * 2^52 shift, N =
+ * 32; 2^(k/N) = 2^(floor(k/N)) * 2^((k mod N)/N) with the 32 values of
+ * 2^(i/N) (correctly rounded doubles, exponent of i/N removed, computed by
+ * tests/test_oracle_formats.py from exact arithmetic); 2^(r/N) from the cubic
+ * C0 r^3 + C1 r^2 + C2 r + 1; everything in double, rounded once.  Overflow
+ * above 0x1.62e42ep6, zero below -0x1.9fe368p6.  fused != 0 takes x * N/ln 2
+ * into the shift and into r with fma, as the x86-64 FMA build of libm does.
+ * The device's exponential is this algorithm with fused = 1. */
+static const uint64_t exp2_tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+uint64_t orc_exp2_tab(int i) { return exp2_tab[i & 31]; }
+
+float orc_expf_published(float x, int fused) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return INFINITY;
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32768.0, c1 = 0x1.ebfce50fac4f3p-3 / 1024.0,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x, z = inv_ln2_n * xd;
+    double kd = fused ? fma(inv_ln2_n, xd, shift) : z + shift;
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = fused ? fma(inv_ln2_n, xd, -kd) : z - kd;
+    const uint64_t t = exp2_tab[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double p = c0 * r + c1, r2 = r * r;
+    double y = c2 * r + 1.0;
+    y = p * r2 + y;
+    return (float)(y * s);
+}
+
+void orc_expf_published_many(const float *x, float *y, int64_t n, int fused) {
+    for (int64_t i = 0; i < n; i++) y[i] = orc_expf_published(x[i], fused);
+}
+
 /* src/lib/tlm_model.c:171-172 */
 float orc_silu(float x) { return x / (1.0f + expf(-x)); }
 float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }

@@ -59,6 +59,10 @@ void  orc_block_isum(int dt, const void *wblock, const void *act_block,
 
 /* ---- decoder glue (src/lib/tlm_model.c:164-172, 776-839) ------------------ */
 void  orc_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps);
+void orc_expf_many(const float *x, float *y, int64_t n);
+uint64_t orc_exp2_tab(int i);
+float orc_expf_published(float x, int fused);
+void orc_expf_published_many(const float *x, float *y, int64_t n, int fused);
 float orc_silu(float x);
 float orc_sigmoid(float x);
 void  orc_topk(const float *v, const uint8_t *mask, int E, int k, int *ids);

@@ -113,17 +113,3 @@ def device_block(case, device, *, router=0, routed_scale=1.0, eps=1e-6, mask=Non
                      shared=shared, shared_gate_inp=t(shared_gate_inp), device=device)
     torch.cuda.synchronize()
     return block, keep
-
-
-def residual_tolerance(want_h, want_w, got_w, trace_eo, rtol=1e-5):
-    """Per-element bound for a device residual against the oracle's:
-    rtol x (|ref| + 1e-3 max|ref|), plus what a routing weight that differs in
-    its last place contributes through the combine, sum_r |dw_r| |eo_r|.  The
-    device's e^x is not libm's expf, so a weight can differ by an ulp; where
-    the combine cancels (large expert outputs, small sum) that alone can exceed
-    the relative bound, and nothing else is admitted."""
-    want_h = np.asarray(want_h, np.float32)
-    dw = np.abs(np.asarray(got_w, np.float64) - np.asarray(want_w, np.float64))
-    assert np.all(dw <= 2 * np.spacing(np.abs(np.asarray(want_w, np.float32))).astype(np.float64)), (got_w, want_w)
-    base = rtol * (np.abs(want_h) + 1e-3 * np.abs(want_h).max())
-    return base + (dw[:, None] * np.abs(np.asarray(trace_eo, np.float64))).sum(0) * 1.01

@@ -1,28 +1,24 @@
 """The device MoE block (tlm_hip_moe_layer) vs the oracle's MoE block
 (src/lib/tlm_model.c:940-1055).
 
-Tolerance (from the build's numerics contract): routing ids identical,
-weights within an ulp; the updated residual within 1e-5 relative per element,
-relative to |ref| + 1e-3 * max|ref|, plus what an ulp of routing weight
-contributes through the combine (tests.synth.residual_tolerance).  Integer
-block sums, fma chains, quantisation and the combine order are the
-reference's, so most elements are bit-identical; the device e^x (silu,
-softmax) and the tree-ordered double sum of rmsnorm can move a value by about
-an ulp."""
+Bar: bit for bit - routing ids, routing weights and every element of the
+updated residual.  Integer block sums, fma chains, quantisation, the combine
+order and e^x (libm's expf, restated) are the reference's; the one remaining
+difference in order, rmsnorm's double sum of squares as a tree, changes the
+float result only when that sum lies within a few double ulps of a float
+rounding boundary (never met in these cases)."""
 import numpy as np
 import pytest
 import torch
 
 import oracle
-from tests.synth import build_moe_case, residual_tolerance
+from tests.synth import build_moe_case
 
 pytestmark = pytest.mark.gpu
 
-RTOL = 1e-5
 
-
-def rel_err(got, want):
-    return np.abs(got - want) / (np.abs(want) + 1e-3 * np.abs(want).max())
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
 def run_dev(case, h0, dev):
@@ -34,18 +30,14 @@ def run_dev(case, h0, dev):
 
 def check_case(case, dev, tokens=3, seed=0):
     rng = np.random.default_rng(seed)
-    worst, exact = 0.0, []
     for t in range(tokens):
         h0 = case.h0 if t == 0 else (rng.standard_normal(case.D) * (1 + t)).astype(np.float32)
-        want_h, want_ids, want_w, tr = case.host.run(h0, trace=True)
+        want_h, want_ids, want_w, _ = case.host.run(h0, trace=True)
         got_h, got_ids, got_w = run_dev(case, h0, dev)
         assert np.array_equal(got_ids, want_ids), (t, got_ids, want_ids)
-        e = rel_err(got_h, want_h)
-        worst = max(worst, float(e.max()))
-        exact.append(np.mean(got_h.view(np.uint32) == want_h.view(np.uint32)))
-        tol = residual_tolerance(want_h, want_w, got_w, tr["eo"], RTOL)
-        assert np.all(np.abs(got_h - want_h) <= tol), f"token {t}: max rel err {e.max():.3g}"
-    return worst, float(np.mean(exact))
+        assert np.array_equal(bits(got_w), bits(want_w)), (t, got_w, want_w)
+        nd = int((bits(got_h) != bits(want_h)).sum())
+        assert nd == 0, f"token {t}: {nd} of {case.D} residual elements differ from the oracle"
 
 
 def test_moe_small_config_shape(hip, dev):
@@ -53,8 +45,7 @@ def test_moe_small_config_shape(hip, dev):
     Q6_K experts, Q8_0 shared expert of width 256, softmax + renormalise."""
     case = build_moe_case(D=512, de=256, E=32, k=4, ds=256, expert_dt=oracle.Q6_K, shared_dt=oracle.Q8_0,
                           seed=21, device=dev)
-    worst, exact = check_case(case, dev, tokens=5)
-    assert exact > 0.5, f"only {exact:.2%} of outputs bit-identical"
+    check_case(case, dev, tokens=5)
 
 
 def test_moe_qwen3_30b_shape(hip, dev):

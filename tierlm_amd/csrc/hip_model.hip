@@ -11,10 +11,12 @@
  * router, routing, combine and quantisers are bit-exact (hip_gemv.hip,
  * hip_moe.hip); RoPE and the attention dot products, the softmax scaling and
  * the P.V sums run in the reference's order with separate roundings (one
- * thread per dot product, positions in ascending order).  What may differ in
- * the last bit: sums of squares and the softmax sum are double trees instead
- * of sequential double sums, and e^x is exp in double rounded to float; the
- * reference's greedy tokens are reproduced exactly. */
+ * thread per dot product, positions in ascending order) and e^x is libm's
+ * expf bit for bit (expf_ref).  What may differ in the last bit: sums of
+ * squares and the softmax sum are double trees instead of sequential double
+ * sums (a float rounding of them moves only when the double sum lies within a
+ * few double ulps of a float rounding boundary); the reference's greedy
+ * tokens are reproduced exactly. */
 #include "tlm_hip_internal.h"
 #include <hip/hip_fp16.h>
 #include "tlm_hip_act.h"
@@ -31,18 +33,6 @@ int tlmh_current_device(void);
 namespace {
 
 constexpr int NT = 256;
-
-/* ---- block reductions ------------------------------------------------------ */
-__device__ double block_sum_f64(double v, double *red) {
-    v = wave_sum_f64(v);
-    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    double s = 0.0;
-    for (int i = 0; i < nw; i++) s += red[i];
-    return s;
-}
 
 /* ---- embedding row (tlm_dequantize_row, src/lib/tlm_quant.c:629-660) -------- */
 /* The step's position and token live in device memory (st[0] = pos, seq[pos]
@@ -62,101 +52,153 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
     }
 }
 
-/* ---- attention for one query head, everything it needs fused ---------------
- * (src/lib/tlm_model.c:743-756 with attn_heads :683-719): the head's q-norm
- * and RoPE, the k-norm and RoPE of its key head and the KV append (written by
- * the first query head of each key head; the others take the new key and
- * value from their own copy), scores, softmax and P.V in the reference's
- * order, the output stored to att.  Each score is one thread's dot product in
- * ascending i, each output element one thread's sum over positions in
- * ascending t.
+/* ---- attention: attention() (src/lib/tlm_model.c:743-756) and attn_heads
+ * (:683-719), the reference's bits, in two launches -------------------------
+ * k_attn_scores: one group per (key head, slice of positions).  It
+ * normalises and rotates the query heads that share the key head (q-norm,
+ * RoPE) and the new key (k-norm, RoPE), then walks its slice in chunks of
+ * ATT_CH positions staged in LDS and stores every (query head, position)
+ * score - the dot in ascending i, scaled after the dot - with the slice's
+ * maximum per query head; the group whose slice holds the new position
+ * appends its key and value to the cache.
+ * k_attn_pv: a group per QPG query heads.  The softmax in the reference's
+ * order - the maximum over the slice maxima, e_t = e^(s_t - max), their sum in
+ * double, inv = 1 / sum, p_t = e_t * inv (probabilities in LDS) - then the
+ * P.V sums: one lane per output element runs the reference's chain
+ * out += p_t * v_t[i] over ascending t, one wave per 64 elements, so that
+ * each SIMD holds one chain wave.  V streams into registers two blocks of
+ * ATT_PD positions ahead (a lane reads column i of consecutive rows; the
+ * wave's lanes cover 256 contiguous bytes of a row).
  *
- * Cache layout (per layer and key head): keys dimension-major, K[i][t] at
- * i * max_ctx + t, so that the lanes of a score pass (one position each)
- * read consecutive words for every i; values position-major, V[t][i], so
- * that a chunk of positions is one contiguous run.
+ * Numerics: the scores, maxima, products and chains are the reference's
+ * operations in its order; the double sum of the softmax terms is a tree
+ * instead of a sequence (its float reciprocal can differ only when that sum
+ * lies within a double ulp or so of a rounding boundary); e^x is libm's expf
+ * (expf_ref).
  *
- * Latency, not bandwidth, sets this kernel's time (one group per head), so
- * it is arranged around the memory counter, which retires loads in issue
- * order: the loads go out unconditionally (indices clamped) in the order the
- * values are consumed - head vectors, norm weights and RoPE factors and the
- * first pass's key columns per thread at entry (HD <= 128; later passes load
- * theirs at once too), the first two V chunks (ATT_VF floats each) once the
- * scores are done - and no global store precedes a barrier (a barrier waits
- * for the group's stores): the KV append goes last.  The
- * probabilities stay in LDS (dynamic, max_ctx floats) when SPL, else in the
- * head's global scratch row; they are scaled by 1/sum in place (the
- * reference's p = s[t] * inv).  P.V is a pipeline inside the group: waves
- * 2-3 hold V chunks two ahead in registers and store each chunk to one of
- * two LDS buffers as the products p_t * v_t[i]; waves 0-1 (one output
- * element per lane) sum the previous chunk meanwhile, 16 positions per group
- * of LDS reads, the last group of a chunk read whole (a chunk holds a
- * multiple of 16 positions) and its adds masked.  q_norm / k_norm are read
- * only when has_qn / has_kn. */
-constexpr int ATT_VF = 8192;                 /* floats of V per LDS chunk (32 KB) */
-constexpr int ATT_PF = ATT_VF / 4 / 128;     /* 16-byte V loads per producer thread per chunk */
-constexpr int ATT_LDS_POS = 4096;            /* contexts whose probabilities fit in LDS */
-constexpr int ATT_PU = 16;                   /* positions per group in the ordered sums */
-constexpr int ATT_SPLIT_MIN = 2 * NT;         /* longest context scored inside the fused launch */
+ * Cache layout (per layer and key head, the reference's own): K[t][i] and
+ * V[t][i] at t * HD + i.  Slices: G per key head (fixed for the captured
+ * graph), att_slice_len(T, G) positions at context T; groups past the
+ * context return at once. */
+constexpr int ATT_CH = 32;       /* positions per LDS chunk of the scores */
+constexpr int ATT_LMIN = 32;     /* shortest slice */
+constexpr int ATT_QMAX = 4096;   /* query values per key head (query heads per key head x HD) */
+constexpr int ATT_GMAX = 128;    /* slices per key head */
+constexpr int ATT_PD = 32;       /* V positions per register block of a chain */
 
-/* max over non-NaN values (a NaN never compares greater), -inf if none */
-__device__ float block_max_dpp(float v, float *red) {
-    v = wave_max_f32(v);
-    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float m = -INFINITY;
-    for (int i = 0; i < nw; i++) m = red[i] > m ? red[i] : m;
-    return m;
+__host__ __device__ inline int att_slice_len(int T, int G) {
+    int L = (T + G - 1) / G;
+    L = (L + 15) & ~15;
+    return L < ATT_LMIN ? ATT_LMIN : L;
 }
 
-/* Scores of one query head over one slice of NT positions (grid: heads x
- * max_ctx / NT slices; slices past the current position return): the head's
- * q (wave 0) and the new key (wave 1) normalised and rotated exactly as the
- * fused launch does it, then one position per thread - the dot in ascending
- * i, scaled after the dot - into the head's score row, and the slice's
- * maximum (non-NaN values, -inf if none) into smax[h * nslice + slice]. */
+/* LDS of k_attn_scores, offsets in floats: query heads, new key and value,
+ * a chunk of K (rows padded by 4 floats) */
+struct AttLds {
+    int q, kn, vn, k, total;
+};
+__host__ __device__ inline AttLds att_lds(int hd, int R) {
+    AttLds o;
+    o.q = 0;
+    o.kn = R * hd;
+    o.vn = o.kn + hd;
+    o.k = o.vn + hd;
+    o.total = o.k + ATT_CH * (hd + 4);
+    return o;
+}
+
+/* max over the aligned 32 lanes of a half wave, uniform in it (no NaN
+ * inputs wins: a NaN never compares greater) */
+__device__ __forceinline__ float half_max_f32(float v) {
+    float o;
+    o = dpp_f32<DPP_XOR1>(v);        v = o > v ? o : v;
+    o = dpp_f32<DPP_XOR2>(v);        v = o > v ? o : v;
+    o = dpp_f32<DPP_HALF_MIRROR>(v); v = o > v ? o : v;
+    o = dpp_f32<DPP_MIRROR>(v);      v = o > v ? o : v;
+    o = __shfl_xor(v, 16, 64);       v = o > v ? o : v;
+    return v;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int HD>
 __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kx,
-                                                    const float *__restrict__ q_norm, const float *__restrict__ k_norm,
-                                                    int has_qn, int has_kn, const float *__restrict__ cs_all,
-                                                    const float *__restrict__ sn_all, const float *__restrict__ kc,
+                                                    const float *__restrict__ vx, const float *__restrict__ q_norm,
+                                                    const float *__restrict__ k_norm, int has_qn, int has_kn,
+                                                    const float *__restrict__ cs_all, const float *__restrict__ sn_all,
+                                                    float *__restrict__ kc, float *__restrict__ vc,
                                                     float *__restrict__ scores, float *__restrict__ smax, int H,
-                                                    int KV, int max_ctx, const int32_t *__restrict__ st, float eps) {
-    constexpr int HALF = HD / 2, H4 = HD / 4;
-    constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;
-    constexpr bool KPRE = HD <= 128;
-    __shared__ __align__(16) float s_q[HD], s_k[HD];
-    __shared__ float s_redf[NT / 64];
-    const int pos = st[0], T = pos + 1;
-    const int p0 = (int)blockIdx.y * NT;
-    if (p0 >= T) return;
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int kvh = h / (H / KV);
-    const float *K = kc + (size_t)kvh * max_ctx * HD;
-    const int t = p0 + tid;
-    const float *hv = wave == 1 ? kx + (size_t)kvh * HD : q + (size_t)h * HD;
-    const float *nwp = wave == 1 ? k_norm : q_norm;
-    float e[KE], nw[KE], cv[KH], sv[KH];
+                                                    int KV, int max_ctx, int G, const int32_t *__restrict__ st,
+                                                    float eps) {
+    constexpr int H4 = HD / 4, HALF = HD / 2, KS = HD + 4;
+    constexpr int CF = ATT_CH * H4 / NT;            /* float4 of a chunk's K per thread */
+    constexpr int QF = ATT_QMAX / 4 / NT;           /* float4 of the query heads per thread, at most */
+    constexpr int SU = ATT_QMAX / HD * ATT_CH / NT; /* (query head, position) items per thread per chunk, at most */
+    constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;   /* elements / pairs per lane */
+    extern __shared__ __align__(16) float s_dyn[];
+    const int pos = st[0], T = pos + 1, R = H / KV;
+    const int L = att_slice_len(T, G), t0 = (int)blockIdx.y * L;
+    if (t0 >= T) return;
+    const int tn = min(L, T - t0), kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const AttLds lo = att_lds(HD, R);
+    float *s_q = s_dyn + lo.q, *s_kn = s_dyn + lo.kn, *s_vn = s_dyn + lo.vn, *s_k = s_dyn + lo.k;
+    float *K = kc + (size_t)kvh * max_ctx * HD, *V = vc + (size_t)kvh * max_ctx * HD;
+
+    /* every load at entry, in the order of use: the query heads (consecutive
+     * heads h = kvh * R + j), the new key and value, norm weights and RoPE
+     * factors, then the first chunk's key rows (clamped to the context; rows
+     * past the slice are never used) */
+    const int nq4 = R * H4;
+    const f32x4 *q4 = (const f32x4 *)(q + (size_t)kvh * R * HD);
+    f32x4 qv[QF];
 #pragma unroll
-    for (int k = 0; k < KE; k++) e[k] = hv[min(lane + 64 * k, HD - 1)];
+    for (int k = 0; k < QF; k++) qv[k] = q4[min(tid + NT * k, nq4 - 1)];
+    const f32x4 knv = ((const f32x4 *)kx)[(size_t)kvh * H4 + min(tid, H4 - 1)];
+    const f32x4 vnv = ((const f32x4 *)vx)[(size_t)kvh * H4 + min(tid, H4 - 1)];
+    float qn[KE], kn[KE], cv[KH], sv[KH];
 #pragma unroll
-    for (int k = 0; k < KE; k++) nw[k] = nwp[min(lane + 64 * k, HD - 1)];
+    for (int k = 0; k < KE; k++) qn[k] = q_norm[min(lane + 64 * k, HD - 1)];
+#pragma unroll
+    for (int k = 0; k < KE; k++) kn[k] = k_norm[min(lane + 64 * k, HD - 1)];
 #pragma unroll
     for (int k = 0; k < KH; k++) {
         cv[k] = cs_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
         sv[k] = sn_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
     }
-    float kr[KPRE ? HD : 1];
-    if constexpr (KPRE) {   /* this slice's key columns, all at once (rows clamped to pos) */
-        const float *kt = K + min(t, pos);
+    const int nch = (tn + ATT_CH - 1) / ATT_CH;
+    f32x4 kr[CF];
+    auto kload = [&](int c) {
+        const int tc = t0 + c * ATT_CH;
 #pragma unroll
-        for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
+        for (int k = 0; k < CF; k++) {
+            const int e = tid + NT * k, t = min(tc + e / H4, T - 1);
+            kr[k] = ((const f32x4 *)(K + (size_t)t * HD))[e % H4];
+        }
+    };
+    kload(0);
+
+#pragma unroll
+    for (int k = 0; k < QF; k++)
+        if (tid + NT * k < nq4) ((f32x4 *)s_q)[tid + NT * k] = qv[k];
+    if (tid < H4) {
+        ((f32x4 *)s_kn)[tid] = knv;
+        ((f32x4 *)s_vn)[tid] = vnv;
     }
-    if (wave < 2) {   /* norm (tlm_model.c:743-746) and RoPE (rope(), :721-728: pairs (j, j + HD/2)) */
-        float *v = wave == 0 ? s_q : s_k;
-        if (wave == 0 ? has_qn : has_kn) {
+    __syncthreads();
+
+    /* rmsnorm of each query head and of the new key (tlm_model.c:743-746:
+     * double sum of squares, x * r * w), then RoPE (rope(), :721-728: pairs
+     * (j, j + HD/2)); vector R is the key, one vector per wave at a time */
+    for (int v = wave; v <= R; v += NT / 64) {
+        float *x = v < R ? s_q + v * HD : s_kn;
+        if (v < R ? has_qn : has_kn) {
+            float e[KE];
+#pragma unroll
+            for (int k = 0; k < KE; k++) e[k] = x[min(lane + 64 * k, HD - 1)];
             double ss = 0.0;
 #pragma unroll
             for (int k = 0; k < KE; k++)
@@ -164,374 +206,225 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
             ss = wave_sum_f64(ss);
             const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
 #pragma unroll
-            for (int k = 0; k < KE; k++) e[k] = e[k] * r * nw[k];
+            for (int k = 0; k < KE; k++)
+                if (lane + 64 * k < HD) x[lane + 64 * k] = e[k] * r * (v < R ? qn[k] : kn[k]);
+            wave_lds_sync();
         }
-#pragma unroll
-        for (int k = 0; k < KE; k++)
-            if (lane + 64 * k < HD) v[lane + 64 * k] = e[k];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int k = 0; k < KH; k++) {
             const int j = lane + 64 * k;
             if (j < HALF) {
-                const float a = v[j], c = v[j + HALF];
-                v[j] = a * cv[k] - c * sv[k];
-                v[j + HALF] = c * cv[k] + a * sv[k];
+                const float a = x[j], c = x[j + HALF];
+                x[j] = a * cv[k] - c * sv[k];
+                x[j + HALF] = c * cv[k] + a * sv[k];
             }
         }
     }
     __syncthreads();
+
     const float scale = 1.0f / sqrtf((float)HD);
-    const f32x4 *q4 = (const f32x4 *)s_q;
-    float d = 0.0f, mx = -INFINITY;
-    if (KPRE) {
-        if (t == pos) {   /* the new key, from this group's copy */
+    const int nsc = R * ATT_CH;
+    float rmx[SU];
 #pragma unroll
-            for (int i4 = 0; i4 < H4; i4++) {
-                const f32x4 k4 = ((const f32x4 *)s_k)[i4];
-                kr[4 * i4] = k4.x;
-                kr[4 * i4 + 1] = k4.y;
-                kr[4 * i4 + 2] = k4.z;
-                kr[4 * i4 + 3] = k4.w;
+    for (int u = 0; u < SU; u++) rmx[u] = -INFINITY;
+    for (int c = 0; c < nch; c++) {   /* uniform over the group */
+        const int tc = t0 + c * ATT_CH, tnc = min(ATT_CH, tn - c * ATT_CH);
+        /* stage the chunk's keys; row pos from this group's copy */
+#pragma unroll
+        for (int k = 0; k < CF; k++) {
+            const int e = tid + NT * k, t = e / H4, i4 = e % H4;
+            ((f32x4 *)(s_k + t * KS))[i4] = tc + t == pos ? ((const f32x4 *)s_kn)[i4] : kr[k];
+        }
+        __syncthreads();
+        if (c + 1 < nch) kload(c + 1);   /* the next chunk flies while this one is scored */
+        /* item (j, t), positions fastest: a query head's ATT_CH positions are
+         * one half wave */
+#pragma unroll
+        for (int u = 0; u < SU; u++) {
+            const int idx = tid + NT * u;
+            if (idx < nsc) {
+                const int j = idx / ATT_CH, t = idx % ATT_CH;
+                const f32x4 *qq = (const f32x4 *)(s_q + j * HD), *kk = (const f32x4 *)(s_k + t * KS);
+                float d = 0.0f;
+#pragma unroll 8
+                for (int i4 = 0; i4 < H4; i4++) {
+                    const f32x4 a = qq[i4], b = kk[i4];
+                    d += a.x * b.x;
+                    d += a.y * b.y;
+                    d += a.z * b.z;
+                    d += a.w * b.w;
+                }
+                d *= scale;   /* after the dot, before the maximum (tlm_model.c:699-702) */
+                if (t < tnc) {
+                    scores[(size_t)(kvh * R + j) * max_ctx + tc + t] = d;
+                    rmx[u] = d > rmx[u] ? d : rmx[u];
+                }
             }
         }
+        __syncthreads();   /* before the next chunk overwrites the keys */
+    }
 #pragma unroll
-        for (int c = 0; c < HD / 16; c++) {   /* q in batches of 16 */
-            f32x4 qb[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) qb[u] = q4[4 * c + u];
-#pragma unroll
-            for (int u = 0; u < 16; u++) d += qb[u / 4][u % 4] * kr[16 * c + u];
+    for (int u = 0; u < SU; u++) {
+        const int idx = tid + NT * u;
+        if (idx < nsc) {
+            const float m = half_max_f32(rmx[u]);
+            if (idx % ATT_CH == 0) smax[(size_t)(kvh * R + idx / ATT_CH) * G + blockIdx.y] = m;
         }
-    } else if (t == pos) {
-#pragma unroll
-        for (int i = 0; i < HD; i++) d += s_q[i] * s_k[i];
-    } else if (t < T) {
-        const float *kt = K + t;
-#pragma unroll 16
-        for (int i = 0; i < HD; i++) d += s_q[i] * kt[(size_t)i * max_ctx];
     }
-    if (t < T) {
-        d *= scale;
-        scores[(size_t)h * max_ctx + t] = d;
-        if (d > mx) mx = d;
-    }
-    mx = block_max_dpp(mx, s_redf);
-    if (tid == 0) smax[(size_t)h * gridDim.y + blockIdx.y] = mx;
+    if (t0 + tn == T)   /* the KV append (tlm_model.c:748-752), after the last read */
+        for (int i4 = tid; i4 < H4; i4 += NT) {
+            ((f32x4 *)K)[(size_t)pos * H4 + i4] = ((const f32x4 *)s_kn)[i4];
+            ((f32x4 *)V)[(size_t)pos * H4 + i4] = ((const f32x4 *)s_vn)[i4];
+        }
 }
 
-template <int HD, bool SPL, bool SPLIT>
-__global__ __launch_bounds__(NT) void k_attn_fused(const float *__restrict__ q, const float *__restrict__ kx,
-                                                   const float *__restrict__ vx, const float *__restrict__ q_norm,
-                                                   const float *__restrict__ k_norm, int has_qn, int has_kn,
-                                                   const float *__restrict__ cs_all, const float *__restrict__ sn_all,
-                                                   float *__restrict__ kc, float *__restrict__ vc,
-                                                   float *__restrict__ scores, const float *__restrict__ smax,
-                                                   float *__restrict__ att, int H, int KV, int max_ctx,
-                                                   const int32_t *__restrict__ st, float eps) {
-    constexpr int HALF = HD / 2, H4 = HD / 4;
-    constexpr int VC = (ATT_VF / HD) & ~(ATT_PU - 1);   /* V positions per chunk */
-    constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;     /* elements / pairs per lane */
-    constexpr bool KPRE = HD <= 128 && !SPLIT;
-    extern __shared__ __align__(16) float s_dyn[];
-    __shared__ __align__(16) float s_q[HD], s_k[HD], s_vn[HD];
-    __shared__ __align__(16) float s_v[2 * ATT_VF];
-    __shared__ double s_red[NT / 64];
-    __shared__ float s_redf[NT / 64];
-    const int pos = st[0], T = pos + 1;
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int kvh = h / (H / KV);
-    const float *K = kc + (size_t)kvh * max_ctx * HD, *V = vc + (size_t)kvh * max_ctx * HD;
+template <int HD>
+__global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ smax,
+                                                const float *__restrict__ vc, float *__restrict__ att, int H, int KV,
+                                                int max_ctx, int G, const int32_t *__restrict__ st) {
+    constexpr int NWC = (HD + 63) / 64;          /* chain waves per query head */
+    constexpr int QPG = NWC <= 4 ? 4 / NWC : 1;  /* query heads per group */
+    constexpr int TPH = NT / QPG;                /* threads per head in the softmax */
+    constexpr int PSEG = 8192 / QPG;             /* probabilities per head in LDS */
+    constexpr int PB = 8;                        /* score loads per thread per round */
+    constexpr int GM = ATT_GMAX / 64;            /* slice maxima per lane */
+    __shared__ __align__(16) float s_p[QPG][PSEG + ATT_PD];
+    __shared__ double s_sum[NT / 64];
+    const int pos = st[0], T = pos + 1, L = att_slice_len(T, G), ns = (T + L - 1) / L;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h0 = (int)blockIdx.x * QPG;
+    /* softmax role: head jj (a wave never straddles two), positions tt + TPH k */
+    const int jj = tid / TPH, tt = tid % TPH, hs = min(h0 + jj, H - 1);
+    /* chain role: head jc, element ic */
+    const int jc = wave / NWC, hc = h0 + jc, ic = 64 * (wave % NWC) + lane;
+    const bool chain = jc < QPG && hc < H;
+    const float *S = scores + (size_t)hs * max_ctx;
+    const float *vcol = vc + (size_t)(min(hc, H - 1) / (H / KV)) * max_ctx * HD + min(ic, HD - 1);
 
-    /* 1. wave 0: the query head, wave 1: the key head, wave 2: the value
-     *    head (the others load the query head too and drop it) */
-    const float *hv = wave == 1 ? kx + (size_t)kvh * HD : wave == 2 ? vx + (size_t)kvh * HD : q + (size_t)h * HD;
-    const float *nwp = wave == 1 ? k_norm : q_norm;
-    float e[KE], nw[KE], cv[KH], sv[KH];
+    /* entry loads: the head's slice maxima, the first scores, the chain's first V block */
+    float mm[GM];
 #pragma unroll
-    for (int k = 0; k < KE; k++) e[k] = hv[min(lane + 64 * k, HD - 1)];
+    for (int k = 0; k < GM; k++) mm[k] = smax[(size_t)hs * G + min(lane + 64 * k, ns - 1)];
+    float sv[PB];
 #pragma unroll
-    for (int k = 0; k < KE; k++) nw[k] = nwp[min(lane + 64 * k, HD - 1)];
+    for (int k = 0; k < PB; k++) sv[k] = S[min(tt + TPH * k, T - 1)];
+    float va[ATT_PD], vb[ATT_PD];
+    auto vld = [&](int t0, float (&r)[ATT_PD]) {
 #pragma unroll
-    for (int k = 0; k < KH; k++) {
-        cv[k] = cs_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
-        sv[k] = sn_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
-    }
-    /* 2. without the split launch: the first pass's key columns */
-    float kr[KPRE ? HD : 1];
-    if constexpr (KPRE) {
-        const float *kt = K + min(tid, pos);
-#pragma unroll
-        for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
-    }
-    /* V chunks (VC positions): the producer threads (tid >= 128, waves 2-3)
-     * hold two in registers, loaded two chunks ahead */
-    const int ptid = tid - 128, nch = (T + VC - 1) / VC;
-    f32x4 va[ATT_PF], vb[ATT_PF];
-    auto vload = [&](int c, f32x4 (&pv)[ATT_PF]) {
-        const int t0 = c * VC;
-        const int n4 = (T - t0 < VC ? T - t0 : VC) * H4;
-        const f32x4 *src = (const f32x4 *)(V + (size_t)t0 * HD);
-#pragma unroll
-        for (int j = 0; j < ATT_PF; j++) pv[j] = src[min(ptid + 128 * j, n4 - 1)];
+        for (int u = 0; u < ATT_PD; u++) r[u] = vcol[(size_t)min(t0 + u, T - 1) * HD];
     };
+    if (chain) vld(0, va);
 
-    /* norm (tlm_model.c:743-746) and RoPE (rope(), :721-728: pairs (j, j + HD/2)) */
-    if (wave < 3) {
-        float *v = wave == 0 ? s_q : wave == 1 ? s_k : s_vn;
-        if (wave < 2 && (wave == 0 ? has_qn : has_kn)) {
-            double ss = 0.0;
+    float mx = -INFINITY;   /* the reference's maximum: NaN never compares greater */
 #pragma unroll
-            for (int k = 0; k < KE; k++)
-                if (lane + 64 * k < HD) ss += (double)e[k] * (double)e[k];
-            ss = wave_sum_f64(ss);
-            const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
-#pragma unroll
-            for (int k = 0; k < KE; k++) e[k] = e[k] * r * nw[k];
-        }
-#pragma unroll
-        for (int k = 0; k < KE; k++)
-            if (lane + 64 * k < HD) v[lane + 64 * k] = e[k];
-        if (wave < 2) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int k = 0; k < KH; k++) {
-                const int j = lane + 64 * k;
-                if (j < HALF) {
-                    const float a = v[j], c = v[j + HALF];
-                    v[j] = a * cv[k] - c * sv[k];
-                    v[j + HALF] = c * cv[k] + a * sv[k];
-                }
-            }
-        }
-    }
-    __syncthreads();
-
-    /* scores (scale after the dot, before the max): from the split launch
-     * (the head's row and its slices' maxima), or here, a pass of NT
-     * positions at a time */
-    float *sp;
-    if constexpr (SPL) sp = s_dyn;
-    else sp = scores + (size_t)h * max_ctx;
-    const float *sg = SPLIT ? (const float *)(scores + (size_t)h * max_ctx) : (const float *)sp;
-    float mx = -INFINITY;   /* the maximum of non-NaN values, -inf if none */
-    if constexpr (SPLIT) {
-        if (tid >= 128) {   /* the first V chunks go out before the maximum, exp and sum */
-            vload(0, va);
-            if (nch > 1) vload(1, vb);
-        }
-        const int nslice = (max_ctx + NT - 1) / NT, nsl = (T + NT - 1) / NT;
-        for (int i = 0; i < nsl; i++) {
-            const float m = smax[(size_t)h * nslice + i];
-            mx = m > mx ? m : mx;
-        }
-    } else {
-        const float scale = 1.0f / sqrtf((float)HD);
-        const f32x4 *q4 = (const f32x4 *)s_q;
-        for (int p0 = 0; p0 < T; p0 += NT) {   /* passes of NT positions, uniform over the group */
-            const int t = p0 + tid;
-            float d = 0.0f;
-            if (KPRE) {
-                if (p0 > 0) {   /* this pass's key columns, all at once (rows clamped to pos) */
-                    const float *kt = K + min(t, pos);
-#pragma unroll
-                    for (int i = 0; i < HD; i++) kr[i] = kt[(size_t)i * max_ctx];
-                }
-                if (t == pos) {   /* the new key, from this group's copy */
-#pragma unroll
-                    for (int i4 = 0; i4 < H4; i4++) {
-                        const f32x4 k4 = ((const f32x4 *)s_k)[i4];
-                        kr[4 * i4] = k4.x;
-                        kr[4 * i4 + 1] = k4.y;
-                        kr[4 * i4 + 2] = k4.z;
-                        kr[4 * i4 + 3] = k4.w;
-                    }
-                }
-#pragma unroll
-                for (int c = 0; c < HD / 16; c++) {   /* q in batches of 16 */
-                    f32x4 qb[4];
-#pragma unroll
-                    for (int u = 0; u < 4; u++) qb[u] = q4[4 * c + u];
-#pragma unroll
-                    for (int u = 0; u < 16; u++) d += qb[u / 4][u % 4] * kr[16 * c + u];
-                }
-            } else if (t == pos) {
-#pragma unroll
-                for (int i = 0; i < HD; i++) d += s_q[i] * s_k[i];
-            } else if (t < T) {
-                const float *kt = K + t;
-#pragma unroll 16
-                for (int i = 0; i < HD; i++) d += s_q[i] * kt[(size_t)i * max_ctx];
-            }
-            if (t < T) {
-                d *= scale;
-                sp[t] = d;
-                if (d > mx) mx = d;
-            }
-        }
-        if (tid >= 128) {   /* the key registers are free now; max, exp and sum cover the latency */
-            vload(0, va);
-            if (nch > 1) vload(1, vb);
-        }
-        mx = block_max_dpp(mx, s_redf);
-    }
+    for (int k = 0; k < GM; k++) mx = mm[k] > mx ? mm[k] : mx;
+    mx = wave_max_f32(mx);
+    const int nseg = (T + PSEG - 1) / PSEG;
+    float *prow = s_p[jj];
     double sum = 0.0;
-    for (int t = tid; t < T; t += NT) {
-        const float p = exp_rn(sg[t] - mx);
-        sp[t] = p;
-        sum += (double)p;
+    for (int b0 = 0; b0 < T; b0 += PB * TPH) {   /* e_t and their sum (tlm_model.c:704-709) */
+        if (b0 > 0) {
+#pragma unroll
+            for (int k = 0; k < PB; k++) sv[k] = S[min(b0 + tt + TPH * k, T - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int t = b0 + tt + TPH * k;
+            if (t < T) {
+                const float e = expf_ref(sv[k] - mx);
+                sum += (double)e;
+                if (nseg == 1) prow[t] = e;
+            }
+        }
     }
-    sum = block_sum_f64(sum, s_red);
-    const float inv = (float)(1.0 / sum);
-    for (int t = tid; t < T; t += NT) sp[t] = sp[t] * inv;
-    __syncthreads();   /* every p stored before the producers read them */
-
-    /* P.V, chunk by chunk, as a pipeline inside the group: the producers
-     * store chunk c + 1 to LDS as the products c = p_t * v_t[i] (the
-     * reference's product, bit for bit) while the consumers (tid < 128, lane
-     * = output element i, and i + 128 when HD = 256) run the ordered sums over
-     * chunk c - one add per position; two LDS buffers, one barrier per chunk.
-     * A producer reads its chunk's probabilities at once (one wait), and the
-     * new row only in the last chunk. */
-    constexpr int CD = (HD + 127) / 128;
-    float o[CD];
-#pragma unroll
-    for (int m = 0; m < CD; m++) o[m] = 0.0f;
-    float *buf0 = s_v, *buf1 = s_v + ATT_VF;
-    auto produce = [&](int c, const f32x4 (&pv)[ATT_PF], float *buf) {
-        const int t0 = c * VC, tn = T - t0 < VC ? T - t0 : VC;
-        float pt[ATT_PF];
-#pragma unroll
-        for (int j = 0; j < ATT_PF; j++) {
-            const int tl = (ptid + 128 * j) / H4;
-            pt[j] = sp[t0 + min(tl, tn - 1)];
-        }
-        if (c == nch - 1) {   /* the chunk holding row pos: this group's copy, and nothing past T */
-#pragma unroll
-            for (int j = 0; j < ATT_PF; j++) {
-                const int e4 = ptid + 128 * j, tl = e4 / H4;
-                f32x4 v4 = t0 + tl == pos ? ((const f32x4 *)s_vn)[e4 % H4] : pv[j];
-                const float q = tl < tn ? pt[j] : 0.0f;
-                f32x4 cc;
-#pragma unroll
-                for (int k = 0; k < 4; k++) cc[k] = q * v4[k];
-                ((f32x4 *)buf)[e4] = cc;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < ATT_PF; j++) {
-                f32x4 cc;
-#pragma unroll
-                for (int k = 0; k < 4; k++) cc[k] = pt[j] * pv[j][k];
-                ((f32x4 *)buf)[ptid + 128 * j] = cc;
-            }
-        }
-    };
-    auto consume = [&](int c, const float *buf) {
-        const int t0 = c * VC, tn = T - t0 < VC ? T - t0 : VC;
-        const int ng = (tn + ATT_PU - 1) / ATT_PU;
-        /* group g + 1's products load while group g's ordered sums run;
-         * reads past the chunk's last position stay inside the buffer and
-         * are masked in the last group */
-        float ra[CD][ATT_PU], rb[CD][ATT_PU];
-        auto ld = [&](int g, float (&r)[CD][ATT_PU]) {
-#pragma unroll
-            for (int m = 0; m < CD; m++)
-#pragma unroll
-                for (int u = 0; u < ATT_PU; u++) r[m][u] = buf[(g * ATT_PU + u) * HD + min(tid + 128 * m, HD - 1)];
-        };
-        auto add = [&](int g, const float (&r)[CD][ATT_PU]) {
-            if (g + 1 < ng) {
-#pragma unroll
-                for (int u = 0; u < ATT_PU; u++)
-#pragma unroll
-                    for (int m = 0; m < CD; m++) o[m] += r[m][u];
-            } else {
-                const int lim = tn - g * ATT_PU;
-#pragma unroll
-                for (int u = 0; u < ATT_PU; u++)
-#pragma unroll
-                    for (int m = 0; m < CD; m++) {
-                        const float a = o[m] + r[m][u];
-                        o[m] = u < lim ? a : o[m];
-                    }
-            }
-        };
-        ld(0, ra);
-#pragma unroll 1
-        for (int g = 0; g < ng; g += 2) {
-            if (g + 1 < ng) ld(g + 1, rb);
-            add(g, ra);
-            if (g + 1 >= ng) break;
-            if (g + 2 < ng) ld(g + 2, ra);
-            add(g + 1, rb);
-        }
-    };
-    if (tid >= 128) {
-        produce(0, va, buf0);
-        if (nch > 2) vload(2, va);
-    }
+    sum = wave_sum_f64(sum);
+    if (lane == 0) s_sum[wave] = sum;
     __syncthreads();
-    for (int c = 0; c < nch; c += 2) {   /* uniform over the group; even chunks in va / buf0, odd in vb / buf1 */
-        if (tid < 128) consume(c, buf0);
-        else if (c + 1 < nch) {
-            produce(c + 1, vb, buf1);
-            if (c + 3 < nch) vload(c + 3, vb);
+    auto inv_of = [&](int j) {
+        double s = 0.0;
+        for (int w = j * (TPH / 64); w < (j + 1) * (TPH / 64); w++) s += s_sum[w];
+        return (float)(1.0 / s);
+    };
+    const float inv_s = inv_of(jj);
+    float acc = 0.0f;
+    for (int sb = 0; sb < T; sb += PSEG) {   /* uniform over the group */
+        const int se = min(T, sb + PSEG);
+        if (nseg == 1) {   /* each thread scales the terms it stored: p = e * inv */
+            for (int t = tt; t < T; t += TPH) prow[t] = prow[t] * inv_s;
+        } else {
+            for (int t = sb + tt; t < se; t += TPH) prow[t - sb] = expf_ref(S[t] - mx) * inv_s;
         }
         __syncthreads();
-        if (c + 1 >= nch) break;
-        if (tid < 128) consume(c + 1, buf1);
-        else if (c + 2 < nch) {
-            produce(c + 2, va, buf0);
-            if (c + 4 < nch) vload(c + 4, va);
-        }
-        __syncthreads();
-    }
+        if (chain) {
+            const float *pp = s_p[jc];
+            auto add = [&](int t0, const float (&r)[ATT_PD]) {
+                const f32x4 *p4 = (const f32x4 *)(pp + (t0 - sb));
+                if (t0 + ATT_PD <= se) {
 #pragma unroll
-    for (int m = 0; m < CD; m++)
-        if (tid < 128 && tid + 128 * m < HD) att[(size_t)h * HD + tid + 128 * m] = o[m];
-    if (h % (H / KV) == 0)   /* the KV append, after the last barrier */
-        for (int i = tid; i < HD; i += NT) {
-            kc[((size_t)kvh * HD + i) * max_ctx + pos] = s_k[i];
-            vc[((size_t)kvh * max_ctx + pos) * HD + i] = s_vn[i];
+                    for (int u4 = 0; u4 < ATT_PD / 4; u4++) {
+                        const f32x4 p = p4[u4];
+                        acc += p.x * r[4 * u4];
+                        acc += p.y * r[4 * u4 + 1];
+                        acc += p.z * r[4 * u4 + 2];
+                        acc += p.w * r[4 * u4 + 3];
+                    }
+                } else {
+                    const int lim = se - t0;
+#pragma unroll
+                    for (int u = 0; u < ATT_PD; u++) {
+                        const float a = acc + pp[t0 - sb + u] * r[u];
+                        acc = u < lim ? a : acc;
+                    }
+                }
+            };
+            /* blocks of ATT_PD positions, two in flight; a segment holds an even
+             * number of blocks unless it is the last, so va holds block se on leaving */
+            for (int t0 = sb; t0 < se; t0 += 2 * ATT_PD) {
+                if (t0 + ATT_PD < T) vld(t0 + ATT_PD, vb);
+                add(t0, va);
+                if (t0 + ATT_PD >= se) break;
+                if (t0 + 2 * ATT_PD < T) vld(t0 + 2 * ATT_PD, va);
+                add(t0 + ATT_PD, vb);
+            }
         }
+        __syncthreads();   /* before the next segment's probabilities */
+    }
+    if (chain && ic < HD) att[(size_t)hc * HD + ic] = acc;
+}
+
+/* slices per key head: enough groups to cover the chip at long contexts
+ * (about 256 with every key head), a slice at least ATT_LMIN positions long;
+ * req > 0 asks for that many (a test hook: several chunks per slice) */
+int att_groups(int max_ctx, int KV, int req) {
+    if (req > 0) return req < ATT_GMAX ? req : ATT_GMAX;
+    int cap = 256 / KV;
+    cap = cap < 1 ? 1 : cap > ATT_GMAX ? ATT_GMAX : cap;
+    const int want = (max_ctx + ATT_LMIN - 1) / ATT_LMIN;
+    return want < cap ? want : cap;
+}
+
+/* whether the attention kernels take this geometry (query heads per key
+ * head x head width within the scores launch's share and LDS) */
+bool att_supported(int hd, int H, int KV) {
+    const int R = H / KV;
+    return hd % 32 == 0 && hd <= 256 && R * hd <= ATT_QMAX && (size_t)att_lds(hd, R).total * 4 <= 65536;
 }
 
 /* host: launch for the model's head width (a multiple of 32, at most 256) */
-int launch_attn(int hd, int H, int KV, int max_ctx, const float *q, const float *kx, const float *vx,
+int launch_attn(int hd, int H, int KV, int max_ctx, int G, const float *q, const float *kx, const float *vx,
                 const float *q_norm, const float *k_norm, const float *cs, const float *sn, float *kc, float *vc,
                 float *scores, float *smax, float *att, const int32_t *st, float eps, hipStream_t s) {
-    const bool spl = max_ctx <= ATT_LDS_POS;
     const int has_qn = q_norm != nullptr, has_kn = k_norm != nullptr;
     if (!q_norm) q_norm = q;   /* read (clamped) and dropped */
     if (!k_norm) k_norm = q;
-    const size_t dyn = spl ? (size_t)(max_ctx + ATT_PU) * 4 : 0;   /* the last group reads whole */
-    const unsigned nslice = (unsigned)((max_ctx + NT - 1) / NT);
-    /* contexts of at most ATT_SPLIT_MIN positions score inside the fused launch (one or two
-     * passes); longer ones in the split launch, a group per (head, NT positions) */
-    const bool split = max_ctx > ATT_SPLIT_MIN;
+    const size_t dyn = (size_t)att_lds(hd, H / KV).total * 4;
+    const int nwc = (hd + 63) / 64, qpg = nwc <= 4 ? 4 / nwc : 1;
+    const unsigned npv = (unsigned)((H + qpg - 1) / qpg);
 #define TLM_ATT(W)                                                                                                \
     case W:                                                                                                       \
-        if (!split)                                                                                               \
-            hipLaunchKernelGGL((k_attn_fused<W, true, false>), dim3(H), dim3(NT), dyn, s, q, kx, vx, q_norm,      \
-                               k_norm, has_qn, has_kn, cs, sn, kc, vc, scores, smax, att, H, KV, max_ctx, st,     \
-                               eps);                                                                              \
-        else {                                                                                                    \
-            hipLaunchKernelGGL((k_attn_scores<W>), dim3(H, nslice), dim3(NT), 0, s, q, kx, q_norm, k_norm,       \
-                               has_qn, has_kn, cs, sn, kc, scores, smax, H, KV, max_ctx, st, eps);                \
-            if (spl)                                                                                              \
-                hipLaunchKernelGGL((k_attn_fused<W, true, true>), dim3(H), dim3(NT), dyn, s, q, kx, vx, q_norm,   \
-                                   k_norm, has_qn, has_kn, cs, sn, kc, vc, scores, smax, att, H, KV, max_ctx, st, \
-                                   eps);                                                                          \
-            else                                                                                                  \
-                hipLaunchKernelGGL((k_attn_fused<W, false, true>), dim3(H), dim3(NT), 0, s, q, kx, vx, q_norm,   \
-                                   k_norm, has_qn, has_kn, cs, sn, kc, vc, scores, smax, att, H, KV, max_ctx, st, \
-                                   eps);                                                                          \
-        }                                                                                                         \
+        hipLaunchKernelGGL((k_attn_scores<W>), dim3(KV, G), dim3(NT), dyn, s, q, kx, vx, q_norm, k_norm, has_qn, \
+                           has_kn, cs, sn, kc, vc, scores, smax, H, KV, max_ctx, G, st, eps);                    \
+        hipLaunchKernelGGL((k_attn_pv<W>), dim3(npv), dim3(NT), 0, s, scores, smax, vc, att, H, KV, max_ctx, G,  \
+                           st);                                                                                   \
         break;
     switch (hd) {
         TLM_ATT(32) TLM_ATT(64) TLM_ATT(96) TLM_ATT(128) TLM_ATT(160) TLM_ATT(192) TLM_ATT(224) TLM_ATT(256)
@@ -591,7 +484,9 @@ struct tlm_hip_model {
     size_t embd_row = 0;
     const float *out_norm = nullptr;
     DevMat lm_head;
-    float *kc = nullptr, *vc = nullptr, *cs = nullptr, *sn = nullptr, *scores = nullptr, *smax = nullptr;
+    float *kc = nullptr, *vc = nullptr, *cs = nullptr, *sn = nullptr;
+    int att_g = 1;                                     /* attention slices per key head */
+    float *scores = nullptr, *smax = nullptr;          /* [H][max_ctx] scores; [H][att_g] slice maxima */
     float *h = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
     float *logits = nullptr;
     uint8_t *moe_ws = nullptr;
@@ -743,6 +638,10 @@ int prepare(tlm_hip_model *M, const tlm_hip_model_opts *o) {
     if (g.max_ctx > 0 && max_ctx > (int)g.max_ctx) max_ctx = (int)g.max_ctx;
     M->max_ctx = max_ctx;
     M->graph_failed[0] = M->graph_failed[1] = o && o->eager;
+    if (!att_supported((int)g.head_dim, (int)g.n_heads, (int)g.n_kv_heads))
+        return tlmh_seterr(TLM_HIP_EUNSUP, "model: %u query heads per key head of width %u exceed the attention "
+                           "kernel's share", g.n_heads / g.n_kv_heads, g.head_dim);
+    M->att_g = att_groups(max_ctx, (int)g.n_kv_heads, o ? o->attn_slices : 0);
     const int64_t hd = g.head_dim;
 
     int rc = tlmh_check(hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking), "model: stream");
@@ -783,8 +682,8 @@ int finish(tlm_hip_model *M) {
     const size_t per = (size_t)g.n_layers * KV * (size_t)max_ctx * hd;
     M->kc = (float *)M->dalloc(per * 4);
     M->vc = (float *)M->dalloc(per * 4);
-    M->scores = (float *)M->dalloc(((size_t)H * max_ctx + 16) * 4);   /* attention reads a row in groups of 16 */
-    M->smax = (float *)M->dalloc((size_t)H * ((max_ctx + NT - 1) / NT) * 4);   /* per (head, slice) score maxima */
+    M->scores = (float *)M->dalloc((size_t)H * max_ctx * 4);
+    M->smax = (float *)M->dalloc((size_t)H * M->att_g * 4);
     M->h = (float *)M->dalloc((size_t)D * 4);
     M->q = (float *)M->dalloc((size_t)H * hd * 4);
     M->kx = (float *)M->dalloc((size_t)KV * hd * 4);
@@ -796,8 +695,8 @@ int finish(tlm_hip_model *M) {
     M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
     M->st = (int32_t *)M->dalloc(16);
     M->seq = (int32_t *)M->dalloc(((size_t)max_ctx + 1) * 4);
-    M->ids = (int32_t *)M->dalloc(32 * 4);
-    M->w = (float *)M->dalloc(32 * 4);
+    M->ids = (int32_t *)M->dalloc((size_t)g.n_layers * 32 * 4);   /* the step's routing, per layer */
+    M->w = (float *)M->dalloc((size_t)g.n_layers * 32 * 4);
     M->keys = (unsigned long long *)M->dalloc(((size_t)g.vocab + TILE_ROWS - 1) / TILE_ROWS * 8);
     for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->smax, (void *)M->h,
                     (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
@@ -975,8 +874,9 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
         }
         if (rc) break;
         const size_t lbase = (size_t)l * KV * M->max_ctx * hd;
-        rc = launch_attn(hd, H, KV, M->max_ctx, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm, M->cs, M->sn,
-                         M->kc + lbase, M->vc + lbase, M->scores, M->smax, M->att, (const int32_t *)M->st, g.norm_eps, s);
+        rc = launch_attn(hd, H, KV, M->max_ctx, M->att_g, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm, M->cs, M->sn,
+                         M->kc + lbase, M->vc + lbase, M->scores, M->smax, M->att,
+                         (const int32_t *)M->st, g.norm_eps, s);
         /* o: every group quantises the attention output itself */
         const MvNorm ao{M->att, nullptr, 0.0f};
         const void *Wo = Ly.o.p;
@@ -984,7 +884,7 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
         float *const Yo = M->h;
         if (!rc) rc = launch_mv_segs(Ly.o.dt, (int64_t)H * hd, &Wo, &Ro, &Yo, 1, 1, nullptr, s, &ao);
         /* moe(), tlm_model.c:940-1055 */
-        if (!rc) rc = launch_moe_layer(&Ly.moe, M->h, M->ids, M->w, M->moe_ws, s);
+        if (!rc) rc = launch_moe_layer(&Ly.moe, M->h, M->ids + (size_t)l * 32, M->w + (size_t)l * 32, M->moe_ws, s);
     }
     if (rc) return rc;
     const int nkeys = (int)((g.vocab + TILE_ROWS - 1) / TILE_ROWS);
@@ -1251,6 +1151,23 @@ void tlm_hip_model_close(tlm_hip_model *M) { delete M; }
 const tlm_hip_model_geom *tlm_hip_model_geom_of(const tlm_hip_model *M) { return M ? &M->g : nullptr; }
 int tlm_hip_model_kv_len(const tlm_hip_model *M) { return M ? M->kv_len : 0; }
 int tlm_hip_model_kv_capacity(const tlm_hip_model *M) { return M ? M->max_ctx : 0; }
+
+int tlm_hip_model_routes(tlm_hip_model *M, int32_t *ids, float *w) {
+    if (!M || !ids || !w) return tlmh_seterr(TLM_HIP_EINVAL, "model routes: NULL argument");
+    const int L = (int)M->g.n_layers, k = (int)M->g.top_k;
+    std::vector<int32_t> di((size_t)L * 32);
+    std::vector<float> dw((size_t)L * 32);
+    int rc = tlmh_check(hipStreamSynchronize(M->stream), "model routes");
+    if (!rc) rc = tlmh_check(hipMemcpy(di.data(), M->ids, di.size() * 4, hipMemcpyDeviceToHost), "model routes");
+    if (!rc) rc = tlmh_check(hipMemcpy(dw.data(), M->w, dw.size() * 4, hipMemcpyDeviceToHost), "model routes");
+    if (rc) return rc;
+    for (int l = 0; l < L; l++)
+        for (int r = 0; r < k; r++) {
+            ids[(size_t)l * k + r] = di[(size_t)l * 32 + r];
+            w[(size_t)l * k + r] = dw[(size_t)l * 32 + r];
+        }
+    return TLM_HIP_OK;
+}
 void tlm_hip_model_reset(tlm_hip_model *M) {
     if (!M) return;
     M->kv_len = 0;

@@ -179,7 +179,7 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
     const float bias = (sig && in && d.router_bias) ? ((const GAS float *)d.router_bias)[t] : 0.0f;
     float p;
     if (sig) {   /* sigmoid score = weight; bias for selection only */
-        p = 1.0f / (1.0f + exp_rn(-l));
+        p = 1.0f / (1.0f + expf_ref(-l));
     } else {     /* softmax over the routable experts */
         float m = wave_max_f32((unmasked && l > -INFINITY) ? l : -INFINITY);
         if (lane == 0) R->redf[wave] = m;
@@ -188,7 +188,7 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
 #pragma unroll
         for (int q = 1; q < NWAVE; q++) mx = R->redf[q] > mx ? R->redf[q] : mx;
         const bool off = !unmasked || l != l || mx == -INFINITY;
-        const float x = off ? 0.0f : exp_rn(l - mx);
+        const float x = off ? 0.0f : expf_ref(l - mx);
         const double s = wave_sum_f64((double)x);
         if (lane == 0) R->red[wave] = s;
         __syncthreads();
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
                 float acc = 0.0f;
                 if (lane == 0)
                     for (int64_t i = 0; i < D; i++) acc += gi[i] * xb[i];
-                g = 1.0f / (1.0f + exp_rn(-acc));
+                g = 1.0f / (1.0f + expf_ref(-acc));
             }
             if (lane == 0) *(GAS float *)ws_sgate(ws, L) = g;
         }
@@ -558,7 +558,7 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
     if (threadIdx.x < 64) {   /* wave 0: up value from lane i + 16 */
         const float up = __shfl_down(acc, TILE_ROWS, 64);
         if (threadIdx.x < TILE_ROWS)
-            hh[t * TILE_ROWS + threadIdx.x] = acc / (1.0f + exp_rn(-acc)) * up;   /* silu(g) * u (tlm_model.c:171, 927) */
+            hh[t * TILE_ROWS + threadIdx.x] = acc / (1.0f + expf_ref(-acc)) * up;   /* silu(g) * u (tlm_model.c:171, 927) */
     }
 }
 
@@ -1108,7 +1108,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             const int i = 4 * q + (threadIdx.x >> 6);
             if (i < n) {
                 const float g = gu[i * 64 + r2], u = gu[(32 + i) * 64 + r2];
-                hb[(size_t)(s0 + i) * rows + orow] = g / (1.0f + exp_rn(-g)) * u;
+                hb[(size_t)(s0 + i) * rows + orow] = g / (1.0f + expf_ref(-g)) * u;
             }
         }
     }

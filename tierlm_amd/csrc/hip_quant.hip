@@ -69,6 +69,21 @@ __global__ void k_copy_f32(const float *__restrict__ x, int64_t n, float *__rest
 
 }  // namespace
 
+/* y = e^x elementwise, the softmax / sigmoid / SiLU exponential (expf_ref) */
+__global__ __launch_bounds__(256) void k_expf(const float *__restrict__ x, float *__restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] = expf_ref(x[i]);
+}
+
+int launch_expf(const float *x, float *y, int64_t n, hipStream_t s) {
+    if (n <= 0) return TLM_HIP_OK;
+    if (!x || !y) return tlmh_seterr(TLM_HIP_EINVAL, "expf: NULL pointer");
+    const int64_t ng = (n + 255) / 256;
+    if (ng > 0x7FFFFFFF) return tlmh_seterr(TLM_HIP_EINVAL, "expf: %lld values exceed one launch", (long long)n);
+    hipLaunchKernelGGL(k_expf, dim3((unsigned)ng), dim3(256), 0, s, x, y, n);
+    return tlmh_check(hipGetLastError(), "expf launch");
+}
+
 int launch_quantize_act(int kind, const float *x, int64_t n, void *dst, hipStream_t s) {
     if (n <= 0) return TLM_HIP_OK;   /* src/lib/tlm_quant.c:700 */
     if (!x || !dst) return tlmh_seterr(TLM_HIP_EINVAL, "quantize_act: NULL pointer");

@@ -6,8 +6,9 @@
  *
  * Checked: the device activation quantisers (bytes), the plain-layout matvec
  * and the packed-layout matvec (bits of every row) for F32, Q8_0, Q4_K, Q5_K,
- * Q6_K and Q8_K.  Returns the number of failing kernels; bit dt of *mask is
- * set for every dtype whose kernels failed. */
+ * Q6_K and Q8_K, and the exponential against this host's libm expf.  Returns
+ * the number of failing kernels; bit dt of *mask is set for every dtype whose
+ * kernels failed, bit 30 for the exponential. */
 #include "tlm_hip_internal.h"
 
 #include <math.h>
@@ -260,6 +261,30 @@ int tlmh_selftest(int *failed_mask) {
         if (!ok) {
             fails++;
             mask |= 1 << dt;
+        }
+    }
+    /* the exponential against this host's libm expf (what the reference
+     * calls): float bit patterns strided over the whole range, the overflow and
+     * underflow edges and two inputs whose result needs the fused shift */
+    {
+        const int NE = 4096;
+        std::vector<float> ex(NE), ey(NE), eg(NE);
+        for (int i = 0; i < NE - 6; i++) {
+            const uint32_t u = (uint32_t)i * 1048573u;
+            memcpy(&ex[i], &u, 4);
+        }
+        const float edge[6] = {0x1.62e42ep6f, 0x1.62e430p6f, -0x1.9fe368p6f, -0x1.9fe366p6f, 0x1.04845ep+5f,
+                               -0x1.f8cbb2p+5f};
+        for (int i = 0; i < 6; i++) ex[NE - 6 + i] = edge[i];
+        for (int i = 0; i < NE; i++) ey[i] = expf(ex[i]);
+        float *dx = (float *)(dev + o_w), *dy = (float *)(dev + o_p);
+        bool ok = hipMemcpy(dx, ex.data(), NE * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                  launch_expf(dx, dy, NE, nullptr) == TLM_HIP_OK &&
+                  hipMemcpy(eg.data(), dy, NE * 4, hipMemcpyDeviceToHost) == hipSuccess;
+        for (int i = 0; ok && i < NE; i++) ok = same(ey[i], eg[i]) || (ey[i] != ey[i] && eg[i] != eg[i]);
+        if (!ok) {
+            fails++;
+            mask |= 1 << 30;
         }
     }
     (void)hipDeviceSynchronize();

@@ -113,6 +113,10 @@ int tlm_hip_quantize_act(int kind, const float *x, int64_t n, void *dst, void *s
     return launch_quantize_act(kind, x, n, dst, (hipStream_t)stream);
 }
 
+int tlm_hip_expf(const float *x, float *y, int64_t n, void *stream) {
+    return launch_expf(x, y, n, (hipStream_t)stream);
+}
+
 int tlm_hip_matvec_rows(int dt, const void *W, size_t row_bytes, const void *act, float *y, int64_t n, int64_t r0,
                         int64_t r1, void *stream) {
     return launch_matvec_plain(dt, W, row_bytes, act, y, n, r0, r1, (hipStream_t)stream);

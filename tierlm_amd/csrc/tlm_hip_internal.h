@@ -64,13 +64,44 @@ __device__ __forceinline__ int rne_clamp(float v, int lo, int hi) {
     return (int)((t + magic) - magic);
 }
 
-/* e^x for the routing softmax / sigmoid and SiLU: exp in double, rounded
- * once to float - the correctly rounded expf except where the true value lies
- * within ~2^-52 relative of a float rounding midpoint.  The reference calls
- * libm's expf, itself within 0.502 ulp, so the two agree except in rare
- * near-midpoint cases (a float-only device exp is within about 1 ulp and
- * disagrees far more often). */
-__device__ __forceinline__ float exp_rn(float x) { return (float)exp((double)x); }
+/* e^x as the reference computes it: libm's expf (src/lib/tlm_model.c:171-172,
+ * 705, 806, 823), which on glibc 2.27+ is the published ARM optimized-routines
+ * algorithm (Szabolcs Nagy, 2017): x * 32 / ln 2 = k + r with k rounded to the
+ * nearest integer through the 1.5 * 2^52 shift, 2^(k/32) from a 32-entry table
+ * of 2^(i/32) with the exponent of i/32 taken out, 2^(r/32) from a cubic, all
+ * in double, rounded once to float.  The x86-64 FMA build fuses x * 32/ln 2 into
+ * both the shift and r; the fused form is the one that reproduces that libm
+ * bit for bit (every one of the 2^32 inputs, checked against glibc 2.35; the
+ * polynomial's own fusions do not change any result).  Not correctly rounded:
+ * about 8 in 10^5 results differ from exp in double rounded to float. */
+#define TLM_EXP2_TAB                                                                                     \
+    {0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,          \
+     0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,          \
+     0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,          \
+     0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,          \
+     0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,          \
+     0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,          \
+     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,          \
+     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}
+__device__ static const uint64_t tlm_exp2_tab[32] = TLM_EXP2_TAB;
+__device__ __forceinline__ float expf_ref(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return __builtin_inff();       /* overflow */
+    if (x < -0x1.9fe368p6f) return 0.0f;                  /* underflow (and -inf) */
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0, Shift = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / 32768.0, C1 = 0x1.ebfce50fac4f3p-3 / 1024.0,
+                 C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __builtin_fma(InvLn2N, xd, Shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= Shift;
+    const double r = __builtin_fma(InvLn2N, xd, -kd);
+    const double s = __longlong_as_double((long long)(tlm_exp2_tab[ki % 32] + (ki << 47)));
+    const double z = __builtin_fma(C0, r, C1), r2 = r * r;
+    double y = __builtin_fma(C2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return (float)(y * s);
+}
 
 /* Address-space qualified pointers.  Pointers that travel through structs,
  * tables or lambdas lose their address space and compile to flat_* accesses,
@@ -163,6 +194,7 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 }
 /* ---- launchers (defined in the .hip files) ------------------------------ */
 int launch_quantize_act(int kind, const float *x, int64_t n, void *dst, hipStream_t s);
+int launch_expf(const float *x, float *y, int64_t n, hipStream_t s);
 int launch_matvec_plain(int dt, const void *W, size_t row_bytes, const void *act, float *y,
                         int64_t n, int64_t r0, int64_t r1, hipStream_t s);
 int launch_nan_fill(float *y, int64_t count, hipStream_t s);

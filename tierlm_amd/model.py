@@ -19,7 +19,7 @@ from ._lib import check, lib
 
 class ModelOpts(C.Structure):
     """tlm_hip_model_opts"""
-    _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32)]
+    _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32)]
 
 
 # Qwen3-30B-A3B: 48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128
@@ -30,14 +30,14 @@ QWEN3_30B_A3B = dict(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_d
 
 
 class Model:
-    def __init__(self, manifest_path, max_ctx=0, eager=False):
-        self.opts = ModelOpts(max_ctx, int(eager))
+    def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0):
+        self.opts = ModelOpts(max_ctx, int(eager), attn_slices)
         h = C.c_void_p()
         check(lib.tlm_hip_model_open(str(manifest_path).encode(), C.byref(self.opts), C.byref(h)))
         self._bind(h)
 
     @classmethod
-    def synth(cls, geom, expert_dt=14, dense_dt=8, qk_norm=True, seed=1, max_ctx=0, eager=False):
+    def synth(cls, geom, expert_dt=14, dense_dt=8, qk_norm=True, seed=1, max_ctx=0, eager=False, attn_slices=0):
         """tlm_hip_model_synth: a random-init model of geometry geom (a dict of
         tlm_hip_model_geom fields) built in HBM."""
         from ._lib import ModelGeom, ModelSynthOpts
@@ -47,7 +47,7 @@ class Model:
             setattr(g, k, v)
         so = ModelSynthOpts(expert_dt, dense_dt, int(qk_norm), 0, seed)
         self = cls.__new__(cls)
-        self.opts = ModelOpts(max_ctx, int(eager))
+        self.opts = ModelOpts(max_ctx, int(eager), attn_slices)
         h = C.c_void_p()
         check(lib.tlm_hip_model_synth(C.byref(g), C.byref(so), C.byref(self.opts), C.byref(h)))
         self._bind(h)
@@ -73,6 +73,20 @@ class Model:
 
     def kv_len(self):
         return lib.tlm_hip_model_kv_len(self.h)
+
+    def kv_capacity(self):
+        """The context capacity in effect: the request, capped at the store's
+        max_position_embeddings as tlm_kv_new caps it (src/lib/tlm_model.c:646-650)."""
+        return lib.tlm_hip_model_kv_capacity(self.h)
+
+    def routes(self):
+        """The last step's routing: (ids, weights), each [n_layers, top_k] in
+        rank order (what the reference's routing hook receives)."""
+        L, k = self.geom.n_layers, self.geom.top_k
+        ids = np.empty((L, k), np.int32)
+        w = np.empty((L, k), np.float32)
+        check(lib.tlm_hip_model_routes(self.h, ids.ctypes.data, w.ctypes.data))
+        return ids, w
 
     def step(self, token, logits=True):
         """One token; returns (logits as float32 [vocab] or None, greedy next token)."""
