@@ -162,6 +162,19 @@ size_t tlm_hip_moe_workspace_bytes(const tlm_hip_moe_desc *d);
  * on different streams need different workspaces. */
 int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w,
                       void *workspace, void *stream);
+/* No counterpart in the reference: tlm_hip_moe_layer for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The workspace is a static device array of
+ * TLM_HIP_MOE_NOALLOC_MAX_BYTES per GPU (the library's, held until the process
+ * ends; its address is taken at tlm_hip_init, which must have run on the
+ * current device).  Calls no allocator.  Blocks whose
+ * tlm_hip_moe_workspace_bytes exceeds the limit get TLM_HIP_ERANGE and no
+ * launch.  Every call on one GPU uses that GPU's one array: calls that overlap
+ * on one GPU (other streams, other threads) race, so serialise them.  No part
+ * of the array needs to start at zero (each call writes what it reads). */
+#define TLM_HIP_MOE_NOALLOC_MAX_BYTES (1u << 20)
+int tlm_hip_moe_layer_noalloc(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w, void *stream);
+
 /* The same block as its launches, one per call, for callers that interleave
  * other work or time each launch (the reference's moe() is likewise route,
  * then the gate/up job, then the down job + combine, src/lib/tlm_model.c:972,

@@ -132,6 +132,7 @@ _SIGS = {
     "tlm_hip_moe_prefill": (i32, [C.POINTER(MoeDesc), vp, i64, vp, vp, vp, vp]),
     "tlm_hip_moe_workspace_bytes": (sz, [C.POINTER(MoeDesc)]),
     "tlm_hip_moe_layer": (i32, [C.POINTER(MoeDesc), vp, vp, vp, vp, vp]),
+    "tlm_hip_moe_layer_noalloc": (i32, [C.POINTER(MoeDesc), vp, vp, vp, vp]),
     "tlm_hip_moe_layer_phase": (i32, [C.POINTER(MoeDesc), i32, vp, vp, vp, vp, vp]),
     "tlm_kern_hip_fill": (i32, [C.POINTER(QuantKernels)]),
     "tlm_hip_store_open": (i32, [C.POINTER(ExpertSrc), i32, C.POINTER(StoreOpts), C.POINTER(vp)]),
@@ -181,6 +182,11 @@ for _name, (_res, _args) in _SIGS.items():
     _f.argtypes = _args
 
 EXPORTS = tuple(_SIGS)
+
+
+# return codes (include/tlm_hip.h; the reference's TLM_E* values)
+TLM_HIP_OK, TLM_HIP_EIO, TLM_HIP_ENOMEM, TLM_HIP_EINVAL = 0, -1, -2, -3
+TLM_HIP_EFORMAT, TLM_HIP_ERANGE, TLM_HIP_ENOTFOUND, TLM_HIP_EUNSUP, TLM_HIP_EBUSY = -4, -5, -6, -7, -8
 
 
 class HipError(RuntimeError):

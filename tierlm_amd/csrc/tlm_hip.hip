@@ -44,6 +44,16 @@ static hipStream_t g_stage_stream = nullptr;
 
 int tlmh_current_device(void) { return g_device; }
 
+/* ---- the workspace of tlm_hip_moe_layer_noalloc ---------------------------
+ * A file-scope device array: every GPU the library is initialised on holds its
+ * own copy, TLM_HIP_MOE_NOALLOC_MAX_BYTES long, until the process ends.  In
+ * host code the array's name is a host-side stand-in, not a device address:
+ * its address on each device comes from hipGetSymbolAddress in tlm_hip_init
+ * (that device current) and only that address ever reaches a kernel. */
+static __device__ __align__(256) uint8_t scratch[TLM_HIP_MOE_NOALLOC_MAX_BYTES];
+constexpr int SCRATCH_DEVICES = 64;
+static void *g_scratch[SCRATCH_DEVICES];   /* per device; set once, under g_mu */
+
 extern "C" {
 
 const char *tlm_hip_errmsg(void) { return g_err; }
@@ -61,6 +71,11 @@ int tlm_hip_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return tlmh_seterr(TLM_HIP_EUNSUP, "tlm_hip_init: device %d is %s, this library is built for gfx950",
                            device, prop.gcnArchName);
+    if (device < SCRATCH_DEVICES && !g_scratch[device]) {
+        void *p = nullptr;
+        HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch[device] = p;
+    }
     if (g_stage) { (void)hipFree(g_stage); g_stage = nullptr; }
     if (g_stage_stream) { (void)hipStreamDestroy(g_stage_stream); g_stage_stream = nullptr; }
     g_stage_bytes = (size_t)64 << 20;
@@ -154,6 +169,20 @@ size_t tlm_hip_moe_workspace_bytes(const tlm_hip_moe_desc *d) { return moe_works
 
 int tlm_hip_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w, void *workspace, void *stream) {
     return launch_moe_layer(d, h, ids, w, workspace, (hipStream_t)stream);
+}
+
+int tlm_hip_moe_layer_noalloc(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w, void *stream) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_DEVICES || !g_scratch[dev])
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_noalloc: tlm_hip_init has not run on the current device");
+    if (!d) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_noalloc: NULL descriptor");
+    const size_t need = moe_workspace_bytes(d);
+    if (need > TLM_HIP_MOE_NOALLOC_MAX_BYTES)
+        return tlmh_seterr(TLM_HIP_ERANGE,
+                           "moe_layer_noalloc: this block needs %zu bytes of workspace, more than the %u-byte "
+                           "static scratch; use tlm_hip_moe_layer with a workspace",
+                           need, (unsigned)TLM_HIP_MOE_NOALLOC_MAX_BYTES);
+    return launch_moe_layer(d, h, ids, w, g_scratch[dev], (hipStream_t)stream);
 }
 
 int tlm_hip_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, float *w, void *workspace,
