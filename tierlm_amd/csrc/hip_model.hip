@@ -66,9 +66,12 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
  * double, inv = 1 / sum, p_t = e_t * inv (probabilities in LDS) - then the
  * P.V sums: one lane per output element runs the reference's chain
  * out += p_t * v_t[i] over ascending t, one wave per 64 elements, so that
- * each SIMD holds one chain wave.  V streams into registers two blocks of
- * ATT_PD positions ahead (a lane reads column i of consecutive rows; the
- * wave's lanes cover 256 contiguous bytes of a row).
+ * each SIMD holds one chain wave.  V streams into registers three blocks of
+ * ATT_PD positions ahead: a wave can have at most 63 loads outstanding, so a
+ * load must bring each lane several positions - the value cache is kept in
+ * tiles of 4 positions, element-major inside (V[t][i] at
+ * ((t / 4) * HD + i) * 4 + t % 4), where one 16-byte lane load is positions
+ * 4j..4j+3 of element i and a wave's load is 1 KB contiguous.
  *
  * Numerics: the scores, maxima, products and chains are the reference's
  * operations in its order; the double sum of the softmax terms is a tree
@@ -76,15 +79,23 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
  * lies within a double ulp or so of a rounding boundary); e^x is libm's expf
  * (expf_ref).
  *
- * Cache layout (per layer and key head, the reference's own): K[t][i] and
- * V[t][i] at t * HD + i.  Slices: G per key head (fixed for the captured
+ * Cache layout (per layer and key head): K[t][i] at t * HD + i (the
+ * reference's), values in the 4-position tiles above (att_vstride floats per
+ * key head).  Slices: G per key head (fixed for the captured
  * graph), att_slice_len(T, G) positions at context T; groups past the
  * context return at once. */
 constexpr int ATT_CH = 32;       /* positions per LDS chunk of the scores */
 constexpr int ATT_LMIN = 32;     /* shortest slice */
 constexpr int ATT_QMAX = 4096;   /* query values per key head (query heads per key head x HD) */
 constexpr int ATT_GMAX = 128;    /* slices per key head */
-constexpr int ATT_PD = 32;       /* V positions per register block of a chain */
+constexpr int ATT_PD = 64;       /* V positions per register block of a chain (three in flight) */
+
+/* floats of value cache per key head: whole 4-position tiles */
+__host__ __device__ inline size_t att_vstride(int max_ctx, int hd) { return (size_t)((max_ctx + 3) & ~3) * hd; }
+/* V[t][i] in the tiled layout */
+__host__ __device__ inline size_t att_vidx(int t, int i, int hd) {
+    return ((size_t)(t >> 2) * hd + i) * 4 + (t & 3);
+}
 
 __host__ __device__ inline int att_slice_len(int T, int G) {
     int L = (T + G - 1) / G;
@@ -146,7 +157,7 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
     const int tn = min(L, T - t0), kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const AttLds lo = att_lds(HD, R);
     float *s_q = s_dyn + lo.q, *s_kn = s_dyn + lo.kn, *s_vn = s_dyn + lo.vn, *s_k = s_dyn + lo.k;
-    float *K = kc + (size_t)kvh * max_ctx * HD, *V = vc + (size_t)kvh * max_ctx * HD;
+    float *K = kc + (size_t)kvh * max_ctx * HD, *V = vc + (size_t)kvh * att_vstride(max_ctx, HD);
 
     /* every load at entry, in the order of use: the query heads (consecutive
      * heads h = kvh * R + j), the new key and value, norm weights and RoPE
@@ -180,6 +191,20 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
         }
     };
     kload(0);
+    /* the value rows of this slice and of its sibling (slice ^ 1) towards this
+     * XCD's L2 for the P.V launch: direct-to-LDS loads into one 1 KB sink, never
+     * read, so they hold no registers (att_pv_group puts a key head's P.V groups
+     * on the XCDs its slices run on; block b runs on XCD b mod 8 and slice
+     * parity alternates the two) */
+    __shared__ __align__(16) float s_sink[256];
+    for (int sl = (int)blockIdx.y & ~1; sl <= ((int)blockIdx.y | 1); sl++) {
+        const int a0 = sl * L;   /* a multiple of 16: whole tiles, one contiguous run */
+        if (a0 >= T) break;
+        const int nc = (min(L, T - a0) + 3) / 4 * HD;   /* 16-byte pieces: a tile's element i each */
+        for (int c = tid; c < nc; c += NT)
+            __builtin_amdgcn_global_load_lds((const void *)(V + att_vidx(a0, 0, HD) + 4 * (size_t)c),
+                                             (__attribute__((address_space(3))) void *)s_sink, 16, 0, 0);
+    }
 
 #pragma unroll
     for (int k = 0; k < QF; k++)
@@ -274,8 +299,13 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
     if (t0 + tn == T)   /* the KV append (tlm_model.c:748-752), after the last read */
         for (int i4 = tid; i4 < H4; i4 += NT) {
             ((f32x4 *)K)[(size_t)pos * H4 + i4] = ((const f32x4 *)s_kn)[i4];
-            ((f32x4 *)V)[(size_t)pos * H4 + i4] = ((const f32x4 *)s_vn)[i4];
+            const f32x4 v4 = ((const f32x4 *)s_vn)[i4];
+            V[att_vidx(pos, 4 * i4, HD)] = v4.x;
+            V[att_vidx(pos, 4 * i4 + 1, HD)] = v4.y;
+            V[att_vidx(pos, 4 * i4 + 2, HD)] = v4.z;
+            V[att_vidx(pos, 4 * i4 + 3, HD)] = v4.w;
         }
+    __builtin_amdgcn_s_waitcnt(0);   /* the prefetches land before the group's LDS is released */
 }
 
 template <int HD>
@@ -285,20 +315,30 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     constexpr int NWC = (HD + 63) / 64;          /* chain waves per query head */
     constexpr int QPG = NWC <= 4 ? 4 / NWC : 1;  /* query heads per group */
     constexpr int TPH = NT / QPG;                /* threads per head in the softmax */
-    constexpr int PSEG = 8192 / QPG;             /* probabilities per head in LDS */
+    constexpr int PSEG = 8192 / QPG / (3 * ATT_PD) * (3 * ATT_PD);   /* probabilities per head in LDS */
     constexpr int PB = 8;                        /* score loads per thread per round */
     constexpr int GM = ATT_GMAX / 64;            /* slice maxima per lane */
     __shared__ __align__(16) float s_p[QPG][PSEG + ATT_PD];
     __shared__ double s_sum[NT / 64];
     const int pos = st[0], T = pos + 1, L = att_slice_len(T, G), ns = (T + L - 1) / L;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h0 = (int)blockIdx.x * QPG;
+    const int R = H / KV, gpk = (R + QPG - 1) / QPG;   /* groups per key head */
+    /* block b: key head b mod KV (so b runs on an XCD of that key head's
+     * slices), its (b / KV)-th run of QPG query heads */
+    const int kvg = (int)blockIdx.x % KV, jg = (int)blockIdx.x / KV;
+    if (jg >= gpk) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h0 = kvg * R + jg * QPG, hend = kvg * R + R;
     /* softmax role: head jj (a wave never straddles two), positions tt + TPH k */
-    const int jj = tid / TPH, tt = tid % TPH, hs = min(h0 + jj, H - 1);
+    const int jj = tid / TPH, tt = tid % TPH, hs = min(h0 + jj, hend - 1);
     /* chain role: head jc, element ic */
     const int jc = wave / NWC, hc = h0 + jc, ic = 64 * (wave % NWC) + lane;
-    const bool chain = jc < QPG && hc < H;
+    const bool chain = jc < QPG && hc < hend;
     const float *S = scores + (size_t)hs * max_ctx;
-    const float *vcol = vc + (size_t)(min(hc, H - 1) / (H / KV)) * max_ctx * HD + min(ic, HD - 1);
+    /* the chain lane's element: 16 bytes at lane_off of each tile (4
+     * positions); the tile's address is uniform, so a load needs no address
+     * registers of its own */
+    const char *vbase = (const char *)(vc + (size_t)kvg * att_vstride(max_ctx, HD));
+    const uint32_t lane_off = (uint32_t)min(ic, HD - 1) * 16u;
+    const int lastq = (T - 1) >> 2;
 
     /* entry loads: the head's slice maxima, the first scores, the chain's first V block */
     float mm[GM];
@@ -307,12 +347,19 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     float sv[PB];
 #pragma unroll
     for (int k = 0; k < PB; k++) sv[k] = S[min(tt + TPH * k, T - 1)];
-    float va[ATT_PD], vb[ATT_PD];
-    auto vld = [&](int t0, float (&r)[ATT_PD]) {
+    constexpr int PQ = ATT_PD / 4;   /* 16-byte loads per block */
+    f32x4 va[PQ], vb[PQ], vc3[PQ];
+    auto vld = [&](int t0, f32x4 (&r)[PQ]) {   /* t0 a multiple of 4; tiles clamped to the context */
 #pragma unroll
-        for (int u = 0; u < ATT_PD; u++) r[u] = vcol[(size_t)min(t0 + u, T - 1) * HD];
+        for (int u = 0; u < PQ; u++) {
+            const int tq = min((t0 >> 2) + u, lastq);
+            r[u] = *(const f32x4 *)(vbase + (size_t)tq * (HD * 16) + lane_off);
+        }
     };
-    if (chain) vld(0, va);
+    if (chain) {
+        vld(0, va);
+        if (ATT_PD < T) vld(ATT_PD, vb);
+    }
 
     float mx = -INFINITY;   /* the reference's maximum: NaN never compares greater */
 #pragma unroll
@@ -327,13 +374,11 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
             for (int k = 0; k < PB; k++) sv[k] = S[min(b0 + tt + TPH * k, T - 1)];
         }
 #pragma unroll
-        for (int k = 0; k < PB; k++) {
+        for (int k = 0; k < PB; k++) {   /* every lane computes; past the context it adds 0, stores nothing */
             const int t = b0 + tt + TPH * k;
-            if (t < T) {
-                const float e = expf_ref(sv[k] - mx);
-                sum += (double)e;
-                if (nseg == 1) prow[t] = e;
-            }
+            const float e = expf_ref(sv[k] - mx);
+            sum += t < T ? (double)e : 0.0;
+            if (nseg == 1 && t < T) prow[t] = e;
         }
     }
     sum = wave_sum_f64(sum);
@@ -356,34 +401,52 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
         __syncthreads();
         if (chain) {
             const float *pp = s_p[jc];
-            auto add = [&](int t0, const float (&r)[ATT_PD]) {
+            /* the chain over ATT_PD positions of r starting at t0; lim < ATT_PD
+             * masks the positions past the segment */
+            auto add_full = [&](int t0, const f32x4 (&r)[PQ]) {
                 const f32x4 *p4 = (const f32x4 *)(pp + (t0 - sb));
-                if (t0 + ATT_PD <= se) {
+                f32x4 p = p4[0];   /* each group's probabilities read one group ahead */
 #pragma unroll
-                    for (int u4 = 0; u4 < ATT_PD / 4; u4++) {
-                        const f32x4 p = p4[u4];
-                        acc += p.x * r[4 * u4];
-                        acc += p.y * r[4 * u4 + 1];
-                        acc += p.z * r[4 * u4 + 2];
-                        acc += p.w * r[4 * u4 + 3];
-                    }
-                } else {
-                    const int lim = se - t0;
+                for (int u = 0; u < PQ; u++) {
+                    const f32x4 pn = p4[u + 1 < PQ ? u + 1 : u];
+                    acc += p.x * r[u].x;
+                    acc += p.y * r[u].y;
+                    acc += p.z * r[u].z;
+                    acc += p.w * r[u].w;
+                    p = pn;
+                }
+            };
+            auto add_part = [&](int t0, const f32x4 (&r)[PQ], int lim) {
+                const f32x4 *p4 = (const f32x4 *)(pp + (t0 - sb));
 #pragma unroll
-                    for (int u = 0; u < ATT_PD; u++) {
-                        const float a = acc + pp[t0 - sb + u] * r[u];
-                        acc = u < lim ? a : acc;
+                for (int u = 0; u < PQ; u++) {
+                    const f32x4 p = p4[u];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const float a = acc + p[k] * r[u][k];
+                        acc = 4 * u + k < lim ? a : acc;
                     }
                 }
             };
-            /* blocks of ATT_PD positions, two in flight; a segment holds an even
-             * number of blocks unless it is the last, so va holds block se on leaving */
-            for (int t0 = sb; t0 < se; t0 += 2 * ATT_PD) {
-                if (t0 + ATT_PD < T) vld(t0 + ATT_PD, vb);
-                add(t0, va);
-                if (t0 + ATT_PD >= se) break;
-                if (t0 + 2 * ATT_PD < T) vld(t0 + 2 * ATT_PD, va);
-                add(t0 + ATT_PD, vb);
+            /* three blocks in flight, loads unconditional (tiles clamped to the
+             * context, so a load past it rereads the last tile); a segment
+             * other than the last holds a multiple of three blocks, so va and vb
+             * hold blocks se and se + ATT_PD on leaving it */
+            int t0 = sb;
+            for (; t0 + 3 * ATT_PD <= se; t0 += 3 * ATT_PD) {
+                vld(t0 + 2 * ATT_PD, vc3);
+                add_full(t0, va);
+                vld(t0 + 3 * ATT_PD, va);
+                add_full(t0 + ATT_PD, vb);
+                vld(t0 + 4 * ATT_PD, vb);
+                add_full(t0 + 2 * ATT_PD, vc3);
+            }
+            const int rem = se - t0;   /* 0 .. 3 ATT_PD - 1 positions left */
+            if (rem > 0) {
+                vld(t0 + 2 * ATT_PD, vc3);
+                add_part(t0, va, rem);
+                if (rem > ATT_PD) add_part(t0 + ATT_PD, vb, rem - ATT_PD);
+                if (rem > 2 * ATT_PD) add_part(t0 + 2 * ATT_PD, vc3, rem - 2 * ATT_PD);
             }
         }
         __syncthreads();   /* before the next segment's probabilities */
@@ -418,7 +481,7 @@ int launch_attn(int hd, int H, int KV, int max_ctx, int G, const float *q, const
     if (!k_norm) k_norm = q;
     const size_t dyn = (size_t)att_lds(hd, H / KV).total * 4;
     const int nwc = (hd + 63) / 64, qpg = nwc <= 4 ? 4 / nwc : 1;
-    const unsigned npv = (unsigned)((H + qpg - 1) / qpg);
+    const unsigned npv = (unsigned)(KV * ((H / KV + qpg - 1) / qpg));
 #define TLM_ATT(W)                                                                                                \
     case W:                                                                                                       \
         hipLaunchKernelGGL((k_attn_scores<W>), dim3(KV, G), dim3(NT), dyn, s, q, kx, vx, q_norm, k_norm, has_qn, \
@@ -681,7 +744,7 @@ int finish(tlm_hip_model *M) {
     int rc;
     const size_t per = (size_t)g.n_layers * KV * (size_t)max_ctx * hd;
     M->kc = (float *)M->dalloc(per * 4);
-    M->vc = (float *)M->dalloc(per * 4);
+    M->vc = (float *)M->dalloc((size_t)g.n_layers * KV * att_vstride(max_ctx, (int)hd) * 4);
     M->scores = (float *)M->dalloc((size_t)H * max_ctx * 4);
     M->smax = (float *)M->dalloc((size_t)H * M->att_g * 4);
     M->h = (float *)M->dalloc((size_t)D * 4);
@@ -873,9 +936,9 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
             }
         }
         if (rc) break;
-        const size_t lbase = (size_t)l * KV * M->max_ctx * hd;
+        const size_t kbase = (size_t)l * KV * M->max_ctx * hd, vbase = (size_t)l * KV * att_vstride(M->max_ctx, hd);
         rc = launch_attn(hd, H, KV, M->max_ctx, M->att_g, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm, M->cs, M->sn,
-                         M->kc + lbase, M->vc + lbase, M->scores, M->smax, M->att,
+                         M->kc + kbase, M->vc + vbase, M->scores, M->smax, M->att,
                          (const int32_t *)M->st, g.norm_eps, s);
         /* o: every group quantises the attention output itself */
         const MvNorm ao{M->att, nullptr, 0.0f};

@@ -85,9 +85,8 @@ __device__ __forceinline__ int rne_clamp(float v, int lo, int hi) {
      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}
 __device__ static const uint64_t tlm_exp2_tab[32] = TLM_EXP2_TAB;
 __device__ __forceinline__ float expf_ref(float x) {
-    if (x != x) return x + x;
-    if (x > 0x1.62e42ep6f) return __builtin_inff();       /* overflow */
-    if (x < -0x1.9fe368p6f) return 0.0f;                  /* underflow (and -inf) */
+    /* branch-free: the main path for every input (out-of-range ones give
+     * values that the selects below replace; the table index stays in range) */
     const double InvLn2N = 0x1.71547652b82fep+0 * 32.0, Shift = 0x1.8p+52;
     const double C0 = 0x1.c6af84b912394p-5 / 32768.0, C1 = 0x1.ebfce50fac4f3p-3 / 1024.0,
                  C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
@@ -100,7 +99,10 @@ __device__ __forceinline__ float expf_ref(float x) {
     const double z = __builtin_fma(C0, r, C1), r2 = r * r;
     double y = __builtin_fma(C2, r, 1.0);
     y = __builtin_fma(z, r2, y);
-    return (float)(y * s);
+    float v = (float)(y * s);
+    v = x > 0x1.62e42ep6f ? __builtin_inff() : v;   /* overflow */
+    v = x < -0x1.9fe368p6f ? 0.0f : v;              /* underflow (and -inf) */
+    return x != x ? x + x : v;
 }
 
 /* Address-space qualified pointers.  Pointers that travel through structs,
