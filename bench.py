@@ -1,25 +1,32 @@
 """Decode benchmark of the quantised-MoE hot path on one MI355X.
 
-Workload (one decode step = one token through one routed MoE block at
-Qwen3-30B-A3B shape): D 2048, 128 experts, top-8 softmax routing with
-renormalisation, expert width 768, Q6_K experts, f32 router, batch 1.  Each
-token has its own seeded N(0,1) residual.  To keep "HBM GB/s" honest the
-tokens cycle through --layers distinct copies of the layer's 128 experts
-(48 copies = the 23.8 GB of Q6_K experts a 48-layer model keeps resident), so
-consecutive tokens never re-read an expert from the 256 MB last-level cache.
+Headline (value): batch-1 greedy decode of the whole Qwen3-30B-A3B-shaped
+model to 2048 positions: 48 layers, hidden 2048, 32 q / 4 kv heads x 128
+(qk-norm, rope theta 1e6), 128 experts top-8 of width 768 (Q6_K, all 23.8 GB
+resident), Q8_0 dense, f32 router, vocabulary 151936; random init built in
+HBM (tlm_hip_model_synth).  A 64-token prompt and one greedy pass fill the
+context to 2047 positions; a "step" is then one decode token (the captured
+step graph: embedding, 48 x (q|k|v, attention scores, softmax + P.V, o,
+router, routed gate/up + SwiGLU, down + combine), lm_head + argmax) at a
+context position taken evenly from 64..2047 (descending; the context is
+rewound to that position first, so the step reads exactly that many cached
+positions).  --steps 1984 is the whole sweep.  Timed with HIP events on the
+model's stream (and the host clock) around exactly K steps.
 
-Timed region: K tokens launched back to back on one stream (HIP graphs of up
-to --graph tokens, replayed), bracketed by synchronisation.  value = tokens/s.
+roofline (the decode step): algorithmic bytes per token = packed weight
+bytes read (48 x (q, k, v, o + router + 8 routed experts) + lm_head =
+2,829,893,632 B) + the f32 KV rows read (K and V, 48 layers x 4 kv heads x T x
+128 x 4 B each, averaged over the timed positions), over the step time,
+against 8 TB/s.  expert_gemv: the routed block alone (one MoE layer per
+token, 48 resident layer copies cycled), per-phase launch times from graphs
+of back-to-back launches (HIP events), as before.
 
-roofline: the dominant kernel is the gate/up launch (phase 2).  Its average
-duration is measured with HIP events around a graph of --roofline-tokens
-back-to-back phase-2 launches (cycling the layer copies), divided by the
-count; algorithmic bytes per launch = top-8 x (gate + up) packed Q6_K bytes =
-8 x 2 x 1,290,240 = 20,643,840 B.
-
-cpu_baseline: the reference's own kernels (oracle/_ref, AVX-512 tier when the
-host has it) running the same block through ref_moe.c on the host cores, on a
-bounded sample of tokens over 128 distinct random-code experts.
+cpu_baseline: the reference's own kernels (oracle/_ref: AVX-512 tier, its
+pool) on the host cores for a bounded sample of the same per-token work -
+one layer's q|k|v and o projections (Q8_0) and routed MoE block at this
+shape, and the lm_head - scaled to tokens/s as 1 / (48 x layer + lm_head)
+(attention's score / softmax / P.V arithmetic and the norms are left out of
+the CPU figure).
 """
 import argparse
 import json
@@ -357,37 +364,81 @@ def c1_bench(reps):
     return out
 
 
-def c3_bench(reps, ctx):
-    """The whole decode step on a random-init model of the full Qwen3-30B-A3B
-    shape (48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128 experts top-8
-    of width 768, vocabulary 151936; Q6_K experts, Q8_0 dense; every expert
-    resident, 23.8 GB), built in HBM by tlm_hip_model_synth: a 64-token
-    prompt, then greedy tokens up to ctx positions.  The reference has no
-    store of this size here, so no CPU figure sits beside it."""
-    from tierlm_amd.model import QWEN3_30B_A3B, Model, time_model
+def c3_geometry_bytes(g):
+    """Packed weight bytes one decode token reads at geometry g (dict), and
+    the KV bytes per cached position."""
+    q80 = lambda rows, n: rows * (n // 32) * 34            # noqa: E731
+    q6k = lambda rows, n: rows * (n // 256) * 210          # noqa: E731
+    D, hd, H, KV, E, k, de = (g[x] for x in ("d_model", "head_dim", "n_heads", "n_kv_heads", "n_experts", "top_k",
+                                             "d_expert"))
+    attn = q80(H * hd, D) + 2 * q80(KV * hd, D) + q80(D, H * hd)
+    router = E * D * 4
+    experts = k * (2 * q6k(de, D) + q6k(D, de))
+    layer = attn + router + experts
+    weights = g["n_layers"] * layer + q80(g["vocab"], D)
+    kv_per_pos = g["n_layers"] * KV * hd * 4 * 2
+    return {"weights_per_token": weights, "attention_per_layer": attn, "router_per_layer": router,
+            "experts_per_layer": experts, "lm_head": q80(g["vocab"], D), "kv_per_position": kv_per_pos}
+
+
+def c3_bench(torch, steps, warmup, ctx):
+    """The headline: whole-model decode at Qwen3-30B-A3B shape, K steps at
+    positions spread evenly over 64..ctx-1 (see the module docstring)."""
+    from tierlm_amd.model import QWEN3_30B_A3B, Model, bench_prompt
     t0 = time.perf_counter()
     m = Model.synth(QWEN3_30B_A3B, expert_dt=Q6_K, dense_dt=8, seed=1, max_ctx=ctx)
     built = time.perf_counter() - t0
     try:
-        r = time_model(m, 64, ctx - 64, reps, warm_n=8)
-        short = time_model(m, 64, 64, reps)
+        prompt = bench_prompt(64, QWEN3_30B_A3B["vocab"])
+        m.reset()
+        t0 = time.perf_counter()
+        toks = m.generate(prompt, ctx - 64)          # fills the context to ctx - 1 positions (graph captured)
+        fill_s = time.perf_counter() - t0
+        top = ctx - 1
+        assert m.kv_len() == top
+        span = top - 64 + 1
+        positions = [top - (i * span) // steps for i in range(steps)]   # descending, evenly over 64..top
+        w = max(1, warmup)
+        m.rewind(top - w)
+        m.decode(w)                                  # warm-up steps (untimed), back at top positions
+        m.sync()
+        st = torch.cuda.ExternalStream(m.stream())
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        ev0.record(st)
+        for p in positions:
+            m.rewind(p)
+            m.decode(1)
+        ev1.record(st)
+        m.sync()
+        wall = time.perf_counter() - h0
+        ev1.synchronize()
+        ev_s = ev0.elapsed_time(ev1) * 1e-3
     finally:
         m.close()
-    out = {"model": "Qwen3-30B-A3B shape, random init (48 layers, 128 experts top-8, Q6_K experts, Q8_0 dense)",
-           "context": ctx, "prefill_tok_s": r["prefill_tok_s"], "decode_tok_s": r["decode_tok_s"],
-           "decode_ms_per_token": round(r["decode_us_per_token"] / 1e3, 3),
-           "decode_tok_s_first_64": short["decode_tok_s"], "build_s": round(built, 2),
-           "timing": f"host wall clock around tlm_hip_model_generate: prefill 64, then {ctx - 64 - 1} decode steps "
-                     f"to {ctx} positions, best of {reps}; each step one replay of a captured HIP graph",
-           "reference_cpu": None}
-    log(f"bench: Qwen3-30B-A3B-shape model: decode {out['decode_tok_s']:.1f} tok/s to {ctx} positions "
-        f"({out['decode_ms_per_token']:.3f} ms/token; {out['decode_tok_s_first_64']:.1f} tok/s over the first 64), "
-        f"prefill {out['prefill_tok_s']:.1f} tok/s")
-    return out
+    gb = c3_geometry_bytes(QWEN3_30B_A3B)
+    kv_mean = sum((p + 1) * gb["kv_per_position"] for p in positions) / len(positions)
+    per_tok = gb["weights_per_token"] + kv_mean
+    sec = ev_s / steps
+    achieved = per_tok / sec / 1e9
+    log(f"bench: Qwen3-30B-A3B-shape decode: {steps / ev_s:.1f} tok/s over {steps} steps at positions "
+        f"{positions[-1]}..{positions[0]} ({sec * 1e3:.3f} ms/token events, {wall / steps * 1e3:.3f} ms/token host); "
+        f"{per_tok / 1e9:.3f} GB/token = {achieved:.0f} GB/s; context fill {ctx - 64} tokens in {fill_s:.1f} s "
+        f"({(ctx - 64) / fill_s:.1f} tok/s)")
+    return {"tok_s": steps / ev_s, "ms_per_step": sec * 1e3, "wall_ms_per_step": wall / steps * 1e3,
+            "positions": [positions[-1], positions[0]], "bytes_per_token": per_tok, "weights_per_token":
+            gb["weights_per_token"], "kv_bytes_per_token_mean": kv_mean, "achieved_GBps": achieved,
+            "build_s": built, "fill_tok_s": (ctx - 64) / fill_s, "tokens_head": toks[:4], "geometry_bytes": gb}
 
 
 def cpu_baseline(args, threads):
-    """Reference kernels on the host (oracle/_ref), bounded sample."""
+    """The reference's kernels on the host cores for a bounded sample of the
+    per-token work at Qwen3-30B-A3B shape (oracle/_ref): one layer's q|k|v
+    and o projections and routed MoE block, repeated, and the lm_head; tok/s
+    = 1 / (48 x layer + lm_head)."""
+    import ctypes as C
+
     import numpy as np
 
     import oracle
@@ -395,75 +446,72 @@ def cpu_baseline(args, threads):
     if oracle.ref is None:
         return None
     rng = np.random.default_rng(3)
-    experts = []
-    for _ in range(E):
-        experts.append((random_code_rows(rng, Q6_K, DE, D), random_code_rows(rng, Q6_K, DE, D),
-                        random_code_rows(rng, Q6_K, D, DE)))
+    Q8_0 = 8
+    H, KVH, HD, V = 32, 4, 128, 151936
+    experts = [(random_code_rows(rng, Q6_K, DE, D), random_code_rows(rng, Q6_K, DE, D),
+                random_code_rows(rng, Q6_K, D, DE)) for _ in range(E)]
     host = oracle.MoeHost(D=D, de=DE, E=E, k=K, expert_dt=Q6_K, ffn_norm=np.ones(D, np.float32),
                           router_w=(rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32), experts=experts)
-    hs = rng.standard_normal((64, D)).astype(np.float32)
-    out = {}
-    for nthr in sorted({1, threads}):
-        handle = oracle.ref.refmoe_new(nthr)
-        host.run_ref(handle, hs[0])            # warm
+    # 8 distinct layers of dense weights (160 MB) beside the 495 MB of experts and the 330 MB
+    # lm_head, so the sample streams from memory rather than the host's last-level cache
+    NL = 8
+    dense = [[random_code_rows(rng, Q8_0, r, D) for r in (H * HD, KVH * HD, KVH * HD)] +
+             [random_code_rows(rng, Q8_0, D, H * HD)] for _ in range(NL)]
+    wl = random_code_rows(rng, Q8_0, V, D)
+    ys = [np.empty(r, np.float32) for r in (H * HD, KVH * HD, KVH * HD, D, V)]
+    xs = rng.standard_normal((64, H * HD)).astype(np.float32)
+
+    def mvs(handle, mats, n, x, outs):
+        W = (C.c_void_p * len(mats))(*[mm.ctypes.data for mm in mats])
+        R = (C.c_int64 * len(mats))(*[mm.shape[0] for mm in mats])
+        Y = (C.c_void_p * len(mats))(*[o.ctypes.data for o in outs])
+        oracle.ref.refmoe_matvecs(handle, Q8_0, W, R, n, x.ctypes.data, Y, len(mats))
+
+    handle = oracle.ref.refmoe_new(threads)
+    try:
+        def layer(i):
+            x = xs[i % 64]
+            wq, wk, wv, wo = dense[i % NL]
+            mvs(handle, [wq, wk, wv], D, np.ascontiguousarray(x[:D]), ys[:3])
+            mvs(handle, [wo], H * HD, x, [ys[3]])
+            host.run_ref(handle, np.ascontiguousarray(x[:D]))
+
+        layer(0)
         t0, n = time.perf_counter(), 0
-        while time.perf_counter() - t0 < args.cpu_seconds / 2 or n < 8:
-            host.run_ref(handle, hs[n % 64])
+        while time.perf_counter() - t0 < args.cpu_seconds * 0.8 or n < 4:
+            layer(n)
             n += 1
-        dt = time.perf_counter() - t0
+        t_layer = (time.perf_counter() - t0) / n
+        mvs(handle, [wl], D, np.ascontiguousarray(xs[0][:D]), [ys[4]])
+        t0, nl = time.perf_counter(), 0
+        while time.perf_counter() - t0 < args.cpu_seconds * 0.2 or nl < 2:
+            mvs(handle, [wl], D, np.ascontiguousarray(xs[nl % 64][:D]), [ys[4]])
+            nl += 1
+        t_lm = (time.perf_counter() - t0) / nl
+    finally:
         oracle.ref.refmoe_free(handle)
-        out[nthr] = (n / dt, n)
     tier = oracle.ref.refmoe_tier().decode()
-    best = out[threads]
-    return {"value": round(best[0], 2), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"{best[1]} tokens of the same block (128 distinct random-code Q6_K experts, 495 MB) "
-                      f"through the reference's {tier} tier + pool on {threads} threads",
-            "single_thread_tok_s": round(out[1][0], 2), "gpu_over_cpu": None}
+    per_tok = 48 * t_layer + t_lm
+    return {"value": round(1.0 / per_tok, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} layers (q|k|v + o Q8_0 projections cycling 8 distinct layers, and the routed top-8 Q6_K "
+                      f"MoE block over 128 random-code experts, at Qwen3-30B-A3B shape; about 1 GB of weights in "
+                      f"all) and {nl} lm_head passes (151936 x 2048 Q8_0) "
+                      f"through the reference's {tier} tier + pool on {threads} threads; tok/s = 1 / (48 x "
+                      f"{t_layer * 1e3:.2f} ms + {t_lm * 1e3:.2f} ms); attention arithmetic and norms not included",
+            "layer_ms": round(t_layer * 1e3, 3), "lm_head_ms": round(t_lm * 1e3, 3)}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10000, help="timed tokens")
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--layers", type=int, default=48, help="distinct layer copies cycled by the tokens")
-    ap.add_argument("--graph", type=int, default=100, help="tokens per captured HIP graph (0 = eager launches)")
-    ap.add_argument("--roofline-tokens", type=int, default=960, help="launches per phase in the roofline graphs")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill measurement")
-    ap.add_argument("--no-store", action="store_true", help="skip the expert slot cache measurement")
-    ap.add_argument("--no-c1", action="store_true", help="skip the whole-step synthetic model measurement")
-    ap.add_argument("--no-c3", action="store_true", help="skip the full Qwen3-30B-A3B-shape model measurement")
-    ap.add_argument("--c3-context", type=int, default=2048, help="positions the full-model decode runs to")
-    ap.add_argument("--store-tokens", type=int, default=400, help="tokens per slot-cache decode measurement")
-    ap.add_argument("--no-c5", action="store_true", help="skip the Qwen3-235B-shape slot-cache measurement")
-    ap.add_argument("--c5-tokens", type=int, default=20, help="timed tokens of the Qwen3-235B-shape slot-cache run")
-    ap.add_argument("--c5-cache-gb", type=float, default=64.0, help="slot cache cap of that run (GB)")
-    ap.add_argument("--copy-check-mib", type=int, default=0,
-                    help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
-                         "of known size, the scale for HBM byte counters")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
-              "multi-GPU runs are not part of it", file=sys.stderr)
-        sys.exit(2)
-
+def expert_gemv_bench(torch, dev, args, gen):
+    """The routed MoE block alone at Qwen3-30B-A3B shape (one layer per token,
+    --layers resident copies of the 128 experts cycled, HIP graphs of --graph
+    tokens), and per phase the average launch time from a graph of
+    back-to-back launches of that phase (HIP events).  Returns the block's
+    figures and the weights/tensors the prefill and cache legs reuse."""
     import numpy as np
-    import torch
-
-    import tierlm_amd
     from tierlm_amd import MoeBlock
-    from tierlm_amd import quant as hq
-
-    dev = torch.device("cuda", 0)
-    hq.init(0)
-    assert hq.selftest_failures() == 0, "HIP self-test failures"
     L = args.layers
     log(f"bench: allocating {L} x {E} Q6_K experts ({L * E * EXPERT_BYTES / 1e9:.1f} GB)")
     W = make_weights(torch, dev, L, seed=1)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(2)
     router_w = torch.randn((E, D), generator=gen, device=dev) / float(np.sqrt(D))
     ffn_norm = torch.ones(D, device=dev)
     blocks = []
@@ -472,7 +520,8 @@ def main():
         ptrs = [base + ((layer * E + e) * 3 + j) * MAT_BYTES for e in range(E) for j in range(3)]
         blocks.append(MoeBlock(D=D, de=DE, E=E, k=K, expert_dt=Q6_K, ffn_norm=ffn_norm, router_w=router_w,
                                expert_ptrs=ptrs, router=0, eps=1e-6, device=dev))
-    total = args.warmup + args.steps
+    ntok, warm = args.c2_tokens, 200
+    total = warm + ntok
     H = torch.randn((max(total, args.roofline_tokens), D), generator=gen, device=dev)
     torch.cuda.synchronize()
 
@@ -480,48 +529,33 @@ def main():
         for t in range(t0, t1):
             blocks[t % L](H[t])
 
-    graphs = []
-    if args.graph > 0:
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            run_tokens(0, min(args.graph, total))          # warm the launch path before capture
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-
-        def capture(t0, t1):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                run_tokens(t0, t1)
-            return g
-        G = args.graph
-        warm_chunks = [(t, min(t + G, args.warmup)) for t in range(0, args.warmup, G)]
-        timed_chunks = [(t, min(t + G, total)) for t in range(args.warmup, total, G)]
-        log(f"bench: capturing {len(warm_chunks) + len(timed_chunks)} graphs of <= {G} tokens")
-        warm_graphs = [capture(*c) for c in warm_chunks]
-        graphs = [capture(*c) for c in timed_chunks]
-        torch.cuda.synchronize()
-        for g in warm_graphs:
-            g.replay()
-    else:
-        run_tokens(0, args.warmup)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run_tokens(0, min(args.graph, total))
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
 
-    t0 = time.perf_counter()
-    if graphs:
-        for g in graphs:
-            g.replay()
-    else:
-        run_tokens(args.warmup, total)
+    def capture(t0, t1):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run_tokens(t0, t1)
+        return g
+    G = args.graph
+    warm_graphs = [capture(t, min(t + G, warm)) for t in range(0, warm, G)]
+    graphs = [capture(t, min(t + G, total)) for t in range(warm, total, G)]
+    for g in warm_graphs:
+        g.replay()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    tok_s = args.steps / elapsed
-    ms_per_step = elapsed * 1e3 / args.steps
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for g in graphs:
+        g.replay()
+    ev1.record()
+    ev1.synchronize()
+    block_us = ev0.elapsed_time(ev1) * 1e3 / ntok
+    del graphs, warm_graphs
 
-    # roofline pass: per phase, one HIP graph of R launches of that phase
-    # alone, each on the next layer copy (so weights stream from HBM), replayed
-    # between two events on the stream it runs on; average launch = elapsed / R
-    # (kernel time plus the graph's dispatch gap between dependent launches)
     R = args.roofline_tokens
     hr = torch.randn(D, generator=gen, device=dev)
     for b in blocks:                       # every workspace holds a routed token
@@ -556,55 +590,123 @@ def main():
     gu_gbs = GATEUP_BYTES / (p2 * 1e-6) / 1e9
     dn_gbs = DOWN_BYTES / (p3 * 1e-6) / 1e9
     expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
-    log(f"bench: {tok_s:.0f} tok/s ({ms_per_step * 1e3:.2f} us/token); per launch: router {p1:.2f} us, "
+    log(f"bench: MoE block {1e6 / block_us:.0f} tok/s ({block_us:.2f} us/token); per launch: router {p1:.2f} us, "
         f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down+combine {p3:.2f} us ({dn_gbs:.0f} GB/s)")
-    # on-box streaming-read reference: this library's packed Q6_K GEMV over a span of up to
-    # 2 GiB of the resident expert bytes read as one 2048-wide matrix (values irrelevant); the
-    # span never exceeds the buffer it reads
-    srows = min(2 << 30, W.numel()) // 1680 // 16 * 16
-    sbytes = hq.packed_bytes(Q6_K, srows, D)
-    assert 0 < sbytes <= W.numel(), (sbytes, W.numel())
-    xs = hq.quantize_act(hq.Q8_K, torch.randn(D, generator=gen, device=dev))
-    ys = torch.empty(srows, dtype=torch.float32, device=dev)
-    hq.matvec_packed(Q6_K, W, srows, D, xs, ys)
+    out = {"workload": "one routed MoE block per token at Qwen3-30B-A3B shape (D 2048, 128 experts top-8 "
+                       "softmax+renorm, expert width 768, Q6_K random-code experts, f32 router), "
+                       f"{L} resident layer copies cycled", "block_tok_s": round(1e6 / block_us, 1),
+           "block_us_per_token": round(block_us, 3), "tokens": ntok,
+           "expert_bytes_per_token": TOKEN_BYTES, "expert_gemv_GBps": round(expert_gbs, 1),
+           "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4),
+           "gateup": {"kernel": "k_moe_gateup (routing + gate/up of the top-8 experts + SwiGLU)",
+                      "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(p2, 3),
+                      "achieved_GBps": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                      "traffic": GATEUP_TRAFFIC_BYTES,
+                      "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled by a 256 MiB copy"},
+           "down_combine": {"bytes_per_launch": DOWN_BYTES, "avg_launch_us": round(p3, 3),
+                            "achieved_GBps": round(dn_gbs, 1)},
+           "router_avg_launch_us": round(p1, 3),
+           "timing": "HIP events: the block over graphs of --graph tokens; per phase a graph of "
+                     f"{R} back-to-back launches of that phase, / {R} (best of 3)"}
+    return out, W, router_w, ffn_norm
+
+
+def stream_read_peak(torch, dev, nbytes):
+    """A plain streaming read (tlm_hip_stream_read) over nbytes of device
+    memory, best of 5, HIP events."""
+    import ctypes as C
+
+    from tierlm_amd._lib import check, lib
+    from tierlm_amd.quant import stream
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(7)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    check(lib.tlm_hip_stream_read(C.c_void_p(buf.data_ptr()), nbytes, C.c_void_p(sink.data_ptr()), stream()))
     torch.cuda.synchronize()
-    stream_us = None
+    best = None
     for _ in range(5):
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
-        hq.matvec_packed(Q6_K, W, srows, D, xs, ys)
+        check(lib.tlm_hip_stream_read(C.c_void_p(buf.data_ptr()), nbytes, C.c_void_p(sink.data_ptr()), stream()))
         ev1.record()
         ev1.synchronize()
         us = ev0.elapsed_time(ev1) * 1e3
-        stream_us = us if stream_us is None else min(stream_us, us)
-    stream_gbs = sbytes / (stream_us * 1e-6) / 1e9
-    log(f"bench: streaming GEMV over {sbytes / 1e9:.2f} GB: {stream_gbs:.0f} GB/s")
+        best = us if best is None else min(best, us)
+    del buf
+    gbs = nbytes / (best * 1e-6) / 1e9
+    log(f"bench: plain streaming read of {nbytes / 1e9:.2f} GB: {gbs:.0f} GB/s")
+    return {"GBps": round(gbs, 1), "bytes": nbytes, "us": round(best, 1),
+            "kernel": "k_stream_read: 16-byte loads, eight in flight per lane, 2048 groups of 256, grid-stride"}
 
-    if args.copy_check_mib > 0:
-        nbytes = args.copy_check_mib << 20
-        src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"bench: copy check {args.copy_check_mib} MiB done")
-        del src, dst
 
-    prefill = prefill_q5k = None
-    if not args.no_prefill:
-        prefill = prefill_bench(torch, dev, W, MAT_BYTES, Q6_K, router_w, ffn_norm, gen)
-        W5 = make_weights_q5k(torch, dev, seed=5)
-        prefill_q5k = prefill_bench(torch, dev, W5, MAT_BYTES_Q5K, Q5_K, router_w, ffn_norm, gen)
-        del W5
-    slot_cache = None if args.no_store else slot_cache_bench(torch, dev, router_w, ffn_norm, gen, args.store_tokens)
-    c1 = None if args.no_c1 or not os.path.exists(C1_STORE) else c1_bench(3)
-    if not args.no_c3:
-        del W                                  # the block's 23.8 GB of experts; the model builds its own
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1984, help="timed decode steps (positions spread over 64..2047)")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--c3-context", type=int, default=2048, help="context the decode positions span")
+    ap.add_argument("--layers", type=int, default=48, help="MoE block: distinct layer copies cycled by the tokens")
+    ap.add_argument("--c2-tokens", type=int, default=2000, help="MoE block: timed tokens")
+    ap.add_argument("--graph", type=int, default=100, help="MoE block: tokens per captured HIP graph")
+    ap.add_argument("--roofline-tokens", type=int, default=960, help="MoE block: launches per phase graph")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c2", action="store_true", help="skip the MoE-block measurement (and prefill / cache)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill measurement")
+    ap.add_argument("--no-store", action="store_true", help="skip the expert slot cache measurement")
+    ap.add_argument("--no-c1", action="store_true", help="skip the whole-step synthetic model measurement")
+    ap.add_argument("--store-tokens", type=int, default=400, help="tokens per slot-cache decode measurement")
+    ap.add_argument("--no-c5", action="store_true", help="skip the Qwen3-235B-shape slot-cache measurement")
+    ap.add_argument("--c5-tokens", type=int, default=20, help="timed tokens of the Qwen3-235B-shape slot-cache run")
+    ap.add_argument("--c5-cache-gb", type=float, default=64.0, help="slot cache cap of that run (GB)")
+    ap.add_argument("--copy-check-mib", type=int, default=0,
+                    help="after the timed work, one device-to-device copy of this many MiB: a plain copy kernel "
+                         "of known size, the scale for HBM byte counters")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
+              "multi-GPU runs are not part of it", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1:
+        ap.error("--steps must be at least 1")
+
+    import torch
+
+    from tierlm_amd import quant as hq
+
+    dev = torch.device("cuda", 0)
+    hq.init(0)
+    assert hq.selftest_failures() == 0, "HIP self-test failures"
+
+    c3 = c3_bench(torch, args.steps, args.warmup, args.c3_context)
+    torch.cuda.empty_cache()
+    peak = stream_read_peak(torch, dev, 2 << 30)
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    c2 = prefill = prefill_q5k = slot_cache = None
+    if not args.no_c2:
+        c2, W, router_w, ffn_norm = expert_gemv_bench(torch, dev, args, gen)
+        if args.copy_check_mib > 0:
+            nbytes = args.copy_check_mib << 20
+            src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            log(f"bench: copy check {args.copy_check_mib} MiB done")
+            del src, dst
+        if not args.no_prefill:
+            prefill = prefill_bench(torch, dev, W, MAT_BYTES, Q6_K, router_w, ffn_norm, gen)
+            W5 = make_weights_q5k(torch, dev, seed=5)
+            prefill_q5k = prefill_bench(torch, dev, W5, MAT_BYTES_Q5K, Q5_K, router_w, ffn_norm, gen)
+            del W5
+        if not args.no_store:
+            slot_cache = slot_cache_bench(torch, dev, router_w, ffn_norm, gen, args.store_tokens)
+        del W
         torch.cuda.empty_cache()
-    c3 = None if args.no_c3 else c3_bench(1, args.c3_context)
+    c1 = None if args.no_c1 or not os.path.exists(C1_STORE) else c1_bench(3)
     c5 = None
     if not args.no_c5:
-        torch.cuda.empty_cache()
         try:
             c5 = c5_bench(torch, dev, args.c5_tokens, args.c5_cache_gb)
         except Exception as e:                 # recorded, so the rest of the line still prints
@@ -618,36 +720,38 @@ def main():
         log(f"bench: cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(args, threads)
         if cpu:
-            cpu["gpu_over_cpu"] = round(tok_s / cpu["value"], 1)
+            cpu["gpu_over_cpu"] = round(c3["tok_s"] / cpu["value"], 1)
 
     line = {
         "metric": "decode tok/s batch-1, Qwen3-30B-A3B shape; expert GEMV HBM GB/s vs peak",
-        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8xu6->int32 (Q6_K x Q8_K), f32 chain", "data": "synthetic",
-        "config": {"workload": "single routed MoE block at Qwen3-30B-A3B shape (D 2048, 128 experts top-8 softmax+renorm, "
-                               "expert width 768, Q6_K random-code experts, f32 router), batch-1 decode, "
-                               f"one token per step, {L} resident layer copies cycled",
-                   "tokens_timed": args.steps, "graph_tokens": args.graph, "layers_resident": L,
-                   "expert_bytes_per_token": TOKEN_BYTES},
-        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
-                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled by a 256 MiB copy",
-                     "kernel": "k_moe_gateup (routing + gate/up of the top-8 experts + SwiGLU)",
-                     "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(p2, 3),
-                     "down_combine_GBps": round(dn_gbs, 1), "down_combine_avg_launch_us": round(p3, 3),
-                     "router_avg_launch_us": round(p1, 3),
-                     "timing": "HIP events around a graph of R back-to-back launches of the phase (R = roofline_launches), / R",
-                     "roofline_launches": R,
-                     "expert_gemv_GBps": round(expert_gbs, 1), "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4),
-                     "stream_read_peak_GBps": round(stream_gbs, 1),
-                     "stream_read_kernel": "k_mv_packed<Q6_K> over ~2 GB of resident expert bytes, one launch (best of 5)"},
+        "value": round(c3["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(c3["ms_per_step"], 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8xu6/int8->int32 (Q6_K/Q8_0 x Q8_K/a8), f32 chains", "data": "synthetic",
+        "config": {"workload": "whole-model batch-1 greedy decode to 2048 positions, Qwen3-30B-A3B shape: 48 layers, "
+                               "hidden 2048, 32 q / 4 kv heads x 128, 128 experts top-8 of width 768 (Q6_K, all "
+                               "resident), Q8_0 dense, f32 router, vocabulary 151936, random init in HBM; one step = "
+                               "one token at a context position spread evenly over 64..2047",
+                   "positions": c3["positions"], "context": args.c3_context,
+                   "wall_ms_per_step": round(c3["wall_ms_per_step"], 4),
+                   "timing": "HIP events on the model's stream around exactly K steps (each a context rewind + "
+                             "one replay of the captured step graph)"},
+        "roofline": {"bound": "hbm", "achieved": round(c3["achieved_GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(c3["achieved_GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "the decode step (its kernels' algorithmic bytes / the step time)",
+                     "bytes_per_step": int(c3["bytes_per_token"]),
+                     "weights_per_step": c3["weights_per_token"],
+                     "kv_bytes_per_step_mean": int(c3["kv_bytes_per_token_mean"]),
+                     "avg_step_us": round(c3["ms_per_step"] * 1e3, 2),
+                     "stream_read_peak_GBps": peak["GBps"], "stream_read_frac": round(
+                         c3["achieved_GBps"] / peak["GBps"], 4),
+                     "stream_read_kernel": peak["kernel"]},
+        "expert_gemv": c2,
         "cpu_baseline": cpu,
         "prefill": prefill,
         "prefill_q5k": prefill_q5k,
         "slot_cache": slot_cache,
         "c1_whole_step": c1,
-        "qwen3_30b_a3b_whole_model": c3,
+        "qwen3_30b_a3b_context_fill_tok_s": round(c3["fill_tok_s"], 1),
         "qwen3_235b_a22b_slot_cache": c5,
     }
     print(json.dumps(line), flush=True)

@@ -71,6 +71,12 @@ int tlm_hip_sync(void *stream);
 size_t tlm_hip_qact_bytes(int kind, int64_t n);
 int    tlm_hip_quantize_act(int kind, const float *x, int64_t n, void *dst, void *stream);
 
+/* No counterpart in the reference: a plain streaming read of bytes (16-byte
+ * aligned) from device memory - the read rate of this device that the GEMVs'
+ * HBM figures are set beside.  sink: one device word, written only in the
+ * (practically never) event that the folded data equals a fixed constant. */
+int    tlm_hip_stream_read(const void *p, size_t bytes, uint32_t *sink, void *stream);
+
 /* ---- the exponential ----------------------------------------------------
  * y[i] = e^(x[i]) on device memory, bit for bit libm's expf as the reference
  * calls it (silu / sigmoidf_, src/lib/tlm_model.c:171-172; the routing softmax
@@ -434,6 +440,21 @@ int  tlm_hip_model_step(tlm_hip_model *M, int token, float *logits, int32_t *nex
 /* prefill the prompt, then n_gen greedy tokens into out; between steps the
  * token stays on the device. */
 int  tlm_hip_model_generate(tlm_hip_model *M, const int32_t *prompt, int n_prompt, int n_gen, int32_t *out);
+/* No counterpart in the reference (whose KV cache only resets): keep the
+ * first len positions of the context (0 <= len <= kv_len) and drop the rest,
+ * as after rejected speculative tokens; the next step decodes position len
+ * with the token a previous step stored there.  Enqueued on the model's
+ * stream, no wait. */
+int  tlm_hip_model_rewind(tlm_hip_model *M, int len);
+/* n greedy steps from the current position, each on the token the previous
+ * step chose (the loop of tierlm bench / generate after its prefill, src/bin/
+ * tierlm.c:720-729), enqueued without waiting; tlm_hip_model_sync waits.  The
+ * context must hold at least one position. */
+int  tlm_hip_model_decode(tlm_hip_model *M, int n);
+int  tlm_hip_model_sync(tlm_hip_model *M);
+/* the model's stream (hipStream_t), for callers that time or order work
+ * against its steps */
+void *tlm_hip_model_stream(const tlm_hip_model *M);
 
 /* ---- reference tier ABI --------------------------------------------------
  * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a

@@ -80,6 +80,7 @@ if ref is not None:
         ("refmoe_new", vp, [i32]), ("refmoe_free", None, [vp]), ("refmoe_tier", C.c_char_p, []),
         ("refmoe_force_tier", None, [C.c_char_p]),
         ("refmoe_layer", i32, [vp, C.POINTER(OrcMoeDesc), vp, vp, vp]),
+        ("refmoe_matvecs", None, [vp, i32, vp, vp, i64, vp, vp, i32]),
     ]:
         _f = getattr(ref, _n)
         _f.restype, _f.argtypes = _r, _a

@@ -98,6 +98,23 @@ void refmoe_force_tier(const char *tier) {
     tlm_quant_init();
 }
 
+/* nseg matvecs of one dtype and width n on one activation (quantised here
+ * with the reference's quantiser) through the pool as one job, the way mv_exec
+ * runs the dense projections of attention() and the lm_head
+ * (src/lib/tlm_model.c:175-222, 734-739, 1087-1095). */
+void refmoe_matvecs(refmoe *m, int dt, const void *const *W, const int64_t *rows, int64_t n, const float *x,
+                    float *const *y, int nseg) {
+    tlm_dtype t = (tlm_dtype)dt, ak = tlm_act_kind_for(t);
+    uint8_t *act = malloc(tlm_qact_bytes(ak, n) + 64);
+    const void *a = x;
+    if (ak != TLM_DT_F32) { tlm_quantize_act(ak, x, n, act); a = act; }
+    job *j = calloc(1, sizeof *j);
+    for (int i = 0; i < nseg && i < SEG_MAX; i++) job_push(j, t, W[i], rows[i], n, a, y[i]);
+    job_run(m, j);
+    free(j);
+    free(act);
+}
+
 int refmoe_layer(refmoe *m, const orc_moe_desc *d, float *h, int *ids, float *w) {
     int64_t D = d->D, de = d->de, ds = d->ds;
     int k = d->k;

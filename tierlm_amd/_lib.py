@@ -122,6 +122,7 @@ _SIGS = {
     "tlm_hip_qact_bytes": (sz, [i32, i64]),
     "tlm_hip_quantize_act": (i32, [i32, vp, i64, vp, vp]),
     "tlm_hip_expf": (i32, [vp, vp, i64, vp]),
+    "tlm_hip_stream_read": (i32, [vp, sz, vp, vp]),
     "tlm_hip_matvec_rows": (i32, [i32, vp, sz, vp, vp, i64, i64, i64, vp]),
     "tlm_hip_packed_bytes": (sz, [i32, i64, i64]),
     "tlm_hip_pack": (i32, [i32, vp, sz, i64, i64, vp, vp]),
@@ -168,6 +169,10 @@ _SIGS = {
     "tlm_hip_model_kv_len": (i32, [vp]),
     "tlm_hip_model_kv_capacity": (i32, [vp]),
     "tlm_hip_model_routes": (i32, [vp, vp, vp]),
+    "tlm_hip_model_rewind": (i32, [vp, i32]),
+    "tlm_hip_model_decode": (i32, [vp, i32]),
+    "tlm_hip_model_sync": (i32, [vp]),
+    "tlm_hip_model_stream": (vp, [vp]),
     "tlm_hip_model_reset": (None, [vp]),
     "tlm_hip_model_step": (i32, [vp, i32, vp, C.POINTER(C.c_int32)]),
     "tlm_hip_model_generate": (i32, [vp, C.POINTER(C.c_int32), i32, i32, C.POINTER(C.c_int32)]),

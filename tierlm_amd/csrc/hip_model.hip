@@ -522,6 +522,9 @@ __global__ __launch_bounds__(1024) void k_advance(int32_t *st, int32_t *seq, con
     if (threadIdx.x == 0) st[0] = pos + 1;
 }
 
+/* the context position (the next step's), as a rollback sets it */
+__global__ void k_set_pos(int32_t *st, int pos) { st[0] = pos; }
+
 struct DevMat {
     int dt = -1;
     int64_t rows = 0, n = 0;
@@ -1231,6 +1234,34 @@ int tlm_hip_model_routes(tlm_hip_model *M, int32_t *ids, float *w) {
         }
     return TLM_HIP_OK;
 }
+int tlm_hip_model_rewind(tlm_hip_model *M, int len) {
+    if (!M) return tlmh_seterr(TLM_HIP_EINVAL, "model rewind: NULL");
+    if (len < 0 || len > M->kv_len)
+        return tlmh_seterr(TLM_HIP_ERANGE, "model rewind: %d positions, the context holds %d", len, M->kv_len);
+    if (len == M->kv_len) return TLM_HIP_OK;
+    hipLaunchKernelGGL(k_set_pos, dim3(1), dim3(1), 0, M->stream, M->st, len);
+    int rc = tlmh_check(hipGetLastError(), "model rewind");
+    if (!rc) M->kv_len = len;
+    return rc;
+}
+
+int tlm_hip_model_decode(tlm_hip_model *M, int n) {
+    if (!M || n < 0) return tlmh_seterr(TLM_HIP_EINVAL, "model decode: bad arguments");
+    if (M->kv_len == 0) return tlmh_seterr(TLM_HIP_EINVAL, "model decode: no token yet (prefill first)");
+    if ((int64_t)M->kv_len + n > M->max_ctx)
+        return tlmh_seterr(TLM_HIP_ERANGE, "model decode: %d + %d tokens exceed the context (%d)", M->kv_len, n,
+                           M->max_ctx);
+    int rc = TLM_HIP_OK;
+    for (int i = 0; i < n && !rc; i++) rc = step(M, true);
+    return rc;
+}
+
+int tlm_hip_model_sync(tlm_hip_model *M) {
+    return M ? tlmh_check(hipStreamSynchronize(M->stream), "model sync") : TLM_HIP_OK;
+}
+
+void *tlm_hip_model_stream(const tlm_hip_model *M) { return M ? (void *)M->stream : nullptr; }
+
 void tlm_hip_model_reset(tlm_hip_model *M) {
     if (!M) return;
     M->kv_len = 0;

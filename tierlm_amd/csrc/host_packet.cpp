@@ -20,7 +20,9 @@
 
 #include <algorithm>
 #include <cmath>
+#include <memory>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/tlm_hip.h"
@@ -138,56 +140,67 @@ struct Sha256 {
 
 bool str_ok(const char *s, size_t cap, bool allow_empty) { return memchr(s, 0, cap) && (allow_empty || s[0]); }
 
-int key_cmp(const tlm_hip_packet_loc &a, const tlm_hip_packet_loc &b) {
-    if (a.type != b.type) return a.type < b.type ? -1 : 1;
-    if (a.layer != b.layer) return a.layer < b.layer ? -1 : 1;
-    if (a.id != b.id) return a.id < b.id ? -1 : 1;
-    return 0;
-}
+/* ---- packet table rules ------------------------------------------------------
+ * What a loaded table must satisfy (the format of src/lib/tlm_packet.h:39-95,
+ * the same rejections as the reference's loader, src/lib/tlm_packet.c:
+ * 211-275): each record is checked against the list of per-record rules
+ * below, the table must be in strictly increasing (type, layer, id) order,
+ * and no two byte ranges (a packet or its replica) may share bytes of one
+ * drive file. */
+using PacketKey = std::tuple<uint16_t, uint16_t, uint32_t>;
+PacketKey packet_key(const tlm_hip_packet_loc &l) { return PacketKey(l.type, l.layer, l.id); }
 
-/* src/lib/tlm_packet.c:211-275 */
-int validate_packets(const std::vector<tlm_hip_packet_loc> &p, uint32_t n_drives) {
-    const uint32_t n = (uint32_t)p.size();
-    for (uint32_t i = 0; i < n; i++) {
+bool aligned_range(uint64_t off, uint64_t len) { return off % ALIGN_IO == 0 && off <= UINT64_MAX - len; }
+
+struct RecordRule {
+    const char *what;
+    bool (*ok)(const tlm_hip_packet_loc &, uint32_t n_drives);
+};
+const RecordRule RECORD_RULES[] = {
+    {"type outside DENSE..TOKEN",
+     [](const tlm_hip_packet_loc &l, uint32_t) { return l.type >= TLM_HIP_PK_DENSE && l.type <= TLM_HIP_PK_TOKEN; }},
+    {"drive index past the drive list", [](const tlm_hip_packet_loc &l, uint32_t nd) { return l.drive < nd; }},
+    {"replica drive invalid or equal to the primary",
+     [](const tlm_hip_packet_loc &l, uint32_t nd) {
+         return l.replica_drive == 0xFF || (l.replica_drive < nd && l.replica_drive != l.drive);
+     }},
+    {"flag bits this format does not define",
+     [](const tlm_hip_packet_loc &l, uint32_t) { return (l.flags & ~KNOWN_FLAGS) == 0; }},
+    {"length not a positive multiple of 4096 within the payload limit",
+     [](const tlm_hip_packet_loc &l, uint32_t) {
+         return l.total_len >= ALIGN_IO && l.total_len % ALIGN_IO == 0 && l.total_len <= MAX_PAYLOAD + ALIGN_IO;
+     }},
+    {"offset not 4096-aligned or wrapping", [](const tlm_hip_packet_loc &l, uint32_t) { return aligned_range(l.offset, l.total_len); }},
+    {"replica offset not 4096-aligned or wrapping",
+     [](const tlm_hip_packet_loc &l, uint32_t) {
+         return l.replica_drive == 0xFF || aligned_range(l.replica_offset, l.total_len);
+     }},
+    {"heat negative or not finite", [](const tlm_hip_packet_loc &l, uint32_t) { return std::isfinite(l.heat) && l.heat >= 0.0f; }},
+};
+
+int check_table(const std::vector<tlm_hip_packet_loc> &p, uint32_t n_drives) {
+    /* byte ranges per drive: [first, last) with the record that owns them */
+    std::vector<std::vector<std::pair<uint64_t, uint32_t>>> starts(n_drives);
+    for (uint32_t i = 0; i < (uint32_t)p.size(); i++) {
         const tlm_hip_packet_loc &l = p[i];
-        if (l.type < TLM_HIP_PK_DENSE || l.type > TLM_HIP_PK_TOKEN)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u has bad type %u", i, l.type);
-        if (l.drive >= n_drives)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u drive %u >= %u drives", i, l.drive, n_drives);
-        if (l.replica_drive != 0xFF && (l.replica_drive >= n_drives || l.replica_drive == l.drive))
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u bad replica drive %u", i, l.replica_drive);
-        if (l.flags & ~KNOWN_FLAGS)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u unknown flags 0x%x", i, l.flags);
-        if (l.total_len < ALIGN_IO || l.total_len % ALIGN_IO || l.total_len > MAX_PAYLOAD + ALIGN_IO)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u bad length %llu", i,
-                               (unsigned long long)l.total_len);
-        if (l.offset % ALIGN_IO || l.offset > UINT64_MAX - l.total_len)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u misaligned offset", i);
-        if (l.replica_drive != 0xFF &&
-            (l.replica_offset % ALIGN_IO || l.replica_offset > UINT64_MAX - l.total_len))
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u misaligned replica offset", i);
-        if (!std::isfinite(l.heat) || l.heat < 0.0f)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet %u bad heat", i);
-        if (i > 0 && key_cmp(p[i - 1], l) >= 0)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packet table not strictly sorted at %u", i);
+        for (const RecordRule &r : RECORD_RULES)
+            if (!r.ok(l, n_drives))
+                return tlmh_seterr(TLM_HIP_EFORMAT, "store table: record %u (type %u, layer %u, id %u): %s", i, l.type,
+                                   l.layer, l.id, r.what);
+        if (i && !(packet_key(p[i - 1]) < packet_key(l)))
+            return tlmh_seterr(TLM_HIP_EFORMAT, "store table: record %u is not after record %u in (type, layer, id) "
+                               "order", i, i - 1);
+        starts[l.drive].push_back({l.offset, i});
+        if (l.replica_drive != 0xFF) starts[l.replica_drive].push_back({l.replica_offset, i});
     }
-    struct Ext {
-        uint64_t off, len;
-        uint32_t drive, idx;
-    };
-    std::vector<Ext> ex;
-    ex.reserve(2 * (size_t)n);
-    for (uint32_t i = 0; i < n; i++) {
-        ex.push_back(Ext{p[i].offset, p[i].total_len, p[i].drive, i});
-        if (p[i].replica_drive != 0xFF) ex.push_back(Ext{p[i].replica_offset, p[i].total_len, p[i].replica_drive, i});
+    for (uint32_t d = 0; d < n_drives; d++) {
+        auto &v = starts[d];
+        std::sort(v.begin(), v.end());
+        for (size_t j = 1; j < v.size(); j++)
+            if (v[j - 1].first + p[v[j - 1].second].total_len > v[j].first)
+                return tlmh_seterr(TLM_HIP_EFORMAT, "store table: records %u and %u claim the same bytes of drive %u",
+                                   v[j - 1].second, v[j].second, d);
     }
-    std::sort(ex.begin(), ex.end(), [](const Ext &a, const Ext &b) {
-        return a.drive != b.drive ? a.drive < b.drive : a.off < b.off;
-    });
-    for (size_t i = 1; i < ex.size(); i++)
-        if (ex[i].drive == ex[i - 1].drive && ex[i - 1].off + ex[i - 1].len > ex[i].off)
-            return tlmh_seterr(TLM_HIP_EFORMAT, "manifest: packets %u and %u overlap on drive %u", ex[i - 1].idx,
-                               ex[i].idx, ex[i].drive);
     return TLM_HIP_OK;
 }
 
@@ -228,70 +241,117 @@ struct tlm_hip_manifest {
 
 extern "C" {
 
-/* src/lib/tlm_packet.c:673-751 */
+/* ---- the manifest file ----------------------------------------------------------
+ * Layout (src/lib/tlm_packet.h:39-95, src/lib/tlm_packet.c:8-34): a 512-byte
+ * fixed header, the drive paths (256 bytes each), the packet table (48-byte
+ * records) and a text report, back to back, with the header's own CRC32C over
+ * its first 508 bytes and the drive paths, the table's SHA-256 and the
+ * report's CRC32C.  The header's section fields are checked as a list of rules
+ * on the decoded values, then the checksums, then the strings and records. */
+struct ManifestHeader {
+    uint32_t magic, version, fixed, rec, n_drives, n_packets, n_pruned, report_crc, header_crc;
+    uint64_t drives_off, table_off, table_len, report_off, report_len, file_size, actual;
+    explicit ManifestHeader(const uint8_t *b, size_t size)
+        : magic(rd32(b)), version(rd32(b + 4)), fixed(rd32(b + 8)), rec(rd32(b + 12)), n_drives(rd32(b + 16)),
+          n_packets(rd32(b + 20)), n_pruned(rd32(b + 24)), report_crc(rd32(b + 28)), header_crc(rd32(b + CRC_AT)),
+          drives_off(rd64(b + 32)), table_off(rd64(b + 40)), table_len(rd64(b + 48)), report_off(rd64(b + 56)),
+          report_len(rd64(b + 64)), file_size(rd64(b + 72)), actual(size) {}
+};
+
+struct HeaderRule {
+    const char *what;
+    bool (*ok)(const ManifestHeader &);
+};
+const HeaderRule HEADER_RULES[] = {
+    {"not a tierlm manifest (magic)", [](const ManifestHeader &h) { return h.magic == MANIFEST_MAGIC; }},
+    {"store format version other than 2", [](const ManifestHeader &h) { return h.version == STORE_VERSION; }},
+    {"header or record size not 512 / 48", [](const ManifestHeader &h) { return h.fixed == FIXED && h.rec == REC_BYTES; }},
+    {"drive count outside 1..16", [](const ManifestHeader &h) { return h.n_drives >= 1 && h.n_drives <= MAX_DRIVES; }},
+    {"more than 2^24 packets", [](const ManifestHeader &h) { return h.n_packets <= MAX_PACKETS; }},
+    {"more pruned packets than packets", [](const ManifestHeader &h) { return h.n_pruned <= h.n_packets; }},
+    {"drive list not right after the header", [](const ManifestHeader &h) { return h.drives_off == FIXED; }},
+    {"packet table not right after the drive list",
+     [](const ManifestHeader &h) { return h.table_off == h.drives_off + (uint64_t)h.n_drives * DRIVE_BYTES; }},
+    {"packet table length not 48 bytes per packet",
+     [](const ManifestHeader &h) { return h.table_len == (uint64_t)h.n_packets * REC_BYTES; }},
+    {"report not right after the packet table",
+     [](const ManifestHeader &h) { return h.report_off == h.table_off + h.table_len; }},
+    {"report longer than 64 MiB", [](const ManifestHeader &h) { return h.report_len <= MAX_REPORT; }},
+    {"recorded file size disagrees with the sections or the file",
+     [](const ManifestHeader &h) { return h.file_size == h.report_off + h.report_len && h.file_size == h.actual; }},
+};
+
 int tlm_hip_manifest_load(const char *path, tlm_hip_manifest **out) {
     if (!path || !out) return tlmh_seterr(TLM_HIP_EINVAL, "manifest load: NULL argument");
     *out = nullptr;
     std::vector<uint8_t> raw;
     if (int rc = read_file(path, raw)) return rc;
     const uint8_t *b = raw.data();
-    const size_t size = raw.size();
-#define BAD(...) return tlmh_seterr(TLM_HIP_EFORMAT, __VA_ARGS__)
-    if (size < FIXED) BAD("manifest %s: truncated (%zu bytes)", path, size);
-    if (rd32(b) != MANIFEST_MAGIC) BAD("manifest %s: bad magic", path);
-    if (rd32(b + 4) != STORE_VERSION) BAD("manifest %s: version %u, this reader reads %u", path, rd32(b + 4), STORE_VERSION);
-    if (rd32(b + 8) != FIXED || rd32(b + 12) != REC_BYTES) BAD("manifest %s: unexpected header geometry", path);
-    const uint32_t n_drives = rd32(b + 16), n_packets = rd32(b + 20), n_pruned = rd32(b + 24);
-    if (n_drives < 1 || n_drives > MAX_DRIVES) BAD("manifest %s: n_drives %u", path, n_drives);
-    if (n_packets > MAX_PACKETS) BAD("manifest %s: n_packets %u too large", path, n_packets);
-    if (n_pruned > n_packets) BAD("manifest %s: n_pruned > n_packets", path);
-    const uint64_t drives_off = rd64(b + 32), table_off = rd64(b + 40), table_len = rd64(b + 48);
-    const uint64_t report_off = rd64(b + 56), report_len = rd64(b + 64), file_size = rd64(b + 72);
-    if (drives_off != FIXED || table_off != drives_off + (uint64_t)n_drives * DRIVE_BYTES ||
-        table_len != (uint64_t)n_packets * REC_BYTES || report_off != table_off + table_len ||
-        report_len > MAX_REPORT || file_size != report_off + report_len || file_size != size)
-        BAD("manifest %s: section bounds inconsistent with file size %zu", path, size);
-    const uint32_t hcrc = crc32c(crc32c(0, b, CRC_AT), b + FIXED, (size_t)n_drives * DRIVE_BYTES);
-    if (rd32(b + CRC_AT) != hcrc) BAD("manifest %s: header checksum mismatch", path);
-    uint8_t digest[32];
-    Sha256::digest(b + table_off, (size_t)table_len, digest);
-    if (memcmp(digest, b + 80, 32) != 0) BAD("manifest %s: packet table SHA-256 mismatch", path);
-    const uint32_t rcrc = report_len ? crc32c(0, b + report_off, (size_t)report_len) : 0;
-    if (rcrc != rd32(b + 28)) BAD("manifest %s: report checksum mismatch", path);
-    if (report_len && memchr(b + report_off, 0, (size_t)report_len)) BAD("manifest %s: NUL inside report", path);
+    if (raw.size() < FIXED)
+        return tlmh_seterr(TLM_HIP_EFORMAT, "%s: %zu bytes, shorter than a manifest header", path, raw.size());
+    const ManifestHeader h(b, raw.size());
+    for (const HeaderRule &r : HEADER_RULES)
+        if (!r.ok(h)) return tlmh_seterr(TLM_HIP_EFORMAT, "%s: %s", path, r.what);
 
-    tlm_hip_manifest *m = new tlm_hip_manifest;
+    /* integrity: header CRC32C (first 508 bytes, then the drive paths), table
+     * SHA-256 (stored at byte 80), report CRC32C and its text */
+    if (crc32c(crc32c(0, b, CRC_AT), b + FIXED, (size_t)h.n_drives * DRIVE_BYTES) != h.header_crc)
+        return tlmh_seterr(TLM_HIP_EFORMAT, "%s: header CRC32C does not match its contents", path);
+    uint8_t sha[32];
+    Sha256::digest(b + h.table_off, (size_t)h.table_len, sha);
+    if (memcmp(sha, b + 80, 32) != 0)
+        return tlmh_seterr(TLM_HIP_EFORMAT, "%s: packet table does not hash to the recorded SHA-256", path);
+    if ((h.report_len ? crc32c(0, b + h.report_off, (size_t)h.report_len) : 0u) != h.report_crc)
+        return tlmh_seterr(TLM_HIP_EFORMAT, "%s: report CRC32C does not match its text", path);
+    if (h.report_len && memchr(b + h.report_off, 0, (size_t)h.report_len))
+        return tlmh_seterr(TLM_HIP_EFORMAT, "%s: report text holds a NUL byte", path);
+
+    std::unique_ptr<tlm_hip_manifest> m(new tlm_hip_manifest);
     memcpy(m->table_sha256, b + 80, 32);
     memcpy(m->source_sha256, b + 112, 32);
     memcpy(m->name, b + 176, 64);
     memcpy(m->profile, b + 240, 16);
-    tlm_hip_model_geom &g = m->geom;   /* tlm_packet.c:535-548: arch, then 22 u32/f32 fields */
+    /* geometry (src/lib/tlm_packet.c:535-548): the architecture string, then
+     * u32 / f32 fields in this order */
+    tlm_hip_model_geom &g = m->geom;
     memcpy(g.arch, b + 256, 32);
-    const uint8_t *v = b + 256 + 32;
-    g.n_layers = rd32(v + 0); g.d_model = rd32(v + 4); g.n_heads = rd32(v + 8); g.n_kv_heads = rd32(v + 12);
-    g.head_dim = rd32(v + 16); g.vocab = rd32(v + 20); g.n_experts = rd32(v + 24); g.top_k = rd32(v + 28);
-    g.d_expert = rd32(v + 32); g.n_shared = rd32(v + 36); g.d_shared = rd32(v + 40); g.max_ctx = rd32(v + 44);
-    g.router = rd32(v + 48); g.rope_theta = rdf(v + 52); g.norm_eps = rdf(v + 56); g.routed_scale = rdf(v + 60);
-    g.mtp_layers = rd32(v + 64); g.rope_scale = rd32(v + 68); g.rope_factor = rdf(v + 72);
-    g.rope_beta_fast = rdf(v + 76); g.rope_beta_slow = rdf(v + 80); g.rope_orig_len = rd32(v + 84);
-    if (!str_ok(m->name, 64, false) || strchr(m->name, '/') || !strcmp(m->name, ".") || !strcmp(m->name, "..") ||
-        !str_ok(m->profile, 16, true) || !str_ok(g.arch, 32, true)) {
-        delete m;
-        BAD("manifest %s: bad store name or unterminated string", path);
+    struct Field {
+        uint32_t *u;
+        float *f;
+    };
+    const Field geom_fields[] = {
+        {&g.n_layers, nullptr}, {&g.d_model, nullptr}, {&g.n_heads, nullptr}, {&g.n_kv_heads, nullptr},
+        {&g.head_dim, nullptr}, {&g.vocab, nullptr}, {&g.n_experts, nullptr}, {&g.top_k, nullptr},
+        {&g.d_expert, nullptr}, {&g.n_shared, nullptr}, {&g.d_shared, nullptr}, {&g.max_ctx, nullptr},
+        {&g.router, nullptr}, {nullptr, &g.rope_theta}, {nullptr, &g.norm_eps}, {nullptr, &g.routed_scale},
+        {&g.mtp_layers, nullptr}, {&g.rope_scale, nullptr}, {nullptr, &g.rope_factor}, {nullptr, &g.rope_beta_fast},
+        {nullptr, &g.rope_beta_slow}, {&g.rope_orig_len, nullptr}};
+    const uint8_t *gp = b + 288;
+    for (const Field &f : geom_fields) {
+        if (f.u) *f.u = rd32(gp);
+        else *f.f = rdf(gp);
+        gp += 4;
     }
-    for (uint32_t i = 0; i < n_drives; i++) {
-        const char *d = (const char *)(b + drives_off + (size_t)i * DRIVE_BYTES);
-        if (!str_ok(d, DRIVE_BYTES, false)) {
-            delete m;
-            BAD("manifest %s: bad drive %u path", path, i);
-        }
-        m->drives.push_back(std::string(d) + "/" + m->name + ".tlmp");   /* tlm_packet.c:780-786 */
+    const bool name_ok = str_ok(m->name, 64, false) && !strchr(m->name, '/') && strcmp(m->name, ".") != 0 &&
+                         strcmp(m->name, "..") != 0;
+    if (!name_ok || !str_ok(m->profile, 16, true) || !str_ok(g.arch, 32, true))
+        return tlmh_seterr(TLM_HIP_EFORMAT, "%s: store name, profile or architecture is not a terminated string "
+                           "(or the name is a path)", path);
+    for (uint32_t i = 0; i < h.n_drives; i++) {
+        const char *dir = (const char *)(b + h.drives_off + (size_t)i * DRIVE_BYTES);
+        if (!str_ok(dir, DRIVE_BYTES, false))
+            return tlmh_seterr(TLM_HIP_EFORMAT, "%s: drive %u path is empty or unterminated", path, i);
+        m->drives.push_back(std::string(dir) + "/" + m->name + ".tlmp");   /* tlm_packet.c:780-786 */
     }
-    m->fd.assign(n_drives, -1);
-    m->n_pruned = n_pruned;
-    m->packets.resize(n_packets);
-    for (uint32_t i = 0; i < n_packets; i++) {   /* tlm_packet.c:565-578 */
-        const uint8_t *r = b + table_off + (size_t)i * REC_BYTES;
+    m->fd.assign(h.n_drives, -1);
+    m->n_pruned = h.n_pruned;
+    /* records (src/lib/tlm_packet.c:565-578): type u16, layer u16, id u32,
+     * drive u8, replica drive u8, flags u16, crc32c u32, offset u64, replica
+     * offset u64, total length u64, heat f32, 4 bytes spare */
+    m->packets.resize(h.n_packets);
+    for (uint32_t i = 0; i < h.n_packets; i++) {
+        const uint8_t *r = b + h.table_off + (size_t)i * REC_BYTES;
+        m->packets[i] = tlm_hip_packet_loc{};
         tlm_hip_packet_loc &l = m->packets[i];
         l.type = rd16(r);
         l.layer = rd16(r + 2);
@@ -305,12 +365,8 @@ int tlm_hip_manifest_load(const char *path, tlm_hip_manifest **out) {
         l.total_len = rd64(r + 32);
         l.heat = rdf(r + 40);
     }
-    if (int rc = validate_packets(m->packets, n_drives)) {
-        delete m;
-        return rc;
-    }
-#undef BAD
-    *out = m;
+    if (int rc = check_table(m->packets, h.n_drives)) return rc;
+    *out = m.release();
     return TLM_HIP_OK;
 }
 
@@ -332,8 +388,10 @@ const tlm_hip_packet_loc *tlm_hip_manifest_find(const tlm_hip_manifest *m, int t
     key.layer = (uint16_t)layer;
     key.id = id;
     auto it = std::lower_bound(m->packets.begin(), m->packets.end(), key,
-                               [](const tlm_hip_packet_loc &a, const tlm_hip_packet_loc &b) { return key_cmp(a, b) < 0; });
-    return it != m->packets.end() && key_cmp(*it, key) == 0 ? &*it : nullptr;
+                               [](const tlm_hip_packet_loc &a, const tlm_hip_packet_loc &b) {
+                                   return packet_key(a) < packet_key(b);
+                               });
+    return it != m->packets.end() && packet_key(*it) == packet_key(key) ? &*it : nullptr;
 }
 
 const char *tlm_hip_manifest_drive_path(const tlm_hip_manifest *m, int i) {

@@ -128,6 +128,10 @@ int tlm_hip_quantize_act(int kind, const float *x, int64_t n, void *dst, void *s
     return launch_quantize_act(kind, x, n, dst, (hipStream_t)stream);
 }
 
+int tlm_hip_stream_read(const void *p, size_t bytes, uint32_t *sink, void *stream) {
+    return launch_stream_read(p, bytes, sink, (hipStream_t)stream);
+}
+
 int tlm_hip_expf(const float *x, float *y, int64_t n, void *stream) {
     return launch_expf(x, y, n, (hipStream_t)stream);
 }

@@ -197,6 +197,7 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 /* ---- launchers (defined in the .hip files) ------------------------------ */
 int launch_quantize_act(int kind, const float *x, int64_t n, void *dst, hipStream_t s);
 int launch_expf(const float *x, float *y, int64_t n, hipStream_t s);
+int launch_stream_read(const void *p, size_t bytes, uint32_t *sink, hipStream_t s);
 int launch_matvec_plain(int dt, const void *W, size_t row_bytes, const void *act, float *y,
                         int64_t n, int64_t r0, int64_t r1, hipStream_t s);
 int launch_nan_fill(float *y, int64_t count, hipStream_t s);

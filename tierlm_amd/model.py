@@ -79,6 +79,21 @@ class Model:
         max_position_embeddings as tlm_kv_new caps it (src/lib/tlm_model.c:646-650)."""
         return lib.tlm_hip_model_kv_capacity(self.h)
 
+    def rewind(self, n):
+        """Keep the first n positions of the context (enqueued)."""
+        check(lib.tlm_hip_model_rewind(self.h, int(n)))
+
+    def decode(self, n):
+        """n greedy steps from the current position, enqueued (sync() waits)."""
+        check(lib.tlm_hip_model_decode(self.h, int(n)))
+
+    def sync(self):
+        check(lib.tlm_hip_model_sync(self.h))
+
+    def stream(self):
+        """the model's HIP stream handle (an int)"""
+        return lib.tlm_hip_model_stream(self.h)
+
     def routes(self):
         """The last step's routing: (ids, weights), each [n_layers, top_k] in
         rank order (what the reference's routing hook receives)."""
