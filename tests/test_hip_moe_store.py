@@ -42,7 +42,8 @@ def store_block(case, dev):
     blk = MoeBlock(D=case.D, de=case.de, E=case.E, k=case.k, expert_dt=case.expert_dt, ffn_norm=b.keep[0],
                    router_w=b.keep[1], expert_ptrs=[dummy.data_ptr()] * (3 * case.E), router_bias=b.keep[2],
                    mask=b.keep[3], ds=case.ds, shared_dt=case.shared_dt, shared=b.keep[4],
-                   shared_gate_inp=b.keep[5], device=dev)
+                   shared_gate_inp=b.keep[5], router=b.desc.router, routed_scale=b.desc.routed_scale,
+                   eps=b.desc.eps, device=dev)
     blk.keep.append(dummy)
     return blk
 
@@ -137,5 +138,100 @@ def test_budget_below_top_k_is_ebusy_and_leaves_h(hip, dev):
         torch.cuda.synchronize()
         assert torch.equal(h, h0)
         assert store.stats()["in_use"] == 0
+    finally:
+        store.close()
+
+
+def test_two_hints_prefetch_their_own_routes(hip, dev):
+    """Two lookahead hints in one call (tlm_model.c:988-991): each prefetches
+    the experts its own router picks on the block's input residual, so after
+    the loader drains both layers' routes are all hits."""
+    cases = [build_moe_case(D=512, de=256, E=32, k=4, ds=0, expert_dt=oracle.Q6_K, seed=120 + s, device=dev,
+                            weights="random_codes") for s in range(3)]
+    blocks = [store_block(c, dev) for c in cases]
+    store = open_store(cases, 40, 4)
+    try:
+        rng = np.random.default_rng(9)
+        h0 = rng.standard_normal(cases[0].D).astype(np.float32)
+        want = [c.host.run(h0, trace=True)[1].tolist() for c in cases]
+        assert want[1] != want[2]
+        h = torch.from_numpy(h0.copy()).to(dev)
+        ids, _ = blocks[0].step_store(store, 0, h, hints=[(blocks[1], 1, 4), (blocks[2], 2, 4)])
+        assert ids == want[0]
+        torch.cuda.synchronize()
+        store.settle()
+        before = store.stats()
+        assert before["prefetch_issued"] == 8
+        for layer in (1, 2):
+            rc, refs = store.acquire(layer, want[layer])
+            assert rc == 0
+            for j in range(4):
+                assert store.wait(refs, j) == 0
+                store.release(refs, j)
+        after = store.stats()
+        assert after["hits"] - before["hits"] == 8 and after["misses"] == before["misses"]
+    finally:
+        store.close()
+
+
+def test_hints_sharing_a_workspace_are_rejected(hip, dev):
+    """Routes are read back after all of them ran: a workspace shared by two
+    hints (or by a hint and the block) would hand both the last route."""
+    import ctypes as C
+    from tierlm_amd._lib import MoeDesc, MoeHint, lib
+    cases = two_layers(dev)
+    blocks = [store_block(c, dev) for c in cases]
+    store = open_store(cases, 16, 4)
+    try:
+        h = torch.randn(cases[0].D, device=dev)
+        dsc = MoeDesc.from_buffer_copy(blocks[1].desc)
+        ws = torch.empty(int(lib.tlm_hip_moe_workspace_bytes(C.byref(dsc))) + 4096, dtype=torch.uint8, device=dev)
+        ids, w = (C.c_int32 * 4)(), (C.c_float * 4)()
+        for off_a, off_b in ((0, 0), (0, 256)):
+            arr = (MoeHint * 2)(MoeHint(C.pointer(dsc), 1, C.c_void_p(ws.data_ptr() + off_a)),
+                                MoeHint(C.pointer(dsc), 0, C.c_void_p(ws.data_ptr() + off_b)))
+            rc = lib.tlm_hip_moe_layer_store(C.byref(blocks[0].desc), store.h, 0, C.c_void_p(h.data_ptr()), ids, w,
+                                             arr, 2, C.c_void_p(blocks[0].workspace.data_ptr()), None)
+            assert rc == -3
+        arr = (MoeHint * 1)(MoeHint(C.pointer(dsc), 1, C.c_void_p(blocks[0].workspace.data_ptr())))
+        rc = lib.tlm_hip_moe_layer_store(C.byref(blocks[0].desc), store.h, 0, C.c_void_p(h.data_ptr()), ids, w,
+                                         arr, 1, C.c_void_p(blocks[0].workspace.data_ptr()), None)
+        assert rc == -3
+        assert store.stats()["in_use"] == 0
+    finally:
+        store.close()
+
+
+@pytest.mark.parametrize("dt,router", [(oracle.Q4_K, 2), (oracle.Q5_K, 0)])
+def test_store_block_c5_shape(hip, dev, dt, router):
+    """The 94-layer D 4096 model's block: 128 experts top-8 of width 1536,
+    Q4_K or Q5_K (10.6 / 13.0 MB per expert), sigmoid + bias selection with a
+    routed scale or softmax + renormalise, through a 24-slot cache (fewer
+    slots than experts, so tokens evict each other's experts) with a
+    lookahead hint - every token's ids, weights and residual bits equal the
+    oracle's block."""
+    bias = np.linspace(-0.05, 0.05, 128).astype(np.float32) if router == 2 else None
+    case = build_moe_case(D=4096, de=1536, E=128, k=8, ds=0, expert_dt=dt, seed=500 + router, device=dev,
+                          weights="random_codes", router=router, routed_scale=2.5 if router else 1.0,
+                          router_bias=bias)
+    blk = store_block(case, dev)
+    store = open_store([case], 24, 8)
+    rng = np.random.default_rng(router)
+    try:
+        for t in range(6):
+            h0 = (rng.standard_normal(case.D) * (1 + t % 3)).astype(np.float32)
+            want_h, want_ids, want_w, _ = case.host.run(h0, trace=True)
+            h = torch.from_numpy(h0.copy()).to(dev)
+            ids, w = blk.step_store(store, 0, h, hints=[(blk, 0, 8)])
+            store.tick()
+            assert ids == want_ids.tolist(), t
+            assert np.array_equal(np.asarray(w, np.float32).view(np.uint32),
+                                  np.asarray(want_w, np.float32).view(np.uint32)), t
+            got = h.cpu().numpy()
+            nd = int((got.view(np.uint32) != want_h.view(np.uint32)).sum())
+            assert nd == 0, f"token {t}: {nd} of {case.D} residual elements differ from the oracle"
+        store.settle()
+        st = store.stats()
+        assert st["misses"] > 0 and st["evictions"] > 0 and st["in_use"] == 0
     finally:
         store.close()

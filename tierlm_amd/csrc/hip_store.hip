@@ -246,42 +246,69 @@ struct tlm_hip_store {
         for (int v = 0; v < n_slots; v++) refresh(v);
     }
 
-    int pick_victim(int kind) const {           /* tlm_store.c:196-214 */
-        int best = -1;
-        uint32_t bf = 0;
-        uint64_t bl = 0;
-        for (int i = 0; i < n_slots; i++) {
-            const Slot &s = sl[i];
-            if (s.refs > 0 || s.pinned) continue;
-            if (s.state == S_FREE) return i;
-            if (s.state != S_READY) continue;
-            uint32_t f = ex[s.ex].freq;
-            if (kind == K_HINT && f > 0) continue;
-            if (best < 0 || f < bf || (f == bf && s.last < bl)) {
-                best = i;
-                bf = f;
-                bl = s.last;
+    /* Victim choice (the rule of tlm_store.c:196-214): among slots that are
+     * neither referenced nor pinned, the smallest eviction key - a FREE slot
+     * before any READY one, then the lower decayed selection count, then the
+     * older last use, then the lower slot index; a LOADING slot never
+     * qualifies, and a hint takes only FREE slots or READY slots whose count
+     * has decayed to 0.  -1 if nothing qualifies. */
+    struct EvictKey {
+        int busy;           /* 0 FREE, 1 READY */
+        uint32_t freq;
+        uint64_t last;
+        int slot;
+        bool operator<(const EvictKey &o) const {
+            if (busy != o.busy) return busy < o.busy;
+            if (freq != o.freq) return freq < o.freq;
+            if (last != o.last) return last < o.last;
+            return slot < o.slot;
+        }
+    };
+    bool evictable(int v, int kind, EvictKey *key) const {
+        const Slot &s = sl[v];
+        if (s.refs > 0 || s.pinned || s.state == S_LOADING) return false;
+        const bool free_slot = s.state == S_FREE;
+        const uint32_t f = free_slot ? 0u : ex[s.ex].freq;
+        if (!free_slot && kind == K_HINT && f > 0) return false;
+        *key = EvictKey{free_slot ? 0 : 1, free_slot ? 0u : f, free_slot ? 0ull : s.last, v};
+        return true;
+    }
+    int pick_victim(int kind) const {
+        bool any = false;
+        EvictKey best{};
+        for (int v = 0; v < n_slots; v++) {
+            EvictKey k;
+            if (evictable(v, kind, &k) && (!any || k < best)) {
+                best = k;
+                any = true;
+                if (k.busy == 0) break;   /* nothing beats the first FREE slot */
             }
         }
-        return best;
+        return any ? best.slot : -1;
     }
 
-    void take_ref(int v, uint64_t stamp, tlm_hip_expert_ref *r) {   /* tlm_store.c:216-234 */
-        Slot &s = sl[v];
-        s.refs++;
-        s.last = stamp;
-        if (s.hinted) {
-            s.hinted = 0;
-            st.prefetch_used++;
-        }
-        if (s.state == S_LOADING && !s.demand) {
-            s.demand = 1;
-            hint_loading--;
-            demand_loading++;
-        }
+    /* where slot v's expert matrices sit */
+    void describe(int v, tlm_hip_expert_ref *r) const {
         r->slot = v;
-        const Expert &x = ex[s.ex];
+        const Expert &x = ex[sl[v].ex];
         for (int m = 0; m < 3; m++) r->mats[m] = arena + (size_t)v * slot_bytes + x.off[m];
+    }
+    /* A step takes slot v (its expert is resident or on its way): one more
+     * reference, last use now; a hinted expert counts as a used prefetch
+     * once, and a hint still loading becomes demand traffic (the rules of
+     * tlm_store.c:216-234). */
+    void attach(int v, uint64_t stamp, tlm_hip_expert_ref *r) {
+        Slot &s = sl[v];
+        s.refs += 1;
+        s.last = stamp;
+        st.prefetch_used += s.hinted ? 1 : 0;
+        s.hinted = 0;
+        if (s.state == S_LOADING && s.demand == 0) {
+            s.demand = 1;
+            hint_loading -= 1;
+            demand_loading += 1;
+        }
+        describe(v, r);
     }
 
     void drop_ref(int v) {                      /* tlm_store.c:236-246 */
@@ -563,110 +590,125 @@ void tlm_hip_store_close(tlm_hip_store *s) {
 int tlm_hip_store_n_slots(const tlm_hip_store *s) { return s ? s->n_slots : 0; }
 uint64_t tlm_hip_store_slot_bytes(const tlm_hip_store *s) { return s ? s->slot_bytes : 0; }
 
-/* tlm_store.c:525-583 */
-int tlm_hip_store_warm(tlm_hip_store *s) {
-    if (!s) return tlmh_seterr(TLM_HIP_EINVAL, "store warm: NULL");
-    if (s->n_slots == 0) return TLM_HIP_OK;
-    double frac = s->o.pin_frac;
-    if (!(frac > 0.0)) return TLM_HIP_OK;
-    if (frac > 0.9) frac = 0.9;
-    int target = (int)floor(frac * s->n_slots);
-    if (target > s->n_slots - 1) target = s->n_slots - 1;
-    if (target <= 0) return TLM_HIP_OK;
-    std::unique_lock<std::mutex> lk(s->mu);
+/* Pinning at start (the rules of tlm_store.c:525-583): a pin budget of
+ * floor(min(pin_frac, 0.9) x slots), never all of them; candidates are the
+ * experts the compiler flagged, or with heat or a sidecar count, in
+ * pin_before order; a resident candidate is pinned where it is, any other is
+ * loaded into a victim slot as a pin; the call returns once its own loads
+ * have finished. */
+static int pin_budget(const tlm_hip_store *s) {
+    const double frac = s->o.pin_frac > 0.9 ? 0.9 : s->o.pin_frac;
+    if (!(frac > 0.0)) return 0;
+    const int want = (int)floor(frac * s->n_slots);
+    return std::max(0, std::min(want, s->n_slots - 1));
+}
+
+static std::vector<PinCand> pin_candidates(const tlm_hip_store *s) {
     std::vector<PinCand> c;
     for (int i = 0; i < (int)s->ex.size(); i++) {
         const tlm_hip_expert_src &x = s->ex[i].src;
-        const int cp = (x.flags & 1u) != 0;
-        if (!cp && !(x.heat > 0.0f) && x.seed == 0) continue;
-        c.push_back(PinCand{i, cp, x.heat, x.seed, x.layer, x.id});
+        const PinCand pc{i, (x.flags & 1u) ? 1 : 0, x.heat, x.seed, x.layer, x.id};
+        if (pc.cp || pc.heat > 0.0f || pc.seed != 0) c.push_back(pc);
     }
     std::stable_sort(c.begin(), c.end(), pin_before);
-    int pinned = s->n_pinned, rc = TLM_HIP_OK;
-    std::vector<int> mine;
-    for (size_t i = 0; i < c.size() && pinned < target; i++) {
-        int e = c[i].e, v = s->ex[e].slot;
-        if (v >= 0) {
-            if (!s->sl[v].pinned) {
-                s->sl[v].pinned = 1;
+    return c;
+}
+
+/* block until a slot this call started loading has left LOADING */
+static void settle_slot(tlm_hip_store *s, std::unique_lock<std::mutex> &lk, int v) {
+    Slot &sl = s->sl[v];
+    while (sl.state == S_LOADING) {
+        if (!sl.submitted) {
+            s->cv.wait(lk);
+            continue;
+        }
+        hipEvent_t ev = sl.loaded;
+        lk.unlock();
+        (void)hipEventSynchronize(ev);
+        lk.lock();
+        s->refresh(v);
+    }
+}
+
+int tlm_hip_store_warm(tlm_hip_store *s) {
+    if (!s) return tlmh_seterr(TLM_HIP_EINVAL, "store warm: NULL");
+    const int budget = s->n_slots ? pin_budget(s) : 0;
+    if (budget <= 0) return TLM_HIP_OK;
+    std::unique_lock<std::mutex> lk(s->mu);
+    const std::vector<PinCand> cand = pin_candidates(s);
+    std::vector<int> started;
+    /* start_load counts a pin load in n_pinned at once, as pinning in place does */
+    for (size_t i = 0; i < cand.size() && s->n_pinned < budget; i++) {
+        const int e = cand[i].e, resident = s->ex[e].slot;
+        if (resident >= 0) {
+            if (!s->sl[resident].pinned) {
+                s->sl[resident].pinned = 1;
                 s->n_pinned++;
-                pinned++;
             }
             continue;
         }
-        v = s->pick_victim(K_PIN);
+        const int v = s->pick_victim(K_PIN);
         if (v < 0) break;
         s->start_load(v, e, K_PIN);
-        mine.push_back(v);
-        pinned++;
+        started.push_back(v);
     }
-    for (int v : mine) {
-        Slot &sl = s->sl[v];
-        while (sl.state == S_LOADING) {
-            if (!sl.submitted) {
-                s->cv.wait(lk);
-                continue;
-            }
-            hipEvent_t ev = sl.loaded;
-            lk.unlock();
-            (void)hipEventSynchronize(ev);
-            lk.lock();
-            s->refresh(v);
+    int rc = TLM_HIP_OK;
+    for (int v : started) {
+        settle_slot(s, lk, v);
+        if (s->sl[v].state != S_READY && rc == TLM_HIP_OK) {
+            const int err = s->sl[v].err ? s->sl[v].err : TLM_HIP_EIO;
+            rc = tlmh_seterr(err, "store warm: a slot chosen for pinning ended without its expert");
         }
-        if (sl.state != S_READY && rc == TLM_HIP_OK)
-            rc = tlmh_seterr(sl.err ? sl.err : TLM_HIP_EIO, "store warm: pinned expert failed to load");
         s->drop_ref(v);
     }
     return rc;
 }
 
-/* tlm_store.c:586-640 */
+/* One step's experts of a layer (the rules of tlm_store.c:586-640): every
+ * known id is counted as selected; then a pass over the resident experts
+ * references them, so that no miss of this step can evict them; then the
+ * misses in rank order take victims and start loading (an id repeated in the
+ * step finds the slot its first occurrence took). */
 int tlm_hip_store_acquire(tlm_hip_store *s, int layer, const int *ids, int k, tlm_hip_expert_ref *out) {
     if (!s || k < 0 || (k > 0 && (!ids || !out))) return tlmh_seterr(TLM_HIP_EINVAL, "store acquire: bad arguments");
-    int rc = TLM_HIP_OK;
     std::unique_lock<std::mutex> lk(s->mu);
     s->refresh_all();
     const uint64_t stamp = ++s->clock;
+    int rc = TLM_HIP_OK;
+    std::vector<int> exp_of(k);
     for (int i = 0; i < k; i++) {
+        out[i] = tlm_hip_expert_ref{};
         out[i].slot = -1;
-        out[i].mats[0] = out[i].mats[1] = out[i].mats[2] = nullptr;
-        const int e = s->find(layer, ids[i]);
-        if (e < 0) {
+        exp_of[i] = s->find(layer, ids[i]);
+        if (exp_of[i] < 0) {
             if (rc == TLM_HIP_OK)
-                rc = tlmh_seterr(TLM_HIP_ENOTFOUND, "store: layer %d expert %d has no packet (absent or pruned)",
-                                 layer, ids[i]);
-            continue;
+                rc = tlmh_seterr(TLM_HIP_ENOTFOUND, "store acquire: no routable expert %d in layer %d", ids[i], layer);
+        } else if (s->ex[exp_of[i]].freq != UINT32_MAX) {
+            s->ex[exp_of[i]].freq += 1;
         }
-        if (s->ex[e].freq < UINT32_MAX) s->ex[e].freq++;
     }
-    for (int i = 0; i < k; i++) {   /* hits first: a miss never evicts this step's hit */
-        const int e = s->find(layer, ids[i]);
-        if (e < 0 || s->ex[e].slot < 0) continue;
-        s->take_ref(s->ex[e].slot, stamp, &out[i]);
-        s->st.hits++;
-    }
-    for (int i = 0; i < k; i++) {
-        if (out[i].slot >= 0) continue;
-        const int e = s->find(layer, ids[i]);
-        if (e < 0) continue;
-        if (s->ex[e].slot >= 0) {   /* repeated id, placed earlier in this pass */
-            s->take_ref(s->ex[e].slot, stamp, &out[i]);
-            s->st.hits++;
-            continue;
+    for (int pass = 0; pass < 2; pass++) {   /* 0: resident experts, 1: everything still missing */
+        for (int i = 0; i < k; i++) {
+            const int e = exp_of[i];
+            if (e < 0 || out[i].slot >= 0) continue;
+            if (s->ex[e].slot >= 0) {
+                s->attach(s->ex[e].slot, stamp, &out[i]);
+                s->st.hits++;
+                continue;
+            }
+            if (pass == 0) continue;
+            int v = s->pick_victim(K_DEMAND);
+            while (v < 0 && s->wait_unreferenced_load(lk)) v = s->pick_victim(K_DEMAND);
+            if (v < 0) {
+                if (rc == TLM_HIP_OK)
+                    rc = tlmh_seterr(TLM_HIP_EBUSY, "store acquire: none of the %d slots is free to evict (each is "
+                                     "referenced or pinned); keep top_k slots unpinned", s->n_slots);
+                continue;
+            }
+            s->st.misses++;
+            s->start_load(v, e, K_DEMAND);
+            s->describe(v, &out[i]);
         }
-        int v = s->pick_victim(K_DEMAND);
-        while (v < 0 && s->wait_unreferenced_load(lk)) v = s->pick_victim(K_DEMAND);
-        if (v < 0) {
-            if (rc == TLM_HIP_OK)
-                rc = tlmh_seterr(TLM_HIP_EBUSY, "store: all %d slots are referenced or pinned; the slot budget "
-                                 "must hold at least top_k unpinned slots", s->n_slots);
-            continue;
-        }
-        s->st.misses++;
-        s->start_load(v, e, K_DEMAND);
-        const Expert &x = s->ex[e];
-        out[i].slot = v;
-        for (int m = 0; m < 3; m++) out[i].mats[m] = s->arena + (size_t)v * s->slot_bytes + x.off[m];
     }
     return rc;
 }
@@ -747,21 +789,24 @@ void tlm_hip_store_release(tlm_hip_store *s, tlm_hip_expert_ref *ref, void *stre
     ref->mats[0] = ref->mats[1] = ref->mats[2] = nullptr;
 }
 
-/* tlm_store.c:694-718 */
+/* Lookahead hints (the rules of tlm_store.c:694-718): an expert not yet
+ * resident is loaded ahead only while at most HINT_BACKLOG demand loads are
+ * in flight and fewer hints than the hint budget (slots minus pins minus the
+ * top_k reserve, at most HINT_INFLIGHT) are, and only into a slot a hint may
+ * take (pick_victim); otherwise the hint is dropped and counted. */
+static bool hint_admitted(const tlm_hip_store *s) {
+    const int budget = std::min(HINT_INFLIGHT, s->n_slots - s->n_pinned - s->reserve);
+    return s->demand_loading <= HINT_BACKLOG && s->hint_loading < budget;
+}
+
 void tlm_hip_store_prefetch(tlm_hip_store *s, int layer, const int *ids, int k) {
     if (!s || !s->o.prefetch || !ids || k <= 0) return;
     std::lock_guard<std::mutex> lk(s->mu);
     s->refresh_all();
-    int cap = s->n_slots - s->n_pinned - s->reserve;
-    if (cap > HINT_INFLIGHT) cap = HINT_INFLIGHT;
     for (int i = 0; i < k; i++) {
         const int e = s->find(layer, ids[i]);
-        if (e < 0 || s->ex[e].slot >= 0) continue;
-        if (s->demand_loading > HINT_BACKLOG || s->hint_loading >= cap) {
-            s->st.prefetch_dropped++;
-            continue;
-        }
-        const int v = s->pick_victim(K_HINT);
+        if (e < 0 || s->ex[e].slot >= 0) continue;   /* unknown, or resident / already loading */
+        const int v = hint_admitted(s) ? s->pick_victim(K_HINT) : -1;
         if (v < 0) {
             s->st.prefetch_dropped++;
             continue;
@@ -771,12 +816,14 @@ void tlm_hip_store_prefetch(tlm_hip_store *s, int layer, const int *ids, int k) 
     }
 }
 
-/* tlm_store.c:720-726 */
+/* One step of time (tlm_store.c:720-726): every DECAY_TICKS ticks the
+ * selection counts halve, so old popularity fades. */
 void tlm_hip_store_tick(tlm_hip_store *s) {
     if (!s) return;
     std::lock_guard<std::mutex> lk(s->mu);
-    if (++s->ticks % DECAY_TICKS == 0)
-        for (Expert &x : s->ex) x.freq >>= 1;
+    s->ticks += 1;
+    if (s->ticks % DECAY_TICKS != 0) return;
+    for (Expert &x : s->ex) x.freq /= 2;
 }
 
 /* Every queued load submitted and finished (READY or failed). */
@@ -850,9 +897,23 @@ int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int lay
     if (!d || !s || !h || !workspace || n_hints < 0 || n_hints > MAX_HINTS || (n_hints > 0 && !hints))
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: bad arguments");
     if (d->k <= 0 || d->k > MOE_MAXK) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: k=%d", d->k);
-    for (int i = 0; i < n_hints; i++)
-        if (!hints[i].desc || !hints[i].workspace || hints[i].workspace == workspace)
-            return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: hint %d needs its own descriptor and workspace", i);
+    /* each route lands in its own workspace until one export reads them all:
+     * no two of them (the block's, the hints') may share a byte */
+    const uint8_t *lo[1 + MAX_HINTS];
+    size_t len[1 + MAX_HINTS];
+    lo[0] = (const uint8_t *)workspace;
+    len[0] = moe_workspace_bytes(d);
+    for (int i = 0; i < n_hints; i++) {
+        if (!hints[i].desc || !hints[i].workspace)
+            return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: hint %d has no descriptor or workspace", i);
+        lo[1 + i] = (const uint8_t *)hints[i].workspace;
+        len[1 + i] = moe_workspace_bytes(hints[i].desc);
+    }
+    for (int a = 0; a <= n_hints; a++)
+        for (int b = a + 1; b <= n_hints; b++)
+            if (lo[a] < lo[b] + len[b] && lo[b] < lo[a] + len[a])
+                return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: %s%d and hint %d share workspace bytes",
+                                   a ? "hint " : "the block's workspace ", a ? a - 1 : 0, b - 1);
     hipStream_t st = (hipStream_t)stream;
     /* every route first (the hints read the same residual, before this
      * block's update), then one round trip for all of them */

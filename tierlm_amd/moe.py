@@ -89,7 +89,9 @@ class MoeBlock:
             for i, (blk, hl, hk) in enumerate(hints):
                 dsc = MoeDesc.from_buffer_copy(blk.desc)
                 dsc.k = hk
-                ws = blk._hint_ws(dsc)
+                # one workspace per hint: each route is read back after all of them ran
+                ws = torch.empty(int(lib.tlm_hip_moe_workspace_bytes(C.byref(dsc))), dtype=torch.uint8,
+                                 device=self.workspace.device)
                 keep.append((blk, dsc, ws))
                 arr[i] = MoeHint(C.pointer(dsc), hl, C.c_void_p(ws.data_ptr()))
             cache[key] = (arr, keep)
@@ -100,13 +102,6 @@ class MoeBlock:
         check(lib.tlm_hip_moe_layer_store(C.byref(self.desc), store.h, layer, C.c_void_p(h.data_ptr()), ids, w, arr,
                                           n, C.c_void_p(self.workspace.data_ptr()), stream()))
         return list(ids), list(w)
-
-    def _hint_ws(self, dsc):
-        """the workspace this block's router uses when it predicts for a hint"""
-        nbytes = int(lib.tlm_hip_moe_workspace_bytes(C.byref(dsc)))
-        if getattr(self, "_hws", None) is None or self._hws.numel() < nbytes:
-            self._hws = torch.empty(nbytes, dtype=torch.uint8, device=self.workspace.device)
-        return self._hws
 
     def set_expert_ptrs(self, expert_ptrs):
         """Point the block at another set of packed experts (same geometry)."""
