@@ -403,8 +403,13 @@ typedef struct {
     int32_t eager;       /* 1: launch each step's kernels directly; 0: replay the step as a HIP graph
                             captured at first use (the position and tokens live in device memory) */
     int32_t attn_slices; /* attention slices per key head; 0 = automatic (enough groups to cover the
-                            chip at long contexts); 1 = one group per key head, which stores the
-                            output itself */
+                            chip at long contexts) */
+    int32_t attn_split;  /* 0: attn_heads' order of operations (src/lib/tlm_model.c:683-719), the
+                            reference's bits: one serial P.V chain per output element;
+                            1: split attention - softmax and P.V partials per slice of positions,
+                            merged per query head: each attention output within float rounding of
+                            the reference's, but not its bits, and the int8 activation codes and
+                            top-k routing downstream turn such differences into larger ones */
 } tlm_hip_model_opts;
 int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
 void tlm_hip_model_close(tlm_hip_model *M);

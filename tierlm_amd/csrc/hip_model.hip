@@ -61,17 +61,21 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
  * score - the dot in ascending i, scaled after the dot - with the slice's
  * maximum per query head; the group whose slice holds the new position
  * appends its key and value to the cache.
- * k_attn_pv: a group per QPG query heads.  The softmax in the reference's
- * order - the maximum over the slice maxima, e_t = e^(s_t - max), their sum in
- * double, inv = 1 / sum, p_t = e_t * inv (probabilities in LDS) - then the
- * P.V sums: one lane per output element runs the reference's chain
- * out += p_t * v_t[i] over ascending t, one wave per 64 elements, so that
- * each SIMD holds one chain wave.  V streams into registers three blocks of
- * ATT_PD positions ahead: a wave can have at most 63 loads outstanding, so a
- * load must bring each lane several positions - the value cache is kept in
- * tiles of 4 positions, element-major inside (V[t][i] at
- * ((t / 4) * HD + i) * 4 + t % 4), where one 16-byte lane load is positions
- * 4j..4j+3 of element i and a wave's load is 1 KB contiguous.
+ * k_attn_pv: a group per (query head, 64 output elements).  All four waves
+ * run the softmax in the reference's order - the maximum over the slice
+ * maxima, e_t = e^(s_t - max), their sum in double, inv = 1 / sum, p_t = e_t *
+ * inv (probabilities in LDS) - then the P.V sums out += p_t * v_t[i] over
+ * ascending t: wave 0 holds one chain per lane and only adds, one dependent
+ * add per position (about 4.5 clocks); waves 1-3 form the products p_t v_t[i]
+ * (the reference's rounded products) into a ring of three LDS blocks of
+ * ATT_BT value tiles, two blocks ahead of the chains, with the value tiles
+ * ATT_VPF blocks ahead in registers; one barrier per block.  A chain wave that
+ * also formed its products issued a multiply and an add per position, and
+ * one that read its values from memory as well shared the CU's load
+ * bandwidth with three others: both ran at 9-10 ns per position against 5
+ * now.  The value cache is kept in tiles of 4 positions, element-major inside
+ * (V[t][i] at ((t / 4) * HD + i) * 4 + t % 4), where one 16-byte lane load is
+ * positions 4j..4j+3 of element i and a wave's load is 1 KB contiguous.
  *
  * Numerics: the scores, maxima, products and chains are the reference's
  * operations in its order; the double sum of the softmax terms is a tree
@@ -88,7 +92,9 @@ constexpr int ATT_CH = 32;       /* positions per LDS chunk of the scores */
 constexpr int ATT_LMIN = 32;     /* shortest slice */
 constexpr int ATT_QMAX = 4096;   /* query values per key head (query heads per key head x HD) */
 constexpr int ATT_GMAX = 128;    /* slices per key head */
-constexpr int ATT_PD = 64;       /* V positions per register block of a chain (three in flight) */
+constexpr int ATT_PSEG = 4096;   /* probabilities per LDS segment of k_attn_pv */
+constexpr int ATT_BT = 24;       /* value tiles (4 positions each) per block of k_attn_pv's product ring */
+constexpr int ATT_VPF = 3;       /* blocks of value tiles k_attn_pv's producers hold in flight (a multiple of 3) */
 
 /* floats of value cache per key head: whole 4-position tiles */
 __host__ __device__ inline size_t att_vstride(int max_ctx, int hd) { return (size_t)((max_ctx + 3) & ~3) * hd; }
@@ -312,146 +318,527 @@ template <int HD>
 __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ smax,
                                                 const float *__restrict__ vc, float *__restrict__ att, int H, int KV,
                                                 int max_ctx, int G, const int32_t *__restrict__ st) {
-    constexpr int NWC = (HD + 63) / 64;          /* chain waves per query head */
-    constexpr int QPG = NWC <= 4 ? 4 / NWC : 1;  /* query heads per group */
-    constexpr int TPH = NT / QPG;                /* threads per head in the softmax */
-    constexpr int PSEG = 8192 / QPG / (3 * ATT_PD) * (3 * ATT_PD);   /* probabilities per head in LDS */
-    constexpr int PB = 8;                        /* score loads per thread per round */
-    constexpr int GM = ATT_GMAX / 64;            /* slice maxima per lane */
-    __shared__ __align__(16) float s_p[QPG][PSEG + ATT_PD];
+    constexpr int NWC = (HD + 63) / 64;   /* 64-element slabs per query head, a group each */
+    constexpr int PB = 8;                 /* score loads per thread per round */
+    constexpr int GM = ATT_GMAX / 64;     /* slice maxima per lane */
+    constexpr int NPW = NT / 64 - 1;      /* producer waves */
+    constexpr int TPP = ATT_BT / NPW;     /* tiles per producer per block */
+    static_assert(ATT_BT % NPW == 0, "a block's tiles split evenly over the producers");
+    __shared__ __align__(16) float s_p[ATT_PSEG];
+    __shared__ __align__(16) f32x4 s_prod[3][ATT_BT][64];   /* three blocks of products, tile-major */
     __shared__ double s_sum[NT / 64];
     const int pos = st[0], T = pos + 1, L = att_slice_len(T, G), ns = (T + L - 1) / L;
-    const int R = H / KV, gpk = (R + QPG - 1) / QPG;   /* groups per key head */
+    const int R = H / KV;
     /* block b: key head b mod KV (so b runs on an XCD of that key head's
-     * slices), its (b / KV)-th run of QPG query heads */
-    const int kvg = (int)blockIdx.x % KV, jg = (int)blockIdx.x / KV;
-    if (jg >= gpk) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h0 = kvg * R + jg * QPG, hend = kvg * R + R;
-    /* softmax role: head jj (a wave never straddles two), positions tt + TPH k */
-    const int jj = tid / TPH, tt = tid % TPH, hs = min(h0 + jj, hend - 1);
-    /* chain role: head jc, element ic */
-    const int jc = wave / NWC, hc = h0 + jc, ic = 64 * (wave % NWC) + lane;
-    const bool chain = jc < QPG && hc < hend;
-    const float *S = scores + (size_t)hs * max_ctx;
-    /* the chain lane's element: 16 bytes at lane_off of each tile (4
-     * positions); the tile's address is uniform, so a load needs no address
-     * registers of its own */
+     * slices, where k_attn_scores left its values), then (query head of the key
+     * head, slab) */
+    const int kvg = (int)blockIdx.x % KV, rest = (int)blockIdx.x / KV;
+    if (rest >= R * NWC) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = kvg * R + rest / NWC, ic = 64 * (rest % NWC) + lane;
+    const float *S = scores + (size_t)h * max_ctx;
     const char *vbase = (const char *)(vc + (size_t)kvg * att_vstride(max_ctx, HD));
-    const uint32_t lane_off = (uint32_t)min(ic, HD - 1) * 16u;
+    const uint32_t lane_off = (uint32_t)min(ic, HD - 1) * 16u;   /* element ic's 16 bytes of a tile */
     const int lastq = (T - 1) >> 2;
 
-    /* entry loads: the head's slice maxima, the first scores, the chain's first V block */
+    /* entry loads: the head's slice maxima, the first scores */
     float mm[GM];
 #pragma unroll
-    for (int k = 0; k < GM; k++) mm[k] = smax[(size_t)hs * G + min(lane + 64 * k, ns - 1)];
+    for (int k = 0; k < GM; k++) mm[k] = smax[(size_t)h * G + min(lane + 64 * k, ns - 1)];
     float sv[PB];
 #pragma unroll
-    for (int k = 0; k < PB; k++) sv[k] = S[min(tt + TPH * k, T - 1)];
-    constexpr int PQ = ATT_PD / 4;   /* 16-byte loads per block */
-    f32x4 va[PQ], vb[PQ], vc3[PQ];
-    auto vld = [&](int t0, f32x4 (&r)[PQ]) {   /* t0 a multiple of 4; tiles clamped to the context */
-#pragma unroll
-        for (int u = 0; u < PQ; u++) {
-            const int tq = min((t0 >> 2) + u, lastq);
-            r[u] = *(const f32x4 *)(vbase + (size_t)tq * (HD * 16) + lane_off);
-        }
-    };
-    if (chain) {
-        vld(0, va);
-        if (ATT_PD < T) vld(ATT_PD, vb);
-    }
+    for (int k = 0; k < PB; k++) sv[k] = S[min(tid + NT * k, T - 1)];
 
     float mx = -INFINITY;   /* the reference's maximum: NaN never compares greater */
 #pragma unroll
     for (int k = 0; k < GM; k++) mx = mm[k] > mx ? mm[k] : mx;
     mx = wave_max_f32(mx);
-    const int nseg = (T + PSEG - 1) / PSEG;
-    float *prow = s_p[jj];
+    const int nseg = (T + ATT_PSEG - 1) / ATT_PSEG;
     double sum = 0.0;
-    for (int b0 = 0; b0 < T; b0 += PB * TPH) {   /* e_t and their sum (tlm_model.c:704-709) */
+    for (int b0 = 0; b0 < T; b0 += PB * NT) {   /* e_t and their sum (tlm_model.c:704-709) */
         if (b0 > 0) {
 #pragma unroll
-            for (int k = 0; k < PB; k++) sv[k] = S[min(b0 + tt + TPH * k, T - 1)];
+            for (int k = 0; k < PB; k++) sv[k] = S[min(b0 + tid + NT * k, T - 1)];
         }
 #pragma unroll
         for (int k = 0; k < PB; k++) {   /* every lane computes; past the context it adds 0, stores nothing */
-            const int t = b0 + tt + TPH * k;
+            const int t = b0 + tid + NT * k;
             const float e = expf_ref(sv[k] - mx);
             sum += t < T ? (double)e : 0.0;
-            if (nseg == 1 && t < T) prow[t] = e;
+            if (nseg == 1 && t < T) s_p[t] = e;
         }
     }
     sum = wave_sum_f64(sum);
     if (lane == 0) s_sum[wave] = sum;
     __syncthreads();
-    auto inv_of = [&](int j) {
-        double s = 0.0;
-        for (int w = j * (TPH / 64); w < (j + 1) * (TPH / 64); w++) s += s_sum[w];
-        return (float)(1.0 / s);
-    };
-    const float inv_s = inv_of(jj);
+    double tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) tot += s_sum[w];
+    const float inv_s = (float)(1.0 / tot);
+
+    /* P.V: wave 0 runs the chains out += p_t v_t[i] (one lane per element,
+     * ascending t); waves 1..NPW form the products p_t v_t[i] - the
+     * reference's rounded products - into a ring of three LDS blocks of
+     * ATT_BT tiles, two blocks ahead of the chains, with their value tiles
+     * three blocks ahead in registers.  Products past the segment are +0, and
+     * adding +0 leaves the chain unchanged (it starts at +0 and never holds
+     * -0), so the chains run whole blocks. */
+    const int pw = wave - 1;
     float acc = 0.0f;
-    for (int sb = 0; sb < T; sb += PSEG) {   /* uniform over the group */
-        const int se = min(T, sb + PSEG);
+    f32x4 vq[ATT_VPF][TPP];   /* producers: value tiles of ATT_VPF blocks */
+    for (int sb = 0; sb < T; sb += ATT_PSEG) {   /* uniform over the group */
+        const int se = min(T, sb + ATT_PSEG);
         if (nseg == 1) {   /* each thread scales the terms it stored: p = e * inv */
-            for (int t = tt; t < T; t += TPH) prow[t] = prow[t] * inv_s;
+            for (int t = tid; t < T; t += NT) s_p[t] = s_p[t] * inv_s;
         } else {
-            for (int t = sb + tt; t < se; t += TPH) prow[t - sb] = expf_ref(S[t] - mx) * inv_s;
+            for (int t = sb + tid; t < se; t += NT) s_p[t - sb] = expf_ref(S[t] - mx) * inv_s;
+        }
+        const int nbk = (se - sb + ATT_BT * 4 - 1) / (ATT_BT * 4);   /* blocks of the segment */
+        const int q0 = sb >> 2;   /* the segment's first tile */
+        /* producers: tiles pw * TPP .. + TPP - 1 of each block; a tile's
+         * address is uniform, the lane adds its element's 16 bytes */
+        auto vload = [&](int blk, f32x4 (&r)[TPP]) {
+#pragma unroll
+            for (int u = 0; u < TPP; u++) {
+                const int tq = min(q0 + blk * ATT_BT + pw * TPP + u, lastq);
+                r[u] = *(const f32x4 *)(vbase + (size_t)tq * (HD * 16) + lane_off);
+            }
+        };
+        /* the probabilities of a producer's tiles of block blk (uniform LDS
+         * reads), read a block ahead of their use */
+        auto pread = [&](int blk, f32x4 (&p)[TPP]) {
+            const f32x4 *p4 = (const f32x4 *)s_p + min(blk * ATT_BT + pw * TPP, ATT_PSEG / 4 - TPP);
+#pragma unroll
+            for (int u = 0; u < TPP; u++) p[u] = p4[u];
+        };
+        auto produce = [&](int blk, const f32x4 (&p)[TPP], const f32x4 (&r)[TPP], int buf) {
+            const int tl0 = blk * ATT_BT + pw * TPP;   /* the producer's first tile in the segment */
+            f32x4 *dst = &s_prod[buf][pw * TPP][lane];
+            if (sb + 4 * (tl0 + TPP) <= se) {   /* uniform: the tiles lie inside the segment */
+#pragma unroll
+                for (int u = 0; u < TPP; u++) {
+                    f32x4 o;
+                    o.x = p[u].x * r[u].x;
+                    o.y = p[u].y * r[u].y;
+                    o.z = p[u].z * r[u].z;
+                    o.w = p[u].w * r[u].w;
+                    dst[u * 64] = o;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < TPP; u++) {
+                    const int t = sb + 4 * (tl0 + u);
+                    f32x4 o;
+                    o.x = t < se ? p[u].x * r[u].x : 0.0f;
+                    o.y = t + 1 < se ? p[u].y * r[u].y : 0.0f;
+                    o.z = t + 2 < se ? p[u].z * r[u].z : 0.0f;
+                    o.w = t + 3 < se ? p[u].w * r[u].w : 0.0f;
+                    dst[u * 64] = o;
+                }
+            }
+        };
+        /* the two roles run separate loops with the same barriers, so that
+         * neither's memory counters are merged with the other's path */
+        if (wave > 0) {
+#pragma unroll
+            for (int k = 0; k < ATT_VPF; k++) vload(k, vq[k]);
+            f32x4 pc[TPP];
+            __syncthreads();   /* the segment's probabilities */
+            pread(0, pc);
+            produce(0, pc, vq[0], 0);
+            vload(ATT_VPF, vq[0]);
+            pread(1, pc);
+            produce(1, pc, vq[1], 1);
+            vload(ATT_VPF + 1, vq[1]);
+            pread(2, pc);
+            __syncthreads();
+            for (int b = 0; b < nbk; b += ATT_VPF) {
+#pragma unroll
+                for (int k = 0; k < ATT_VPF; k++) {   /* block b + k + 2 into buffer (b + k + 2) mod 3 */
+                    if (b + k >= nbk) break;          /* uniform: the chain wave leaves at the same block */
+                    produce(b + k + 2, pc, vq[(k + 2) % ATT_VPF], (k + 2) % 3);
+                    vload(b + k + 2 + ATT_VPF, vq[(k + 2) % ATT_VPF]);
+                    pread(b + k + 3, pc);
+                    __syncthreads();
+                }
+            }
+        } else {
+            /* the chain reads a block in three parts, each one part ahead of
+             * its adds (the next block's first part during this block's last) */
+            constexpr int SUB = ATT_BT / 3;
+            __syncthreads();   /* the segment's probabilities */
+            __syncthreads();
+            f32x4 cur[SUB];
+#pragma unroll
+            for (int u = 0; u < SUB; u++) cur[u] = s_prod[0][u][lane];
+            for (int b = 0; b < nbk; b += ATT_VPF) {
+#pragma unroll
+                for (int k = 0; k < ATT_VPF; k++) {   /* block b + k from buffer (b + k) mod 3 */
+                    if (b + k >= nbk) break;
+#pragma unroll
+                    for (int c = 0; c < 3; c++) {
+                        f32x4 nx[SUB];
+#pragma unroll
+                        for (int u = 0; u < SUB; u++)
+                            nx[u] = c < 2 ? s_prod[k % 3][SUB * (c + 1) + u][lane] : s_prod[(k + 1) % 3][u][lane];
+#pragma unroll
+                        for (int u = 0; u < SUB; u++) {
+                            acc += cur[u].x;
+                            acc += cur[u].y;
+                            acc += cur[u].z;
+                            acc += cur[u].w;
+                        }
+#pragma unroll
+                        for (int u = 0; u < SUB; u++) cur[u] = nx[u];
+                    }
+                    __syncthreads();
+                }
+            }
+        }
+    }
+    if (wave == 0 && ic < HD) att[(size_t)h * HD + ic] = acc;
+}
+
+/* ---- split attention (attn_split): a partial softmax and P.V per (key
+ * head, slice of positions), merged per query head ---------------------------
+ * k_attn_split: one group per (key head, slice), as k_attn_scores: the query
+ * heads and the new key normalised and rotated, the slice's keys staged in
+ * LDS a chunk at a time, the scores (each dot as four interleaved partial
+ * sums) kept in LDS; then per query head j the slice maximum m_j, e_t =
+ * e^(s_t - m_j), l_j = sum_t e_t, and o_j[i] = sum_t e_t v_t[i] (thread (i,
+ * js) runs the heads j = js (mod NT / HD) of element i, fma chains over the
+ * slice's positions with the value tiles one chunk ahead in registers),
+ * stored as the slice's partials; the group holding the new position also
+ * appends its key and value.
+ * k_attn_merge: one group per query head: M = max_s m_s, w_s = e^(m_s - M),
+ * out[i] = (sum_s w_s o_s[i]) / (sum_s w_s l_s).
+ * The same quantity as attn_heads (src/lib/tlm_model.c:683-719) in another
+ * order of operations: within 1e-5 relative of the reference's outputs, not
+ * its bits (the exact order is k_attn_scores + k_attn_pv). */
+struct AttSplitLds {
+    int q, kn, vn, k, e, m, total;
+};
+__host__ __device__ inline AttSplitLds att_split_lds(int hd, int R, int lmax) {
+    AttSplitLds o;
+    o.q = 0;
+    o.kn = R * hd;
+    o.vn = o.kn + hd;
+    o.k = o.vn + hd;
+    o.e = o.k + ATT_CH * (hd + 4);
+    o.m = o.e + R * lmax;   /* lmax: a multiple of 16 */
+    o.total = o.m + R;
+    return o;
+}
+
+/* sum over the aligned 32 lanes of a half wave, uniform in it */
+__device__ __forceinline__ float half_sum_f32(float v) {
+    v += dpp_f32<DPP_XOR1>(v);
+    v += dpp_f32<DPP_XOR2>(v);
+    v += dpp_f32<DPP_HALF_MIRROR>(v);
+    v += dpp_f32<DPP_MIRROR>(v);
+    v += __shfl_xor(v, 16, 64);
+    return v;
+}
+
+template <int HD>
+__global__ __launch_bounds__(NT) void k_attn_split(const float *__restrict__ q, const float *__restrict__ kx,
+                                                   const float *__restrict__ vx, const float *__restrict__ q_norm,
+                                                   const float *__restrict__ k_norm, int has_qn, int has_kn,
+                                                   const float *__restrict__ cs_all, const float *__restrict__ sn_all,
+                                                   float *__restrict__ kc, float *__restrict__ vc,
+                                                   float *__restrict__ part_o, float *__restrict__ part_ml, int H,
+                                                   int KV, int max_ctx, int G, int lmax,
+                                                   const int32_t *__restrict__ st, float eps) {
+    constexpr int H4 = HD / 4, HALF = HD / 2, KS = HD + 4;
+    constexpr int CF = ATT_CH * H4 / NT;            /* float4 of a chunk's K per thread */
+    constexpr int QF = ATT_QMAX / 4 / NT;           /* float4 of the query heads per thread, at most */
+    constexpr int SU = ATT_QMAX / HD * ATT_CH / NT; /* (query head, position) items per thread per chunk, at most */
+    constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;   /* elements / pairs per lane */
+    constexpr int JS = NT / HD;                     /* threads per output element in the P.V */
+    constexpr int JK = ATT_QMAX / HD / JS;          /* query heads per P.V thread, at most */
+    constexpr int VQ = ATT_CH / 4;                  /* value tiles per chunk */
+    extern __shared__ __align__(16) float s_dyn[];
+    const int pos = st[0], T = pos + 1, R = H / KV;
+    const int L = att_slice_len(T, G), t0 = (int)blockIdx.y * L;
+    if (t0 >= T) return;
+    const int tn = min(L, T - t0), kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const AttSplitLds lo = att_split_lds(HD, R, lmax);
+    float *s_q = s_dyn + lo.q, *s_kn = s_dyn + lo.kn, *s_vn = s_dyn + lo.vn, *s_k = s_dyn + lo.k;
+    float *s_e = s_dyn + lo.e, *s_m = s_dyn + lo.m;
+    float *K = kc + (size_t)kvh * max_ctx * HD, *V = vc + (size_t)kvh * att_vstride(max_ctx, HD);
+
+    /* entry loads in the order of use: query heads, new key and value, norm
+     * weights and RoPE factors, the first chunk's keys, the first chunk's
+     * value tiles */
+    const int nq4 = R * H4;
+    const f32x4 *q4 = (const f32x4 *)(q + (size_t)kvh * R * HD);
+    f32x4 qv[QF];
+#pragma unroll
+    for (int k = 0; k < QF; k++) qv[k] = q4[min(tid + NT * k, nq4 - 1)];
+    const f32x4 knv = ((const f32x4 *)kx)[(size_t)kvh * H4 + min(tid, H4 - 1)];
+    const f32x4 vnv = ((const f32x4 *)vx)[(size_t)kvh * H4 + min(tid, H4 - 1)];
+    float qn[KE], kn[KE], cv[KH], sv[KH];
+#pragma unroll
+    for (int k = 0; k < KE; k++) qn[k] = q_norm[min(lane + 64 * k, HD - 1)];
+#pragma unroll
+    for (int k = 0; k < KE; k++) kn[k] = k_norm[min(lane + 64 * k, HD - 1)];
+#pragma unroll
+    for (int k = 0; k < KH; k++) {
+        cv[k] = cs_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
+        sv[k] = sn_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
+    }
+    const int nch = (tn + ATT_CH - 1) / ATT_CH;
+    f32x4 kr[CF];
+    auto kload = [&](int c) {
+        const int tc = t0 + c * ATT_CH;
+#pragma unroll
+        for (int k = 0; k < CF; k++) {
+            const int e = tid + NT * k, t = min(tc + e / H4, T - 1);
+            kr[k] = ((const f32x4 *)(K + (size_t)t * HD))[e % H4];
+        }
+    };
+    kload(0);
+    const int vi = tid % HD, js = tid / HD, lastq = (T - 1) >> 2;
+    f32x4 vr[VQ];
+    auto vload = [&](int c) {   /* chunk c's tiles of element vi, clamped to the context */
+        const int q0 = (t0 + c * ATT_CH) >> 2;
+#pragma unroll
+        for (int u = 0; u < VQ; u++) vr[u] = ((const f32x4 *)V)[(size_t)min(q0 + u, lastq) * HD + vi];
+    };
+    vload(0);
+
+#pragma unroll
+    for (int k = 0; k < QF; k++)
+        if (tid + NT * k < nq4) ((f32x4 *)s_q)[tid + NT * k] = qv[k];
+    if (tid < H4) {
+        ((f32x4 *)s_kn)[tid] = knv;
+        ((f32x4 *)s_vn)[tid] = vnv;
+    }
+    __syncthreads();
+
+    /* q-norm / k-norm and RoPE as in k_attn_scores (tlm_model.c:743-746,
+     * 721-728) */
+    for (int v = wave; v <= R; v += NT / 64) {
+        float *x = v < R ? s_q + v * HD : s_kn;
+        if (v < R ? has_qn : has_kn) {
+            float e[KE];
+#pragma unroll
+            for (int k = 0; k < KE; k++) e[k] = x[min(lane + 64 * k, HD - 1)];
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < KE; k++)
+                if (lane + 64 * k < HD) ss += (double)e[k] * (double)e[k];
+            ss = wave_sum_f64(ss);
+            const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
+#pragma unroll
+            for (int k = 0; k < KE; k++)
+                if (lane + 64 * k < HD) x[lane + 64 * k] = e[k] * r * (v < R ? qn[k] : kn[k]);
+            wave_lds_sync();
+        }
+#pragma unroll
+        for (int k = 0; k < KH; k++) {
+            const int j = lane + 64 * k;
+            if (j < HALF) {
+                const float a = x[j], c = x[j + HALF];
+                x[j] = a * cv[k] - c * sv[k];
+                x[j + HALF] = c * cv[k] + a * sv[k];
+            }
+        }
+    }
+    __syncthreads();
+
+    /* scores of the slice into LDS (row j of s_e: query head j's positions),
+     * with each thread's running maximum over its items */
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int nsc = R * ATT_CH;
+    float rmx[SU];
+#pragma unroll
+    for (int u = 0; u < SU; u++) rmx[u] = -INFINITY;
+    for (int c = 0; c < nch; c++) {   /* uniform over the group */
+        const int tc = t0 + c * ATT_CH, tnc = min(ATT_CH, tn - c * ATT_CH);
+#pragma unroll
+        for (int k = 0; k < CF; k++) {
+            const int e = tid + NT * k, t = e / H4, i4 = e % H4;
+            ((f32x4 *)(s_k + t * KS))[i4] = tc + t == pos ? ((const f32x4 *)s_kn)[i4] : kr[k];
         }
         __syncthreads();
-        if (chain) {
-            const float *pp = s_p[jc];
-            /* the chain over ATT_PD positions of r starting at t0; lim < ATT_PD
-             * masks the positions past the segment */
-            auto add_full = [&](int t0, const f32x4 (&r)[PQ]) {
-                const f32x4 *p4 = (const f32x4 *)(pp + (t0 - sb));
-                f32x4 p = p4[0];   /* each group's probabilities read one group ahead */
+        if (c + 1 < nch) kload(c + 1);
 #pragma unroll
-                for (int u = 0; u < PQ; u++) {
-                    const f32x4 pn = p4[u + 1 < PQ ? u + 1 : u];
-                    acc += p.x * r[u].x;
-                    acc += p.y * r[u].y;
-                    acc += p.z * r[u].z;
-                    acc += p.w * r[u].w;
-                    p = pn;
+        for (int u = 0; u < SU; u++) {
+            const int idx = tid + NT * u;
+            if (idx < nsc) {
+                const int j = idx / ATT_CH, t = idx % ATT_CH;
+                const f32x4 *qq = (const f32x4 *)(s_q + j * HD), *kk = (const f32x4 *)(s_k + t * KS);
+                float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll 8
+                for (int i4 = 0; i4 < H4; i4++) {
+                    const f32x4 a = qq[i4], b = kk[i4];
+                    d0 = fmaf(a.x, b.x, d0);
+                    d1 = fmaf(a.y, b.y, d1);
+                    d2 = fmaf(a.z, b.z, d2);
+                    d3 = fmaf(a.w, b.w, d3);
                 }
-            };
-            auto add_part = [&](int t0, const f32x4 (&r)[PQ], int lim) {
-                const f32x4 *p4 = (const f32x4 *)(pp + (t0 - sb));
-#pragma unroll
-                for (int u = 0; u < PQ; u++) {
-                    const f32x4 p = p4[u];
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const float a = acc + p[k] * r[u][k];
-                        acc = 4 * u + k < lim ? a : acc;
-                    }
+                const float d = ((d0 + d1) + (d2 + d3)) * scale;
+                if (t < tnc) {
+                    s_e[j * lmax + c * ATT_CH + t] = d;
+                    rmx[u] = d > rmx[u] ? d : rmx[u];
                 }
-            };
-            /* three blocks in flight, loads unconditional (tiles clamped to the
-             * context, so a load past it rereads the last tile); a segment
-             * other than the last holds a multiple of three blocks, so va and vb
-             * hold blocks se and se + ATT_PD on leaving it */
-            int t0 = sb;
-            for (; t0 + 3 * ATT_PD <= se; t0 += 3 * ATT_PD) {
-                vld(t0 + 2 * ATT_PD, vc3);
-                add_full(t0, va);
-                vld(t0 + 3 * ATT_PD, va);
-                add_full(t0 + ATT_PD, vb);
-                vld(t0 + 4 * ATT_PD, vb);
-                add_full(t0 + 2 * ATT_PD, vc3);
-            }
-            const int rem = se - t0;   /* 0 .. 3 ATT_PD - 1 positions left */
-            if (rem > 0) {
-                vld(t0 + 2 * ATT_PD, vc3);
-                add_part(t0, va, rem);
-                if (rem > ATT_PD) add_part(t0 + ATT_PD, vb, rem - ATT_PD);
-                if (rem > 2 * ATT_PD) add_part(t0 + 2 * ATT_PD, vc3, rem - 2 * ATT_PD);
             }
         }
-        __syncthreads();   /* before the next segment's probabilities */
+        __syncthreads();   /* before the next chunk overwrites the keys */
     }
-    if (chain && ic < HD) att[(size_t)hc * HD + ic] = acc;
+    /* the slice maximum per query head (a half wave holds one head's items) */
+#pragma unroll
+    for (int u = 0; u < SU; u++) {
+        const int idx = tid + NT * u;
+        if (idx < nsc) {
+            const float m = half_max_f32(rmx[u]);
+            if (idx % ATT_CH == 0) s_m[idx / ATT_CH] = m;
+        }
+    }
+    __syncthreads();
+    /* e_t = e^(s_t - m_j) in place; l_j */
+    float rl[SU];
+#pragma unroll
+    for (int u = 0; u < SU; u++) rl[u] = 0.0f;
+    for (int c = 0; c < nch; c++) {
+#pragma unroll
+        for (int u = 0; u < SU; u++) {
+            const int idx = tid + NT * u, t = c * ATT_CH + idx % ATT_CH;
+            if (idx < nsc && t < tn) {
+                float *e = s_e + (idx / ATT_CH) * lmax + t;
+                const float v = expf_ref(*e - s_m[idx / ATT_CH]);
+                *e = v;
+                rl[u] += v;
+            }
+        }
+    }
+    const size_t slot = (size_t)kvh * R * G + blockIdx.y;   /* (head kvh * R + j, slice) at slot + j * G */
+#pragma unroll
+    for (int u = 0; u < SU; u++) {
+        const int idx = tid + NT * u;
+        if (idx < nsc) {
+            const float l = half_sum_f32(rl[u]);
+            if (idx % ATT_CH == 0) {
+                const int j = idx / ATT_CH;
+                part_ml[(slot + (size_t)j * G) * 2] = s_m[j];
+                part_ml[(slot + (size_t)j * G) * 2 + 1] = l;
+            }
+        }
+    }
+    __syncthreads();
+
+    /* o_j[i] = sum_t e_t v_t[i] over the slice; the new position's value from
+     * this group's copy */
+    const int jk = js < JS ? (R - js + JS - 1) / JS : 0;
+    float acc[JK];
+#pragma unroll
+    for (int k = 0; k < JK; k++) acc[k] = 0.0f;
+    const float vnew = s_vn[vi];
+    for (int c = 0; c < nch; c++) {
+        f32x4 vcur[VQ];
+#pragma unroll
+        for (int u = 0; u < VQ; u++) vcur[u] = vr[u];
+        if (c + 1 < nch) vload(c + 1);
+        const int tb = c * ATT_CH, tnc = min(ATT_CH, tn - tb);
+        if (t0 + tb <= pos && pos < t0 + tb + ATT_CH) vcur[(pos - t0 - tb) >> 2][pos & 3] = vnew;
+        if (tnc == ATT_CH) {
+#pragma unroll
+            for (int u = 0; u < VQ; u++) {
+#pragma unroll
+                for (int k = 0; k < JK; k++) {
+                    if (k < jk) {
+                        const f32x4 e4 = *(const f32x4 *)(s_e + (js + JS * k) * lmax + tb + 4 * u);
+                        acc[k] = fmaf(e4.x, vcur[u].x, acc[k]);
+                        acc[k] = fmaf(e4.y, vcur[u].y, acc[k]);
+                        acc[k] = fmaf(e4.z, vcur[u].z, acc[k]);
+                        acc[k] = fmaf(e4.w, vcur[u].w, acc[k]);
+                    }
+                }
+            }
+        } else {   /* the slice's last, partial chunk: positions past it skipped */
+#pragma unroll
+            for (int u = 0; u < VQ; u++) {
+#pragma unroll
+                for (int k = 0; k < JK; k++) {
+                    if (k < jk) {
+                        const f32x4 e4 = *(const f32x4 *)(s_e + (js + JS * k) * lmax + tb + 4 * u);
+#pragma unroll
+                        for (int w = 0; w < 4; w++)
+                            if (4 * u + w < tnc) acc[k] = fmaf(e4[w], vcur[u][w], acc[k]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < JK; k++)
+        if (k < jk) part_o[(slot + (size_t)(js + JS * k) * G) * HD + vi] = acc[k];
+    if (t0 + tn == T) {   /* the KV append (tlm_model.c:748-752), after the group's reads */
+        __syncthreads();
+        for (int i4 = tid; i4 < H4; i4 += NT) {
+            ((f32x4 *)K)[(size_t)pos * H4 + i4] = ((const f32x4 *)s_kn)[i4];
+            const f32x4 v4 = ((const f32x4 *)s_vn)[i4];
+            V[att_vidx(pos, 4 * i4, HD)] = v4.x;
+            V[att_vidx(pos, 4 * i4 + 1, HD)] = v4.y;
+            V[att_vidx(pos, 4 * i4 + 2, HD)] = v4.z;
+            V[att_vidx(pos, 4 * i4 + 3, HD)] = v4.w;
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(NT) void k_attn_merge(const float *__restrict__ part_o,
+                                                   const float *__restrict__ part_ml, float *__restrict__ att,
+                                                   int G, const int32_t *__restrict__ st) {
+    constexpr int JS = NT / HD;               /* threads per element: slices s = js (mod JS) each */
+    constexpr int SP = ATT_GMAX / JS;         /* slices per thread, at most */
+    __shared__ float s_w[ATT_GMAX];
+    __shared__ float s_part[NT];
+    __shared__ float s_mx[NT / 64];
+    __shared__ double s_l[NT / 64];
+    const int pos = st[0], T = pos + 1, L = att_slice_len(T, G), ns = (T + L - 1) / L;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int vi = tid % HD, js = tid / HD;
+    const float *po = part_o + (size_t)h * G * HD, *ml = part_ml + (size_t)h * G * 2;
+    /* every load at entry: the slice's maximum and sum (thread s), the
+     * thread's partial outputs */
+    const float m = tid < ns ? ml[2 * tid] : -INFINITY;
+    const float l = tid < ns ? ml[2 * tid + 1] : 0.0f;
+    float o[SP];
+#pragma unroll
+    for (int k = 0; k < SP; k++) {
+        const int sl = js + JS * k;
+        o[k] = js < JS && sl < ns ? po[(size_t)sl * HD + vi] : 0.0f;
+    }
+    float mx = wave_max_f32(m);
+    if (lane == 0) s_mx[wave] = mx;
+    __syncthreads();
+    mx = s_mx[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) mx = s_mx[w] > mx ? s_mx[w] : mx;
+    const float w = tid < ns ? expf_ref(m - mx) : 0.0f;
+    if (tid < ATT_GMAX) s_w[tid] = w;
+    const double wl = wave_sum_f64((double)w * (double)l);
+    if (lane == 0) s_l[wave] = wl;
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < SP; k++) {
+        const int sl = js + JS * k;
+        if (sl < ns) acc = fmaf(s_w[sl], o[k], acc);
+    }
+    s_part[tid] = acc;
+    __syncthreads();
+    if (tid < HD) {
+        double tot = 0.0;
+#pragma unroll
+        for (int v = 0; v < NT / 64; v++) tot += s_l[v];
+        float out = 0.0f;
+#pragma unroll
+        for (int k = 0; k < JS; k++) out += s_part[tid + HD * k];
+        att[(size_t)h * HD + tid] = out * (float)(1.0 / tot);
+    }
 }
 
 /* slices per key head: enough groups to cover the chip at long contexts
@@ -471,23 +858,37 @@ bool att_supported(int hd, int H, int KV) {
     const int R = H / KV;
     return hd % 32 == 0 && hd <= 256 && R * hd <= ATT_QMAX && (size_t)att_lds(hd, R).total * 4 <= 65536;
 }
+/* LDS bytes of the split launch at a context capacity of max_ctx positions */
+size_t att_split_bytes(int hd, int H, int KV, int max_ctx, int G) {
+    return (size_t)att_split_lds(hd, H / KV, att_slice_len(max_ctx, G)).total * 4;
+}
 
-/* host: launch for the model's head width (a multiple of 32, at most 256) */
-int launch_attn(int hd, int H, int KV, int max_ctx, int G, const float *q, const float *kx, const float *vx,
-                const float *q_norm, const float *k_norm, const float *cs, const float *sn, float *kc, float *vc,
-                float *scores, float *smax, float *att, const int32_t *st, float eps, hipStream_t s) {
+/* host: launch for the model's head width (a multiple of 32, at most 256);
+ * split: k_attn_split + k_attn_merge (partials in part_o / part_ml), else the
+ * reference's order k_attn_scores + k_attn_pv */
+int launch_attn(int hd, int H, int KV, int max_ctx, int G, bool split, const float *q, const float *kx,
+                const float *vx, const float *q_norm, const float *k_norm, const float *cs, const float *sn,
+                float *kc, float *vc, float *scores, float *smax, float *part_o, float *part_ml, float *att,
+                const int32_t *st, float eps, hipStream_t s) {
     const int has_qn = q_norm != nullptr, has_kn = k_norm != nullptr;
     if (!q_norm) q_norm = q;   /* read (clamped) and dropped */
     if (!k_norm) k_norm = q;
     const size_t dyn = (size_t)att_lds(hd, H / KV).total * 4;
-    const int nwc = (hd + 63) / 64, qpg = nwc <= 4 ? 4 / nwc : 1;
-    const unsigned npv = (unsigned)(KV * ((H / KV + qpg - 1) / qpg));
+    const int lmax = att_slice_len(max_ctx, G);
+    const size_t dyn_split = att_split_bytes(hd, H, KV, max_ctx, G);
+    const unsigned npv = (unsigned)(H * ((hd + 63) / 64));   /* k_attn_pv: a group per (query head, 64 elements) */
 #define TLM_ATT(W)                                                                                                \
     case W:                                                                                                       \
-        hipLaunchKernelGGL((k_attn_scores<W>), dim3(KV, G), dim3(NT), dyn, s, q, kx, vx, q_norm, k_norm, has_qn, \
-                           has_kn, cs, sn, kc, vc, scores, smax, H, KV, max_ctx, G, st, eps);                    \
-        hipLaunchKernelGGL((k_attn_pv<W>), dim3(npv), dim3(NT), 0, s, scores, smax, vc, att, H, KV, max_ctx, G,  \
-                           st);                                                                                   \
+        if (split) {                                                                                              \
+            hipLaunchKernelGGL((k_attn_split<W>), dim3(KV, G), dim3(NT), dyn_split, s, q, kx, vx, q_norm, k_norm, \
+                               has_qn, has_kn, cs, sn, kc, vc, part_o, part_ml, H, KV, max_ctx, G, lmax, st, eps); \
+            hipLaunchKernelGGL((k_attn_merge<W>), dim3(H), dim3(NT), 0, s, part_o, part_ml, att, G, st);          \
+        } else {                                                                                                  \
+            hipLaunchKernelGGL((k_attn_scores<W>), dim3(KV, G), dim3(NT), dyn, s, q, kx, vx, q_norm, k_norm,      \
+                               has_qn, has_kn, cs, sn, kc, vc, scores, smax, H, KV, max_ctx, G, st, eps);         \
+            hipLaunchKernelGGL((k_attn_pv<W>), dim3(npv), dim3(NT), 0, s, scores, smax, vc, att, H, KV, max_ctx, \
+                               G, st);                                                                            \
+        }                                                                                                         \
         break;
     switch (hd) {
         TLM_ATT(32) TLM_ATT(64) TLM_ATT(96) TLM_ATT(128) TLM_ATT(160) TLM_ATT(192) TLM_ATT(224) TLM_ATT(256)
@@ -552,7 +953,9 @@ struct tlm_hip_model {
     DevMat lm_head;
     float *kc = nullptr, *vc = nullptr, *cs = nullptr, *sn = nullptr;
     int att_g = 1;                                     /* attention slices per key head */
+    bool att_split = false;                            /* split attention; false: the reference's order */
     float *scores = nullptr, *smax = nullptr;          /* [H][max_ctx] scores; [H][att_g] slice maxima */
+    float *part_o = nullptr, *part_ml = nullptr;       /* split partials: [H][att_g][hd]; [H][att_g] (m, l) */
     float *h = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
     float *logits = nullptr;
     uint8_t *moe_ws = nullptr;
@@ -708,6 +1111,11 @@ int prepare(tlm_hip_model *M, const tlm_hip_model_opts *o) {
         return tlmh_seterr(TLM_HIP_EUNSUP, "model: %u query heads per key head of width %u exceed the attention "
                            "kernel's share", g.n_heads / g.n_kv_heads, g.head_dim);
     M->att_g = att_groups(max_ctx, (int)g.n_kv_heads, o ? o->attn_slices : 0);
+    M->att_split = o && o->attn_split;
+    if (M->att_split &&
+        att_split_bytes((int)g.head_dim, (int)g.n_heads, (int)g.n_kv_heads, max_ctx, M->att_g) > 65536)
+        return tlmh_seterr(TLM_HIP_EUNSUP, "model: a context of %d positions in %d slices exceeds the split "
+                           "attention's LDS (more attn_slices, or attn_split 0)", max_ctx, M->att_g);
     const int64_t hd = g.head_dim;
 
     int rc = tlmh_check(hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking), "model: stream");
@@ -750,6 +1158,8 @@ int finish(tlm_hip_model *M) {
     M->vc = (float *)M->dalloc((size_t)g.n_layers * KV * att_vstride(max_ctx, (int)hd) * 4);
     M->scores = (float *)M->dalloc((size_t)H * max_ctx * 4);
     M->smax = (float *)M->dalloc((size_t)H * M->att_g * 4);
+    M->part_o = (float *)M->dalloc((size_t)H * M->att_g * hd * 4);
+    M->part_ml = (float *)M->dalloc((size_t)H * M->att_g * 2 * 4);
     M->h = (float *)M->dalloc((size_t)D * 4);
     M->q = (float *)M->dalloc((size_t)H * hd * 4);
     M->kx = (float *)M->dalloc((size_t)KV * hd * 4);
@@ -764,7 +1174,8 @@ int finish(tlm_hip_model *M) {
     M->ids = (int32_t *)M->dalloc((size_t)g.n_layers * 32 * 4);   /* the step's routing, per layer */
     M->w = (float *)M->dalloc((size_t)g.n_layers * 32 * 4);
     M->keys = (unsigned long long *)M->dalloc(((size_t)g.vocab + TILE_ROWS - 1) / TILE_ROWS * 8);
-    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->smax, (void *)M->h,
+    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->smax, (void *)M->part_o,
+                    (void *)M->part_ml, (void *)M->h,
                     (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
                     (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
                     (void *)M->w, (void *)M->keys})
@@ -940,9 +1351,9 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
         }
         if (rc) break;
         const size_t kbase = (size_t)l * KV * M->max_ctx * hd, vbase = (size_t)l * KV * att_vstride(M->max_ctx, hd);
-        rc = launch_attn(hd, H, KV, M->max_ctx, M->att_g, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm, M->cs, M->sn,
-                         M->kc + kbase, M->vc + vbase, M->scores, M->smax, M->att,
-                         (const int32_t *)M->st, g.norm_eps, s);
+        rc = launch_attn(hd, H, KV, M->max_ctx, M->att_g, M->att_split, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm,
+                         M->cs, M->sn, M->kc + kbase, M->vc + vbase, M->scores, M->smax, M->part_o, M->part_ml,
+                         M->att, (const int32_t *)M->st, g.norm_eps, s);
         /* o: every group quantises the attention output itself */
         const MvNorm ao{M->att, nullptr, 0.0f};
         const void *Wo = Ly.o.p;

@@ -19,7 +19,7 @@ from ._lib import check, lib
 
 class ModelOpts(C.Structure):
     """tlm_hip_model_opts"""
-    _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32)]
+    _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32), ("attn_split", C.c_int32)]
 
 
 # Qwen3-30B-A3B: 48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128
@@ -30,14 +30,15 @@ QWEN3_30B_A3B = dict(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_d
 
 
 class Model:
-    def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0):
-        self.opts = ModelOpts(max_ctx, int(eager), attn_slices)
+    def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0, split=False):
+        self.opts = ModelOpts(max_ctx, int(eager), attn_slices, int(split))
         h = C.c_void_p()
         check(lib.tlm_hip_model_open(str(manifest_path).encode(), C.byref(self.opts), C.byref(h)))
         self._bind(h)
 
     @classmethod
-    def synth(cls, geom, expert_dt=14, dense_dt=8, qk_norm=True, seed=1, max_ctx=0, eager=False, attn_slices=0):
+    def synth(cls, geom, expert_dt=14, dense_dt=8, qk_norm=True, seed=1, max_ctx=0, eager=False, attn_slices=0,
+              split=False):
         """tlm_hip_model_synth: a random-init model of geometry geom (a dict of
         tlm_hip_model_geom fields) built in HBM."""
         from ._lib import ModelGeom, ModelSynthOpts
@@ -47,7 +48,7 @@ class Model:
             setattr(g, k, v)
         so = ModelSynthOpts(expert_dt, dense_dt, int(qk_norm), 0, seed)
         self = cls.__new__(cls)
-        self.opts = ModelOpts(max_ctx, int(eager), attn_slices)
+        self.opts = ModelOpts(max_ctx, int(eager), attn_slices, int(split))
         h = C.c_void_p()
         check(lib.tlm_hip_model_synth(C.byref(g), C.byref(so), C.byref(self.opts), C.byref(h)))
         self._bind(h)
@@ -153,6 +154,43 @@ def time_model(m, prompt_len=64, n=64, reps=3, warm_n=None):
             "decode_us_per_token": round(dec / (n - 1) * 1e6, 1), "tokens": toks}
 
 
+def _roctx():
+    """roctxProfilerPause / Resume (rocprofv3 --selected-regions traces only
+    what runs between a resume and the next pause), or None without the
+    library."""
+    try:
+        lib_ = C.CDLL("librocprofiler-sdk-roctx.so.1")
+    except OSError:
+        return None
+    lib_.roctxProfilerPause.argtypes = lib_.roctxProfilerResume.argtypes = [C.c_uint64]
+    return lib_
+
+
+def time_at_context(m, context, n, rx=None):
+    """n decode steps ending at position context - 1: the context is filled to
+    context - n positions first (a pseudo-random prompt, greedy from there),
+    then the n steps are timed (host clock around the enqueued steps and a
+    sync).  With rx (_roctx()), only the timed steps run between
+    roctxProfilerResume and roctxProfilerPause."""
+    if not 1 <= n < context <= m.kv_capacity():
+        raise ValueError(f"context {context}, {n} steps, capacity {m.kv_capacity()}")
+    if rx:
+        rx.roctxProfilerPause(0)
+    m.reset()
+    m.generate(bench_prompt(context - n, m.geom.vocab), 1)   # positions 0 .. context - n - 1
+    m.sync()
+    if rx:
+        rx.roctxProfilerResume(0)
+    t0 = time.perf_counter()
+    m.decode(n)
+    m.sync()
+    dt = time.perf_counter() - t0
+    if rx:
+        rx.roctxProfilerPause(0)
+    return {"positions": [context - n, context - 1], "decode_tok_s": round(n / dt, 1),
+            "decode_us_per_token": round(dt / n * 1e6, 1)}
+
+
 def bench(path, prompt_len=64, n=64, reps=3, eager=False, max_ctx=0):
     """time_model on a compiled store."""
     m = Model(path, max_ctx=max_ctx or prompt_len + n + 1, eager=eager)
@@ -174,21 +212,43 @@ if __name__ == "__main__":
     ap.add_argument("-n", type=int, default=64)
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--eager", action="store_true", help="launch kernels directly instead of replaying a graph")
+    ap.add_argument("--split", action="store_true", help="split attention (attn_split) instead of the reference's order")
+    ap.add_argument("--context", type=int, default=0,
+                    help="time only the n decode steps ending at position CONTEXT - 1 (the context filled first)")
+    ap.add_argument("--roctx", action="store_true",
+                    help="with --context: pause the profiler outside the timed steps (rocprofv3 --selected-regions)")
     a = ap.parse_args()
     if (a.store is None) == (a.synth is None):
         ap.error("give a store or --synth")
+    if a.roctx and not a.context:
+        ap.error("--roctx needs --context")
+    rx = None
+    if a.roctx:   # loaded before the runtime starts, so the profiler sees its calls
+        rx = _roctx()
+        if rx is None:
+            raise SystemExit("librocprofiler-sdk-roctx.so.1 not found")
+        rx.roctxProfilerPause(0)
     init(0)
+    ctx = a.context or a.prompt_len + a.n + 1
     if a.synth:
         geom = dict(QWEN3_30B_A3B, **({"n_layers": a.layers} if a.layers else {}))
-        m = Model.synth(geom, seed=1, max_ctx=a.prompt_len + a.n + 1, eager=a.eager)
-        try:
-            r = time_model(m, a.prompt_len, a.n, a.reps)
-        finally:
-            m.close()
+        m = Model.synth(geom, seed=1, max_ctx=ctx, eager=a.eager, split=a.split)
         name = f"{a.synth} ({geom['n_layers']} layers, random init)"
     else:
-        r = bench(a.store, a.prompt_len, a.n, a.reps, a.eager)
+        m = Model(a.store, max_ctx=ctx, eager=a.eager, split=a.split)
         name = a.store
+    try:
+        if a.context:
+            r = time_at_context(m, a.context, a.n, rx)
+        else:
+            r = time_model(m, a.prompt_len, a.n, a.reps)
+    finally:
+        m.close()
+    if a.context:
+        print(f"bench {name}: decode {a.n} tokens at positions {r['positions'][0]}..{r['positions'][1]} "
+              f"({r['decode_tok_s']:.1f} tok/s, {r['decode_us_per_token']:.1f} us/token)"
+              f"{' eager' if a.eager else ''}", flush=True)
+        raise SystemExit(0)
     print(f"bench {name}: prompt {a.prompt_len} tokens ({r['prefill_tok_s']:.1f} tok/s), decode {a.n} tokens "
           f"({r['decode_tok_s']:.1f} tok/s, {r['decode_us_per_token']:.1f} us/token){' eager' if a.eager else ''}",
           flush=True)
