@@ -1,0 +1,91 @@
+"""The drop-in: the reference's own `tierlm` with libtlm_hip.so taken into its
+kernel dispatch and its decode step (oracle/dropin.py builds it from a
+build-directory copy of the reference's sources), run on the 4-layer
+synthetic store (oracle/make_c1.sh) against the reference's own outputs
+(tests/golden/make_c1_golden.sh):
+
+* --kernel hip: tlm_quant_tier() is "hip" with no self-test failures (the
+  reference's bit-exact self-test, src/lib/tlm_quant.c:1015-1056, run over
+  the HIP entries), and tlm_model_step runs the whole step on the device:
+  `tierlm run` gives the reference's 64 greedy tokens, `tierlm oracle` its
+  teacher-forced top-10 logits text for text (9 significant digits, so bit
+  for bit), `tierlm bench` runs its loop;
+* TIERLM_HIP_TIER_ONLY=1 --kernel hip: the reference's own CPU step with
+  every quantised matvec of its kernel table on the device (the host-pointer
+  entries of tlm_kern_hip_fill): the same tokens."""
+import os
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+TIERLM = os.path.join(ROOT, "oracle", "_ref", "dropin", "bin", "tierlm")
+C1 = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
+GOLD = os.path.join(ROOT, "tests", "golden")
+needs = pytest.mark.skipif(not (os.path.exists(TIERLM) and os.path.exists(C1)),
+                           reason="oracle/_ref/dropin (python3 oracle/dropin.py) or oracle/_ref/c1 not built")
+
+
+def prompt_ids(n=64, vocab=4096):
+    x, out, m = 42, [], (1 << 64) - 1
+    for _ in range(n):   # src/bin/tierlm.c:711-715
+        x ^= (x << 13) & m
+        x ^= x >> 7
+        x ^= (x << 17) & m
+        out.append(x % vocab)
+    return out
+
+
+def golden(name):
+    return open(os.path.join(GOLD, name)).read()
+
+
+def tierlm(args, env=None):
+    e = dict(os.environ)
+    e.update(env or {})
+    r = subprocess.run([TIERLM] + args, capture_output=True, text=True, timeout=300, env=e)
+    assert r.returncode == 0, f"tierlm {' '.join(args[:2])} failed ({r.returncode}): {r.stderr[-2000:]}"
+    return r
+
+
+@needs
+def test_run_hip_step_greedy_tokens():
+    p = ",".join(map(str, prompt_ids()))
+    r = tierlm(["run", C1, "--tokens", p, "-n", "64", "--print-tokens", "--cache", "1G", "--kernel", "hip",
+                "--stats"])
+    assert r.stdout.split() == golden("c1_greedy.txt").split()
+    assert "kernel hip (self-test failures 0)" in r.stderr, r.stderr[-1500:]
+
+
+@needs
+def test_oracle_hip_step_top10_text_identical():
+    gen = golden("c1_greedy.txt").split()[:63]
+    toks = ",".join(map(str, prompt_ids())) + "," + ",".join(gen)
+    r = tierlm(["oracle", C1, "--tokens", toks, "--cache", "1G", "--kernel", "hip"])
+    want = golden("c1_oracle.jsonl").splitlines()
+    got = r.stdout.splitlines()
+    assert len(got) == len(want) == 127
+    bad = [i for i, (a, b) in enumerate(zip(got, want)) if a != b]
+    assert not bad, f"{len(bad)} positions differ, first {bad[0]}: {got[bad[0]]} vs {want[bad[0]]}"
+
+
+@needs
+def test_run_hip_tier_only_greedy_tokens():
+    p = ",".join(map(str, prompt_ids()))
+    r = tierlm(["run", C1, "--tokens", p, "-n", "64", "--print-tokens", "--cache", "1G", "--kernel", "hip",
+                "--stats"], env={"TIERLM_HIP_TIER_ONLY": "1"})
+    assert r.stdout.split() == golden("c1_greedy.txt").split()
+    assert "kernel hip (self-test failures 0)" in r.stderr, r.stderr[-1500:]
+
+
+@needs
+def test_bench_hip_step():
+    r = tierlm(["bench", C1, "--prompt-len", "64", "-n", "64", "--cache", "1G", "--kernel", "hip"])
+    line = r.stdout.splitlines()[0]
+    assert "decode 64 tokens in" in line, r.stdout
+    assert "kernel hip (self-test failures 0)" in r.stdout, r.stdout[-1500:]
+    dec = float(line.split("decode 64 tokens in")[1].split("(")[1].split(" tok/s")[0])
+    print(f"tierlm bench --kernel hip: {line}")
+    assert dec > 0
