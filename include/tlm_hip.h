@@ -108,8 +108,12 @@ int    tlm_hip_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, co
                              float *y, void *stream);
 
 /* ---- segment job: several matvecs in one launch --------------------------
- * Mirrors mv_job / mv_exec (src/lib/tlm_model.c:175-222): every output row is
- * computed by exactly one work-group, so batching never changes a bit. */
+ * Mirrors mv_job / mv_exec (src/lib/tlm_model.c:175-222): up to 24 segments of
+ * any dtype, width, layout and activation run in one launch (a longer job in
+ * one launch per 24); every output row is computed by exactly one work-group,
+ * so batching never changes a bit.  An invalid segment (dtype, width,
+ * pointers, alignment) has its rows NaN-filled and makes the call return
+ * TLM_HIP_EINVAL; the others still run. */
 typedef struct {
     int32_t     dt;        /* weight dtype */
     int32_t     packed;    /* 1 = tlm_hip_pack layout, 0 = plain rows (row_bytes) */

@@ -267,6 +267,53 @@ def test_mv_job_segments(hip, dev):
         assert np.all(same(s["y"].cpu().numpy(), want))
 
 
+def test_mv_job_one_launch_any_mix(hip, dev):
+    """30 segments (more than one launch's 24): every format packed and plain,
+    the deep Q8_0 tile (2048 columns), f32 rows at an unaligned offset, a
+    segment of zero rows; each equals its separate matvec bit for bit.  A
+    segment with a bad dtype is NaN-filled and reported while the others run
+    (tlm_matvec_rows' rule, src/lib/tlm_quant.c:1119-1127)."""
+    from tierlm_amd._lib import HipError
+    rng = np.random.default_rng(12)
+    specs = [(oracle.Q6_K, 40, 512, 1), (oracle.Q8_0, 33, 2048, 1), (oracle.Q5_K, 17, 768, 1),
+             (oracle.Q4_K, 50, 256, 1), (oracle.Q8_K, 9, 512, 1), (oracle.Q8_0, 21, 256, 0),
+             (oracle.Q5_K, 6, 512, 0), (oracle.Q8_K, 5, 256, 0), (oracle.F32, 11, 96, 0), (oracle.F32, 7, 64, 2)]
+    specs = (specs * 3)[:30]
+    segs, wants, keep = [], [], []
+    for k, (dt, rows, n, packed) in enumerate(specs):
+        if dt == oracle.F32:
+            off = 1 if packed == 2 else 0          # packed == 2 here: f32 rows one byte off alignment
+            W = rng.standard_normal((rows, n)).astype(np.float32).view(np.uint8)
+            act = rng.standard_normal(n).astype(np.float32)
+            want = oracle.matvec_rows(dt, W, 4 * n, act, n, 0, rows)
+            raw = torch.from_numpy(np.concatenate([np.zeros(off, np.uint8), W.reshape(-1)])).to(dev)
+            Wd, rb, pk = raw[off:], 4 * n, 0
+        else:
+            W = random_code_rows(rng, dt, rows, n)
+            act = oracle.quantize_act(oracle.act_kind_for(dt), rng.standard_normal(n).astype(np.float32))
+            want = oracle.matvec_rows(dt, W, W.shape[1], act, n, 0, rows)
+            Wd, rb, pk = to_dev(W, dev), W.shape[1], packed
+            if packed:
+                Wd = hip.pack(dt, Wd, W.shape[1], rows, n)
+        r = 0 if k == 3 else rows                  # one segment with no rows
+        y = torch.zeros(rows, device=dev)
+        ad = to_dev(act, dev)
+        keep += [Wd, ad, y]
+        segs.append(dict(dt=dt, packed=pk, W=Wd, row_bytes=rb, act=ad, y=y, n=n, rows=r))
+        wants.append(want if r else np.zeros(rows, np.float32))
+    hip.mv_job(segs)
+    torch.cuda.synchronize()
+    for k, (sg, want) in enumerate(zip(segs, wants)):
+        assert np.all(same(sg["y"].cpu().numpy(), want)), k
+    bad = dict(segs[0], dt=7, y=torch.zeros(40, device=dev))     # 7: not a dtype of the path
+    good = dict(segs[1], y=torch.zeros(33, device=dev))
+    with pytest.raises(HipError):
+        hip.mv_job([bad, good])
+    torch.cuda.synchronize()
+    assert np.isnan(bad["y"].cpu().numpy()).all()
+    assert np.all(same(good["y"].cpu().numpy(), wants[1]))
+
+
 def pack_layout_host(dt, W, rows, n):
     """The packed tile layout written out in numpy: unit u = (t*nb + b)*16 + i
     holds row t*16 + i, block b (Q6_K bytes 0..207, Q8_0 codes, other formats

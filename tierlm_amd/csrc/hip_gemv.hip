@@ -96,15 +96,15 @@ __device__ __forceinline__ void plain_scales(const uint8_t *w, const uint8_t *a,
  * ...; the chain runs in every lane (same values) over shuffled block results
  * in ascending order. */
 template <int DT>
-__global__ __launch_bounds__(256) void k_mv_plain_int(const uint8_t *__restrict__ W, size_t row_bytes,
-                                                      const uint8_t *__restrict__ act, float *__restrict__ y,
-                                                      int64_t n, int64_t r0, int64_t r1) {
+__device__ __forceinline__ void mv_plain_rows(const uint8_t *__restrict__ W, size_t row_bytes,
+                                              const uint8_t *__restrict__ act, float *__restrict__ y, int64_t n,
+                                              int64_t r0, int64_t r1, int64_t bid) {
     constexpr int BV = DT == DT_Q8_0 ? 32 : 256;
     constexpr int AB = DT == DT_Q8_0 ? 36 : 292;
     constexpr int WB = DT == DT_Q8_0 ? 34 : DT == DT_Q4_K ? 144 : DT == DT_Q5_K ? 176 : DT == DT_Q6_K ? 210 : 292;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
     const int lane = threadIdx.x & 63;
-    const int64_t row = r0 + (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t row = r0 + bid * 4 + (threadIdx.x >> 6);
     if (row >= r1) return;
     const uint8_t *w = W + (size_t)row * row_bytes;
     const int64_t nb = n / BV;
@@ -126,15 +126,21 @@ __global__ __launch_bounds__(256) void k_mv_plain_int(const uint8_t *__restrict_
     }
     if (lane == 0) y[row] = acc;
 }
+template <int DT>
+__global__ __launch_bounds__(256) void k_mv_plain_int(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                      const uint8_t *__restrict__ act, float *__restrict__ y,
+                                                      int64_t n, int64_t r0, int64_t r1) {
+    mv_plain_rows<DT>(W, row_bytes, act, y, n, r0, r1, blockIdx.x);
+}
 
 /* F32 row dot with the reference lane order: lanes 0..31 of a half-wave own
  * elements i = lane mod 32; two rows per wave, 8 rows per work-group. */
 template <bool ALIGNED>
-__global__ __launch_bounds__(256) void k_mv_f32(const uint8_t *__restrict__ W, size_t row_bytes,
-                                                const float *__restrict__ x, float *__restrict__ y,
-                                                int64_t n, int64_t r0, int64_t r1) {
+__device__ __forceinline__ void mv_f32_rows(const uint8_t *__restrict__ W, size_t row_bytes,
+                                            const float *__restrict__ x, float *__restrict__ y, int64_t n,
+                                            int64_t r0, int64_t r1, int64_t bid) {
     const int lane = threadIdx.x & 31;
-    const int64_t row = r0 + (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int64_t row = r0 + bid * 8 + (threadIdx.x >> 5);
     const bool live = row < r1;
     float r = 0.0f;
     if (live) {
@@ -156,6 +162,12 @@ __global__ __launch_bounds__(256) void k_mv_f32(const uint8_t *__restrict__ W, s
     float a = s + __shfl_down(s, 2, 32);           /* lane 0: s4[0] + s4[2]; lane 1: s4[1] + s4[3] */
     float res = a + __shfl_down(a, 1, 32);
     if (live && lane == 0) y[row] = res;
+}
+template <bool ALIGNED>
+__global__ __launch_bounds__(256) void k_mv_f32(const uint8_t *__restrict__ W, size_t row_bytes,
+                                                const float *__restrict__ x, float *__restrict__ y,
+                                                int64_t n, int64_t r0, int64_t r1) {
+    mv_f32_rows<ALIGNED>(W, row_bytes, x, y, n, r0, r1, blockIdx.x);
 }
 
 __global__ void k_nan_fill(float *y, int64_t count) {
@@ -428,17 +440,24 @@ static __device__ __forceinline__ XLds stage_norm_act(int kind, const float *__r
  * launch (segment s owns tiles [tile_end[s-1], tile_end[s])), all taking the
  * same activation; accum: y[r] += acc instead of y[r] = acc (the reference's
  * residual update h += W x, tlm_model.c:762, adds the finished product). */
+struct MvTile {
+    const uint8_t *Wp;   /* packed matrix */
+    int64_t rows, t;     /* its rows; the tile this group computes */
+    float *y;
+    const float *nx, *nw;
+    float eps;
+    int accum;
+    unsigned long long *keys;
+};
 template <int DT, bool DEEP>
-__global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
+__device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const uint8_t *__restrict__ act) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
     constexpr int IPL = MvCfg<DT, DEEP>::IPL;
     extern __shared__ __align__(16) uint8_t lds[];
-    int s = 0;
-    while (s + 1 < sg.n && (int64_t)blockIdx.x >= sg.tile_end[s]) s++;
-    const uint8_t *Wp = sg.W[s];
-    const int64_t rows = sg.rows[s], t = (int64_t)blockIdx.x - (s ? sg.tile_end[s - 1] : 0);
-    float *y = sg.y[s];
+    const uint8_t *Wp = sg.Wp;
+    const int64_t rows = sg.rows, t = sg.t;
+    float *y = sg.y;
     const int kind = dt_act_kind(DT);
     XLds X = xlds_at(kind, nb, lds);
     NormIn nin;
@@ -491,6 +510,65 @@ __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const 
             key = other > key ? other : key;
         }
         if (threadIdx.x == 0) sg.keys[t] = key;
+    }
+}
+template <int DT, bool DEEP>
+__global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
+    int s = 0;
+    while (s + 1 < sg.n && (int64_t)blockIdx.x >= sg.tile_end[s]) s++;
+    const MvTile tl{sg.W[s], sg.rows[s], (int64_t)blockIdx.x - (s ? sg.tile_end[s - 1] : 0), sg.y[s], sg.nx,
+                    sg.nw, sg.eps, sg.accum, sg.keys};
+    mv_packed_tile<DT, DEEP>(tl, nb, act);
+}
+
+/* One launch for a whole job of matrices (mv_job / mv_exec,
+ * src/lib/tlm_model.c:175-222): JOB_SEGS segments of any dtype, width,
+ * layout and activation; segment s owns groups [first[s], first[s + 1]) and
+ * every group runs its segment's body (a uniform switch): a 16-row tile of a
+ * packed matrix, 4 plain rows of an integer format or 8 f32 rows. */
+enum { JK_PACKED = 0, JK_PACKED_DEEP = 1, JK_PLAIN = 2, JK_F32 = 3, JK_F32_UNALIGNED = 4 };
+struct JobSeg {
+    const uint8_t *W, *act;
+    float *y;
+    uint64_t row_bytes;
+    int64_t n, rows, first;
+    int dt, kind;
+};
+#define JOB_SEGS 24
+struct MvJob {
+    JobSeg s[JOB_SEGS];
+    int n;
+};
+__global__ __launch_bounds__(256) void k_mv_job(MvJob j) {
+    int s = 0;
+    while (s + 1 < j.n && (int64_t)blockIdx.x >= j.s[s + 1].first) s++;
+    const JobSeg &g = j.s[s];
+    const int64_t bid = (int64_t)blockIdx.x - g.first;
+    if (g.kind == JK_PACKED || g.kind == JK_PACKED_DEEP) {
+        const int nb = (int)(g.n / dt_block_values(g.dt));
+        const MvTile tl{g.W, g.rows, bid, g.y, nullptr, nullptr, 0.0f, 0, nullptr};
+        switch (g.dt) {
+        case DT_Q8_0:
+            if (g.kind == JK_PACKED_DEEP) mv_packed_tile<DT_Q8_0, true>(tl, nb, g.act);
+            else mv_packed_tile<DT_Q8_0, false>(tl, nb, g.act);
+            break;
+        case DT_Q4_K: mv_packed_tile<DT_Q4_K, false>(tl, nb, g.act); break;
+        case DT_Q5_K: mv_packed_tile<DT_Q5_K, false>(tl, nb, g.act); break;
+        case DT_Q6_K: mv_packed_tile<DT_Q6_K, false>(tl, nb, g.act); break;
+        case DT_Q8_K: mv_packed_tile<DT_Q8_K, false>(tl, nb, g.act); break;
+        }
+    } else if (g.kind == JK_PLAIN) {
+        switch (g.dt) {
+        case DT_Q8_0: mv_plain_rows<DT_Q8_0>(g.W, g.row_bytes, g.act, g.y, g.n, 0, g.rows, bid); break;
+        case DT_Q4_K: mv_plain_rows<DT_Q4_K>(g.W, g.row_bytes, g.act, g.y, g.n, 0, g.rows, bid); break;
+        case DT_Q5_K: mv_plain_rows<DT_Q5_K>(g.W, g.row_bytes, g.act, g.y, g.n, 0, g.rows, bid); break;
+        case DT_Q6_K: mv_plain_rows<DT_Q6_K>(g.W, g.row_bytes, g.act, g.y, g.n, 0, g.rows, bid); break;
+        case DT_Q8_K: mv_plain_rows<DT_Q8_K>(g.W, g.row_bytes, g.act, g.y, g.n, 0, g.rows, bid); break;
+        }
+    } else if (g.kind == JK_F32) {
+        mv_f32_rows<true>(g.W, g.row_bytes, (const float *)g.act, g.y, g.n, 0, g.rows, bid);
+    } else {
+        mv_f32_rows<false>(g.W, g.row_bytes, (const float *)g.act, g.y, g.n, 0, g.rows, bid);
     }
 }
 
@@ -650,11 +728,70 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
 int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s) {
     if (nseg < 0 || nseg > TLM_HIP_MAX_SEGS || (nseg > 0 && !segs))
         return tlmh_seterr(TLM_HIP_EINVAL, "mv_job: bad segment count %d", nseg);
+    /* every segment checked as tlm_hip_matvec_rows / _packed check theirs; an
+     * invalid one is NaN-filled (its rows, as tlm_matvec_rows does) and
+     * reported, the others still run */
+    int rc = TLM_HIP_OK;
+    MvJob j{};
+    size_t lds = 0;
+    int64_t groups = 0;
+    auto flush = [&]() -> int {
+        if (j.n == 0) return TLM_HIP_OK;
+        hipLaunchKernelGGL(k_mv_job, dim3((unsigned)groups), dim3(256), lds, s, j);
+        j.n = 0;
+        groups = 0;
+        lds = 0;
+        return tlmh_check(hipGetLastError(), "mv_job launch");
+    };
     for (int i = 0; i < nseg; i++) {
         const tlm_hip_seg *g = &segs[i];
-        int rc = g->packed ? launch_matvec_packed(g->dt, g->W, g->rows, g->n, g->act, g->y, s)
-                           : launch_matvec_plain(g->dt, g->W, (size_t)g->row_bytes, g->act, g->y, g->n, 0, g->rows, s);
-        if (rc) return rc;
+        const int bv = dt_block_values(g->dt);
+        const bool fmt = bv > 0 && g->n > 0 && g->n % bv == 0 && (g->dt == DT_F32 || dt_int_ok(g->dt));
+        const bool ptrs = g->W && g->act && g->y && !((uintptr_t)g->act & 3u);
+        if (g->rows <= 0) continue;
+        int kind = -1;
+        size_t need = 0;
+        int64_t ng = 0;
+        if (fmt && ptrs && g->packed && g->dt != DT_F32 && !((uintptr_t)g->W & 15u)) {
+            const int nb = (int)(g->n / bv);
+            need = packed_lds_bytes(g->dt, nb);
+            if (need <= 64 * 1024) {
+                kind = mv_deep(g->dt, nb) ? JK_PACKED_DEEP : JK_PACKED;
+                ng = (g->rows + TILE_ROWS - 1) / TILE_ROWS;
+            }
+        } else if (fmt && ptrs && !g->packed &&
+                   g->row_bytes >= (uint64_t)(g->n / bv) * (uint64_t)dt_block_bytes(g->dt)) {
+            if (g->dt == DT_F32) {
+                kind = ((uintptr_t)g->W % 4 == 0 && g->row_bytes % 4 == 0) ? JK_F32 : JK_F32_UNALIGNED;
+                ng = (g->rows + 7) / 8;
+            } else {
+                kind = JK_PLAIN;
+                ng = (g->rows + 3) / 4;
+            }
+        }
+        if (kind < 0) {
+            if (g->y) launch_nan_fill(g->y, g->rows, s);
+            rc = tlmh_seterr(TLM_HIP_EINVAL, "mv_job: segment %d (dtype %d, n=%lld, %s layout) is invalid", i, g->dt,
+                             (long long)g->n, g->packed ? "packed" : "plain");
+            continue;
+        }
+        if (j.n == JOB_SEGS) {
+            const int r2 = flush();
+            if (r2) return r2;
+        }
+        JobSeg &d = j.s[j.n++];
+        d.W = (const uint8_t *)g->W;
+        d.act = (const uint8_t *)g->act;
+        d.y = g->y;
+        d.row_bytes = g->row_bytes;
+        d.n = g->n;
+        d.rows = g->rows;
+        d.first = groups;
+        d.dt = g->dt;
+        d.kind = kind;
+        groups += ng;
+        lds = need > lds ? need : lds;
     }
-    return TLM_HIP_OK;
+    const int r2 = flush();
+    return r2 ? r2 : rc;
 }
