@@ -312,11 +312,12 @@ void     tlm_hip_store_get_stats(tlm_hip_store *s, tlm_hip_store_stats *out);
 /* One routed MoE block with its experts in the cache: moe() of
  * src/lib/tlm_model.c:960-1055 with tlm_store_acquire, the router lookahead
  * (:844-877, issued at :988-991) and the releases.  Routes on device, reads
- * the routing back (one round trip, shared with the hints), acquires the k
- * experts, issues each hint's ids as prefetch hints, points the routed
- * entries of d->experts (a writable device table of 3*E pointers) at the
- * slots, makes `stream` wait for loads still in flight, runs the block
- * (h += MoE(h), as tlm_hip_moe_layer) and releases.  ids_host / w_host (may
+ * the routing back (one round trip, shared with the hints, through mapped
+ * memory without a stream synchronisation), acquires the k experts, makes
+ * `stream` wait for loads still in flight, runs the block (h += MoE(h), as
+ * tlm_hip_moe_layer) with the routing and the slots' matrices handed to it
+ * at launch (d->experts is not read or written), issues each hint's ids as
+ * prefetch hints and releases.  ids_host / w_host (may
  * be NULL) receive the routing.  On an error h is unchanged and every
  * reference is released.  A hint: layer `layer`'s block descriptor with
  * k = the number of experts to hint (lookahead_k, <= 32), and a workspace of
@@ -329,6 +330,33 @@ typedef struct {
 int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int layer, float *h,
                             int32_t *ids_host, float *w_host, const tlm_hip_moe_hint *hints, int n_hints,
                             void *workspace, void *stream);
+
+/* The routed MoE blocks of a stack of layers for one token through the cache:
+ * tlm_model_step's loop over moe() (src/lib/tlm_model.c:1075-1083) with the
+ * store (:960-1055), lookahead() for `lookahead` layers ahead with
+ * lookahead_k experts routed for each and, when interest > 0, the prefetch
+ * breadth weighted as :863-874 (W = interest (1 - I) (1 - H), I the layer's
+ * instinct averaged with the current top-1 share, H its heat), the instinct
+ * update of :974-980, and one tlm_hip_store_tick at the end (:1097).
+ * Pipelined: the host waits for each layer's routing through a sequence word
+ * the export stores last (no stream synchronisation), and layer l + 1's
+ * routing is queued right behind layer l's block, so the device idles only
+ * while the host acquires.  descs[l]: layer l's block (its expert table
+ * is not used); ids / w (n_layers x top_k,
+ * host, may be NULL) receive the routing; workspace: 256-byte aligned,
+ * tlm_hip_moe_stack_workspace_bytes bytes.  On an error at layer l the
+ * layers before it have updated h and every reference is released. */
+typedef struct {
+    int32_t      lookahead;      /* layers ahead (0..7), tlm_model_opts.lookahead */
+    int32_t      lookahead_k;    /* experts routed for each hint (<= 32; 0 = the layer's top_k) */
+    double       interest;       /* tlm_model_opts.interest; 0 = every hint lookahead_k wide */
+    const float *layer_heat;     /* per layer, or NULL (0) */
+    double      *instinct;       /* per layer, the caller's state (tlm_model's instinct), or NULL */
+    uint32_t    *instinct_seen;  /* per layer, or NULL */
+} tlm_hip_stack_opts;
+size_t tlm_hip_moe_stack_workspace_bytes(const tlm_hip_moe_desc *descs, int n_layers, const tlm_hip_stack_opts *o);
+int    tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
+                               const tlm_hip_stack_opts *o, int32_t *ids, float *w, void *workspace, void *stream);
 
 /* ---- compiled model stores: manifest + packet files -----------------------
  * Reader of the reference's store format (src/lib/tlm_packet.h:8-151,

@@ -235,3 +235,116 @@ def test_store_block_c5_shape(hip, dev, dt, router):
         assert st["misses"] > 0 and st["evictions"] > 0 and st["in_use"] == 0
     finally:
         store.close()
+
+
+def breadth(hw, hk, top, interest, instinct, seen, heat):
+    """The prefetch breadth of a hint, tlm_model.c:863-874 restated: W =
+    interest (1 - I) (1 - H) clamped to [0, 1], I the layer's instinct averaged
+    with the current top-1 share (the share alone before the layer was seen),
+    H its heat; top_k + round(W x (lookahead_k - top_k))."""
+    if not (interest > 0.0 and hk > top):
+        return hk
+    s = float(np.sum(np.asarray(hw[:hk], np.float64)))
+    now = float(hw[0]) / s if s > 0.0 else 0.0
+    i = 0.5 * (now + instinct) if seen else now
+    w = min(1.0, max(0.0, interest * (1.0 - i) * (1.0 - heat)))
+    return top + int(w * (hk - top) + 0.5)
+
+
+def three_layers(dev):
+    return [build_moe_case(D=512, de=256, E=32, k=4, ds=0, expert_dt=oracle.Q6_K, seed=300 + s, device=dev,
+                           weights="random_codes") for s in range(3)]
+
+
+def hint_weights(blk, hk, h, dev):
+    """The lookahead's routing of block blk with hk experts from residual h
+    (tlm_hip_moe_route on a copy of its descriptor), host weights."""
+    from tierlm_amd._lib import MoeDesc, check, lib
+    from tierlm_amd.quant import stream
+    hid = torch.zeros(32, dtype=torch.int32, device=dev)
+    hw = torch.zeros(32, dtype=torch.float32, device=dev)
+    hd = MoeDesc.from_buffer_copy(blk.desc)
+    hd.k = hk
+    ws = torch.empty(int(lib.tlm_hip_moe_workspace_bytes(C.byref(hd))), dtype=torch.uint8, device=dev)
+    check(lib.tlm_hip_moe_route(C.byref(hd), C.c_void_p(h.data_ptr()), C.c_void_p(hid.data_ptr()),
+                                C.c_void_p(hw.data_ptr()), C.c_void_p(ws.data_ptr()), stream()))
+    torch.cuda.synchronize()
+    return hw.cpu().numpy()
+
+
+@pytest.mark.parametrize("interest,lk,slots", [(0.0, 0, 40), (0.0, 8, 40), (0.8, 10, 36), (0.8, 10, 96)])
+def test_stack_equals_resident(hip, dev, interest, lk, slots):
+    """tlm_hip_moe_stack_store over three layers for eight tokens: every
+    token's h and routing bit for bit the resident blocks', the instinct
+    state updated from each block's routing as the reference updates it, and
+    one acquire of top_k per layer per token in the cache's counters."""
+    from tierlm_amd import MoeStack
+    cases = three_layers(dev)
+    L, k = len(cases), cases[0].k
+    store = open_store(cases, slots, 1)
+    blocks = [store_block(c, dev) for c in cases]
+    stack = MoeStack(blocks, lookahead=1, lookahead_k=lk, interest=interest, heat=[0.1, 0.4, 0.0])
+    instinct, seen = np.zeros(L), np.zeros(L, np.int64)
+    rng = np.random.default_rng(5)
+    try:
+        for t in range(8):
+            h0 = (rng.standard_normal(512) * (1 + t % 3)).astype(np.float32)
+            h_res = torch.from_numpy(h0.copy()).to(dev)
+            h_st = torch.from_numpy(h0.copy()).to(dev)
+            stack(store, h_st)
+            for layer, case in enumerate(cases):
+                case.block(h_res)
+                assert stack.ids[layer].tolist() == case.block.ids.cpu().numpy()[:k].tolist(), (t, layer)
+                w = case.block.w.cpu().numpy()[:k].astype(np.float64)   # tlm_model.c:974-980
+                instinct[layer] += (w[0] / w.sum() - instinct[layer]) * 0.05
+                seen[layer] += 1
+            torch.cuda.synchronize()
+            assert np.array_equal(h_st.cpu().numpy().view(np.uint32), h_res.cpu().numpy().view(np.uint32)), t
+            assert np.allclose(stack.instinct, instinct, rtol=0, atol=1e-12) and (stack.seen == seen).all()
+        store.settle()
+        st = store.stats()
+        assert st["hits"] + st["misses"] == 8 * L * k
+        if lk or interest:
+            assert st["prefetch_issued"] > 0
+    finally:
+        store.close()
+
+
+@pytest.mark.parametrize("interest,heat", [(0.8, [0.0, 0.3, 0.6]), (0.35, [0.2, 0.0, 0.1]), (0.0, [0.0] * 3)])
+def test_stack_lookahead_breadth(hip, dev, interest, heat):
+    """The interest-weighted lookahead breadth: each token through a fresh
+    cache with a slot for every expert, so every hinted expert of the next
+    layer is admitted and none is there yet; the prefetches issued must be
+    the sum over layers of the breadth restated here (tlm_model.c:863-874)
+    from the hint's routing, with the instinct state carried from token to
+    token."""
+    from tierlm_amd import MoeStack
+    cases = three_layers(dev)
+    L, k, hk = len(cases), cases[0].k, 10
+    blocks = [store_block(c, dev) for c in cases]
+    stack = MoeStack(blocks, lookahead=1, lookahead_k=hk, interest=interest, heat=heat)
+    instinct, seen = np.zeros(L), np.zeros(L, np.int64)
+    rng = np.random.default_rng(9)
+    for t in range(3):
+        store = open_store(cases, L * cases[0].E, 1)
+        try:
+            h0 = rng.standard_normal(512).astype(np.float32)
+            h_res = torch.from_numpy(h0.copy()).to(dev)
+            want = 0
+            for layer, case in enumerate(cases):
+                if layer + 1 < L:   # the hint reads the residual before this layer's update
+                    hw = hint_weights(blocks[layer + 1], hk, h_res, dev)
+                    want += breadth(hw, hk, k, interest, instinct[layer + 1], seen[layer + 1], heat[layer + 1])
+                case.block(h_res)
+                w = case.block.w.cpu().numpy()[:k].astype(np.float64)
+                instinct[layer] += (w[0] / w.sum() - instinct[layer]) * 0.05
+                seen[layer] += 1
+            h_st = torch.from_numpy(h0.copy()).to(dev)
+            stack(store, h_st)
+            store.settle()
+            got = store.stats()["prefetch_issued"]
+            assert got == want, (t, got, want)
+            if interest == 0.0:
+                assert want == (L - 1) * hk
+        finally:
+            store.close()

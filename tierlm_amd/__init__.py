@@ -6,4 +6,4 @@ importing fails if the library is not built.
 """
 from ._lib import EXPORTS, LIB_PATH, HipError, lib  # noqa: F401
 from . import quant  # noqa: F401
-from .moe import MoeBlock  # noqa: F401
+from .moe import MoeBlock, MoeStack  # noqa: F401

@@ -64,6 +64,12 @@ class StoreStats(C.Structure):
                 ("in_use", C.c_int32)]
 
 
+class StackOpts(C.Structure):
+    """tlm_hip_stack_opts"""
+    _fields_ = [("lookahead", C.c_int32), ("lookahead_k", C.c_int32), ("interest", C.c_double),
+                ("layer_heat", C.c_void_p), ("instinct", C.c_void_p), ("instinct_seen", C.c_void_p)]
+
+
 class MoeHint(C.Structure):
     """tlm_hip_moe_hint"""
     _fields_ = [("desc", C.POINTER(MoeDesc)), ("layer", C.c_int32), ("workspace", vp)]
@@ -179,6 +185,8 @@ _SIGS = {
     "tlm_hip_crc32c": (C.c_uint32, [C.c_uint32, vp, sz]),
     "tlm_hip_sha256": (None, [vp, sz, vp]),
     "tlm_hip_moe_layer_store": (i32, [C.POINTER(MoeDesc), vp, i32, vp, vp, vp, C.POINTER(MoeHint), i32, vp, vp]),
+    "tlm_hip_moe_stack_workspace_bytes": (sz, [C.POINTER(MoeDesc), i32, C.POINTER(StackOpts)]),
+    "tlm_hip_moe_stack_store": (i32, [C.POINTER(MoeDesc), i32, vp, vp, C.POINTER(StackOpts), vp, vp, vp, vp]),
 }
 
 for _name, (_res, _args) in _SIGS.items():

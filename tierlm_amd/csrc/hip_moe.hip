@@ -310,16 +310,12 @@ __device__ __forceinline__ float reduce32(float r) {
 
 /* blockIdx.y = token: its residual at hptr + y * D, its workspace at
  * ws + y * tstride (the decode launches have one token). */
-__global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
-                                                   uint8_t *ws, size_t tstride) {
+__device__ __forceinline__ void router_body(const tlm_hip_moe_desc &d, const WsLayout &L, const float *__restrict__ hptr,
+                                            uint8_t *ws, const int blk) {
     extern __shared__ __align__(16) uint8_t lds[];
-    args_now(d.D, d.E, d.eps, d.router_w, d.ffn_norm, d.ds, d.expert_dt, d.shared_dt, d.shared_gate_inp, L.logits,
-             L.xb, L.xe, L.xs, L.route, hptr, ws, tstride, blockDim.x, gridDim.x);
-    hptr += (size_t)blockIdx.y * d.D;
-    ws += (size_t)blockIdx.y * tstride;
     const int lane = threadIdx.x, hl = lane & 31;
     const int64_t D = d.D;
-    const int64_t row = (int64_t)blockIdx.x * 2 + (lane >> 5);
+    const int64_t row = (int64_t)blk * 2 + (lane >> 5);
     const bool live = row < d.E;
     const GAS float *wr = (const GAS float *)d.router_w + (live ? row : 0) * D;
     const GAS f32x4 *h4 = (const GAS f32x4 *)hptr, *n4 = (const GAS f32x4 *)d.ffn_norm;
@@ -435,7 +431,7 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
 
     /* group b quantises activation block b for the experts / shared expert
      * into the split layout the gate/up launch copies straight into LDS */
-    const int b = blockIdx.x;
+    const int b = blk;
 #pragma unroll 1
     for (int which = 0; which < (d.ds > 0 ? 2 : 1); which++) {
         const int kind = dt_act_kind(which ? d.shared_dt : d.expert_dt), bv = bvals(kind);
@@ -466,6 +462,29 @@ __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout 
             if (lane == 0) *(GAS float *)ws_sgate(ws, L) = g;
         }
     }
+}
+
+__global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
+                                                   uint8_t *ws, size_t tstride) {
+    args_now(d.D, d.E, d.eps, d.router_w, d.ffn_norm, d.ds, d.expert_dt, d.shared_dt, d.shared_gate_inp, L.logits,
+             L.xb, L.xe, L.xs, L.route, hptr, ws, tstride, blockDim.x, gridDim.x);
+    router_body(d, L, hptr + (size_t)blockIdx.y * d.D, ws + (size_t)blockIdx.y * tstride, blockIdx.x);
+}
+
+/* Several routers over the same residual in one launch (a block's and its
+ * lookahead hints'): blockIdx.y picks the router, each with its own
+ * descriptor, workspace and group count. */
+constexpr int MULTI_ROUTES = 8;
+struct RouterSet {
+    tlm_hip_moe_desc d[MULTI_ROUTES];
+    WsLayout L[MULTI_ROUTES];
+    uint8_t *ws[MULTI_ROUTES];
+    int groups[MULTI_ROUTES];
+};
+__global__ __launch_bounds__(64) void k_moe_router_multi(const RouterSet S, const float *__restrict__ h) {
+    const int i = blockIdx.y;
+    if ((int)blockIdx.x >= S.groups[i]) return;
+    router_body(S.d[i], S.L[i], h, S.ws[i], blockIdx.x);
 }
 
 inline int router_groups(const tlm_hip_moe_desc &d) {
@@ -564,7 +583,7 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
 
 template <int EDT, int SDT>
 __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout L, int32_t *ids_out, float *w_out,
-                                                    uint8_t *ws) {
+                                                    uint8_t *ws, const MoeGiven gv) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ RouteLds s_route;
     args_now(d.D, d.de, d.ds, d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, d.experts, L.logits, L.route,
@@ -581,6 +600,18 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
         }
     }
     const int r = (int)blockIdx.x / te, t = (int)blockIdx.x - r * te;
+    if (gv.on) {   /* routing and matrices given: the weight loads go out at once */
+        if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
+            const int q = threadIdx.x;
+            ws_ids(ws, L)[q] = gv.ids[q];
+            ws_w(ws, L)[q] = gv.w[q];
+            if (ids_out) ids_out[q] = gv.ids[q];
+            if (w_out) w_out[q] = gv.w[q];
+        }
+        gateup_tile<EDT>(d, gv.p[3 * r], gv.p[3 * r + 1], ws + L.xe, d.de, t, (float *)(ws + L.hh) + (size_t)r * d.de,
+                         lds);
+        return;
+    }
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
     /* every expert's gate / up matrix, loaded with the logits and parked in
      * LDS during routing, so the chosen one costs no extra round trip */
@@ -702,7 +733,7 @@ __host__ __device__ inline size_t down_lds_part(int kind, int nq) {
 
 template <int EDT, int SDT>
 __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h,
-                                                  uint8_t *ws) {
+                                                  uint8_t *ws, const MoeGiven gv) {
     extern __shared__ __align__(16) uint8_t lds[];
     args_now(d.D, d.de, d.ds, d.E, d.k, d.experts, L.route, L.hh, h, ws, blockDim.x, gridDim.x);
     if constexpr (SDT != NONE) args_now(d.sd);
@@ -725,11 +756,13 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
     __shared__ float s_w[MAXK];
     __shared__ float s_out[(MAXK + 1) * DROWS];
     const int tid = threadIdx.x;
-    const int eid = tid < k ? ((const GAS int32_t *)ws_ids(ws, L))[tid] : 0;
-    const uint8_t *tab = tid < d.E ? (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * tid + 2] : nullptr;
+    const bool given = gv.on;
+    const int eid = tid < k && !given ? ((const GAS int32_t *)ws_ids(ws, L))[tid] : 0;
+    const uint8_t *tab =
+        tid < d.E && !given ? (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * tid + 2] : nullptr;
     /* the combine's inputs, loaded before anything waits; w reaches LDS only
      * after the rows are done, so no wave stalls on it early */
-    const float wl = tid < k ? ((const GAS float *)ws_w(ws, L))[tid] : 0.0f;
+    const float wl = tid < k ? (given ? gv.w[tid] : ((const GAS float *)ws_w(ws, L))[tid]) : 0.0f;
     float hv = 0.0f, sg = 0.0f;
     if (tid < DROWS) {
         hv = h[row0 + tid];
@@ -741,8 +774,8 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
         __syncthreads();
     };
     const Park pe = park_at(lds + ((stage_bytes(ek, k * nbe) + 15) & ~(size_t)15), k * nbe * DROWS);
-    down_rows<EDT>(k, [&](int r) { return s_tab[s_eid[r]]; }, table, (const float *)(ws + L.hh), d.de, d.D, row0, lds,
-                   pe);
+    down_rows<EDT>(k, [&](int r) { return given ? gv.p[3 * r + 2] : s_tab[s_eid[r]]; }, table,
+                   (const float *)(ws + L.hh), d.de, d.D, row0, lds, pe);
     Park ps = pe;
     int nbs = 0;
     if constexpr (SDT != NONE) {
@@ -983,6 +1016,36 @@ __global__ __launch_bounds__(256) void k_moe_route(tlm_hip_moe_desc d, WsLayout 
     }
 }
 
+/* The routing of several routers (group i: router i's logits in its
+ * workspace) straight into a page-locked host area: ids int32[32] at 256 i,
+ * w f32[32] at 256 i + 128, then the route's sequence word at seq_off + 4 i,
+ * stored after a system-scope fence so that the host sees the routing first. */
+struct RouteSet {
+    tlm_hip_moe_desc d[MULTI_ROUTES];
+    WsLayout L[MULTI_ROUTES];
+    uint8_t *ws[MULTI_ROUTES];
+};
+__global__ __launch_bounds__(256) void k_moe_route_host(const RouteSet S, uint32_t *host, int seq_off, uint32_t seq) {
+    __shared__ RouteLds s_route;
+    const int i = blockIdx.x;
+    const tlm_hip_moe_desc &d = S.d[i];
+    LAS RouteLds *R = (LAS RouteLds *)&s_route;
+    route_group(d, (const GAS float *)(S.ws[i] + S.L[i].logits), R, []() {});
+    const int q = threadIdx.x;
+    if (q < 32) {
+        const bool on = q < d.k;
+        host[64 * i + q] = on ? (uint32_t)R->ids[q] : 0u;
+        host[64 * i + 32 + q] = on ? __float_as_uint(R->w[q]) : 0u;
+        if (on) {
+            ws_ids(S.ws[i], S.L[i])[q] = R->ids[q];
+            ws_w(S.ws[i], S.L[i])[q] = R->w[q];
+        }
+    }
+    __threadfence_system();
+    __syncthreads();
+    if (q == 0) __hip_atomic_store(host + seq_off / 4 + i, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 /* One group: slots grouped by expert (order within an expert is free - every
  * slot is computed on its own), and the tile table of 32-slot runs. */
 __global__ __launch_bounds__(256) void k_pf_bucket(tlm_hip_moe_desc d, PfLayout P, uint8_t *ws) {
@@ -1197,8 +1260,8 @@ __global__ __launch_bounds__(256) void k_pf_combine(tlm_hip_moe_desc d, PfLayout
 }
 
 /* ---- instantiation table: [expert dtype][shared dtype or none] --------------- */
-typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *);
-typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *);
+typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *, const MoeGiven);
+typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *, const MoeGiven);
 
 inline int dt_slot(int dt) { return dt == DT_Q6_K ? 0 : dt == DT_Q8_0 ? 1 : dt == DT_Q4_K ? 2 : dt == DT_Q5_K ? 3 : -1; }
 
@@ -1253,9 +1316,10 @@ static int moe_check(const tlm_hip_moe_desc *d, const float *h, const void *ws) 
     return TLM_HIP_OK;
 }
 
-/* phase 0 = all launches; 1 router, 2 gate/up, 3 down + combine */
-int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
-                     hipStream_t s) {
+/* phase 0 = all launches; 1 router, 2 gate/up, 3 down + combine; gv (may be
+ * NULL): routing and matrices given by the caller */
+static int moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
+                     const MoeGiven *gvp, hipStream_t s) {
     if (phase < 0 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
     if (int rc = moe_check(d, h, ws)) return rc;
     const int ebv = dt_block_values(d->expert_dt);
@@ -1284,9 +1348,24 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const unsigned g3 = (unsigned)(d->D / DROWS);
     if (phase == 0 || phase == 1)
         hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8, (size_t)0);
-    if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8);
-    if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(256), lds3, s, dv, L, h, w8);
+    MoeGiven gv{};
+    if (gvp) gv = *gvp;
+    if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8, gv);
+    if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(256), lds3, s, dv, L, h, w8, gv);
     return tlmh_check(hipGetLastError(), "moe_layer launch");
+}
+int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
+                     hipStream_t s) {
+    return moe_phase(d, phase, h, ids, w, ws, nullptr, s);
+}
+int launch_moe_phase_given(const tlm_hip_moe_desc *d, int phase, float *h, void *ws, const MoeGiven *gv,
+                           hipStream_t s) {
+    if (!gv || d->k > 32) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: given routing");
+    for (int r = 0; r < d->k; r++)
+        for (int m = 0; m < 3; m++)
+            if (!gv->p[3 * r + m] || ((uintptr_t)gv->p[3 * r + m] & 15u))
+                return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: given matrix %d of rank %d", m, r);
+    return moe_phase(d, phase, h, nullptr, nullptr, ws, gv, s);
 }
 
 /* The router launch, then routing alone: ids / w (k each) in the workspace's
@@ -1295,6 +1374,30 @@ int launch_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, fl
     if (int rc = launch_moe_phase(d, 1, (float *)h, nullptr, nullptr, ws, s)) return rc;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, s, *d, ws_layout(*d), (uint8_t *)ws, ids, w);
     return tlmh_check(hipGetLastError(), "moe_route launch");
+}
+
+/* The routers of d[0..n) over the same residual h (one launch), then their
+ * routing into the host area (one launch, see k_moe_route_host) */
+int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, int n, const float *h,
+                           uint32_t *host, int seq_off, uint32_t seq, hipStream_t s) {
+    if (n < 1 || n > MULTI_ROUTES) return tlmh_seterr(TLM_HIP_EINVAL, "moe routes: %d routers", n);
+    RouterSet rs{};
+    RouteSet qs{};
+    int g = 0;
+    size_t lds = 0;
+    for (int i = 0; i < n; i++) {
+        if (int rc = moe_check(d[i], h, ws[i])) return rc;
+        rs.d[i] = qs.d[i] = *d[i];
+        rs.L[i] = qs.L[i] = ws_layout(*d[i]);
+        rs.ws[i] = qs.ws[i] = (uint8_t *)ws[i];
+        rs.groups[i] = router_groups(*d[i]);
+        g = rs.groups[i] > g ? rs.groups[i] : g;
+        lds = al256((size_t)d[i]->D * 8) > lds ? al256((size_t)d[i]->D * 8) : lds;
+    }
+    if (lds > 64 * 1024) return tlmh_seterr(TLM_HIP_EUNSUP, "moe routes: D exceeds the LDS staging limit");
+    hipLaunchKernelGGL(k_moe_router_multi, dim3((unsigned)g, (unsigned)n), dim3(64), lds, s, rs, h);
+    hipLaunchKernelGGL(k_moe_route_host, dim3((unsigned)n), dim3(256), 0, s, qs, host, seq_off, seq);
+    return tlmh_check(hipGetLastError(), "moe routes launch");
 }
 
 size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T) {

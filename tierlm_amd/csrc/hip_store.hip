@@ -55,6 +55,11 @@ constexpr int NLOAD = 2;             /* load streams: consecutive loads overlap 
 constexpr size_t MAT_ALIGN = 256;
 constexpr int MAX_HINTS = 7;         /* lookahead layers per tlm_hip_moe_layer_store call */
 constexpr int ROUTE_BYTES = 256;     /* ids int32[32] at +0, w f32[32] at +128 (moe_route_offset) */
+/* a route area: the block's and its hints' routes, then the sequence word the
+ * export stores last; two areas, so the host reads one layer's routes while
+ * the next layer's export lands in the other */
+constexpr int ROUTE_AREA = ROUTE_BYTES * (1 + MAX_HINTS) + 64;
+constexpr int ROUTE_SEQ = ROUTE_BYTES * (1 + MAX_HINTS);   /* byte offset of the sequence word */
 constexpr int MOE_MAXK = 32;
 
 struct Expert {
@@ -118,8 +123,10 @@ struct tlm_hip_store {
     uint64_t clock = 0, ticks = 0;
     int loading = 0, demand_loading = 0, hint_loading = 0, n_pinned = 0;
     tlm_hip_store_stats st{};
-    uint8_t *route_host = nullptr;      /* pinned: routing results of tlm_hip_moe_layer_store */
+    uint8_t *route_host = nullptr;      /* pinned: two route areas (ROUTE_AREA bytes each) */
     uint32_t *route_dev = nullptr;      /* route_host as the device addresses it (mapped, coherent) */
+    uint32_t route_seq = 0;             /* the last export's sequence number */
+    int route_n[2] = {0, 0};            /* routes in each area */
     /* release points: an event recorded on a release stream when a load first
      * needs one, shared by every load that needs a point on that stream
      * before the next release; reused once no queued load waits for it */
@@ -564,10 +571,11 @@ int tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store
             s->stage_dev[i] = (const uint8_t *)dp;
             if (!rc) rc = tlmh_check(hipEventCreateWithFlags(&s->stage_packed[i], hipEventDisableTiming), "store: event");
         }
-        /* mapped and coherent: k_route_export stores the routing straight into it, and the stream
-         * synchronisation that follows makes those stores visible to the host */
-        if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->route_host, ROUTE_BYTES * (1 + MAX_HINTS),
+        /* mapped and coherent: k_moe_route_host stores the routing straight into it, its sequence
+         * word last; the host waits for that word instead of synchronising the stream */
+        if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->route_host, 2 * ROUTE_AREA,
                                                hipHostMallocMapped | hipHostMallocCoherent), "store: routing scratch");
+        if (!rc) memset(s->route_host, 0, 2 * ROUTE_AREA);
         if (!rc) rc = tlmh_check(hipHostGetDevicePointer((void **)&s->route_dev, s->route_host, 0),
                                  "store: routing scratch address");
         if (!rc) s->loader = std::thread([s] { s->loader_main(); });
@@ -858,30 +866,80 @@ void tlm_hip_store_get_stats(tlm_hip_store *s, tlm_hip_store_stats *out) {
 /* ---- one MoE block through the cache -------------------------------------- */
 namespace {
 
-constexpr int TS_MAX = 3 * MOE_MAXK;
 
-struct TableSet {
-    int32_t n;
-    int32_t idx[TS_MAX];
-    const void *ptr[TS_MAX];
-};
-
-/* table[idx[i]] = ptr[i]: the routed experts' gate / up / down entries */
-/* Route areas of the block and its hints -> route_host, ROUTE_BYTES each, in one launch (one
- * dword per thread, vector stores over PCIe) instead of 1 + n_hints device-to-host copies. */
-struct RouteSrc {
-    const uint32_t *src[1 + MAX_HINTS];
-};
-constexpr int ROUTE_DW = ROUTE_BYTES / 4;
-
-__global__ __launch_bounds__(ROUTE_DW * (1 + MAX_HINTS)) void k_route_export(uint32_t *dst, RouteSrc r, int n) {
-    const int i = threadIdx.x / ROUTE_DW, j = threadIdx.x % ROUTE_DW;
-    if (i < n) dst[i * ROUTE_DW + j] = r.src[i][j];
+/* the block's route and its hints' routes from h (the residual before the
+ * block's update): their routers in one launch, then their routing into route
+ * area `area` of the host under a new sequence number (returned in *seq) */
+int enqueue_routes(tlm_hip_store *s, const tlm_hip_moe_desc *d, float *h, void *ws, const tlm_hip_moe_desc *hd,
+                   void *const *hws, int n_hints, int area, uint32_t *seq, hipStream_t st) {
+    const tlm_hip_moe_desc *ds[1 + MAX_HINTS];
+    void *wss[1 + MAX_HINTS];
+    ds[0] = d;
+    wss[0] = ws;
+    for (int i = 0; i < n_hints; i++) {
+        ds[1 + i] = &hd[i];
+        wss[1 + i] = hws[i];
+    }
+    *seq = ++s->route_seq;
+    s->route_n[area] = 1 + n_hints;
+    return launch_moe_routes_host(ds, wss, 1 + n_hints, h, s->route_dev + area * (ROUTE_AREA / 4), ROUTE_SEQ, *seq,
+                                  st);
 }
 
-__global__ __launch_bounds__(128) void k_table_set(const void **table, TableSet t) {
-    const int i = threadIdx.x;
-    if (i < t.n) table[t.idx[i]] = t.ptr[i];
+/* wait (spinning, no stream synchronisation) until every route of area
+ * `area` carries sequence number seq; a stream error or a minute without
+ * them is an error */
+int wait_routes(tlm_hip_store *s, int area, uint32_t seq, hipStream_t st) {
+    const uint32_t *w = (const uint32_t *)(s->route_host + (size_t)area * ROUTE_AREA + ROUTE_SEQ);
+    const int n = s->route_n[area];
+    auto arrived = [&] {
+        for (int i = 0; i < n; i++)
+            if (__atomic_load_n(w + i, __ATOMIC_ACQUIRE) != seq) return false;
+        return true;
+    };
+    const int64_t t0 = now_ns();
+    for (uint64_t i = 0;; i++) {
+        if (arrived()) return TLM_HIP_OK;
+        if ((i & 4095) == 4095) {
+            const hipError_t e = hipStreamQuery(st);
+            if (e != hipSuccess && e != hipErrorNotReady) return tlmh_check(e, "moe_layer_store: stream");
+            if (e == hipSuccess && !arrived())
+                return tlmh_seterr(TLM_HIP_EIO, "moe_layer_store: the routing export did not arrive");
+            if (now_ns() - t0 > 60ll * 1000000000ll)
+                return tlmh_seterr(TLM_HIP_EIO, "moe_layer_store: no routing export after 60 s");
+        }
+        __builtin_ia32_pause();
+    }
+}
+
+/* acquire the routed experts (ids[0..k), weights w), make the stream wait
+ * for loads in flight and enqueue phases 2 and 3 on the slots' matrices;
+ * refs hold the references (released by the caller, also on an error) */
+int run_block(tlm_hip_store *s, const tlm_hip_moe_desc *d, int layer, const int *ids, const float *w, float *h,
+              void *ws, tlm_hip_expert_ref *refs, hipStream_t st) {
+    const int k = d->k;
+    for (int r = 0; r < k; r++) {
+        refs[r] = tlm_hip_expert_ref{};
+        refs[r].slot = -1;
+    }
+    for (int r = 0; r < k; r++)   /* the table write below indexes 3 * id + m */
+        if (ids[r] < 0 || ids[r] >= d->E)
+            return tlmh_seterr(TLM_HIP_EIO, "moe_layer_store: routing produced expert %d of %d", ids[r], d->E);
+    int rc = tlm_hip_store_acquire(s, layer, ids, k, refs);
+    if (rc) return rc;
+    /* the routing and the slots' matrices go to the block as launch
+     * arguments: its weight loads start at once, no table is written */
+    MoeGiven gv{};
+    gv.on = 1;
+    for (int r = 0; r < k; r++) {
+        gv.ids[r] = ids[r];
+        gv.w[r] = w[r];
+        for (int m = 0; m < 3; m++) gv.p[3 * r + m] = (const uint8_t *)refs[r].mats[m];
+    }
+    for (int r = 0; r < k && !rc; r++) rc = tlm_hip_store_stream_wait(s, &refs[r], st);
+    if (!rc) rc = launch_moe_phase_given(d, 2, h, ws, &gv, st);
+    if (!rc) rc = launch_moe_phase_given(d, 3, h, ws, &gv, st);
+    return rc;
 }
 
 }  // namespace
@@ -917,59 +975,149 @@ int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int lay
     hipStream_t st = (hipStream_t)stream;
     /* every route first (the hints read the same residual, before this
      * block's update), then one round trip for all of them */
-    int rc = launch_moe_route(d, h, nullptr, nullptr, workspace, st);
-    if (rc) return rc;
-    RouteSrc rs{};
-    rs.src[0] = (const uint32_t *)((const uint8_t *)workspace + moe_route_offset(d));
+    tlm_hip_moe_desc hd[MAX_HINTS];
+    void *hws[MAX_HINTS];
     for (int i = 0; i < n_hints; i++) {
-        if ((rc = launch_moe_route(hints[i].desc, h, nullptr, nullptr, hints[i].workspace, st))) return rc;
-        rs.src[1 + i] = (const uint32_t *)((const uint8_t *)hints[i].workspace + moe_route_offset(hints[i].desc));
+        hd[i] = *hints[i].desc;
+        hws[i] = hints[i].workspace;
     }
-    for (int i = 0; i <= n_hints; i++)
-        if ((uintptr_t)rs.src[i] & 3u)
-            return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer_store: workspace %d is not 4-byte aligned", i);
-    hipLaunchKernelGGL(k_route_export, dim3(1), dim3(ROUTE_DW * (1 + MAX_HINTS)), 0, st, s->route_dev, rs,
-                       1 + n_hints);
-    HIPCHK(hipGetLastError());
-    HIPCHK(hipStreamSynchronize(st));
+    uint32_t seq = 0;
+    int rc = enqueue_routes(s, d, h, workspace, hd, hws, n_hints, 0, &seq, st);
+    if (!rc) rc = wait_routes(s, 0, seq, st);
+    if (rc) return rc;
     const int k = d->k;
     int ids[MOE_MAXK];
-    float w[MOE_MAXK];
     memcpy(ids, s->route_host, sizeof(int) * k);
-    memcpy(w, s->route_host + 128, sizeof(float) * k);
     if (ids_host) memcpy(ids_host, ids, sizeof(int) * k);
-    if (w_host) memcpy(w_host, w, sizeof(float) * k);
-    for (int r = 0; r < k; r++)   /* the table write below indexes 3 * id + m */
-        if (ids[r] < 0 || ids[r] >= d->E)
-            return tlmh_seterr(TLM_HIP_EIO, "moe_layer_store: routing produced expert %d of %d", ids[r], d->E);
-
+    if (w_host) memcpy(w_host, s->route_host + 128, sizeof(float) * k);
     tlm_hip_expert_ref refs[MOE_MAXK];
-    auto release_all = [&] {
-        for (int r = 0; r < k; r++) tlm_hip_store_release(s, &refs[r], stream);
-    };
-    rc = tlm_hip_store_acquire(s, layer, ids, k, refs);
-    if (rc) {
-        release_all();
-        return rc;
-    }
-    TableSet t{};
-    for (int r = 0; r < k; r++)
-        for (int m = 0; m < 3; m++) {
-            t.idx[t.n] = 3 * ids[r] + m;
-            t.ptr[t.n] = refs[r].mats[m];
-            t.n++;
-        }
-    hipLaunchKernelGGL(k_table_set, dim3(1), dim3(128), 0, st, (const void **)d->experts, t);
-    rc = tlmh_check(hipGetLastError(), "moe_layer_store: table");
-    for (int r = 0; r < k && !rc; r++) rc = tlm_hip_store_stream_wait(s, &refs[r], stream);
-    if (!rc) rc = launch_moe_phase(d, 2, h, nullptr, nullptr, workspace, st);
-    if (!rc) rc = launch_moe_phase(d, 3, h, nullptr, nullptr, workspace, st);
+    float w[MOE_MAXK];
+    memcpy(w, s->route_host + 128, sizeof(float) * k);
+    rc = run_block(s, d, layer, ids, w, h, workspace, refs, st);
     /* hints while this block's experts still hold references (:988-990), issued after the block's
      * launches so that the loader's bookkeeping is off the path to them */
     for (int i = 0; i < n_hints && !rc; i++)
         tlm_hip_store_prefetch(s, hints[i].layer, (const int *)(s->route_host + ROUTE_BYTES * (1 + i)),
                                hints[i].desc->k);
-    release_all();
+    for (int r = 0; r < k; r++) tlm_hip_store_release(s, &refs[r], stream);
+    return rc;
+}
+
+/* the lookahead's workspaces after the two block workspaces, each 256-byte
+ * aligned: block[2], then hint[2][depth] */
+static void stack_layout(const tlm_hip_moe_desc *descs, int n, int depth, int lk, size_t *blk, size_t *hint) {
+    size_t b = 0, hb = 0;
+    for (int l = 0; l < n; l++) {
+        b = std::max(b, moe_workspace_bytes(&descs[l]));
+        if (depth > 0) {
+            tlm_hip_moe_desc d = descs[l];
+            d.k = lk > 0 ? std::min(lk, d.E) : d.k;
+            hb = std::max(hb, moe_workspace_bytes(&d));
+        }
+    }
+    *blk = align_up(b, 256);
+    *hint = align_up(hb, 256);
+}
+
+static int stack_depth(const tlm_hip_stack_opts *o) {
+    const int d = o ? o->lookahead : 0;
+    return d < 0 ? 0 : d > MAX_HINTS ? MAX_HINTS : d;
+}
+
+size_t tlm_hip_moe_stack_workspace_bytes(const tlm_hip_moe_desc *descs, int n_layers, const tlm_hip_stack_opts *o) {
+    if (!descs || n_layers <= 0) return 0;
+    size_t b, hb;
+    const int depth = stack_depth(o);
+    stack_layout(descs, n_layers, depth, o ? o->lookahead_k : 0, &b, &hb);
+    return 2 * b + 2 * (size_t)depth * hb;
+}
+
+/* tlm_model_step's loop over moe() with the store (src/lib/tlm_model.c:
+ * 1075-1083, 960-1055), lookahead() (:844-877) and the instinct update
+ * (:974-980), then tlm_store_tick (:1097); pipelined as described in
+ * tlm_hip.h. */
+int tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
+                            const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace,
+                            void *stream) {
+    if (!descs || n_layers <= 0 || !s || !h || !workspace)
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: bad arguments");
+    if ((uintptr_t)workspace & 255u)
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: workspace must be 256-byte aligned");
+    for (int l = 0; l < n_layers; l++)
+        if (descs[l].k <= 0 || descs[l].k > MOE_MAXK || !descs[l].experts)
+            return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: layer %d (k=%d)", l, descs[l].k);
+    if (o && o->lookahead > 0 && o->lookahead_k > MOE_MAXK)
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: lookahead_k %d above %d", o->lookahead_k, MOE_MAXK);
+    const int depth = stack_depth(o), lk = o ? o->lookahead_k : 0;
+    size_t bsz, hsz;
+    stack_layout(descs, n_layers, depth, lk, &bsz, &hsz);
+    uint8_t *base = (uint8_t *)workspace;
+    void *blk[2] = {base, base + bsz};
+    void *hws[2][MAX_HINTS];
+    for (int p = 0; p < 2; p++)
+        for (int i = 0; i < depth; i++) hws[p][i] = base + 2 * bsz + ((size_t)p * depth + i) * hsz;
+    hipStream_t st = (hipStream_t)stream;
+    tlm_hip_moe_desc hd[MAX_HINTS];
+    int nh = 0;
+    /* layer l's routes (block + hints for l+1 .. l+depth) into area l mod 2 */
+    auto enqueue = [&](int l, uint32_t *seq) {
+        nh = std::min(depth, n_layers - 1 - l);
+        for (int i = 0; i < nh; i++) {
+            hd[i] = descs[l + 1 + i];
+            hd[i].k = lk > 0 ? std::min(lk, hd[i].E) : hd[i].k;
+        }
+        return enqueue_routes(s, &descs[l], h, blk[l & 1], hd, hws[l & 1], nh, l & 1, seq, st);
+    };
+    uint32_t seq = 0;
+    int rc = enqueue(0, &seq);
+    for (int l = 0; l < n_layers && !rc; l++) {
+        const int hints_here = nh;   /* the hints routed with this layer */
+        tlm_hip_moe_desc hdl[MAX_HINTS];
+        for (int i = 0; i < hints_here; i++) hdl[i] = hd[i];
+        if ((rc = wait_routes(s, l & 1, seq, st))) break;
+        const uint8_t *area = s->route_host + (size_t)(l & 1) * ROUTE_AREA;
+        const int k = descs[l].k;
+        int ids[MOE_MAXK];
+        float w[MOE_MAXK];
+        memcpy(ids, area, sizeof(int) * k);
+        memcpy(w, area + 128, sizeof(float) * k);
+        if (ids_out) memcpy(ids_out + (size_t)l * k, ids, sizeof(int) * k);
+        if (w_out) memcpy(w_out + (size_t)l * k, w, sizeof(float) * k);
+        if (o && o->instinct && o->instinct_seen) {   /* tlm_model.c:974-980 */
+            double sw = 0.0;
+            for (int r = 0; r < k; r++) sw += (double)w[r];
+            const double share = sw > 0.0 ? (double)w[0] / sw : 0.0;
+            o->instinct[l] += (share - o->instinct[l]) * 0.05;
+            o->instinct_seen[l]++;
+        }
+        tlm_hip_expert_ref refs[MOE_MAXK];
+        rc = run_block(s, &descs[l], l, ids, w, h, blk[l & 1], refs, st);
+        /* the next layer's routing queued behind this block, before the host's bookkeeping */
+        if (!rc && l + 1 < n_layers) rc = enqueue(l + 1, &seq);
+        /* lookahead() for layers l+1 .. l+depth while this block's experts hold their
+         * references (:988-990), the breadth interest-weighted (:863-874) */
+        for (int i = 0; i < hints_here && !rc; i++) {
+            const int tl = l + 1 + i, hk = hdl[i].k, top = descs[tl].k;
+            const int32_t *hid = (const int32_t *)(area + ROUTE_BYTES * (1 + i));
+            const float *hw = (const float *)(area + ROUTE_BYTES * (1 + i) + 128);
+            int kk = hk;
+            if (o && o->interest > 0.0 && hk > top) {
+                double sw = 0.0;
+                for (int r = 0; r < hk; r++) sw += (double)hw[r];
+                const double now = sw > 0.0 ? (double)hw[0] / sw : 0.0;
+                const bool seen = o->instinct_seen && o->instinct && o->instinct_seen[tl];
+                const double I = seen ? 0.5 * (now + o->instinct[tl]) : now;
+                const double Hh = o->layer_heat ? (double)o->layer_heat[tl] : 0.0;
+                double W = o->interest * (1.0 - I) * (1.0 - Hh);
+                W = W < 0.0 ? 0.0 : W > 1.0 ? 1.0 : W;
+                kk = top + (int)(W * (double)(hk - top) + 0.5);
+                kk = std::min(kk, hdl[i].E);
+            }
+            tlm_hip_store_prefetch(s, tl, (const int *)hid, kk);
+        }
+        for (int r = 0; r < k; r++) tlm_hip_store_release(s, &refs[r], stream);
+    }
+    if (!rc) tlm_hip_store_tick(s);
     return rc;
 }
 

@@ -251,5 +251,19 @@ int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
                      hipStream_t s);
 int launch_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, float *w, void *ws, hipStream_t s);
 size_t moe_route_offset(const tlm_hip_moe_desc *d);
+/* The routing of a block and its routed experts' packed matrices, given by
+ * the caller (the slot cache knows them before the block runs): rank r's
+ * gate / up / down at p[3r], p[3r + 1], p[3r + 2].  on = 0: the block routes
+ * itself and reads its expert table. */
+struct MoeGiven {
+    const uint8_t *p[3 * 32];
+    float w[32];
+    int32_t ids[32];
+    int32_t on;
+};
+int launch_moe_phase_given(const tlm_hip_moe_desc *d, int phase, float *h, void *ws, const MoeGiven *gv,
+                           hipStream_t s);
+int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, int n, const float *h,
+                           uint32_t *host, int seq_off, uint32_t seq, hipStream_t s);
 
 #endif

@@ -10,7 +10,9 @@ import ctypes as C
 
 import torch
 
-from ._lib import MoeDesc, MoeHint, check, lib
+import numpy as np
+
+from ._lib import MoeDesc, MoeHint, StackOpts, check, lib
 from .quant import stream
 
 
@@ -106,3 +108,37 @@ class MoeBlock:
     def set_expert_ptrs(self, expert_ptrs):
         """Point the block at another set of packed experts (same geometry)."""
         self.table.copy_(torch.tensor(list(expert_ptrs), dtype=torch.int64))
+
+
+class MoeStack:
+    """The routed MoE blocks of a stack of layers run for a token through the
+    slot cache in one call (tlm_hip_moe_stack_store): blocks[l] is layer l,
+    `lookahead` layers ahead are hinted with lookahead_k experts each, the
+    breadth interest-weighted when interest > 0 (heat: per-layer floats or
+    None).  The instinct state per layer lives here, as the reference keeps it
+    in its model."""
+
+    def __init__(self, blocks, *, lookahead=1, lookahead_k=0, interest=0.0, heat=None):
+        n = len(blocks)
+        self.blocks = blocks
+        self.descs = (MoeDesc * n)(*[MoeDesc.from_buffer_copy(b.desc) for b in blocks])
+        self.instinct = np.zeros(n, np.float64)
+        self.seen = np.zeros(n, np.uint32)
+        self.heat = None if heat is None else np.ascontiguousarray(heat, np.float32)
+        self.opts = StackOpts(lookahead, lookahead_k, interest,
+                              None if self.heat is None else self.heat.ctypes.data,
+                              self.instinct.ctypes.data, self.seen.ctypes.data)
+        nbytes = int(lib.tlm_hip_moe_stack_workspace_bytes(self.descs, n, C.byref(self.opts)))
+        self.workspace = torch.empty(nbytes + 256, dtype=torch.uint8, device=blocks[0].workspace.device)
+        self._ws = (self.workspace.data_ptr() + 255) & ~255
+        k = blocks[0].desc.k
+        self.ids = np.zeros((n, k), np.int32)
+        self.w = np.zeros((n, k), np.float32)
+
+    def __call__(self, store, h):
+        """h += the stack's MoE blocks for one token; the routing lands in
+        self.ids / self.w [n_layers, top_k]."""
+        check(lib.tlm_hip_moe_stack_store(self.descs, len(self.blocks), store.h, C.c_void_p(h.data_ptr()),
+                                          C.byref(self.opts), self.ids.ctypes.data, self.w.ctypes.data,
+                                          C.c_void_p(self._ws), stream()))
+        return h
