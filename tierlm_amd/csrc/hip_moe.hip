@@ -26,6 +26,7 @@
  * order are the reference's; e^x (double exp rounded to float) and rmsnorm's
  * double sum of squares (a tree) are the device's. */
 #include "tlm_hip_internal.h"
+#include <type_traits>
 #include "tlm_hip_act.h"
 #include "tlm_hip_items.h"
 #include "tlm_hip_mfma.h"
@@ -581,9 +582,14 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
     }
 }
 
-template <int EDT, int SDT>
+/* GIVEN: the routing and the routed experts' matrices come as a launch
+ * argument (the slot cache's blocks); otherwise none is passed */
+struct NoGiven {};
+template <bool GIVEN> using GivenArg = typename std::conditional<GIVEN, MoeGiven, NoGiven>::type;
+
+template <int EDT, int SDT, bool GIVEN>
 __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout L, int32_t *ids_out, float *w_out,
-                                                    uint8_t *ws, const MoeGiven gv) {
+                                                    uint8_t *ws, const GivenArg<GIVEN> gv) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ RouteLds s_route;
     args_now(d.D, d.de, d.ds, d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, d.experts, L.logits, L.route,
@@ -600,7 +606,7 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
         }
     }
     const int r = (int)blockIdx.x / te, t = (int)blockIdx.x - r * te;
-    if (gv.on) {   /* routing and matrices given: the weight loads go out at once */
+    if constexpr (GIVEN) {   /* routing and matrices given: the weight loads go out at once */
         if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
             const int q = threadIdx.x;
             ws_ids(ws, L)[q] = gv.ids[q];
@@ -731,9 +737,9 @@ __host__ __device__ inline size_t down_lds_part(int kind, int nq) {
     return ((stage_bytes(kind, nq) + 15) & ~(size_t)15) + park_bytes(nq * DROWS);
 }
 
-template <int EDT, int SDT>
+template <int EDT, int SDT, bool GIVEN>
 __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h,
-                                                  uint8_t *ws, const MoeGiven gv) {
+                                                  uint8_t *ws, const GivenArg<GIVEN> gv) {
     extern __shared__ __align__(16) uint8_t lds[];
     args_now(d.D, d.de, d.ds, d.E, d.k, d.experts, L.route, L.hh, h, ws, blockDim.x, gridDim.x);
     if constexpr (SDT != NONE) args_now(d.sd);
@@ -756,13 +762,17 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
     __shared__ float s_w[MAXK];
     __shared__ float s_out[(MAXK + 1) * DROWS];
     const int tid = threadIdx.x;
-    const bool given = gv.on;
-    const int eid = tid < k && !given ? ((const GAS int32_t *)ws_ids(ws, L))[tid] : 0;
-    const uint8_t *tab =
-        tid < d.E && !given ? (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * tid + 2] : nullptr;
-    /* the combine's inputs, loaded before anything waits; w reaches LDS only
-     * after the rows are done, so no wave stalls on it early */
-    const float wl = tid < k ? (given ? gv.w[tid] : ((const GAS float *)ws_w(ws, L))[tid]) : 0.0f;
+    int eid = 0;
+    const uint8_t *tab = nullptr;
+    float wl = 0.0f;   /* the combine's inputs, loaded before anything waits; w reaches LDS only
+                        * after the rows are done, so no wave stalls on it early */
+    if constexpr (GIVEN) {
+        if (tid < k) wl = gv.w[tid];
+    } else {
+        eid = tid < k ? ((const GAS int32_t *)ws_ids(ws, L))[tid] : 0;
+        tab = tid < d.E ? (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * tid + 2] : nullptr;
+        wl = tid < k ? ((const GAS float *)ws_w(ws, L))[tid] : 0.0f;
+    }
     float hv = 0.0f, sg = 0.0f;
     if (tid < DROWS) {
         hv = h[row0 + tid];
@@ -774,8 +784,12 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
         __syncthreads();
     };
     const Park pe = park_at(lds + ((stage_bytes(ek, k * nbe) + 15) & ~(size_t)15), k * nbe * DROWS);
-    down_rows<EDT>(k, [&](int r) { return given ? gv.p[3 * r + 2] : s_tab[s_eid[r]]; }, table,
-                   (const float *)(ws + L.hh), d.de, d.D, row0, lds, pe);
+    if constexpr (GIVEN)
+        down_rows<EDT>(k, [&](int r) { return gv.p[3 * r + 2]; }, []() {}, (const float *)(ws + L.hh), d.de, d.D,
+                       row0, lds, pe);
+    else
+        down_rows<EDT>(k, [&](int r) { return s_tab[s_eid[r]]; }, table, (const float *)(ws + L.hh), d.de, d.D, row0,
+                       lds, pe);
     Park ps = pe;
     int nbs = 0;
     if constexpr (SDT != NONE) {
@@ -1260,16 +1274,22 @@ __global__ __launch_bounds__(256) void k_pf_combine(tlm_hip_moe_desc d, PfLayout
 }
 
 /* ---- instantiation table: [expert dtype][shared dtype or none] --------------- */
-typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *, const MoeGiven);
-typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *, const MoeGiven);
+typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *, const NoGiven);
+typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *, const NoGiven);
+typedef void (*gateup_given_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *, const MoeGiven);
+typedef void (*down_given_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *, const MoeGiven);
 
 inline int dt_slot(int dt) { return dt == DT_Q6_K ? 0 : dt == DT_Q8_0 ? 1 : dt == DT_Q4_K ? 2 : dt == DT_Q5_K ? 3 : -1; }
 
-#define ROW(K, E) {K<E, NONE>, K<E, DT_Q6_K>, K<E, DT_Q8_0>, K<E, DT_Q4_K>, K<E, DT_Q5_K>}
-const gateup_fn GU[4][5] = {ROW(k_moe_gateup, DT_Q6_K), ROW(k_moe_gateup, DT_Q8_0), ROW(k_moe_gateup, DT_Q4_K),
-                            ROW(k_moe_gateup, DT_Q5_K)};
-const down_fn DN[4][5] = {ROW(k_moe_down, DT_Q6_K), ROW(k_moe_down, DT_Q8_0), ROW(k_moe_down, DT_Q4_K),
-                          ROW(k_moe_down, DT_Q5_K)};
+#define ROW(K, E, G) {K<E, NONE, G>, K<E, DT_Q6_K, G>, K<E, DT_Q8_0, G>, K<E, DT_Q4_K, G>, K<E, DT_Q5_K, G>}
+const gateup_fn GU[4][5] = {ROW(k_moe_gateup, DT_Q6_K, false), ROW(k_moe_gateup, DT_Q8_0, false),
+                            ROW(k_moe_gateup, DT_Q4_K, false), ROW(k_moe_gateup, DT_Q5_K, false)};
+const down_fn DN[4][5] = {ROW(k_moe_down, DT_Q6_K, false), ROW(k_moe_down, DT_Q8_0, false),
+                          ROW(k_moe_down, DT_Q4_K, false), ROW(k_moe_down, DT_Q5_K, false)};
+const gateup_given_fn GUG[4][5] = {ROW(k_moe_gateup, DT_Q6_K, true), ROW(k_moe_gateup, DT_Q8_0, true),
+                                   ROW(k_moe_gateup, DT_Q4_K, true), ROW(k_moe_gateup, DT_Q5_K, true)};
+const down_given_fn DNG[4][5] = {ROW(k_moe_down, DT_Q6_K, true), ROW(k_moe_down, DT_Q8_0, true),
+                                 ROW(k_moe_down, DT_Q4_K, true), ROW(k_moe_down, DT_Q5_K, true)};
 #undef ROW
 
 }  // namespace
@@ -1348,10 +1368,16 @@ static int moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const unsigned g3 = (unsigned)(d->D / DROWS);
     if (phase == 0 || phase == 1)
         hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8, (size_t)0);
-    MoeGiven gv{};
-    if (gvp) gv = *gvp;
-    if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8, gv);
-    if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(256), lds3, s, dv, L, h, w8, gv);
+    if (gvp) {
+        const MoeGiven gv = *gvp;
+        if (phase == 0 || phase == 2)
+            hipLaunchKernelGGL(GUG[es][ss], dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8, gv);
+        if (phase == 0 || phase == 3) hipLaunchKernelGGL(DNG[es][ss], dim3(g3), dim3(256), lds3, s, dv, L, h, w8, gv);
+    } else {
+        if (phase == 0 || phase == 2) hipLaunchKernelGGL(gu, dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8,
+                                                         NoGiven{});
+        if (phase == 0 || phase == 3) hipLaunchKernelGGL(dn, dim3(g3), dim3(256), lds3, s, dv, L, h, w8, NoGiven{});
+    }
     return tlmh_check(hipGetLastError(), "moe_layer launch");
 }
 int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
