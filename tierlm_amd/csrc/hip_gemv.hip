@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ W
 
     const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS, t = blockIdx.x;
     const int64_t units = T * nb * TILE_ROWS;
-    const int round_items = (int)(blockDim.x / F::LPI) * IPL;
+    const int round_items = (GROUP_THREADS / F::LPI) * IPL;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += cap) {
         const int nbc = nb - b0 < cap ? nb - b0 : cap;
@@ -358,7 +358,7 @@ struct NormMap {
         const bool k8 = kind == DT_Q8_K;
         const int lpb = k8 ? 16 : 2;   /* lanes per block */
         bv = k8 ? 256 : 32;
-        per = (int)blockDim.x / lpb;
+        per = GROUP_THREADS / lpb;
         myb = (int)threadIdx.x / lpb;
         sub = (int)threadIdx.x % lpb;
     }
@@ -381,7 +381,7 @@ static __device__ __forceinline__ XLds stage_norm_act(int kind, const float *__r
                                                       const NormIn &in) {
     __shared__ double red[16];
     const NormMap m(kind);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = GROUP_THREADS >> 6;
     const int n = nb * m.bv, nit = (nb + m.per - 1) / m.per;
     const bool plain = w == nullptr;
     auto ld = [&](const float *p, int b, f32x4 (&v)[4]) {
@@ -463,6 +463,9 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     NormIn nin;
     if (!sg.nx) {
         stage_act(kind, act, nb, lds);
+        /* its loads are all consumed; a wait the compiler can see keeps its
+         * count from holding back the other path's first weight loads */
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     } else {
         norm_act_load(kind, sg.nx, sg.nw, nb, nin);
@@ -470,9 +473,13 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     const int cap = nb < MvCfg<DT, DEEP>::NBC ? nb : MvCfg<DT, DEEP>::NBC;
     const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * TILE_ROWS);
     bool staged = !sg.nx;
-    /* the activation from rmsnorm once the first weight loads are out */
+    /* the activation from rmsnorm once the first weight loads are out: the
+     * empty asm keeps the norm's arithmetic (and so its wait for x) below
+     * the weight loads, where the compiler would otherwise hoist it */
     auto stage = [&]() {
         if (!staged) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) asm volatile("" : "+v"(nin.xv[u]), "+v"(nin.wv[u])::"memory");
             stage_norm_act(kind, sg.nx, sg.nw, sg.eps, nb, lds, nin);
             __syncthreads();
             staged = true;
@@ -481,7 +488,7 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     };
     const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS;
     const int64_t units = T * nb * TILE_ROWS;
-    const int round_items = (int)(blockDim.x / F::LPI) * IPL;
+    const int round_items = (GROUP_THREADS / F::LPI) * IPL;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += cap) {
         const int nbc = nb - b0 < cap ? nb - b0 : cap;
@@ -500,6 +507,10 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
         __syncthreads();
         if (threadIdx.x < TILE_ROWS) acc = chain_park<AFF>(park, nbc, 0, TILE_ROWS, threadIdx.x, acc);
         __syncthreads();
+        /* nothing is in flight here (a dropped item's load aside); a wait
+         * the compiler can see keeps the loop head's counts from holding the
+         * first pass's weight loads back behind the norm's x and w */
+        __builtin_amdgcn_s_waitcnt(0);
     }
     const int64_t r = t * TILE_ROWS + threadIdx.x;
     if (threadIdx.x < TILE_ROWS && r < rows) y[r] = sg.accum ? y[r] + acc : acc;

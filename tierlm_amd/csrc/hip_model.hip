@@ -452,16 +452,23 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
             vload(ATT_VPF + 1, vq[1]);
             pread(2, pc);
             __syncthreads();
-            for (int b = 0; b < nbk; b += ATT_VPF) {
+            /* whole rounds of ATT_VPF blocks in the loop, the last partial
+             * round after it: the loop head is reached only with the full
+             * prefetch in flight, so the compiler's wait counts there keep it */
+            auto step = [&](int b, int k) {   /* block b + k + 2 into buffer (b + k + 2) mod 3 */
+                produce(b + k + 2, pc, vq[(k + 2) % ATT_VPF], (k + 2) % 3);
+                vload(b + k + 2 + ATT_VPF, vq[(k + 2) % ATT_VPF]);
+                pread(b + k + 3, pc);
+                __syncthreads();
+            };
+            int b = 0;
+            for (; b + ATT_VPF <= nbk; b += ATT_VPF) {
 #pragma unroll
-                for (int k = 0; k < ATT_VPF; k++) {   /* block b + k + 2 into buffer (b + k + 2) mod 3 */
-                    if (b + k >= nbk) break;          /* uniform: the chain wave leaves at the same block */
-                    produce(b + k + 2, pc, vq[(k + 2) % ATT_VPF], (k + 2) % 3);
-                    vload(b + k + 2 + ATT_VPF, vq[(k + 2) % ATT_VPF]);
-                    pread(b + k + 3, pc);
-                    __syncthreads();
-                }
+                for (int k = 0; k < ATT_VPF; k++) step(b, k);
             }
+#pragma unroll
+            for (int k = 0; k < ATT_VPF - 1; k++)   /* uniform: the chain wave runs the same blocks */
+                if (b + k < nbk) step(b, k);
         } else {
             /* the chain reads a block in three parts, each one part ahead of
              * its adds (the next block's first part during this block's last) */
@@ -471,29 +478,36 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
             f32x4 cur[SUB];
 #pragma unroll
             for (int u = 0; u < SUB; u++) cur[u] = s_prod[0][u][lane];
-            for (int b = 0; b < nbk; b += ATT_VPF) {
+            auto block = [&](int k) {   /* block b + k from buffer (b + k) mod 3 */
 #pragma unroll
-                for (int k = 0; k < ATT_VPF; k++) {   /* block b + k from buffer (b + k) mod 3 */
-                    if (b + k >= nbk) break;
+                for (int c = 0; c < 3; c++) {
+                    f32x4 nx[SUB];
 #pragma unroll
-                    for (int c = 0; c < 3; c++) {
-                        f32x4 nx[SUB];
+                    for (int u = 0; u < SUB; u++)
+                        nx[u] = c < 2 ? s_prod[k % 3][SUB * (c + 1) + u][lane] : s_prod[(k + 1) % 3][u][lane];
+                    /* the reads stay ahead of the adds (the scheduler would
+                     * otherwise sink them to their use) */
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int u = 0; u < SUB; u++)
-                            nx[u] = c < 2 ? s_prod[k % 3][SUB * (c + 1) + u][lane] : s_prod[(k + 1) % 3][u][lane];
-#pragma unroll
-                        for (int u = 0; u < SUB; u++) {
-                            acc += cur[u].x;
-                            acc += cur[u].y;
-                            acc += cur[u].z;
-                            acc += cur[u].w;
-                        }
-#pragma unroll
-                        for (int u = 0; u < SUB; u++) cur[u] = nx[u];
+                    for (int u = 0; u < SUB; u++) {
+                        acc += cur[u].x;
+                        acc += cur[u].y;
+                        acc += cur[u].z;
+                        acc += cur[u].w;
                     }
-                    __syncthreads();
+#pragma unroll
+                    for (int u = 0; u < SUB; u++) cur[u] = nx[u];
                 }
+                __syncthreads();
+            };
+            int b = 0;
+            for (; b + ATT_VPF <= nbk; b += ATT_VPF) {
+#pragma unroll
+                for (int k = 0; k < ATT_VPF; k++) block(k);
             }
+#pragma unroll
+            for (int k = 0; k < ATT_VPF - 1; k++)
+                if (b + k < nbk) block(k);
         }
     }
     if (wave == 0 && ic < HD) att[(size_t)h * HD + ic] = acc;

@@ -468,7 +468,7 @@ __device__ __forceinline__ void router_body(const tlm_hip_moe_desc &d, const WsL
 __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
                                                    uint8_t *ws, size_t tstride) {
     args_now(d.D, d.E, d.eps, d.router_w, d.ffn_norm, d.ds, d.expert_dt, d.shared_dt, d.shared_gate_inp, L.logits,
-             L.xb, L.xe, L.xs, L.route, hptr, ws, tstride, blockDim.x, gridDim.x);
+             L.xb, L.xe, L.xs, L.route, hptr, ws, tstride, gridDim.x);
     router_body(d, L, hptr + (size_t)blockIdx.y * d.D, ws + (size_t)blockIdx.y * tstride, blockIdx.x);
 }
 
@@ -545,7 +545,7 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
     const int cb = nb < PARK_MAX / TILE_ROWS / 2 ? nb : PARK_MAX / TILE_ROWS / 2;   /* blocks per chunk */
     const Park park = park_at(lds + xstride * NWAVE, 2 * cb * TILE_ROWS);
     const int64_t T = F / TILE_ROWS, units = T * nb * TILE_ROWS;
-    const int slots = (int)blockDim.x / Fm::LPI;
+    const int slots = GROUP_THREADS / Fm::LPI;
     bool staged = false;
     XLds X = xlds_at(kind, nb, xarea);
     float acc = 0.0f;
@@ -593,7 +593,7 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ RouteLds s_route;
     args_now(d.D, d.de, d.ds, d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, d.experts, L.logits, L.route,
-             L.hh, L.xe, ids_out, w_out, ws, blockDim.x, gridDim.x);
+             L.hh, L.xe, ids_out, w_out, ws, gridDim.x);
     if constexpr (SDT != NONE) args_now(d.sg, d.su, L.xs);
     const int te = (int)(d.de / TILE_ROWS), nexp = d.k * te;
     const bool shared = SDT != NONE && (int)blockIdx.x >= nexp;
@@ -672,8 +672,8 @@ __device__ void down_rows(int nmat, WPtr wptr, Pre pre, const float *hsrc, int64
     constexpr int BPW = 64 / LPB;                   /* activation blocks per wave per pass */
     constexpr int QB = 2;                           /* passes whose loads go out first */
     const int nb = (int)(F / BV), nq = nmat * nb, nitems = nq * DROWS;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    const int slots = (int)blockDim.x / Fm::LPI;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = GROUP_THREADS >> 6;
+    const int slots = GROUP_THREADS / Fm::LPI;
     const int64_t units = (D / TILE_ROWS) * nb * TILE_ROWS;
     const int64_t t = row0 / TILE_ROWS, i0 = row0 % TILE_ROWS;
     const XLds X = xlds_at(kind, nq, xarea);
@@ -741,7 +741,7 @@ template <int EDT, int SDT, bool GIVEN>
 __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h,
                                                   uint8_t *ws, const GivenArg<GIVEN> gv) {
     extern __shared__ __align__(16) uint8_t lds[];
-    args_now(d.D, d.de, d.ds, d.E, d.k, d.experts, L.route, L.hh, h, ws, blockDim.x, gridDim.x);
+    args_now(d.D, d.de, d.ds, d.E, d.k, d.experts, L.route, L.hh, h, ws, gridDim.x);
     if constexpr (SDT != NONE) args_now(d.sd);
     constexpr int ek = EDT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
     const int k = d.k;
@@ -803,7 +803,7 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
     __syncthreads();
     /* row chains, one thread per (matrix, row); then the rank-order sum */
     const int nm = k + (SDT != NONE ? 1 : 0);
-    for (int t = tid; t < nm * DROWS; t += blockDim.x) {
+    for (int t = tid; t < nm * DROWS; t += GROUP_THREADS) {
         const int r = t >> 3, i = t & (DROWS - 1);
         if constexpr (SDT != NONE) s_out[t] = r < k ? down_chain<EDT>(pe, r, nbe, i) : down_chain<SDT>(ps, 0, nbs, i);
         else s_out[t] = down_chain<EDT>(pe, r, nbe, i);

@@ -17,6 +17,12 @@ enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_Q8_0 = 8, DT_Q4_K = 12, DT_Q5_K =
  * tile with 4 lanes per (row, block) for the 256-value formats. */
 #define TILE_ROWS 16
 
+/* Threads per group of the streaming kernels: their launch bound and the size
+ * they are always launched with.  A constant, because blockDim.x is read
+ * through a vector memory load whose wait also waits for every load issued
+ * before it. */
+#define GROUP_THREADS 256
+
 /* ---- host-side error plumbing (tlm_hip.cpp) ----------------------------- */
 int tlmh_seterr(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int tlmh_check(hipError_t e, const char *what);

@@ -41,7 +41,7 @@ __device__ __forceinline__ static XLds xlds_at(int kind, int nb, uint8_t *lds_ge
 /* Copy nb activation blocks (global, reference layout) into the LDS layout;
  * every thread of the group takes part; the caller synchronises. */
 static __device__ __forceinline__ XLds stage_act(int kind, const uint8_t *__restrict__ act, int nb, uint8_t *lds_g) {
-    const int tid = threadIdx.x, nt = blockDim.x;
+    const int tid = threadIdx.x, nt = GROUP_THREADS;
     const GAS uint32_t *a = (const GAS uint32_t *)act;
     LAS uint8_t *lds = (LAS uint8_t *)lds_g;
     if (kind == DT_Q8_K) {
@@ -282,7 +282,7 @@ template <int DT, int IPL, bool CLAMP = false, class Map, class Stage>
 __device__ __forceinline__ XLds run_items(int nitems, Map map, Stage stage, Park park) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    const int slots = blockDim.x / F::LPI;
+    const int slots = GROUP_THREADS / F::LPI;
     const int q = threadIdx.x % F::LPI, slot = threadIdx.x / F::LPI;
     typename F::Raw raw[IPL];
     int bb[IPL], pk[IPL];
