@@ -54,40 +54,45 @@ __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, 
 
 /* ---- attention: attention() (src/lib/tlm_model.c:743-756) and attn_heads
  * (:683-719), the reference's bits, in two launches -------------------------
+ * Both kernels issue every load that does not depend on the position before
+ * the position itself arrives (it lives in device memory, so one captured
+ * graph serves every step), clamped to the cache's capacity where the
+ * context would bound them; what lies past the context is masked.
  * k_attn_scores: one group per (key head, slice of positions).  It
  * normalises and rotates the query heads that share the key head (q-norm,
- * RoPE) and the new key (k-norm, RoPE), then walks its slice in chunks of
- * ATT_CH positions staged in LDS and stores every (query head, position)
- * score - the dot in ascending i, scaled after the dot - with the slice's
- * maximum per query head; the group whose slice holds the new position
- * appends its key and value to the cache.
+ * RoPE) and the new key (k-norm, RoPE) - 16 lanes per vector, every vector
+ * at once - then walks its slice in chunks of ATT_CH positions staged in LDS
+ * and stores every (query head, position) score: the dot in ascending i,
+ * scaled after the dot.  The group whose slice holds the new position appends
+ * its key and value to the cache.
  * k_attn_pv: a group per (query head, 64 output elements).  All four waves
- * run the softmax in the reference's order - the maximum over the slice
- * maxima, e_t = e^(s_t - max), their sum in double, inv = 1 / sum, p_t = e_t *
- * inv (probabilities in LDS) - then the P.V sums out += p_t * v_t[i] over
- * ascending t: wave 0 holds one chain per lane and only adds, one dependent
- * add per position (about 4.5 clocks); waves 1-3 form the products p_t v_t[i]
- * (the reference's rounded products) into a ring of three LDS blocks of
- * ATT_BT value tiles, two blocks ahead of the chains, with the value tiles
- * ATT_VPF blocks ahead in registers; one barrier per block.  A chain wave that
- * also formed its products issued a multiply and an add per position, and
- * one that read its values from memory as well shared the CU's load
- * bandwidth with three others: both ran at 9-10 ns per position against 5
- * now.  The value cache is kept in tiles of 4 positions, element-major inside
- * (V[t][i] at ((t / 4) * HD + i) * 4 + t % 4), where one 16-byte lane load is
- * positions 4j..4j+3 of element i and a wave's load is 1 KB contiguous.
+ * run the softmax in the reference's order - the maximum over the context,
+ * e_t = e^(s_t - max), their sum in double, inv = 1 / sum, p_t = e_t * inv
+ * (probabilities in LDS), e^x with its table held in the lanes - then the
+ * P.V sums out += p_t * v_t[i] over ascending t: wave 0 holds one chain per
+ * lane and only adds, one dependent add per position (about 4.5 clocks);
+ * waves 1-3 form the products p_t v_t[i] (the reference's rounded products)
+ * into a ring of three LDS blocks of ATT_BT value tiles, two blocks ahead of
+ * the chains, with the value tiles ATT_VPF blocks ahead in registers (the
+ * first ones loaded at entry); one barrier per block.  A chain wave that also
+ * formed its products issued a multiply and an add per position, and one that
+ * read its values from memory as well shared the CU's load bandwidth with
+ * three others: both ran at 9-10 ns per position.  The value cache is kept in
+ * tiles of 4 positions, element-major inside (V[t][i] at ((t / 4) * HD + i) *
+ * 4 + t % 4), where one 16-byte lane load is positions 4j..4j+3 of element i
+ * and a wave's load is 1 KB contiguous.
  *
- * Numerics: the scores, maxima, products and chains are the reference's
- * operations in its order; the double sum of the softmax terms is a tree
- * instead of a sequence (its float reciprocal can differ only when that sum
- * lies within a double ulp or so of a rounding boundary); e^x is libm's expf
- * (expf_ref).
+ * Numerics: the scores, maximum, products and chains are the reference's
+ * operations in its order; the double sums (squares of the norms, softmax
+ * terms) are trees instead of sequences (a float rounding of such a sum can
+ * differ only when it lies within a double ulp or so of a rounding
+ * boundary); e^x is libm's expf (expf_ref).
  *
  * Cache layout (per layer and key head): K[t][i] at t * HD + i (the
  * reference's), values in the 4-position tiles above (att_vstride floats per
- * key head).  Slices: G per key head (fixed for the captured
- * graph), att_slice_len(T, G) positions at context T; groups past the
- * context return at once. */
+ * key head).  Slices: G per key head (fixed for the captured graph),
+ * att_slice_len(T, G) positions at context T; groups past the context return
+ * at once. */
 constexpr int ATT_CH = 32;       /* positions per LDS chunk of the scores */
 constexpr int ATT_LMIN = 32;     /* shortest slice */
 constexpr int ATT_QMAX = 4096;   /* query values per key head (query heads per key head x HD) */
@@ -148,27 +153,22 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
                                                     const float *__restrict__ k_norm, int has_qn, int has_kn,
                                                     const float *__restrict__ cs_all, const float *__restrict__ sn_all,
                                                     float *__restrict__ kc, float *__restrict__ vc,
-                                                    float *__restrict__ scores, float *__restrict__ smax, int H,
-                                                    int KV, int max_ctx, int G, const int32_t *__restrict__ st,
-                                                    float eps) {
+                                                    float *__restrict__ scores, int H, int KV, int max_ctx, int G,
+                                                    const int32_t *__restrict__ st, float eps) {
     constexpr int H4 = HD / 4, HALF = HD / 2, KS = HD + 4;
     constexpr int CF = ATT_CH * H4 / NT;            /* float4 of a chunk's K per thread */
     constexpr int QF = ATT_QMAX / 4 / NT;           /* float4 of the query heads per thread, at most */
     constexpr int SU = ATT_QMAX / HD * ATT_CH / NT; /* (query head, position) items per thread per chunk, at most */
-    constexpr int KE = (HD + 63) / 64, KH = (HALF + 63) / 64;   /* elements / pairs per lane */
+    constexpr int EL = HD / 16;                     /* elements per lane of a vector's 16 lanes */
     extern __shared__ __align__(16) float s_dyn[];
-    const int pos = st[0], T = pos + 1, R = H / KV;
-    const int L = att_slice_len(T, G), t0 = (int)blockIdx.y * L;
-    if (t0 >= T) return;
-    const int tn = min(L, T - t0), kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int R = H / KV, kvh = blockIdx.x, tid = threadIdx.x, sub = tid & 15;
     const AttLds lo = att_lds(HD, R);
     float *s_q = s_dyn + lo.q, *s_kn = s_dyn + lo.kn, *s_vn = s_dyn + lo.vn, *s_k = s_dyn + lo.k;
     float *K = kc + (size_t)kvh * max_ctx * HD, *V = vc + (size_t)kvh * att_vstride(max_ctx, HD);
 
-    /* every load at entry, in the order of use: the query heads (consecutive
-     * heads h = kvh * R + j), the new key and value, norm weights and RoPE
-     * factors, then the first chunk's key rows (clamped to the context; rows
-     * past the slice are never used) */
+    /* what does not depend on the position is loaded while the position is
+     * read: the query heads (consecutive heads h = kvh * R + j), the new key
+     * and value, the norm weights of the lane's elements sub + 16 e */
     const int nq4 = R * H4;
     const f32x4 *q4 = (const f32x4 *)(q + (size_t)kvh * R * HD);
     f32x4 qv[QF];
@@ -176,15 +176,24 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
     for (int k = 0; k < QF; k++) qv[k] = q4[min(tid + NT * k, nq4 - 1)];
     const f32x4 knv = ((const f32x4 *)kx)[(size_t)kvh * H4 + min(tid, H4 - 1)];
     const f32x4 vnv = ((const f32x4 *)vx)[(size_t)kvh * H4 + min(tid, H4 - 1)];
-    float qn[KE], kn[KE], cv[KH], sv[KH];
+    float qn[EL], kn[EL];
 #pragma unroll
-    for (int k = 0; k < KE; k++) qn[k] = q_norm[min(lane + 64 * k, HD - 1)];
+    for (int e = 0; e < EL; e++) {
+        qn[e] = q_norm[sub + 16 * e];
+        kn[e] = k_norm[sub + 16 * e];
+    }
+    const int pos = st[0], T = pos + 1;
+    const int L = att_slice_len(T, G), t0 = (int)blockIdx.y * L;
+    if (t0 >= T) return;
+    const int tn = min(L, T - t0);
+    /* RoPE factors of the lane's pairs (sub + 16 e, sub + 16 e + HD/2), then
+     * the first chunk's key rows (clamped to the context; rows past the
+     * slice are never used) */
+    float cv[EL / 2], sv[EL / 2];
 #pragma unroll
-    for (int k = 0; k < KE; k++) kn[k] = k_norm[min(lane + 64 * k, HD - 1)];
-#pragma unroll
-    for (int k = 0; k < KH; k++) {
-        cv[k] = cs_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
-        sv[k] = sn_all[(size_t)pos * HALF + min(lane + 64 * k, HALF - 1)];
+    for (int e = 0; e < EL / 2; e++) {
+        cv[e] = cs_all[(size_t)pos * HALF + sub + 16 * e];
+        sv[e] = sn_all[(size_t)pos * HALF + sub + 16 * e];
     }
     const int nch = (tn + ATT_CH - 1) / ATT_CH;
     f32x4 kr[CF];
@@ -199,7 +208,7 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
     kload(0);
     /* the value rows of this slice and of its sibling (slice ^ 1) towards this
      * XCD's L2 for the P.V launch: direct-to-LDS loads into one 1 KB sink, never
-     * read, so they hold no registers (att_pv_group puts a key head's P.V groups
+     * read, so they hold no registers (k_attn_pv puts a key head's P.V groups
      * on the XCDs its slices run on; block b runs on XCD b mod 8 and slice
      * parity alternates the two) */
     __shared__ __align__(16) float s_sink[256];
@@ -222,42 +231,40 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
     __syncthreads();
 
     /* rmsnorm of each query head and of the new key (tlm_model.c:743-746:
-     * double sum of squares, x * r * w), then RoPE (rope(), :721-728: pairs
-     * (j, j + HD/2)); vector R is the key, one vector per wave at a time */
-    for (int v = wave; v <= R; v += NT / 64) {
+     * double sum of squares - the lane's elements in order, then a 16-lane
+     * tree -, x * r * w), then RoPE (rope(), :721-728: the pair (j, j + HD/2)
+     * is elements e and e + EL/2 of one lane); 16 lanes per vector, all
+     * vectors at once, vector R being the key */
+    for (int v = tid >> 4; v <= R; v += NT / 16) {   /* uniform over each 16 lanes */
         float *x = v < R ? s_q + v * HD : s_kn;
-        if (v < R ? has_qn : has_kn) {
-            float e[KE];
+        float e[EL];
 #pragma unroll
-            for (int k = 0; k < KE; k++) e[k] = x[min(lane + 64 * k, HD - 1)];
+        for (int k = 0; k < EL; k++) e[k] = x[sub + 16 * k];
+        if (v < R ? has_qn : has_kn) {
             double ss = 0.0;
 #pragma unroll
-            for (int k = 0; k < KE; k++)
-                if (lane + 64 * k < HD) ss += (double)e[k] * (double)e[k];
-            ss = wave_sum_f64(ss);
+            for (int k = 0; k < EL; k++) ss += (double)e[k] * (double)e[k];
+            ss += dpp_f64<DPP_XOR1>(ss);
+            ss += dpp_f64<DPP_XOR2>(ss);
+            ss += dpp_f64<DPP_HALF_MIRROR>(ss);
+            ss += dpp_f64<DPP_MIRROR>(ss);
             const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
 #pragma unroll
-            for (int k = 0; k < KE; k++)
-                if (lane + 64 * k < HD) x[lane + 64 * k] = e[k] * r * (v < R ? qn[k] : kn[k]);
-            wave_lds_sync();
+            for (int k = 0; k < EL; k++) e[k] = e[k] * r * (v < R ? qn[k] : kn[k]);
         }
 #pragma unroll
-        for (int k = 0; k < KH; k++) {
-            const int j = lane + 64 * k;
-            if (j < HALF) {
-                const float a = x[j], c = x[j + HALF];
-                x[j] = a * cv[k] - c * sv[k];
-                x[j + HALF] = c * cv[k] + a * sv[k];
-            }
+        for (int k = 0; k < EL / 2; k++) {
+            const float a = e[k], c = e[k + EL / 2];
+            e[k] = a * cv[k] - c * sv[k];
+            e[k + EL / 2] = c * cv[k] + a * sv[k];
         }
+#pragma unroll
+        for (int k = 0; k < EL; k++) x[sub + 16 * k] = e[k];
     }
     __syncthreads();
 
     const float scale = 1.0f / sqrtf((float)HD);
     const int nsc = R * ATT_CH;
-    float rmx[SU];
-#pragma unroll
-    for (int u = 0; u < SU; u++) rmx[u] = -INFINITY;
     for (int c = 0; c < nch; c++) {   /* uniform over the group */
         const int tc = t0 + c * ATT_CH, tnc = min(ATT_CH, tn - c * ATT_CH);
         /* stage the chunk's keys; row pos from this group's copy */
@@ -286,21 +293,10 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
                     d += a.w * b.w;
                 }
                 d *= scale;   /* after the dot, before the maximum (tlm_model.c:699-702) */
-                if (t < tnc) {
-                    scores[(size_t)(kvh * R + j) * max_ctx + tc + t] = d;
-                    rmx[u] = d > rmx[u] ? d : rmx[u];
-                }
+                if (t < tnc) scores[(size_t)(kvh * R + j) * max_ctx + tc + t] = d;
             }
         }
         __syncthreads();   /* before the next chunk overwrites the keys */
-    }
-#pragma unroll
-    for (int u = 0; u < SU; u++) {
-        const int idx = tid + NT * u;
-        if (idx < nsc) {
-            const float m = half_max_f32(rmx[u]);
-            if (idx % ATT_CH == 0) smax[(size_t)(kvh * R + idx / ATT_CH) * G + blockIdx.y] = m;
-        }
     }
     if (t0 + tn == T)   /* the KV append (tlm_model.c:748-752), after the last read */
         for (int i4 = tid; i4 < H4; i4 += NT) {
@@ -315,19 +311,18 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
 }
 
 template <int HD>
-__global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ smax,
-                                                const float *__restrict__ vc, float *__restrict__ att, int H, int KV,
-                                                int max_ctx, int G, const int32_t *__restrict__ st) {
+__global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
+                                                float *__restrict__ att, int H, int KV, int max_ctx,
+                                                const int32_t *__restrict__ st) {
     constexpr int NWC = (HD + 63) / 64;   /* 64-element slabs per query head, a group each */
     constexpr int PB = 8;                 /* score loads per thread per round */
-    constexpr int GM = ATT_GMAX / 64;     /* slice maxima per lane */
     constexpr int NPW = NT / 64 - 1;      /* producer waves */
     constexpr int TPP = ATT_BT / NPW;     /* tiles per producer per block */
     static_assert(ATT_BT % NPW == 0, "a block's tiles split evenly over the producers");
     __shared__ __align__(16) float s_p[ATT_PSEG];
     __shared__ __align__(16) f32x4 s_prod[3][ATT_BT][64];   /* three blocks of products, tile-major */
     __shared__ double s_sum[NT / 64];
-    const int pos = st[0], T = pos + 1, L = att_slice_len(T, G), ns = (T + L - 1) / L;
+    __shared__ float s_max[NT / 64];
     const int R = H / KV;
     /* block b: key head b mod KV (so b runs on an XCD of that key head's
      * slices, where k_attn_scores left its values), then (query head of the key
@@ -339,31 +334,65 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     const float *S = scores + (size_t)h * max_ctx;
     const char *vbase = (const char *)(vc + (size_t)kvg * att_vstride(max_ctx, HD));
     const uint32_t lane_off = (uint32_t)min(ic, HD - 1) * 16u;   /* element ic's 16 bytes of a tile */
-    const int lastq = (T - 1) >> 2;
-
-    /* entry loads: the head's slice maxima, the first scores */
-    float mm[GM];
+    /* producer pw forms tiles pw * TPP .. + TPP - 1 of each block; the chain
+     * wave issues producer 0's first loads too (and drops them), so that every
+     * wave runs the same loads up to the role split and the compiler's wait
+     * for the scores is the same count on every path */
+    const int pw = wave > 0 ? wave - 1 : 0;
+    auto vload = [&](int q0, int blk, int lastq, f32x4 (&r)[TPP]) {
 #pragma unroll
-    for (int k = 0; k < GM; k++) mm[k] = smax[(size_t)h * G + min(lane + 64 * k, ns - 1)];
+        for (int u = 0; u < TPP; u++) {
+            const int tq = min(q0 + blk * ATT_BT + pw * TPP + u, lastq);
+            r[u] = *(const f32x4 *)(vbase + (size_t)tq * (HD * 16) + lane_off);
+        }
+    };
+
+    /* entry loads, none waiting for the position: the first scores and the
+     * first blocks' value tiles (both clamped to the capacity: what lies past
+     * the context is masked below), the exp table */
     float sv[PB];
 #pragma unroll
-    for (int k = 0; k < PB; k++) sv[k] = S[min(tid + NT * k, T - 1)];
-
-    float mx = -INFINITY;   /* the reference's maximum: NaN never compares greater */
+    for (int k = 0; k < PB; k++) sv[k] = S[min(tid + NT * k, max_ctx - 1)];
+    ExpTabLanes tab;
+    tab.load();
+    f32x4 vq[ATT_VPF][TPP];   /* producers: value tiles of ATT_VPF blocks */
 #pragma unroll
-    for (int k = 0; k < GM; k++) mx = mm[k] > mx ? mm[k] : mx;
-    mx = wave_max_f32(mx);
+    for (int k = 0; k < ATT_VPF; k++) vload(0, k, (max_ctx - 1) >> 2, vq[k]);
+    const int pos = st[0], T = pos + 1, lastq = (T - 1) >> 2;
+
+    /* the maximum over the context (tlm_model.c:698-703; NaN never compares
+     * greater, and a maximum is the same in any order), then e_t = e^(s_t -
+     * max) and their sum (:704-709, the double sum as a tree) */
+    const int nround = (T + PB * NT - 1) / (PB * NT);
+    float m = -INFINITY;
+    for (int r = 0; r < nround; r++) {
+        if (r > 0) {
+#pragma unroll
+            for (int k = 0; k < PB; k++) sv[k] = S[min(r * PB * NT + tid + NT * k, T - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int t = r * PB * NT + tid + NT * k;
+            m = t < T && sv[k] > m ? sv[k] : m;
+        }
+    }
+    m = wave_max_f32(m);
+    if (lane == 0) s_max[wave] = m;
+    __syncthreads();
+    float mx = s_max[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) mx = s_max[w] > mx ? s_max[w] : mx;
     const int nseg = (T + ATT_PSEG - 1) / ATT_PSEG;
     double sum = 0.0;
-    for (int b0 = 0; b0 < T; b0 += PB * NT) {   /* e_t and their sum (tlm_model.c:704-709) */
-        if (b0 > 0) {
+    for (int r = 0; r < nround; r++) {
+        if (nround > 1) {
 #pragma unroll
-            for (int k = 0; k < PB; k++) sv[k] = S[min(b0 + tid + NT * k, T - 1)];
+            for (int k = 0; k < PB; k++) sv[k] = S[min(r * PB * NT + tid + NT * k, T - 1)];
         }
 #pragma unroll
         for (int k = 0; k < PB; k++) {   /* every lane computes; past the context it adds 0, stores nothing */
-            const int t = b0 + tid + NT * k;
-            const float e = expf_ref(sv[k] - mx);
+            const int t = r * PB * NT + tid + NT * k;
+            const float e = expf_ref_with(sv[k] - mx, tab);
             sum += t < T ? (double)e : 0.0;
             if (nseg == 1 && t < T) s_p[t] = e;
         }
@@ -383,27 +412,16 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
      * three blocks ahead in registers.  Products past the segment are +0, and
      * adding +0 leaves the chain unchanged (it starts at +0 and never holds
      * -0), so the chains run whole blocks. */
-    const int pw = wave - 1;
     float acc = 0.0f;
-    f32x4 vq[ATT_VPF][TPP];   /* producers: value tiles of ATT_VPF blocks */
     for (int sb = 0; sb < T; sb += ATT_PSEG) {   /* uniform over the group */
         const int se = min(T, sb + ATT_PSEG);
         if (nseg == 1) {   /* each thread scales the terms it stored: p = e * inv */
             for (int t = tid; t < T; t += NT) s_p[t] = s_p[t] * inv_s;
         } else {
-            for (int t = sb + tid; t < se; t += NT) s_p[t - sb] = expf_ref(S[t] - mx) * inv_s;
+            for (int t = sb + tid; t < se; t += NT) s_p[t - sb] = expf_ref_with(S[t] - mx, tab) * inv_s;
         }
         const int nbk = (se - sb + ATT_BT * 4 - 1) / (ATT_BT * 4);   /* blocks of the segment */
         const int q0 = sb >> 2;   /* the segment's first tile */
-        /* producers: tiles pw * TPP .. + TPP - 1 of each block; a tile's
-         * address is uniform, the lane adds its element's 16 bytes */
-        auto vload = [&](int blk, f32x4 (&r)[TPP]) {
-#pragma unroll
-            for (int u = 0; u < TPP; u++) {
-                const int tq = min(q0 + blk * ATT_BT + pw * TPP + u, lastq);
-                r[u] = *(const f32x4 *)(vbase + (size_t)tq * (HD * 16) + lane_off);
-            }
-        };
         /* the probabilities of a producer's tiles of block blk (uniform LDS
          * reads), read a block ahead of their use */
         auto pread = [&](int blk, f32x4 (&p)[TPP]) {
@@ -440,35 +458,44 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
         /* the two roles run separate loops with the same barriers, so that
          * neither's memory counters are merged with the other's path */
         if (wave > 0) {
+            if (sb > 0) {   /* later segments: their first blocks' tiles now */
 #pragma unroll
-            for (int k = 0; k < ATT_VPF; k++) vload(k, vq[k]);
+                for (int k = 0; k < ATT_VPF; k++) vload(q0, k, lastq, vq[k]);
+            }
             f32x4 pc[TPP];
             __syncthreads();   /* the segment's probabilities */
             pread(0, pc);
             produce(0, pc, vq[0], 0);
-            vload(ATT_VPF, vq[0]);
+            vload(q0, ATT_VPF, lastq, vq[0]);
             pread(1, pc);
             produce(1, pc, vq[1], 1);
-            vload(ATT_VPF + 1, vq[1]);
+            vload(q0, ATT_VPF + 1, lastq, vq[1]);
             pread(2, pc);
             __syncthreads();
-            /* whole rounds of ATT_VPF blocks in the loop, the last partial
-             * round after it: the loop head is reached only with the full
-             * prefetch in flight, so the compiler's wait counts there keep it */
-            auto step = [&](int b, int k) {   /* block b + k + 2 into buffer (b + k + 2) mod 3 */
+            /* one step (and barrier) per block of the segment; step s of a
+             * round produces block b + s + 2 into buffer (s + 2) mod 3.  The
+             * loop runs the rounds whose blocks all lie in the segment, with
+             * the full prefetch in flight at its head (so the compiler's wait
+             * counts there keep it); the steps after it produce only blocks
+             * of the segment, so none waits for a tile past the context */
+            auto step = [&](int b, int k) {
                 produce(b + k + 2, pc, vq[(k + 2) % ATT_VPF], (k + 2) % 3);
-                vload(b + k + 2 + ATT_VPF, vq[(k + 2) % ATT_VPF]);
+                vload(q0, b + k + 2 + ATT_VPF, lastq, vq[(k + 2) % ATT_VPF]);
                 pread(b + k + 3, pc);
                 __syncthreads();
             };
             int b = 0;
-            for (; b + ATT_VPF <= nbk; b += ATT_VPF) {
+            for (; b + ATT_VPF + 2 <= nbk; b += ATT_VPF) {
 #pragma unroll
                 for (int k = 0; k < ATT_VPF; k++) step(b, k);
             }
 #pragma unroll
-            for (int k = 0; k < ATT_VPF - 1; k++)   /* uniform: the chain wave runs the same blocks */
-                if (b + k < nbk) step(b, k);
+            for (int k = 0; k < ATT_VPF + 1; k++) {   /* uniform: the chain wave runs the same blocks */
+                if (b + k >= nbk) break;
+                if (b + k + 2 < nbk) produce(b + k + 2, pc, vq[(k + 2) % ATT_VPF], (k + 2) % 3);
+                pread(b + k + 3, pc);
+                __syncthreads();
+            }
         } else {
             /* the chain reads a block in three parts, each one part ahead of
              * its adds (the next block's first part during this block's last) */
@@ -882,7 +909,7 @@ size_t att_split_bytes(int hd, int H, int KV, int max_ctx, int G) {
  * reference's order k_attn_scores + k_attn_pv */
 int launch_attn(int hd, int H, int KV, int max_ctx, int G, bool split, const float *q, const float *kx,
                 const float *vx, const float *q_norm, const float *k_norm, const float *cs, const float *sn,
-                float *kc, float *vc, float *scores, float *smax, float *part_o, float *part_ml, float *att,
+                float *kc, float *vc, float *scores, float *part_o, float *part_ml, float *att,
                 const int32_t *st, float eps, hipStream_t s) {
     const int has_qn = q_norm != nullptr, has_kn = k_norm != nullptr;
     if (!q_norm) q_norm = q;   /* read (clamped) and dropped */
@@ -899,9 +926,8 @@ int launch_attn(int hd, int H, int KV, int max_ctx, int G, bool split, const flo
             hipLaunchKernelGGL((k_attn_merge<W>), dim3(H), dim3(NT), 0, s, part_o, part_ml, att, G, st);          \
         } else {                                                                                                  \
             hipLaunchKernelGGL((k_attn_scores<W>), dim3(KV, G), dim3(NT), dyn, s, q, kx, vx, q_norm, k_norm,      \
-                               has_qn, has_kn, cs, sn, kc, vc, scores, smax, H, KV, max_ctx, G, st, eps);         \
-            hipLaunchKernelGGL((k_attn_pv<W>), dim3(npv), dim3(NT), 0, s, scores, smax, vc, att, H, KV, max_ctx, \
-                               G, st);                                                                            \
+                               has_qn, has_kn, cs, sn, kc, vc, scores, H, KV, max_ctx, G, st, eps);               \
+            hipLaunchKernelGGL((k_attn_pv<W>), dim3(npv), dim3(NT), 0, s, scores, vc, att, H, KV, max_ctx, st);    \
         }                                                                                                         \
         break;
     switch (hd) {
@@ -968,7 +994,7 @@ struct tlm_hip_model {
     float *kc = nullptr, *vc = nullptr, *cs = nullptr, *sn = nullptr;
     int att_g = 1;                                     /* attention slices per key head */
     bool att_split = false;                            /* split attention; false: the reference's order */
-    float *scores = nullptr, *smax = nullptr;          /* [H][max_ctx] scores; [H][att_g] slice maxima */
+    float *scores = nullptr;                           /* [H][max_ctx] scores */
     float *part_o = nullptr, *part_ml = nullptr;       /* split partials: [H][att_g][hd]; [H][att_g] (m, l) */
     float *h = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
     float *logits = nullptr;
@@ -1171,7 +1197,6 @@ int finish(tlm_hip_model *M) {
     M->kc = (float *)M->dalloc(per * 4);
     M->vc = (float *)M->dalloc((size_t)g.n_layers * KV * att_vstride(max_ctx, (int)hd) * 4);
     M->scores = (float *)M->dalloc((size_t)H * max_ctx * 4);
-    M->smax = (float *)M->dalloc((size_t)H * M->att_g * 4);
     M->part_o = (float *)M->dalloc((size_t)H * M->att_g * hd * 4);
     M->part_ml = (float *)M->dalloc((size_t)H * M->att_g * 2 * 4);
     M->h = (float *)M->dalloc((size_t)D * 4);
@@ -1188,7 +1213,7 @@ int finish(tlm_hip_model *M) {
     M->ids = (int32_t *)M->dalloc((size_t)g.n_layers * 32 * 4);   /* the step's routing, per layer */
     M->w = (float *)M->dalloc((size_t)g.n_layers * 32 * 4);
     M->keys = (unsigned long long *)M->dalloc(((size_t)g.vocab + TILE_ROWS - 1) / TILE_ROWS * 8);
-    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->smax, (void *)M->part_o,
+    for (void *p : {(void *)M->kc, (void *)M->vc, (void *)M->scores, (void *)M->part_o,
                     (void *)M->part_ml, (void *)M->h,
                     (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
                     (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
@@ -1366,7 +1391,7 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
         if (rc) break;
         const size_t kbase = (size_t)l * KV * M->max_ctx * hd, vbase = (size_t)l * KV * att_vstride(M->max_ctx, hd);
         rc = launch_attn(hd, H, KV, M->max_ctx, M->att_g, M->att_split, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm,
-                         M->cs, M->sn, M->kc + kbase, M->vc + vbase, M->scores, M->smax, M->part_o, M->part_ml,
+                         M->cs, M->sn, M->kc + kbase, M->vc + vbase, M->scores, M->part_o, M->part_ml,
                          M->att, (const int32_t *)M->st, g.norm_eps, s);
         /* o: every group quantises the attention output itself */
         const MvNorm ao{M->att, nullptr, 0.0f};

@@ -54,10 +54,17 @@ static inline int dt_int_ok(int dt) {
 /* binary16 -> binary32 built from the bit fields: exact for every code,
  * subnormals included, NaN payload kept and quieted (src/lib/tlm_quant.c:118-128). */
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
-    uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
-    if (e == 31u) return __uint_as_float(s | 0x7F800000u | (m << 13) | (m ? 0x00400000u : 0u));
-    if (e == 0u) return __uint_as_float(__float_as_uint((float)m * 0x1p-24f) | s);
-    return __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
+    /* integer operations and selects only, so the compiler keeps it
+     * branch-free and a kernel's items stay in one basic block; a subnormal
+     * m * 2^-24 is normalised through its leading bit p: exponent p + 103,
+     * mantissa the bits below p */
+    const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    const uint32_t mnz = 0u - (uint32_t)(m != 0u), e31 = 0u - (uint32_t)(e == 31u), e0 = 0u - (uint32_t)(e == 0u);
+    const uint32_t special = s | 0x7F800000u | (m << 13) | (mnz & 0x00400000u);
+    const uint32_t p = 31u - (uint32_t)__clz((int)(m | 1u));
+    const uint32_t sub = s | ((((p + 103u) << 23) | ((m << (23u - p)) & 0x7FFFFFu)) & mnz);
+    const uint32_t norm = s | ((e + 112u) << 23) | (m << 13);
+    return __uint_as_float((special & e31) | (sub & e0) | (norm & ~(e31 | e0)));
 }
 
 /* Round half to even via 1.5*2^23, clamp to [lo, hi], NaN -> 0
@@ -90,7 +97,8 @@ __device__ __forceinline__ int rne_clamp(float v, int lo, int hi) {
      0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,          \
      0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}
 __device__ static const uint64_t tlm_exp2_tab[32] = TLM_EXP2_TAB;
-__device__ __forceinline__ float expf_ref(float x) {
+/* tab(i) returns entry i of the table (i < 32) */
+template <class Tab> __device__ __forceinline__ float expf_ref_with(float x, const Tab &tab) {
     /* branch-free: the main path for every input (out-of-range ones give
      * values that the selects below replace; the table index stays in range) */
     const double InvLn2N = 0x1.71547652b82fep+0 * 32.0, Shift = 0x1.8p+52;
@@ -101,7 +109,7 @@ __device__ __forceinline__ float expf_ref(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= Shift;
     const double r = __builtin_fma(InvLn2N, xd, -kd);
-    const double s = __longlong_as_double((long long)(tlm_exp2_tab[ki % 32] + (ki << 47)));
+    const double s = __longlong_as_double((long long)(tab((int)(ki % 32)) + (ki << 47)));
     const double z = __builtin_fma(C0, r, C1), r2 = r * r;
     double y = __builtin_fma(C2, r, 1.0);
     y = __builtin_fma(z, r2, y);
@@ -110,6 +118,23 @@ __device__ __forceinline__ float expf_ref(float x) {
     v = x < -0x1.9fe368p6f ? 0.0f : v;              /* underflow (and -inf) */
     return x != x ? x + x : v;
 }
+__device__ __forceinline__ float expf_ref(float x) {
+    return expf_ref_with(x, [](int i) { return tlm_exp2_tab[i]; });
+}
+/* The same table held by a wave's lanes (lane l keeps entry l mod 32), for
+ * kernels whose exponentials should not wait on a global read: a lookup is
+ * two cross-lane reads.  Every lane of the wave must take part in a lookup. */
+struct ExpTabLanes {
+    uint32_t lo, hi;
+    __device__ __forceinline__ void load() {
+        const uint64_t v = tlm_exp2_tab[__lane_id() & 31];
+        lo = (uint32_t)v;
+        hi = (uint32_t)(v >> 32);
+    }
+    __device__ __forceinline__ uint64_t operator()(int i) const {
+        return ((uint64_t)(uint32_t)__shfl((int)hi, i, 64) << 32) | (uint32_t)__shfl((int)lo, i, 64);
+    }
+};
 
 /* Address-space qualified pointers.  Pointers that travel through structs,
  * tables or lambdas lose their address space and compile to flat_* accesses,
