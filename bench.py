@@ -46,9 +46,9 @@ GATEUP_BYTES = K * 2 * MAT_BYTES         # 20,643,840 B per gate/up launch
 DOWN_BYTES = K * MAT_BYTES               # 10,321,920 B per down launch
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per gate/up launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (KiB per dispatch), each
-# scaled by its reading for a 256 MiB device copy (factors 1.99976 and 1.0); the run and its
+# scaled by its reading for a 256 MiB device copy (factors 1.99980 and 1.0); the run and its
 # figures: profiles/moe_block_qwen3_30b_hbm_traffic.md
-GATEUP_TRAFFIC_BYTES = 20918804
+GATEUP_TRAFFIC_BYTES = 20945811
 
 
 def log(msg):
@@ -660,6 +660,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill measurement")
     ap.add_argument("--no-store", action="store_true", help="skip the expert slot cache measurement")
     ap.add_argument("--no-c1", action="store_true", help="skip the whole-step synthetic model measurement")
+    ap.add_argument("--no-c3", action="store_true",
+                    help="skip the whole-model decode legs (graph replays): for profiler runs, which trace the "
+                         "other legs only; the line then carries no value")
     ap.add_argument("--store-tokens", type=int, default=400, help="tokens per slot-cache decode measurement")
     ap.add_argument("--no-c5", action="store_true", help="skip the Qwen3-235B-shape slot-cache measurement")
     ap.add_argument("--c5-tokens", type=int, default=20, help="timed tokens of the Qwen3-235B-shape slot-cache run")
@@ -683,10 +686,11 @@ def main():
     hq.init(0)
     assert hq.selftest_failures() == 0, "HIP self-test failures"
 
-    c3 = c3_bench(torch, args.steps, args.warmup, args.c3_context)
-    torch.cuda.empty_cache()
-    c3s = None
-    if args.split_steps > 0:
+    c3 = c3s = None
+    if not args.no_c3:
+        c3 = c3_bench(torch, args.steps, args.warmup, args.c3_context)
+        torch.cuda.empty_cache()
+    if args.split_steps > 0 and not args.no_c3:
         c3s = c3_bench(torch, args.split_steps, args.warmup, args.c3_context, split=True)
         torch.cuda.empty_cache()
     peak = stream_read_peak(torch, dev, 2 << 30)
@@ -729,8 +733,15 @@ def main():
         threads = min(16, os.cpu_count() or 1)
         log(f"bench: cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(args, threads)
-        if cpu:
+        if cpu and c3:
             cpu["gpu_over_cpu"] = round(c3["tok_s"] / cpu["value"], 1)
+    if c3 is None:   # --no-c3: the other legs only
+        print(json.dumps({"metric": "decode tok/s batch-1, Qwen3-30B-A3B shape; expert GEMV HBM GB/s vs peak",
+                          "value": None, "unit": "tok/s", "n_gpus": 1, "note": "--no-c3: whole-model legs skipped",
+                          "expert_gemv": c2, "cpu_baseline": cpu, "prefill": prefill, "prefill_q5k": prefill_q5k,
+                          "slot_cache": slot_cache, "c1_whole_step": c1, "stream_read": peak,
+                          "qwen3_235b_a22b_slot_cache": c5}), flush=True)
+        return
 
     line = {
         "metric": "decode tok/s batch-1, Qwen3-30B-A3B shape; expert GEMV HBM GB/s vs peak",
