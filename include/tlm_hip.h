@@ -442,6 +442,21 @@ typedef struct {
                             merged per query head: each attention output within float rounding of
                             the reference's, but not its bits, and the int8 activation codes and
                             top-k routing downstream turn such differences into larger ones */
+    /* The experts through the HBM slot cache (tlm_hip_store) instead of all
+     * resident, as tierlm's runtime opens its store (src/bin/tierlm.c:
+     * 286-309: tlm_store_open, tlm_store_warm, tlm_model_open with the
+     * lookahead): each expert's packet payload stays in page-locked host
+     * memory, the step routes each layer on the device, the host acquires the
+     * experts (and hints the next layers') while the device runs on, and the
+     * block reads the slots (tlm_model.c:960-1055 through
+     * tlm_hip_moe_stack_store's loop with the attention queued before each
+     * router).  Such a step is not captured as a graph. */
+    uint64_t expert_cache_bytes; /* 0: every expert resident; else the slot budget (at least top_k slots) */
+    double   pin_frac;           /* memory.pin_frac: 0 = the reference's default 0.30, < 0 = none; capped so
+                                    pins leave top_k slots (src/bin/tierlm.c:288-294) */
+    int32_t  prefetch_off;       /* io.prefetch off: no hints, no lookahead (default: lookahead 1) */
+    int32_t  lookahead_k;        /* io.lookahead_k: experts hinted per lookahead layer (0 = top_k) */
+    double   interest;           /* nav.interest_aggressiveness (0 = fixed breadth) */
 } tlm_hip_model_opts;
 int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
 void tlm_hip_model_close(tlm_hip_model *M);
@@ -466,8 +481,11 @@ void tlm_hip_model_reset(tlm_hip_model *M);   /* tlm_kv_reset */
 typedef struct {
     int32_t  expert_dt, dense_dt;   /* Q4_K, Q5_K, Q6_K or Q8_0 (dtype codes above) */
     int32_t  qk_norm;               /* 1: q_norm / k_norm present */
-    int32_t  reserved;
+    int32_t  expert_pool;           /* with expert_cache_bytes: distinct expert payloads kept in host memory,
+                                       expert (l, e) using payload (l E + e) mod pool (0 = one each) */
     uint64_t seed;
+    double   heat_gamma;            /* > 0 with sigmoid routing: router bias -heat_gamma ln(r + 1) for the
+                                       expert of rank r in a seeded per-layer permutation (a Zipf-like heat) */
 } tlm_hip_model_synth_opts;
 int  tlm_hip_model_synth(const tlm_hip_model_geom *g, const tlm_hip_model_synth_opts *so,
                          const tlm_hip_model_opts *o, tlm_hip_model **out);
@@ -492,6 +510,10 @@ int  tlm_hip_model_sync(tlm_hip_model *M);
 /* the model's stream (hipStream_t), for callers that time or order work
  * against its steps */
 void *tlm_hip_model_stream(const tlm_hip_model *M);
+/* the model's expert slot cache (expert_cache_bytes > 0), for its counters
+ * (tlm_hip_store_get_stats) as tierlm's stats print them (src/bin/tierlm.c:
+ * 441-460); NULL when every expert is resident */
+tlm_hip_store *tlm_hip_model_expert_store(const tlm_hip_model *M);
 
 /* ---- reference tier ABI --------------------------------------------------
  * Layout-compatible with tlm_quant_kernels (src/lib/tlm_quant.h:152-166, a

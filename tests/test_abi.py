@@ -39,6 +39,7 @@ def test_python_binding_covers_header():
 def test_struct_layouts_match_c():
     from tierlm_amd._lib import (ExpertRef, ExpertSrc, ModelGeom, ModelSynthOpts, MoeDesc, PacketLoc, QuantKernels,
                                  Seg, StoreOpts, StoreStats, TensorRef)
+    from tierlm_amd.model import ModelOpts
     prog = r'''
 #include <stdio.h>
 #include <stddef.h>
@@ -62,8 +63,10 @@ int main(void) {
   O(tlm_hip_packet_loc, flags); O(tlm_hip_packet_loc, offset); O(tlm_hip_packet_loc, crc32c); O(tlm_hip_packet_loc, heat);
   O(tlm_hip_model_geom, router); O(tlm_hip_model_geom, rope_theta); O(tlm_hip_model_geom, rope_orig_len);
   O(tlm_hip_tensor_ref, dtype); O(tlm_hip_tensor_ref, shape); O(tlm_hip_tensor_ref, nbytes);
-  printf("synth %zu\n", sizeof(tlm_hip_model_synth_opts));
-  O(tlm_hip_model_synth_opts, qk_norm); O(tlm_hip_model_synth_opts, seed);
+  printf("synth %zu\nmopts %zu\n", sizeof(tlm_hip_model_synth_opts), sizeof(tlm_hip_model_opts));
+  O(tlm_hip_model_synth_opts, qk_norm); O(tlm_hip_model_synth_opts, seed); O(tlm_hip_model_synth_opts, heat_gamma);
+  O(tlm_hip_model_opts, attn_split); O(tlm_hip_model_opts, expert_cache_bytes); O(tlm_hip_model_opts, pin_frac);
+  O(tlm_hip_model_opts, lookahead_k); O(tlm_hip_model_opts, interest);
   return 0;
 }'''
     with tempfile.TemporaryDirectory() as d:
@@ -78,7 +81,8 @@ int main(void) {
     assert vals["moe"] == C.sizeof(MoeDesc)
     assert vals["qk"] == C.sizeof(QuantKernels)
     for name, cls in (("src", ExpertSrc), ("opts", StoreOpts), ("ref", ExpertRef), ("stats", StoreStats),
-                      ("loc", PacketLoc), ("geom", ModelGeom), ("tref", TensorRef), ("synth", ModelSynthOpts)):
+                      ("loc", PacketLoc), ("geom", ModelGeom), ("tref", TensorRef), ("synth", ModelSynthOpts),
+                      ("mopts", ModelOpts)):
         assert vals[name] == C.sizeof(cls), name
     for k, v in vals.items():
         if "." not in k:
@@ -87,7 +91,8 @@ int main(void) {
         cls = {"tlm_hip_seg": Seg, "tlm_hip_moe_desc": MoeDesc, "tlm_hip_quant_kernels": QuantKernels,
                "tlm_hip_expert_src": ExpertSrc, "tlm_hip_store_opts": StoreOpts, "tlm_hip_expert_ref": ExpertRef,
                "tlm_hip_store_stats": StoreStats, "tlm_hip_packet_loc": PacketLoc, "tlm_hip_model_geom": ModelGeom,
-               "tlm_hip_tensor_ref": TensorRef, "tlm_hip_model_synth_opts": ModelSynthOpts}[t]
+               "tlm_hip_tensor_ref": TensorRef, "tlm_hip_model_synth_opts": ModelSynthOpts,
+               "tlm_hip_model_opts": ModelOpts}[t]
         assert getattr(cls, f).offset == v, k
 
 

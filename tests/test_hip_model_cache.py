@@ -1,0 +1,136 @@
+"""The whole decode step with the experts in the HBM slot cache
+(tlm_hip_model_opts.expert_cache_bytes): the payloads stay in page-locked host
+memory, each layer routes on the device, the host acquires the experts (and
+hints the next layer's) and the block reads the slots - tierlm's runtime with
+its store (src/bin/tierlm.c:286-309, src/lib/tlm_model.c:960-1055).  A block
+that reads slots carries the resident block's bits, so:
+
+* on the reference's compiled stores (C1, C2S, C3S) the step must give the
+  reference's outputs exactly as the resident step does - teacher-forced
+  top-10 logits bit for bit, free-running greedy tokens - with a cache of
+  only top_k slots (every token evicts) and with one that holds every expert;
+* a synthetic model built with its experts in host memory (one payload per
+  expert) gives the resident synthetic model's logits and routing bit for bit,
+  for each expert dtype, with and without a shared expert;
+* the counters move as a cache's should (evictions on a cache of top_k
+  slots, hits and misses, lookahead hints issued and used), and a routing
+  heat plus the interest-weighted lookahead run."""
+import numpy as np
+import pytest
+
+from tests.test_hip_model import C1, C2S, C3S, greedy_tokens, needs_c1, needs_c2s, needs_c3s, prompt_tokens, \
+    teacher_forced
+
+pytestmark = pytest.mark.gpu
+
+TINY = 1          # raised to top_k slots by the model (src/bin/tierlm.c:273-285)
+ALL = 1 << 34     # every expert in a slot
+
+
+@needs_c1
+@pytest.mark.parametrize("budget", [TINY, ALL])
+def test_c1_cached_reference_bits(hip, budget):
+    from tierlm_amd.model import Model
+    m = Model(C1, max_ctx=256, expert_cache=budget)
+    try:
+        st = m.store_stats()
+        assert st is not None
+        assert st["slots"] == (m.geom.top_k if budget == TINY else m.geom.n_layers * m.geom.n_experts)
+        teacher_forced(m, "c1_oracle.jsonl", prompt_tokens() + greedy_tokens()[:63])
+        m.reset()
+        assert m.generate(prompt_tokens(), 64) == greedy_tokens()
+        st = m.store_stats()
+        assert st["misses"] > 0
+        if budget == TINY:   # 4 slots for 4 layers' top-4: every layer evicts the previous one's
+            assert st["evictions"] > 0
+        else:                # every expert stays once loaded
+            assert st["hits"] > 0 and st["evictions"] == 0
+    finally:
+        m.close()
+
+
+@needs_c2s
+def test_c2s_cached_reference_bits(hip):
+    """Sigmoid routing with selection bias and routed scale, Q4_K experts."""
+    from tierlm_amd.model import Model
+    m = Model(C2S, max_ctx=256, expert_cache=TINY)
+    try:
+        gen = greedy_tokens("c2s_greedy.txt")
+        teacher_forced(m, "c2s_oracle.jsonl", prompt_tokens(2048) + gen[:63])
+        m.reset()
+        assert m.generate(prompt_tokens(2048), 64) == gen
+    finally:
+        m.close()
+
+
+@needs_c3s
+def test_c3s_cached_reference_bits(hip):
+    """Qwen3-30B-A3B attention geometry, 16 experts top-8 through 8 slots,
+    over the fixture's 2047 positions."""
+    from tierlm_amd.model import Model
+    m = Model(C3S, max_ctx=2048, expert_cache=TINY, lookahead_k=12, interest=0.5)
+    try:
+        assert m.store_stats()["slots"] == 8
+        gen = greedy_tokens("c3s_greedy.txt")
+        prompt = prompt_tokens(2048, 1920)
+        teacher_forced(m, "c3s_oracle.jsonl", prompt + gen[:127])
+        m.reset()
+        assert m.generate(prompt, 128) == gen
+    finally:
+        m.close()
+
+
+SMALL = dict(n_layers=3, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, vocab=4096, n_experts=32, top_k=4,
+             d_expert=256, n_shared=0, d_shared=0, max_ctx=4096, router=0, rope_theta=1e6, norm_eps=1e-6,
+             routed_scale=1.0)
+
+
+@pytest.mark.parametrize("edt,shared,router", [(14, 0, 0), (12, 1, 0), (13, 0, 2), (8, 1, 2)])
+def test_synth_cached_equals_resident(hip, edt, shared, router):
+    """The same seed with the experts resident and in host memory behind a
+    cache of top_k slots: every step's logits and routing bit for bit."""
+    from tierlm_amd.model import Model, bench_prompt
+    g = dict(SMALL, n_shared=shared, d_shared=256 * shared, router=router)
+    a = Model.synth(g, expert_dt=edt, seed=5, max_ctx=64)
+    b = Model.synth(g, expert_dt=edt, seed=5, max_ctx=64, expert_cache=TINY)
+    try:
+        for pos, t in enumerate(bench_prompt(20, g["vocab"])):
+            la, na = a.step(t)
+            lb, nb = b.step(t)
+            assert na == nb and np.array_equal(la.view(np.uint32), lb.view(np.uint32)), pos
+            ia, wa = a.routes()
+            ib, wb = b.routes()
+            assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32)), pos
+        a.reset()
+        b.reset()
+        p = bench_prompt(8, g["vocab"])
+        assert a.generate(p, 12) == b.generate(p, 12)
+        assert b.store_stats()["evictions"] > 0
+    finally:
+        a.close()
+        b.close()
+
+
+def test_synth_cached_heat_lookahead(hip):
+    """Sigmoid routing with a Zipf-like selection bias, a pool of 6 distinct
+    payloads, the lookahead with interest-weighted breadth: a cache of half
+    the experts serves most selections; hints are issued and used."""
+    from tierlm_amd.model import Model, bench_prompt
+    g = dict(SMALL, router=2, n_layers=4)
+    slot = 3 * 256 * 512 // 256 * 210   # three Q6_K matrices of 256 x 512 (no padding at 256-byte alignment)
+    m = Model.synth(g, expert_dt=14, seed=9, max_ctx=96, expert_pool=6, heat_gamma=0.8,
+                    expert_cache=slot * 64, lookahead_k=8, interest=0.7)
+    try:
+        assert m.store_stats()["slots"] == 64
+        p = bench_prompt(16, g["vocab"])
+        out = m.generate(p, 48)
+        assert len(out) == 48
+        lg, _ = m.step(out[-1])
+        assert np.isfinite(lg).all()
+        st = m.store_stats()
+        total = st["hits"] + st["misses"]
+        assert total == (16 + 48) * 4 * 4
+        assert st["hits"] > st["misses"]
+        assert st["prefetch_issued"] > 0 and st["prefetch_used"] > 0
+    finally:
+        m.close()

@@ -95,8 +95,8 @@ class ModelGeom(C.Structure):
 
 class ModelSynthOpts(C.Structure):
     """tlm_hip_model_synth_opts"""
-    _fields_ = [("expert_dt", C.c_int32), ("dense_dt", C.c_int32), ("qk_norm", C.c_int32), ("reserved", C.c_int32),
-                ("seed", C.c_uint64)]
+    _fields_ = [("expert_dt", C.c_int32), ("dense_dt", C.c_int32), ("qk_norm", C.c_int32), ("expert_pool", C.c_int32),
+                ("seed", C.c_uint64), ("heat_gamma", C.c_double)]
 
 
 class TensorRef(C.Structure):
@@ -179,6 +179,7 @@ _SIGS = {
     "tlm_hip_model_decode": (i32, [vp, i32]),
     "tlm_hip_model_sync": (i32, [vp]),
     "tlm_hip_model_stream": (vp, [vp]),
+    "tlm_hip_model_expert_store": (vp, [vp]),
     "tlm_hip_model_reset": (None, [vp]),
     "tlm_hip_model_step": (i32, [vp, i32, vp, C.POINTER(C.c_int32)]),
     "tlm_hip_model_generate": (i32, [vp, C.POINTER(C.c_int32), i32, i32, C.POINTER(C.c_int32)]),

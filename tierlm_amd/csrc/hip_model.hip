@@ -1005,6 +1005,21 @@ struct tlm_hip_model {
     int32_t *host_tok = nullptr;   /* pinned */
     hipGraphExec_t graph[2] = {nullptr, nullptr};   /* step without / with logits, captured at first use */
     bool graph_failed[2] = {false, false};
+    /* experts through the slot cache (expert_cache_bytes > 0) */
+    uint64_t xs_budget = 0;
+    double xs_pin = 0.0;
+    bool xs_prefetch = true;
+    tlm_hip_store *xs = nullptr;
+    void *xs_payload = nullptr;                  /* page-locked expert payloads */
+    std::vector<tlm_hip_expert_src> xs_src;
+    uint8_t *stack_ws = nullptr;
+    tlm_hip_stack_opts xopts{};
+    std::vector<double> instinct;                /* tlm_model's per-layer instinct (tlm_model.c:974-980) */
+    std::vector<uint32_t> instinct_seen;
+    std::vector<tlm_hip_moe_desc> descs;
+    std::vector<float> layer_heat;               /* mean manifest heat of a layer's experts (tlm_model.c:546-560) */
+    std::vector<int32_t> route_ids;              /* the last step's routing, n_layers x top_k (host) */
+    std::vector<float> route_w;
 
     void *dalloc(size_t n) {
         void *p = nullptr;
@@ -1014,10 +1029,12 @@ struct tlm_hip_model {
     }
     ~tlm_hip_model() {
         if (stream) (void)hipStreamSynchronize(stream);
+        if (xs) tlm_hip_store_close(xs);   /* waits for its loads, which read the payloads */
         for (hipGraphExec_t g : graph)
             if (g) (void)hipGraphExecDestroy(g);
         for (void *p : allocs) (void)hipFree(p);
         if (host_tok) (void)hipHostFree(host_tok);
+        if (xs_payload) (void)hipHostFree(xs_payload);
         if (stream) (void)hipStreamDestroy(stream);
     }
 };
@@ -1146,7 +1163,16 @@ int prepare(tlm_hip_model *M, const tlm_hip_model_opts *o) {
     if (max_ctx <= 0) max_ctx = g.max_ctx > 0 ? (int)g.max_ctx : 4096;
     if (g.max_ctx > 0 && max_ctx > (int)g.max_ctx) max_ctx = (int)g.max_ctx;
     M->max_ctx = max_ctx;
-    M->graph_failed[0] = M->graph_failed[1] = o && o->eager;
+    M->xs_budget = o ? o->expert_cache_bytes : 0;
+    M->xs_pin = !o || o->pin_frac == 0.0 ? 0.30 : o->pin_frac < 0.0 ? 0.0 : o->pin_frac;
+    M->xs_prefetch = !(o && o->prefetch_off);
+    M->xopts.lookahead = M->xs_prefetch ? 1 : 0;   /* src/bin/tierlm.c:307-309 */
+    M->xopts.lookahead_k = o ? o->lookahead_k : 0;
+    M->xopts.interest = o ? o->interest : 0.0;
+    if (M->xopts.lookahead_k < 0 || M->xopts.lookahead_k > 32)
+        return tlmh_seterr(TLM_HIP_EINVAL, "model: lookahead_k %d (0..32)", M->xopts.lookahead_k);
+    /* a step through the cache waits on the host between layers: never a graph */
+    M->graph_failed[0] = M->graph_failed[1] = (o && o->eager) || M->xs_budget > 0;
     if (!att_supported((int)g.head_dim, (int)g.n_heads, (int)g.n_kv_heads))
         return tlmh_seterr(TLM_HIP_EUNSUP, "model: %u query heads per key head of width %u exceed the attention "
                            "kernel's share", g.n_heads / g.n_kv_heads, g.head_dim);
@@ -1225,6 +1251,55 @@ int finish(tlm_hip_model *M) {
     return tlmh_check(hipStreamSynchronize(M->stream), "model: load");
 }
 
+/* The experts' slot cache over M->xs_src (payloads already in M->xs_payload):
+ * the budget raised to top_k slots and the pin share capped so that pins
+ * leave top_k slots (src/bin/tierlm.c:273-294), tlm_store_open +
+ * tlm_store_warm (:295-305); the step's stack workspace and state. */
+int open_expert_store(tlm_hip_model *M) {
+    const tlm_hip_model_geom &g = M->g;
+    const int64_t D = g.d_model, de = g.d_expert;
+    size_t slot = 0;
+    for (const tlm_hip_expert_src &x : M->xs_src) {
+        if (x.flags & 2u) continue;
+        size_t at = 0;
+        const int64_t rows[3] = {de, de, D}, n[3] = {D, D, de};
+        for (int k = 0; k < 3; k++) at += (packed_bytes(x.dtype, rows[k], n[k]) + 255) & ~(size_t)255;
+        slot = std::max(slot, at);
+    }
+    if (slot == 0) return tlmh_seterr(TLM_HIP_EFORMAT, "model: no experts for the slot cache");
+    uint64_t budget = std::max<uint64_t>(M->xs_budget, (uint64_t)g.top_k * slot);
+    uint64_t ns = budget / slot;
+    ns = std::min<uint64_t>(ns, M->xs_src.size());
+    double pin = M->xs_pin;
+    if (ns > 0 && pin > 0.0) {
+        const double maxf = (double)(ns > g.top_k ? ns - g.top_k : 0) / (double)ns;
+        pin = std::min(pin, maxf);
+    }
+    tlm_hip_store_opts so{};
+    so.d_model = D;
+    so.d_expert = de;
+    so.top_k = (int32_t)g.top_k;
+    so.prefetch = M->xs_prefetch ? 1 : 0;
+    so.pin_frac = pin;
+    so.budget_bytes = budget;
+    int rc = tlm_hip_store_open(M->xs_src.data(), (int)M->xs_src.size(), &so, &M->xs);
+    if (!rc) rc = tlm_hip_store_warm(M->xs);
+    if (rc) return rc;
+    M->descs.clear();
+    for (const Layer &Ly : M->L) M->descs.push_back(Ly.moe);
+    M->instinct.assign(g.n_layers, 0.0);
+    M->instinct_seen.assign(g.n_layers, 0);
+    if (M->layer_heat.size() == g.n_layers) M->xopts.layer_heat = M->layer_heat.data();
+    M->xopts.instinct = M->instinct.data();
+    M->xopts.instinct_seen = M->instinct_seen.data();
+    M->route_ids.assign((size_t)g.n_layers * g.top_k, 0);
+    M->route_w.assign((size_t)g.n_layers * g.top_k, 0.0f);
+    const size_t ws = tlm_hip_moe_stack_workspace_bytes(M->descs.data(), (int)g.n_layers, &M->xopts);
+    M->stack_ws = (uint8_t *)M->dalloc(ws + 256);
+    if (!M->stack_ws) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the stack workspace");
+    return TLM_HIP_OK;
+}
+
 int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
     M->g = *tlm_hip_manifest_geom(m);
     int rc = prepare(M, o);
@@ -1280,15 +1355,22 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
             d.sd = sd.p;
         }
     }
-    /* experts (load_experts, tlm_model.c:343-392): every one resident, packed */
+    /* experts (load_experts, tlm_model.c:343-392): every one resident, packed;
+     * or, with the slot cache, every payload kept in page-locked host memory */
+    const bool cached = M->xs_budget > 0;
     std::vector<std::vector<const void *>> tables(g.n_layers, std::vector<const void *>(3 * E, nullptr));
     std::vector<std::vector<uint8_t>> masks(g.n_layers, std::vector<uint8_t>(E, 1));
     std::vector<int> edt(g.n_layers, -1);
+    std::vector<std::vector<uint8_t>> payloads;
+    std::vector<double> heat_sum(g.n_layers, 0.0);
+    std::vector<int> heat_cnt(g.n_layers, 0);
     for (int i = 0; i < tlm_hip_manifest_n_packets(m); i++) {
         const tlm_hip_packet_loc *loc = tlm_hip_manifest_packet(m, i);
         if (loc->type != TLM_HIP_PK_EXPERT) continue;
         if (loc->layer >= g.n_layers || loc->id >= E)
             return tlmh_seterr(TLM_HIP_EFORMAT, "model: EXPERT packet %u:%u out of range", loc->layer, loc->id);
+        heat_sum[loc->layer] += loc->heat;
+        heat_cnt[loc->layer]++;
         if (loc->flags & 2u) continue;   /* pruned: never routable */
         Packet pk;
         pk.buf.resize(loc->total_len);
@@ -1306,11 +1388,40 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
             const uint64_t raw = (uint64_t)shapes[k][0] * (uint64_t)(shapes[k][1] / bv) * (uint64_t)dt_block_bytes(dt);
             if ((uint64_t)off[k] + raw > pk.len)
                 return tlmh_seterr(TLM_HIP_EFORMAT, "model: expert %u:%u item %d overruns", loc->layer, loc->id, k);
+            if (cached) continue;
             DevMat dm;
             if ((rc = dev_matrix(M, dt, pk.payload() + off[k], shapes[k][0], shapes[k][1], &dm))) return rc;
             tables[loc->layer][3 * loc->id + k] = dm.p;
         }
         masks[loc->layer][loc->id] = 0;
+        if (cached) {   /* the store's source: layer, flags, id, dtype, heat, item offsets, payload */
+            tlm_hip_expert_src x{};
+            x.layer = (uint16_t)loc->layer;
+            x.flags = (uint16_t)(loc->flags & 1u);
+            x.id = loc->id;
+            x.dtype = dt;
+            x.heat = loc->heat;
+            for (int k = 0; k < 3; k++) x.item_off[k] = off[k];
+            x.payload_len = pk.len;
+            M->xs_src.push_back(x);
+            payloads.emplace_back(pk.payload(), pk.payload() + pk.len);
+        }
+    }
+    M->layer_heat.assign(g.n_layers, 0.0f);
+    for (uint32_t l = 0; l < g.n_layers; l++)
+        M->layer_heat[l] = heat_cnt[l] ? (float)(heat_sum[l] / (double)heat_cnt[l]) : 0.0f;
+    if (cached) {   /* one page-locked block for every payload */
+        size_t total = 0;
+        for (const auto &pl : payloads) total += (pl.size() + 255) & ~(size_t)255;
+        if ((rc = tlmh_check(hipHostMalloc(&M->xs_payload, total ? total : 256, hipHostMallocDefault),
+                             "model: page-locked expert payloads")))
+            return rc;
+        size_t at = 0;
+        for (size_t i = 0; i < payloads.size(); i++) {
+            memcpy((uint8_t *)M->xs_payload + at, payloads[i].data(), payloads[i].size());
+            M->xs_src[i].payload = (uint8_t *)M->xs_payload + at;
+            at += (payloads[i].size() + 255) & ~(size_t)255;
+        }
     }
     for (uint32_t l = 0; l < g.n_layers; l++) {
         int live = 0;
@@ -1318,6 +1429,14 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
         if (live < (int)g.top_k)   /* tlm_model.c:597-600 */
             return tlmh_seterr(TLM_HIP_EFORMAT, "model: layer %u has %d routable experts, needs top_k=%u", l, live,
                                g.top_k);
+        if (cached) {   /* the block reads the slots the store hands out; no table */
+            void *mp;
+            if ((rc = dev_upload(M, masks[l].data(), masks[l].size(), &mp))) return rc;
+            M->L[l].moe.experts = nullptr;
+            M->L[l].moe.mask = (const uint8_t *)mp;
+            M->L[l].moe.expert_dt = edt[l];
+            continue;
+        }
         /* absent experts point at a present one: never routed (masked), never read */
         const void *any[3] = {nullptr, nullptr, nullptr};
         for (int64_t e = 0; e < E && !any[0]; e++)
@@ -1357,6 +1476,7 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
         if ((rc = dev_upload(M, pk.payload() + t.offset, (size_t)t.nbytes, &p))) return rc;
         M->embd = (const uint8_t *)p;
     }
+    if (M->xs_budget > 0 && (rc = open_expert_store(M))) return rc;
     return finish(M);
 }
 
@@ -1364,57 +1484,99 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
  * seq[pos], pos = st[0]; with logits, the greedy next token goes to
  * seq[pos + 1]; st[0] advances.  Every argument is the same at every position
  * (the step is captured once as a graph). */
-int enqueue_step(tlm_hip_model *M, bool want_logits) {
+/* layer l's attention (attention(), tlm_model.c:730-763): q | k | v in one
+ * launch whose groups each normalise and quantise h themselves, the two
+ * attention kernels, o added into h */
+int enqueue_attention(tlm_hip_model *M, uint32_t l) {
     const tlm_hip_model_geom &g = M->g;
     const int D = (int)g.d_model, hd = (int)g.head_dim, H = (int)g.n_heads, KV = (int)g.n_kv_heads;
     hipStream_t s = M->stream;
-    hipLaunchKernelGGL(k_embed, dim3((D + NT - 1) / NT), dim3(NT), 0, s, M->embd, M->embd_row, M->embd_dt,
-                       (const int32_t *)M->seq, (const int32_t *)M->st, D, M->h);
-    int rc = tlmh_check(hipGetLastError(), "model: embed");
-    for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
-        const Layer &Ly = M->L[l];
-        /* attention(), tlm_model.c:730-763: q | k | v in one launch whose
-         * groups each normalise and quantise h themselves, the fused head
-         * kernel, o added into h */
-        const MvNorm an{M->h, Ly.attn_norm, g.norm_eps};
-        const void *W3[3] = {Ly.q.p, Ly.k.p, Ly.v.p};
-        const int64_t R3[3] = {Ly.q.rows, Ly.k.rows, Ly.v.rows};
-        float *const Y3[3] = {M->q, M->kx, M->vx};
-        if (Ly.q.dt == Ly.k.dt && Ly.q.dt == Ly.v.dt) {
-            rc = launch_mv_segs(Ly.q.dt, D, W3, R3, Y3, 3, 0, nullptr, s, &an);
-        } else {
-            for (int m = 0; m < 3 && !rc; m++) {
-                const DevMat &Wm = m == 0 ? Ly.q : m == 1 ? Ly.k : Ly.v;
-                rc = launch_mv_segs(Wm.dt, D, &W3[m], &R3[m], &Y3[m], 1, 0, nullptr, s, &an);
-            }
+    const Layer &Ly = M->L[l];
+    const MvNorm an{M->h, Ly.attn_norm, g.norm_eps};
+    const void *W3[3] = {Ly.q.p, Ly.k.p, Ly.v.p};
+    const int64_t R3[3] = {Ly.q.rows, Ly.k.rows, Ly.v.rows};
+    float *const Y3[3] = {M->q, M->kx, M->vx};
+    int rc = TLM_HIP_OK;
+    if (Ly.q.dt == Ly.k.dt && Ly.q.dt == Ly.v.dt) {
+        rc = launch_mv_segs(Ly.q.dt, D, W3, R3, Y3, 3, 0, nullptr, s, &an);
+    } else {
+        for (int m = 0; m < 3 && !rc; m++) {
+            const DevMat &Wm = m == 0 ? Ly.q : m == 1 ? Ly.k : Ly.v;
+            rc = launch_mv_segs(Wm.dt, D, &W3[m], &R3[m], &Y3[m], 1, 0, nullptr, s, &an);
         }
-        if (rc) break;
-        const size_t kbase = (size_t)l * KV * M->max_ctx * hd, vbase = (size_t)l * KV * att_vstride(M->max_ctx, hd);
-        rc = launch_attn(hd, H, KV, M->max_ctx, M->att_g, M->att_split, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm,
-                         M->cs, M->sn, M->kc + kbase, M->vc + vbase, M->scores, M->part_o, M->part_ml,
-                         M->att, (const int32_t *)M->st, g.norm_eps, s);
-        /* o: every group quantises the attention output itself */
-        const MvNorm ao{M->att, nullptr, 0.0f};
-        const void *Wo = Ly.o.p;
-        const int64_t Ro = Ly.o.rows;
-        float *const Yo = M->h;
-        if (!rc) rc = launch_mv_segs(Ly.o.dt, (int64_t)H * hd, &Wo, &Ro, &Yo, 1, 1, nullptr, s, &ao);
-        /* moe(), tlm_model.c:940-1055 */
-        if (!rc) rc = launch_moe_layer(&Ly.moe, M->h, M->ids + (size_t)l * 32, M->w + (size_t)l * 32, M->moe_ws, s);
     }
     if (rc) return rc;
+    const size_t kbase = (size_t)l * KV * M->max_ctx * hd, vbase = (size_t)l * KV * att_vstride(M->max_ctx, hd);
+    rc = launch_attn(hd, H, KV, M->max_ctx, M->att_g, M->att_split, M->q, M->kx, M->vx, Ly.q_norm, Ly.k_norm,
+                     M->cs, M->sn, M->kc + kbase, M->vc + vbase, M->scores, M->part_o, M->part_ml,
+                     M->att, (const int32_t *)M->st, g.norm_eps, s);
+    /* o: every group quantises the attention output itself */
+    const MvNorm ao{M->att, nullptr, 0.0f};
+    const void *Wo = Ly.o.p;
+    const int64_t Ro = Ly.o.rows;
+    float *const Yo = M->h;
+    if (!rc) rc = launch_mv_segs(Ly.o.dt, (int64_t)H * hd, &Wo, &Ro, &Yo, 1, 1, nullptr, s, &ao);
+    return rc;
+}
+
+/* the step's end: final norm + lm_head with the greedy keys (tlm_model.c:
+ * 1087-1095), then the argmax and the position's advance */
+int enqueue_tail(tlm_hip_model *M, bool want_logits) {
+    const tlm_hip_model_geom &g = M->g;
+    const int D = (int)g.d_model;
+    hipStream_t s = M->stream;
     const int nkeys = (int)((g.vocab + TILE_ROWS - 1) / TILE_ROWS);
-    if (want_logits) {   /* tlm_model.c:1087-1095 (norm in the lm_head's groups), the greedy key */
+    if (want_logits) {
         const MvNorm on{M->h, M->out_norm, g.norm_eps};
         const void *Wl = M->lm_head.p;
         const int64_t Rl = M->lm_head.rows;
         float *const Yl = M->logits;
-        rc = launch_mv_segs(M->lm_head.dt, D, &Wl, &Rl, &Yl, 1, 0, nullptr, s, &on, M->keys);
+        const int rc = launch_mv_segs(M->lm_head.dt, D, &Wl, &Rl, &Yl, 1, 0, nullptr, s, &on, M->keys);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(want_logits ? 1024 : 64), 0, s, M->st, M->seq,
                        want_logits ? (const unsigned long long *)M->keys : nullptr, nkeys);
     return tlmh_check(hipGetLastError(), "model: step");
+}
+
+void enqueue_embed(tlm_hip_model *M) {
+    const int D = (int)M->g.d_model;
+    hipLaunchKernelGGL(k_embed, dim3((D + NT - 1) / NT), dim3(NT), 0, M->stream, M->embd, M->embd_row, M->embd_dt,
+                       (const int32_t *)M->seq, (const int32_t *)M->st, D, M->h);
+}
+
+/* tlm_model_step, src/lib/tlm_model.c:1058-1103, enqueued: the token is
+ * seq[pos], pos = st[0]; with logits, the greedy next token goes to
+ * seq[pos + 1]; st[0] advances.  Every argument is the same at every position
+ * (the step is captured once as a graph). */
+int enqueue_step(tlm_hip_model *M, bool want_logits) {
+    enqueue_embed(M);
+    int rc = tlmh_check(hipGetLastError(), "model: embed");
+    for (uint32_t l = 0; l < M->g.n_layers && !rc; l++) {
+        const Layer &Ly = M->L[l];
+        rc = enqueue_attention(M, l);
+        /* moe(), tlm_model.c:940-1055 */
+        if (!rc) rc = launch_moe_layer(&Ly.moe, M->h, M->ids + (size_t)l * 32, M->w + (size_t)l * 32, M->moe_ws,
+                                       M->stream);
+    }
+    if (rc) return rc;
+    return enqueue_tail(M, want_logits);
+}
+
+/* The same step with the experts in the slot cache: tlm_model_step's layer
+ * loop with moe() through the store (tlm_model.c:960-1055) and the router
+ * lookahead, one tick per token (:1097): each layer's attention is queued
+ * right before its router, and the host acquires layer l + 1's experts while
+ * the device runs layer l's block (moe_stack_run). */
+int step_cached(tlm_hip_model *M, bool want_logits) {
+    enqueue_embed(M);
+    int rc = tlmh_check(hipGetLastError(), "model: embed");
+    if (!rc)
+        rc = moe_stack_run(M->descs.data(), (int)M->g.n_layers, M->xs, M->h, &M->xopts, M->route_ids.data(),
+                           M->route_w.data(), M->stack_ws, M->stream,
+                           [M](int l) { return enqueue_attention(M, (uint32_t)l); });
+    if (rc) return rc;
+    return enqueue_tail(M, want_logits);
 }
 
 /* One step (the caller checked the context): the captured graph of the kind,
@@ -1437,8 +1599,9 @@ int step(tlm_hip_model *M, bool want_logits) {
             (void)hipGetLastError();
         }
     }
-    int rc = M->graph[k] ? tlmh_check(hipGraphLaunch(M->graph[k], M->stream), "model: step graph")
-                         : enqueue_step(M, want_logits);
+    int rc = M->xs ? step_cached(M, want_logits)
+             : M->graph[k] ? tlmh_check(hipGraphLaunch(M->graph[k], M->stream), "model: step graph")
+                           : enqueue_step(M, want_logits);
     if (!rc) M->kv_len++;
     return rc;
 }
@@ -1552,10 +1715,28 @@ int synth(tlm_hip_model *M, const tlm_hip_model_synth_opts *so, const tlm_hip_mo
     if (!tmp) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
     uint64_t tensor = 0;
     auto next = [&]() { return mix64(so->seed * 0x100000001B3ull + ++tensor); };
-    /* experts: one arena, 256-byte aligned matrices */
+    /* experts: one arena, 256-byte aligned matrices; or, with the slot cache,
+     * payloads in the reference's row layout (gate | up | down) in page-locked
+     * host memory, expert (l, e) reading payload (l E + e) mod pool - the same
+     * bytes as the resident arena's when every expert has its own */
+    const bool cached = M->xs_budget > 0;
     const size_t pg = (packed_bytes(edt, de, D) + 255) & ~(size_t)255, pd = (packed_bytes(edt, D, de) + 255) & ~(size_t)255;
-    uint8_t *arena = (uint8_t *)M->dalloc((size_t)g.n_layers * E * (2 * pg + pd));
-    if (!arena) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory for the experts");
+    uint8_t *arena = nullptr;
+    if (!cached) {
+        arena = (uint8_t *)M->dalloc((size_t)g.n_layers * E * (2 * pg + pd));
+        if (!arena) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory for the experts");
+    }
+    const int ebv = dt_block_values(edt);
+    const size_t rg = (size_t)(D / ebv) * dt_block_bytes(edt), rd = (size_t)(de / ebv) * dt_block_bytes(edt);
+    const size_t plen = 2 * (size_t)de * rg + (size_t)D * rd, pst = (plen + 255) & ~(size_t)255;
+    const int64_t nexp = (int64_t)g.n_layers * E;
+    const int64_t pool = cached ? (so->expert_pool > 0 ? std::min<int64_t>(so->expert_pool, nexp) : nexp) : 0;
+    if (cached) {
+        if ((rc = tlmh_check(hipHostMalloc(&M->xs_payload, (size_t)pool * pst, hipHostMallocDefault),
+                             "model synth: page-locked expert payloads")))
+            return rc;
+        M->xs_src.reserve((size_t)nexp);
+    }
     std::vector<const void *> table(3 * E);
     for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
         Layer &Ly = M->L[l];
@@ -1583,21 +1764,66 @@ int synth(tlm_hip_model *M, const tlm_hip_model_synth_opts *so, const tlm_hip_mo
         d.ffn_norm = Ly.ffn_norm;
         d.router_w = synth_vec(M, E * D, next(), 1.0f / sqrtf((float)D), 0.0f);
         if (!d.router_w) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
+        if (so->heat_gamma > 0.0 && g.router == 2) {   /* bias -gamma ln(rank + 1), ranks a seeded permutation */
+            std::vector<int> perm(E);
+            for (int64_t e = 0; e < E; e++) perm[e] = (int)e;
+            uint64_t r = next();
+            for (int64_t e = E - 1; e > 0; e--) {   /* Fisher-Yates on the splitmix64 stream */
+                r = mix64(r);
+                std::swap(perm[e], perm[(int64_t)(r % (uint64_t)(e + 1))]);
+            }
+            std::vector<float> bias(E);
+            for (int64_t e = 0; e < E; e++) bias[e] = (float)(-so->heat_gamma * log((double)perm[e] + 1.0));
+            void *bp;
+            if ((rc = dev_upload(M, bias.data(), bias.size() * 4, &bp))) return rc;
+            d.router_bias = (const float *)bp;
+        }
         d.expert_dt = edt;
         for (int64_t e = 0; e < E && !rc; e++) {
+            const uint64_t s1 = next(), s2 = next(), s3 = next();
+            if (cached) {
+                const int64_t slot = ((int64_t)l * E + e) % pool;
+                uint8_t *hp = (uint8_t *)M->xs_payload + (size_t)slot * pst;
+                if ((int64_t)l * E + e < pool) {   /* this payload's bytes, as the arena would hold them */
+                    const uint64_t seeds[3] = {s1, s2, s3};
+                    const int64_t rows[3] = {de, de, D}, n[3] = {D, D, de};
+                    const size_t off[3] = {0, (size_t)de * rg, 2 * (size_t)de * rg};
+                    const size_t bytes[3] = {(size_t)de * rg, (size_t)de * rg, (size_t)D * rd};
+                    for (int k = 0; k < 3 && !rc; k++) {
+                        rc = synth_rows(M->stream, edt, tmp, rows[k], n[k], seeds[k]);
+                        if (!rc) rc = tlmh_check(hipMemcpyAsync(hp + off[k], tmp, bytes[k], hipMemcpyDeviceToHost,
+                                                                M->stream), "model synth: payload");
+                        if (!rc) rc = tlmh_check(hipStreamSynchronize(M->stream), "model synth: payload");
+                    }
+                    if (rc) return rc;
+                }
+                tlm_hip_expert_src x{};
+                x.layer = (uint16_t)l;
+                x.id = (uint32_t)e;
+                x.dtype = edt;
+                x.item_off[0] = 0;
+                x.item_off[1] = (uint32_t)((size_t)de * rg);
+                x.item_off[2] = (uint32_t)(2 * (size_t)de * rg);
+                x.payload_len = plen;
+                x.payload = hp;
+                M->xs_src.push_back(x);
+                continue;
+            }
             uint8_t *base = arena + ((size_t)l * E + e) * (2 * pg + pd);
             DevMat dm;
-            if ((rc = synth_matrix(M, edt, de, D, next(), tmp, base, &dm)) ||
-                (rc = synth_matrix(M, edt, de, D, next(), tmp, base + pg, &dm)) ||
-                (rc = synth_matrix(M, edt, D, de, next(), tmp, base + 2 * pg, &dm)))
+            if ((rc = synth_matrix(M, edt, de, D, s1, tmp, base, &dm)) ||
+                (rc = synth_matrix(M, edt, de, D, s2, tmp, base + pg, &dm)) ||
+                (rc = synth_matrix(M, edt, D, de, s3, tmp, base + 2 * pg, &dm)))
                 return rc;
             table[3 * e] = base;
             table[3 * e + 1] = base + pg;
             table[3 * e + 2] = base + 2 * pg;
         }
-        void *tp;
-        if ((rc = dev_upload(M, table.data(), table.size() * sizeof(void *), &tp))) return rc;
-        d.experts = (const void *const *)tp;
+        if (!cached) {
+            void *tp;
+            if ((rc = dev_upload(M, table.data(), table.size() * sizeof(void *), &tp))) return rc;
+            d.experts = (const void *const *)tp;
+        }
         if (ds > 0) {
             DevMat sg, su, sd;
             if ((rc = synth_matrix(M, edt, ds, D, next(), tmp, nullptr, &sg)) ||
@@ -1621,6 +1847,7 @@ int synth(tlm_hip_model *M, const tlm_hip_model_synth_opts *so, const tlm_hip_mo
     if (!embd) return tlmh_seterr(TLM_HIP_ENOMEM, "model synth: out of device memory");
     if ((rc = synth_rows(M->stream, DT_Q8_0, embd, V, D, next()))) return rc;
     M->embd = embd;
+    if (cached && (rc = open_expert_store(M))) return rc;
     return finish(M);
 }
 
@@ -1671,6 +1898,13 @@ int tlm_hip_model_kv_capacity(const tlm_hip_model *M) { return M ? M->max_ctx : 
 int tlm_hip_model_routes(tlm_hip_model *M, int32_t *ids, float *w) {
     if (!M || !ids || !w) return tlmh_seterr(TLM_HIP_EINVAL, "model routes: NULL argument");
     const int L = (int)M->g.n_layers, k = (int)M->g.top_k;
+    if (M->xs) {   /* the cached step read them on the host */
+        int rc = tlmh_check(hipStreamSynchronize(M->stream), "model routes");
+        if (rc) return rc;
+        memcpy(ids, M->route_ids.data(), (size_t)L * k * 4);
+        memcpy(w, M->route_w.data(), (size_t)L * k * 4);
+        return TLM_HIP_OK;
+    }
     std::vector<int32_t> di((size_t)L * 32);
     std::vector<float> dw((size_t)L * 32);
     int rc = tlmh_check(hipStreamSynchronize(M->stream), "model routes");
@@ -1711,6 +1945,7 @@ int tlm_hip_model_sync(tlm_hip_model *M) {
 }
 
 void *tlm_hip_model_stream(const tlm_hip_model *M) { return M ? (void *)M->stream : nullptr; }
+tlm_hip_store *tlm_hip_model_expert_store(const tlm_hip_model *M) { return M ? M->xs : nullptr; }
 
 void tlm_hip_model_reset(tlm_hip_model *M) {
     if (!M) return;

@@ -1306,8 +1306,10 @@ size_t moe_route_offset(const tlm_hip_moe_desc *d) { return ws_layout(*d).route;
 
 static size_t x_area(int kind, int nb) { return (stage_bytes(kind, nb) + 15) & ~(size_t)15; }
 
-/* descriptor checks shared by the decode and prefill launches */
-static int moe_check(const tlm_hip_moe_desc *d, const float *h, const void *ws) {
+/* descriptor checks shared by the decode and prefill launches; table: the
+ * launch reads the expert table (not the routing-only launches, nor a block
+ * whose routed matrices are given) */
+static int moe_check(const tlm_hip_moe_desc *d, const float *h, const void *ws, bool table = true) {
     if (!d || !h || !ws) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL argument");
     if ((uintptr_t)ws & 255u) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: workspace must be 256-byte aligned");
     if (d->E <= 0 || d->E > MAXE || d->k <= 0 || d->k > MAXK || d->k > d->E)
@@ -1328,7 +1330,8 @@ static int moe_check(const tlm_hip_moe_desc *d, const float *h, const void *ws) 
                                (long long)d->ds);
         if (!d->sg || !d->su || !d->sd) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: shared matrices missing");
     }
-    if (!d->ffn_norm || !d->router_w || !d->experts) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL weights");
+    if (!d->ffn_norm || !d->router_w || (table && !d->experts))
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: NULL weights");
     if (((uintptr_t)h | (uintptr_t)d->ffn_norm) & 15u)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: h and ffn_norm must be 16-byte aligned");
     if ((size_t)d->D * 8 > 64 * 1024)
@@ -1341,7 +1344,7 @@ static int moe_check(const tlm_hip_moe_desc *d, const float *h, const void *ws) 
 static int moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
                      const MoeGiven *gvp, hipStream_t s) {
     if (phase < 0 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
-    if (int rc = moe_check(d, h, ws)) return rc;
+    if (int rc = moe_check(d, h, ws, gvp == nullptr && phase != 1)) return rc;
     const int ebv = dt_block_values(d->expert_dt);
     const int ek = dt_act_kind(d->expert_dt), sk = d->ds > 0 ? dt_act_kind(d->shared_dt) : ek;
     const int nbe = (int)(d->D / ebv), nbde = (int)(d->de / ebv);
@@ -1412,7 +1415,7 @@ int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, in
     int g = 0;
     size_t lds = 0;
     for (int i = 0; i < n; i++) {
-        if (int rc = moe_check(d[i], h, ws[i])) return rc;
+        if (int rc = moe_check(d[i], h, ws[i], false)) return rc;
         rs.d[i] = qs.d[i] = *d[i];
         rs.L[i] = qs.L[i] = ws_layout(*d[i]);
         rs.ws[i] = qs.ws[i] = (uint8_t *)ws[i];

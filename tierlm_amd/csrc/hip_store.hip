@@ -1032,19 +1032,23 @@ size_t tlm_hip_moe_stack_workspace_bytes(const tlm_hip_moe_desc *descs, int n_la
     return 2 * b + 2 * (size_t)depth * hb;
 }
 
+}  // extern "C"
+
 /* tlm_model_step's loop over moe() with the store (src/lib/tlm_model.c:
  * 1075-1083, 960-1055), lookahead() (:844-877) and the instinct update
  * (:974-980), then tlm_store_tick (:1097); pipelined as described in
- * tlm_hip.h. */
-int tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
-                            const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace,
-                            void *stream) {
+ * tlm_hip.h.  before(l), when given, enqueues what precedes layer l's router
+ * on the stream (a model's attention); it runs right before that router's
+ * launch, so layer l + 1's attention is queued behind layer l's block. */
+int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
+                  const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace, void *stream,
+                  const std::function<int(int)> &before) {
     if (!descs || n_layers <= 0 || !s || !h || !workspace)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: bad arguments");
     if ((uintptr_t)workspace & 255u)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: workspace must be 256-byte aligned");
     for (int l = 0; l < n_layers; l++)
-        if (descs[l].k <= 0 || descs[l].k > MOE_MAXK || !descs[l].experts)
+        if (descs[l].k <= 0 || descs[l].k > MOE_MAXK)
             return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: layer %d (k=%d)", l, descs[l].k);
     if (o && o->lookahead > 0 && o->lookahead_k > MOE_MAXK)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: lookahead_k %d above %d", o->lookahead_k, MOE_MAXK);
@@ -1061,6 +1065,10 @@ int tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip
     int nh = 0;
     /* layer l's routes (block + hints for l+1 .. l+depth) into area l mod 2 */
     auto enqueue = [&](int l, uint32_t *seq) {
+        if (before) {
+            const int rc = before(l);
+            if (rc) return rc;
+        }
         nh = std::min(depth, n_layers - 1 - l);
         for (int i = 0; i < nh; i++) {
             hd[i] = descs[l + 1 + i];
@@ -1119,6 +1127,17 @@ int tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip
     }
     if (!rc) tlm_hip_store_tick(s);
     return rc;
+}
+
+extern "C" {
+
+int tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
+                            const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace,
+                            void *stream) {
+    if (descs)
+        for (int l = 0; l < n_layers; l++)
+            if (!descs[l].experts) return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: layer %d has no expert table", l);
+    return moe_stack_run(descs, n_layers, s, h, o, ids_out, w_out, workspace, stream, {});
 }
 
 }  // extern "C"

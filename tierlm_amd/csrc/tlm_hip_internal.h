@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <functional>
+
 #include "../../include/tlm_hip.h"
 
 /* tlm_dtype codes (src/lib/tlm_quant.h:31-42) */
@@ -296,5 +298,11 @@ int launch_moe_phase_given(const tlm_hip_moe_desc *d, int phase, float *h, void 
                            hipStream_t s);
 int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, int n, const float *h,
                            uint32_t *host, int seq_off, uint32_t seq, hipStream_t s);
+/* tlm_hip_moe_stack_store's loop (hip_store.hip); before(l), when given,
+ * enqueues what precedes layer l's router (a model's attention) and returns 0
+ * or an error; descs' expert tables are not used */
+int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
+                  const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace, void *stream,
+                  const std::function<int(int)> &before);
 
 #endif

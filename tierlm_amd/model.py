@@ -19,7 +19,20 @@ from ._lib import check, lib
 
 class ModelOpts(C.Structure):
     """tlm_hip_model_opts"""
-    _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32), ("attn_split", C.c_int32)]
+    _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32), ("attn_split", C.c_int32),
+                ("expert_cache_bytes", C.c_uint64), ("pin_frac", C.c_double), ("prefetch_off", C.c_int32),
+                ("lookahead_k", C.c_int32), ("interest", C.c_double)]
+
+
+def model_opts(max_ctx=0, eager=False, attn_slices=0, split=False, expert_cache=0, pin_frac=0.0, prefetch=True,
+               lookahead_k=0, interest=0.0):
+    """tlm_hip_model_opts; expert_cache > 0 (bytes) serves the experts through
+    an HBM slot cache of that size from page-locked host memory, as tierlm's
+    runtime serves them from its store (pin_frac 0 = its default 0.30,
+    prefetch = its router lookahead, lookahead_k / interest its io and nav
+    options)."""
+    return ModelOpts(max_ctx, int(eager), attn_slices, int(split), int(expert_cache), float(pin_frac),
+                     0 if prefetch else 1, int(lookahead_k), float(interest))
 
 
 # Qwen3-30B-A3B: 48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128
@@ -30,25 +43,30 @@ QWEN3_30B_A3B = dict(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_d
 
 
 class Model:
-    def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0, split=False):
-        self.opts = ModelOpts(max_ctx, int(eager), attn_slices, int(split))
+    def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0, split=False, **cache):
+        """cache: expert_cache, pin_frac, prefetch, lookahead_k, interest (model_opts)"""
+        self.opts = model_opts(max_ctx, eager, attn_slices, split, **cache)
         h = C.c_void_p()
         check(lib.tlm_hip_model_open(str(manifest_path).encode(), C.byref(self.opts), C.byref(h)))
         self._bind(h)
 
     @classmethod
     def synth(cls, geom, expert_dt=14, dense_dt=8, qk_norm=True, seed=1, max_ctx=0, eager=False, attn_slices=0,
-              split=False):
+              split=False, expert_pool=0, heat_gamma=0.0, **cache):
         """tlm_hip_model_synth: a random-init model of geometry geom (a dict of
-        tlm_hip_model_geom fields) built in HBM."""
+        tlm_hip_model_geom fields) built in HBM; with cache (model_opts'
+        expert_cache ...) its experts stay in page-locked host memory (a pool
+        of expert_pool distinct payloads, 0 = one each) behind the slot cache;
+        heat_gamma > 0 with sigmoid routing biases selection towards a
+        per-layer order of the experts (-heat_gamma ln(rank + 1))."""
         from ._lib import ModelGeom, ModelSynthOpts
         g = ModelGeom()
         g.arch = b"synthetic"
         for k, v in geom.items():
             setattr(g, k, v)
-        so = ModelSynthOpts(expert_dt, dense_dt, int(qk_norm), 0, seed)
+        so = ModelSynthOpts(expert_dt, dense_dt, int(qk_norm), int(expert_pool), seed, float(heat_gamma))
         self = cls.__new__(cls)
-        self.opts = ModelOpts(max_ctx, int(eager), attn_slices, int(split))
+        self.opts = model_opts(max_ctx, eager, attn_slices, split, **cache)
         h = C.c_void_p()
         check(lib.tlm_hip_model_synth(C.byref(g), C.byref(so), C.byref(self.opts), C.byref(h)))
         self._bind(h)
@@ -94,6 +112,17 @@ class Model:
     def stream(self):
         """the model's HIP stream handle (an int)"""
         return lib.tlm_hip_model_stream(self.h)
+
+    def store_stats(self):
+        """The expert slot cache's counters (tlm_hip_store_get_stats), or None
+        when every expert is resident."""
+        from ._lib import StoreStats
+        st = lib.tlm_hip_model_expert_store(self.h)
+        if not st:
+            return None
+        out = StoreStats()
+        lib.tlm_hip_store_get_stats(st, C.byref(out))
+        return {f: int(getattr(out, f)) for f, _ in StoreStats._fields_}
 
     def routes(self):
         """The last step's routing: (ids, weights), each [n_layers, top_k] in
