@@ -77,6 +77,7 @@ INT8_PEAK_TOPS = 5000.0                  # MI355X dense int8 MFMA
 
 
 Q5_K = 13
+Q4_K = 12
 MAT_BYTES_Q5K = DE * D // 256 * 176      # one packed Q5_K matrix: 1,081,344 B
 
 
@@ -436,6 +437,62 @@ def c3_bench(torch, steps, warmup, ctx, split=False):
             "build_s": built, "fill_tok_s": (ctx - 64) / fill_s, "tokens_head": toks[:4], "geometry_bytes": gb}
 
 
+QWEN3_235B_A22B = dict(n_layers=94, d_model=4096, n_heads=64, n_kv_heads=4, head_dim=128, vocab=151936,
+                      n_experts=128, top_k=8, d_expert=1536, n_shared=0, d_shared=0, max_ctx=40960, router=2,
+                      rope_theta=1e6, norm_eps=1e-6, routed_scale=1.0)
+
+
+def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gamma=0.14):
+    """The whole Qwen3-235B-A22B-shaped model (94 layers, hidden 4096, 64 q / 4
+    kv heads x 128 with qk-norm, 128 experts top-8 of width 1536 in Q4_K,
+    Q8_0 dense and lm_head, vocabulary 151936, random init) decoding with its
+    experts behind the HBM slot cache capped at cache_gb: the payloads
+    (127.7 GB as the cache sees them: 12,032 experts of 10.6 MB, drawn from a
+    pool of `pool` distinct payloads in page-locked host memory so the host
+    holds under 1 GB) load over PCIe on a miss; sigmoid routing with the
+    Zipf-like selection bias -gamma ln(rank + 1) on a per-layer order of the
+    experts; the reference runtime's store defaults (pin share 0.30, router
+    lookahead one layer ahead, top_k hints).  A prompt, `warm` greedy tokens
+    to fill the cache, then `tokens` timed greedy tokens (host clock around
+    the steps: every layer waits for its routing on the host)."""
+    from tierlm_amd.model import Model, bench_prompt
+    t0 = time.perf_counter()
+    m = Model.synth(QWEN3_235B_A22B, expert_dt=Q4_K, dense_dt=8, seed=11, max_ctx=prompt_len + warm + tokens + 8,
+                    expert_pool=pool, heat_gamma=gamma, expert_cache=int(cache_gb * (1 << 30)))
+    built = time.perf_counter() - t0
+    try:
+        p = bench_prompt(prompt_len, QWEN3_235B_A22B["vocab"])
+        m.reset()
+        m.generate(p, warm)
+        m.sync()
+        s0 = m.store_stats()
+        h0 = time.perf_counter()
+        m.decode(tokens)
+        m.sync()
+        dt = time.perf_counter() - h0
+        s1 = m.store_stats()
+    finally:
+        m.close()
+    L, K = QWEN3_235B_A22B["n_layers"], QWEN3_235B_A22B["top_k"]
+    miss = (s1["misses"] - s0["misses"]) / tokens
+    pre = (s1["prefetch_issued"] - s0["prefetch_issued"]) / tokens
+    plen = 2 * 1536 * (4096 // 256 * 144) + 4096 * (1536 // 256 * 144)
+    r = {"model": "Qwen3-235B-A22B shape, whole model: 94 layers, hidden 4096, 64 q / 4 kv heads x 128, qk-norm, "
+                  "128 experts top-8 of width 1536 (Q4_K, 10.6 MB each, 127.7 GB) behind the HBM slot cache, Q8_0 "
+                  "dense and lm_head, vocabulary 151936, random init",
+         "cache_GB": cache_gb, "slots": s1["slots"], "pinned": s1["pinned"], "tokens": tokens,
+         "warmup_tokens": warm, "prompt": prompt_len, "tok_s": round(tokens / dt, 2),
+         "ms_per_token": round(dt / tokens * 1e3, 2), "misses_per_token": round(miss, 2),
+         "hit_rate": round(1.0 - miss / (L * K), 4), "prefetch_issued_per_token": round(pre, 2),
+         "load_GBps": round((miss + pre) * plen * tokens / dt / 1e9, 2), "build_s": round(built, 1),
+         "timing": "host wall clock around tlm_hip_model_decode of the timed tokens and a sync, after the prompt and "
+                   "the warm-up tokens"}
+    log(f"bench: C5 whole model ({r['slots']} slots, {cache_gb:.0f} GB): {r['tok_s']:.2f} tok/s "
+        f"({r['ms_per_token']:.2f} ms/token), {r['misses_per_token']:.2f} misses/token (hit rate {r['hit_rate']:.4f}), "
+        f"{r['prefetch_issued_per_token']:.1f} lookahead loads/token, {r['load_GBps']:.2f} GB/s over PCIe")
+    return r
+
+
 def cpu_baseline(args, threads):
     """The reference's kernels on the host cores for a bounded sample of the
     per-token work at Qwen3-30B-A3B shape (oracle/_ref): one layer's q|k|v
@@ -719,13 +776,19 @@ def main():
         del W
         torch.cuda.empty_cache()
     c1 = None if args.no_c1 or not os.path.exists(C1_STORE) else c1_bench(3)
-    c5 = None
+    c5 = c5m = None
     if not args.no_c5:
         try:
             c5 = c5_bench(torch, dev, args.c5_tokens, args.c5_cache_gb)
         except Exception as e:                 # recorded, so the rest of the line still prints
             c5 = {"error": repr(e)}
             log(f"bench: C5 slot cache failed: {e!r}")
+        torch.cuda.empty_cache()
+        try:
+            c5m = c5_model_bench(torch, args.c5_tokens, args.c5_cache_gb)
+        except Exception as e:
+            c5m = {"error": repr(e)}
+            log(f"bench: C5 whole model failed: {e!r}")
         torch.cuda.empty_cache()
 
     cpu = None
@@ -740,7 +803,7 @@ def main():
                           "value": None, "unit": "tok/s", "n_gpus": 1, "note": "--no-c3: whole-model legs skipped",
                           "expert_gemv": c2, "cpu_baseline": cpu, "prefill": prefill, "prefill_q5k": prefill_q5k,
                           "slot_cache": slot_cache, "c1_whole_step": c1, "stream_read": peak,
-                          "qwen3_235b_a22b_slot_cache": c5}), flush=True)
+                          "qwen3_235b_a22b_slot_cache": c5, "qwen3_235b_a22b_model": c5m}), flush=True)
         return
 
     line = {
@@ -781,6 +844,7 @@ def main():
                     "activation codes and near-tied top-k routing amplify the differences); greedy tokens equal on "
                     "the reference fixtures"},
         "qwen3_235b_a22b_slot_cache": c5,
+        "qwen3_235b_a22b_model": c5m,
     }
     print(json.dumps(line), flush=True)
 
