@@ -132,10 +132,10 @@ int tlm_hip_mv_job(const tlm_hip_seg *segs, int nseg, void *stream);
  * streams a packed matrix once for all ntok tokens (int8 MFMA) and returns,
  * for every token t and row r, exactly the decode result:
  *   Y[t * rows + r] == tlm_hip_matvec_packed(dt, Wp, rows, n, act_t, .)[r]
- * act: ntok activation vectors in the reference layout (Q8_K blocks,
- * n/256 * 292 bytes each, consecutive, 4-byte aligned; well-formed, i.e. each
- * bsum the sum of its 16 codes, as the quantiser writes them).  dt: Q4_K, Q5_K
- * or Q6_K. */
+ * act: ntok activation vectors in the reference layout, consecutive, 4-byte
+ * aligned: for Q4_K / Q5_K / Q6_K, Q8_K blocks (n/256 * 292 bytes each;
+ * well-formed, i.e. each bsum the sum of its 16 codes, as the quantiser writes
+ * them); for Q8_0, a8 blocks (n/32 * 36 bytes each).  n: a multiple of 256. */
 int tlm_hip_matmul_tokens(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok,
                           float *Y, void *stream);
 

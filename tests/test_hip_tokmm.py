@@ -7,7 +7,9 @@ token by token (itself bit-exact with the oracle, test_hip_gemv.py), and a
 sample against the oracle directly.  Shapes cover token counts around the
 32-token tile, rows around the 16-row tile and the 128-row group, the edge
 weight patterns of the reference's matvec tests, and poisoned activations,
-for each weight format with a token kernel (Q4_K, Q5_K, Q6_K)."""
+for each weight format with a token kernel (Q4_K, Q5_K, Q6_K against Q8_K
+activations; Q8_0 against a8 activations, eight blocks per staged 256
+values)."""
 import numpy as np
 import pytest
 import torch
@@ -33,9 +35,10 @@ def run_case(hip, dev, dt, rows, n, ntok, seed, wmode=None, poison=False):
         X[3, n - 1] = np.inf
     Wd = torch.from_numpy(W.reshape(-1)).to(dev)
     Wp = hip.pack(dt, Wd, rb, rows, n)
-    act = hip.quantize_act(hip.Q8_K, torch.from_numpy(X.reshape(-1)).to(dev))
+    kind = oracle.Q8_0 if dt == oracle.Q8_0 else oracle.Q8_K
+    act = hip.quantize_act(kind, torch.from_numpy(X.reshape(-1)).to(dev))
     Y = hip.matmul_tokens(dt, Wp, rows, n, act, ntok)
-    ab = oracle.qact_bytes(oracle.Q8_K, n)
+    ab = oracle.qact_bytes(kind, n)
     want = torch.empty((ntok, rows), dtype=torch.float32, device=dev)
     for t in range(ntok):
         hip.matvec_packed(dt, Wp, rows, n, act[t * ab:(t + 1) * ab], want[t])
@@ -46,7 +49,7 @@ def run_case(hip, dev, dt, rows, n, ntok, seed, wmode=None, poison=False):
     return W, X, got
 
 
-KQ = [oracle.Q4_K, oracle.Q5_K, oracle.Q6_K]
+KQ = [oracle.Q4_K, oracle.Q5_K, oracle.Q6_K, oracle.Q8_0]
 
 
 @pytest.mark.parametrize("dt", KQ)
@@ -71,7 +74,7 @@ def test_tokmm_poisoned_tokens(hip, dev, dt):
 def test_tokmm_vs_oracle(hip, dev, dt):
     W, X, got = run_case(hip, dev, dt, 64, 512, 9, seed=3, wmode=3)
     for t in range(X.shape[0]):
-        act = oracle.quantize_act(oracle.Q8_K, X[t])
+        act = oracle.quantize_act(oracle.Q8_0 if dt == oracle.Q8_0 else oracle.Q8_K, X[t])
         want = oracle.matvec_rows(dt, W, W.shape[1], act, 512, 0, 64)
         assert same(got[t], want).all(), t
 
@@ -83,4 +86,4 @@ def test_tokmm_rejects_bad_arguments(hip, dev):
     with pytest.raises(HipError):
         hip.matmul_tokens(oracle.Q6_K, Wp, 16, 100, act, 2)      # n not a multiple of 256
     with pytest.raises(HipError):
-        hip.matmul_tokens(oracle.Q8_0, Wp, 16, 256, act, 2)      # dtype without a token kernel
+        hip.matmul_tokens(oracle.Q8_K, Wp, 16, 256, act, 2)      # dtype without a token kernel

@@ -1,5 +1,6 @@
 /* hip_tokmm.hip - many tokens through one packed matrix (tlm_hip_matmul_tokens):
- * the int8 MFMA tile of tlm_hip_mfma.h over (128-row, 32-token) groups. */
+ * the int8 MFMA tile of tlm_hip_mfma.h over (128-row, 32-token) groups; K-quant
+ * matrices take Q8_K activations, Q8_0 matrices a8 activations. */
 #include "tlm_hip_internal.h"
 #include "tlm_hip_items.h"
 #include "tlm_hip_mfma.h"
@@ -17,14 +18,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5;
     const int64_t row = (int64_t)blockIdx.x * GROUP_ROWS + wave * TM_ROWS + (lane & 31);
     const int tok0 = blockIdx.y * TM_TOK;
-    const int64_t units = ((rows + TILE_ROWS - 1) / TILE_ROWS) * nb * TILE_ROWS;
+    const int nbu = nb * tokmm::blocks_per_stage<DT>();   /* packed units per row */
+    const int64_t units = ((rows + TILE_ROWS - 1) / TILE_ROWS) * nbu * TILE_ROWS;
     /* rows past the last one read the last valid row and write nothing;
      * tokens past the last one stage the last valid token */
     const int64_t rr = row < rows ? row : rows - 1;
-    const tokmm::Chain ch = tokmm::chain_at<DT>(Wp, units, (rr / TILE_ROWS) * nb * TILE_ROWS + rr % TILE_ROWS);
+    const tokmm::Chain ch = tokmm::chain_at<DT>(Wp, units, (rr / TILE_ROWS) * nbu * TILE_ROWS + rr % TILE_ROWS);
     const int ts = tok0 + ((int)threadIdx.x >> 3) < ntok ? tok0 + ((int)threadIdx.x >> 3) : ntok - 1;
+    const int64_t astride = DT == DT_Q8_0 ? (int64_t)nb * 8 * 36 : (int64_t)nb * 292;   /* a8 / Q8_K bytes per token */
     float acc[16];
-    tokmm::tile_run<DT, false>(ch, nb, (const GAS uint8_t *)act + (int64_t)ts * nb * 292, (LAS uint8_t *)s_tile, acc);
+    tokmm::tile_run<DT, false>(ch, nb, (const GAS uint8_t *)act + (int64_t)ts * astride, (LAS uint8_t *)s_tile, acc);
     if (row < rows) {
 #pragma unroll
         for (int v = 0; v < 16; v++) {
@@ -51,6 +54,7 @@ int launch_tokmm(int dt, const void *Wp, int64_t rows, int64_t n, const void *ac
     switch (dt) {
     case DT_Q4_K: hipLaunchKernelGGL(k_tokmm<DT_Q4_K>, grid, dim3(256), 0, s, w, rows, nb, a, (int)ntok, Y); break;
     case DT_Q5_K: hipLaunchKernelGGL(k_tokmm<DT_Q5_K>, grid, dim3(256), 0, s, w, rows, nb, a, (int)ntok, Y); break;
+    case DT_Q8_0: hipLaunchKernelGGL(k_tokmm<DT_Q8_0>, grid, dim3(256), 0, s, w, rows, nb, a, (int)ntok, Y); break;
     default: hipLaunchKernelGGL(k_tokmm<DT_Q6_K>, grid, dim3(256), 0, s, w, rows, nb, a, (int)ntok, Y); break;
     }
     return tlmh_check(hipGetLastError(), "matmul_tokens launch");

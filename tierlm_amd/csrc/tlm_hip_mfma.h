@@ -19,6 +19,9 @@
  *   Q4_K / Q5_K: isum = sum_s sc_s * sum_{k in s} q_k x_k over 8 sub-blocks
  *          of 32, one v_mfma_i32_32x32x32_i8 each; msum = sum_s mn_s *
  *          (bsums[2s] + bsums[2s+1]) (src/lib/tlm_quant.c:812-843).
+ *   Q8_0:  isum = sum_k w_k x_k over each 32-value block (a8 activations),
+ *          one v_mfma_i32_32x32x32_i8 per block, eight blocks per staged
+ *          256 values (src/lib/tlm_quant.c:778-792).
  * The group-sum terms sum_i c_i S_i (c = sc or mn) take two MFMAs per block:
  * S = 64 hi + lo with lo in [0,63] and hi in [-64,63] (the range of a
  * well-formed Q8_K block, whose bsums are sums of 16 int8 codes) is staged as
@@ -42,12 +45,18 @@ constexpr int TM_WAVES = 4;      /* waves per group */
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-__host__ __device__ constexpr bool tile_dt(int dt) { return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K; }
+__host__ __device__ constexpr bool tile_dt(int dt) {
+    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_Q8_0;
+}
 
 /* bytes of one (row, block) unit of the packed layout: the Q6_K block
  * without its d (which sits in a plane after the units), whole Q4_K / Q5_K
  * blocks */
-template <int DT> constexpr int unit_bytes() { return DT == DT_Q6_K ? 208 : DT == DT_Q5_K ? 176 : 144; }
+template <int DT> constexpr int unit_bytes() {
+    return DT == DT_Q6_K ? 208 : DT == DT_Q5_K ? 176 : DT == DT_Q8_0 ? 32 : 144;
+}
+/* packed (row, block) units per staged 256 values: one K-quant block, eight Q8_0 blocks */
+template <int DT> constexpr int blocks_per_stage() { return DT == DT_Q8_0 ? 8 : 1; }
 
 /* One staged Q8_K block of the tile's 32 tokens in LDS.  Code rows are 8
  * (Q6_K: 8-byte reads) or 16 (16-byte reads) bytes past a multiple of 256 so
@@ -59,6 +68,13 @@ template <int DT> struct Stage {
     static constexpr int D = TM_TOK * CS;           /* f32 d per token */
     static constexpr int S = D + TM_TOK * 4;        /* group sums: lo bytes [0,16), hi bytes [16,32) */
     static constexpr int BYTES = S + TM_TOK * SS;
+};
+/* Q8_0: the eight a8 blocks' codes of a token in a row, their d block-major
+ * ([block][token], so four consecutive tokens are one 16-byte read) */
+template <> struct Stage<DT_Q8_0> {
+    static constexpr int CS = 272;
+    static constexpr int D = TM_TOK * CS;
+    static constexpr int BYTES = D + 8 * TM_TOK * 4;
 };
 template <int DT> constexpr int tile_lds_bytes() { return 2 * Stage<DT>::BYTES; }
 
@@ -75,6 +91,10 @@ template <> struct WRaw<DT_Q5_K> {   /* d | dmin, scales[12]; qs bytes 32c + 16 
 template <> struct WRaw<DT_Q4_K> {
     u32x4 hdr, qs[4];
 };
+template <> struct WRaw<DT_Q8_0> {   /* eight blocks: this lane's 16 code bytes of each, and each block's d */
+    u32x4 q[8];
+    uint32_t d[8];
+};
 
 /* block 0 of a chain's row: its unit, and (Q6_K) its d in the d plane */
 struct Chain {
@@ -86,7 +106,8 @@ template <int DT>
 __device__ __forceinline__ Chain chain_at(const uint8_t *Wp, int64_t units, int64_t ubase) {
     Chain c;
     c.unit = (const GAS uint8_t *)Wp + ubase * unit_bytes<DT>();
-    c.dp = (const GAS uint16_t *)((const GAS uint8_t *)Wp + units * 208) + ubase;
+    /* the f16 d plane after the units (Q6_K, Q8_0; unused for Q4_K / Q5_K) */
+    c.dp = (const GAS uint16_t *)((const GAS uint8_t *)Wp + units * unit_bytes<DT>()) + ubase;
     return c;
 }
 
@@ -105,6 +126,12 @@ __device__ __forceinline__ WRaw<DT> wload(const Chain &ch, int b, int half) {
             r.qh[p] = *(const GAS u32x2 *)(u + 128 + 32 * (p >> 1) + 16 * (p & 1) + 8 * half);
         r.sc = *(const GAS u32x4 *)(u + 192);
         r.d = ch.dp[b * TILE_ROWS];
+    } else if constexpr (DT == DT_Q8_0) {   /* b counts staged 256-value groups: blocks 8b .. 8b + 7 */
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            r.q[i] = *(const GAS u32x4 *)(ch.unit + (size_t)(8 * b + i) * (TILE_ROWS * 32) + 16 * half);
+            r.d[i] = ch.dp[(8 * b + i) * TILE_ROWS];
+        }
     } else {
         constexpr int QS = DT == DT_Q5_K ? 48 : 16;
         r.hdr = *(const GAS u32x4 *)u;
@@ -146,9 +173,33 @@ __device__ __forceinline__ StageRegs stage_load(const GAS uint8_t *x, int nb, in
     return r;
 }
 
+/* a8 activations (reference layout, 36-byte blocks: d, 32 codes; 4-byte
+ * aligned): part p of staged group b is block 8b + p */
+__device__ __forceinline__ StageRegs stage_load_a8(const GAS uint8_t *x, int b, int p) {
+    StageRegs r;
+    const GAS uint32_t *blk = (const GAS uint32_t *)(x + (size_t)(8 * b + p) * 36);
+    r.d = __uint_as_float(blk[0]);
+    r.c0 = u32x4{blk[1], blk[2], blk[3], blk[4]};
+    r.c1 = u32x4{blk[5], blk[6], blk[7], blk[8]};
+    r.bs = 0;
+    return r;
+}
+
+template <int DT, bool SPLIT>
+__device__ __forceinline__ StageRegs stage_in(const GAS uint8_t *x, int nb, int b, int p) {
+    if constexpr (DT == DT_Q8_0) return stage_load_a8(x, b, p);
+    else return stage_load<SPLIT>(x, nb, b, p);
+}
+
 template <int DT>
 __device__ __forceinline__ void stage_store(LAS uint8_t *buf, const StageRegs &r, int j, int p) {
     using S = Stage<DT>;
+    if constexpr (DT == DT_Q8_0) {   /* block p of token j: codes at 32 p of the row, d block-major */
+        *(LAS u32x4 *)(buf + j * S::CS + 32 * p) = r.c0;
+        *(LAS u32x4 *)(buf + j * S::CS + 32 * p + 16) = r.c1;
+        *(LAS float *)(buf + S::D + 4 * (32 * p + j)) = r.d;
+        return;
+    } else {
     LAS uint8_t *c = buf + j * S::CS + 16 * p;
     if constexpr (S::CS % 16 == 0) {
         *(LAS u32x4 *)c = r.c0;
@@ -169,6 +220,7 @@ __device__ __forceinline__ void stage_store(LAS uint8_t *buf, const StageRegs &r
         const int s = s0 + s1;
         sv[p] = (uint8_t)(s & 63);
         sv[16 + p] = (uint8_t)((s >> 6) & 0xFF);
+    }
     }
 }
 
@@ -226,6 +278,31 @@ __device__ __forceinline__ void block_chain(const WRaw<DT_Q6_K> &w, const LAS ui
             const int v = 4 * q + k;
             const int is = __mul24(m[v], -32) + isum[v];
             acc[v] = fmaf(dwf * da[k], (float)is, acc[v]);
+        }
+    }
+}
+
+/* eight Q8_0 blocks: per block the exact int32 sum, then the row's fma
+ * (d_w d_a, isum) in ascending block order, as the decode dot */
+__device__ __forceinline__ void block_chain(const WRaw<DT_Q8_0> &w, const LAS uint8_t *buf, int t, int half,
+                                            float (&acc)[16]) {
+    using S = Stage<DT_Q8_0>;
+    const LAS uint8_t *cod = buf + t * S::CS + 16 * half;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const v4i ax = *(const LAS v4i *)(cod + 32 * i);
+        const v4i bw = {(int)w.q[i].x, (int)w.q[i].y, (int)w.q[i].z, (int)w.q[i].w};
+        const v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bw, v16i{}, 0, 0, 0);
+        const LAS float *dd = (const LAS float *)(buf + S::D) + 32 * i + 4 * half;
+        const float dw = f16_to_f32(w.d[i]);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const f32x4 da = *(const LAS f32x4 *)(dd + 8 * q);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int v = 4 * q + k;
+                acc[v] = fmaf(dw * da[k], (float)p[v], acc[v]);
+            }
         }
     }
 }
@@ -292,19 +369,19 @@ __device__ __forceinline__ void tile_run(const Chain &ch, int nb, const GAS uint
     const int tid = threadIdx.x, j = tid >> 3, p = tid & 7, lane = tid & 63, t = lane & 31, half = lane >> 5;
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[v] = 0.0f;
-    if constexpr (DT != DT_Q6_K) {   /* the unused bytes of the group-sum rows, both buffers */
+    if constexpr (DT == DT_Q4_K || DT == DT_Q5_K) {   /* the unused bytes of the group-sum rows, both buffers */
         if (tid < 128)
             *(LAS uint64_t *)(lds + (tid >> 6) * S::BYTES + S::S + ((tid >> 1) & 31) * S::SS + 8 + 16 * (tid & 1)) = 0;
     }
     LAS uint8_t *buf0 = lds, *buf1 = lds + S::BYTES;
-    StageRegs r = stage_load<SPLIT>(x, nb, 0, p);
+    StageRegs r = stage_in<DT, SPLIT>(x, nb, 0, p);
     WRaw<DT> w0 = wload<DT>(ch, 0, half), w1;
     stage_store<DT>(buf0, r, j, p);
     __syncthreads();
     for (int b = 0; b < nb; b += 2) {
         const bool n1 = b + 1 < nb;
         if (n1) {
-            r = stage_load<SPLIT>(x, nb, b + 1, p);
+            r = stage_in<DT, SPLIT>(x, nb, b + 1, p);
             w1 = wload<DT>(ch, b + 1, half);
         }
         block_chain(w0, buf0, t, half, acc);
@@ -313,7 +390,7 @@ __device__ __forceinline__ void tile_run(const Chain &ch, int nb, const GAS uint
         if (!n1) break;
         const bool n2 = b + 2 < nb;
         if (n2) {
-            r = stage_load<SPLIT>(x, nb, b + 2, p);
+            r = stage_in<DT, SPLIT>(x, nb, b + 2, p);
             w0 = wload<DT>(ch, b + 2, half);
         }
         block_chain(w1, buf1, t, half, acc);
