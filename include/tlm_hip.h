@@ -457,6 +457,17 @@ typedef struct {
     int32_t  prefetch_off;       /* io.prefetch off: no hints, no lookahead (default: lookahead 1) */
     int32_t  lookahead_k;        /* io.lookahead_k: experts hinted per lookahead layer (0 = top_k) */
     double   interest;           /* nav.interest_aggressiveness (0 = fixed breadth) */
+    /* Prompts (tlm_hip_model_prefill / _generate): 0 = batched where the
+     * model allows it - every resident layer's q/k/v/o Q4_K / Q5_K / Q6_K /
+     * Q8_0 with widths multiples of 256, routed Q4_K / Q5_K / Q6_K experts
+     * without a shared expert, head width 32 / 64 / 96 / 128, the reference's
+     * attention order (attn_split 0) - in chunks sized to the context
+     * capacity (at most 512 tokens); n > 0: chunks of at most n tokens; < 0:
+     * one step per token.  A batched chunk runs each layer once for all of
+     * its tokens (int8 MFMA token matmuls, the batched MoE block, causal
+     * attention over the cache) with each token's result bit for bit the
+     * step's. */
+    int32_t  prefill_chunk;
 } tlm_hip_model_opts;
 int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
 void tlm_hip_model_close(tlm_hip_model *M);
@@ -492,8 +503,16 @@ int  tlm_hip_model_synth(const tlm_hip_model_geom *g, const tlm_hip_model_synth_
 /* tlm_model_step: logits (host, vocab floats) and next (the greedy token)
  * may each be NULL. */
 int  tlm_hip_model_step(tlm_hip_model *M, int token, float *logits, int32_t *next);
-/* prefill the prompt, then n_gen greedy tokens into out; between steps the
- * token stays on the device. */
+/* tlm_model_prefill (src/lib/tlm_model.c:1105-1113): the n tokens from the
+ * current position, logits (host, vocab floats, may be NULL) of the last;
+ * the same bits as n steps (batched as tlm_hip_model_opts.prefill_chunk
+ * says).  Waits for the work. */
+int  tlm_hip_model_prefill(tlm_hip_model *M, const int32_t *tokens, int n, float *logits);
+/* 1 when prompts run batched on this model (prefill_chunk and the model's
+ * dtypes and geometry allow it), 0 when they run one step per token */
+int  tlm_hip_model_prefill_batched(const tlm_hip_model *M);
+/* prefill the prompt (as tlm_hip_model_prefill), then n_gen greedy tokens
+ * into out; between steps the token stays on the device. */
 int  tlm_hip_model_generate(tlm_hip_model *M, const int32_t *prompt, int n_prompt, int n_gen, int32_t *out);
 /* No counterpart in the reference (whose KV cache only resets): keep the
  * first len positions of the context (0 <= len <= kv_len) and drop the rest,

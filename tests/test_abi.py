@@ -66,7 +66,7 @@ int main(void) {
   printf("synth %zu\nmopts %zu\n", sizeof(tlm_hip_model_synth_opts), sizeof(tlm_hip_model_opts));
   O(tlm_hip_model_synth_opts, qk_norm); O(tlm_hip_model_synth_opts, seed); O(tlm_hip_model_synth_opts, heat_gamma);
   O(tlm_hip_model_opts, attn_split); O(tlm_hip_model_opts, expert_cache_bytes); O(tlm_hip_model_opts, pin_frac);
-  O(tlm_hip_model_opts, lookahead_k); O(tlm_hip_model_opts, interest);
+  O(tlm_hip_model_opts, lookahead_k); O(tlm_hip_model_opts, interest); O(tlm_hip_model_opts, prefill_chunk);
   return 0;
 }'''
     with tempfile.TemporaryDirectory() as d:

@@ -183,6 +183,8 @@ _SIGS = {
     "tlm_hip_model_reset": (None, [vp]),
     "tlm_hip_model_step": (i32, [vp, i32, vp, C.POINTER(C.c_int32)]),
     "tlm_hip_model_generate": (i32, [vp, C.POINTER(C.c_int32), i32, i32, C.POINTER(C.c_int32)]),
+    "tlm_hip_model_prefill": (i32, [vp, C.POINTER(C.c_int32), i32, vp]),
+    "tlm_hip_model_prefill_batched": (i32, [vp]),
     "tlm_hip_crc32c": (C.c_uint32, [C.c_uint32, vp, sz]),
     "tlm_hip_sha256": (None, [vp, sz, vp]),
     "tlm_hip_moe_layer_store": (i32, [C.POINTER(MoeDesc), vp, i32, vp, vp, vp, C.POINTER(MoeHint), i32, vp, vp]),

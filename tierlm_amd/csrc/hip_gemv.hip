@@ -436,6 +436,50 @@ static __device__ __forceinline__ XLds stage_norm_act(int kind, const float *__r
     return xlds_at(kind, nb, lds_g);
 }
 
+/* Per token: rmsnorm (w given) or the plain vector, then the activation
+ * quantiser of kind, with the decode GEMV prologue's code (norm_act_load +
+ * stage_norm_act, the same thread mapping and reduction tree, so the same
+ * codes and scales), written in the reference layout (a8: 36-byte blocks;
+ * Q8_K: 292-byte blocks) at out + t * ostride.  One group per token. */
+__global__ __launch_bounds__(256) void k_tok_norm_act(int kind, const float *__restrict__ x, int64_t xstride,
+                                                      const float *__restrict__ w, float eps, int nb,
+                                                      uint8_t *__restrict__ out, int64_t ostride) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const float *xt = x + (int64_t)blockIdx.x * xstride;
+    NormIn nin;
+    norm_act_load(kind, xt, w, nb, nin);
+    stage_norm_act(kind, xt, w, eps, nb, lds, nin);
+    __syncthreads();
+    const bool k8 = kind == DT_Q8_K;
+    const int words = k8 ? 73 : 9;   /* 4-byte words per block: d, codes (, bsums) */
+    const LAS uint8_t *l = (const LAS uint8_t *)lds;
+    const LAS float *dl = (const LAS float *)(l + (k8 ? nb * 288 : nb * 32));
+    GAS uint32_t *o = (GAS uint32_t *)(out + (int64_t)blockIdx.x * ostride);
+    for (int i = threadIdx.x; i < nb * words; i += GROUP_THREADS) {
+        const int b = i / words, wd = i - b * words;
+        uint32_t v;
+        if (wd == 0) v = __float_as_uint(dl[b]);
+        else if (wd <= (k8 ? 64 : 8)) v = *(const LAS uint32_t *)(l + (size_t)b * (k8 ? 256 : 32) + 4 * (wd - 1));
+        else v = *(const LAS uint32_t *)(l + (size_t)nb * 256 + (size_t)b * 32 + 4 * (wd - 65));
+        o[i] = v;
+    }
+}
+
+int launch_tok_norm_act(int kind, const float *x, int64_t xstride, const float *w, float eps, int64_t n,
+                        int64_t ntok, void *out, int64_t ostride, hipStream_t s) {
+    if (kind != DT_Q8_0 && kind != DT_Q8_K) return tlmh_seterr(TLM_HIP_EINVAL, "tok_norm_act: kind %d", kind);
+    const int bv = kind == DT_Q8_K ? 256 : 32;
+    if (n <= 0 || n % bv || ntok <= 0 || ((uintptr_t)x & 15u) || (xstride & 3) || (ostride & 3) ||
+        ((uintptr_t)out & 3u))
+        return tlmh_seterr(TLM_HIP_EINVAL, "tok_norm_act: n=%lld ntok=%lld", (long long)n, (long long)ntok);
+    const int nb = (int)(n / bv);
+    const size_t lds = stage_bytes(kind, nb);
+    if (lds > 64 * 1024) return tlmh_seterr(TLM_HIP_EUNSUP, "tok_norm_act: n=%lld exceeds LDS", (long long)n);
+    hipLaunchKernelGGL(k_tok_norm_act, dim3((unsigned)ntok), dim3(256), lds, s, kind, x, xstride, w, eps, nb,
+                       (uint8_t *)out, ostride);
+    return tlmh_check(hipGetLastError(), "tok_norm_act launch");
+}
+
 /* The same tile for up to MV_SEGS matrices of one dtype and width in one
  * launch (segment s owns tiles [tile_end[s-1], tile_end[s])), all taking the
  * same activation; accum: y[r] += acc instead of y[r] = acc (the reference's

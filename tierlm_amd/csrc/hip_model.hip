@@ -37,19 +37,28 @@ constexpr int NT = 256;
 /* ---- embedding row (tlm_dequantize_row, src/lib/tlm_quant.c:629-660) -------- */
 /* The step's position and token live in device memory (st[0] = pos, seq[pos]
  * = the token), so one captured graph serves every position. */
+__device__ __forceinline__ float embed_at(const uint8_t *row, int dt, int i) {
+    if (dt == DT_F32) return ((const float *)row)[i];
+    const uint8_t *b = row + (size_t)(i >> 5) * 34;   /* Q8_0: y = f16(d) * (float)q */
+    const float dd = f16_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    return dd * (float)(int8_t)b[2 + (i & 31)];
+}
 __global__ __launch_bounds__(NT) void k_embed(const uint8_t *__restrict__ embd, size_t row_bytes, int dt,
                                               const int32_t *__restrict__ seq, const int32_t *__restrict__ st, int D,
                                               float *__restrict__ h) {
     const uint8_t *row = embd + (size_t)seq[st[0]] * row_bytes;
-    for (int i = threadIdx.x + blockIdx.x * blockDim.x; i < D; i += blockDim.x * gridDim.x) {
-        if (dt == DT_F32) {
-            h[i] = ((const float *)row)[i];
-        } else {   /* Q8_0: y = f16(d) * (float)q */
-            const uint8_t *b = row + (size_t)(i >> 5) * 34;
-            const float dd = f16_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
-            h[i] = dd * (float)(int8_t)b[2 + (i & 31)];
-        }
-    }
+    for (int i = threadIdx.x + blockIdx.x * NT; i < D; i += NT * gridDim.x) h[i] = embed_at(row, dt, i);
+}
+/* prefill: the rows of tokens seq[0 .. gridDim.y) into h[t * D ..] */
+__global__ __launch_bounds__(NT) void k_pf_embed(const uint8_t *__restrict__ embd, size_t row_bytes, int dt,
+                                                 const int32_t *__restrict__ seq, int D, float *__restrict__ h) {
+    const uint8_t *row = embd + (size_t)seq[blockIdx.y] * row_bytes;
+    float *ht = h + (size_t)blockIdx.y * D;
+    for (int i = threadIdx.x + blockIdx.x * NT; i < D; i += NT * gridDim.x) ht[i] = embed_at(row, dt, i);
+}
+/* prefill: h += y (the o projection's accumulation, tlm_model.c:762) */
+__global__ __launch_bounds__(NT) void k_pf_add(float *__restrict__ h, const float *__restrict__ y, int64_t n) {
+    for (int64_t i = threadIdx.x + (int64_t)blockIdx.x * NT; i < n; i += (int64_t)NT * gridDim.x) h[i] = h[i] + y[i];
 }
 
 /* ---- attention: attention() (src/lib/tlm_model.c:743-756) and attn_heads
@@ -147,6 +156,42 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+/* One head vector x (LDS, HD floats) by 16 lanes (lane sub holds elements
+ * sub + 16 e): rmsnorm when norm (tlm_model.c:743-746: double sum of squares -
+ * the lane's elements in order, then a 16-lane tree -, x * r * w), then RoPE
+ * (rope(), :721-728: the pair (j, j + HD/2) is elements e and e + EL/2 of one
+ * lane).  w, cv, sv: the lane's norm weights and RoPE factors.  Shared by the
+ * decode and prefill attention, so both rotate with the same bits. */
+template <int HD>
+__device__ __forceinline__ void norm_rope16(float *x, bool norm, const float (&w)[HD / 16],
+                                            const float (&cv)[HD / 32], const float (&sv)[HD / 32], float eps,
+                                            int sub) {
+    constexpr int EL = HD / 16;
+    float e[EL];
+#pragma unroll
+    for (int k = 0; k < EL; k++) e[k] = x[sub + 16 * k];
+    if (norm) {
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < EL; k++) ss += (double)e[k] * (double)e[k];
+        ss += dpp_f64<DPP_XOR1>(ss);
+        ss += dpp_f64<DPP_XOR2>(ss);
+        ss += dpp_f64<DPP_HALF_MIRROR>(ss);
+        ss += dpp_f64<DPP_MIRROR>(ss);
+        const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
+#pragma unroll
+        for (int k = 0; k < EL; k++) e[k] = e[k] * r * w[k];
+    }
+#pragma unroll
+    for (int k = 0; k < EL / 2; k++) {
+        const float a = e[k], c = e[k + EL / 2];
+        e[k] = a * cv[k] - c * sv[k];
+        e[k + EL / 2] = c * cv[k] + a * sv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < EL; k++) x[sub + 16 * k] = e[k];
+}
+
 template <int HD>
 __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kx,
                                                     const float *__restrict__ vx, const float *__restrict__ q_norm,
@@ -230,37 +275,10 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
     }
     __syncthreads();
 
-    /* rmsnorm of each query head and of the new key (tlm_model.c:743-746:
-     * double sum of squares - the lane's elements in order, then a 16-lane
-     * tree -, x * r * w), then RoPE (rope(), :721-728: the pair (j, j + HD/2)
-     * is elements e and e + EL/2 of one lane); 16 lanes per vector, all
-     * vectors at once, vector R being the key */
-    for (int v = tid >> 4; v <= R; v += NT / 16) {   /* uniform over each 16 lanes */
-        float *x = v < R ? s_q + v * HD : s_kn;
-        float e[EL];
-#pragma unroll
-        for (int k = 0; k < EL; k++) e[k] = x[sub + 16 * k];
-        if (v < R ? has_qn : has_kn) {
-            double ss = 0.0;
-#pragma unroll
-            for (int k = 0; k < EL; k++) ss += (double)e[k] * (double)e[k];
-            ss += dpp_f64<DPP_XOR1>(ss);
-            ss += dpp_f64<DPP_XOR2>(ss);
-            ss += dpp_f64<DPP_HALF_MIRROR>(ss);
-            ss += dpp_f64<DPP_MIRROR>(ss);
-            const float r = 1.0f / sqrtf((float)(ss / (double)HD) + eps);
-#pragma unroll
-            for (int k = 0; k < EL; k++) e[k] = e[k] * r * (v < R ? qn[k] : kn[k]);
-        }
-#pragma unroll
-        for (int k = 0; k < EL / 2; k++) {
-            const float a = e[k], c = e[k + EL / 2];
-            e[k] = a * cv[k] - c * sv[k];
-            e[k + EL / 2] = c * cv[k] + a * sv[k];
-        }
-#pragma unroll
-        for (int k = 0; k < EL; k++) x[sub + 16 * k] = e[k];
-    }
+    /* rmsnorm of each query head and of the new key, then RoPE (norm_rope16);
+     * 16 lanes per vector, all vectors at once, vector R being the key */
+    for (int v = tid >> 4; v <= R; v += NT / 16)   /* uniform over each 16 lanes */
+        norm_rope16<HD>(v < R ? s_q + v * HD : s_kn, v < R ? has_qn : has_kn, v < R ? qn : kn, cv, sv, eps, sub);
     __syncthreads();
 
     const float scale = 1.0f / sqrtf((float)HD);
@@ -882,6 +900,278 @@ __global__ __launch_bounds__(NT) void k_attn_merge(const float *__restrict__ par
     }
 }
 
+/* ---- prefill attention: the step's attention for a chunk of ntok prompt
+ * tokens at positions p0 .. p0 + ntok - 1 (tlm_model_prefill, src/lib/
+ * tlm_model.c:1105-1113, steps each token in turn: token t attends to
+ * positions 0 .. p0 + t), the step's operations in the step's order per
+ * token, in four launches:
+ * k_pf_prep: a group per token: q-norm + RoPE of every query head in place,
+ *   k-norm + RoPE of every key head (norm_rope16, the decode's code), the key
+ *   and value appended to the cache at the token's position.
+ * k_pf_scores: a group per (key head, PF_TOK tokens, 64 positions): lane =
+ *   position with its key row in registers, wave = token, HB query heads of
+ *   the key head at a time from LDS; each score is the dot in ascending i,
+ *   scaled after the dot (the decode's expression).
+ * k_pf_softmax: a group per (token, query head): the decode P.V launch's
+ *   softmax with its thread mapping and reduction trees (the maximum, e_t,
+ *   their double sum, inv); p_t = e_t * inv replaces the score.
+ * k_pf_pv: a group per (key head, 64-element slab, PF_TOK tokens): lane =
+ *   element, wave = token, one chain per query head (HB at a time), out +=
+ *   p_t * v_t[i] over ascending t up to the token's position (the rounded
+ *   product, then the add), the probabilities staged in LDS PF_PCH positions
+ *   at a time.  Products past the position are never added (adding +0 would
+ *   leave the chain unchanged, as in the decode ring).
+ * Score rows: [token][query head][SL] floats, SL the capacity rounded up to 4. */
+constexpr int PF_TOK = 4;     /* tokens per group, a wave each */
+constexpr int PF_PCH = 256;   /* positions per staged chunk of probabilities */
+
+template <int HD>
+__global__ __launch_bounds__(NT) void k_pf_prep(float *__restrict__ q, const float *__restrict__ kx,
+                                                const float *__restrict__ vx, const float *__restrict__ q_norm,
+                                                const float *__restrict__ k_norm, int has_qn, int has_kn,
+                                                const float *__restrict__ cs_all, const float *__restrict__ sn_all,
+                                                float *__restrict__ kc, float *__restrict__ vc, int H, int KV,
+                                                int max_ctx, int p0, float eps) {
+    constexpr int EL = HD / 16, HALF = HD / 2;
+    const int t = blockIdx.x, pos = p0 + t, tid = threadIdx.x, sub = tid & 15;
+    float qn[EL], kn[EL], cv[EL / 2], sv[EL / 2];
+#pragma unroll
+    for (int e = 0; e < EL; e++) {
+        qn[e] = q_norm[sub + 16 * e];
+        kn[e] = k_norm[sub + 16 * e];
+    }
+#pragma unroll
+    for (int e = 0; e < EL / 2; e++) {
+        cv[e] = cs_all[(size_t)pos * HALF + sub + 16 * e];
+        sv[e] = sn_all[(size_t)pos * HALF + sub + 16 * e];
+    }
+    for (int v = tid >> 4; v < H + KV; v += NT / 16) {   /* uniform over each 16 lanes */
+        if (v < H) {
+            norm_rope16<HD>(q + ((size_t)t * H + v) * HD, has_qn, qn, cv, sv, eps, sub);
+        } else {   /* the KV append (tlm_model.c:748-752): the rotated key, the value in its tile */
+            const int kvh = v - H;
+            float *K = kc + ((size_t)kvh * max_ctx + pos) * HD, *V = vc + (size_t)kvh * att_vstride(max_ctx, HD);
+            const float *kr = kx + ((size_t)t * KV + kvh) * HD, *vr = vx + ((size_t)t * KV + kvh) * HD;
+#pragma unroll
+            for (int e = 0; e < EL; e++) {
+                K[sub + 16 * e] = kr[sub + 16 * e];
+                V[att_vidx(pos, sub + 16 * e, HD)] = vr[sub + 16 * e];
+            }
+            norm_rope16<HD>(K, has_kn, kn, cv, sv, eps, sub);   /* the lane's own elements, in place */
+        }
+    }
+}
+
+template <int HD, int HB>
+__global__ __launch_bounds__(NT) void k_pf_scores(const float *__restrict__ q, const float *__restrict__ kc,
+                                                  float *__restrict__ scores, int H, int KV, int max_ctx, int p0,
+                                                  int ntok, int SL) {
+    constexpr int H4 = HD / 4;
+    __shared__ __align__(16) f32x4 s_q[PF_TOK][HB][H4];
+    const int R = H / KV, kvh = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = (int)blockIdx.y * PF_TOK, u0 = (int)blockIdx.x * 64;
+    const int tlast = min(t0 + PF_TOK, ntok) - 1;
+    if (u0 > p0 + tlast) return;   /* uniform: no token of the group reaches these positions */
+    const int t = t0 + wave, P = t < ntok ? p0 + t : -1, u = u0 + lane;
+    /* the lane's key row (positions past the group's last are clamped, never stored) */
+    const f32x4 *K4 = (const f32x4 *)(kc + ((size_t)kvh * max_ctx + min(u, p0 + tlast)) * HD);
+    f32x4 kr[H4];
+#pragma unroll
+    for (int i4 = 0; i4 < H4; i4++) kr[i4] = K4[i4];
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int hb = 0; hb < R; hb += HB) {   /* uniform */
+        if (hb > 0) __syncthreads();       /* the previous heads are read */
+        for (int idx = tid; idx < PF_TOK * HB * H4; idx += NT) {
+            const int tk = idx / (HB * H4), j = (idx / H4) % HB, i4 = idx % H4;
+            const int tt = min(t0 + tk, ntok - 1);
+            s_q[tk][j][i4] = ((const f32x4 *)(q + ((size_t)tt * H + kvh * R + hb + j) * HD))[i4];
+        }
+        __syncthreads();
+        float acc[HB];
+#pragma unroll
+        for (int j = 0; j < HB; j++) acc[j] = 0.0f;
+#pragma unroll 8
+        for (int i4 = 0; i4 < H4; i4++) {
+            const f32x4 b = kr[i4];
+#pragma unroll
+            for (int j = 0; j < HB; j++) {
+                const f32x4 a = s_q[wave][j][i4];
+                acc[j] += a.x * b.x;
+                acc[j] += a.y * b.y;
+                acc[j] += a.z * b.z;
+                acc[j] += a.w * b.w;
+            }
+        }
+        if (u <= P) {
+#pragma unroll
+            for (int j = 0; j < HB; j++) scores[((size_t)t * H + kvh * R + hb + j) * SL + u] = acc[j] * scale;
+        }
+    }
+}
+
+__global__ __launch_bounds__(NT) void k_pf_softmax(float *__restrict__ scores, int H, int p0, int SL) {
+    constexpr int PB = 8;   /* k_attn_pv's scores per thread per round */
+    __shared__ double s_sum[NT / 64];
+    __shared__ float s_max[NT / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float *S = scores + ((size_t)blockIdx.y * H + blockIdx.x) * SL;
+    const int T = p0 + (int)blockIdx.y + 1;
+    ExpTabLanes tab;
+    tab.load();
+    const int nround = (T + PB * NT - 1) / (PB * NT);
+    float sv[PB];
+    float m = -INFINITY;
+    for (int r = 0; r < nround; r++) {
+#pragma unroll
+        for (int k = 0; k < PB; k++) sv[k] = S[min(r * PB * NT + tid + NT * k, T - 1)];
+#pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int t = r * PB * NT + tid + NT * k;
+            m = t < T && sv[k] > m ? sv[k] : m;
+        }
+    }
+    m = wave_max_f32(m);
+    if (lane == 0) s_max[wave] = m;
+    __syncthreads();
+    float mx = s_max[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) mx = s_max[w] > mx ? s_max[w] : mx;
+    double sum = 0.0;
+    float e[PB];
+    for (int r = 0; r < nround; r++) {
+        if (nround > 1) {
+#pragma unroll
+            for (int k = 0; k < PB; k++) sv[k] = S[min(r * PB * NT + tid + NT * k, T - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < PB; k++) {
+            const int t = r * PB * NT + tid + NT * k;
+            e[k] = expf_ref_with(sv[k] - mx, tab);
+            sum += t < T ? (double)e[k] : 0.0;
+        }
+    }
+    sum = wave_sum_f64(sum);
+    if (lane == 0) s_sum[wave] = sum;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) tot += s_sum[w];
+    const float inv_s = (float)(1.0 / tot);
+    if (nround == 1) {
+#pragma unroll
+        for (int k = 0; k < PB; k++)
+            if (tid + NT * k < T) S[tid + NT * k] = e[k] * inv_s;
+    } else {
+        for (int t = tid; t < T; t += NT) S[t] = expf_ref_with(S[t] - mx, tab) * inv_s;
+    }
+}
+
+template <int HD, int HB>
+__global__ __launch_bounds__(NT) void k_pf_pv(const float *__restrict__ scores, const float *__restrict__ vc,
+                                              float *__restrict__ att, int H, int KV, int max_ctx, int p0, int ntok,
+                                              int SL) {
+    constexpr int NWC = (HD + 63) / 64, PQ = PF_PCH / 4;
+    __shared__ __align__(16) f32x4 s_p[PF_TOK][HB][PQ];
+    const int R = H / KV, kvh = (int)blockIdx.x / NWC, slab = (int)blockIdx.x % NWC;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = (int)blockIdx.y * PF_TOK, tlast = min(t0 + PF_TOK, ntok) - 1, pmax = p0 + tlast;
+    const int t = t0 + wave, P = t < ntok ? p0 + t : -1, ic = 64 * slab + lane;
+    const char *vbase = (const char *)(vc + (size_t)kvh * att_vstride(max_ctx, HD));
+    const uint32_t lane_off = (uint32_t)min(ic, HD - 1) * 16u;   /* element ic's 16 bytes of a tile */
+    auto vtile = [&](int tq) { return *(const f32x4 *)(vbase + (size_t)tq * (HD * 16) + lane_off); };
+    for (int hb = 0; hb < R; hb += HB) {   /* uniform */
+        float acc[HB];
+#pragma unroll
+        for (int j = 0; j < HB; j++) acc[j] = 0.0f;
+        for (int c0 = 0; c0 <= pmax; c0 += PF_PCH) {   /* uniform */
+            __syncthreads();   /* the previous chunk is read */
+            for (int idx = tid; idx < PF_TOK * HB * PQ; idx += NT) {
+                const int tk = idx / (HB * PQ), j = (idx / PQ) % HB, u4 = idx % PQ;
+                const int tt = t0 + tk, uu = c0 + 4 * u4;
+                f32x4 pv = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (tt <= tlast && uu <= p0 + tt)   /* row tt holds positions 0 .. p0 + tt (within SL) */
+                    pv = *(const f32x4 *)(scores + ((size_t)tt * H + kvh * R + hb + j) * SL + uu);
+                s_p[tk][j][u4] = pv;
+            }
+            __syncthreads();
+            const int ue = min(P, c0 + PF_PCH - 1);   /* the wave's last position in the chunk */
+            int u = c0;
+            for (; u + 15 <= ue; u += 16) {
+                f32x4 vt[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) vt[k] = vtile((u >> 2) + k);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+#pragma unroll
+                    for (int j = 0; j < HB; j++) {
+                        const f32x4 pp = s_p[wave][j][((u - c0) >> 2) + k];
+                        acc[j] += pp.x * vt[k].x;
+                        acc[j] += pp.y * vt[k].y;
+                        acc[j] += pp.z * vt[k].z;
+                        acc[j] += pp.w * vt[k].w;
+                    }
+                }
+            }
+            for (; u <= ue; u += 4) {   /* the last positions, up to ue */
+                const f32x4 vt = vtile(u >> 2);
+#pragma unroll
+                for (int j = 0; j < HB; j++) {
+                    const f32x4 pp = s_p[wave][j][(u - c0) >> 2];
+                    acc[j] += pp.x * vt.x;
+                    if (u + 1 <= ue) acc[j] += pp.y * vt.y;
+                    if (u + 2 <= ue) acc[j] += pp.z * vt.z;
+                    if (u + 3 <= ue) acc[j] += pp.w * vt.w;
+                }
+            }
+        }
+        if (t < ntok && ic < HD) {
+#pragma unroll
+            for (int j = 0; j < HB; j++) att[((size_t)t * H + kvh * R + hb + j) * HD + ic] = acc[j];
+        }
+    }
+}
+
+/* prefill: whether the attention launches take this geometry (the key row in
+ * registers: head width at most 128) */
+bool pf_att_supported(int hd, int H, int KV) {
+    return (hd == 32 || hd == 64 || hd == 96 || hd == 128) && KV > 0 && H % KV == 0;
+}
+
+/* the four prefill attention launches for ntok tokens at p0 (q rotated in
+ * place, K/V appended, att [ntok][H][hd]) */
+int launch_pf_attn(int hd, int H, int KV, int max_ctx, int p0, int ntok, float *q, const float *kx, const float *vx,
+                   const float *q_norm, const float *k_norm, const float *cs, const float *sn, float *kc, float *vc,
+                   float *scores, int SL, float *att, float eps, hipStream_t s) {
+    const int has_qn = q_norm != nullptr, has_kn = k_norm != nullptr;
+    if (!q_norm) q_norm = q;   /* read and dropped */
+    if (!k_norm) k_norm = q;
+    const int R = H / KV, HB = R % 8 == 0 ? 8 : R % 4 == 0 ? 4 : R % 2 == 0 ? 2 : 1;
+    const dim3 gsc((unsigned)((p0 + ntok + 63) / 64), (unsigned)((ntok + PF_TOK - 1) / PF_TOK), (unsigned)KV);
+    const dim3 gpv((unsigned)(KV * ((hd + 63) / 64)), (unsigned)((ntok + PF_TOK - 1) / PF_TOK));
+#define TLM_PF_HB(W, B)                                                                                         \
+    case B:                                                                                                     \
+        hipLaunchKernelGGL((k_pf_scores<W, B>), gsc, dim3(NT), 0, s, (const float *)q, (const float *)kc,      \
+                           scores, H, KV, max_ctx, p0, ntok, SL);                                               \
+        hipLaunchKernelGGL(k_pf_softmax, dim3((unsigned)H, (unsigned)ntok), dim3(NT), 0, s, scores, H, p0, SL); \
+        hipLaunchKernelGGL((k_pf_pv<W, B>), gpv, dim3(NT), 0, s, (const float *)scores, (const float *)vc, att, \
+                           H, KV, max_ctx, p0, ntok, SL);                                                       \
+        break;
+#define TLM_PF(W)                                                                                                \
+    case W:                                                                                                      \
+        hipLaunchKernelGGL((k_pf_prep<W>), dim3((unsigned)ntok), dim3(NT), 0, s, q, kx, vx, q_norm, k_norm,     \
+                           has_qn, has_kn, cs, sn, kc, vc, H, KV, max_ctx, p0, eps);                            \
+        switch (HB) { TLM_PF_HB(W, 8) TLM_PF_HB(W, 4) TLM_PF_HB(W, 2) TLM_PF_HB(W, 1) }                          \
+        break;
+    switch (hd) {
+        TLM_PF(32) TLM_PF(64) TLM_PF(96) TLM_PF(128)
+    default: return tlmh_seterr(TLM_HIP_EUNSUP, "model prefill: head width %d", hd);
+    }
+#undef TLM_PF
+#undef TLM_PF_HB
+    return tlmh_check(hipGetLastError(), "model: prefill attention");
+}
+
 /* slices per key head: enough groups to cover the chip at long contexts
  * (about 256 with every key head), a slice at least ATT_LMIN positions long;
  * req > 0 asks for that many (a test hook: several chunks per slice) */
@@ -1020,6 +1310,13 @@ struct tlm_hip_model {
     std::vector<float> layer_heat;               /* mean manifest heat of a layer's experts (tlm_model.c:546-560) */
     std::vector<int32_t> route_ids;              /* the last step's routing, n_layers x top_k (host) */
     std::vector<float> route_w;
+    /* batched prefill: chunk option, then its buffers (allocated at first use,
+     * pf_cap tokens each; score rows of pf_sl floats) */
+    int pf_chunk = 0, pf_cap = 0, pf_sl = 0;
+    float *pf_h = nullptr, *pf_q = nullptr, *pf_kx = nullptr, *pf_vx = nullptr, *pf_att = nullptr, *pf_y = nullptr;
+    float *pf_scores = nullptr, *pf_w = nullptr;
+    uint8_t *pf_act = nullptr, *pf_ws = nullptr;
+    int32_t *pf_ids = nullptr;
 
     void *dalloc(size_t n) {
         void *p = nullptr;
@@ -1169,6 +1466,7 @@ int prepare(tlm_hip_model *M, const tlm_hip_model_opts *o) {
     M->xopts.lookahead = M->xs_prefetch ? 1 : 0;   /* src/bin/tierlm.c:307-309 */
     M->xopts.lookahead_k = o ? o->lookahead_k : 0;
     M->xopts.interest = o ? o->interest : 0.0;
+    M->pf_chunk = o ? o->prefill_chunk : 0;
     if (M->xopts.lookahead_k < 0 || M->xopts.lookahead_k > 32)
         return tlmh_seterr(TLM_HIP_EINVAL, "model: lookahead_k %d (0..32)", M->xopts.lookahead_k);
     /* a step through the cache waits on the host between layers: never a graph */
@@ -1606,6 +1904,149 @@ int step(tlm_hip_model *M, bool want_logits) {
     return rc;
 }
 
+/* ---- batched prefill --------------------------------------------------------
+ * tlm_model_prefill steps each prompt token in turn (src/lib/tlm_model.c:
+ * 1105-1113).  Per chunk of tokens each layer runs once for all of them:
+ * rmsnorm + the activation quantiser per token (the decode GEMV prologue's
+ * code), q / k / v as int8 MFMA token matmuls (bit-equal to the decode GEMV
+ * per token), the causal attention launches (the step's order per token),
+ * o the same way plus the residual add, and the batched MoE block (the
+ * decode block's result per token); the chunk's last token then takes the
+ * step's final norm, lm_head and argmax.  Every token's values are the
+ * step's bits, so the cache, the logits and the greedy token are those of n
+ * steps. */
+bool pf_dense_ok(const DevMat &m) {
+    return m.dt == DT_Q4_K || m.dt == DT_Q5_K || m.dt == DT_Q6_K || m.dt == DT_Q8_0;
+}
+bool pf_supported(const tlm_hip_model *M) {
+    const tlm_hip_model_geom &g = M->g;
+    if (M->pf_chunk < 0 || M->xs || M->att_split) return false;
+    if (!pf_att_supported((int)g.head_dim, (int)g.n_heads, (int)g.n_kv_heads)) return false;
+    if (g.d_model % 256 || ((int64_t)g.n_heads * g.head_dim) % 256 || g.d_model > 8192 ||
+        (int64_t)g.n_heads * g.head_dim > 8192)
+        return false;
+    for (const Layer &Ly : M->L) {
+        if (!pf_dense_ok(Ly.q) || !pf_dense_ok(Ly.k) || !pf_dense_ok(Ly.v) || !pf_dense_ok(Ly.o)) return false;
+        const int edt = Ly.moe.expert_dt;
+        if ((edt != DT_Q4_K && edt != DT_Q5_K && edt != DT_Q6_K) || Ly.moe.ds > 0 || !Ly.moe.experts) return false;
+    }
+    return true;
+}
+
+/* the chunk's buffers: pf_cap tokens, score rows for the whole capacity
+ * (at most 256 MB of scores, the chunk a multiple of 4, at most 512) */
+int pf_alloc(tlm_hip_model *M) {
+    if (M->pf_cap) return TLM_HIP_OK;
+    const tlm_hip_model_geom &g = M->g;
+    const int64_t D = g.d_model, HQ = (int64_t)g.n_heads * g.head_dim, KVD = (int64_t)g.n_kv_heads * g.head_dim;
+    const int sl = (M->max_ctx + 3) & ~3;
+    int64_t cap = ((int64_t)256 << 20) / ((int64_t)g.n_heads * sl * 4);
+    cap = cap > 512 ? 512 : cap;
+    if (M->pf_chunk > 0 && cap > M->pf_chunk) cap = M->pf_chunk;
+    cap = cap >= 4 ? cap & ~3 : cap < 1 ? 1 : cap;
+    size_t ws = 0;
+    for (const Layer &Ly : M->L) {
+        const size_t b = moe_prefill_workspace_bytes(&Ly.moe, cap);
+        ws = b > ws ? b : ws;
+    }
+    const int64_t wmax = D > HQ ? D : HQ;
+    M->pf_h = (float *)M->dalloc((size_t)cap * D * 4);
+    M->pf_q = (float *)M->dalloc((size_t)cap * HQ * 4);
+    M->pf_kx = (float *)M->dalloc((size_t)cap * KVD * 4);
+    M->pf_vx = (float *)M->dalloc((size_t)cap * KVD * 4);
+    M->pf_att = (float *)M->dalloc((size_t)cap * HQ * 4);
+    M->pf_y = (float *)M->dalloc((size_t)cap * D * 4);
+    M->pf_scores = (float *)M->dalloc((size_t)cap * g.n_heads * sl * 4);
+    M->pf_act = (uint8_t *)M->dalloc((size_t)cap * (wmax / 256) * 292);   /* Q8_K or a8 rows of the widest input */
+    M->pf_ws = (uint8_t *)M->dalloc(ws);
+    M->pf_ids = (int32_t *)M->dalloc((size_t)cap * g.top_k * 4);
+    M->pf_w = (float *)M->dalloc((size_t)cap * g.top_k * 4);
+    if (!M->pf_h || !M->pf_q || !M->pf_kx || !M->pf_vx || !M->pf_att || !M->pf_y || !M->pf_scores || !M->pf_act ||
+        !M->pf_ws || !M->pf_ids || !M->pf_w)
+        return tlmh_seterr(TLM_HIP_ENOMEM, "model prefill: out of device memory (%lld-token chunks)", (long long)cap);
+    M->pf_sl = sl;
+    M->pf_cap = (int)cap;
+    return TLM_HIP_OK;
+}
+
+/* rmsnorm (w given) + the activation quantiser of dt's kind on nt rows of x
+ * (width n), then the token matmul into y [nt][W.rows] */
+int pf_matmul(tlm_hip_model *M, const DevMat &W, const float *x, int64_t n, const float *w, int nt, float *y,
+              int *act_kind) {
+    const int kind = dt_act_kind(W.dt);
+    const int64_t astride = (int64_t)act_bytes(kind, n);
+    int rc = TLM_HIP_OK;
+    if (*act_kind != kind) {
+        rc = launch_tok_norm_act(kind, x, n, w, M->g.norm_eps, n, nt, M->pf_act, astride, M->stream);
+        *act_kind = rc ? -1 : kind;
+    }
+    if (!rc) rc = launch_tokmm(W.dt, W.p, W.rows, n, M->pf_act, nt, y, M->stream);
+    return rc;
+}
+
+/* tokens seq[p0 .. p0 + n) (already on the device) through the model, from
+ * position p0; the step's tail on the last one */
+int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
+    if (int rc = pf_alloc(M)) return rc;
+    const tlm_hip_model_geom &g = M->g;
+    const int D = (int)g.d_model, hd = (int)g.head_dim, H = (int)g.n_heads, KV = (int)g.n_kv_heads;
+    const int k = (int)g.top_k;
+    hipStream_t s = M->stream;
+    int rc = TLM_HIP_OK;
+    int nt = 0;
+    for (int c0 = 0; c0 < n && !rc; c0 += M->pf_cap) {
+        nt = n - c0 < M->pf_cap ? n - c0 : M->pf_cap;
+        const int pc = p0 + c0;
+        hipLaunchKernelGGL(k_pf_embed, dim3((D + NT - 1) / NT, nt), dim3(NT), 0, s, M->embd, M->embd_row, M->embd_dt,
+                           (const int32_t *)M->seq + pc, D, M->pf_h);
+        rc = tlmh_check(hipGetLastError(), "model prefill: embed");
+        for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
+            const Layer &Ly = M->L[l];
+            int ak = -1;
+            rc = pf_matmul(M, Ly.q, M->pf_h, D, Ly.attn_norm, nt, M->pf_q, &ak);
+            if (!rc) rc = pf_matmul(M, Ly.k, M->pf_h, D, Ly.attn_norm, nt, M->pf_kx, &ak);
+            if (!rc) rc = pf_matmul(M, Ly.v, M->pf_h, D, Ly.attn_norm, nt, M->pf_vx, &ak);
+            const size_t kbase = (size_t)l * KV * M->max_ctx * hd, vbase = (size_t)l * KV * att_vstride(M->max_ctx, hd);
+            if (!rc)
+                rc = launch_pf_attn(hd, H, KV, M->max_ctx, pc, nt, M->pf_q, M->pf_kx, M->pf_vx, Ly.q_norm, Ly.k_norm,
+                                    M->cs, M->sn, M->kc + kbase, M->vc + vbase, M->pf_scores, M->pf_sl, M->pf_att,
+                                    g.norm_eps, s);
+            ak = -1;
+            if (!rc) rc = pf_matmul(M, Ly.o, M->pf_att, (int64_t)H * hd, nullptr, nt, M->pf_y, &ak);
+            if (!rc) {
+                const int64_t cnt = (int64_t)nt * D;
+                hipLaunchKernelGGL(k_pf_add, dim3((unsigned)((cnt + NT * 4 - 1) / (NT * 4))), dim3(NT), 0, s, M->pf_h,
+                                   (const float *)M->pf_y, cnt);
+                rc = tlmh_check(hipGetLastError(), "model prefill: residual");
+            }
+            if (!rc) rc = launch_moe_prefill(&Ly.moe, M->pf_h, nt, M->pf_ids, M->pf_w, M->pf_ws, s);
+            if (!rc && c0 + nt == n) {   /* the last token's routing, as the step leaves it */
+                rc = tlmh_check(hipMemcpyAsync(M->ids + (size_t)l * 32, M->pf_ids + (size_t)(nt - 1) * k, (size_t)k * 4,
+                                               hipMemcpyDeviceToDevice, s), "model prefill: routes");
+                if (!rc)
+                    rc = tlmh_check(hipMemcpyAsync(M->w + (size_t)l * 32, M->pf_w + (size_t)(nt - 1) * k,
+                                                   (size_t)k * 4, hipMemcpyDeviceToDevice, s), "model prefill: routes");
+            }
+        }
+    }
+    if (rc) return rc;
+    rc = tlmh_check(hipMemcpyAsync(M->h, M->pf_h + (size_t)(nt - 1) * D, (size_t)D * 4, hipMemcpyDeviceToDevice, s),
+                    "model prefill: h");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_set_pos, dim3(1), dim3(1), 0, s, M->st, p0 + n - 1);
+    rc = enqueue_tail(M, want_logits);
+    if (!rc) M->kv_len = p0 + n;
+    return rc;
+}
+
+/* the n tokens at seq[kv_len ..]: batched where supported, else one step each */
+int run_prompt(tlm_hip_model *M, int n, bool want_logits) {
+    if (pf_supported(M)) return prefill_batched(M, M->kv_len, n, want_logits);
+    int rc = TLM_HIP_OK;
+    for (int i = 0; i < n && !rc; i++) rc = step(M, want_logits && i == n - 1);
+    return rc;
+}
+
 /* ---- random-init models (tlm_hip_model_synth) -----------------------------
  * Counter-based: every byte is a function of (seed, tensor, index), through
  * the splitmix64 output function (Steele, Lea, Flood, "Fast splittable
@@ -1976,6 +2417,26 @@ int tlm_hip_model_step(tlm_hip_model *M, int token, float *logits, int32_t *next
     return rc;
 }
 
+int tlm_hip_model_prefill_batched(const tlm_hip_model *M) { return M && pf_supported(M) ? 1 : 0; }
+
+int tlm_hip_model_prefill(tlm_hip_model *M, const int32_t *tokens, int n, float *logits) {
+    if (!M || !tokens || n <= 0) return tlmh_seterr(TLM_HIP_EINVAL, "prefill: no tokens");
+    const int pos0 = M->kv_len;
+    if ((int64_t)pos0 + n > M->max_ctx)
+        return tlmh_seterr(TLM_HIP_ERANGE, "model prefill: %d + %d tokens exceed the context (%d)", pos0, n,
+                           M->max_ctx);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= M->g.vocab)
+            return tlmh_seterr(TLM_HIP_EINVAL, "token %d out of range", tokens[i]);
+    int rc = tlmh_check(hipMemcpy(M->seq + pos0, tokens, (size_t)n * 4, hipMemcpyHostToDevice), "model: prompt");
+    if (!rc) rc = run_prompt(M, n, logits != nullptr);
+    if (!rc && logits)
+        rc = tlmh_check(hipMemcpyAsync(logits, M->logits, (size_t)M->g.vocab * 4, hipMemcpyDeviceToHost, M->stream),
+                        "model: logits");
+    if (!rc) rc = tlmh_check(hipStreamSynchronize(M->stream), "model: prefill");
+    return rc;
+}
+
 /* tlm_model_prefill (src/lib/tlm_model.c:1105-1113) then n_gen greedy tokens
  * (tierlm bench's loop, src/bin/tierlm.c:720-729): the prompt is written to
  * the device once, each step's token is read there and each greedy token is
@@ -1991,7 +2452,7 @@ int tlm_hip_model_generate(tlm_hip_model *M, const int32_t *prompt, int n_prompt
         if (prompt[i] < 0 || (uint32_t)prompt[i] >= M->g.vocab)
             return tlmh_seterr(TLM_HIP_EINVAL, "token %d out of range", prompt[i]);
     int rc = tlmh_check(hipMemcpy(M->seq + pos0, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice), "model: prompt");
-    for (int i = 0; i < n_prompt && !rc; i++) rc = step(M, i == n_prompt - 1);
+    if (!rc) rc = run_prompt(M, n_prompt, n_gen > 0);
     for (int gi = 1; gi < n_gen && !rc; gi++) rc = step(M, true);
     if (!rc && n_gen > 0)
         rc = tlmh_check(hipMemcpyAsync(out, M->seq + pos0 + n_prompt, (size_t)n_gen * 4, hipMemcpyDeviceToHost,

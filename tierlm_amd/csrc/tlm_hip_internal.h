@@ -239,6 +239,11 @@ int launch_pack(int dt, const void *src, size_t row_bytes, int64_t rows, int64_t
 int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, float *y,
                          hipStream_t s);
 int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s);
+/* ntok vectors of n floats (row stride xstride floats): rmsnorm with w (NULL:
+ * none) then the activation quantiser of kind (Q8_0 = a8, or Q8_K), exactly
+ * as the decode GEMV's prologue computes it, into the reference layout */
+int launch_tok_norm_act(int kind, const float *x, int64_t xstride, const float *w, float eps, int64_t n,
+                        int64_t ntok, void *out, int64_t ostride, hipStream_t s);
 /* up to MV_SEGS packed matrices of one dtype and width n in one launch, one
  * shared activation; accum: y += W x.  With nx set, every group computes the
  * activation itself, quantising rmsnorm(nx) * nw (eps), or nx itself when nw

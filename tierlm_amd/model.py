@@ -21,18 +21,19 @@ class ModelOpts(C.Structure):
     """tlm_hip_model_opts"""
     _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32), ("attn_split", C.c_int32),
                 ("expert_cache_bytes", C.c_uint64), ("pin_frac", C.c_double), ("prefetch_off", C.c_int32),
-                ("lookahead_k", C.c_int32), ("interest", C.c_double)]
+                ("lookahead_k", C.c_int32), ("interest", C.c_double), ("prefill_chunk", C.c_int32)]
 
 
 def model_opts(max_ctx=0, eager=False, attn_slices=0, split=False, expert_cache=0, pin_frac=0.0, prefetch=True,
-               lookahead_k=0, interest=0.0):
+               lookahead_k=0, interest=0.0, prefill_chunk=0):
     """tlm_hip_model_opts; expert_cache > 0 (bytes) serves the experts through
     an HBM slot cache of that size from page-locked host memory, as tierlm's
     runtime serves them from its store (pin_frac 0 = its default 0.30,
     prefetch = its router lookahead, lookahead_k / interest its io and nav
-    options)."""
+    options); prefill_chunk: 0 batched prompts where the model allows them,
+    n > 0 at most n tokens per batch, < 0 one step per token."""
     return ModelOpts(max_ctx, int(eager), attn_slices, int(split), int(expert_cache), float(pin_frac),
-                     0 if prefetch else 1, int(lookahead_k), float(interest))
+                     0 if prefetch else 1, int(lookahead_k), float(interest), int(prefill_chunk))
 
 
 # Qwen3-30B-A3B: 48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128
@@ -44,7 +45,7 @@ QWEN3_30B_A3B = dict(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_d
 
 class Model:
     def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0, split=False, **cache):
-        """cache: expert_cache, pin_frac, prefetch, lookahead_k, interest (model_opts)"""
+        """cache: expert_cache, pin_frac, prefetch, lookahead_k, interest, prefill_chunk (model_opts)"""
         self.opts = model_opts(max_ctx, eager, attn_slices, split, **cache)
         h = C.c_void_p()
         check(lib.tlm_hip_model_open(str(manifest_path).encode(), C.byref(self.opts), C.byref(h)))
@@ -139,6 +140,18 @@ class Model:
         nxt = C.c_int32()
         check(lib.tlm_hip_model_step(self.h, int(token), lg.ctypes.data if logits else None, C.byref(nxt)))
         return lg, nxt.value
+
+    def prefill(self, tokens, logits=True):
+        """tlm_model_prefill: the tokens from the current position; the last
+        one's logits (float32 [vocab]) or None."""
+        p = (C.c_int32 * len(tokens))(*tokens)
+        lg = np.empty(self.geom.vocab, np.float32) if logits else None
+        check(lib.tlm_hip_model_prefill(self.h, p, len(tokens), lg.ctypes.data if logits else None))
+        return lg
+
+    def prefill_batched(self):
+        """Whether prompts run batched on this model."""
+        return bool(lib.tlm_hip_model_prefill_batched(self.h))
 
     def generate(self, prompt, n):
         p = (C.c_int32 * len(prompt))(*prompt)
