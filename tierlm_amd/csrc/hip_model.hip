@@ -991,8 +991,8 @@ __global__ __launch_bounds__(NT) void k_pf_scores(const float *__restrict__ q, c
         float acc[HB];
 #pragma unroll
         for (int j = 0; j < HB; j++) acc[j] = 0.0f;
-#pragma unroll 8
-        for (int i4 = 0; i4 < H4; i4++) {
+#pragma unroll
+        for (int i4 = 0; i4 < H4; i4++) {   /* whole: the key row stays in registers */
             const f32x4 b = kr[i4];
 #pragma unroll
             for (int j = 0; j < HB; j++) {

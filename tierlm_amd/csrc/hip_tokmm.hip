@@ -12,7 +12,7 @@ using tokmm::TM_TOK;
 constexpr int GROUP_ROWS = tokmm::TM_WAVES * TM_ROWS;
 
 template <int DT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_tokmm(const uint8_t *__restrict__ Wp, int64_t rows, int nb,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == DT_Q8_0 ? 2 : 3))) void k_tokmm(const uint8_t *__restrict__ Wp, int64_t rows, int nb,
                                                const uint8_t *__restrict__ act, int ntok, float *__restrict__ Y) {
     __shared__ __align__(16) uint8_t s_tile[tokmm::tile_lds_bytes<DT>()];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5;

@@ -288,11 +288,21 @@ __device__ __forceinline__ void block_chain(const WRaw<DT_Q8_0> &w, const LAS ui
                                             float (&acc)[16]) {
     using S = Stage<DT_Q8_0>;
     const LAS uint8_t *cod = buf + t * S::CS + 16 * half;
+    auto mm = [&](int i) {
+        v4i ax = *(const LAS v4i *)(cod + 32 * i);
+        /* ordered after the previous block's chain (the volatile statements
+         * below keep their order): at most two products live - hoisting all
+         * eight 16-register results spills */
+        asm volatile("" : "+v"(ax));
+        const v4i bw = {(int)w.q[i].x, (int)w.q[i].y, (int)w.q[i].z, (int)w.q[i].w};
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bw, v16i{}, 0, 0, 0);
+    };
+    /* block i + 1's product is issued before block i's chain */
+    v16i pn = mm(0);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const v4i ax = *(const LAS v4i *)(cod + 32 * i);
-        const v4i bw = {(int)w.q[i].x, (int)w.q[i].y, (int)w.q[i].z, (int)w.q[i].w};
-        const v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax, bw, v16i{}, 0, 0, 0);
+        const v16i p = pn;
+        if (i < 7) pn = mm(i + 1);
         const LAS float *dd = (const LAS float *)(buf + S::D) + 32 * i + 4 * half;
         const float dw = f16_to_f32(w.d[i]);
 #pragma unroll
@@ -304,6 +314,8 @@ __device__ __forceinline__ void block_chain(const WRaw<DT_Q8_0> &w, const LAS ui
                 acc[v] = fmaf(dw * da[k], (float)p[v], acc[v]);
             }
         }
+#pragma unroll
+        for (int v = 0; v < 16; v++) asm volatile("" : "+v"(acc[v]));
     }
 }
 
