@@ -419,6 +419,17 @@ def c3_bench(torch, steps, warmup, ctx, split=False):
         wall = time.perf_counter() - h0
         ev1.synchronize()
         ev_s = ev0.elapsed_time(ev1) * 1e-3
+        # batched prefill of a (ctx - 1)-token prompt (tlm_model_prefill's
+        # result, 512-token chunks): first run allocates, best of the next two
+        pf_prompt = bench_prompt(ctx - 1, QWEN3_30B_A3B["vocab"], seed=7)
+        pf = []
+        for _ in range(3):
+            m.reset()
+            t0 = time.perf_counter()
+            m.prefill(pf_prompt)
+            pf.append(time.perf_counter() - t0)
+        prefill_s = min(pf[1:])
+        batched = m.prefill_batched()
     finally:
         m.close()
     gb = c3_geometry_bytes(QWEN3_30B_A3B)
@@ -430,8 +441,10 @@ def c3_bench(torch, steps, warmup, ctx, split=False):
         f"{steps} steps at positions "
         f"{positions[-1]}..{positions[0]} ({sec * 1e3:.3f} ms/token events, {wall / steps * 1e3:.3f} ms/token host); "
         f"{per_tok / 1e9:.3f} GB/token = {achieved:.0f} GB/s; context fill {ctx - 64} tokens in {fill_s:.1f} s "
-        f"({(ctx - 64) / fill_s:.1f} tok/s)")
-    return {"tok_s": steps / ev_s, "ms_per_step": sec * 1e3, "wall_ms_per_step": wall / steps * 1e3,
+        f"({(ctx - 64) / fill_s:.1f} tok/s); prefill {ctx - 1} tokens in {prefill_s * 1e3:.1f} ms "
+        f"({(ctx - 1) / prefill_s:.0f} tok/s{'' if batched else ', one step per token'})")
+    return {"prefill_tok_s": (ctx - 1) / prefill_s, "prefill_ms": prefill_s * 1e3, "prefill_batched": batched,
+            "tok_s": steps / ev_s, "ms_per_step": sec * 1e3, "wall_ms_per_step": wall / steps * 1e3,
             "positions": [positions[-1], positions[0]], "bytes_per_token": per_tok, "weights_per_token":
             gb["weights_per_token"], "kv_bytes_per_token_mean": kv_mean, "achieved_GBps": achieved,
             "build_s": built, "fill_tok_s": (ctx - 64) / fill_s, "tokens_head": toks[:4], "geometry_bytes": gb}
@@ -836,6 +849,12 @@ def main():
         "slot_cache": slot_cache,
         "c1_whole_step": c1,
         "qwen3_30b_a3b_context_fill_tok_s": round(c3["fill_tok_s"], 1),
+        "qwen3_30b_a3b_prefill": {
+            "tokens": args.c3_context - 1, "ms": round(c3["prefill_ms"], 2), "tok_s": round(c3["prefill_tok_s"], 1),
+            "batched": c3["prefill_batched"],
+            "timing": "host wall clock around tlm_hip_model_prefill (prompt upload, the batched chunks, the last "
+                      "token's lm_head and logits download), best of 2 after one run that allocates",
+            "note": "each token's cache entries, logits and greedy token are the step-by-step prefill's bits"},
         "qwen3_30b_a3b_split_attention": None if c3s is None else {
             "tok_s": round(c3s["tok_s"], 2), "ms_per_step": round(c3s["ms_per_step"], 4), "steps": args.split_steps,
             "positions": c3s["positions"],

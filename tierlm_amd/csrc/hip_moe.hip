@@ -1440,7 +1440,7 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
                        hipStream_t s) {
     if (int rc = moe_check(d, h, ws)) return rc;
     if (T <= 0 || T > 65536) return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld outside 1..65536", (long long)T);
-    if (!tokmm::tile_dt(d->expert_dt) || d->ds > 0)
+    if ((d->expert_dt != DT_Q4_K && d->expert_dt != DT_Q5_K && d->expert_dt != DT_Q6_K) || d->ds > 0)
         return tlmh_seterr(TLM_HIP_EUNSUP, "moe_prefill: routed Q4_K / Q5_K / Q6_K experts without a shared "
                            "expert only (expert dtype %d, ds %lld)", d->expert_dt, (long long)d->ds);
     const tlm_hip_moe_desc dv = *d;
