@@ -1288,6 +1288,7 @@ struct tlm_hip_model {
     float *part_o = nullptr, *part_ml = nullptr;       /* split partials: [H][att_g][hd]; [H][att_g] (m, l) */
     float *h = nullptr, *q = nullptr, *kx = nullptr, *vx = nullptr, *att = nullptr;
     float *logits = nullptr;
+    uint8_t *lm_act = nullptr;   /* the final norm's quantised activation, once per step for every lm_head group */
     uint8_t *moe_ws = nullptr;
     int32_t *st = nullptr, *seq = nullptr, *ids = nullptr;   /* st[0] = position; seq[max_ctx + 1] tokens */
     unsigned long long *keys = nullptr;                      /* greedy key per lm_head tile */
@@ -1529,6 +1530,7 @@ int finish(tlm_hip_model *M) {
     M->vx = (float *)M->dalloc((size_t)KV * hd * 4);
     M->att = (float *)M->dalloc((size_t)H * hd * 4);
     M->logits = (float *)M->dalloc((size_t)g.vocab * 4);
+    M->lm_act = (uint8_t *)M->dalloc(act_bytes(DT_Q8_K, D) + act_bytes(DT_Q8_0, D));
     size_t ws = 0;
     for (const Layer &Ly : M->L) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
     M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
@@ -1541,7 +1543,7 @@ int finish(tlm_hip_model *M) {
                     (void *)M->part_ml, (void *)M->h,
                     (void *)M->q, (void *)M->kx, (void *)M->vx, (void *)M->att, (void *)M->logits,
                     (void *)M->moe_ws, (void *)M->st, (void *)M->seq, (void *)M->ids,
-                    (void *)M->w, (void *)M->keys})
+                    (void *)M->w, (void *)M->keys, (void *)M->lm_act})
         if (!p) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the KV cache / scratch");
     if ((rc = tlmh_check(hipHostMalloc((void **)&M->host_tok, 64, hipHostMallocDefault), "model: pinned scratch")))
         return rc;
@@ -1825,11 +1827,15 @@ int enqueue_tail(tlm_hip_model *M, bool want_logits) {
     hipStream_t s = M->stream;
     const int nkeys = (int)((g.vocab + TILE_ROWS - 1) / TILE_ROWS);
     if (want_logits) {
-        const MvNorm on{M->h, M->out_norm, g.norm_eps};
+        /* the final norm and its activation once (the GEMV prologue's code,
+         * so the same bytes), not in each of the vocab / 16 groups */
+        const int kind = dt_act_kind(M->lm_head.dt);
+        int rc = launch_tok_norm_act(kind, M->h, D, M->out_norm, g.norm_eps, D, 1, M->lm_act,
+                                     (int64_t)act_bytes(kind, D), s);
         const void *Wl = M->lm_head.p;
         const int64_t Rl = M->lm_head.rows;
         float *const Yl = M->logits;
-        const int rc = launch_mv_segs(M->lm_head.dt, D, &Wl, &Rl, &Yl, 1, 0, nullptr, s, &on, M->keys);
+        if (!rc) rc = launch_mv_segs(M->lm_head.dt, D, &Wl, &Rl, &Yl, 1, 0, M->lm_act, s, nullptr, M->keys);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(want_logits ? 1024 : 64), 0, s, M->st, M->seq,
