@@ -134,3 +134,24 @@ def test_synth_cached_heat_lookahead(hip):
         assert st["prefetch_issued"] > 0 and st["prefetch_used"] > 0
     finally:
         m.close()
+
+
+def test_cached_prompt_matches_resident_batched(hip):
+    """A model with its experts behind the slot cache prefills one step per
+    token; the resident model batches the same prompt: the last position's
+    logits and routing agree bit for bit."""
+    from tierlm_amd.model import Model, bench_prompt
+    a = Model.synth(SMALL, expert_dt=13, seed=4, max_ctx=128)
+    b = Model.synth(SMALL, expert_dt=13, seed=4, max_ctx=128, expert_cache=TINY)
+    try:
+        assert a.prefill_batched() and not b.prefill_batched()
+        p = bench_prompt(70, SMALL["vocab"], seed=3)
+        la, lb = a.prefill(p), b.prefill(p)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        ia, wa = a.routes()
+        ib, wb = b.routes()
+        assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32))
+        assert a.kv_len() == b.kv_len() == 70
+    finally:
+        a.close()
+        b.close()

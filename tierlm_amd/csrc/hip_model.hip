@@ -1314,6 +1314,7 @@ struct tlm_hip_model {
     /* batched prefill: chunk option, then its buffers (allocated at first use,
      * pf_cap tokens each; score rows of pf_sl floats) */
     int pf_chunk = 0, pf_cap = 0, pf_sl = 0;
+    bool pf_nomem = false;                       /* the buffers did not fit: prompts step token by token */
     float *pf_h = nullptr, *pf_q = nullptr, *pf_kx = nullptr, *pf_vx = nullptr, *pf_att = nullptr, *pf_y = nullptr;
     float *pf_scores = nullptr, *pf_w = nullptr;
     uint8_t *pf_act = nullptr, *pf_ws = nullptr;
@@ -1926,7 +1927,7 @@ bool pf_dense_ok(const DevMat &m) {
 }
 bool pf_supported(const tlm_hip_model *M) {
     const tlm_hip_model_geom &g = M->g;
-    if (M->pf_chunk < 0 || M->xs || M->att_split) return false;
+    if (M->pf_chunk < 0 || M->xs || M->att_split || M->pf_nomem) return false;
     if (!pf_att_supported((int)g.head_dim, (int)g.n_heads, (int)g.n_kv_heads)) return false;
     if (g.d_model % 256 || ((int64_t)g.n_heads * g.head_dim) % 256 || g.d_model > 8192 ||
         (int64_t)g.n_heads * g.head_dim > 8192)
@@ -1968,8 +1969,10 @@ int pf_alloc(tlm_hip_model *M) {
     M->pf_ids = (int32_t *)M->dalloc((size_t)cap * g.top_k * 4);
     M->pf_w = (float *)M->dalloc((size_t)cap * g.top_k * 4);
     if (!M->pf_h || !M->pf_q || !M->pf_kx || !M->pf_vx || !M->pf_att || !M->pf_y || !M->pf_scores || !M->pf_act ||
-        !M->pf_ws || !M->pf_ids || !M->pf_w)
+        !M->pf_ws || !M->pf_ids || !M->pf_w) {
+        M->pf_nomem = true;
         return tlmh_seterr(TLM_HIP_ENOMEM, "model prefill: out of device memory (%lld-token chunks)", (long long)cap);
+    }
     M->pf_sl = sl;
     M->pf_cap = (int)cap;
     return TLM_HIP_OK;
@@ -2045,9 +2048,15 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
     return rc;
 }
 
-/* the n tokens at seq[kv_len ..]: batched where supported, else one step each */
+/* the n tokens at seq[kv_len ..]: batched where supported (and its chunk
+ * buffers fit), else one step each */
 int run_prompt(tlm_hip_model *M, int n, bool want_logits) {
-    if (pf_supported(M)) return prefill_batched(M, M->kv_len, n, want_logits);
+    if (pf_supported(M)) {
+        const int rc = pf_alloc(M);
+        if (!rc) return prefill_batched(M, M->kv_len, n, want_logits);
+        if (rc != TLM_HIP_ENOMEM) return rc;
+        (void)hipGetLastError();   /* no room for the chunk buffers: step token by token */
+    }
     int rc = TLM_HIP_OK;
     for (int i = 0; i < n && !rc; i++) rc = step(M, want_logits && i == n - 1);
     return rc;
