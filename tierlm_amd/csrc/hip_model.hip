@@ -2012,9 +2012,19 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
         for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
             const Layer &Ly = M->L[l];
             int ak = -1;
-            rc = pf_matmul(M, Ly.q, M->pf_h, D, Ly.attn_norm, nt, M->pf_q, &ak);
-            if (!rc) rc = pf_matmul(M, Ly.k, M->pf_h, D, Ly.attn_norm, nt, M->pf_kx, &ak);
-            if (!rc) rc = pf_matmul(M, Ly.v, M->pf_h, D, Ly.attn_norm, nt, M->pf_vx, &ak);
+            if (Ly.q.dt == Ly.k.dt && Ly.q.dt == Ly.v.dt) {   /* q | k | v in one launch */
+                const int kind = dt_act_kind(Ly.q.dt);
+                rc = launch_tok_norm_act(kind, M->pf_h, D, Ly.attn_norm, g.norm_eps, D, nt, M->pf_act,
+                                         (int64_t)act_bytes(kind, D), s);
+                const void *W3[3] = {Ly.q.p, Ly.k.p, Ly.v.p};
+                const int64_t R3[3] = {Ly.q.rows, Ly.k.rows, Ly.v.rows};
+                float *const Y3[3] = {M->pf_q, M->pf_kx, M->pf_vx};
+                if (!rc) rc = launch_tokmm_segs(Ly.q.dt, 3, W3, R3, D, M->pf_act, nt, Y3, s);
+            } else {
+                rc = pf_matmul(M, Ly.q, M->pf_h, D, Ly.attn_norm, nt, M->pf_q, &ak);
+                if (!rc) rc = pf_matmul(M, Ly.k, M->pf_h, D, Ly.attn_norm, nt, M->pf_kx, &ak);
+                if (!rc) rc = pf_matmul(M, Ly.v, M->pf_h, D, Ly.attn_norm, nt, M->pf_vx, &ak);
+            }
             const size_t kbase = (size_t)l * KV * M->max_ctx * hd, vbase = (size_t)l * KV * att_vstride(M->max_ctx, hd);
             if (!rc)
                 rc = launch_pf_attn(hd, H, KV, M->max_ctx, pc, nt, M->pf_q, M->pf_kx, M->pf_vx, Ly.q_norm, Ly.k_norm,

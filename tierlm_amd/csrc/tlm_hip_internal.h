@@ -283,6 +283,10 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
                        hipStream_t s);
 int launch_tokmm(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok, float *Y,
                  hipStream_t s);
+/* up to 4 matrices of one dtype and width n against the same ntok tokens in
+ * one launch (the q / k / v of a prefill chunk) */
+int launch_tokmm_segs(int dt, int nseg, const void *const *W, const int64_t *rows, int64_t n, const void *act,
+                      int64_t ntok, float *const *Y, hipStream_t s);
 size_t moe_workspace_bytes(const tlm_hip_moe_desc *d);
 int launch_moe_layer(const tlm_hip_moe_desc *d, float *h, int32_t *ids, float *w, void *ws, hipStream_t s);
 int launch_moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
