@@ -142,3 +142,31 @@ def test_shared_expert_steps(hip):
     """A shared expert: the batched path declines, the prompt still runs (one
     step per token) with the same bits."""
     compare_models(dict(BASE, n_shared=1, d_shared=256), 14, 8, True, 0, [20], n_after=2, batched=False)
+
+
+@pytest.mark.parametrize("parts,max_ctx,n_after", [([1, 2, 1, 3], 320, 4), ([63, 1], 64, 0), ([29, 35], 64, 0)])
+def test_synth_tiny_and_full_prompts(hip, parts, max_ctx, n_after):
+    """Prompts of 1-3 tokens (a chunk smaller than one group's 4 tokens), and
+    prompts that fill the context capacity exactly."""
+    compare_models(BASE, 14, 8, True, 0, parts, n_after=n_after, max_ctx=max_ctx)
+
+
+def test_prefill_errors(hip):
+    """Past the capacity, an empty prompt and a token outside the vocabulary
+    are refused, and the context is left as it was."""
+    from tierlm_amd._lib import HipError
+    from tierlm_amd.model import Model, bench_prompt
+    m = Model.synth(BASE, expert_dt=14, seed=3, max_ctx=32)
+    try:
+        m.prefill(bench_prompt(20, BASE["vocab"]))
+        with pytest.raises(HipError):
+            m.prefill(bench_prompt(13, BASE["vocab"]))
+        with pytest.raises(HipError):
+            m.prefill([])
+        with pytest.raises(HipError):
+            m.prefill([BASE["vocab"]])
+        assert m.kv_len() == 20
+        lg = m.prefill(bench_prompt(12, BASE["vocab"], seed=9))
+        assert np.isfinite(lg).all() and m.kv_len() == 32
+    finally:
+        m.close()
