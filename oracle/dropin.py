@@ -19,7 +19,9 @@ library (each one anchored on a line of the reference and asserted to apply):
   (tlm_kv_new, :646-664) also opens the store on the device
   (tlm_hip_model_open, with the same capacity); tlm_model_step (:1058-1103)
   then runs the whole step there (tlm_hip_model_step: logits back to the
-  host only when asked for), tlm_kv_reset / tlm_kv_free reset and close it;
+  host only when asked for), tlm_model_prefill (:1105-1113) hands the whole
+  prompt over (tlm_hip_model_prefill: batched where the model allows it, the
+  same bits), tlm_kv_reset / tlm_kv_free reset and close it;
 * src/bin/tierlm.c, rt_open (:196-202): --kernel hip sets the device manifest
   to the store being opened (TIERLM_HIP_TIER_ONLY=1 keeps the reference's CPU
   step with only the kernel table on the device), and the stats line names
@@ -69,6 +71,8 @@ PATCHES = [
      "    if (kv->hip) tlm_hip_model_close((tlm_hip_model *)kv->hip);\n"),
     ("lib/tlm_model.c", "int tlm_model_step(tlm_model *M, tlm_kv *kv, int token, float *logits) {\n",
      None),
+    ("lib/tlm_model.c", "    if (n <= 0) return tlm_seterr(TLM_EINVAL, \"prefill: no tokens\");\n",
+     "    if (kv->hip) return dropin_prefill(M, kv, tokens, n, logits);\n"),
     ("lib/tlm_model.c",
      "    if (kv->len >= kv->max_ctx) return tlm_seterr(TLM_ERANGE, \"context full (%d tokens)\", kv->max_ctx);\n",
      "    if (kv->hip) return dropin_step(M, kv, token, logits);\n"),
@@ -111,6 +115,16 @@ DROPIN_STEP = """static int dropin_step(tlm_model *M, tlm_kv *kv, int token, flo
     if (rc) return tlm_seterr(rc, "hip step: %s", tlm_hip_errmsg());
     kv->len++;
     M->st.tokens++;
+    M->st.other_ns += tlm_now_ns() - t0;
+    return TLM_OK;
+}
+
+static int dropin_prefill(tlm_model *M, tlm_kv *kv, const int *tokens, int n, float *logits) {
+    uint64_t t0 = tlm_now_ns();
+    int rc = tlm_hip_model_prefill((tlm_hip_model *)kv->hip, (const int32_t *)tokens, n, logits);
+    if (rc) return tlm_seterr(rc, "hip prefill: %s", tlm_hip_errmsg());
+    kv->len += n;
+    M->st.tokens += n;
     M->st.other_ns += tlm_now_ns() - t0;
     return TLM_OK;
 }

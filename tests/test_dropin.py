@@ -10,6 +10,9 @@ synthetic store (oracle/make_c1.sh) against the reference's own outputs
   `tierlm run` gives the reference's 64 greedy tokens, `tierlm oracle` its
   teacher-forced top-10 logits text for text (9 significant digits, so bit
   for bit), `tierlm bench` runs its loop;
+* on C2S (oracle/make_c2s.sh), whose geometry the batched prefill takes,
+  tlm_model_prefill hands the prompt to tlm_hip_model_prefill: `tierlm run`
+  gives the reference's greedy tokens;
 * TIERLM_HIP_TIER_ONLY=1 --kernel hip: the reference's own CPU step with
   every quantised matvec of its kernel table on the device (the host-pointer
   entries of tlm_kern_hip_fill): the same tokens."""
@@ -24,6 +27,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 TIERLM = os.path.join(ROOT, "oracle", "_ref", "dropin", "bin", "tierlm")
 C1 = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
 GOLD = os.path.join(ROOT, "tests", "golden")
+C2S = os.path.join(ROOT, "oracle", "_ref", "c2s", "c2s.tlmm")
 needs = pytest.mark.skipif(not (os.path.exists(TIERLM) and os.path.exists(C1)),
                            reason="oracle/_ref/dropin (python3 oracle/dropin.py) or oracle/_ref/c1 not built")
 
@@ -89,3 +93,10 @@ def test_bench_hip_step():
     dec = float(line.split("decode 64 tokens in")[1].split("(")[1].split(" tok/s")[0])
     print(f"tierlm bench --kernel hip: {line}")
     assert dec > 0
+
+
+@pytest.mark.skipif(not (os.path.exists(TIERLM) and os.path.exists(C2S)), reason="oracle/_ref/dropin or c2s not built")
+def test_run_hip_batched_prefill_c2s():
+    p = ",".join(map(str, prompt_ids(64, 2048)))
+    r = tierlm(["run", C2S, "--tokens", p, "-n", "64", "--print-tokens", "--cache", "1G", "--kernel", "hip"])
+    assert r.stdout.split() == golden("c2s_greedy.txt").split()
