@@ -208,8 +208,11 @@ int tlm_hip_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, f
  * block has no cross-token terms, so this gives every token exactly the
  * result of tlm_hip_moe_layer on it: h[t*D .. t*D+D) += MoE(h_t), routing in
  * ids / w [T*k] (either may be NULL).  Tokens are bucketed by expert and each
- * expert's rows stream once per 32 of its tokens (int8 MFMA).  Routed Q4_K,
- * Q5_K or Q6_K experts, no shared expert (others: TLM_HIP_EUNSUP).
+ * expert's rows stream once per 32 of its tokens (int8 MFMA); a shared expert
+ * runs as token matmuls and is added after the routed sum, as the decode
+ * block adds it.  Routed Q4_K, Q5_K or Q6_K experts; a shared expert of Q4_K,
+ * Q5_K, Q6_K or Q8_0 with D and ds multiples of 256 (others:
+ * TLM_HIP_EUNSUP).
  * workspace: tlm_hip_moe_prefill_workspace_bytes bytes, 256-byte aligned. */
 size_t tlm_hip_moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T);
 int tlm_hip_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w,
@@ -460,7 +463,8 @@ typedef struct {
     /* Prompts (tlm_hip_model_prefill / _generate): 0 = batched where the
      * model allows it - every resident layer's q/k/v/o Q4_K / Q5_K / Q6_K /
      * Q8_0 with widths multiples of 256, routed Q4_K / Q5_K / Q6_K experts
-     * without a shared expert, head width 32 / 64 / 96 / 128, the reference's
+     * (a shared expert of those dtypes or Q8_0, width a multiple of 256), head
+     * width 32 / 64 / 96 / 128, the reference's
      * attention order (attn_split 0) - in chunks sized to the context
      * capacity (at most 512 tokens); n > 0: chunks of at most n tokens; < 0:
      * one step per token.  A batched chunk runs each layer once for all of

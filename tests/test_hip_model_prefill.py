@@ -15,7 +15,8 @@ batched MoE block) and must leave every token's values the step's bits:
   the chunk), prompts in two calls (a chunk starting past position 0), head
   widths 32 / 64 / 96 / 128, 1 / 3 / 4 / 8 query heads per key head, each
   expert dtype, both routers, Q8_0 and K-quant dense matrices;
-* a model the batched path does not take (a shared expert) still prefills,
+* C1 (a shared expert) batched against the reference's logits and tokens;
+* a model the batched path does not take (head width 160) still prefills,
   one step per token, with the same bits."""
 import json
 import os
@@ -23,7 +24,7 @@ import os
 import numpy as np
 import pytest
 
-from tests.test_hip_model import C2S, C3S, GOLD, greedy_tokens, needs_c2s, needs_c3s, prompt_tokens
+from tests.test_hip_model import C1, C2S, C3S, GOLD, greedy_tokens, needs_c1, needs_c2s, needs_c3s, prompt_tokens
 
 pytestmark = pytest.mark.gpu
 
@@ -138,10 +139,33 @@ def test_synth_long_context_chunks(hip):
     compare_models(BASE, 14, 8, True, 256, [1100], n_after=3, max_ctx=1200)
 
 
-def test_shared_expert_steps(hip):
-    """A shared expert: the batched path declines, the prompt still runs (one
+def test_shared_expert_batched(hip):
+    """A shared expert (the synthetic model's is of the experts' dtype, Q6_K):
+    batched, the same bits as the steps."""
+    compare_models(dict(BASE, n_shared=1, d_shared=256), 14, 8, True, 16, [45], n_after=3)
+
+
+def test_unsupported_width_steps(hip):
+    """Head width 160: the batched path declines, the prompt still runs (one
     step per token) with the same bits."""
-    compare_models(dict(BASE, n_shared=1, d_shared=256), 14, 8, True, 0, [20], n_after=2, batched=False)
+    compare_models(dict(BASE, head_dim=160, n_heads=8, n_kv_heads=2, d_model=512), 14, 8, True, 0, [20],
+                   n_after=2, batched=False)
+
+
+@needs_c1
+def test_c1_batched_prefill_reference_bits(hip):
+    """C1 (a shared expert, head width 64): the 64-token prompt batched, the
+    last position's top-10 logits the reference's and its 64 greedy tokens."""
+    from tierlm_amd.model import Model
+    m = Model(C1, max_ctx=256, prefill_chunk=24)
+    try:
+        assert m.prefill_batched()
+        lg = m.prefill(prompt_tokens())
+        assert_topk(lg, oracle_row("c1_oracle.jsonl", 63))
+        m.reset()
+        assert m.generate(prompt_tokens(), 64) == greedy_tokens()
+    finally:
+        m.close()
 
 
 @pytest.mark.parametrize("parts,max_ctx,n_after", [([1, 2, 1, 3], 320, 4), ([63, 1], 64, 0), ([29, 35], 64, 0)])

@@ -126,11 +126,22 @@ def test_prefill_routers_and_mask(hip, dev, router):
     assert not np.any(mask[ids])
 
 
+@pytest.mark.parametrize("sdt,gate", [(oracle.Q8_0, False), (oracle.Q6_K, True)])
+@pytest.mark.parametrize("T", [5, 70])
+def test_prefill_shared_expert(hip, dev, sdt, gate, T):
+    """A shared expert (C1's kind: Q8_0, or Q6_K with a sigmoid gate input)
+    beside the routed ones: its gate / up / down as token matmuls, added
+    after the routed sum in the decode block's order - every token's bits."""
+    case = build_moe_case(D=512, de=256, E=16, k=4, ds=256, expert_dt=oracle.Q6_K, shared_dt=sdt, seed=80 + T,
+                          device=dev, weights="random_codes", shared_gate=gate)
+    prefill_vs_decode(case, dev, T, seed=T)
+
+
 def test_prefill_rejects_unsupported(hip, dev):
     from tierlm_amd._lib import HipError
-    case = build_moe_case(D=256, de=256, E=8, k=2, ds=256, expert_dt=oracle.Q6_K, shared_dt=oracle.Q8_0, seed=1,
+    case = build_moe_case(D=256, de=256, E=8, k=2, ds=128, expert_dt=oracle.Q6_K, shared_dt=oracle.Q8_0, seed=1,
                           device=dev, weights="random_codes")
-    with pytest.raises(HipError):
+    with pytest.raises(HipError):   # a shared width that is not a multiple of 256
         case.block.prefill(torch.zeros((4, 256), device=dev))
     case = build_moe_case(D=256, de=256, E=8, k=2, ds=0, expert_dt=oracle.Q8_0, seed=1, device=dev,
                           weights="random_codes")

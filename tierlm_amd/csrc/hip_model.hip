@@ -1935,7 +1935,10 @@ bool pf_supported(const tlm_hip_model *M) {
     for (const Layer &Ly : M->L) {
         if (!pf_dense_ok(Ly.q) || !pf_dense_ok(Ly.k) || !pf_dense_ok(Ly.v) || !pf_dense_ok(Ly.o)) return false;
         const int edt = Ly.moe.expert_dt;
-        if ((edt != DT_Q4_K && edt != DT_Q5_K && edt != DT_Q6_K) || Ly.moe.ds > 0 || !Ly.moe.experts) return false;
+        if ((edt != DT_Q4_K && edt != DT_Q5_K && edt != DT_Q6_K) || !Ly.moe.experts) return false;
+        const int sdt = Ly.moe.shared_dt;
+        if (Ly.moe.ds > 0 && ((sdt != DT_Q4_K && sdt != DT_Q5_K && sdt != DT_Q6_K && sdt != DT_Q8_0) || Ly.moe.ds % 256))
+            return false;
     }
     return true;
 }

@@ -842,6 +842,9 @@ struct PfLayout {
     size_t hbuf;       /* f32 [T*k][de]: silu(g) * u per slot */
     size_t hq;         /* [T*k] split-layout Q8_K of hbuf rows, stride hq_stride */
     size_t out;        /* f32 [T*k][D]: down output per slot */
+    /* the shared expert (ds > 0): its activation per token (reference layout,
+     * xb's then h's), gate and up [T][ds], h [T][ds], down output [T][D], gate */
+    size_t sact, sg, su, sh, sout, sgate, sact_stride;   /* sact_stride: the larger token row */
     size_t tstride, hq_stride, total;
     int64_t T;
     int MT;
@@ -866,6 +869,15 @@ inline PfLayout pf_layout(const tlm_hip_moe_desc &d, int64_t T) {
     P.hbuf = o;     o += al256(pairs * d.de * 4);
     P.hq = o;       o += P.hq_stride * pairs;
     P.out = o;      o += al256(pairs * d.D * 4);
+    const size_t ds = d.ds > 0 ? (size_t)d.ds : 0, Ts = ds ? (size_t)T : 0;
+    const int sk = ds ? dt_act_kind(d.shared_dt) : DT_Q8_K;
+    P.sact_stride = ds ? act_bytes(sk, d.D > d.ds ? d.D : d.ds) : 0;
+    P.sact = o;     o += al256(Ts * P.sact_stride);
+    P.sg = o;       o += al256(Ts * ds * 4);
+    P.su = o;       o += al256(Ts * ds * 4);
+    P.sh = o;       o += al256(Ts * ds * 4);
+    P.sout = o;     o += al256(Ts * d.D * 4);
+    P.sgate = o;    o += al256(Ts * 4);
     P.total = o;
     return P;
 }
@@ -1235,7 +1247,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     }
 }
 
-/* h[t] += sum_r w_r * out[slot(t, r)] in rank order (src/lib/tlm_model.c:1029-1050). */
+/* The shared expert's h = silu(g) * u per (token, row) (tlm_model.c:171, 927,
+ * the decode gate/up tile's expression). */
+__global__ __launch_bounds__(256) void k_pf_swiglu(const float *__restrict__ g, const float *__restrict__ u,
+                                                   float *__restrict__ hs, int64_t n) {
+    for (int64_t i = threadIdx.x + (int64_t)blockIdx.x * 256; i < n; i += (int64_t)gridDim.x * 256) {
+        const float a = g[i];
+        hs[i] = a / (1.0f + expf_ref(-a)) * u[i];
+    }
+}
+
+/* The shared expert's gate per token (src/lib/tlm_model.c:1043-1046): the
+ * sigmoid of the sequential float dot of shared_gate_inp with xb, or 1 -
+ * the decode router launch's computation. */
+__global__ __launch_bounds__(64) void k_pf_sgate(tlm_hip_moe_desc d, WsLayout L, PfLayout P, uint8_t *ws) {
+    const int64_t t = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (t >= P.T) return;
+    float g = 1.0f;
+    if (d.shared_gate_inp) {
+        const float *xb = (const float *)(ws + P.tok + (size_t)t * P.tstride + L.xb);
+        const float *gi = (const float *)d.shared_gate_inp;
+        float acc = 0.0f;
+        for (int64_t i = 0; i < d.D; i++) acc += gi[i] * xb[i];
+        g = 1.0f / (1.0f + expf_ref(-acc));
+    }
+    ((float *)(ws + P.sgate))[t] = g;
+}
+
+/* h[t] += sum_r w_r * out[slot(t, r)] in rank order, then + sgate * the
+ * shared expert's output (src/lib/tlm_model.c:1029-1050). */
 __global__ __launch_bounds__(256) void k_pf_combine(tlm_hip_moe_desc d, PfLayout P, float *__restrict__ h,
                                                     uint8_t *ws) {
     args_now(d.D, d.k, P.pair_w, P.slot_of, P.out, h, ws);
@@ -1257,6 +1297,12 @@ __global__ __launch_bounds__(256) void k_pf_combine(tlm_hip_moe_desc d, PfLayout
     }
     GAS f32x4 *hp = (GAS f32x4 *)(h + (size_t)t * d.D) + r4;
     const f32x4 hv = *hp;
+    f32x4 sv = {0.0f, 0.0f, 0.0f, 0.0f};
+    float sg = 0.0f;
+    if (d.ds > 0) {
+        sv = *(const GAS f32x4 *)((const GAS float *)(ws + P.sout) + (size_t)t * d.D + 4 * r4);
+        sg = ((const GAS float *)(ws + P.sgate))[t];
+    }
     f32x4 o;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -1268,6 +1314,7 @@ __global__ __launch_bounds__(256) void k_pf_combine(tlm_hip_moe_desc d, PfLayout
                 ffn += x;
             }
         }
+        if (d.ds > 0) ffn += sg * sv[c];
         o[c] = hv[c] + ffn;
     }
     *hp = o;
@@ -1440,9 +1487,11 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
                        hipStream_t s) {
     if (int rc = moe_check(d, h, ws)) return rc;
     if (T <= 0 || T > 65536) return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld outside 1..65536", (long long)T);
-    if ((d->expert_dt != DT_Q4_K && d->expert_dt != DT_Q5_K && d->expert_dt != DT_Q6_K) || d->ds > 0)
-        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_prefill: routed Q4_K / Q5_K / Q6_K experts without a shared "
-                           "expert only (expert dtype %d, ds %lld)", d->expert_dt, (long long)d->ds);
+    if ((d->expert_dt != DT_Q4_K && d->expert_dt != DT_Q5_K && d->expert_dt != DT_Q6_K) ||
+        (d->ds > 0 && (!tokmm::tile_dt(d->shared_dt) || d->ds % 256 || d->D % 256)))
+        return tlmh_seterr(TLM_HIP_EUNSUP, "moe_prefill: routed Q4_K / Q5_K / Q6_K experts, a shared expert of "
+                           "Q4_K / Q5_K / Q6_K / Q8_0 and widths a multiple of 256 only (expert dtype %d, shared "
+                           "dtype %d, ds %lld)", d->expert_dt, d->shared_dt, (long long)d->ds);
     const tlm_hip_moe_desc dv = *d;
     const WsLayout L = ws_layout(*d);
     const PfLayout P = pf_layout(*d, T);
@@ -1454,6 +1503,27 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
                        w8);
     hipLaunchKernelGGL(k_pf_logits, dim3((unsigned)((d->E + PFL_ROWS - 1) / PFL_ROWS), (unsigned)((T + PFL_TOK - 1) / PFL_TOK)),
                        dim3(256), 0, s, dv, L, P, w8);
+    if (d->ds > 0) {   /* the shared expert of every token: its gate / up, SwiGLU, down and gate */
+        const int sk = dt_act_kind(d->shared_dt);
+        float *G = (float *)(w8 + P.sg), *U = (float *)(w8 + P.su), *Hs = (float *)(w8 + P.sh);
+        /* token rows of the activation as the token matmul reads them: act_bytes of the width */
+        int rc = launch_tok_norm_act(sk, (const float *)(w8 + P.tok + L.xb), (int64_t)(P.tstride / 4), nullptr, 0.0f,
+                                     d->D, T, w8 + P.sact, (int64_t)act_bytes(sk, d->D), s);
+        const void *Wgu[2] = {d->sg, d->su};
+        const int64_t Rgu[2] = {d->ds, d->ds};
+        float *const Ygu[2] = {G, U};
+        if (!rc) rc = launch_tokmm_segs(d->shared_dt, 2, Wgu, Rgu, d->D, w8 + P.sact, T, Ygu, s);
+        if (!rc) {
+            const int64_t n = T * d->ds;
+            hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, s, (const float *)G,
+                               (const float *)U, Hs, n);
+            rc = launch_tok_norm_act(sk, Hs, d->ds, nullptr, 0.0f, d->ds, T, w8 + P.sact, (int64_t)act_bytes(sk, d->ds),
+                                     s);
+        }
+        if (!rc) rc = launch_tokmm(d->shared_dt, d->sd, d->D, d->ds, w8 + P.sact, T, (float *)(w8 + P.sout), s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_pf_sgate, dim3((unsigned)((T + 63) / 64)), dim3(64), 0, s, dv, L, P, w8);
+    }
     hipLaunchKernelGGL(k_pf_route, dim3((unsigned)T), dim3(256), 0, s, dv, L, P, w8, ids, w);
     hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(256), 0, s, dv, P, w8);
     const dim3 ggu((unsigned)((d->de + 63) / 64), (unsigned)P.MT), gdn((unsigned)((d->D + 127) / 128), (unsigned)P.MT);
