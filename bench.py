@@ -314,7 +314,7 @@ def c5_bench(torch, dev, tokens, cache_gb, pool=64, gamma=0.14, seed=11):
                                               * plen * ntok / dt / 1e9, 2),
              "heat_top10pct_share": round(float(fs[:13].sum() / fs.sum()), 3)}
         st.close()
-        log(f"bench: C5 slot cache ({r['slots']} slots, {cap_gb:.0f} GB): {r['tok_s']:.2f} tok/s, "
+        log(f"bench: Qwen3-235B-A22B-shape MoE stack through the slot cache ({r['slots']} slots, {cap_gb:.0f} GB): {r['tok_s']:.2f} tok/s, "
             f"{r['misses_per_token']:.1f} misses/token (hit rate {r['hit_rate']:.3f}), {r['miss_GBps']:.1f} GB/s "
             f"of misses; lookahead {r['prefetch_issued_per_token']:.1f} loads/token "
             f"({r['prefetch_used_per_token']:.1f} used); all loads {r['load_GBps_with_prefetch']:.1f} GB/s over PCIe, "
@@ -362,7 +362,7 @@ def c1_bench(reps):
                                     "kind": "reference", "command": "tierlm bench --prompt-len 64 -n 64 --cache 1G"}
         except (IndexError, ValueError):
             out["reference_cpu"] = None
-    log(f"bench: C1 whole step: prefill {out['prefill_tok_s']:.0f} tok/s, decode {out['decode_tok_s']:.0f} tok/s "
+    log(f"bench: 4-layer synthetic store (D 512, 32 experts top-4), whole step: prefill {out['prefill_tok_s']:.0f} tok/s, decode {out['decode_tok_s']:.0f} tok/s "
         f"({out['decode_us_per_token']:.1f} us/token); reference CPU {out.get('reference_cpu')}")
     return out
 
@@ -500,7 +500,7 @@ def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gam
          "load_GBps": round((miss + pre) * plen * tokens / dt / 1e9, 2), "build_s": round(built, 1),
          "timing": "host wall clock around tlm_hip_model_decode of the timed tokens and a sync, after the prompt and "
                    "the warm-up tokens"}
-    log(f"bench: C5 whole model ({r['slots']} slots, {cache_gb:.0f} GB): {r['tok_s']:.2f} tok/s "
+    log(f"bench: Qwen3-235B-A22B-shape whole model through the slot cache ({r['slots']} slots, {cache_gb:.0f} GB): {r['tok_s']:.2f} tok/s "
         f"({r['ms_per_token']:.2f} ms/token), {r['misses_per_token']:.2f} misses/token (hit rate {r['hit_rate']:.4f}), "
         f"{r['prefetch_issued_per_token']:.1f} lookahead loads/token, {r['load_GBps']:.2f} GB/s over PCIe")
     return r
@@ -795,13 +795,13 @@ def main():
             c5 = c5_bench(torch, dev, args.c5_tokens, args.c5_cache_gb)
         except Exception as e:                 # recorded, so the rest of the line still prints
             c5 = {"error": repr(e)}
-            log(f"bench: C5 slot cache failed: {e!r}")
+            log(f"bench: Qwen3-235B-A22B-shape slot-cache stack failed: {e!r}")
         torch.cuda.empty_cache()
         try:
             c5m = c5_model_bench(torch, args.c5_tokens, args.c5_cache_gb)
         except Exception as e:
             c5m = {"error": repr(e)}
-            log(f"bench: C5 whole model failed: {e!r}")
+            log(f"bench: Qwen3-235B-A22B-shape whole model failed: {e!r}")
         torch.cuda.empty_cache()
 
     cpu = None
