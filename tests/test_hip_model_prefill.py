@@ -194,3 +194,30 @@ def test_prefill_errors(hip):
         assert np.isfinite(lg).all() and m.kv_len() == 32
     finally:
         m.close()
+
+
+def test_synth_prompt_past_2048(hip):
+    """A 2400-token prompt at capacity 2600: the softmax's second round of 2048
+    positions per thread set, P.V chunks past position 2048."""
+    compare_models(BASE, 12, 8, True, 512, [2400], n_after=3, max_ctx=2600)
+
+
+@needs_c3s
+@pytest.mark.parametrize("chunk", [0, -1])
+def test_c3s_past_2048_reference_tokens(hip, chunk):
+    """Past 2048 positions (tests/golden/make_c3s_long_golden.sh: a 2300-token
+    prompt, the reference's 48 greedy tokens), batched and stepped."""
+    from tierlm_amd.model import Model
+    m = Model(C3S, max_ctx=4096, prefill_chunk=chunk)
+    try:
+        assert m.prefill_batched() == (chunk == 0)
+        assert m.generate(prompt_tokens(2048, 2300), 48) == greedy_tokens("c3s_long_greedy.txt")
+    finally:
+        m.close()
+
+
+def test_synth_prompt_past_4096(hip):
+    """A 4400-token prompt at capacity 4600: the stepped decode's probabilities
+    in two LDS segments (past 4096 positions) and the batched softmax's third
+    round, bit for bit."""
+    compare_models(dict(BASE, max_ctx=8192), 13, 8, True, 512, [4400], n_after=3, max_ctx=4600)

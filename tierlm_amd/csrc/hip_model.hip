@@ -435,8 +435,12 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
         const int se = min(T, sb + ATT_PSEG);
         if (nseg == 1) {   /* each thread scales the terms it stored: p = e * inv */
             for (int t = tid; t < T; t += NT) s_p[t] = s_p[t] * inv_s;
-        } else {
-            for (int t = sb + tid; t < se; t += NT) s_p[t - sb] = expf_ref_with(S[t] - mx, tab) * inv_s;
+        } else {   /* every lane through every pass: e^x reads its table from the other lanes */
+            for (int t0 = sb; t0 < se; t0 += NT) {
+                const int t = t0 + tid;
+                const float p = expf_ref_with(S[min(t, se - 1)] - mx, tab) * inv_s;
+                if (t < se) s_p[t - sb] = p;
+            }
         }
         const int nbk = (se - sb + ATT_BT * 4 - 1) / (ATT_BT * 4);   /* blocks of the segment */
         const int q0 = sb >> 2;   /* the segment's first tile */
@@ -1062,8 +1066,12 @@ __global__ __launch_bounds__(NT) void k_pf_softmax(float *__restrict__ scores, i
 #pragma unroll
         for (int k = 0; k < PB; k++)
             if (tid + NT * k < T) S[tid + NT * k] = e[k] * inv_s;
-    } else {
-        for (int t = tid; t < T; t += NT) S[t] = expf_ref_with(S[t] - mx, tab) * inv_s;
+    } else {   /* every lane through every pass: e^x reads its table from the other lanes */
+        for (int t0 = 0; t0 < T; t0 += NT) {
+            const int t = t0 + tid;
+            const float p = expf_ref_with(S[min(t, T - 1)] - mx, tab) * inv_s;
+            if (t < T) S[t] = p;
+        }
     }
 }
 
