@@ -420,7 +420,7 @@ def c3_bench(torch, steps, warmup, ctx, split=False):
         ev1.synchronize()
         ev_s = ev0.elapsed_time(ev1) * 1e-3
         # batched prefill of a (ctx - 1)-token prompt (tlm_model_prefill's
-        # result, 512-token chunks): first run allocates, best of the next two
+        # result, 1024-token chunks): first run allocates, best of the next two
         pf_prompt = bench_prompt(ctx - 1, QWEN3_30B_A3B["vocab"], seed=7)
         pf = []
         for _ in range(3):

@@ -466,7 +466,8 @@ typedef struct {
      * (a shared expert of those dtypes or Q8_0, width a multiple of 256), head
      * width 32 / 64 / 96 / 128, the reference's
      * attention order (attn_split 0) - in chunks sized to the context
-     * capacity (at most 512 tokens); n > 0: chunks of at most n tokens; < 0:
+     * capacity (at most 1024 tokens); n > 0: chunks of at most n tokens (also
+     * bounded by 256 MB of score rows at the context capacity); < 0:
      * one step per token.  A batched chunk runs each layer once for all of
      * its tokens (int8 MFMA token matmuls, the batched MoE block, causal
      * attention over the cache) with each token's result bit for bit the

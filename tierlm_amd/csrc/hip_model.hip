@@ -1952,15 +1952,16 @@ bool pf_supported(const tlm_hip_model *M) {
 }
 
 /* the chunk's buffers: pf_cap tokens, score rows for the whole capacity
- * (at most 256 MB of scores, the chunk a multiple of 4, at most 512) */
+ * (at most 256 MB of scores, the chunk a multiple of 4, by default at most
+ * 1024: 2047 tokens in 122 ms against 130 in chunks of 512) */
 int pf_alloc(tlm_hip_model *M) {
     if (M->pf_cap) return TLM_HIP_OK;
     const tlm_hip_model_geom &g = M->g;
     const int64_t D = g.d_model, HQ = (int64_t)g.n_heads * g.head_dim, KVD = (int64_t)g.n_kv_heads * g.head_dim;
     const int sl = (M->max_ctx + 3) & ~3;
     int64_t cap = ((int64_t)256 << 20) / ((int64_t)g.n_heads * sl * 4);
-    cap = cap > 512 ? 512 : cap;
-    if (M->pf_chunk > 0 && cap > M->pf_chunk) cap = M->pf_chunk;
+    const int64_t want = M->pf_chunk > 0 ? M->pf_chunk : 1024;
+    cap = cap > want ? want : cap;
     cap = cap >= 4 ? cap & ~3 : cap < 1 ? 1 : cap;
     size_t ws = 0;
     for (const Layer &Ly : M->L) {
