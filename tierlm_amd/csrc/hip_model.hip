@@ -2015,8 +2015,14 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
     hipStream_t s = M->stream;
     int rc = TLM_HIP_OK;
     int nt = 0;
-    for (int c0 = 0; c0 < n && !rc; c0 += M->pf_cap) {
-        nt = n - c0 < M->pf_cap ? n - c0 : M->pf_cap;
+    /* chunks of equal length (a multiple of 4 up to the buffers' pf_cap): a
+     * short last chunk would run its long causal chains on a few groups */
+    const int nch = (n + M->pf_cap - 1) / M->pf_cap;
+    int per = (n + nch - 1) / nch;
+    per = (per + 3) & ~3;
+    per = per > M->pf_cap ? M->pf_cap : per;
+    for (int c0 = 0; c0 < n && !rc; c0 += per) {
+        nt = n - c0 < per ? n - c0 : per;
         const int pc = p0 + c0;
         hipLaunchKernelGGL(k_pf_embed, dim3((D + NT - 1) / NT, nt), dim3(NT), 0, s, M->embd, M->embd_row, M->embd_dt,
                            (const int32_t *)M->seq + pc, D, M->pf_h);
