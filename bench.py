@@ -400,8 +400,8 @@ def c3_bench(torch, steps, warmup, ctx, split=False):
         fill_s = time.perf_counter() - t0
         top = ctx - 1
         assert m.kv_len() == top
-        span = top - 64 + 1
-        positions = [top - (i * span) // steps for i in range(steps)]   # descending, evenly over 64..top
+        # descending, evenly over 64..top, both ends included
+        positions = [top - (i * (top - 64)) // (steps - 1) for i in range(steps)] if steps > 1 else [top]
         w = max(1, warmup)
         m.rewind(top - w)
         m.decode(w)                                  # warm-up steps (untimed), back at top positions
@@ -450,6 +450,8 @@ def c3_bench(torch, steps, warmup, ctx, split=False):
             "build_s": built, "fill_tok_s": (ctx - 64) / fill_s, "tokens_head": toks[:4], "geometry_bytes": gb}
 
 
+# the Qwen3-235B-A22B geometry with sigmoid routing, whose selection bias
+# gives the experts a Zipf-like heat (the slot-cache legs)
 QWEN3_235B_A22B = dict(n_layers=94, d_model=4096, n_heads=64, n_kv_heads=4, head_dim=128, vocab=151936,
                       n_experts=128, top_k=8, d_expert=1536, n_shared=0, d_shared=0, max_ctx=40960, router=2,
                       rope_theta=1e6, norm_eps=1e-6, routed_scale=1.0)
@@ -504,6 +506,68 @@ def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gam
         f"({r['ms_per_token']:.2f} ms/token), {r['misses_per_token']:.2f} misses/token (hit rate {r['hit_rate']:.4f}), "
         f"{r['prefetch_issued_per_token']:.1f} lookahead loads/token, {r['load_GBps']:.2f} GB/s over PCIe")
     return r
+
+
+def host_cores():
+    """Physical cores of the host and of this process's CPU set (distinct
+    (package, core) pairs), and the thread count the CPU baseline uses: every
+    physical core of the CPU set, at most 16 (the CPU share a one-GPU job
+    has on the GPU hosts)."""
+    def core_of(c):
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                core = f.read().strip()
+            return (pkg, core)
+        except OSError:
+            return ("?", str(c))
+    online = [int(d[3:]) for d in os.listdir("/sys/devices/system/cpu") if d[3:].isdigit()]
+    mine = sorted(os.sched_getaffinity(0))
+    phys_host = len({core_of(c) for c in online}) or (os.cpu_count() or 1)
+    phys_mine = len({core_of(c) for c in mine}) or len(mine)
+    threads = max(1, min(16, phys_mine))
+    return {"host_physical_cores": phys_host, "host_logical_cpus": len(online), "process_cpus": len(mine),
+            "process_physical_cores": phys_mine, "threads": threads,
+            "note": (f"{phys_mine} physical cores in this process's CPU set of {len(mine)} CPUs "
+                     f"(host: {phys_host} physical cores, {len(online)} logical CPUs)"
+                     + ("; capped at the 16-CPU share of a one-GPU job" if phys_mine > 16 else ""))}
+
+
+def q6k_kernel_gbps(seconds=0.5):
+    """The reference's own single-thread kernel figure (tests/test_quant.c:
+    897-938): tlm_matvec_rows of a 4096 x 4096 Q6_K matrix against a Q8_K
+    activation, weight bytes / best time (a 13.8 MB matrix may sit in a large
+    last-level cache: a kernel, not a memory, figure)."""
+    import ctypes as C
+
+    import numpy as np
+
+    import oracle
+    from tests.synth import random_code_rows
+    rng = np.random.default_rng(5)
+    W = random_code_rows(rng, Q6_K, 4096, 4096)
+    x = rng.standard_normal(4096).astype(np.float32)
+    y = np.empty(4096, np.float32)
+    handle = oracle.ref.refmoe_new(1)
+    try:
+        Wp = (C.c_void_p * 1)(W.ctypes.data)
+        R = (C.c_int64 * 1)(4096)
+        Y = (C.c_void_p * 1)(y.ctypes.data)
+        oracle.ref.refmoe_matvecs(handle, Q6_K, Wp, R, 4096, x.ctypes.data, Y, 1)   # warm
+        best, spent, it = 1e30, 0.0, 0
+        while (spent < seconds and it < 400) or it < 2:
+            t0 = time.perf_counter()
+            oracle.ref.refmoe_matvecs(handle, Q6_K, Wp, R, 4096, x.ctypes.data, Y, 1)
+            dt = time.perf_counter() - t0
+            best = min(best, dt)
+            spent += dt
+            it += 1
+    finally:
+        oracle.ref.refmoe_free(handle)
+    return {"GBps": round(W.nbytes / best / 1e9, 2), "tier": oracle.ref.refmoe_tier().decode(), "runs": it,
+            "note": "tlm_matvec_rows, one thread, best of the runs; the activation quantised inside each run"}
 
 
 def cpu_baseline(args, threads):
@@ -666,12 +730,19 @@ def expert_gemv_bench(torch, dev, args, gen):
     expert_gbs = TOKEN_BYTES / ((p2 + p3) * 1e-6) / 1e9
     log(f"bench: MoE block {1e6 / block_us:.0f} tok/s ({block_us:.2f} us/token); per launch: router {p1:.2f} us, "
         f"gate/up {p2:.2f} us ({gu_gbs:.0f} GB/s), down+combine {p3:.2f} us ({dn_gbs:.0f} GB/s)")
+    block_gbs = TOKEN_BYTES / (block_us * 1e-6) / 1e9
     out = {"workload": "one routed MoE block per token at Qwen3-30B-A3B shape (D 2048, 128 experts top-8 "
-                       "softmax+renorm, expert width 768, Q6_K random-code experts, f32 router), "
-                       f"{L} resident layer copies cycled", "block_tok_s": round(1e6 / block_us, 1),
+                       "softmax+renorm, expert width 768, Q6_K experts, f32 router), "
+                       f"{L} resident layer copies cycled; {ntok} timed tokens of N(0,1) residuals (seeded); "
+                       "the experts are random 6-bit codes with scales of N(0,0.02)-quantised magnitude, not "
+                       "quantised N(0,0.02) draws (the kernels' speed does not depend on the values)",
+           "block_tok_s": round(1e6 / block_us, 1),
            "block_us_per_token": round(block_us, 3), "tokens": ntok,
            "expert_bytes_per_token": TOKEN_BYTES, "expert_gemv_GBps": round(expert_gbs, 1),
            "expert_gemv_frac": round(expert_gbs / HBM_PEAK_GBS, 4),
+           "block_GBps": round(block_gbs, 1), "block_frac": round(block_gbs / HBM_PEAK_GBS, 4),
+           "frac_note": "expert_gemv_frac: expert bytes / (gate/up + down launch times); block_frac: expert bytes "
+                        "/ the whole block's time per token (router, routing and launch gaps included)",
            "gateup": {"kernel": "k_moe_gateup (routing + gate/up of the top-8 experts + SwiGLU)",
                       "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(p2, 3),
                       "achieved_GBps": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
@@ -721,7 +792,7 @@ def main():
     ap.add_argument("--split-steps", type=int, default=248,
                     help="steps of the same sweep with the split attention option (0: skip)")
     ap.add_argument("--layers", type=int, default=48, help="MoE block: distinct layer copies cycled by the tokens")
-    ap.add_argument("--c2-tokens", type=int, default=2000, help="MoE block: timed tokens")
+    ap.add_argument("--c2-tokens", type=int, default=10000, help="MoE block: timed tokens")
     ap.add_argument("--graph", type=int, default=100, help="MoE block: tokens per captured HIP graph")
     ap.add_argument("--roofline-tokens", type=int, default=960, help="MoE block: launches per phase graph")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -806,11 +877,18 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"bench: cpu baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
+        cores = host_cores()
+        threads = cores["threads"]
+        log(f"bench: cpu baseline ({threads} threads: {cores['note']}; ~{args.cpu_seconds:.0f} s), then 1 thread")
         cpu = cpu_baseline(args, threads)
-        if cpu and c3:
-            cpu["gpu_over_cpu"] = round(c3["tok_s"] / cpu["value"], 1)
+        if cpu:
+            cpu["host_cores"] = cores
+            one = cpu_baseline(args, 1)
+            cpu["one_thread"] = {k: one[k] for k in ("value", "unit", "cores", "layer_ms", "lm_head_ms")}
+            cpu["q6_k_4096x4096_1thread"] = q6k_kernel_gbps()
+            if c3:
+                cpu["gpu_over_cpu"] = round(c3["tok_s"] / cpu["value"], 1)
+                cpu["gpu_over_cpu_1thread"] = round(c3["tok_s"] / one["value"], 1)
     if c3 is None:   # --no-c3: the other legs only
         print(json.dumps({"metric": "decode tok/s batch-1, Qwen3-30B-A3B shape; expert GEMV HBM GB/s vs peak",
                           "value": None, "unit": "tok/s", "n_gpus": 1, "note": "--no-c3: whole-model legs skipped",

@@ -27,8 +27,17 @@ Checks:
   1e6 - with 16 experts top-8, over 2047 positions (a 1920-token prompt and
   the first 127 greedy tokens) at context capacities 2048 and 4096, and the
   reference's 128 greedy tokens after the prompt;
+* C5S (oracle/make_c5s.sh, tests/golden/make_c5s_golden.sh): the attention
+  grouping of Qwen3-235B-A22B - 16 query heads per key head of width 128
+  (32 / 2 heads at D 2048), qk-norm - with 16 Q4_K experts top-8, over 1163
+  positions (a 1100-token prompt and the first 63 greedy tokens), and the
+  reference's 64 greedy tokens after the prompt;
 * the split attention option (attn_split) on the three: the reference's
-  greedy tokens, its top-1 at 99% or more of the teacher-forced positions."""
+  greedy tokens, its top-1 at 99% or more of the teacher-forced positions;
+* the full Qwen3-235B-A22B geometry (D 4096, 64 / 4 heads x 128, 128 Q4_K
+  experts top-8 of 1536, vocabulary 151936) as a 2-layer random-init model:
+  graph replays equal eager launches, the lm_head's greedy token is the
+  first maximum of its logits."""
 import json
 import os
 
@@ -41,10 +50,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 C1 = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
 C2S = os.path.join(ROOT, "oracle", "_ref", "c2s", "c2s.tlmm")
 C3S = os.path.join(ROOT, "oracle", "_ref", "c3s", "c3s.tlmm")
+C5S = os.path.join(ROOT, "oracle", "_ref", "c5s", "c5s.tlmm")
 GOLD = os.path.join(ROOT, "tests", "golden")
 needs_c1 = pytest.mark.skipif(not os.path.exists(C1), reason="oracle/_ref/c1 not built (oracle/make_c1.sh)")
 needs_c2s = pytest.mark.skipif(not os.path.exists(C2S), reason="oracle/_ref/c2s not built (oracle/make_c2s.sh)")
 needs_c3s = pytest.mark.skipif(not os.path.exists(C3S), reason="oracle/_ref/c3s not built (oracle/make_c3s.sh)")
+needs_c5s = pytest.mark.skipif(not os.path.exists(C5S), reason="oracle/_ref/c5s not built (oracle/make_c5s.sh)")
 
 
 def prompt_tokens(vocab=4096, n=64):
@@ -162,6 +173,30 @@ def test_c3s_long_context_head_width_128(hip, max_ctx, slices):
         m.reset()
         assert m.generate(prompt, 128) == gen
         assert m.kv_len() == 1920 + 127
+    finally:
+        m.close()
+
+
+@needs_c5s
+@pytest.mark.parametrize("max_ctx,slices", [(1200, 0), (4096, 2)])
+def test_c5s_sixteen_query_heads_per_key_head(hip, max_ctx, slices):
+    """Qwen3-235B-A22B's attention grouping (16 query heads per key head,
+    width 128) over 1163 positions: every position's top-10 logits
+    teacher-forced, then the reference's 64 greedy tokens after the
+    1100-token prompt."""
+    from tierlm_amd.model import Model
+    m = Model(C5S, max_ctx=max_ctx, attn_slices=slices)
+    try:
+        g = m.geom
+        assert (g.d_model, g.n_heads, g.n_kv_heads, g.head_dim, g.n_experts, g.top_k, g.n_shared, g.vocab) == \
+            (2048, 32, 2, 128, 16, 8, 0, 2048)
+        gen = greedy_tokens("c5s_greedy.txt")
+        assert len(gen) == 64
+        prompt = prompt_tokens(2048, 1100)
+        exact, total, worst = teacher_forced(m, "c5s_oracle.jsonl", prompt + gen[:63])
+        assert total == 1163 * 10
+        m.reset()
+        assert m.generate(prompt, 64) == gen
     finally:
         m.close()
 
@@ -315,6 +350,31 @@ def test_synth_qwen3_30b_a3b_shape(hip):
             la, na = a.step(t)
             lb, nb = b.step(t)
             assert np.isfinite(la).all() and na == nb and np.array_equal(la.view(np.uint32), lb.view(np.uint32)), pos
+    finally:
+        a.close()
+        b.close()
+
+
+def test_synth_qwen3_235b_a22b_geometry(hip):
+    """Two layers of the Qwen3-235B-A22B geometry (hidden 4096, 64 / 4 heads
+    x 128 with qk-norm, 128 Q4_K experts top-8 of 1536, Q8_0 dense and
+    lm_head, vocabulary 151936): over 40 positions the graph replays give the
+    eager launches' bits, logits are finite and the greedy token is the first
+    maximum of the downloaded logits (the lm_head's per-tile keys and the
+    argmax launch against numpy)."""
+    from tierlm_amd.model import QWEN3_235B_A22B, Model, bench_prompt
+    g = dict(QWEN3_235B_A22B, n_layers=2)
+    a = Model.synth(g, expert_dt=12, seed=5, max_ctx=64)
+    b = Model.synth(g, expert_dt=12, seed=5, max_ctx=64, eager=True)
+    try:
+        assert (a.geom.d_model, a.geom.n_heads, a.geom.n_kv_heads, a.geom.head_dim, a.geom.vocab) == \
+            (4096, 64, 4, 128, 151936)
+        for pos, t in enumerate(bench_prompt(40, g["vocab"], seed=9)):
+            la, na = a.step(t)
+            lb, nb = b.step(t)
+            assert np.isfinite(la).all(), pos
+            assert na == nb and np.array_equal(la.view(np.uint32), lb.view(np.uint32)), pos
+            assert na == int(np.argmax(la)), pos
     finally:
         a.close()
         b.close()

@@ -18,8 +18,8 @@ that reads slots carries the resident block's bits, so:
 import numpy as np
 import pytest
 
-from tests.test_hip_model import C1, C2S, C3S, greedy_tokens, needs_c1, needs_c2s, needs_c3s, prompt_tokens, \
-    teacher_forced
+from tests.test_hip_model import C1, C2S, C3S, C5S, greedy_tokens, needs_c1, needs_c2s, needs_c3s, needs_c5s, \
+    prompt_tokens, teacher_forced
 
 pytestmark = pytest.mark.gpu
 
@@ -78,6 +78,48 @@ def test_c3s_cached_reference_bits(hip):
         assert m.generate(prompt, 128) == gen
     finally:
         m.close()
+
+
+@needs_c5s
+def test_c5s_cached_reference_bits(hip):
+    """16 query heads per key head, 16 Q4_K experts top-8 through 8 slots,
+    over the fixture's 1163 positions."""
+    from tierlm_amd.model import Model
+    m = Model(C5S, max_ctx=1200, expert_cache=TINY)
+    try:
+        assert m.store_stats()["slots"] == 8
+        gen = greedy_tokens("c5s_greedy.txt")
+        prompt = prompt_tokens(2048, 1100)
+        teacher_forced(m, "c5s_oracle.jsonl", prompt + gen[:63])
+        m.reset()
+        assert m.generate(prompt, 64) == gen
+        assert m.store_stats()["evictions"] > 0
+    finally:
+        m.close()
+
+
+def test_synth_qwen3_235b_a22b_cached_equals_resident(hip):
+    """Two layers of the full Qwen3-235B-A22B geometry (hidden 4096, 64 / 4
+    heads x 128, 128 Q4_K experts top-8 of 1536, vocabulary 151936), the
+    experts resident and behind a cache of top_k slots of 10.6 MB: every
+    step's logits and routing bit for bit."""
+    from tierlm_amd.model import QWEN3_235B_A22B, Model, bench_prompt
+    g = dict(QWEN3_235B_A22B, n_layers=2)
+    a = Model.synth(g, expert_dt=12, seed=5, max_ctx=48)
+    b = Model.synth(g, expert_dt=12, seed=5, max_ctx=48, expert_cache=TINY)
+    try:
+        assert b.store_stats()["slots"] == 8
+        for pos, t in enumerate(bench_prompt(16, g["vocab"], seed=9)):
+            la, na = a.step(t)
+            lb, nb = b.step(t)
+            assert na == nb and np.array_equal(la.view(np.uint32), lb.view(np.uint32)), pos
+            ia, wa = a.routes()
+            ib, wb = b.routes()
+            assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32)), pos
+        assert b.store_stats()["evictions"] > 0
+    finally:
+        a.close()
+        b.close()
 
 
 SMALL = dict(n_layers=3, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, vocab=4096, n_experts=32, top_k=4,

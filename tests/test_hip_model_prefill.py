@@ -24,7 +24,8 @@ import os
 import numpy as np
 import pytest
 
-from tests.test_hip_model import C1, C2S, C3S, GOLD, greedy_tokens, needs_c1, needs_c2s, needs_c3s, prompt_tokens
+from tests.test_hip_model import C1, C2S, C3S, C5S, GOLD, greedy_tokens, needs_c1, needs_c2s, needs_c3s, needs_c5s, \
+    prompt_tokens
 
 pytestmark = pytest.mark.gpu
 
@@ -51,9 +52,10 @@ def bits_equal(a, b):
 @needs_c3s
 @pytest.mark.parametrize("chunk", [0, 200])
 def test_c3s_batched_prefill_reference_bits(hip, chunk):
-    """1920-token prompt in chunks of the automatic size (512) and of 200
-    (ragged: 9 full chunks and one of 120): the last position's top-10 logits
-    are the reference's, then its 128 greedy tokens."""
+    """1920-token prompt in chunks of the automatic size (at most 1024
+    tokens, equal lengths: two chunks of 960) and of 200 (ragged: 9 full
+    chunks and one of 120): the last position's top-10 logits are the
+    reference's, then its 128 greedy tokens."""
     from tierlm_amd.model import Model
     m = Model(C3S, max_ctx=2048, prefill_chunk=chunk)
     try:
@@ -63,6 +65,24 @@ def test_c3s_batched_prefill_reference_bits(hip, chunk):
         assert_topk(lg, oracle_row("c3s_oracle.jsonl", len(prompt) - 1))
         m.reset()
         assert m.generate(prompt, 128) == greedy_tokens("c3s_greedy.txt")
+    finally:
+        m.close()
+
+
+@needs_c5s
+def test_c5s_batched_prefill_reference_bits(hip):
+    """16 query heads per key head: the 1100-token prompt batched (chunks of
+    at most 1024, equal lengths: 552 + 548) gives the reference's top-10
+    logits at its last position bit for bit, then its 64 greedy tokens."""
+    from tierlm_amd.model import Model
+    m = Model(C5S, max_ctx=1200)
+    try:
+        assert m.prefill_batched()
+        prompt = prompt_tokens(2048, 1100)
+        lg = m.prefill(prompt)
+        assert_topk(lg, oracle_row("c5s_oracle.jsonl", len(prompt) - 1))
+        m.reset()
+        assert m.generate(prompt, 64) == greedy_tokens("c5s_greedy.txt")
     finally:
         m.close()
 
@@ -221,3 +241,10 @@ def test_synth_prompt_past_4096(hip):
     in two LDS segments (past 4096 positions) and the batched softmax's third
     round, bit for bit."""
     compare_models(dict(BASE, max_ctx=8192), 13, 8, True, 512, [4400], n_after=3, max_ctx=4600)
+
+
+def test_synth_full_1024_chunk(hip):
+    """An explicit chunk of 1024 on a 1025-token prompt: the prompt splits
+    into two chunks of near-equal length (neither a multiple of the other),
+    each token the step's bits."""
+    compare_models(BASE, 14, 8, True, 1024, [1025], n_after=3, max_ctx=1040)

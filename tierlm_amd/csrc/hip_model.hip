@@ -1334,6 +1334,17 @@ struct tlm_hip_model {
         allocs.push_back(p);
         return p;
     }
+    /* frees an allocation of dalloc now (nullptr: nothing) */
+    void dfree(void *p) {
+        if (!p) return;
+        for (size_t i = 0; i < allocs.size(); i++)
+            if (allocs[i] == p) {
+                (void)hipFree(p);
+                allocs[i] = allocs.back();
+                allocs.pop_back();
+                return;
+            }
+    }
     ~tlm_hip_model() {
         if (stream) (void)hipStreamSynchronize(stream);
         if (xs) tlm_hip_store_close(xs);   /* waits for its loads, which read the payloads */
@@ -1952,8 +1963,10 @@ bool pf_supported(const tlm_hip_model *M) {
 }
 
 /* the chunk's buffers: pf_cap tokens, score rows for the whole capacity
- * (at most 256 MB of scores, the chunk a multiple of 4, by default at most
- * 1024: 2047 tokens in 122 ms against 130 in chunks of 512) */
+ * (at most 256 MB of scores, no more tokens than the context holds, the
+ * chunk a multiple of 4, by default at most 1024: 2047 tokens in 122 ms
+ * against 130 in chunks of 512).  On a failed allocation the buffers this
+ * call did get are freed again. */
 int pf_alloc(tlm_hip_model *M) {
     if (M->pf_cap) return TLM_HIP_OK;
     const tlm_hip_model_geom &g = M->g;
@@ -1962,6 +1975,7 @@ int pf_alloc(tlm_hip_model *M) {
     int64_t cap = ((int64_t)256 << 20) / ((int64_t)g.n_heads * sl * 4);
     const int64_t want = M->pf_chunk > 0 ? M->pf_chunk : 1024;
     cap = cap > want ? want : cap;
+    cap = cap > sl ? sl : cap;   /* a chunk never holds more tokens than the capacity */
     cap = cap >= 4 ? cap & ~3 : cap < 1 ? 1 : cap;
     size_t ws = 0;
     for (const Layer &Ly : M->L) {
@@ -1982,6 +1996,12 @@ int pf_alloc(tlm_hip_model *M) {
     M->pf_w = (float *)M->dalloc((size_t)cap * g.top_k * 4);
     if (!M->pf_h || !M->pf_q || !M->pf_kx || !M->pf_vx || !M->pf_att || !M->pf_y || !M->pf_scores || !M->pf_act ||
         !M->pf_ws || !M->pf_ids || !M->pf_w) {
+        for (void **p : {(void **)&M->pf_h, (void **)&M->pf_q, (void **)&M->pf_kx, (void **)&M->pf_vx,
+                         (void **)&M->pf_att, (void **)&M->pf_y, (void **)&M->pf_scores, (void **)&M->pf_act,
+                         (void **)&M->pf_ws, (void **)&M->pf_ids, (void **)&M->pf_w}) {
+            M->dfree(*p);
+            *p = nullptr;
+        }
         M->pf_nomem = true;
         return tlmh_seterr(TLM_HIP_ENOMEM, "model prefill: out of device memory (%lld-token chunks)", (long long)cap);
     }

@@ -639,7 +639,7 @@ static void settle_slot(tlm_hip_store *s, std::unique_lock<std::mutex> &lk, int 
 }
 
 int tlm_hip_store_warm(tlm_hip_store *s) {
-    if (!s) return tlmh_seterr(TLM_HIP_EINVAL, "store warm: NULL");
+    if (!s) return tlmh_seterr(TLM_HIP_EINVAL, "store warm: no store given");
     const int budget = s->n_slots ? pin_budget(s) : 0;
     if (budget <= 0) return TLM_HIP_OK;
     std::unique_lock<std::mutex> lk(s->mu);
@@ -678,7 +678,8 @@ int tlm_hip_store_warm(tlm_hip_store *s) {
  * misses in rank order take victims and start loading (an id repeated in the
  * step finds the slot its first occurrence took). */
 int tlm_hip_store_acquire(tlm_hip_store *s, int layer, const int *ids, int k, tlm_hip_expert_ref *out) {
-    if (!s || k < 0 || (k > 0 && (!ids || !out))) return tlmh_seterr(TLM_HIP_EINVAL, "store acquire: bad arguments");
+    if (!s || k < 0 || (k > 0 && (!ids || !out)))
+        return tlmh_seterr(TLM_HIP_EINVAL, "store acquire: no store, or a negative count, or no ids / output");
     std::unique_lock<std::mutex> lk(s->mu);
     s->refresh_all();
     const uint64_t stamp = ++s->clock;
@@ -733,8 +734,8 @@ static int wait_status(tlm_hip_store *s, int v) {
 
 /* tlm_store.c:642-671: blocks the host until the slot is READY */
 int tlm_hip_store_wait(tlm_hip_store *s, tlm_hip_expert_ref *ref) {
-    if (!s || !ref) return tlmh_seterr(TLM_HIP_EINVAL, "store wait: NULL argument");
-    if (ref->slot < 0 || ref->slot >= s->n_slots) return tlmh_seterr(TLM_HIP_EINVAL, "store wait: expert was not acquired");
+    if (!s || !ref) return tlmh_seterr(TLM_HIP_EINVAL, "store wait: no store or slot given");
+    if (ref->slot < 0 || ref->slot >= s->n_slots) return tlmh_seterr(TLM_HIP_EINVAL, "store wait: the slot holds no acquired expert");
     const int v = ref->slot;
     std::unique_lock<std::mutex> lk(s->mu);
     int64_t t0 = 0;
@@ -759,9 +760,9 @@ int tlm_hip_store_wait(tlm_hip_store *s, tlm_hip_expert_ref *ref) {
 /* The device-side wait: work enqueued on `stream` after this call runs after
  * the slot's load.  The host blocks only until the load has been submitted. */
 int tlm_hip_store_stream_wait(tlm_hip_store *s, const tlm_hip_expert_ref *ref, void *stream) {
-    if (!s || !ref) return tlmh_seterr(TLM_HIP_EINVAL, "store stream wait: NULL argument");
+    if (!s || !ref) return tlmh_seterr(TLM_HIP_EINVAL, "store stream wait: no store or slot given");
     if (ref->slot < 0 || ref->slot >= s->n_slots)
-        return tlmh_seterr(TLM_HIP_EINVAL, "store stream wait: expert was not acquired");
+        return tlmh_seterr(TLM_HIP_EINVAL, "store stream wait: the slot holds no acquired expert");
     const int v = ref->slot;
     std::unique_lock<std::mutex> lk(s->mu);
     Slot &sl = s->sl[v];

@@ -403,7 +403,7 @@ const char *tlm_hip_manifest_drive_path(const tlm_hip_manifest *m, int i) {
  * primary copy the replica is read and checked the same way. */
 int tlm_hip_packet_read(tlm_hip_manifest *m, const tlm_hip_packet_loc *loc, void *buf, uint64_t *payload_off,
                         uint64_t *payload_len) {
-    if (!m || !loc || !buf) return tlmh_seterr(TLM_HIP_EINVAL, "packet read: NULL argument");
+    if (!m || !loc || !buf) return tlmh_seterr(TLM_HIP_EINVAL, "packet read: missing manifest, record or buffer");
     int rc = TLM_HIP_EIO;
     for (int copy = 0; copy < 2 && rc; copy++) {
         const int drive = copy == 0 ? loc->drive : loc->replica_drive;
@@ -421,25 +421,25 @@ int tlm_hip_packet_read(tlm_hip_manifest *m, const tlm_hip_packet_loc *loc, void
             got += (uint64_t)r;
         }
         if (got != loc->total_len) {
-            rc = tlmh_seterr(TLM_HIP_EIO, "short read of packet type %u layer %u id %u", loc->type, loc->layer, loc->id);
+            rc = tlmh_seterr(TLM_HIP_EIO, "%s: file ends inside packet (%u, %u, %u)", m->drives[drive].c_str(), loc->type, loc->layer, loc->id);
             continue;
         }
         const uint8_t *h = (const uint8_t *)buf;   /* tlm_packet_hdr, tlm_packet.h:39-54 */
         const uint64_t plen = rd64(h + 24);
         if (rd32(h) != PACKET_MAGIC || rd16(h + 6) != STORE_VERSION)
-            rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet type %u layer %u id %u: bad magic/version", loc->type, loc->layer,
-                             loc->id);
+            rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet (%u, %u, %u): not a packet of this store version", loc->type,
+                             loc->layer, loc->id);
         else if (rd16(h + 4) != loc->type || rd16(h + 8) != loc->layer || rd32(h + 12) != loc->id)
-            rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet header does not match the manifest (type %u layer %u id %u)",
+            rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet (%u, %u, %u): its header names another packet than the manifest record",
                              loc->type, loc->layer, loc->id);
         else if (plen > loc->total_len - HDR_BYTES || (HDR_BYTES + plen + ALIGN_IO - 1) / ALIGN_IO * ALIGN_IO != loc->total_len)
-            rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet type %u layer %u id %u: length mismatch", loc->type, loc->layer,
-                             loc->id);
+            rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet (%u, %u, %u): payload length disagrees with the record", loc->type,
+                             loc->layer, loc->id);
         else {
             const uint32_t c = plen ? crc32c(0, h + HDR_BYTES, (size_t)plen) : 0;
             if (c != rd32(h + 32) || c != loc->crc32c)
-                rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet type %u layer %u id %u: CRC mismatch", loc->type, loc->layer,
-                                 loc->id);
+                rc = tlmh_seterr(TLM_HIP_EFORMAT, "packet (%u, %u, %u): payload CRC32C check failed", loc->type,
+                                 loc->layer, loc->id);
             else {
                 rc = TLM_HIP_OK;
                 if (payload_off) *payload_off = HDR_BYTES;
@@ -463,12 +463,12 @@ int tlm_hip_packet_header(const void *buf, uint32_t *dtype, uint32_t item_off[3]
 /* Tensor directory lookup (tlm_packet.c:877-917): the entry named `name` of a
  * DENSE / META / EMBED payload, bounds-checked; TLM_HIP_ENOTFOUND if absent. */
 int tlm_hip_dir_find(const void *payload, uint64_t len, const char *name, tlm_hip_tensor_ref *out) {
-    if (!payload || !name || !out) return tlmh_seterr(TLM_HIP_EINVAL, "dir find: NULL argument");
+    if (!payload || !name || !out) return tlmh_seterr(TLM_HIP_EINVAL, "dir find: missing payload, name or output");
     const uint8_t *p = (const uint8_t *)payload;
-    if (len < 8) return tlmh_seterr(TLM_HIP_EFORMAT, "tensor directory truncated");
+    if (len < 8) return tlmh_seterr(TLM_HIP_EFORMAT, "tensor directory: payload shorter than its header");
     const uint32_t n = rd32(p);
     constexpr uint64_t REF = 88;   /* tlm_tensor_ref, packed */
-    if ((uint64_t)n * REF > len - 8) return tlmh_seterr(TLM_HIP_EFORMAT, "tensor directory: %u entries exceed payload", n);
+    if ((uint64_t)n * REF > len - 8) return tlmh_seterr(TLM_HIP_EFORMAT, "tensor directory: %u records do not fit the payload", n);
     const uint64_t data_start = 8 + (uint64_t)n * REF;
     for (uint32_t i = 0; i < n; i++) {
         const uint8_t *r = p + 8 + (size_t)i * REF;
@@ -483,7 +483,7 @@ int tlm_hip_dir_find(const void *payload, uint64_t len, const char *name, tlm_hi
         const bool ok = memchr(t.name, 0, 48) && t.name[0] && (t.ndim == 1 || t.ndim == 2) &&
                         t.offset % ALIGN_DIR == 0 && t.offset <= len && t.nbytes <= len - t.offset &&
                         t.offset >= data_start;
-        if (!ok) return tlmh_seterr(TLM_HIP_EFORMAT, "tensor directory: entry %u out of bounds", i);
+        if (!ok) return tlmh_seterr(TLM_HIP_EFORMAT, "tensor directory: record %u lies outside the payload", i);
         if (strncmp(t.name, name, 48) == 0) {
             *out = t;
             return TLM_HIP_OK;

@@ -42,6 +42,13 @@ QWEN3_30B_A3B = dict(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_d
                      n_experts=128, top_k=8, d_expert=768, n_shared=0, d_shared=0, max_ctx=40960, router=0,
                      rope_theta=1e6, norm_eps=1e-6, routed_scale=1.0)
 
+# Qwen3-235B-A22B: 94 layers, hidden 4096, 64 q / 4 kv heads x 128 (16 query
+# heads per key head), 128 experts top-8 of width 1536, vocabulary 151936,
+# qk-norm, rope theta 1e6, softmax routing
+QWEN3_235B_A22B = dict(n_layers=94, d_model=4096, n_heads=64, n_kv_heads=4, head_dim=128, vocab=151936,
+                       n_experts=128, top_k=8, d_expert=1536, n_shared=0, d_shared=0, max_ctx=40960, router=0,
+                       rope_theta=1e6, norm_eps=1e-6, routed_scale=1.0)
+
 
 class Model:
     def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0, split=False, **cache):
