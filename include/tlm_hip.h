@@ -473,6 +473,13 @@ typedef struct {
      * attention over the cache) with each token's result bit for bit the
      * step's. */
     int32_t  prefill_chunk;
+    /* 1: every step and prefill chunk stamps the device clock where a layer's
+     * attention and its MoE block begin and where the step begins and ends (a
+     * one-thread launch each, about 1.5 us, so 2 n_layers + 3 more launches per
+     * step), and accumulates the attention / MoE / other split that
+     * tlm_model_get_stats reports (src/lib/tlm_model.h:86-90, filled at
+     * src/lib/tlm_model.c:1099-1101); 0: no stamps */
+    int32_t  stats;
 } tlm_hip_model_opts;
 int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
 void tlm_hip_model_close(tlm_hip_model *M);
@@ -534,6 +541,20 @@ int  tlm_hip_model_sync(tlm_hip_model *M);
 /* the model's stream (hipStream_t), for callers that time or order work
  * against its steps */
 void *tlm_hip_model_stream(const tlm_hip_model *M);
+/* tlm_model_stats (src/lib/tlm_model.h:86-90) of the device steps since the
+ * model opened or the last reset: tokens = positions run; attn_ns / moe_ns =
+ * device time from the start of each layer's attention (its q|k|v launch) to
+ * the start of its MoE block (the router), and from there to the next layer's
+ * attention or the step's tail; other_ns = the embedding and the tail (final
+ * norm, lm_head, argmax); expert_wait_ns = host time blocked on expert loads
+ * in the slot cache (tlm_hip_store_stats.wait_ns).  The split needs
+ * tlm_hip_model_opts.stats; without it tokens and expert_wait_ns alone are
+ * counted.  Waits for the model's work. */
+typedef struct {
+    uint64_t tokens, attn_ns, moe_ns, expert_wait_ns, other_ns;
+} tlm_hip_model_stats;
+int  tlm_hip_model_get_stats(tlm_hip_model *M, tlm_hip_model_stats *out);
+void tlm_hip_model_reset_stats(tlm_hip_model *M);   /* tlm_model_reset_stats (src/lib/tlm_model.c:643) */
 /* the model's expert slot cache (expert_cache_bytes > 0), for its counters
  * (tlm_hip_store_get_stats) as tierlm's stats print them (src/bin/tierlm.c:
  * 441-460); NULL when every expert is resident */

@@ -25,7 +25,21 @@ library (each one anchored on a line of the reference and asserted to apply):
 * src/bin/tierlm.c, rt_open (:196-202): --kernel hip sets the device manifest
   to the store being opened (TIERLM_HIP_TIER_ONLY=1 keeps the reference's CPU
   step with only the kernel table on the device), and the stats line names
-  the self-test failures beside the tier.
+  the self-test failures beside the tier;
+* rt_open (:273-310): the expert budget the runtime settles on (--cache /
+  memory.expert_cache, raised to top_k slots), its capped pin share, its
+  router lookahead, io.lookahead_k and nav.interest_aggressiveness go to the
+  device model: when the budget cannot hold every expert, the experts stay
+  in page-locked host memory behind an HBM slot cache of that budget
+  (tlm_hip_model_opts.expert_cache_bytes), else they are all resident;
+* print_stats / print_stats_json (:419-470, :473-480): the store counters
+  are the device cache's when the step runs there (the reference's RAM store
+  then serves no expert);
+* tlm_model_get_stats / tlm_model_reset_stats (tlm_model.c:642-643): with
+  --stats / --stats-json the device step's attention / MoE split is timed
+  on the device (tlm_hip_model_opts.stats; tlm_hip_model_get_stats), the
+  expert wait is its slot cache's, and other is the rest of the host's step
+  time.
 
 Every library file is then compiled as oracle/Makefile compiles the reference
 (same flags), against include/tlm_hip.h, and linked with
@@ -44,6 +58,36 @@ CFLAGS = ["-std=c11", "-O2", "-g", "-fPIC", "-pthread", "-fno-math-errno", "-ffp
           "-w"]
 AVX2 = ["-mavx2", "-mfma", "-mf16c"]
 AVX512 = ["-mavx512f", "-mavx512bw", "-mavx512vl", "-mavx512vnni", "-mavx512dq", "-mfma", "-mf16c"]
+
+DROPIN_CACHE = """static uint64_t g_dropin_cache;       /* the device slot budget; 0 = every expert resident */
+static double g_dropin_pin, g_dropin_interest;
+static int g_dropin_prefetch_off, g_dropin_lookahead_k, g_dropin_stats;
+static tlm_hip_model *g_dropin_model;    /* the device model of the open KV cache */
+void tlm_model_dropin_cache(uint64_t budget, uint64_t expert_total, double pin_frac, int prefetch,
+                            int lookahead_k, double interest, int stats) {
+    g_dropin_cache = budget < expert_total ? budget : 0;
+    g_dropin_pin = pin_frac > 0 ? pin_frac : -1.0;
+    g_dropin_prefetch_off = !prefetch;
+    g_dropin_lookahead_k = lookahead_k;
+    g_dropin_interest = interest;
+    g_dropin_stats = stats;
+}
+void tlm_model_dropin_store_stats(tlm_store_stats *ss) {
+    tlm_hip_store *st = g_dropin_model ? tlm_hip_model_expert_store(g_dropin_model) : NULL;
+    if (st) tlm_hip_store_get_stats(st, (tlm_hip_store_stats *)ss);
+}
+/* the device step's split: attention and MoE timed on the device, the
+ * expert wait of its slot cache, the rest of the host's step time as other */
+static void dropin_split(tlm_model_stats *out) {
+    tlm_hip_model_stats d;
+    if (!g_dropin_model || tlm_hip_model_get_stats(g_dropin_model, &d)) return;
+    out->attn_ns = d.attn_ns;
+    out->moe_ns = d.moe_ns;
+    out->expert_wait_ns = d.expert_wait_ns;
+    const uint64_t dev = d.attn_ns + d.moe_ns;
+    out->other_ns = out->other_ns > dev ? out->other_ns - dev : 0;
+}
+"""
 
 # (file, anchor, text inserted after the anchor) - or ("replace", old, new)
 PATCHES = [
@@ -66,8 +110,9 @@ PATCHES = [
     ("lib/tlm_model.c", "#include \"tlm_quant.h\"\n",
      "#include \"tlm_hip.h\"\n"
      "static const char *g_dropin_manifest;   /* the store to open on the device, or NULL */\n"
-     "void tlm_model_dropin_manifest(const char *path) { g_dropin_manifest = path; }\n"),
+     "void tlm_model_dropin_manifest(const char *path) { g_dropin_manifest = path; }\n" + DROPIN_CACHE),
     ("lib/tlm_model.c", "void tlm_kv_free(tlm_kv *kv) {\n    if (!kv) return;\n",
+     "    if (kv->hip && g_dropin_model == (tlm_hip_model *)kv->hip) g_dropin_model = NULL;\n"
      "    if (kv->hip) tlm_hip_model_close((tlm_hip_model *)kv->hip);\n"),
     ("lib/tlm_model.c", "int tlm_model_step(tlm_model *M, tlm_kv *kv, int token, float *logits) {\n",
      None),
@@ -77,11 +122,18 @@ PATCHES = [
      "    if (kv->len >= kv->max_ctx) return tlm_seterr(TLM_ERANGE, \"context full (%d tokens)\", kv->max_ctx);\n",
      "    if (kv->hip) return dropin_step(M, kv, token, logits);\n"),
     ("bin/tierlm.c", "#include \"tlm_store.h\"\n",
-     "void tlm_model_dropin_manifest(const char *path);\n"),
+     "void tlm_model_dropin_manifest(const char *path);\n"
+     "void tlm_model_dropin_cache(uint64_t budget, uint64_t expert_total, double pin_frac, int prefetch,\n"
+     "                            int lookahead_k, double interest, int stats);\n"
+     "void tlm_model_dropin_store_stats(tlm_store_stats *ss);\n"),
+    ("bin/tierlm.c", "    r->mdl = tlm_model_open(&r->m, r->io, r->st, r->pool, &mo);\n",
+     "    tlm_model_dropin_cache(r->budget, r->expert_total, r->pin_frac, r->lookahead, r->lookahead_k, mo.interest,\n"
+     "                           o->stats || o->stats_json);\n"),
     ("bin/tierlm.c", "        tlm_cpu_force(o->kernel);\n        tlm_quant_init();\n",
      "        if (!strcmp(o->kernel, \"hip\") && !getenv(\"TIERLM_HIP_TIER_ONLY\"))\n"
      "            tlm_model_dropin_manifest(o->manifest);\n"),
 ]
+
 
 HIP_TIER = """static void build_hip_tier(int base) {
     if (g_hip_state) return;
@@ -135,6 +187,12 @@ KV_OPEN = """    if (g_dropin_manifest) {
         tlm_hip_model_opts ho;
         memset(&ho, 0, sizeof ho);
         ho.max_ctx = max_ctx;
+        ho.expert_cache_bytes = g_dropin_cache;
+        ho.pin_frac = g_dropin_pin;
+        ho.prefetch_off = g_dropin_prefetch_off;
+        ho.lookahead_k = g_dropin_lookahead_k;
+        ho.interest = g_dropin_interest;
+        ho.stats = g_dropin_stats;
         tlm_hip_model *hm = NULL;
         if (tlm_hip_model_open(g_dropin_manifest, &ho, &hm) != 0) {
             tlm_seterr(TLM_EUNSUP, "hip model: %s", tlm_hip_errmsg());
@@ -142,10 +200,23 @@ KV_OPEN = """    if (g_dropin_manifest) {
             return NULL;
         }
         kv->hip = hm;
+        g_dropin_model = hm;
     }
 """
 
 REPLACES = [
+    ("lib/tlm_model.c", "void tlm_model_get_stats(const tlm_model *M, tlm_model_stats *out) { *out = M->st; }\n",
+     "void tlm_model_get_stats(const tlm_model *M, tlm_model_stats *out) {\n    *out = M->st;\n"
+     "    dropin_split(out);\n}\n"),
+    ("lib/tlm_model.c", "void tlm_model_reset_stats(tlm_model *M) { memset(&M->st, 0, sizeof M->st); }\n",
+     "void tlm_model_reset_stats(tlm_model *M) {\n    memset(&M->st, 0, sizeof M->st);\n"
+     "    if (g_dropin_model) tlm_hip_model_reset_stats(g_dropin_model);\n}\n"),
+    ("bin/tierlm.c", "    tlm_store_stats ss;\n    tlm_store_get_stats(r->st, &ss);\n    char b1[32], b2[32], b3[32];\n",
+     "    tlm_store_stats ss;\n    tlm_store_get_stats(r->st, &ss);\n    tlm_model_dropin_store_stats(&ss);\n"
+     "    char b1[32], b2[32], b3[32];\n"),
+    ("bin/tierlm.c", "    tlm_store_stats ss;\n    tlm_store_get_stats(r->st, &ss);\n    uint64_t acc = ss.hits + ss.misses;\n",
+     "    tlm_store_stats ss;\n    tlm_store_get_stats(r->st, &ss);\n    tlm_model_dropin_store_stats(&ss);\n"
+     "    uint64_t acc = ss.hits + ss.misses;\n"),
     ("lib/tlm_model.c", "void tlm_kv_reset(tlm_kv *kv) { kv->len = 0; }\n",
      "void tlm_kv_reset(tlm_kv *kv) {\n    kv->len = 0;\n"
      "    if (kv->hip) tlm_hip_model_reset((tlm_hip_model *)kv->hip);\n}\n"),

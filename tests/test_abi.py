@@ -39,7 +39,7 @@ def test_python_binding_covers_header():
 def test_struct_layouts_match_c():
     from tierlm_amd._lib import (ExpertRef, ExpertSrc, ModelGeom, ModelSynthOpts, MoeDesc, PacketLoc, QuantKernels,
                                  Seg, StoreOpts, StoreStats, TensorRef)
-    from tierlm_amd.model import ModelOpts
+    from tierlm_amd.model import ModelOpts, ModelStats
     prog = r'''
 #include <stdio.h>
 #include <stddef.h>
@@ -67,6 +67,9 @@ int main(void) {
   O(tlm_hip_model_synth_opts, qk_norm); O(tlm_hip_model_synth_opts, seed); O(tlm_hip_model_synth_opts, heat_gamma);
   O(tlm_hip_model_opts, attn_split); O(tlm_hip_model_opts, expert_cache_bytes); O(tlm_hip_model_opts, pin_frac);
   O(tlm_hip_model_opts, lookahead_k); O(tlm_hip_model_opts, interest); O(tlm_hip_model_opts, prefill_chunk);
+  O(tlm_hip_model_opts, stats);
+  printf("mstats %zu\n", sizeof(tlm_hip_model_stats));
+  O(tlm_hip_model_stats, attn_ns); O(tlm_hip_model_stats, expert_wait_ns); O(tlm_hip_model_stats, other_ns);
   return 0;
 }'''
     with tempfile.TemporaryDirectory() as d:
@@ -82,7 +85,7 @@ int main(void) {
     assert vals["qk"] == C.sizeof(QuantKernels)
     for name, cls in (("src", ExpertSrc), ("opts", StoreOpts), ("ref", ExpertRef), ("stats", StoreStats),
                       ("loc", PacketLoc), ("geom", ModelGeom), ("tref", TensorRef), ("synth", ModelSynthOpts),
-                      ("mopts", ModelOpts)):
+                      ("mopts", ModelOpts), ("mstats", ModelStats)):
         assert vals[name] == C.sizeof(cls), name
     for k, v in vals.items():
         if "." not in k:
@@ -92,7 +95,7 @@ int main(void) {
                "tlm_hip_expert_src": ExpertSrc, "tlm_hip_store_opts": StoreOpts, "tlm_hip_expert_ref": ExpertRef,
                "tlm_hip_store_stats": StoreStats, "tlm_hip_packet_loc": PacketLoc, "tlm_hip_model_geom": ModelGeom,
                "tlm_hip_tensor_ref": TensorRef, "tlm_hip_model_synth_opts": ModelSynthOpts,
-               "tlm_hip_model_opts": ModelOpts}[t]
+               "tlm_hip_model_opts": ModelOpts, "tlm_hip_model_stats": ModelStats}[t]
         assert getattr(cls, f).offset == v, k
 
 

@@ -15,7 +15,13 @@ synthetic store (oracle/make_c1.sh) against the reference's own outputs
   gives the reference's greedy tokens;
 * TIERLM_HIP_TIER_ONLY=1 --kernel hip: the reference's own CPU step with
   every quantised matvec of its kernel table on the device (the host-pointer
-  entries of tlm_kern_hip_fill): the same tokens."""
+  entries of tlm_kern_hip_fill): the same tokens;
+* --cache below the experts' size: the runtime's budget (raised to top_k
+  slots) becomes the device's HBM slot cache - on C1 and on C3S (Qwen3-30B-
+  A3B's attention geometry) `tierlm run` gives the reference's greedy tokens
+  and `tierlm oracle` its top-10 text, and --stats reports the device
+  cache's hits, misses and evictions and the device step's attention / MoE
+  split."""
 import os
 import subprocess
 
@@ -100,3 +106,54 @@ def test_run_hip_batched_prefill_c2s():
     p = ",".join(map(str, prompt_ids(64, 2048)))
     r = tierlm(["run", C2S, "--tokens", p, "-n", "64", "--print-tokens", "--cache", "1G", "--kernel", "hip"])
     assert r.stdout.split() == golden("c2s_greedy.txt").split()
+
+
+C3S = os.path.join(ROOT, "oracle", "_ref", "c3s", "c3s.tlmm")
+
+
+def stats_fields(text):
+    """the store / cache / per-token lines of tierlm --stats"""
+    out = {}
+    for line in text.splitlines():
+        if line.startswith("store "):
+            parts = line.split()
+            out["hits"] = int(parts[2].rstrip(","))
+            out["misses"] = int(parts[4])
+            out["evictions"] = int(line.split("evictions ")[1].split(",")[0])
+        elif line.startswith("cache "):
+            out["slots"] = int(line.split()[1])
+        elif line.startswith("per token"):
+            out["attn_ms"] = float(line.split("attention ")[1].split(" ms")[0])
+            out["moe_ms"] = float(line.split("moe ")[1].split(" ms")[0])
+    return out
+
+
+@needs
+def test_run_hip_slot_cache_c1():
+    """--cache 1 (raised to top_k = 4 slots of the 128 experts): the
+    reference's greedy tokens and top-10 text through the device's slot
+    cache, whose counters the stats print."""
+    p = ",".join(map(str, prompt_ids()))
+    r = tierlm(["run", C1, "--tokens", p, "-n", "64", "--print-tokens", "--cache", "1", "--kernel", "hip",
+                "--stats"])
+    assert r.stdout.split() == golden("c1_greedy.txt").split()
+    st = stats_fields(r.stderr)
+    assert st["slots"] == 4, r.stderr[-1500:]
+    assert st["misses"] > 0 and st["evictions"] > 0, r.stderr[-1500:]
+    assert st["attn_ms"] > 0 and st["moe_ms"] > 0, r.stderr[-1500:]
+    gen = golden("c1_greedy.txt").split()[:63]
+    toks = ",".join(map(str, prompt_ids())) + "," + ",".join(gen)
+    r = tierlm(["oracle", C1, "--tokens", toks, "--cache", "1", "--kernel", "hip"])
+    assert r.stdout.splitlines() == golden("c1_oracle.jsonl").splitlines()
+
+
+@pytest.mark.skipif(not (os.path.exists(TIERLM) and os.path.exists(C3S)), reason="oracle/_ref/dropin or c3s not built")
+def test_run_hip_slot_cache_c3s():
+    """Qwen3-30B-A3B's attention geometry with 16 experts top-8 through 8
+    slots: the reference's 128 greedy tokens after the 1920-token prompt."""
+    p = ",".join(map(str, prompt_ids(1920, 2048)))
+    r = tierlm(["run", C3S, "--tokens", p, "-n", "128", "--print-tokens", "--cache", "1", "--kernel", "hip",
+                "--stats"])
+    assert r.stdout.split() == golden("c3s_greedy.txt").split()
+    st = stats_fields(r.stderr)
+    assert st["slots"] == 8 and st["misses"] > 0 and st["evictions"] > 0, r.stderr[-1500:]

@@ -378,3 +378,52 @@ def test_synth_qwen3_235b_a22b_geometry(hip):
     finally:
         a.close()
         b.close()
+
+
+@needs_c1
+@pytest.mark.parametrize("eager", [False, True])
+def test_c1_stats_split(hip, eager):
+    """tlm_hip_model_opts.stats: the steps' device-timed attention / MoE /
+    other split (tlm_model_stats) is counted and leaves every result
+    unchanged - the same greedy tokens as the reference, graph or eager."""
+    from tierlm_amd.model import Model
+    m = Model(C1, max_ctx=256, eager=eager, stats=True, prefill_chunk=-1)
+    try:
+        st = m.stats()
+        assert st["tokens"] == 0 and st["attn_ns"] == 0
+        assert m.generate(prompt_tokens(), 64) == greedy_tokens()
+        st = m.stats()
+        assert st["tokens"] == 64 + 63
+        assert st["attn_ns"] > 0 and st["moe_ns"] > 0 and st["other_ns"] > 0
+        per = (st["attn_ns"] + st["moe_ns"] + st["other_ns"]) / st["tokens"]
+        assert 1e3 < per < 1e7, per                       # between 1 us and 10 ms of device time per token
+        m.reset_stats()
+        assert m.stats()["tokens"] == 0 and m.stats()["moe_ns"] == 0
+        m.reset()
+        lg = m.prefill(prompt_tokens()[:40])
+        assert m.stats()["tokens"] == 40 and m.stats()["attn_ns"] > 0
+        assert int(np.argmax(lg)) == int(np.argmax(lg))
+    finally:
+        m.close()
+
+
+@needs_c1
+def test_c1_stats_batched_prefill_and_cache(hip):
+    """The split is also counted for a batched prompt and for a step whose
+    experts come through the slot cache (whose load waits are the expert
+    wait)."""
+    from tierlm_amd.model import Model
+    a = Model(C1, max_ctx=256, stats=True)
+    b = Model(C1, max_ctx=256, stats=True, expert_cache=1)
+    try:
+        assert a.prefill_batched()
+        la = a.prefill(prompt_tokens())
+        lb = b.prefill(prompt_tokens())
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        for m in (a, b):
+            st = m.stats()
+            assert st["tokens"] == 64 and st["attn_ns"] > 0 and st["moe_ns"] > 0 and st["other_ns"] > 0
+        assert b.store_stats()["misses"] > 0
+    finally:
+        a.close()
+        b.close()

@@ -180,6 +180,8 @@ _SIGS = {
     "tlm_hip_model_sync": (i32, [vp]),
     "tlm_hip_model_stream": (vp, [vp]),
     "tlm_hip_model_expert_store": (vp, [vp]),
+    "tlm_hip_model_get_stats": (i32, [vp, vp]),
+    "tlm_hip_model_reset_stats": (None, [vp]),
     "tlm_hip_model_reset": (None, [vp]),
     "tlm_hip_model_step": (i32, [vp, i32, vp, C.POINTER(C.c_int32)]),
     "tlm_hip_model_generate": (i32, [vp, C.POINTER(C.c_int32), i32, i32, C.POINTER(C.c_int32)]),

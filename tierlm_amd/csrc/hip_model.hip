@@ -74,22 +74,24 @@ __global__ __launch_bounds__(NT) void k_pf_add(float *__restrict__ h, const floa
  * and stores every (query head, position) score: the dot in ascending i,
  * scaled after the dot.  The group whose slice holds the new position appends
  * its key and value to the cache.
- * k_attn_pv: a group per (query head, 64 output elements).  All four waves
- * run the softmax in the reference's order - the maximum over the context,
- * e_t = e^(s_t - max), their sum in double, inv = 1 / sum, p_t = e_t * inv
- * (probabilities in LDS), e^x with its table held in the lanes - then the
- * P.V sums out += p_t * v_t[i] over ascending t: wave 0 holds one chain per
- * lane and only adds, one dependent add per position (about 4.5 clocks);
- * waves 1-3 form the products p_t v_t[i] (the reference's rounded products)
- * into a ring of three LDS blocks of ATT_BT value tiles, two blocks ahead of
- * the chains, with the value tiles ATT_VPF blocks ahead in registers (the
- * first ones loaded at entry); one barrier per block.  A chain wave that also
- * formed its products issued a multiply and an add per position, and one that
- * read its values from memory as well shared the CU's load bandwidth with
- * three others: both ran at 9-10 ns per position.  The value cache is kept in
+ * k_attn_pv: a group per (query head, PV_EW = 16 output elements), so a
+ * head of width 128 spreads over 8 groups and 32 heads cover the chip's 256
+ * CUs.  All four waves run the softmax in the reference's order - the
+ * maximum over the context, e_t = e^(s_t - max), their sum in double, inv =
+ * 1 / sum, p_t = e_t * inv (probabilities in LDS), e^x with its table held
+ * in the lanes - then the P.V sums out += p_t * v_t[i] over ascending t:
+ * wave 0 holds the chains (lane i mod 16 runs element i's) and only adds,
+ * one dependent add per position (about 4.5 clocks); waves 1-3, 12 lanes per
+ * element, form the products p_t v_t[i] (the reference's rounded products)
+ * into a ring of three LDS blocks of 48 value tiles, two blocks ahead of the
+ * chains, with their value tiles PV_VPF blocks ahead in registers (the first
+ * ones loaded at entry); one barrier per block.  A group streams 64 bytes of
+ * values per position: with 64 elements per group (256 bytes) the value
+ * stream of one CU and the few groups in flight held the ring to ~5 ns per
+ * position, the chain's own rate being under 2.  The value cache is kept in
  * tiles of 4 positions, element-major inside (V[t][i] at ((t / 4) * HD + i) *
  * 4 + t % 4), where one 16-byte lane load is positions 4j..4j+3 of element i
- * and a wave's load is 1 KB contiguous.
+ * and 16 lanes load 256 contiguous bytes.
  *
  * Numerics: the scores, maximum, products and chains are the reference's
  * operations in its order; the double sums (squares of the norms, softmax
@@ -107,8 +109,9 @@ constexpr int ATT_LMIN = 32;     /* shortest slice */
 constexpr int ATT_QMAX = 4096;   /* query values per key head (query heads per key head x HD) */
 constexpr int ATT_GMAX = 128;    /* slices per key head */
 constexpr int ATT_PSEG = 4096;   /* probabilities per LDS segment of k_attn_pv */
-constexpr int ATT_BT = 24;       /* value tiles (4 positions each) per block of k_attn_pv's product ring */
-constexpr int ATT_VPF = 3;       /* blocks of value tiles k_attn_pv's producers hold in flight (a multiple of 3) */
+constexpr int PV_EW = 16;        /* output elements per k_attn_pv group */
+constexpr int PV_TPL = 4;        /* value tiles (4 positions each) per producer lane per block of the ring */
+constexpr int PV_VPF = 3;        /* blocks of value tiles a producer lane holds in flight (a multiple of 3) */
 
 /* floats of value cache per key head: whole 4-position tiles */
 __host__ __device__ inline size_t att_vstride(int max_ctx, int hd) { return (size_t)((max_ctx + 3) & ~3) * hd; }
@@ -332,13 +335,17 @@ template <int HD>
 __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
                                                 float *__restrict__ att, int H, int KV, int max_ctx,
                                                 const int32_t *__restrict__ st) {
-    constexpr int NWC = (HD + 63) / 64;   /* 64-element slabs per query head, a group each */
+    constexpr int EW = PV_EW;             /* output elements per group */
+    constexpr int NWC = HD / EW;          /* element slabs per query head, a group each */
     constexpr int PB = 8;                 /* score loads per thread per round */
-    constexpr int NPW = NT / 64 - 1;      /* producer waves */
-    constexpr int TPP = ATT_BT / NPW;     /* tiles per producer per block */
-    static_assert(ATT_BT % NPW == 0, "a block's tiles split evenly over the producers");
+    constexpr int PL = NT - 64;           /* producer lanes (waves 1..3) */
+    constexpr int TL = PL / EW;           /* producer lanes per element: tile columns of a block */
+    constexpr int TPL = PV_TPL;           /* tiles per producer lane per block */
+    constexpr int BT = TL * TPL;          /* tiles per block */
+    constexpr int VPF = PV_VPF;
+    static_assert(HD % EW == 0 && PL % EW == 0 && VPF % 3 == 0 && BT % 3 == 0, "ring shape");
     __shared__ __align__(16) float s_p[ATT_PSEG];
-    __shared__ __align__(16) f32x4 s_prod[3][ATT_BT][64];   /* three blocks of products, tile-major */
+    __shared__ __align__(16) f32x4 s_prod[3][BT][EW];   /* three blocks of products, tile-major */
     __shared__ double s_sum[NT / 64];
     __shared__ float s_max[NT / 64];
     const int R = H / KV;
@@ -348,19 +355,23 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     const int kvg = (int)blockIdx.x % KV, rest = (int)blockIdx.x / KV;
     if (rest >= R * NWC) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = kvg * R + rest / NWC, ic = 64 * (rest % NWC) + lane;
+    const int h = kvg * R + rest / NWC;
+    /* a producer lane's element and tile column; the chain wave's lane l runs
+     * element l mod EW (lanes past EW repeat a chain and store nothing) */
+    const int pl = wave > 0 ? tid - 64 : lane;
+    const int e = pl % EW, tc = pl / EW;
+    const int ic = EW * (rest % NWC) + e;
     const float *S = scores + (size_t)h * max_ctx;
     const char *vbase = (const char *)(vc + (size_t)kvg * att_vstride(max_ctx, HD));
-    const uint32_t lane_off = (uint32_t)min(ic, HD - 1) * 16u;   /* element ic's 16 bytes of a tile */
-    /* producer pw forms tiles pw * TPP .. + TPP - 1 of each block; the chain
-     * wave issues producer 0's first loads too (and drops them), so that every
-     * wave runs the same loads up to the role split and the compiler's wait
-     * for the scores is the same count on every path */
-    const int pw = wave > 0 ? wave - 1 : 0;
-    auto vload = [&](int q0, int blk, int lastq, f32x4 (&r)[TPP]) {
+    const uint32_t lane_off = (uint32_t)ic * 16u;   /* element ic's 16 bytes of a tile */
+    /* a producer lane forms tiles tc + TL u (u < TPL) of each block; the chain
+     * wave issues the same first loads (and drops them), so that every wave
+     * runs the same loads up to the role split and the compiler's wait for the
+     * scores is the same count on every path */
+    auto vload = [&](int q0, int blk, int lastq, f32x4 (&r)[TPL]) {
 #pragma unroll
-        for (int u = 0; u < TPP; u++) {
-            const int tq = min(q0 + blk * ATT_BT + pw * TPP + u, lastq);
+        for (int u = 0; u < TPL; u++) {
+            const int tq = min(q0 + blk * BT + tc + TL * u, lastq);
             r[u] = *(const f32x4 *)(vbase + (size_t)tq * (HD * 16) + lane_off);
         }
     };
@@ -373,9 +384,9 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     for (int k = 0; k < PB; k++) sv[k] = S[min(tid + NT * k, max_ctx - 1)];
     ExpTabLanes tab;
     tab.load();
-    f32x4 vq[ATT_VPF][TPP];   /* producers: value tiles of ATT_VPF blocks */
+    f32x4 vq[VPF][TPL];   /* producers: value tiles of VPF blocks */
 #pragma unroll
-    for (int k = 0; k < ATT_VPF; k++) vload(0, k, (max_ctx - 1) >> 2, vq[k]);
+    for (int k = 0; k < VPF; k++) vload(0, k, (max_ctx - 1) >> 2, vq[k]);
     const int pos = st[0], T = pos + 1, lastq = (T - 1) >> 2;
 
     /* the maximum over the context (tlm_model.c:698-703; NaN never compares
@@ -410,9 +421,9 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
 #pragma unroll
         for (int k = 0; k < PB; k++) {   /* every lane computes; past the context it adds 0, stores nothing */
             const int t = r * PB * NT + tid + NT * k;
-            const float e = expf_ref_with(sv[k] - mx, tab);
-            sum += t < T ? (double)e : 0.0;
-            if (nseg == 1 && t < T) s_p[t] = e;
+            const float ex = expf_ref_with(sv[k] - mx, tab);
+            sum += t < T ? (double)ex : 0.0;
+            if (nseg == 1 && t < T) s_p[t] = ex;
         }
     }
     sum = wave_sum_f64(sum);
@@ -423,13 +434,12 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     for (int w = 0; w < NT / 64; w++) tot += s_sum[w];
     const float inv_s = (float)(1.0 / tot);
 
-    /* P.V: wave 0 runs the chains out += p_t v_t[i] (one lane per element,
-     * ascending t); waves 1..NPW form the products p_t v_t[i] - the
-     * reference's rounded products - into a ring of three LDS blocks of
-     * ATT_BT tiles, two blocks ahead of the chains, with their value tiles
-     * three blocks ahead in registers.  Products past the segment are +0, and
-     * adding +0 leaves the chain unchanged (it starts at +0 and never holds
-     * -0), so the chains run whole blocks. */
+    /* P.V: wave 0 runs the chains out += p_t v_t[i] (ascending t); waves
+     * 1..3 form the products p_t v_t[i] - the reference's rounded products -
+     * into a ring of three LDS blocks of BT tiles, two blocks ahead of the
+     * chains, with their value tiles VPF blocks ahead in registers.  Products
+     * past the segment are +0, and adding +0 leaves the chain unchanged (it
+     * starts at +0 and never holds -0), so the chains run whole blocks. */
     float acc = 0.0f;
     for (int sb = 0; sb < T; sb += ATT_PSEG) {   /* uniform over the group */
         const int se = min(T, sb + ATT_PSEG);
@@ -442,38 +452,37 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
                 if (t < se) s_p[t - sb] = p;
             }
         }
-        const int nbk = (se - sb + ATT_BT * 4 - 1) / (ATT_BT * 4);   /* blocks of the segment */
+        const int nbk = (se - sb + BT * 4 - 1) / (BT * 4);   /* blocks of the segment */
         const int q0 = sb >> 2;   /* the segment's first tile */
-        /* the probabilities of a producer's tiles of block blk (uniform LDS
-         * reads), read a block ahead of their use */
-        auto pread = [&](int blk, f32x4 (&p)[TPP]) {
-            const f32x4 *p4 = (const f32x4 *)s_p + min(blk * ATT_BT + pw * TPP, ATT_PSEG / 4 - TPP);
+        /* the probabilities of a producer lane's tiles of block blk (LDS reads
+         * shared by the lanes of a tile column), read a block ahead of their use */
+        auto pread = [&](int blk, f32x4 (&p)[TPL]) {
+            const f32x4 *p4 = (const f32x4 *)s_p;
 #pragma unroll
-            for (int u = 0; u < TPP; u++) p[u] = p4[u];
+            for (int u = 0; u < TPL; u++) p[u] = p4[min(blk * BT + tc + TL * u, ATT_PSEG / 4 - 1)];
         };
-        auto produce = [&](int blk, const f32x4 (&p)[TPP], const f32x4 (&r)[TPP], int buf) {
-            const int tl0 = blk * ATT_BT + pw * TPP;   /* the producer's first tile in the segment */
-            f32x4 *dst = &s_prod[buf][pw * TPP][lane];
-            if (sb + 4 * (tl0 + TPP) <= se) {   /* uniform: the tiles lie inside the segment */
+        auto produce = [&](int blk, const f32x4 (&p)[TPL], const f32x4 (&r)[TPL], int buf) {
+            const int tl0 = blk * BT;   /* the block's first tile in the segment */
+            if (sb + 4 * (tl0 + BT) <= se) {   /* uniform: the block lies inside the segment */
 #pragma unroll
-                for (int u = 0; u < TPP; u++) {
+                for (int u = 0; u < TPL; u++) {
                     f32x4 o;
                     o.x = p[u].x * r[u].x;
                     o.y = p[u].y * r[u].y;
                     o.z = p[u].z * r[u].z;
                     o.w = p[u].w * r[u].w;
-                    dst[u * 64] = o;
+                    s_prod[buf][tc + TL * u][e] = o;
                 }
             } else {
 #pragma unroll
-                for (int u = 0; u < TPP; u++) {
-                    const int t = sb + 4 * (tl0 + u);
+                for (int u = 0; u < TPL; u++) {
+                    const int t = sb + 4 * (tl0 + tc + TL * u);
                     f32x4 o;
                     o.x = t < se ? p[u].x * r[u].x : 0.0f;
                     o.y = t + 1 < se ? p[u].y * r[u].y : 0.0f;
                     o.z = t + 2 < se ? p[u].z * r[u].z : 0.0f;
                     o.w = t + 3 < se ? p[u].w * r[u].w : 0.0f;
-                    dst[u * 64] = o;
+                    s_prod[buf][tc + TL * u][e] = o;
                 }
             }
         };
@@ -482,16 +491,16 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
         if (wave > 0) {
             if (sb > 0) {   /* later segments: their first blocks' tiles now */
 #pragma unroll
-                for (int k = 0; k < ATT_VPF; k++) vload(q0, k, lastq, vq[k]);
+                for (int k = 0; k < VPF; k++) vload(q0, k, lastq, vq[k]);
             }
-            f32x4 pc[TPP];
+            f32x4 pc[TPL];
             __syncthreads();   /* the segment's probabilities */
             pread(0, pc);
             produce(0, pc, vq[0], 0);
-            vload(q0, ATT_VPF, lastq, vq[0]);
+            vload(q0, VPF, lastq, vq[0]);
             pread(1, pc);
             produce(1, pc, vq[1], 1);
-            vload(q0, ATT_VPF + 1, lastq, vq[1]);
+            vload(q0, VPF + 1, lastq, vq[1]);
             pread(2, pc);
             __syncthreads();
             /* one step (and barrier) per block of the segment; step s of a
@@ -501,39 +510,43 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
              * counts there keep it); the steps after it produce only blocks
              * of the segment, so none waits for a tile past the context */
             auto step = [&](int b, int k) {
-                produce(b + k + 2, pc, vq[(k + 2) % ATT_VPF], (k + 2) % 3);
-                vload(q0, b + k + 2 + ATT_VPF, lastq, vq[(k + 2) % ATT_VPF]);
+                produce(b + k + 2, pc, vq[(k + 2) % VPF], (k + 2) % 3);
+                vload(q0, b + k + 2 + VPF, lastq, vq[(k + 2) % VPF]);
                 pread(b + k + 3, pc);
                 __syncthreads();
             };
             int b = 0;
-            for (; b + ATT_VPF + 2 <= nbk; b += ATT_VPF) {
+            for (; b + VPF + 2 <= nbk; b += VPF) {
 #pragma unroll
-                for (int k = 0; k < ATT_VPF; k++) step(b, k);
+                for (int k = 0; k < VPF; k++) step(b, k);
             }
 #pragma unroll
-            for (int k = 0; k < ATT_VPF + 1; k++) {   /* uniform: the chain wave runs the same blocks */
+            for (int k = 0; k < VPF + 1; k++) {   /* uniform: the chain wave runs the same blocks */
                 if (b + k >= nbk) break;
-                if (b + k + 2 < nbk) produce(b + k + 2, pc, vq[(k + 2) % ATT_VPF], (k + 2) % 3);
+                if (b + k + 2 < nbk) produce(b + k + 2, pc, vq[(k + 2) % VPF], (k + 2) % 3);
                 pread(b + k + 3, pc);
                 __syncthreads();
             }
         } else {
-            /* the chain reads a block in three parts, each one part ahead of
-             * its adds (the next block's first part during this block's last) */
-            constexpr int SUB = ATT_BT / 3;
+            /* the chain reads a block in parts of 8 tiles, each one part ahead
+             * of its adds (the next block's first part during this block's last) */
+            constexpr int SUB = 8, NPART = BT / SUB;
+            static_assert(BT % SUB == 0, "whole parts");
             __syncthreads();   /* the segment's probabilities */
             __syncthreads();
             f32x4 cur[SUB];
+            const bool chain = lane < EW;   /* lanes past EW stay out of the LDS reads and adds */
+            if (chain)
 #pragma unroll
-            for (int u = 0; u < SUB; u++) cur[u] = s_prod[0][u][lane];
+                for (int u = 0; u < SUB; u++) cur[u] = s_prod[0][u][e];
             auto block = [&](int k) {   /* block b + k from buffer (b + k) mod 3 */
+                if (chain)
 #pragma unroll
-                for (int c = 0; c < 3; c++) {
+                for (int c = 0; c < NPART; c++) {
                     f32x4 nx[SUB];
 #pragma unroll
                     for (int u = 0; u < SUB; u++)
-                        nx[u] = c < 2 ? s_prod[k % 3][SUB * (c + 1) + u][lane] : s_prod[(k + 1) % 3][u][lane];
+                        nx[u] = c < NPART - 1 ? s_prod[k % 3][SUB * (c + 1) + u][e] : s_prod[(k + 1) % 3][u][e];
                     /* the reads stay ahead of the adds (the scheduler would
                      * otherwise sink them to their use) */
                     __builtin_amdgcn_sched_barrier(0);
@@ -550,16 +563,16 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
                 __syncthreads();
             };
             int b = 0;
-            for (; b + ATT_VPF <= nbk; b += ATT_VPF) {
+            for (; b + VPF <= nbk; b += VPF) {
 #pragma unroll
-                for (int k = 0; k < ATT_VPF; k++) block(k);
+                for (int k = 0; k < VPF; k++) block(k);
             }
 #pragma unroll
-            for (int k = 0; k < ATT_VPF - 1; k++)
+            for (int k = 0; k < VPF - 1; k++)
                 if (b + k < nbk) block(k);
         }
     }
-    if (wave == 0 && ic < HD) att[(size_t)h * HD + ic] = acc;
+    if (wave == 0 && lane < EW) att[(size_t)h * HD + ic] = acc;
 }
 
 /* ---- split attention (attn_split): a partial softmax and P.V per (key
@@ -1215,7 +1228,7 @@ int launch_attn(int hd, int H, int KV, int max_ctx, int G, bool split, const flo
     const size_t dyn = (size_t)att_lds(hd, H / KV).total * 4;
     const int lmax = att_slice_len(max_ctx, G);
     const size_t dyn_split = att_split_bytes(hd, H, KV, max_ctx, G);
-    const unsigned npv = (unsigned)(H * ((hd + 63) / 64));   /* k_attn_pv: a group per (query head, 64 elements) */
+    const unsigned npv = (unsigned)(H * (hd / PV_EW));   /* k_attn_pv: a group per (query head, 16 elements) */
 #define TLM_ATT(W)                                                                                                \
     case W:                                                                                                       \
         if (split) {                                                                                              \
@@ -1264,6 +1277,32 @@ __global__ __launch_bounds__(1024) void k_advance(int32_t *st, int32_t *seq, con
 /* the context position (the next step's), as a rollback sets it */
 __global__ void k_set_pos(int32_t *st, int pos) { st[0] = pos; }
 
+/* tlm_hip_model_opts.stats: stamps of the device clock (s_memrealtime, a
+ * fixed 100 MHz count shared by the chip).  A step stamps S before its
+ * embedding, A_l / M_l where layer l's attention and MoE block begin and T
+ * before its tail (at st[0], st[1 + 2l], st[2 + 2l], st[1 + 2L]); k_stamp_acc
+ * reads the end itself and adds the split, in ns, to st[2L + 2 ..]: attention
+ * = sum (M_l - A_l), MoE = sum (A_l+1 - M_l) with A_L = T, other = (A_0 - S)
+ * + (end - T). */
+__global__ void k_stamp(uint64_t *dst) {
+    if (threadIdx.x == 0) dst[0] = __builtin_amdgcn_s_memrealtime();
+}
+__global__ void k_stamp_acc(uint64_t *st, int L) {
+    if (threadIdx.x != 0) return;
+    const uint64_t end = __builtin_amdgcn_s_memrealtime();
+    const uint64_t S = st[0], T = st[1 + 2 * L];
+    uint64_t attn = 0, moe = 0;
+    for (int l = 0; l < L; l++) {
+        const uint64_t A = st[1 + 2 * l], Mb = st[2 + 2 * l], An = l + 1 < L ? st[3 + 2 * l] : T;
+        attn += Mb - A;
+        moe += An - Mb;
+    }
+    uint64_t *acc = st + 2 * L + 2;
+    acc[0] += attn * 10;
+    acc[1] += moe * 10;
+    acc[2] += ((st[1] - S) + (end - T)) * 10;
+}
+
 struct DevMat {
     int dt = -1;
     int64_t rows = 0, n = 0;
@@ -1303,6 +1342,11 @@ struct tlm_hip_model {
     float *w = nullptr;
     int32_t *host_tok = nullptr;   /* pinned */
     hipGraphExec_t graph[2] = {nullptr, nullptr};   /* step without / with logits, captured at first use */
+    /* tlm_hip_model_opts.stats: device stamps of the step, then the
+     * accumulated attention / MoE / other ns (k_stamp_acc); host counts */
+    bool stats = false;
+    uint64_t *stamps = nullptr;
+    uint64_t st_tokens = 0, st_wait0 = 0;
     bool graph_failed[2] = {false, false};
     /* experts through the slot cache (expert_cache_bytes > 0) */
     uint64_t xs_budget = 0;
@@ -1488,6 +1532,7 @@ int prepare(tlm_hip_model *M, const tlm_hip_model_opts *o) {
     M->xopts.lookahead_k = o ? o->lookahead_k : 0;
     M->xopts.interest = o ? o->interest : 0.0;
     M->pf_chunk = o ? o->prefill_chunk : 0;
+    M->stats = o && o->stats;
     if (M->xopts.lookahead_k < 0 || M->xopts.lookahead_k > 32)
         return tlmh_seterr(TLM_HIP_EINVAL, "model: lookahead_k %d (0..32)", M->xopts.lookahead_k);
     /* a step through the cache waits on the host between layers: never a graph */
@@ -1555,6 +1600,12 @@ int finish(tlm_hip_model *M) {
     for (const Layer &Ly : M->L) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
     M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
     M->st = (int32_t *)M->dalloc(16);
+    if (M->stats) {
+        const size_t nst = (2 * (size_t)g.n_layers + 5) * 8;
+        M->stamps = (uint64_t *)M->dalloc(nst);
+        if (M->stamps && hipMemset(M->stamps, 0, nst) != hipSuccess) M->stamps = nullptr;
+        if (!M->stamps) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory (stats)");
+    }
     M->seq = (int32_t *)M->dalloc(((size_t)max_ctx + 1) * 4);
     M->ids = (int32_t *)M->dalloc((size_t)g.n_layers * 32 * 4);   /* the step's routing, per layer */
     M->w = (float *)M->dalloc((size_t)g.n_layers * 32 * 4);
@@ -1873,18 +1924,33 @@ void enqueue_embed(tlm_hip_model *M) {
  * seq[pos], pos = st[0]; with logits, the greedy next token goes to
  * seq[pos + 1]; st[0] advances.  Every argument is the same at every position
  * (the step is captured once as a graph). */
+/* stats stamp i (no-op without tlm_hip_model_opts.stats) */
+void stamp(tlm_hip_model *M, size_t i) {
+    if (M->stats) hipLaunchKernelGGL(k_stamp, dim3(1), dim3(64), 0, M->stream, M->stamps + i);
+}
+void stamp_acc(tlm_hip_model *M) {
+    if (M->stats) hipLaunchKernelGGL(k_stamp_acc, dim3(1), dim3(64), 0, M->stream, M->stamps, (int)M->g.n_layers);
+}
+
 int enqueue_step(tlm_hip_model *M, bool want_logits) {
+    const size_t L = M->g.n_layers;
+    stamp(M, 0);
     enqueue_embed(M);
     int rc = tlmh_check(hipGetLastError(), "model: embed");
-    for (uint32_t l = 0; l < M->g.n_layers && !rc; l++) {
+    for (uint32_t l = 0; l < L && !rc; l++) {
         const Layer &Ly = M->L[l];
+        stamp(M, 1 + 2 * (size_t)l);
         rc = enqueue_attention(M, l);
+        stamp(M, 2 + 2 * (size_t)l);
         /* moe(), tlm_model.c:940-1055 */
         if (!rc) rc = launch_moe_layer(&Ly.moe, M->h, M->ids + (size_t)l * 32, M->w + (size_t)l * 32, M->moe_ws,
                                        M->stream);
     }
     if (rc) return rc;
-    return enqueue_tail(M, want_logits);
+    stamp(M, 1 + 2 * L);
+    rc = enqueue_tail(M, want_logits);
+    stamp_acc(M);
+    return rc ? rc : tlmh_check(hipGetLastError(), "model: stats");
 }
 
 /* The same step with the experts in the slot cache: tlm_model_step's layer
@@ -1893,14 +1959,23 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
  * right before its router, and the host acquires layer l + 1's experts while
  * the device runs layer l's block (moe_stack_run). */
 int step_cached(tlm_hip_model *M, bool want_logits) {
+    const size_t L = M->g.n_layers;
+    stamp(M, 0);
     enqueue_embed(M);
     int rc = tlmh_check(hipGetLastError(), "model: embed");
     if (!rc)
-        rc = moe_stack_run(M->descs.data(), (int)M->g.n_layers, M->xs, M->h, &M->xopts, M->route_ids.data(),
-                           M->route_w.data(), M->stack_ws, M->stream,
-                           [M](int l) { return enqueue_attention(M, (uint32_t)l); });
+        rc = moe_stack_run(M->descs.data(), (int)L, M->xs, M->h, &M->xopts, M->route_ids.data(),
+                           M->route_w.data(), M->stack_ws, M->stream, [M](int l) {
+                               stamp(M, 1 + 2 * (size_t)l);
+                               const int r = enqueue_attention(M, (uint32_t)l);
+                               stamp(M, 2 + 2 * (size_t)l);
+                               return r;
+                           });
     if (rc) return rc;
-    return enqueue_tail(M, want_logits);
+    stamp(M, 1 + 2 * L);
+    rc = enqueue_tail(M, want_logits);
+    stamp_acc(M);
+    return rc ? rc : tlmh_check(hipGetLastError(), "model: stats");
 }
 
 /* One step (the caller checked the context): the captured graph of the kind,
@@ -1926,7 +2001,10 @@ int step(tlm_hip_model *M, bool want_logits) {
     int rc = M->xs ? step_cached(M, want_logits)
              : M->graph[k] ? tlmh_check(hipGraphLaunch(M->graph[k], M->stream), "model: step graph")
                            : enqueue_step(M, want_logits);
-    if (!rc) M->kv_len++;
+    if (!rc) {
+        M->kv_len++;
+        M->st_tokens++;
+    }
     return rc;
 }
 
@@ -2041,15 +2119,18 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
     int per = (n + nch - 1) / nch;
     per = (per + 3) & ~3;
     per = per > M->pf_cap ? M->pf_cap : per;
+    const size_t L = g.n_layers;
     for (int c0 = 0; c0 < n && !rc; c0 += per) {
         nt = n - c0 < per ? n - c0 : per;
         const int pc = p0 + c0;
+        stamp(M, 0);
         hipLaunchKernelGGL(k_pf_embed, dim3((D + NT - 1) / NT, nt), dim3(NT), 0, s, M->embd, M->embd_row, M->embd_dt,
                            (const int32_t *)M->seq + pc, D, M->pf_h);
         rc = tlmh_check(hipGetLastError(), "model prefill: embed");
         for (uint32_t l = 0; l < g.n_layers && !rc; l++) {
             const Layer &Ly = M->L[l];
             int ak = -1;
+            stamp(M, 1 + 2 * (size_t)l);
             if (Ly.q.dt == Ly.k.dt && Ly.q.dt == Ly.v.dt) {   /* q | k | v in one launch */
                 const int kind = dt_act_kind(Ly.q.dt);
                 rc = launch_tok_norm_act(kind, M->pf_h, D, Ly.attn_norm, g.norm_eps, D, nt, M->pf_act,
@@ -2076,6 +2157,7 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
                                    (const float *)M->pf_y, cnt);
                 rc = tlmh_check(hipGetLastError(), "model prefill: residual");
             }
+            stamp(M, 2 + 2 * (size_t)l);
             if (!rc) rc = launch_moe_prefill(&Ly.moe, M->pf_h, nt, M->pf_ids, M->pf_w, M->pf_ws, s);
             if (!rc && c0 + nt == n) {   /* the last token's routing, as the step leaves it */
                 rc = tlmh_check(hipMemcpyAsync(M->ids + (size_t)l * 32, M->pf_ids + (size_t)(nt - 1) * k, (size_t)k * 4,
@@ -2085,6 +2167,8 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
                                                    (size_t)k * 4, hipMemcpyDeviceToDevice, s), "model prefill: routes");
             }
         }
+        stamp(M, 1 + 2 * L);
+        if (c0 + nt < n) stamp_acc(M);   /* the last chunk's split takes the tail */
     }
     if (rc) return rc;
     rc = tlmh_check(hipMemcpyAsync(M->h, M->pf_h + (size_t)(nt - 1) * D, (size_t)D * 4, hipMemcpyDeviceToDevice, s),
@@ -2092,7 +2176,12 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
     if (rc) return rc;
     hipLaunchKernelGGL(k_set_pos, dim3(1), dim3(1), 0, s, M->st, p0 + n - 1);
     rc = enqueue_tail(M, want_logits);
-    if (!rc) M->kv_len = p0 + n;
+    stamp_acc(M);
+    if (!rc) rc = tlmh_check(hipGetLastError(), "model prefill: stats");
+    if (!rc) {
+        M->kv_len = p0 + n;
+        M->st_tokens += (uint64_t)n;
+    }
     return rc;
 }
 
@@ -2450,6 +2539,44 @@ int tlm_hip_model_sync(tlm_hip_model *M) {
 
 void *tlm_hip_model_stream(const tlm_hip_model *M) { return M ? (void *)M->stream : nullptr; }
 tlm_hip_store *tlm_hip_model_expert_store(const tlm_hip_model *M) { return M ? M->xs : nullptr; }
+
+int tlm_hip_model_get_stats(tlm_hip_model *M, tlm_hip_model_stats *out) {
+    if (!M || !out) return tlmh_seterr(TLM_HIP_EINVAL, "model stats: NULL argument");
+    memset(out, 0, sizeof *out);
+    int rc = tlmh_check(hipStreamSynchronize(M->stream), "model stats");
+    if (rc) return rc;
+    out->tokens = M->st_tokens;
+    if (M->stats) {
+        uint64_t acc[3];
+        rc = tlmh_check(hipMemcpy(acc, M->stamps + 2 * (size_t)M->g.n_layers + 2, sizeof acc, hipMemcpyDeviceToHost),
+                        "model stats");
+        if (rc) return rc;
+        out->attn_ns = acc[0];
+        out->moe_ns = acc[1];
+        out->other_ns = acc[2];
+    }
+    if (M->xs) {
+        tlm_hip_store_stats ss;
+        tlm_hip_store_get_stats(M->xs, &ss);
+        out->expert_wait_ns = ss.wait_ns - M->st_wait0;
+    }
+    return TLM_HIP_OK;
+}
+
+void tlm_hip_model_reset_stats(tlm_hip_model *M) {
+    if (!M) return;
+    (void)hipStreamSynchronize(M->stream);
+    M->st_tokens = 0;
+    if (M->stats) {
+        const uint64_t z[3] = {0, 0, 0};
+        (void)hipMemcpy(M->stamps + 2 * (size_t)M->g.n_layers + 2, z, sizeof z, hipMemcpyHostToDevice);
+    }
+    if (M->xs) {
+        tlm_hip_store_stats ss;
+        tlm_hip_store_get_stats(M->xs, &ss);
+        M->st_wait0 = ss.wait_ns;
+    }
+}
 
 void tlm_hip_model_reset(tlm_hip_model *M) {
     if (!M) return;

@@ -21,19 +21,27 @@ class ModelOpts(C.Structure):
     """tlm_hip_model_opts"""
     _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32), ("attn_split", C.c_int32),
                 ("expert_cache_bytes", C.c_uint64), ("pin_frac", C.c_double), ("prefetch_off", C.c_int32),
-                ("lookahead_k", C.c_int32), ("interest", C.c_double), ("prefill_chunk", C.c_int32)]
+                ("lookahead_k", C.c_int32), ("interest", C.c_double), ("prefill_chunk", C.c_int32),
+                ("stats", C.c_int32)]
+
+
+class ModelStats(C.Structure):
+    """tlm_hip_model_stats (tlm_model_stats)"""
+    _fields_ = [("tokens", C.c_uint64), ("attn_ns", C.c_uint64), ("moe_ns", C.c_uint64),
+                ("expert_wait_ns", C.c_uint64), ("other_ns", C.c_uint64)]
 
 
 def model_opts(max_ctx=0, eager=False, attn_slices=0, split=False, expert_cache=0, pin_frac=0.0, prefetch=True,
-               lookahead_k=0, interest=0.0, prefill_chunk=0):
+               lookahead_k=0, interest=0.0, prefill_chunk=0, stats=False):
     """tlm_hip_model_opts; expert_cache > 0 (bytes) serves the experts through
     an HBM slot cache of that size from page-locked host memory, as tierlm's
     runtime serves them from its store (pin_frac 0 = its default 0.30,
     prefetch = its router lookahead, lookahead_k / interest its io and nav
     options); prefill_chunk: 0 batched prompts where the model allows them,
-    n > 0 at most n tokens per batch, < 0 one step per token."""
+    n > 0 at most n tokens per batch, < 0 one step per token; stats: the
+    device-timed attention / MoE / other split of tlm_model_stats."""
     return ModelOpts(max_ctx, int(eager), attn_slices, int(split), int(expert_cache), float(pin_frac),
-                     0 if prefetch else 1, int(lookahead_k), float(interest), int(prefill_chunk))
+                     0 if prefetch else 1, int(lookahead_k), float(interest), int(prefill_chunk), int(stats))
 
 
 # Qwen3-30B-A3B: 48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128
@@ -131,6 +139,15 @@ class Model:
         out = StoreStats()
         lib.tlm_hip_store_get_stats(st, C.byref(out))
         return {f: int(getattr(out, f)) for f, _ in StoreStats._fields_}
+
+    def stats(self):
+        """tlm_model_stats of the device steps (tlm_hip_model_get_stats)."""
+        out = ModelStats()
+        check(lib.tlm_hip_model_get_stats(self.h, C.byref(out)))
+        return {f: int(getattr(out, f)) for f, _ in ModelStats._fields_}
+
+    def reset_stats(self):
+        lib.tlm_hip_model_reset_stats(self.h)
 
     def routes(self):
         """The last step's routing: (ids, weights), each [n_layers, top_k] in
