@@ -19,6 +19,7 @@
  *            a 16-byte aligned vector load.  This is the HBM-bandwidth path.
  */
 #include "tlm_hip_internal.h"
+#include <type_traits>
 #include "tlm_hip_items.h"
 #include "tlm_hip_act.h"
 
@@ -487,17 +488,24 @@ int launch_tok_norm_act(int kind, const float *x, int64_t xstride, const float *
 struct MvTile {
     const uint8_t *Wp;   /* packed matrix */
     int64_t rows, t;     /* its rows; the tile this group computes */
+    int i0;              /* the first of the group's RPG rows inside the tile */
     float *y;
     const float *nx, *nw;
     float eps;
     int accum;
     unsigned long long *keys;
 };
-template <int DT, bool DEEP>
+/* RPG rows of a 16-row tile per group (16, 8 or 4): a compute unit streams
+ * only some tens of GB/s, so a matrix of few tiles (the o projection's 128)
+ * spreads its rows over more groups than tiles, each with fewer items in
+ * flight per lane */
+template <int DT, bool DEEP, int RPG>
 __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const uint8_t *__restrict__ act) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    constexpr int IPL = MvCfg<DT, DEEP>::IPL;
+    constexpr int IPL0 = MvCfg<DT, DEEP>::IPL * RPG / TILE_ROWS;
+    constexpr int IPL = IPL0 > 0 ? IPL0 : 1;
+    static_assert(RPG == 16 || RPG == 8 || RPG == 4, "rows per group");
     extern __shared__ __align__(16) uint8_t lds[];
     const uint8_t *Wp = sg.Wp;
     const int64_t rows = sg.rows, t = sg.t;
@@ -515,7 +523,7 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
         norm_act_load(kind, sg.nx, sg.nw, nb, nin);
     }
     const int cap = nb < MvCfg<DT, DEEP>::NBC ? nb : MvCfg<DT, DEEP>::NBC;
-    const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * TILE_ROWS);
+    const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * RPG);
     bool staged = !sg.nx;
     /* the activation from rmsnorm once the first weight loads are out: the
      * empty asm keeps the norm's arithmetic (and so its wait for x) below
@@ -534,31 +542,32 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     const int64_t units = T * nb * TILE_ROWS;
     const int round_items = (GROUP_THREADS / F::LPI) * IPL;
     float acc = 0.0f;
+    const int i0 = sg.i0;
     for (int b0 = 0; b0 < nb; b0 += cap) {
         const int nbc = nb - b0 < cap ? nb - b0 : cap;
-        const int nitems = nbc * TILE_ROWS;
+        const int nitems = nbc * RPG;
         for (int base = 0; base < nitems; base += round_items) {
             auto map = [&](int it, const uint8_t *&W, int64_t &un, int64_t &u, int &b, int &pk) {
-                const int g = base + it, bl = g / TILE_ROWS, i = g % TILE_ROWS;
+                const int g = base + it, bl = g / RPG, i = g % RPG;
                 W = Wp;
                 un = units;
                 b = b0 + bl;
-                u = ((int64_t)t * nb + b) * TILE_ROWS + i;
+                u = ((int64_t)t * nb + b) * TILE_ROWS + i0 + i;
                 pk = g;
             };
             run_items<DT, IPL, MvCfg<DT, DEEP>::CLAMP>(nitems - base, map, stage, park);
         }
         __syncthreads();
-        if (threadIdx.x < TILE_ROWS) acc = chain_park<AFF>(park, nbc, 0, TILE_ROWS, threadIdx.x, acc);
+        if (threadIdx.x < RPG) acc = chain_park<AFF>(park, nbc, 0, RPG, threadIdx.x, acc);
         __syncthreads();
         /* nothing is in flight here (a dropped item's load aside); a wait
          * the compiler can see keeps the loop head's counts from holding the
          * first pass's weight loads back behind the norm's x and w */
         __builtin_amdgcn_s_waitcnt(0);
     }
-    const int64_t r = t * TILE_ROWS + threadIdx.x;
-    if (threadIdx.x < TILE_ROWS && r < rows) y[r] = sg.accum ? y[r] + acc : acc;
-    if (sg.keys && threadIdx.x < 64) {   /* lanes 0..15 hold the tile's rows */
+    const int64_t r = t * TILE_ROWS + i0 + threadIdx.x;
+    if (threadIdx.x < RPG && r < rows) y[r] = sg.accum ? y[r] + acc : acc;
+    if (RPG == TILE_ROWS && sg.keys && threadIdx.x < 64) {   /* lanes 0..15 hold the tile's rows */
         unsigned long long key = threadIdx.x < TILE_ROWS && r < rows ? argmax_key(acc, (uint32_t)r) : 0ull;
         for (int o = 8; o > 0; o >>= 1) {
             const unsigned long long other = __shfl_xor(key, o, 64);
@@ -567,13 +576,32 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
         if (threadIdx.x == 0) sg.keys[t] = key;
     }
 }
-template <int DT, bool DEEP>
+/* group g -> (tile, part): work-groups go to the 8 XCDs round-robin by id,
+ * so in each run of 8 SPT ids the parts of 8 tiles go to one XCD each (ids g,
+ * g + 8, ... share the XCD, and its L2, whose lines hold neighbouring rows of
+ * a tile); ids of a last incomplete run map straight */
+template <int RPG>
+__device__ __forceinline__ void mv_group_tile(int64_t g, int64_t ngroups, int64_t &tile, int &part) {
+    constexpr int SPT = TILE_ROWS / RPG;
+    const int64_t run = g / (8 * SPT);
+    if ((run + 1) * 8 * SPT <= ngroups) {
+        tile = run * 8 + g % 8;
+        part = (int)((g / 8) % SPT);
+    } else {
+        tile = g / SPT;
+        part = (int)(g % SPT);
+    }
+}
+template <int DT, bool DEEP, int RPG>
 __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
+    int64_t tile;
+    int part;
+    mv_group_tile<RPG>(blockIdx.x, gridDim.x, tile, part);
     int s = 0;
-    while (s + 1 < sg.n && (int64_t)blockIdx.x >= sg.tile_end[s]) s++;
-    const MvTile tl{sg.W[s], sg.rows[s], (int64_t)blockIdx.x - (s ? sg.tile_end[s - 1] : 0), sg.y[s], sg.nx,
+    while (s + 1 < sg.n && tile >= sg.tile_end[s]) s++;
+    const MvTile tl{sg.W[s], sg.rows[s], tile - (s ? sg.tile_end[s - 1] : 0), part * RPG, sg.y[s], sg.nx,
                     sg.nw, sg.eps, sg.accum, sg.keys};
-    mv_packed_tile<DT, DEEP>(tl, nb, act);
+    mv_packed_tile<DT, DEEP, RPG>(tl, nb, act);
 }
 
 /* One launch for a whole job of matrices (mv_job / mv_exec,
@@ -601,16 +629,16 @@ __global__ __launch_bounds__(256) void k_mv_job(MvJob j) {
     const int64_t bid = (int64_t)blockIdx.x - g.first;
     if (g.kind == JK_PACKED || g.kind == JK_PACKED_DEEP) {
         const int nb = (int)(g.n / dt_block_values(g.dt));
-        const MvTile tl{g.W, g.rows, bid, g.y, nullptr, nullptr, 0.0f, 0, nullptr};
+        const MvTile tl{g.W, g.rows, bid, 0, g.y, nullptr, nullptr, 0.0f, 0, nullptr};
         switch (g.dt) {
         case DT_Q8_0:
-            if (g.kind == JK_PACKED_DEEP) mv_packed_tile<DT_Q8_0, true>(tl, nb, g.act);
-            else mv_packed_tile<DT_Q8_0, false>(tl, nb, g.act);
+            if (g.kind == JK_PACKED_DEEP) mv_packed_tile<DT_Q8_0, true, TILE_ROWS>(tl, nb, g.act);
+            else mv_packed_tile<DT_Q8_0, false, TILE_ROWS>(tl, nb, g.act);
             break;
-        case DT_Q4_K: mv_packed_tile<DT_Q4_K, false>(tl, nb, g.act); break;
-        case DT_Q5_K: mv_packed_tile<DT_Q5_K, false>(tl, nb, g.act); break;
-        case DT_Q6_K: mv_packed_tile<DT_Q6_K, false>(tl, nb, g.act); break;
-        case DT_Q8_K: mv_packed_tile<DT_Q8_K, false>(tl, nb, g.act); break;
+        case DT_Q4_K: mv_packed_tile<DT_Q4_K, false, TILE_ROWS>(tl, nb, g.act); break;
+        case DT_Q5_K: mv_packed_tile<DT_Q5_K, false, TILE_ROWS>(tl, nb, g.act); break;
+        case DT_Q6_K: mv_packed_tile<DT_Q6_K, false, TILE_ROWS>(tl, nb, g.act); break;
+        case DT_Q8_K: mv_packed_tile<DT_Q8_K, false, TILE_ROWS>(tl, nb, g.act); break;
         }
     } else if (g.kind == JK_PLAIN) {
         switch (g.dt) {
@@ -764,20 +792,30 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
         sg.tile_end[i] = end;
     }
     const size_t lds = packed_lds_bytes(dt, nb);
-    const dim3 g((unsigned)end), blk(256);
+    /* rows per group: whole tiles for matrices of many tiles (and for the
+     * greedy keys, one per tile), else halves or quarters of tiles so that
+     * the launch spreads over the chip */
+    const int rpg = keys || end >= 1024 ? 16 : end >= 256 ? 8 : 4;
+    const dim3 blk(256);
     const uint8_t *a = (const uint8_t *)act;
-    switch (dt) {
-    case DT_Q8_0:
-        if (mv_deep(dt, nb)) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, true>), g, blk, lds, s, sg, nb, a);
-        else hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, false>), g, blk, lds, s, sg, nb, a);
-        break;
-    case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q4_K, false>), g, blk, lds, s, sg, nb, a); break;
-    case DT_Q5_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q5_K, false>), g, blk, lds, s, sg, nb, a); break;
-    case DT_Q6_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q6_K, false>), g, blk, lds, s, sg, nb, a); break;
-    case DT_Q8_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_K, false>), g, blk, lds, s, sg, nb, a); break;
-    default: return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: dtype %d", dt);
-    }
-    return tlmh_check(hipGetLastError(), "mv_segs launch");
+    auto go = [&](auto rpg_c) -> int {
+        constexpr int R = decltype(rpg_c)::value;
+        const dim3 g((unsigned)(end * (TILE_ROWS / R)));
+        switch (dt) {
+        case DT_Q8_0:
+            if (mv_deep(dt, nb)) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, true, R>), g, blk, lds, s, sg, nb, a);
+            else hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, false, R>), g, blk, lds, s, sg, nb, a);
+            break;
+        case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q4_K, false, R>), g, blk, lds, s, sg, nb, a); break;
+        case DT_Q5_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q5_K, false, R>), g, blk, lds, s, sg, nb, a); break;
+        case DT_Q6_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q6_K, false, R>), g, blk, lds, s, sg, nb, a); break;
+        case DT_Q8_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_K, false, R>), g, blk, lds, s, sg, nb, a); break;
+        default: return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: dtype %d", dt);
+        }
+        return tlmh_check(hipGetLastError(), "mv_segs launch");
+    };
+    return rpg == 16 ? go(std::integral_constant<int, 16>{})
+           : rpg == 8 ? go(std::integral_constant<int, 8>{}) : go(std::integral_constant<int, 4>{});
 }
 
 int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s) {
