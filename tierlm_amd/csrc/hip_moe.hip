@@ -531,19 +531,19 @@ __device__ XLds wave_stage(int kind, const uint8_t *__restrict__ act, int nb, ui
  * grid: k * de/16 expert tiles (rank-major), then ds/16 shared tiles
  * LDS: NWAVE wave-private activation copies, then the park of the chunk.
  * ==================================================================== */
-template <int DT>
+template <int DT, int GR>
 __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const uint8_t *uW, const uint8_t *act,
-                            int64_t F, int64_t t, float *hh, uint8_t *lds) {
+                            int64_t F, int64_t t, int i0, float *hh, uint8_t *lds) {
     using Fm = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    constexpr int IPL = DT == DT_Q8_0 ? 8 : 4;
+    constexpr int IPL = (DT == DT_Q8_0 ? 8 : 4) * GR / TILE_ROWS;
     constexpr int kind = DT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
     const int nb = (int)(d.D / Fm::BV);
     const int wave = threadIdx.x >> 6;
     const size_t xstride = (stage_bytes(kind, nb) + 15) & ~(size_t)15;
     uint8_t *xarea = lds + xstride * wave;
     const int cb = nb < PARK_MAX / TILE_ROWS / 2 ? nb : PARK_MAX / TILE_ROWS / 2;   /* blocks per chunk */
-    const Park park = park_at(lds + xstride * NWAVE, 2 * cb * TILE_ROWS);
+    const Park park = park_at(lds + xstride * NWAVE, 2 * cb * GR);
     const int64_t T = F / TILE_ROWS, units = T * nb * TILE_ROWS;
     const int slots = GROUP_THREADS / Fm::LPI;
     bool staged = false;
@@ -551,14 +551,14 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += cb) {
         const int nbc = nb - b0 < cb ? nb - b0 : cb;
-        const int per = nbc * TILE_ROWS, nitems = 2 * per;
+        const int per = nbc * GR, nitems = 2 * per;
         for (int base = 0; base < nitems; base += slots * IPL) {
             auto map = [&](int it, const uint8_t *&W, int64_t &un, int64_t &u, int &b, int &pk) {
                 const int g = base + it, m = g >= per, rem = g - m * per;
                 W = m ? uW : gW;
                 un = units;
-                b = b0 + rem / TILE_ROWS;
-                u = (t * nb + b) * TILE_ROWS + rem % TILE_ROWS;
+                b = b0 + rem / GR;
+                u = (t * nb + b) * TILE_ROWS + i0 + rem % GR;
                 pk = g;
             };
             auto stage = [&]() {
@@ -568,17 +568,17 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
             run_items<DT, IPL>(nitems - base, map, stage, park);
         }
         __syncthreads();
-        /* threads 0-15: the gate rows' chains, 16-31: the up rows' */
-        if (threadIdx.x < 2 * TILE_ROWS) {
-            const int i = threadIdx.x & (TILE_ROWS - 1);
-            acc = chain_park<AFF>(park, nbc, threadIdx.x < TILE_ROWS ? 0 : per, TILE_ROWS, i, acc);
+        /* threads 0..GR-1: the gate rows' chains, GR..2GR-1: the up rows' */
+        if (threadIdx.x < 2 * GR) {
+            const int i = threadIdx.x & (GR - 1);
+            acc = chain_park<AFF>(park, nbc, threadIdx.x < GR ? 0 : per, GR, i, acc);
         }
         __syncthreads();
     }
-    if (threadIdx.x < 64) {   /* wave 0: up value from lane i + 16 */
-        const float up = __shfl_down(acc, TILE_ROWS, 64);
-        if (threadIdx.x < TILE_ROWS)
-            hh[t * TILE_ROWS + threadIdx.x] = acc / (1.0f + expf_ref(-acc)) * up;   /* silu(g) * u (tlm_model.c:171, 927) */
+    if (threadIdx.x < 64) {   /* wave 0: up value from lane i + GR */
+        const float up = __shfl_down(acc, GR, 64);
+        if (threadIdx.x < GR)
+            hh[t * TILE_ROWS + i0 + threadIdx.x] = acc / (1.0f + expf_ref(-acc)) * up;   /* silu(g) * u (tlm_model.c:171, 927) */
     }
 }
 
@@ -587,25 +587,30 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
 struct NoGiven {};
 template <bool GIVEN> using GivenArg = typename std::conditional<GIVEN, MoeGiven, NoGiven>::type;
 
+/* rows of a 16-row tile per routed gate/up group: half tiles, 768 groups at
+ * Qwen3-30B-A3B shape, three to a compute unit (the register cap below) */
+constexpr int GUR = 8;
 template <int EDT, int SDT, bool GIVEN>
-__global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout L, int32_t *ids_out, float *w_out,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout L, int32_t *ids_out, float *w_out,
                                                     uint8_t *ws, const GivenArg<GIVEN> gv) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ RouteLds s_route;
     args_now(d.D, d.de, d.ds, d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, d.experts, L.logits, L.route,
              L.hh, L.xe, ids_out, w_out, ws, gridDim.x);
     if constexpr (SDT != NONE) args_now(d.sg, d.su, L.xs);
-    const int te = (int)(d.de / TILE_ROWS), nexp = d.k * te;
+    constexpr int SPT = TILE_ROWS / GUR;
+    const int te = (int)(d.de / TILE_ROWS) * SPT, nexp = d.k * te;
     const bool shared = SDT != NONE && (int)blockIdx.x >= nexp;
     if constexpr (SDT != NONE) {
         if (shared) {
             const int t = (int)blockIdx.x - nexp;
             float *hh = (float *)(ws + L.hh) + (size_t)d.k * d.de;
-            gateup_tile<SDT>(d, (const uint8_t *)d.sg, (const uint8_t *)d.su, ws + L.xs, d.ds, t, hh, lds);
+            gateup_tile<SDT, TILE_ROWS>(d, (const uint8_t *)d.sg, (const uint8_t *)d.su, ws + L.xs, d.ds, t, 0, hh,
+                                        lds);
             return;
         }
     }
-    const int r = (int)blockIdx.x / te, t = (int)blockIdx.x - r * te;
+    const int r = (int)blockIdx.x / te, q = (int)blockIdx.x - r * te, t = q / SPT, i0 = (q % SPT) * GUR;
     if constexpr (GIVEN) {   /* routing and matrices given: the weight loads go out at once */
         if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
             const int q = threadIdx.x;
@@ -614,8 +619,8 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
             if (ids_out) ids_out[q] = gv.ids[q];
             if (w_out) w_out[q] = gv.w[q];
         }
-        gateup_tile<EDT>(d, gv.p[3 * r], gv.p[3 * r + 1], ws + L.xe, d.de, t, (float *)(ws + L.hh) + (size_t)r * d.de,
-                         lds);
+        gateup_tile<EDT, GUR>(d, gv.p[3 * r], gv.p[3 * r + 1], ws + L.xe, d.de, t, i0,
+                              (float *)(ws + L.hh) + (size_t)r * d.de, lds);
         return;
     }
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
@@ -644,7 +649,7 @@ __global__ __launch_bounds__(256) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout
     }
     const int e = R->ids[r];
     float *hh = (float *)(ws + L.hh) + (size_t)r * d.de;
-    gateup_tile<EDT>(d, s_gate[e], s_up[e], ws + L.xe, d.de, t, hh, lds);
+    gateup_tile<EDT, GUR>(d, s_gate[e], s_up[e], ws + L.xe, d.de, t, i0, hh, lds);
 }
 
 /* ======================================================================
@@ -1414,7 +1419,7 @@ static int moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const gateup_fn gu = GU[es][ss];
     const down_fn dn = DN[es][ss];
     const unsigned g1 = (unsigned)router_groups(*d);
-    const unsigned g2 = (unsigned)(d->k * (d->de / TILE_ROWS) + (d->ds > 0 ? d->ds / TILE_ROWS : 0));
+    const unsigned g2 = (unsigned)(d->k * (d->de / GUR) + (d->ds > 0 ? d->ds / TILE_ROWS : 0));
     const unsigned g3 = (unsigned)(d->D / DROWS);
     if (phase == 0 || phase == 1)
         hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8, (size_t)0);
