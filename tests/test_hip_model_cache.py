@@ -156,14 +156,16 @@ def test_synth_cached_equals_resident(hip, edt, shared, router):
 def test_synth_cached_heat_lookahead(hip):
     """Sigmoid routing with a Zipf-like selection bias, a pool of 6 distinct
     payloads, the lookahead with interest-weighted breadth: a cache of half
-    the experts serves most selections; hints are issued and used."""
+    the experts serves most selections; hints are issued and used.  The
+    prompt runs token by token (as the reference's runtime feeds it), so
+    every position acquires top_k experts per layer and hints the next."""
     from tierlm_amd.model import Model, bench_prompt
     g = dict(SMALL, router=2, n_layers=4)
     slot = 3 * 256 * 512 // 256 * 210   # three Q6_K matrices of 256 x 512 (no padding at 256-byte alignment)
     m = Model.synth(g, expert_dt=14, seed=9, max_ctx=96, expert_pool=6, heat_gamma=0.8,
-                    expert_cache=slot * 64, lookahead_k=8, interest=0.7)
+                    expert_cache=slot * 64, lookahead_k=8, interest=0.7, prefill_chunk=-1)
     try:
-        assert m.store_stats()["slots"] == 64
+        assert m.store_stats()["slots"] == 64 and not m.prefill_batched()
         p = bench_prompt(16, g["vocab"])
         out = m.generate(p, 48)
         assert len(out) == 48
@@ -178,22 +180,79 @@ def test_synth_cached_heat_lookahead(hip):
         m.close()
 
 
-def test_cached_prompt_matches_resident_batched(hip):
-    """A model with its experts behind the slot cache prefills one step per
-    token; the resident model batches the same prompt: the last position's
-    logits and routing agree bit for bit."""
+@pytest.mark.parametrize("edt,shared,budget,chunk", [(13, 0, TINY, 0), (14, 1, TINY, 24), (12, 0, ALL, 0),
+                                                     (14, 0, 12 * 3 * 256 * 512 // 256 * 210, 32)])
+def test_cached_prompt_batched_matches_resident(hip, edt, shared, budget, chunk):
+    """The prompt of a model with its experts behind the slot cache runs
+    batched (the chunk's experts acquired in passes of the unpinned slots:
+    top_k slots, twelve, or every expert): the last position's logits and
+    routing, and the following steps, are the resident batched model's and
+    the cached model's own step-by-step prefill's, bit for bit."""
     from tierlm_amd.model import Model, bench_prompt
-    a = Model.synth(SMALL, expert_dt=13, seed=4, max_ctx=128)
-    b = Model.synth(SMALL, expert_dt=13, seed=4, max_ctx=128, expert_cache=TINY)
+    g = dict(SMALL, n_shared=shared, d_shared=256 * shared)
+    a = Model.synth(g, expert_dt=edt, seed=4, max_ctx=128)
+    b = Model.synth(g, expert_dt=edt, seed=4, max_ctx=128, expert_cache=budget, prefill_chunk=chunk)
+    c = Model.synth(g, expert_dt=edt, seed=4, max_ctx=128, expert_cache=budget, prefill_chunk=-1)
     try:
-        assert a.prefill_batched() and not b.prefill_batched()
-        p = bench_prompt(70, SMALL["vocab"], seed=3)
-        la, lb = a.prefill(p), b.prefill(p)
+        assert a.prefill_batched() and b.prefill_batched() and not c.prefill_batched()
+        p = bench_prompt(70, g["vocab"], seed=3)
+        la, lb, lc = a.prefill(p), b.prefill(p), c.prefill(p)
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        assert np.array_equal(lc.view(np.uint32), lb.view(np.uint32))
         ia, wa = a.routes()
         ib, wb = b.routes()
         assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32))
         assert a.kv_len() == b.kv_len() == 70
+        tok = int(np.argmax(la))
+        for s in range(4):
+            la, na = a.step(tok)
+            lb, nb = b.step(tok)
+            assert na == nb and np.array_equal(la.view(np.uint32), lb.view(np.uint32)), s
+            tok = na
+        st = b.store_stats()
+        assert st["misses"] > 0
+        if budget == TINY:
+            assert st["evictions"] > 0
     finally:
         a.close()
         b.close()
+        c.close()
+
+
+@needs_c3s
+def test_c3s_cached_batched_prefill_reference_bits(hip):
+    """Qwen3-30B-A3B attention geometry, 16 experts top-8 through 8 slots,
+    the 1920-token prompt batched (two passes of 8 experts per layer and
+    chunk): the last position's top-10 logits are the reference's bit for
+    bit, then its 128 greedy tokens."""
+    from tests.test_hip_model_prefill import assert_topk, oracle_row
+    from tierlm_amd.model import Model
+    m = Model(C3S, max_ctx=2048, expert_cache=TINY)
+    try:
+        assert m.prefill_batched() and m.store_stats()["slots"] == 8
+        prompt = prompt_tokens(2048, 1920)
+        lg = m.prefill(prompt)
+        assert_topk(lg, oracle_row("c3s_oracle.jsonl", len(prompt) - 1))
+        m.reset()
+        assert m.generate(prompt, 128) == greedy_tokens("c3s_greedy.txt")
+    finally:
+        m.close()
+
+
+@needs_c5s
+def test_c5s_cached_batched_prefill_reference_bits(hip):
+    """16 query heads per key head, Q4_K experts through 8 slots, the
+    1100-token prompt batched: the reference's top-10 logits at its last
+    position and its greedy tokens."""
+    from tests.test_hip_model_prefill import assert_topk, oracle_row
+    from tierlm_amd.model import Model
+    m = Model(C5S, max_ctx=1200, expert_cache=TINY)
+    try:
+        assert m.prefill_batched()
+        prompt = prompt_tokens(2048, 1100)
+        lg = m.prefill(prompt)
+        assert_topk(lg, oracle_row("c5s_oracle.jsonl", len(prompt) - 1))
+        m.reset()
+        assert m.generate(prompt, 64) == greedy_tokens("c5s_greedy.txt")
+    finally:
+        m.close()

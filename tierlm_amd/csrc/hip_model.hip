@@ -1371,6 +1371,12 @@ struct tlm_hip_model {
     float *pf_scores = nullptr, *pf_w = nullptr;
     uint8_t *pf_act = nullptr, *pf_ws = nullptr;
     int32_t *pf_ids = nullptr;
+    /* batched prefill with the experts in the slot cache: the chunk's routing
+     * on the host (page-locked) and one expert table per pass (page-locked
+     * staging, device copies) */
+    int32_t *pf_host_ids = nullptr;
+    const void **pf_host_tab = nullptr;
+    const void **pf_dev_tab = nullptr;
 
     void *dalloc(size_t n) {
         void *p = nullptr;
@@ -1396,6 +1402,8 @@ struct tlm_hip_model {
             if (g) (void)hipGraphExecDestroy(g);
         for (void *p : allocs) (void)hipFree(p);
         if (host_tok) (void)hipHostFree(host_tok);
+        if (pf_host_ids) (void)hipHostFree(pf_host_ids);
+        if (pf_host_tab) (void)hipHostFree(pf_host_tab);
         if (xs_payload) (void)hipHostFree(xs_payload);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -2024,7 +2032,7 @@ bool pf_dense_ok(const DevMat &m) {
 }
 bool pf_supported(const tlm_hip_model *M) {
     const tlm_hip_model_geom &g = M->g;
-    if (M->pf_chunk < 0 || M->xs || M->att_split || M->pf_nomem) return false;
+    if (M->pf_chunk < 0 || M->att_split || M->pf_nomem) return false;
     if (!pf_att_supported((int)g.head_dim, (int)g.n_heads, (int)g.n_kv_heads)) return false;
     if (g.d_model % 256 || ((int64_t)g.n_heads * g.head_dim) % 256 || g.d_model > 8192 ||
         (int64_t)g.n_heads * g.head_dim > 8192)
@@ -2032,7 +2040,7 @@ bool pf_supported(const tlm_hip_model *M) {
     for (const Layer &Ly : M->L) {
         if (!pf_dense_ok(Ly.q) || !pf_dense_ok(Ly.k) || !pf_dense_ok(Ly.v) || !pf_dense_ok(Ly.o)) return false;
         const int edt = Ly.moe.expert_dt;
-        if ((edt != DT_Q4_K && edt != DT_Q5_K && edt != DT_Q6_K) || !Ly.moe.experts) return false;
+        if ((edt != DT_Q4_K && edt != DT_Q5_K && edt != DT_Q6_K) || (!Ly.moe.experts && !M->xs)) return false;
         const int sdt = Ly.moe.shared_dt;
         if (Ly.moe.ds > 0 && ((sdt != DT_Q4_K && sdt != DT_Q5_K && sdt != DT_Q6_K && sdt != DT_Q8_0) || Ly.moe.ds % 256))
             return false;
@@ -2072,14 +2080,28 @@ int pf_alloc(tlm_hip_model *M) {
     M->pf_ws = (uint8_t *)M->dalloc(ws);
     M->pf_ids = (int32_t *)M->dalloc((size_t)cap * g.top_k * 4);
     M->pf_w = (float *)M->dalloc((size_t)cap * g.top_k * 4);
+    bool host_ok = true;
+    if (M->xs) {   /* the routing back on the host; an expert table per pass, at most one pass per expert */
+        const size_t tab = (size_t)g.n_experts * 3 * g.n_experts * sizeof(void *);
+        host_ok = hipHostMalloc((void **)&M->pf_host_ids, (size_t)cap * g.top_k * 4, hipHostMallocDefault) ==
+                      hipSuccess &&
+                  hipHostMalloc((void **)&M->pf_host_tab, tab, hipHostMallocDefault) == hipSuccess;
+        M->pf_dev_tab = (const void **)M->dalloc(tab);
+        host_ok = host_ok && M->pf_dev_tab;
+    }
     if (!M->pf_h || !M->pf_q || !M->pf_kx || !M->pf_vx || !M->pf_att || !M->pf_y || !M->pf_scores || !M->pf_act ||
-        !M->pf_ws || !M->pf_ids || !M->pf_w) {
+        !M->pf_ws || !M->pf_ids || !M->pf_w || !host_ok) {
+        (void)hipGetLastError();
         for (void **p : {(void **)&M->pf_h, (void **)&M->pf_q, (void **)&M->pf_kx, (void **)&M->pf_vx,
                          (void **)&M->pf_att, (void **)&M->pf_y, (void **)&M->pf_scores, (void **)&M->pf_act,
-                         (void **)&M->pf_ws, (void **)&M->pf_ids, (void **)&M->pf_w}) {
+                         (void **)&M->pf_ws, (void **)&M->pf_ids, (void **)&M->pf_w, (void **)&M->pf_dev_tab}) {
             M->dfree(*p);
             *p = nullptr;
         }
+        if (M->pf_host_ids) (void)hipHostFree(M->pf_host_ids);
+        if (M->pf_host_tab) (void)hipHostFree(M->pf_host_tab);
+        M->pf_host_ids = nullptr;
+        M->pf_host_tab = nullptr;
         M->pf_nomem = true;
         return tlmh_seterr(TLM_HIP_ENOMEM, "model prefill: out of device memory (%lld-token chunks)", (long long)cap);
     }
@@ -2100,6 +2122,66 @@ int pf_matmul(tlm_hip_model *M, const DevMat &W, const float *x, int64_t n, cons
         *act_kind = rc ? -1 : kind;
     }
     if (!rc) rc = launch_tokmm(W.dt, W.p, W.rows, n, M->pf_act, nt, y, M->stream);
+    return rc;
+}
+
+/* Layer l's MoE block for the chunk's nt tokens with the experts in the slot
+ * cache: the routing stage, the (token, rank) expert ids back on the host, the
+ * union of the chunk's experts in the order the steps would first select them
+ * (token by token, rank order), acquired in passes of as many experts as the
+ * unpinned slots hold (each pass's loads waited for on the stream, its expert
+ * table - the pass's matrices, null for every other expert - copied up, the
+ * grouped expert work for its experts, its slots released behind that work),
+ * then the rank-order combine.  The (token, rank) results are the resident
+ * block's bits whatever the pass split. */
+int pf_moe_cached(tlm_hip_model *M, uint32_t l, int nt) {
+    const tlm_hip_model_geom &g = M->g;
+    hipStream_t s = M->stream;
+    const int k = (int)g.top_k, E = (int)g.n_experts;
+    tlm_hip_moe_desc d = M->descs[l];
+    int rc = launch_moe_prefill_route(&d, M->pf_h, nt, M->pf_ids, M->pf_w, M->pf_ws, s);
+    if (!rc)
+        rc = tlmh_check(hipMemcpyAsync(M->pf_host_ids, M->pf_ids, (size_t)nt * k * 4, hipMemcpyDeviceToHost, s),
+                        "model prefill: routes");
+    if (!rc) rc = tlmh_check(hipStreamSynchronize(s), "model prefill: routes");
+    if (rc) return rc;
+    std::vector<int> order;
+    std::vector<char> seen(E, 0);
+    for (int i = 0; i < nt * k; i++) {
+        const int e = M->pf_host_ids[i];
+        if (e < 0 || e >= E) return tlmh_seterr(TLM_HIP_EIO, "model prefill: routing produced expert %d of %d", e, E);
+        if (!seen[e]) {
+            seen[e] = 1;
+            order.push_back(e);
+        }
+    }
+    tlm_hip_store_stats ss;
+    tlm_hip_store_get_stats(M->xs, &ss);
+    const int per = std::max(1, ss.slots - ss.pinned);
+    const size_t tabn = (size_t)3 * E;
+    std::vector<tlm_hip_expert_ref> refs;
+    for (int p0 = 0, pass = 0; p0 < (int)order.size() && !rc; p0 += per, pass++) {
+        const int np = std::min(per, (int)order.size() - p0);
+        refs.assign(np, tlm_hip_expert_ref{});
+        rc = tlm_hip_store_acquire(M->xs, (int)l, order.data() + p0, np, refs.data());
+        for (int i = 0; i < np && !rc; i++) rc = tlm_hip_store_stream_wait(M->xs, &refs[i], s);
+        const void **ht = M->pf_host_tab + (size_t)pass * tabn;
+        const void **dt = M->pf_dev_tab + (size_t)pass * tabn;
+        if (!rc) {
+            for (size_t i = 0; i < tabn; i++) ht[i] = nullptr;
+            for (int i = 0; i < np; i++)
+                for (int m = 0; m < 3; m++) ht[3 * (size_t)order[p0 + i] + m] = refs[i].mats[m];
+            rc = tlmh_check(hipMemcpyAsync(dt, ht, tabn * sizeof(void *), hipMemcpyHostToDevice, s),
+                            "model prefill: expert table");
+        }
+        if (!rc) {
+            d.experts = dt;
+            rc = launch_moe_prefill_experts(&d, nt, M->pf_ws, s);
+        }
+        for (int i = 0; i < np; i++)
+            if (refs[i].slot >= 0) tlm_hip_store_release(M->xs, &refs[i], s);
+    }
+    if (!rc) rc = launch_moe_prefill_combine(&d, M->pf_h, nt, M->pf_ws, s);
     return rc;
 }
 
@@ -2158,8 +2240,15 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
                 rc = tlmh_check(hipGetLastError(), "model prefill: residual");
             }
             stamp(M, 2 + 2 * (size_t)l);
-            if (!rc) rc = launch_moe_prefill(&Ly.moe, M->pf_h, nt, M->pf_ids, M->pf_w, M->pf_ws, s);
-            if (!rc && c0 + nt == n) {   /* the last token's routing, as the step leaves it */
+            if (!rc)
+                rc = M->xs ? pf_moe_cached(M, l, nt)
+                           : launch_moe_prefill(&Ly.moe, M->pf_h, nt, M->pf_ids, M->pf_w, M->pf_ws, s);
+            if (!rc && c0 + nt == n && M->xs) {   /* the last token's routing, on the host as the cached step keeps it */
+                for (int r = 0; r < k; r++)
+                    M->route_ids[(size_t)l * k + r] = M->pf_host_ids[(size_t)(nt - 1) * k + r];
+                rc = tlmh_check(hipMemcpyAsync(M->route_w.data() + (size_t)l * k, M->pf_w + (size_t)(nt - 1) * k,
+                                               (size_t)k * 4, hipMemcpyDeviceToHost, s), "model prefill: routes");
+            } else if (!rc && c0 + nt == n) {   /* the last token's routing, as the step leaves it */
                 rc = tlmh_check(hipMemcpyAsync(M->ids + (size_t)l * 32, M->pf_ids + (size_t)(nt - 1) * k, (size_t)k * 4,
                                                hipMemcpyDeviceToDevice, s), "model prefill: routes");
                 if (!rc)
@@ -2181,6 +2270,8 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
     if (!rc) {
         M->kv_len = p0 + n;
         M->st_tokens += (uint64_t)n;
+        if (M->xs)   /* the steps' store ticks (tlm_model.c:1097), one per token */
+            for (int i = 0; i < n; i++) tlm_hip_store_tick(M->xs);
     }
     return rc;
 }

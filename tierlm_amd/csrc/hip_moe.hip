@@ -171,7 +171,7 @@ __device__ __forceinline__ uint32_t ord_bits(float f) {
  * at kernel entry. */
 template <class Stash>
 __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, LAS RouteLds *R, Stash stash,
-                            bool weights = true) {
+                            const ExpTabLanes &tab, bool weights = true) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, E = d.E, k = d.k;
     const bool sig = d.router == 2;
     const bool in = t < E;
@@ -180,7 +180,7 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
     const float bias = (sig && in && d.router_bias) ? ((const GAS float *)d.router_bias)[t] : 0.0f;
     float p;
     if (sig) {   /* sigmoid score = weight; bias for selection only */
-        p = 1.0f / (1.0f + expf_ref(-l));
+        p = 1.0f / (1.0f + expf_ref_with(-l, tab));
     } else {     /* softmax over the routable experts */
         float m = wave_max_f32((unmasked && l > -INFINITY) ? l : -INFINITY);
         if (lane == 0) R->redf[wave] = m;
@@ -189,7 +189,8 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
 #pragma unroll
         for (int q = 1; q < NWAVE; q++) mx = R->redf[q] > mx ? R->redf[q] : mx;
         const bool off = !unmasked || l != l || mx == -INFINITY;
-        const float x = off ? 0.0f : expf_ref(l - mx);
+        const float ex = expf_ref_with(l - mx, tab);   /* every lane: the table lives in the lanes */
+        const float x = off ? 0.0f : ex;
         const double s = wave_sum_f64((double)x);
         if (lane == 0) R->red[wave] = s;
         __syncthreads();
@@ -218,13 +219,16 @@ __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, 
     if (ke != 0ull) {
         if (split) {
             const LAS u32x4 *kp = (const LAS u32x4 *)(R->key + (t >= 128 ? 64 : 0));
+            int cc[4] = {0, 0, 0, 0};   /* independent counts: no chain through one register */
 #pragma unroll
             for (int j = 0; j < 32; j++) {
                 const u32x4 w = kp[j];
                 const unsigned long long a = ((unsigned long long)w.y << 32) | w.x;
                 const unsigned long long b = ((unsigned long long)w.w << 32) | w.z;
-                c += (a > ke ? 1 : 0) + (b > ke ? 1 : 0);
+                cc[(2 * j) & 3] += a > ke ? 1 : 0;
+                cc[(2 * j + 1) & 3] += b > ke ? 1 : 0;
             }
+            c = (cc[0] + cc[1]) + (cc[2] + cc[3]);
         } else {
 #pragma unroll 16
             for (int f = 0; f < E; f++) c += R->key[f] > ke ? 1 : 0;
@@ -533,7 +537,7 @@ __device__ XLds wave_stage(int kind, const uint8_t *__restrict__ act, int nb, ui
  * ==================================================================== */
 template <int DT, int GR>
 __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const uint8_t *uW, const uint8_t *act,
-                            int64_t F, int64_t t, int i0, float *hh, uint8_t *lds) {
+                            int64_t F, int64_t t, int i0, float *hh, uint8_t *lds, const ExpTabLanes &tab) {
     using Fm = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
     constexpr int IPL = (DT == DT_Q8_0 ? 8 : 4) * GR / TILE_ROWS;
@@ -575,10 +579,10 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
         }
         __syncthreads();
     }
-    if (threadIdx.x < 64) {   /* wave 0: up value from lane i + GR */
+    if (threadIdx.x < 64) {   /* wave 0: up value from lane i + GR; e^x in every lane */
         const float up = __shfl_down(acc, GR, 64);
-        if (threadIdx.x < GR)
-            hh[t * TILE_ROWS + i0 + threadIdx.x] = acc / (1.0f + expf_ref(-acc)) * up;   /* silu(g) * u (tlm_model.c:171, 927) */
+        const float hv = acc / (1.0f + expf_ref_with(-acc, tab)) * up;   /* silu(g) * u (tlm_model.c:171, 927) */
+        if (threadIdx.x < GR) hh[t * TILE_ROWS + i0 + threadIdx.x] = hv;
     }
 }
 
@@ -598,6 +602,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     args_now(d.D, d.de, d.ds, d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, d.experts, L.logits, L.route,
              L.hh, L.xe, ids_out, w_out, ws, gridDim.x);
     if constexpr (SDT != NONE) args_now(d.sg, d.su, L.xs);
+    ExpTabLanes tab;   /* e^x's table in the lanes (routing, SwiGLU): no global read on the way */
+    tab.load();
     constexpr int SPT = TILE_ROWS / GUR;
     const int te = (int)(d.de / TILE_ROWS) * SPT, nexp = d.k * te;
     const bool shared = SDT != NONE && (int)blockIdx.x >= nexp;
@@ -606,7 +612,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             const int t = (int)blockIdx.x - nexp;
             float *hh = (float *)(ws + L.hh) + (size_t)d.k * d.de;
             gateup_tile<SDT, TILE_ROWS>(d, (const uint8_t *)d.sg, (const uint8_t *)d.su, ws + L.xs, d.ds, t, 0, hh,
-                                        lds);
+                                        lds, tab);
             return;
         }
     }
@@ -620,7 +626,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             if (w_out) w_out[q] = gv.w[q];
         }
         gateup_tile<EDT, GUR>(d, gv.p[3 * r], gv.p[3 * r + 1], ws + L.xe, d.de, t, i0,
-                              (float *)(ws + L.hh) + (size_t)r * d.de, lds);
+                              (float *)(ws + L.hh) + (size_t)r * d.de, lds, tab);
         return;
     }
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
@@ -639,7 +645,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             s_gate[tid] = tg;
             s_up[tid] = tu;
         },
-        blockIdx.x == 0);
+        tab, blockIdx.x == 0);
     if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
         const int q = threadIdx.x;
         ws_ids(ws, L)[q] = R->ids[q];
@@ -649,7 +655,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     }
     const int e = R->ids[r];
     float *hh = (float *)(ws + L.hh) + (size_t)r * d.de;
-    gateup_tile<EDT, GUR>(d, s_gate[e], s_up[e], ws + L.xe, d.de, t, i0, hh, lds);
+    gateup_tile<EDT, GUR>(d, s_gate[e], s_up[e], ws + L.xe, d.de, t, i0, hh, lds, tab);
 }
 
 /* ======================================================================
@@ -1014,10 +1020,12 @@ __global__ __launch_bounds__(256) void k_pf_route(tlm_hip_moe_desc d, WsLayout L
     __shared__ RouteLds s_route;
     args_now(d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, L.logits, P.tok, P.tstride, P.pair_e,
              P.pair_w, ws, ids_out, w_out);
+    ExpTabLanes tab;
+    tab.load();
     const int t = blockIdx.x;
     const uint8_t *wst = ws + P.tok + (size_t)t * P.tstride;
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
-    route_group(d, (const GAS float *)(wst + L.logits), R, []() {});
+    route_group(d, (const GAS float *)(wst + L.logits), R, []() {}, tab);
     if ((int)threadIdx.x < d.k) {
         const int q = threadIdx.x;
         const size_t pr = (size_t)t * d.k + q;
@@ -1036,8 +1044,10 @@ __global__ __launch_bounds__(256) void k_moe_route(tlm_hip_moe_desc d, WsLayout 
                                                    float *w_out) {
     __shared__ RouteLds s_route;
     args_now(d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, L.logits, L.route, ws, ids_out, w_out);
+    ExpTabLanes tab;
+    tab.load();
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
-    route_group(d, (const GAS float *)(ws + L.logits), R, []() {});
+    route_group(d, (const GAS float *)(ws + L.logits), R, []() {}, tab);
     if ((int)threadIdx.x < d.k) {
         const int q = threadIdx.x;
         ws_ids(ws, L)[q] = R->ids[q];
@@ -1060,8 +1070,10 @@ __global__ __launch_bounds__(256) void k_moe_route_host(const RouteSet S, uint32
     __shared__ RouteLds s_route;
     const int i = blockIdx.x;
     const tlm_hip_moe_desc &d = S.d[i];
+    ExpTabLanes tab;
+    tab.load();
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
-    route_group(d, (const GAS float *)(S.ws[i] + S.L[i].logits), R, []() {});
+    route_group(d, (const GAS float *)(S.ws[i] + S.L[i].logits), R, []() {}, tab);
     const int q = threadIdx.x;
     if (q < 32) {
         const bool on = q < d.k;
@@ -1182,6 +1194,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int tok = ((const GAS int32_t *)(ws + P.slot_tok))[slot];
     const GAS uint8_t *x = (const GAS uint8_t *)(ws + P.tok + (size_t)tok * P.tstride + L.xe);
     const GAS uint64_t *xt = (const GAS uint64_t *)d.experts;
+    if (!xt[3 * e]) return;   /* an expert outside this pass (its matrices in no slot): uniform over the group */
     const tokmm::Chain ch = tokmm::chain_at<DT>((const uint8_t *)xt[3 * e + up], units, ubase);
     float acc[16];
     tokmm::tile_run<DT, true>(ch, nb, x, (LAS uint8_t *)s_tile, acc);
@@ -1239,6 +1252,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int slot = s0 + (js < n ? js : n - 1);
     const GAS uint8_t *x = (const GAS uint8_t *)(ws + P.hq + (size_t)slot * P.hq_stride);
     const uint8_t *wd = (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * e + 2];
+    if (!wd) return;   /* an expert outside this pass: uniform over the group */
     const tokmm::Chain ch = tokmm::chain_at<DT>(wd, units, (rr / TILE_ROWS) * nb * TILE_ROWS + rr % TILE_ROWS);
     float acc[16];
     tokmm::tile_run<DT, true>(ch, nb, x, (LAS uint8_t *)s_tile, acc);
@@ -1488,21 +1502,35 @@ size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T) {
 /* T tokens: norm + quantisation per token, batched router logits, routing per
  * token, bucketing, gate/up + SwiGLU,
  * h quantisation, down, combine. */
-int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
-                       hipStream_t s) {
-    if (int rc = moe_check(d, h, ws)) return rc;
+static int moe_prefill_check(const tlm_hip_moe_desc *d, const float *h, int64_t T, const void *ws, bool table) {
+    if (int rc = moe_check(d, h, ws, table)) return rc;
     if (T <= 0 || T > 65536) return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld outside 1..65536", (long long)T);
     if ((d->expert_dt != DT_Q4_K && d->expert_dt != DT_Q5_K && d->expert_dt != DT_Q6_K) ||
         (d->ds > 0 && (!tokmm::tile_dt(d->shared_dt) || d->ds % 256 || d->D % 256)))
         return tlmh_seterr(TLM_HIP_EUNSUP, "moe_prefill: routed Q4_K / Q5_K / Q6_K experts, a shared expert of "
                            "Q4_K / Q5_K / Q6_K / Q8_0 and widths a multiple of 256 only (expert dtype %d, shared "
                            "dtype %d, ds %lld)", d->expert_dt, d->shared_dt, (long long)d->ds);
+    if (pf_layout(*d, T).MT > 65536)   /* the tile grids' y */
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld x k=%d gives more than 65536 tiles", (long long)T,
+                           d->k);
+    return TLM_HIP_OK;
+}
+
+/* The prefill block in three stages, so that a caller whose experts come
+ * through the slot cache can acquire them between the routing and the
+ * expert work, and run the expert work in passes of the experts it holds:
+ * route = norm, router logits, the shared expert, routing (ids / w per
+ * (token, rank)), bucketing; experts = grouped gate/up, h quantisation,
+ * grouped down for the tiles whose expert has matrices in d->experts (a
+ * null entry skips the expert's tiles; every (token, rank) slot belongs to
+ * one expert, so passes over disjoint expert sets fill disjoint slots);
+ * combine = the rank-order sum into h. */
+int launch_moe_prefill_route(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
+                             hipStream_t s) {
+    if (int rc = moe_prefill_check(d, h, T, ws, false)) return rc;
     const tlm_hip_moe_desc dv = *d;
     const WsLayout L = ws_layout(*d);
     const PfLayout P = pf_layout(*d, T);
-    if (P.MT > 65536)   /* the tile grids' y */
-        return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: T=%lld x k=%d gives %d tiles, more than 65536", (long long)T,
-                           d->k, P.MT);
     uint8_t *w8 = (uint8_t *)ws;
     hipLaunchKernelGGL(k_pf_norm, dim3((unsigned)(d->D / 256), (unsigned)T), dim3(64), 0, s, dv, L, P, (const float *)h,
                        w8);
@@ -1531,6 +1559,15 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
     }
     hipLaunchKernelGGL(k_pf_route, dim3((unsigned)T), dim3(256), 0, s, dv, L, P, w8, ids, w);
     hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(256), 0, s, dv, P, w8);
+    return tlmh_check(hipGetLastError(), "moe_prefill launch");
+}
+
+int launch_moe_prefill_experts(const tlm_hip_moe_desc *d, int64_t T, void *ws, hipStream_t s) {
+    if (!d || !d->experts) return tlmh_seterr(TLM_HIP_EINVAL, "moe_prefill: no expert table");
+    const tlm_hip_moe_desc dv = *d;
+    const WsLayout L = ws_layout(*d);
+    const PfLayout P = pf_layout(*d, T);
+    uint8_t *w8 = (uint8_t *)ws;
     const dim3 ggu((unsigned)((d->de + 63) / 64), (unsigned)P.MT), gdn((unsigned)((d->D + 127) / 128), (unsigned)P.MT);
     switch (d->expert_dt) {
     case DT_Q4_K: hipLaunchKernelGGL(k_pf_gateup<DT_Q4_K>, ggu, dim3(256), 0, s, dv, L, P, w8); break;
@@ -1543,7 +1580,22 @@ int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *
     case DT_Q5_K: hipLaunchKernelGGL(k_pf_down<DT_Q5_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
     default: hipLaunchKernelGGL(k_pf_down<DT_Q6_K>, gdn, dim3(256), 0, s, dv, P, w8); break;
     }
-    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((d->D + 1023) / 1024), (unsigned)T), dim3(256), 0, s, dv, P, h,
-                       w8);
     return tlmh_check(hipGetLastError(), "moe_prefill launch");
+}
+
+int launch_moe_prefill_combine(const tlm_hip_moe_desc *d, float *h, int64_t T, void *ws, hipStream_t s) {
+    const tlm_hip_moe_desc dv = *d;
+    const PfLayout P = pf_layout(*d, T);
+    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((d->D + 1023) / 1024), (unsigned)T), dim3(256), 0, s, dv, P, h,
+                       (uint8_t *)ws);
+    return tlmh_check(hipGetLastError(), "moe_prefill launch");
+}
+
+int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
+                       hipStream_t s) {
+    if (int rc = moe_prefill_check(d, h, T, ws, true)) return rc;
+    int rc = launch_moe_prefill_route(d, h, T, ids, w, ws, s);
+    if (!rc) rc = launch_moe_prefill_experts(d, T, ws, s);
+    if (!rc) rc = launch_moe_prefill_combine(d, h, T, ws, s);
+    return rc;
 }

@@ -281,6 +281,10 @@ __host__ __device__ inline int argmax_index(unsigned long long key) {
 size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T);
 int launch_moe_prefill(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
                        hipStream_t s);
+int launch_moe_prefill_route(const tlm_hip_moe_desc *d, float *h, int64_t T, int32_t *ids, float *w, void *ws,
+                             hipStream_t s);
+int launch_moe_prefill_experts(const tlm_hip_moe_desc *d, int64_t T, void *ws, hipStream_t s);
+int launch_moe_prefill_combine(const tlm_hip_moe_desc *d, float *h, int64_t T, void *ws, hipStream_t s);
 int launch_tokmm(int dt, const void *Wp, int64_t rows, int64_t n, const void *act, int64_t ntok, float *Y,
                  hipStream_t s);
 /* up to 4 matrices of one dtype and width n against the same ntok tokens in
