@@ -14,7 +14,10 @@ that reads slots carries the resident block's bits, so:
   for each expert dtype, with and without a shared expert;
 * the counters move as a cache's should (evictions on a cache of top_k
   slots, hits and misses, lookahead hints issued and used), and a routing
-  heat plus the interest-weighted lookahead run."""
+  heat plus the interest-weighted lookahead run;
+* a prompt runs batched through the cache (each chunk's experts acquired in
+  passes of the unpinned slots) with the resident batched prefill's and the
+  cached step-by-step prefill's bits, and the C3S / C5S references' logits."""
 import numpy as np
 import pytest
 
