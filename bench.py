@@ -457,7 +457,7 @@ QWEN3_235B_A22B = dict(n_layers=94, d_model=4096, n_heads=64, n_kv_heads=4, head
                       rope_theta=1e6, norm_eps=1e-6, routed_scale=1.0)
 
 
-def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gamma=0.14):
+def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gamma=0.14, pf_len=512):
     """The whole Qwen3-235B-A22B-shaped model (94 layers, hidden 4096, 64 q / 4
     kv heads x 128 with qk-norm, 128 experts top-8 of width 1536 in Q4_K,
     Q8_0 dense and lm_head, vocabulary 151936, random init) decoding with its
@@ -469,10 +469,14 @@ def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gam
     experts; the reference runtime's store defaults (pin share 0.30, router
     lookahead one layer ahead, top_k hints).  A prompt, `warm` greedy tokens
     to fill the cache, then `tokens` timed greedy tokens (host clock around
-    the steps: every layer waits for its routing on the host)."""
+    the steps: every layer waits for its routing on the host).  Then, from an
+    empty context and the cache as decoding left it, a `pf_len`-token prompt
+    prefilled batched through the cache (each layer's union of the prompt's
+    experts acquired once), host clock around tlm_hip_model_prefill."""
     from tierlm_amd.model import Model, bench_prompt
     t0 = time.perf_counter()
-    m = Model.synth(QWEN3_235B_A22B, expert_dt=Q4_K, dense_dt=8, seed=11, max_ctx=prompt_len + warm + tokens + 8,
+    m = Model.synth(QWEN3_235B_A22B, expert_dt=Q4_K, dense_dt=8, seed=11,
+                    max_ctx=max(prompt_len + warm + tokens, pf_len) + 8,
                     expert_pool=pool, heat_gamma=gamma, expert_cache=int(cache_gb * (1 << 30)))
     built = time.perf_counter() - t0
     try:
@@ -486,6 +490,15 @@ def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gam
         m.sync()
         dt = time.perf_counter() - h0
         s1 = m.store_stats()
+        assert m.prefill_batched()
+        m.reset()
+        pp = bench_prompt(pf_len, QWEN3_235B_A22B["vocab"], seed=7)
+        m.sync()
+        h1 = time.perf_counter()
+        m.prefill(pp, logits=False)
+        m.sync()
+        pf_dt = time.perf_counter() - h1
+        s2 = m.store_stats()
     finally:
         m.close()
     L, K = QWEN3_235B_A22B["n_layers"], QWEN3_235B_A22B["top_k"]
@@ -500,11 +513,20 @@ def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gam
          "ms_per_token": round(dt / tokens * 1e3, 2), "misses_per_token": round(miss, 2),
          "hit_rate": round(1.0 - miss / (L * K), 4), "prefetch_issued_per_token": round(pre, 2),
          "load_GBps": round((miss + pre) * plen * tokens / dt / 1e9, 2), "build_s": round(built, 1),
+         "prefill": {"prompt": pf_len, "ms": round(pf_dt * 1e3, 1), "tok_s": round(pf_len / pf_dt, 1),
+                     "acquires": s2["hits"] + s2["misses"] - s1["hits"] - s1["misses"],
+                     "misses": s2["misses"] - s1["misses"],
+                     "load_GBps": round((s2["misses"] - s1["misses"]) * plen / pf_dt / 1e9, 2),
+                     "timing": "host wall clock around tlm_hip_model_prefill of the prompt (batched, 1024-token "
+                               "chunks, each layer's union of the chunk's experts through the cache) and a sync"},
          "timing": "host wall clock around tlm_hip_model_decode of the timed tokens and a sync, after the prompt and "
                    "the warm-up tokens"}
     log(f"bench: Qwen3-235B-A22B-shape whole model through the slot cache ({r['slots']} slots, {cache_gb:.0f} GB): {r['tok_s']:.2f} tok/s "
         f"({r['ms_per_token']:.2f} ms/token), {r['misses_per_token']:.2f} misses/token (hit rate {r['hit_rate']:.4f}), "
         f"{r['prefetch_issued_per_token']:.1f} lookahead loads/token, {r['load_GBps']:.2f} GB/s over PCIe")
+    q = r["prefill"]
+    log(f"bench: Qwen3-235B-A22B-shape {pf_len}-token prompt batched through the slot cache: {q['ms']:.1f} ms = "
+        f"{q['tok_s']:.1f} tok/s, {q['acquires']} acquires, {q['misses']} misses ({q['load_GBps']:.2f} GB/s over PCIe)")
     return r
 
 

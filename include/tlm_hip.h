@@ -341,11 +341,20 @@ int tlm_hip_moe_layer_store(const tlm_hip_moe_desc *d, tlm_hip_store *s, int lay
  * breadth weighted as :863-874 (W = interest (1 - I) (1 - H), I the layer's
  * instinct averaged with the current top-1 share, H its heat), the instinct
  * update of :974-980, and one tlm_hip_store_tick at the end (:1097).
- * Pipelined: the host waits for each layer's routing through a sequence word
- * the export stores last (no stream synchronisation), and layer l + 1's
- * routing is queued right behind layer l's block, so the device idles only
- * while the host acquires.  descs[l]: layer l's block (its expert table
- * is not used); ids / w (n_layers x top_k,
+ * Pipelined: by default each layer's block is enqueued with its routing and
+ * reads the slots its routing export found in the store's expert -> slot
+ * table (mapped host memory; an entry is published by its load once the
+ * bytes have landed and cleared when its slot is chosen as a victim), while
+ * the host replays the layer's acquire, hints and release from the export in
+ * the reference's order; a layer whose routed experts have not all landed is
+ * handed back by the export and run by the host behind it, as below.
+ * Nothing on the device waits on the host.  With host_routes = 1 (or a store
+ * whose experts differ in layout) the host waits for each layer's routing
+ * through a sequence word the export stores last, acquires and launches the
+ * block with the slots' matrices, layer l + 1's routing queued right behind
+ * layer l's block.  The store operations and results are the same either
+ * way.  descs[l]:
+ * layer l's block (its expert table is not used); ids / w (n_layers x top_k,
  * host, may be NULL) receive the routing; workspace: 256-byte aligned,
  * tlm_hip_moe_stack_workspace_bytes bytes.  On an error at layer l the
  * layers before it have updated h and every reference is released. */
@@ -356,6 +365,7 @@ typedef struct {
     const float *layer_heat;     /* per layer, or NULL (0) */
     double      *instinct;       /* per layer, the caller's state (tlm_model's instinct), or NULL */
     uint32_t    *instinct_seen;  /* per layer, or NULL */
+    int32_t      host_routes;    /* 1: the host resolves each layer's slots (see above); 0: the device */
 } tlm_hip_stack_opts;
 size_t tlm_hip_moe_stack_workspace_bytes(const tlm_hip_moe_desc *descs, int n_layers, const tlm_hip_stack_opts *o);
 int    tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
@@ -480,6 +490,12 @@ typedef struct {
      * tlm_model_get_stats reports (src/lib/tlm_model.h:86-90, filled at
      * src/lib/tlm_model.c:1099-1101); 0: no stamps */
     int32_t  stats;
+    /* With expert_cache_bytes: 1 = the host resolves each layer's slots
+     * between its routing and its block (tlm_hip_stack_opts.host_routes);
+     * 0 = the routing export resolves them from the store's table and the
+     * block is already queued, the host replaying the store operations
+     * behind it (a layer with an expert not yet landed runs as with 1) */
+    int32_t  host_routes;
 } tlm_hip_model_opts;
 int  tlm_hip_model_open(const char *manifest_path, const tlm_hip_model_opts *o, tlm_hip_model **out);
 void tlm_hip_model_close(tlm_hip_model *M);

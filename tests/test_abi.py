@@ -38,7 +38,7 @@ def test_python_binding_covers_header():
 
 def test_struct_layouts_match_c():
     from tierlm_amd._lib import (ExpertRef, ExpertSrc, ModelGeom, ModelSynthOpts, MoeDesc, PacketLoc, QuantKernels,
-                                 Seg, StoreOpts, StoreStats, TensorRef)
+                                 Seg, StackOpts, StoreOpts, StoreStats, TensorRef)
     from tierlm_amd.model import ModelOpts, ModelStats
     prog = r'''
 #include <stdio.h>
@@ -67,7 +67,9 @@ int main(void) {
   O(tlm_hip_model_synth_opts, qk_norm); O(tlm_hip_model_synth_opts, seed); O(tlm_hip_model_synth_opts, heat_gamma);
   O(tlm_hip_model_opts, attn_split); O(tlm_hip_model_opts, expert_cache_bytes); O(tlm_hip_model_opts, pin_frac);
   O(tlm_hip_model_opts, lookahead_k); O(tlm_hip_model_opts, interest); O(tlm_hip_model_opts, prefill_chunk);
-  O(tlm_hip_model_opts, stats);
+  O(tlm_hip_model_opts, stats); O(tlm_hip_model_opts, host_routes);
+  printf("sopts %zu\n", sizeof(tlm_hip_stack_opts));
+  O(tlm_hip_stack_opts, interest); O(tlm_hip_stack_opts, instinct_seen); O(tlm_hip_stack_opts, host_routes);
   printf("mstats %zu\n", sizeof(tlm_hip_model_stats));
   O(tlm_hip_model_stats, attn_ns); O(tlm_hip_model_stats, expert_wait_ns); O(tlm_hip_model_stats, other_ns);
   return 0;
@@ -85,7 +87,7 @@ int main(void) {
     assert vals["qk"] == C.sizeof(QuantKernels)
     for name, cls in (("src", ExpertSrc), ("opts", StoreOpts), ("ref", ExpertRef), ("stats", StoreStats),
                       ("loc", PacketLoc), ("geom", ModelGeom), ("tref", TensorRef), ("synth", ModelSynthOpts),
-                      ("mopts", ModelOpts), ("mstats", ModelStats)):
+                      ("mopts", ModelOpts), ("sopts", StackOpts), ("mstats", ModelStats)):
         assert vals[name] == C.sizeof(cls), name
     for k, v in vals.items():
         if "." not in k:
@@ -95,7 +97,8 @@ int main(void) {
                "tlm_hip_expert_src": ExpertSrc, "tlm_hip_store_opts": StoreOpts, "tlm_hip_expert_ref": ExpertRef,
                "tlm_hip_store_stats": StoreStats, "tlm_hip_packet_loc": PacketLoc, "tlm_hip_model_geom": ModelGeom,
                "tlm_hip_tensor_ref": TensorRef, "tlm_hip_model_synth_opts": ModelSynthOpts,
-               "tlm_hip_model_opts": ModelOpts, "tlm_hip_model_stats": ModelStats}[t]
+               "tlm_hip_model_opts": ModelOpts, "tlm_hip_stack_opts": StackOpts,
+               "tlm_hip_model_stats": ModelStats}[t]
         assert getattr(cls, f).offset == v, k
 
 
@@ -128,3 +131,61 @@ def test_host_checks_reject_bad_arguments_without_launching():
     assert lib.tlm_hip_qact_bytes(8, 33) == 72
     assert lib.tlm_hip_quantize_act(15, None, 256, None, None) == -3
     assert lib.tlm_hip_quantize_act(15, None, 0, None, None) == 0     # n <= 0 is a no-op
+
+
+def _device_symbols(so_bytes):
+    """Global symbol names of every gfx950 code object in the library's
+    offload bundles (format: magic, entry count, then per entry offset, size,
+    triple length and triple; each entry an ELF64 code object)."""
+    import struct
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    names, n_objs = set(), 0
+    at = so_bytes.find(magic)
+    while at >= 0:
+        (n,) = struct.unpack_from("<Q", so_bytes, at + 24)
+        p = at + 32
+        for _ in range(n):
+            off, size, tlen = struct.unpack_from("<QQQ", so_bytes, p)
+            triple = so_bytes[p + 24:p + 24 + tlen].decode()
+            p += 24 + tlen
+            if "gfx950" not in triple:
+                continue
+            elf = so_bytes[at + off:at + off + size]
+            assert elf[:4] == b"\x7fELF", triple
+            n_objs += 1
+            shoff, = struct.unpack_from("<Q", elf, 0x28)
+            shentsize, shnum = struct.unpack_from("<HH", elf, 0x3A)
+            secs = [struct.unpack_from("<IIQQQQIIQQ", elf, shoff + i * shentsize) for i in range(shnum)]
+            for s in secs:
+                if s[1] != 2:   # SHT_SYMTAB
+                    continue
+                strtab = secs[s[6]]
+                for j in range(s[5] // 24):
+                    st_name, st_info = struct.unpack_from("<IB", elf, s[4] + j * 24)
+                    if st_info >> 4 != 1:   # STB_GLOBAL
+                        continue
+                    end = elf.index(b"\0", strtab[4] + st_name)
+                    names.add(elf[strtab[4] + st_name:end].decode())
+        at = so_bytes.find(magic, at + 24)
+    return names, n_objs
+
+
+def test_registered_kernels_exist_in_code_objects():
+    """Every kernel and device variable the host code registers by name (the
+    mangled names in .rodata) is a global symbol of one of the library's
+    gfx950 code objects: the runtime looks kernels up by those names when it
+    loads a module at its first launch, and a name that the host and device
+    passes mangle differently fails that load."""
+    import re
+    so = os.path.join(ROOT, "tierlm_amd", "libtlm_hip.so")
+    if not os.path.exists(so):
+        pytest.skip("library not built")
+    data = open(so, "rb").read()
+    dev, n_objs = _device_symbols(data)
+    assert n_objs >= 6, n_objs
+    out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "-p", ".rodata", so], capture_output=True, text=True,
+                         check=True).stdout
+    registered = {m.group(1) for m in re.finditer(r"\]\s+(_Z\S+)", out)}
+    assert len(registered) > 100
+    missing = sorted(registered - dev)
+    assert not missing, missing[:5]

@@ -156,6 +156,55 @@ def test_synth_cached_equals_resident(hip, edt, shared, router):
         b.close()
 
 
+STORE_COUNTERS = ("hits", "misses", "prefetch_issued", "prefetch_used", "prefetch_dropped", "evictions", "slots",
+                  "pinned")
+
+
+@pytest.mark.parametrize("slots,gamma,prefetch", [(4, 0.0, True), (12, 0.8, True), (40, 0.8, True), (12, 0.0, False)])
+def test_device_resolved_slots_equal_host_resolved(hip, slots, gamma, prefetch):
+    """The slots resolved on the device (the host replaying acquire, hints
+    and release behind it) and resolved by the host between each layer's
+    routing and its block: the same logits and routing at every step, over
+    caches of top_k slots (every step evicts), twelve and forty slots, with
+    and without the lookahead.  Without it every load a step starts has
+    landed before the next layer acquires (its block waited for it), so the
+    store's decisions, and its counters, are the same step by step; with it
+    a victim choice may see a lookahead load still in flight (such a slot is
+    not a victim) on either path, so only the acquisitions are compared."""
+    from tierlm_amd.model import Model, bench_prompt
+    g = dict(SMALL, router=2 if gamma else 0, n_layers=4)
+    slot = 3 * 256 * 512 // 256 * 210
+    kw = dict(expert_dt=14, seed=9, max_ctx=96, expert_pool=6 if gamma else 0, heat_gamma=gamma,
+              expert_cache=slot * slots, prefetch=prefetch, lookahead_k=8 if prefetch else 0,
+              interest=0.7 if prefetch else 0.0, prefill_chunk=-1)
+    a = Model.synth(g, host_routes=True, **kw)
+    b = Model.synth(g, **kw)
+    try:
+        for pos, t in enumerate(bench_prompt(40, g["vocab"], seed=11)):
+            la, na = a.step(t)
+            lb, nb = b.step(t)
+            assert na == nb and np.array_equal(la.view(np.uint32), lb.view(np.uint32)), pos
+            ia, wa = a.routes()
+            ib, wb = b.routes()
+            assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32)), pos
+            sa, sb = a.store_stats(), b.store_stats()
+            if prefetch:
+                assert sa["hits"] + sa["misses"] == sb["hits"] + sb["misses"] == (pos + 1) * 4 * 4, pos
+            else:
+                assert {c: sa[c] for c in STORE_COUNTERS} == {c: sb[c] for c in STORE_COUNTERS}, pos
+        st = b.store_stats()
+        assert st["misses"] > 0 and st["in_use"] == 0
+        if slots == 4:
+            assert st["evictions"] > 0
+        a.reset()
+        b.reset()
+        p = bench_prompt(8, g["vocab"])
+        assert a.generate(p, 16) == b.generate(p, 16)
+    finally:
+        a.close()
+        b.close()
+
+
 def test_synth_cached_heat_lookahead(hip):
     """Sigmoid routing with a Zipf-like selection bias, a pool of 6 distinct
     payloads, the lookahead with interest-weighted breadth: a cache of half

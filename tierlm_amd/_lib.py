@@ -67,7 +67,8 @@ class StoreStats(C.Structure):
 class StackOpts(C.Structure):
     """tlm_hip_stack_opts"""
     _fields_ = [("lookahead", C.c_int32), ("lookahead_k", C.c_int32), ("interest", C.c_double),
-                ("layer_heat", C.c_void_p), ("instinct", C.c_void_p), ("instinct_seen", C.c_void_p)]
+                ("layer_heat", C.c_void_p), ("instinct", C.c_void_p), ("instinct_seen", C.c_void_p),
+                ("host_routes", C.c_int32)]
 
 
 class MoeHint(C.Structure):

@@ -1541,6 +1541,7 @@ int prepare(tlm_hip_model *M, const tlm_hip_model_opts *o) {
     M->xopts.interest = o ? o->interest : 0.0;
     M->pf_chunk = o ? o->prefill_chunk : 0;
     M->stats = o && o->stats;
+    M->xopts.host_routes = o && o->host_routes ? 1 : 0;
     if (M->xopts.lookahead_k < 0 || M->xopts.lookahead_k > 32)
         return tlmh_seterr(TLM_HIP_EINVAL, "model: lookahead_k %d (0..32)", M->xopts.lookahead_k);
     /* a step through the cache waits on the host between layers: never a graph */
@@ -1964,8 +1965,10 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
 /* The same step with the experts in the slot cache: tlm_model_step's layer
  * loop with moe() through the store (tlm_model.c:960-1055) and the router
  * lookahead, one tick per token (:1097): each layer's attention is queued
- * right before its router, and the host acquires layer l + 1's experts while
- * the device runs layer l's block (moe_stack_run). */
+ * right before its router; the device resolves the routed experts' slots
+ * while the host replays the store operations behind it, or, with
+ * host_routes, the host acquires layer l + 1's experts while the device runs
+ * layer l's block (moe_stack_run). */
 int step_cached(tlm_hip_model *M, bool want_logits) {
     const size_t L = M->g.n_layers;
     stamp(M, 0);

@@ -169,15 +169,19 @@ __device__ __forceinline__ uint32_t ord_bits(float f) {
  * unnormalised probabilities).  stash() runs in every thread before a group
  * barrier, once the softmax is done: a place for LDS writes of values loaded
  * at kernel entry. */
-template <class Stash>
+struct NoHook {
+    __device__ void operator()() const {}
+};
+template <class Stash, class Issued = NoHook>
 __device__ void route_group(const tlm_hip_moe_desc &d, const GAS float *logits, LAS RouteLds *R, Stash stash,
-                            const ExpTabLanes &tab, bool weights = true) {
+                            const ExpTabLanes &tab, bool weights = true, Issued issued = NoHook{}) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, E = d.E, k = d.k;
     const bool sig = d.router == 2;
     const bool in = t < E;
     const bool unmasked = in && !(d.mask && ((const GAS uint8_t *)d.mask)[t]);
     const float l = in ? logits[t] : 0.0f;
     const float bias = (sig && in && d.router_bias) ? ((const GAS float *)d.router_bias)[t] : 0.0f;
+    issued();   /* loads the caller issues here queue behind the routing's own */
     float p;
     if (sig) {   /* sigmoid score = weight; bias for selection only */
         p = 1.0f / (1.0f + expf_ref_with(-l, tab));
@@ -586,17 +590,27 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
     }
 }
 
-/* GIVEN: the routing and the routed experts' matrices come as a launch
- * argument (the slot cache's blocks); otherwise none is passed */
+/* Where a block's routing and routed matrices come from (MODE): the block
+ * routes itself and reads the expert table (ROUTE, no argument); both come as
+ * a launch argument (GIVEN, the slot cache's host-resolved blocks); the
+ * routing is in the workspace and the slots in device memory (SLOTS, the
+ * slot cache's device-resolved blocks) */
+constexpr int ROUTE = 0, GIVEN = 1, SLOTS = 2;
 struct NoGiven {};
-template <bool GIVEN> using GivenArg = typename std::conditional<GIVEN, MoeGiven, NoGiven>::type;
+/* a class-template mapping, so that kernel names mangle the same in the host
+ * and device passes (an expression over an unnamed enum in a parameter type
+ * does not: the two passes number unnamed types differently) */
+template <int MODE> struct GivenArgT { using type = NoGiven; };
+template <> struct GivenArgT<GIVEN> { using type = MoeGiven; };
+template <> struct GivenArgT<SLOTS> { using type = MoeSlots; };
+template <int MODE> using GivenArg = typename GivenArgT<MODE>::type;
 
 /* rows of a 16-row tile per routed gate/up group: half tiles, 768 groups at
  * Qwen3-30B-A3B shape, three to a compute unit (the register cap below) */
 constexpr int GUR = 8;
-template <int EDT, int SDT, bool GIVEN>
+template <int EDT, int SDT, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout L, int32_t *ids_out, float *w_out,
-                                                    uint8_t *ws, const GivenArg<GIVEN> gv) {
+                                                    uint8_t *ws, const GivenArg<MODE> gv) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ RouteLds s_route;
     args_now(d.D, d.de, d.ds, d.E, d.k, d.router, d.routed_scale, d.mask, d.router_bias, d.experts, L.logits, L.route,
@@ -609,6 +623,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const bool shared = SDT != NONE && (int)blockIdx.x >= nexp;
     if constexpr (SDT != NONE) {
         if (shared) {
+            if constexpr (MODE == SLOTS) {   /* the layer went back to the caller */
+                if (((const GAS int32_t *)gv.slot)[0] < 0) return;
+            }
             const int t = (int)blockIdx.x - nexp;
             float *hh = (float *)(ws + L.hh) + (size_t)d.k * d.de;
             gateup_tile<SDT, TILE_ROWS>(d, (const uint8_t *)d.sg, (const uint8_t *)d.su, ws + L.xs, d.ds, t, 0, hh,
@@ -617,7 +634,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         }
     }
     const int r = (int)blockIdx.x / te, q = (int)blockIdx.x - r * te, t = q / SPT, i0 = (q % SPT) * GUR;
-    if constexpr (GIVEN) {   /* routing and matrices given: the weight loads go out at once */
+    if constexpr (MODE == SLOTS) {   /* one load for the slot, then the weight loads */
+        const int v = ((const GAS int32_t *)gv.slot)[r];
+        if (v < 0) return;   /* the layer went back to the caller */
+        const uint8_t *base = gv.arena + (size_t)v * gv.slot_bytes;
+        gateup_tile<EDT, GUR>(d, base + gv.off[0], base + gv.off[1], ws + L.xe, d.de, t, i0,
+                              (float *)(ws + L.hh) + (size_t)r * d.de, lds, tab);
+        return;
+    }
+    if constexpr (MODE == GIVEN) {   /* routing and matrices given: the weight loads go out at once */
         if (blockIdx.x == 0 && (int)threadIdx.x < d.k) {
             const int q = threadIdx.x;
             ws_ids(ws, L)[q] = gv.ids[q];
@@ -748,9 +773,9 @@ __host__ __device__ inline size_t down_lds_part(int kind, int nq) {
     return ((stage_bytes(kind, nq) + 15) & ~(size_t)15) + park_bytes(nq * DROWS);
 }
 
-template <int EDT, int SDT, bool GIVEN>
+template <int EDT, int SDT, int MODE>
 __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L, float *__restrict__ h,
-                                                  uint8_t *ws, const GivenArg<GIVEN> gv) {
+                                                  uint8_t *ws, const GivenArg<MODE> gv) {
     extern __shared__ __align__(16) uint8_t lds[];
     args_now(d.D, d.de, d.ds, d.E, d.k, d.experts, L.route, L.hh, h, ws, gridDim.x);
     if constexpr (SDT != NONE) args_now(d.sd);
@@ -777,8 +802,15 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
     const uint8_t *tab = nullptr;
     float wl = 0.0f;   /* the combine's inputs, loaded before anything waits; w reaches LDS only
                         * after the rows are done, so no wave stalls on it early */
-    if constexpr (GIVEN) {
+    if constexpr (MODE == GIVEN) {
         if (tid < k) wl = gv.w[tid];
+    } else if constexpr (MODE == SLOTS) {   /* rank t's down matrix from its slot */
+        if (((const GAS int32_t *)gv.slot)[0] < 0) return;   /* the layer went back to the caller */
+        if (tid < k) {
+            const int v = ((const GAS int32_t *)gv.slot)[tid];
+            tab = gv.arena + (size_t)v * gv.slot_bytes + gv.off[2];
+            wl = ((const GAS float *)ws_w(ws, L))[tid];
+        }
     } else {
         eid = tid < k ? ((const GAS int32_t *)ws_ids(ws, L))[tid] : 0;
         tab = tid < d.E ? (const uint8_t *)((const GAS uint64_t *)d.experts)[3 * tid + 2] : nullptr;
@@ -795,9 +827,16 @@ __global__ __launch_bounds__(256) void k_moe_down(tlm_hip_moe_desc d, WsLayout L
         __syncthreads();
     };
     const Park pe = park_at(lds + ((stage_bytes(ek, k * nbe) + 15) & ~(size_t)15), k * nbe * DROWS);
-    if constexpr (GIVEN)
+    if constexpr (MODE == GIVEN)
         down_rows<EDT>(k, [&](int r) { return gv.p[3 * r + 2]; }, []() {}, (const float *)(ws + L.hh), d.de, d.D,
                        row0, lds, pe);
+    else if constexpr (MODE == SLOTS)
+        down_rows<EDT>(k, [&](int r) { return s_tab[r]; },
+                       [&]() {
+                           if (tid < k) s_tab[tid] = tab;
+                           __syncthreads();
+                       },
+                       (const float *)(ws + L.hh), d.de, d.D, row0, lds, pe);
     else
         down_rows<EDT>(k, [&](int r) { return s_tab[s_eid[r]]; }, table, (const float *)(ws + L.hh), d.de, d.D, row0,
                        lds, pe);
@@ -1066,15 +1105,27 @@ struct RouteSet {
     WsLayout L[MULTI_ROUTES];
     uint8_t *ws[MULTI_ROUTES];
 };
-__global__ __launch_bounds__(256) void k_moe_route_host(const RouteSet S, uint32_t *host, int seq_off, uint32_t seq) {
+__global__ __launch_bounds__(256) void k_moe_route_host(const RouteSet S, uint32_t *host, int seq_off, uint32_t seq,
+                                                        const RouteDev rd) {
     __shared__ RouteLds s_route;
+    __shared__ int s_bad;
     const int i = blockIdx.x;
     const tlm_hip_moe_desc &d = S.d[i];
+    const int q = threadIdx.x;
+    const bool dev = i == 0 && rd.tab != nullptr;   /* uniform over the group */
+    if (q == 0) s_bad = 0;
     ExpTabLanes tab;
     tab.load();
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
     route_group(d, (const GAS float *)(S.ws[i] + S.L[i].logits), R, []() {}, tab);
-    const int q = threadIdx.x;
+    /* the routed experts' slots: one read of the table each (mapped host
+     * memory, system scope); any expert without a landed slot sends the
+     * whole layer back to the caller */
+    int32_t v = -1;
+    if (dev && q < d.k) {
+        v = __hip_atomic_load(rd.tab + R->ids[q], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (v < 0 || v >= rd.n_slots) s_bad = 1;
+    }
     if (q < 32) {
         const bool on = q < d.k;
         host[64 * i + q] = on ? (uint32_t)R->ids[q] : 0u;
@@ -1084,9 +1135,19 @@ __global__ __launch_bounds__(256) void k_moe_route_host(const RouteSet S, uint32
             ws_w(S.ws[i], S.L[i])[q] = R->w[q];
         }
     }
+    __syncthreads();
+    if (dev) {
+        const bool fast = s_bad == 0;
+        if (q < d.k) rd.slot_out[q] = fast ? v : -1;
+        if (q == 0) __hip_atomic_store(rd.report, fast ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     __threadfence_system();
     __syncthreads();
     if (q == 0) __hip_atomic_store(host + seq_off / 4 + i, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__global__ __launch_bounds__(64) void k_publish_slot(int32_t *entry, int32_t v) {
+    if (threadIdx.x == 0) __hip_atomic_store(entry, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 /* One group: slots grouped by expert (order within an expert is free - every
@@ -1344,18 +1405,24 @@ typedef void (*gateup_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_
 typedef void (*down_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *, const NoGiven);
 typedef void (*gateup_given_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *, const MoeGiven);
 typedef void (*down_given_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *, const MoeGiven);
+typedef void (*gateup_slots_fn)(tlm_hip_moe_desc, WsLayout, int32_t *, float *, uint8_t *, const MoeSlots);
+typedef void (*down_slots_fn)(tlm_hip_moe_desc, WsLayout, float *, uint8_t *, const MoeSlots);
 
 inline int dt_slot(int dt) { return dt == DT_Q6_K ? 0 : dt == DT_Q8_0 ? 1 : dt == DT_Q4_K ? 2 : dt == DT_Q5_K ? 3 : -1; }
 
 #define ROW(K, E, G) {K<E, NONE, G>, K<E, DT_Q6_K, G>, K<E, DT_Q8_0, G>, K<E, DT_Q4_K, G>, K<E, DT_Q5_K, G>}
-const gateup_fn GU[4][5] = {ROW(k_moe_gateup, DT_Q6_K, false), ROW(k_moe_gateup, DT_Q8_0, false),
-                            ROW(k_moe_gateup, DT_Q4_K, false), ROW(k_moe_gateup, DT_Q5_K, false)};
-const down_fn DN[4][5] = {ROW(k_moe_down, DT_Q6_K, false), ROW(k_moe_down, DT_Q8_0, false),
-                          ROW(k_moe_down, DT_Q4_K, false), ROW(k_moe_down, DT_Q5_K, false)};
-const gateup_given_fn GUG[4][5] = {ROW(k_moe_gateup, DT_Q6_K, true), ROW(k_moe_gateup, DT_Q8_0, true),
-                                   ROW(k_moe_gateup, DT_Q4_K, true), ROW(k_moe_gateup, DT_Q5_K, true)};
-const down_given_fn DNG[4][5] = {ROW(k_moe_down, DT_Q6_K, true), ROW(k_moe_down, DT_Q8_0, true),
-                                 ROW(k_moe_down, DT_Q4_K, true), ROW(k_moe_down, DT_Q5_K, true)};
+const gateup_fn GU[4][5] = {ROW(k_moe_gateup, DT_Q6_K, ROUTE), ROW(k_moe_gateup, DT_Q8_0, ROUTE),
+                            ROW(k_moe_gateup, DT_Q4_K, ROUTE), ROW(k_moe_gateup, DT_Q5_K, ROUTE)};
+const down_fn DN[4][5] = {ROW(k_moe_down, DT_Q6_K, ROUTE), ROW(k_moe_down, DT_Q8_0, ROUTE),
+                          ROW(k_moe_down, DT_Q4_K, ROUTE), ROW(k_moe_down, DT_Q5_K, ROUTE)};
+const gateup_given_fn GUG[4][5] = {ROW(k_moe_gateup, DT_Q6_K, GIVEN), ROW(k_moe_gateup, DT_Q8_0, GIVEN),
+                                   ROW(k_moe_gateup, DT_Q4_K, GIVEN), ROW(k_moe_gateup, DT_Q5_K, GIVEN)};
+const down_given_fn DNG[4][5] = {ROW(k_moe_down, DT_Q6_K, GIVEN), ROW(k_moe_down, DT_Q8_0, GIVEN),
+                                 ROW(k_moe_down, DT_Q4_K, GIVEN), ROW(k_moe_down, DT_Q5_K, GIVEN)};
+const gateup_slots_fn GUS[4][5] = {ROW(k_moe_gateup, DT_Q6_K, SLOTS), ROW(k_moe_gateup, DT_Q8_0, SLOTS),
+                                   ROW(k_moe_gateup, DT_Q4_K, SLOTS), ROW(k_moe_gateup, DT_Q5_K, SLOTS)};
+const down_slots_fn DNS[4][5] = {ROW(k_moe_down, DT_Q6_K, SLOTS), ROW(k_moe_down, DT_Q8_0, SLOTS),
+                                 ROW(k_moe_down, DT_Q4_K, SLOTS), ROW(k_moe_down, DT_Q5_K, SLOTS)};
 #undef ROW
 
 }  // namespace
@@ -1406,11 +1473,12 @@ static int moe_check(const tlm_hip_moe_desc *d, const float *h, const void *ws, 
 }
 
 /* phase 0 = all launches; 1 router, 2 gate/up, 3 down + combine; gv (may be
- * NULL): routing and matrices given by the caller */
+ * NULL): routing and matrices given by the caller; ms (may be NULL): the
+ * routing in the workspace and the matrices in slots */
 static int moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *ids, float *w, void *ws,
-                     const MoeGiven *gvp, hipStream_t s) {
+                     const MoeGiven *gvp, hipStream_t s, const MoeSlots *msp = nullptr) {
     if (phase < 0 || phase > 3) return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: phase %d", phase);
-    if (int rc = moe_check(d, h, ws, gvp == nullptr && phase != 1)) return rc;
+    if (int rc = moe_check(d, h, ws, gvp == nullptr && msp == nullptr && phase != 1)) return rc;
     const int ebv = dt_block_values(d->expert_dt);
     const int ek = dt_act_kind(d->expert_dt), sk = d->ds > 0 ? dt_act_kind(d->shared_dt) : ek;
     const int nbe = (int)(d->D / ebv), nbde = (int)(d->de / ebv);
@@ -1437,7 +1505,12 @@ static int moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const unsigned g3 = (unsigned)(d->D / DROWS);
     if (phase == 0 || phase == 1)
         hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8, (size_t)0);
-    if (gvp) {
+    if (msp) {
+        const MoeSlots ms = *msp;
+        if (phase == 0 || phase == 2)
+            hipLaunchKernelGGL(GUS[es][ss], dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8, ms);
+        if (phase == 0 || phase == 3) hipLaunchKernelGGL(DNS[es][ss], dim3(g3), dim3(256), lds3, s, dv, L, h, w8, ms);
+    } else if (gvp) {
         const MoeGiven gv = *gvp;
         if (phase == 0 || phase == 2)
             hipLaunchKernelGGL(GUG[es][ss], dim3(g2), dim3(64 * NWAVE), lds2, s, dv, L, ids, w, w8, gv);
@@ -1463,6 +1536,14 @@ int launch_moe_phase_given(const tlm_hip_moe_desc *d, int phase, float *h, void 
     return moe_phase(d, phase, h, nullptr, nullptr, ws, gv, s);
 }
 
+int launch_moe_phase_slots(const tlm_hip_moe_desc *d, int phase, float *h, void *ws, const MoeSlots *ms,
+                           hipStream_t s) {
+    if (!ms || !ms->slot || !ms->arena || phase == 1 || phase == 0 || ((ms->slot_bytes | ms->off[0] | ms->off[1] |
+                                                                         ms->off[2] | (uintptr_t)ms->arena) & 15u))
+        return tlmh_seterr(TLM_HIP_EINVAL, "moe_layer: slot arena");
+    return moe_phase(d, phase, h, nullptr, nullptr, ws, nullptr, s, ms);
+}
+
 /* The router launch, then routing alone: ids / w (k each) in the workspace's
  * route area (moe_route_offset: ids int32 at +0, w f32 at +128). */
 int launch_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, float *w, void *ws, hipStream_t s) {
@@ -1474,7 +1555,7 @@ int launch_moe_route(const tlm_hip_moe_desc *d, const float *h, int32_t *ids, fl
 /* The routers of d[0..n) over the same residual h (one launch), then their
  * routing into the host area (one launch, see k_moe_route_host) */
 int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, int n, const float *h,
-                           uint32_t *host, int seq_off, uint32_t seq, hipStream_t s) {
+                           uint32_t *host, int seq_off, uint32_t seq, hipStream_t s, const RouteDev *rd) {
     if (n < 1 || n > MULTI_ROUTES) return tlmh_seterr(TLM_HIP_EINVAL, "moe routes: %d routers", n);
     RouterSet rs{};
     RouteSet qs{};
@@ -1491,8 +1572,19 @@ int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, in
     }
     if (lds > 64 * 1024) return tlmh_seterr(TLM_HIP_EUNSUP, "moe routes: D exceeds the LDS staging limit");
     hipLaunchKernelGGL(k_moe_router_multi, dim3((unsigned)g, (unsigned)n), dim3(64), lds, s, rs, h);
-    hipLaunchKernelGGL(k_moe_route_host, dim3((unsigned)n), dim3(256), 0, s, qs, host, seq_off, seq);
+    RouteDev r{};
+    if (rd) {
+        if (!rd->tab || !rd->slot_out || !rd->report || rd->n_slots <= 0)
+            return tlmh_seterr(TLM_HIP_EINVAL, "moe routes: slot resolution");
+        r = *rd;
+    }
+    hipLaunchKernelGGL(k_moe_route_host, dim3((unsigned)n), dim3(256), 0, s, qs, host, seq_off, seq, r);
     return tlmh_check(hipGetLastError(), "moe routes launch");
+}
+
+int launch_publish_slot(int32_t *entry, int32_t v, hipStream_t s) {
+    hipLaunchKernelGGL(k_publish_slot, dim3(1), dim3(64), 0, s, entry, v);
+    return tlmh_check(hipGetLastError(), "store: publish slot");
 }
 
 size_t moe_prefill_workspace_bytes(const tlm_hip_moe_desc *d, int64_t T) {

@@ -56,10 +56,11 @@ constexpr size_t MAT_ALIGN = 256;
 constexpr int MAX_HINTS = 7;         /* lookahead layers per tlm_hip_moe_layer_store call */
 constexpr int ROUTE_BYTES = 256;     /* ids int32[32] at +0, w f32[32] at +128 (moe_route_offset) */
 /* a route area: the block's and its hints' routes, then the sequence word the
- * export stores last; two areas, so the host reads one layer's routes while
- * the next layer's export lands in the other */
+ * export stores last; NAREA areas, so the host reads one layer's routes while
+ * later layers' exports land in the others */
 constexpr int ROUTE_AREA = ROUTE_BYTES * (1 + MAX_HINTS) + 64;
 constexpr int ROUTE_SEQ = ROUTE_BYTES * (1 + MAX_HINTS);   /* byte offset of the sequence word */
+constexpr int NAREA = 4;
 constexpr int MOE_MAXK = 32;
 
 struct Expert {
@@ -123,10 +124,28 @@ struct tlm_hip_store {
     uint64_t clock = 0, ticks = 0;
     int loading = 0, demand_loading = 0, hint_loading = 0, n_pinned = 0;
     tlm_hip_store_stats st{};
-    uint8_t *route_host = nullptr;      /* pinned: two route areas (ROUTE_AREA bytes each) */
+    uint8_t *route_host = nullptr;      /* pinned: NAREA route areas (ROUTE_AREA bytes each) */
     uint32_t *route_dev = nullptr;      /* route_host as the device addresses it (mapped, coherent) */
     uint32_t route_seq = 0;             /* the last export's sequence number */
-    int route_n[2] = {0, 0};            /* routes in each area */
+    int route_n[NAREA] = {};            /* routes in each area */
+    /* The expert -> slot table the device-resolved blocks read (mapped,
+     * coherent host memory; row `layer` of tab_E entries): a slot's index is
+     * stored by the load stream right after its packs (so an entry is never
+     * ahead of the bytes), and set back to -1 by the host when the slot is
+     * chosen as a victim, before its new load is queued. */
+    int32_t *tab_host = nullptr, *tab_dev = nullptr;
+    int tab_L = 0, tab_E = 0;
+    bool uniform = false;               /* every expert's matrices at the same offsets in a slot */
+    size_t uoff[3] = {0, 0, 0};
+    /* per route area, whether the export resolved every routed slot (1) or
+     * handed the layer back (0); mapped, coherent */
+    uint32_t *rep_host = nullptr, *rep_dev = nullptr;
+    int32_t *res_dev = nullptr;         /* device: the resolved slots, NAREA x 32 */
+
+    size_t tab_index(int e) const { return (size_t)ex[e].src.layer * tab_E + ex[e].src.id; }
+    void tab_set(int e, int32_t v) {
+        if (tab_host && e >= 0) __atomic_store_n(tab_host + tab_index(e), v, __ATOMIC_RELEASE);
+    }
     /* release points: an event recorded on a release stream when a load first
      * needs one, shared by every load that needs a point on that stream
      * before the next release; reused once no queued load waits for it */
@@ -145,6 +164,7 @@ struct tlm_hip_store {
     /* ---- policy (all with mu held) ------------------------------------ */
     void fail_slot(int v, int err) {            /* tlm_store.c:139-158 */
         Slot &s = sl[v];
+        if (s.ex >= 0) tab_set(s.ex, -1);
         if (s.ex >= 0 && ex[s.ex].slot == v) ex[s.ex].slot = -1;
         if (s.state == S_LOADING) {
             loading--;
@@ -170,6 +190,7 @@ struct tlm_hip_store {
         Slot &s = sl[v];
         if (s.state == S_READY && s.ex >= 0) {
             ex[s.ex].slot = -1;
+            tab_set(s.ex, -1);
             st.evictions++;
         }
         loading++;
@@ -367,6 +388,7 @@ struct tlm_hip_store {
         for (int m = 0; m < 3 && !rc; m++)
             rc = launch_pack(dt, src + x.src.item_off[m], (size_t)(x.n[m] / dt_block_values(dt)) *
                              (size_t)dt_block_bytes(dt), x.rows[m], x.n[m], base + x.off[m], packs);
+        if (!rc && tab_dev) rc = launch_publish_slot(tab_dev + tab_index(j.e), j.v, packs);
         if (!rc) rc = tlmh_check(hipEventRecord(sl[j.v].loaded, packs), "store: record load");
         if (rc) (void)hipStreamSynchronize(packs);   /* no half-done load may race a later one into the slot */
         if (i >= 0) {
@@ -450,6 +472,9 @@ struct tlm_hip_store {
         }
         if (arena) (void)hipFree(arena);
         if (route_host) (void)hipHostFree(route_host);
+        if (tab_host) (void)hipHostFree(tab_host);
+        if (rep_host) (void)hipHostFree(rep_host);
+        if (res_dev) (void)hipFree(res_dev);
         for (hipStream_t q : lstream)
             if (q) (void)hipStreamDestroy(q);
     }
@@ -573,11 +598,37 @@ int tlm_hip_store_open(const tlm_hip_expert_src *src, int n, const tlm_hip_store
         }
         /* mapped and coherent: k_moe_route_host stores the routing straight into it, its sequence
          * word last; the host waits for that word instead of synchronising the stream */
-        if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->route_host, 2 * ROUTE_AREA,
+        if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->route_host, NAREA * ROUTE_AREA,
                                                hipHostMallocMapped | hipHostMallocCoherent), "store: routing scratch");
-        if (!rc) memset(s->route_host, 0, 2 * ROUTE_AREA);
+        if (!rc) memset(s->route_host, 0, NAREA * ROUTE_AREA);
         if (!rc) rc = tlmh_check(hipHostGetDevicePointer((void **)&s->route_dev, s->route_host, 0),
                                  "store: routing scratch address");
+        /* the device-resolved blocks' table and control words */
+        int maxl = 0, maxe = 0;
+        s->uniform = true;
+        for (const Expert &x : s->ex) {
+            maxl = std::max(maxl, (int)x.src.layer);
+            maxe = std::max(maxe, (int)x.src.id);
+            for (int m = 0; m < 3; m++) s->uniform = s->uniform && x.off[m] == s->ex[0].off[m];
+        }
+        for (int m = 0; m < 3; m++) s->uoff[m] = s->ex[0].off[m];
+        s->tab_L = maxl + 1;
+        s->tab_E = maxe + 1;
+        const size_t tn = (size_t)s->tab_L * s->tab_E;
+        if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->tab_host, tn * 4, hipHostMallocMapped | hipHostMallocCoherent),
+                                 "store: slot table");
+        if (!rc) {
+            for (size_t i = 0; i < tn; i++) s->tab_host[i] = -1;
+            rc = tlmh_check(hipHostGetDevicePointer((void **)&s->tab_dev, s->tab_host, 0), "store: slot table address");
+        }
+        if (!rc) rc = tlmh_check(hipHostMalloc((void **)&s->rep_host, NAREA * 4, hipHostMallocMapped | hipHostMallocCoherent),
+                                 "store: export reports");
+        if (!rc) {
+            memset(s->rep_host, 0, NAREA * 4);
+            rc = tlmh_check(hipHostGetDevicePointer((void **)&s->rep_dev, s->rep_host, 0), "store: export reports address");
+        }
+        if (!rc) rc = tlmh_check(hipMalloc((void **)&s->res_dev, NAREA * 32 * 4), "store: resolved slots");
+        if (!rc) rc = tlmh_check(hipMemset(s->res_dev, 0, NAREA * 32 * 4), "store: resolved slots");
         if (!rc) s->loader = std::thread([s] { s->loader_main(); });
     }
     if (rc) {
@@ -792,6 +843,18 @@ void tlm_hip_store_release(tlm_hip_store *s, tlm_hip_expert_ref *ref, void *stre
             sl.rel_stream = (hipStream_t)stream;
             s->release_seq++;
         }
+        s->drop_ref(ref->slot);
+    }
+    ref->slot = -1;
+    ref->mats[0] = ref->mats[1] = ref->mats[2] = nullptr;
+}
+
+/* A release whose readers have all finished by the time any later load can
+ * start (the device-resolved stack's layers before its last): no release
+ * point is kept for the slot. */
+static void release_retired(tlm_hip_store *s, tlm_hip_expert_ref *ref) {
+    if (ref->slot >= 0 && ref->slot < s->n_slots) {
+        std::lock_guard<std::mutex> lk(s->mu);
         s->drop_ref(ref->slot);
     }
     ref->slot = -1;
@@ -1035,12 +1098,165 @@ size_t tlm_hip_moe_stack_workspace_bytes(const tlm_hip_moe_desc *descs, int n_la
 
 }  // extern "C"
 
+/* the instinct update of tlm_model.c:974-980 from a layer's routing */
+static void update_instinct(const tlm_hip_stack_opts *o, int l, const float *w, int k) {
+    if (!o || !o->instinct || !o->instinct_seen) return;
+    double sw = 0.0;
+    for (int r = 0; r < k; r++) sw += (double)w[r];
+    const double share = sw > 0.0 ? (double)w[0] / sw : 0.0;
+    o->instinct[l] += (share - o->instinct[l]) * 0.05;
+    o->instinct_seen[l]++;
+}
+
+/* lookahead() for layers l+1 .. l+n (tlm_model.c:844-877) from the hint routes
+ * of route area `area` (hints routed hd[i].k wide), the breadth
+ * interest-weighted (:863-874) */
+static void issue_hints(tlm_hip_store *s, const tlm_hip_stack_opts *o, const tlm_hip_moe_desc *descs, int l,
+                        const tlm_hip_moe_desc *hd, int n, const uint8_t *area) {
+    for (int i = 0; i < n; i++) {
+        const int tl = l + 1 + i, hk = hd[i].k, top = descs[tl].k;
+        const int32_t *hid = (const int32_t *)(area + ROUTE_BYTES * (1 + i));
+        const float *hw = (const float *)(area + ROUTE_BYTES * (1 + i) + 128);
+        int kk = hk;
+        if (o && o->interest > 0.0 && hk > top) {
+            double sw = 0.0;
+            for (int r = 0; r < hk; r++) sw += (double)hw[r];
+            const double now = sw > 0.0 ? (double)hw[0] / sw : 0.0;
+            const bool seen = o->instinct_seen && o->instinct && o->instinct_seen[tl];
+            const double I = seen ? 0.5 * (now + o->instinct[tl]) : now;
+            const double Hh = o->layer_heat ? (double)o->layer_heat[tl] : 0.0;
+            double W = o->interest * (1.0 - I) * (1.0 - Hh);
+            W = W < 0.0 ? 0.0 : W > 1.0 ? 1.0 : W;
+            kk = top + (int)(W * (double)(hk - top) + 0.5);
+            kk = std::min(kk, hd[i].E);
+        }
+        tlm_hip_store_prefetch(s, tl, (const int *)hid, kk);
+    }
+}
+
+/* layer l's hint descriptors: the next n layers' blocks, routed lk wide */
+static int hint_descs(const tlm_hip_moe_desc *descs, int n_layers, int l, int depth, int lk, tlm_hip_moe_desc *hd) {
+    const int nh = std::min(depth, n_layers - 1 - l);
+    for (int i = 0; i < nh; i++) {
+        hd[i] = descs[l + 1 + i];
+        hd[i].k = lk > 0 ? std::min(lk, hd[i].E) : hd[i].k;
+    }
+    return nh;
+}
+
+/* Whether the blocks can resolve their slots on the device: the slots share
+ * one layout, and every layer's experts index the store's table. */
+static bool dev_resolvable(const tlm_hip_store *s, const tlm_hip_moe_desc *descs, int n_layers) {
+    if (!s->uniform || !s->tab_host || !s->rep_host || !s->res_dev || n_layers > s->tab_L) return false;
+    for (int l = 0; l < n_layers; l++)
+        if (descs[l].E > s->tab_E || descs[l].k > MOE_MAXK) return false;
+    return true;
+}
+
+/* The stack with the slots resolved on the device where they can be (the
+ * default).  Per layer the host enqueues what precedes the router (before),
+ * the routers, the export - which also reads the routed experts' slots from
+ * the store's expert -> slot table - and the two block launches that read
+ * those slots; then it replays the layer's store operations from the export
+ * in the reference's order (acquire, hints, release; one tick at the end).
+ * When every routed expert's load had landed, the block is already running
+ * on the slots the export found; otherwise the export handed the layer back
+ * (its block launches do nothing) and the host runs it as the host-resolved
+ * path does, behind them: the stream waits for the loads, then the block
+ * with the slots' matrices as arguments.  Nothing on the device waits for
+ * the host or for a load, so no queue the loads share can stall behind it.
+ *
+ * Why no slot is overwritten while a block reads it: a victim is chosen only
+ * while the host replays some layer m - after layer m's export, which runs
+ * after every block before layer m (and any block the host ran for one of
+ * them) has finished - and never among layer m's routed experts, acquired
+ * before any miss chooses a victim and held through the hints; and layer
+ * m + 1's export, which reads the table, is enqueued only after that replay
+ * has cleared every victim's entry.  The last layer's slots keep a release
+ * point on the stream, for whatever the caller enqueues next. */
+static int moe_stack_run_dev(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
+                             const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace,
+                             hipStream_t st, const std::function<int(int)> &before) {
+    const int depth = stack_depth(o), lk = o ? o->lookahead_k : 0;
+    size_t bsz, hsz;
+    stack_layout(descs, n_layers, depth, lk, &bsz, &hsz);
+    uint8_t *base = (uint8_t *)workspace;
+    void *blk[2] = {base, base + bsz};
+    void *hws[2][MAX_HINTS];
+    for (int p = 0; p < 2; p++)
+        for (int i = 0; i < depth; i++) hws[p][i] = base + 2 * bsz + ((size_t)p * depth + i) * hsz;
+    {
+        /* releases on this stream from before: their readers finish before
+         * this call's first export, and so before any load it starts */
+        std::lock_guard<std::mutex> held(s->mu);
+        for (Slot &sl : s->sl)
+            if (sl.reads_pending && sl.rel_stream == st) sl.reads_pending = false;
+    }
+    int rc = TLM_HIP_OK;
+    for (int l = 0; l < n_layers && !rc; l++) {
+        if (before && (rc = before(l))) break;
+        tlm_hip_moe_desc hd[MAX_HINTS];
+        const int nh = hint_descs(descs, n_layers, l, depth, lk, hd);
+        const tlm_hip_moe_desc *ds[1 + MAX_HINTS];
+        void *wss[1 + MAX_HINTS];
+        ds[0] = &descs[l];
+        wss[0] = blk[l & 1];
+        for (int i = 0; i < nh; i++) {
+            ds[1 + i] = &hd[i];
+            wss[1 + i] = hws[l & 1][i];
+        }
+        const int area = l % NAREA;
+        const uint32_t seq = ++s->route_seq;
+        s->route_n[area] = 1 + nh;
+        RouteDev rd{};
+        rd.tab = s->tab_dev + (size_t)l * s->tab_E;
+        rd.slot_out = s->res_dev + area * 32;
+        rd.report = s->rep_dev + area;
+        rd.n_slots = s->n_slots;
+        rc = launch_moe_routes_host(ds, wss, 1 + nh, h, s->route_dev + area * (ROUTE_AREA / 4), ROUTE_SEQ, seq, st,
+                                    &rd);
+        const MoeSlots ms{s->res_dev + area * 32, s->arena, s->slot_bytes, {s->uoff[0], s->uoff[1], s->uoff[2]}};
+        if (!rc) rc = launch_moe_phase_slots(&descs[l], 2, h, blk[l & 1], &ms, st);
+        if (!rc) rc = launch_moe_phase_slots(&descs[l], 3, h, blk[l & 1], &ms, st);
+        if (!rc) rc = wait_routes(s, area, seq, st);
+        if (rc) break;
+        /* the export's routing and whether it kept the layer */
+        const uint8_t *ar = s->route_host + (size_t)area * ROUTE_AREA;
+        const bool kept = __atomic_load_n(s->rep_host + area, __ATOMIC_ACQUIRE) != 0;
+        const int k = descs[l].k;
+        int ids[MOE_MAXK];
+        float w[MOE_MAXK];
+        memcpy(ids, ar, sizeof(int) * k);
+        memcpy(w, ar + 128, sizeof(float) * k);
+        if (ids_out) memcpy(ids_out + (size_t)l * k, ids, sizeof(int) * k);
+        if (w_out) memcpy(w_out + (size_t)l * k, w, sizeof(float) * k);
+        update_instinct(o, l, w, k);
+        tlm_hip_expert_ref refs[MOE_MAXK];
+        if (kept) {
+            rc = tlm_hip_store_acquire(s, l, ids, k, refs);
+        } else {
+            rc = run_block(s, &descs[l], l, ids, w, h, blk[l & 1], refs, st);
+        }
+        /* hints while this block's experts hold their references (:988-990) */
+        if (!rc) issue_hints(s, o, descs, l, hd, nh, ar);
+        for (int r = 0; r < k; r++) {
+            if (l == n_layers - 1 || rc) tlm_hip_store_release(s, &refs[r], st);
+            else release_retired(s, &refs[r]);
+        }
+    }
+    if (!rc) tlm_hip_store_tick(s);
+    return rc;
+}
+
 /* tlm_model_step's loop over moe() with the store (src/lib/tlm_model.c:
  * 1075-1083, 960-1055), lookahead() (:844-877) and the instinct update
  * (:974-980), then tlm_store_tick (:1097); pipelined as described in
  * tlm_hip.h.  before(l), when given, enqueues what precedes layer l's router
  * on the stream (a model's attention); it runs right before that router's
- * launch, so layer l + 1's attention is queued behind layer l's block. */
+ * launch.  With o->host_routes, or when the slots cannot be resolved on the
+ * device, the host resolves each layer's slots: it waits for the layer's
+ * routing, acquires, and launches the block with the slots' matrices as
+ * arguments, and layer l + 1's attention is queued behind layer l's block. */
 int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
                   const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace, void *stream,
                   const std::function<int(int)> &before) {
@@ -1053,6 +1269,9 @@ int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s,
             return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: layer %d (k=%d)", l, descs[l].k);
     if (o && o->lookahead > 0 && o->lookahead_k > MOE_MAXK)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: lookahead_k %d above %d", o->lookahead_k, MOE_MAXK);
+    hipStream_t st = (hipStream_t)stream;
+    if (!(o && o->host_routes) && dev_resolvable(s, descs, n_layers))
+        return moe_stack_run_dev(descs, n_layers, s, h, o, ids_out, w_out, workspace, st, before);
     const int depth = stack_depth(o), lk = o ? o->lookahead_k : 0;
     size_t bsz, hsz;
     stack_layout(descs, n_layers, depth, lk, &bsz, &hsz);
@@ -1061,7 +1280,6 @@ int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s,
     void *hws[2][MAX_HINTS];
     for (int p = 0; p < 2; p++)
         for (int i = 0; i < depth; i++) hws[p][i] = base + 2 * bsz + ((size_t)p * depth + i) * hsz;
-    hipStream_t st = (hipStream_t)stream;
     tlm_hip_moe_desc hd[MAX_HINTS];
     int nh = 0;
     /* layer l's routes (block + hints for l+1 .. l+depth) into area l mod 2 */
@@ -1070,11 +1288,7 @@ int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s,
             const int rc = before(l);
             if (rc) return rc;
         }
-        nh = std::min(depth, n_layers - 1 - l);
-        for (int i = 0; i < nh; i++) {
-            hd[i] = descs[l + 1 + i];
-            hd[i].k = lk > 0 ? std::min(lk, hd[i].E) : hd[i].k;
-        }
+        nh = hint_descs(descs, n_layers, l, depth, lk, hd);
         return enqueue_routes(s, &descs[l], h, blk[l & 1], hd, hws[l & 1], nh, l & 1, seq, st);
     };
     uint32_t seq = 0;
@@ -1092,38 +1306,13 @@ int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s,
         memcpy(w, area + 128, sizeof(float) * k);
         if (ids_out) memcpy(ids_out + (size_t)l * k, ids, sizeof(int) * k);
         if (w_out) memcpy(w_out + (size_t)l * k, w, sizeof(float) * k);
-        if (o && o->instinct && o->instinct_seen) {   /* tlm_model.c:974-980 */
-            double sw = 0.0;
-            for (int r = 0; r < k; r++) sw += (double)w[r];
-            const double share = sw > 0.0 ? (double)w[0] / sw : 0.0;
-            o->instinct[l] += (share - o->instinct[l]) * 0.05;
-            o->instinct_seen[l]++;
-        }
+        update_instinct(o, l, w, k);
         tlm_hip_expert_ref refs[MOE_MAXK];
         rc = run_block(s, &descs[l], l, ids, w, h, blk[l & 1], refs, st);
         /* the next layer's routing queued behind this block, before the host's bookkeeping */
         if (!rc && l + 1 < n_layers) rc = enqueue(l + 1, &seq);
-        /* lookahead() for layers l+1 .. l+depth while this block's experts hold their
-         * references (:988-990), the breadth interest-weighted (:863-874) */
-        for (int i = 0; i < hints_here && !rc; i++) {
-            const int tl = l + 1 + i, hk = hdl[i].k, top = descs[tl].k;
-            const int32_t *hid = (const int32_t *)(area + ROUTE_BYTES * (1 + i));
-            const float *hw = (const float *)(area + ROUTE_BYTES * (1 + i) + 128);
-            int kk = hk;
-            if (o && o->interest > 0.0 && hk > top) {
-                double sw = 0.0;
-                for (int r = 0; r < hk; r++) sw += (double)hw[r];
-                const double now = sw > 0.0 ? (double)hw[0] / sw : 0.0;
-                const bool seen = o->instinct_seen && o->instinct && o->instinct_seen[tl];
-                const double I = seen ? 0.5 * (now + o->instinct[tl]) : now;
-                const double Hh = o->layer_heat ? (double)o->layer_heat[tl] : 0.0;
-                double W = o->interest * (1.0 - I) * (1.0 - Hh);
-                W = W < 0.0 ? 0.0 : W > 1.0 ? 1.0 : W;
-                kk = top + (int)(W * (double)(hk - top) + 0.5);
-                kk = std::min(kk, hdl[i].E);
-            }
-            tlm_hip_store_prefetch(s, tl, (const int *)hid, kk);
-        }
+        /* hints while this block's experts hold their references (:988-990) */
+        if (!rc) issue_hints(s, o, descs, l, hdl, hints_here, area);
         for (int r = 0; r < k; r++) tlm_hip_store_release(s, &refs[r], stream);
     }
     if (!rc) tlm_hip_store_tick(s);

@@ -309,8 +309,36 @@ struct MoeGiven {
 };
 int launch_moe_phase_given(const tlm_hip_moe_desc *d, int phase, float *h, void *ws, const MoeGiven *gv,
                            hipStream_t s);
+/* The routed experts sit in slots of one arena: rank r's slot index is
+ * slot[r] (device memory, written by an earlier launch on the stream), its
+ * gate / up / down at arena + slot[r] * slot_bytes + off[0 / 1 / 2].  The
+ * routing (ids, weights) is already in the block's workspace. */
+struct MoeSlots {
+    const int32_t *slot;
+    const uint8_t *arena;
+    uint64_t slot_bytes;
+    uint64_t off[3];
+};
+int launch_moe_phase_slots(const tlm_hip_moe_desc *d, int phase, float *h, void *ws, const MoeSlots *ms,
+                           hipStream_t s);
+/* The export launch's device-side slot resolution (tab == NULL: none):
+ * after routing, the main route's group reads each routed expert's slot from
+ * tab (the layer's row of the store's expert -> slot table, in mapped host
+ * memory; -1 while the expert is not resident or its load has not landed).
+ * All of them valid: it writes them to slot_out[0..k) and stores 1 at
+ * report; otherwise slot_out[0..k) = -1 and report = 0 (the blocks reading
+ * slot_out then do nothing, and the caller runs the layer itself).  The
+ * report is stored before the export's sequence word.  Nothing waits. */
+struct RouteDev {
+    const int32_t *tab;
+    int32_t *slot_out;
+    uint32_t *report;
+    int32_t n_slots;
+};
 int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, int n, const float *h,
-                           uint32_t *host, int seq_off, uint32_t seq, hipStream_t s);
+                           uint32_t *host, int seq_off, uint32_t seq, hipStream_t s, const RouteDev *rd = nullptr);
+/* one thread stores v at *entry (release, system scope): a load's last step */
+int launch_publish_slot(int32_t *entry, int32_t v, hipStream_t s);
 /* tlm_hip_moe_stack_store's loop (hip_store.hip); before(l), when given,
  * enqueues what precedes layer l's router (a model's attention) and returns 0
  * or an error; descs' expert tables are not used */

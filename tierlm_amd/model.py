@@ -22,7 +22,7 @@ class ModelOpts(C.Structure):
     _fields_ = [("max_ctx", C.c_int32), ("eager", C.c_int32), ("attn_slices", C.c_int32), ("attn_split", C.c_int32),
                 ("expert_cache_bytes", C.c_uint64), ("pin_frac", C.c_double), ("prefetch_off", C.c_int32),
                 ("lookahead_k", C.c_int32), ("interest", C.c_double), ("prefill_chunk", C.c_int32),
-                ("stats", C.c_int32)]
+                ("stats", C.c_int32), ("host_routes", C.c_int32)]
 
 
 class ModelStats(C.Structure):
@@ -32,16 +32,18 @@ class ModelStats(C.Structure):
 
 
 def model_opts(max_ctx=0, eager=False, attn_slices=0, split=False, expert_cache=0, pin_frac=0.0, prefetch=True,
-               lookahead_k=0, interest=0.0, prefill_chunk=0, stats=False):
+               lookahead_k=0, interest=0.0, prefill_chunk=0, stats=False, host_routes=False):
     """tlm_hip_model_opts; expert_cache > 0 (bytes) serves the experts through
     an HBM slot cache of that size from page-locked host memory, as tierlm's
     runtime serves them from its store (pin_frac 0 = its default 0.30,
     prefetch = its router lookahead, lookahead_k / interest its io and nav
     options); prefill_chunk: 0 batched prompts where the model allows them,
     n > 0 at most n tokens per batch, < 0 one step per token; stats: the
-    device-timed attention / MoE / other split of tlm_model_stats."""
+    device-timed attention / MoE / other split of tlm_model_stats;
+    host_routes: the host resolves each layer's slots instead of the device."""
     return ModelOpts(max_ctx, int(eager), attn_slices, int(split), int(expert_cache), float(pin_frac),
-                     0 if prefetch else 1, int(lookahead_k), float(interest), int(prefill_chunk), int(stats))
+                     0 if prefetch else 1, int(lookahead_k), float(interest), int(prefill_chunk), int(stats),
+                     int(host_routes))
 
 
 # Qwen3-30B-A3B: 48 layers, hidden 2048, 32 q / 4 kv heads x 128, 128
@@ -60,7 +62,8 @@ QWEN3_235B_A22B = dict(n_layers=94, d_model=4096, n_heads=64, n_kv_heads=4, head
 
 class Model:
     def __init__(self, manifest_path, max_ctx=0, eager=False, attn_slices=0, split=False, **cache):
-        """cache: expert_cache, pin_frac, prefetch, lookahead_k, interest, prefill_chunk (model_opts)"""
+        """cache: expert_cache, pin_frac, prefetch, lookahead_k, interest, prefill_chunk, stats,
+        host_routes (model_opts)"""
         self.opts = model_opts(max_ctx, eager, attn_slices, split, **cache)
         h = C.c_void_p()
         check(lib.tlm_hip_model_open(str(manifest_path).encode(), C.byref(self.opts), C.byref(h)))

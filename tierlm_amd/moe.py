@@ -118,7 +118,7 @@ class MoeStack:
     None).  The instinct state per layer lives here, as the reference keeps it
     in its model."""
 
-    def __init__(self, blocks, *, lookahead=1, lookahead_k=0, interest=0.0, heat=None):
+    def __init__(self, blocks, *, lookahead=1, lookahead_k=0, interest=0.0, heat=None, host_routes=False):
         n = len(blocks)
         self.blocks = blocks
         self.descs = (MoeDesc * n)(*[MoeDesc.from_buffer_copy(b.desc) for b in blocks])
@@ -127,7 +127,7 @@ class MoeStack:
         self.heat = None if heat is None else np.ascontiguousarray(heat, np.float32)
         self.opts = StackOpts(lookahead, lookahead_k, interest,
                               None if self.heat is None else self.heat.ctypes.data,
-                              self.instinct.ctypes.data, self.seen.ctypes.data)
+                              self.instinct.ctypes.data, self.seen.ctypes.data, int(host_routes))
         nbytes = int(lib.tlm_hip_moe_stack_workspace_bytes(self.descs, n, C.byref(self.opts)))
         self.workspace = torch.empty(nbytes + 256, dtype=torch.uint8, device=blocks[0].workspace.device)
         self._ws = (self.workspace.data_ptr() + 255) & ~255
