@@ -457,25 +457,26 @@ QWEN3_235B_A22B = dict(n_layers=94, d_model=4096, n_heads=64, n_kv_heads=4, head
                       rope_theta=1e6, norm_eps=1e-6, routed_scale=1.0)
 
 
-def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gamma=0.14, pf_len=512):
+def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gamma=0.14, pf_len=512, expert_dt=12):
     """The whole Qwen3-235B-A22B-shaped model (94 layers, hidden 4096, 64 q / 4
-    kv heads x 128 with qk-norm, 128 experts top-8 of width 1536 in Q4_K,
-    Q8_0 dense and lm_head, vocabulary 151936, random init) decoding with its
-    experts behind the HBM slot cache capped at cache_gb: the payloads
-    (127.7 GB as the cache sees them: 12,032 experts of 10.6 MB, drawn from a
-    pool of `pool` distinct payloads in page-locked host memory so the host
-    holds under 1 GB) load over PCIe on a miss; sigmoid routing with the
+    kv heads x 128 with qk-norm, 128 experts top-8 of width 1536 in Q4_K
+    (expert_dt 12) or Q5_K (13), Q8_0 dense and lm_head, vocabulary 151936,
+    random init) decoding with its experts behind the HBM slot cache capped at
+    cache_gb: the payloads (Q4_K: 127.7 GB as the cache sees them, 12,032
+    experts of 10.6 MB; Q5_K: 156.1 GB, 13.0 MB each; drawn from a pool of
+    `pool` distinct payloads in page-locked host memory so the host holds a
+    few GB at most) load over PCIe on a miss; sigmoid routing with the
     Zipf-like selection bias -gamma ln(rank + 1) on a per-layer order of the
     experts; the reference runtime's store defaults (pin share 0.30, router
     lookahead one layer ahead, top_k hints).  A prompt, `warm` greedy tokens
     to fill the cache, then `tokens` timed greedy tokens (host clock around
-    the steps: every layer waits for its routing on the host).  Then, from an
-    empty context and the cache as decoding left it, a `pf_len`-token prompt
-    prefilled batched through the cache (each layer's union of the prompt's
-    experts acquired once), host clock around tlm_hip_model_prefill."""
+    the steps).  Then, with pf_len > 0, from an empty context and the cache as
+    decoding left it, a `pf_len`-token prompt prefilled batched through the
+    cache (each layer's union of the prompt's experts acquired once), host
+    clock around tlm_hip_model_prefill."""
     from tierlm_amd.model import Model, bench_prompt
     t0 = time.perf_counter()
-    m = Model.synth(QWEN3_235B_A22B, expert_dt=Q4_K, dense_dt=8, seed=11,
+    m = Model.synth(QWEN3_235B_A22B, expert_dt=expert_dt, dense_dt=8, seed=11,
                     max_ctx=max(prompt_len + warm + tokens, pf_len) + 8,
                     expert_pool=pool, heat_gamma=gamma, expert_cache=int(cache_gb * (1 << 30)))
     built = time.perf_counter() - t0
@@ -490,30 +491,34 @@ def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gam
         m.sync()
         dt = time.perf_counter() - h0
         s1 = m.store_stats()
-        assert m.prefill_batched()
-        m.reset()
-        pp = bench_prompt(pf_len, QWEN3_235B_A22B["vocab"], seed=7)
-        m.sync()
-        h1 = time.perf_counter()
-        m.prefill(pp, logits=False)
-        m.sync()
-        pf_dt = time.perf_counter() - h1
-        s2 = m.store_stats()
+        if pf_len > 0:
+            assert m.prefill_batched()
+            m.reset()
+            pp = bench_prompt(pf_len, QWEN3_235B_A22B["vocab"], seed=7)
+            m.sync()
+            h1 = time.perf_counter()
+            m.prefill(pp, logits=False)
+            m.sync()
+            pf_dt = time.perf_counter() - h1
+            s2 = m.store_stats()
     finally:
         m.close()
     L, K = QWEN3_235B_A22B["n_layers"], QWEN3_235B_A22B["top_k"]
     miss = (s1["misses"] - s0["misses"]) / tokens
     pre = (s1["prefetch_issued"] - s0["prefetch_issued"]) / tokens
-    plen = 2 * 1536 * (4096 // 256 * 144) + 4096 * (1536 // 256 * 144)
-    r = {"model": "Qwen3-235B-A22B shape, whole model: 94 layers, hidden 4096, 64 q / 4 kv heads x 128, qk-norm, "
-                  "128 experts top-8 of width 1536 (Q4_K, 10.6 MB each, 127.7 GB) behind the HBM slot cache, Q8_0 "
-                  "dense and lm_head, vocabulary 151936, random init",
+    bb = 144 if expert_dt == Q4_K else 176
+    plen = 2 * 1536 * (4096 // 256 * bb) + 4096 * (1536 // 256 * bb)
+    name = "Q4_K" if expert_dt == Q4_K else "Q5_K"
+    r = {"model": f"Qwen3-235B-A22B shape, whole model: 94 layers, hidden 4096, 64 q / 4 kv heads x 128, qk-norm, "
+                  f"128 experts top-8 of width 1536 ({name}, {plen / 1e6:.1f} MB each, {plen * 12032 / 1e9:.1f} GB) "
+                  f"behind the HBM slot cache, Q8_0 dense and lm_head, vocabulary 151936, random init",
+         "expert_dtype": name,
          "cache_GB": cache_gb, "slots": s1["slots"], "pinned": s1["pinned"], "tokens": tokens,
          "warmup_tokens": warm, "prompt": prompt_len, "tok_s": round(tokens / dt, 2),
          "ms_per_token": round(dt / tokens * 1e3, 2), "misses_per_token": round(miss, 2),
          "hit_rate": round(1.0 - miss / (L * K), 4), "prefetch_issued_per_token": round(pre, 2),
          "load_GBps": round((miss + pre) * plen * tokens / dt / 1e9, 2), "build_s": round(built, 1),
-         "prefill": {"prompt": pf_len, "ms": round(pf_dt * 1e3, 1), "tok_s": round(pf_len / pf_dt, 1),
+         "prefill": None if pf_len <= 0 else {"prompt": pf_len, "ms": round(pf_dt * 1e3, 1), "tok_s": round(pf_len / pf_dt, 1),
                      "acquires": s2["hits"] + s2["misses"] - s1["hits"] - s1["misses"],
                      "misses": s2["misses"] - s1["misses"],
                      "load_GBps": round((s2["misses"] - s1["misses"]) * plen / pf_dt / 1e9, 2),
@@ -521,12 +526,13 @@ def c5_model_bench(torch, tokens, cache_gb, prompt_len=32, warm=40, pool=64, gam
                                "chunks, each layer's union of the chunk's experts through the cache) and a sync"},
          "timing": "host wall clock around tlm_hip_model_decode of the timed tokens and a sync, after the prompt and "
                    "the warm-up tokens"}
-    log(f"bench: Qwen3-235B-A22B-shape whole model through the slot cache ({r['slots']} slots, {cache_gb:.0f} GB): {r['tok_s']:.2f} tok/s "
+    log(f"bench: Qwen3-235B-A22B-shape whole model, {name} experts, through the slot cache ({r['slots']} slots, {cache_gb:.0f} GB): {r['tok_s']:.2f} tok/s "
         f"({r['ms_per_token']:.2f} ms/token), {r['misses_per_token']:.2f} misses/token (hit rate {r['hit_rate']:.4f}), "
         f"{r['prefetch_issued_per_token']:.1f} lookahead loads/token, {r['load_GBps']:.2f} GB/s over PCIe")
     q = r["prefill"]
-    log(f"bench: Qwen3-235B-A22B-shape {pf_len}-token prompt batched through the slot cache: {q['ms']:.1f} ms = "
-        f"{q['tok_s']:.1f} tok/s, {q['acquires']} acquires, {q['misses']} misses ({q['load_GBps']:.2f} GB/s over PCIe)")
+    if q:
+        log(f"bench: Qwen3-235B-A22B-shape {pf_len}-token prompt batched through the slot cache: {q['ms']:.1f} ms = "
+            f"{q['tok_s']:.1f} tok/s, {q['acquires']} acquires, {q['misses']} misses ({q['load_GBps']:.2f} GB/s over PCIe)")
     return r
 
 
@@ -882,7 +888,7 @@ def main():
         del W
         torch.cuda.empty_cache()
     c1 = None if args.no_c1 or not os.path.exists(C1_STORE) else c1_bench(3)
-    c5 = c5m = None
+    c5 = c5m = c5q5 = None
     if not args.no_c5:
         try:
             c5 = c5_bench(torch, dev, args.c5_tokens, args.c5_cache_gb)
@@ -895,6 +901,12 @@ def main():
         except Exception as e:
             c5m = {"error": repr(e)}
             log(f"bench: Qwen3-235B-A22B-shape whole model failed: {e!r}")
+        torch.cuda.empty_cache()
+        try:
+            c5q5 = c5_model_bench(torch, args.c5_tokens, args.c5_cache_gb, pf_len=0, expert_dt=13)
+        except Exception as e:
+            c5q5 = {"error": repr(e)}
+            log(f"bench: Qwen3-235B-A22B-shape whole model (Q5_K) failed: {e!r}")
         torch.cuda.empty_cache()
 
     cpu = None
@@ -916,7 +928,8 @@ def main():
                           "value": None, "unit": "tok/s", "n_gpus": 1, "note": "--no-c3: whole-model legs skipped",
                           "expert_gemv": c2, "cpu_baseline": cpu, "prefill": prefill, "prefill_q5k": prefill_q5k,
                           "slot_cache": slot_cache, "c1_whole_step": c1, "stream_read": peak,
-                          "qwen3_235b_a22b_slot_cache": c5, "qwen3_235b_a22b_model": c5m}), flush=True)
+                          "qwen3_235b_a22b_slot_cache": c5, "qwen3_235b_a22b_model": c5m,
+                          "qwen3_235b_a22b_model_q5k": c5q5}), flush=True)
         return
 
     line = {
@@ -964,6 +977,7 @@ def main():
                     "the reference fixtures"},
         "qwen3_235b_a22b_slot_cache": c5,
         "qwen3_235b_a22b_model": c5m,
+        "qwen3_235b_a22b_model_q5k": c5q5,
     }
     print(json.dumps(line), flush=True)
 
