@@ -319,6 +319,10 @@ __device__ __forceinline__ float reduce32(float r) {
 
 /* blockIdx.y = token: its residual at hptr + y * D, its workspace at
  * ws + y * tstride (the decode launches have one token). */
+/* NPRE chunks of each router row in flight from the start (4 for rows of up
+ * to 2048 values, 8 for wider ones, so a 4096-wide row needs no second round
+ * trip for its weights) */
+template <int NPRE>
 __device__ __forceinline__ void router_body(const tlm_hip_moe_desc &d, const WsLayout &L, const float *__restrict__ hptr,
                                             uint8_t *ws, const int blk) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -330,13 +334,12 @@ __device__ __forceinline__ void router_body(const tlm_hip_moe_desc &d, const WsL
     const GAS f32x4 *h4 = (const GAS f32x4 *)hptr, *n4 = (const GAS f32x4 *)d.ffn_norm;
     const int64_t nfull = D / RCHV, ctail = nfull * RCHV;
 
-    /* the first four full chunks (2048 values of the row) and the partial
-     * last chunk in flight before the norm */
-    float v0[RCH], v1[RCH], v2[RCH], v3[RCH], vt[RCH];
-    if (nfull > 0) load_chunk<false>(v0, wr, 0, hl, D);
-    if (nfull > 1) load_chunk<false>(v1, wr, RCHV, hl, D);
-    if (nfull > 2) load_chunk<false>(v2, wr, 2 * RCHV, hl, D);
-    if (nfull > 3) load_chunk<false>(v3, wr, 3 * RCHV, hl, D);
+    /* the first NPRE full chunks and the partial last chunk in flight before
+     * the norm */
+    float v[NPRE][RCH], vt[RCH];
+#pragma unroll
+    for (int c = 0; c < NPRE; c++)
+        if (nfull > c) load_chunk<false>(v[c], wr, c * RCHV, hl, D);
     if (ctail < D) load_chunk<true>(vt, wr, ctail, hl, D);
 
     /* rmsnorm (src/lib/tlm_model.c:164-169): sum of squares in double, lane
@@ -416,22 +419,15 @@ __device__ __forceinline__ void router_body(const tlm_hip_moe_desc &d, const WsL
 
     /* router row: element i -> lane i mod 32, fmaf in element order, then the
      * reduce32 tree (src/lib/tlm_quant.c:724-738); each buffer is refilled
-     * four chunks ahead as soon as it is consumed */
+     * NPRE chunks ahead as soon as it is consumed */
     float r = 0.0f;
-    for (int64_t c = 0; c < nfull; c += 4) {
-        r = fma_chunk<false>(v0, xb, c * RCHV, hl, D, r);
-        if (c + 4 < nfull) load_chunk<false>(v0, wr, (c + 4) * RCHV, hl, D);
-        if (c + 1 < nfull) {
-            r = fma_chunk<false>(v1, xb, (c + 1) * RCHV, hl, D, r);
-            if (c + 5 < nfull) load_chunk<false>(v1, wr, (c + 5) * RCHV, hl, D);
-        }
-        if (c + 2 < nfull) {
-            r = fma_chunk<false>(v2, xb, (c + 2) * RCHV, hl, D, r);
-            if (c + 6 < nfull) load_chunk<false>(v2, wr, (c + 6) * RCHV, hl, D);
-        }
-        if (c + 3 < nfull) {
-            r = fma_chunk<false>(v3, xb, (c + 3) * RCHV, hl, D, r);
-            if (c + 7 < nfull) load_chunk<false>(v3, wr, (c + 7) * RCHV, hl, D);
+    for (int64_t c = 0; c < nfull; c += NPRE) {
+#pragma unroll
+        for (int i = 0; i < NPRE; i++) {
+            if (c + i < nfull) {
+                r = fma_chunk<false>(v[i], xb, (c + i) * RCHV, hl, D, r);
+                if (c + i + NPRE < nfull) load_chunk<false>(v[i], wr, (c + i + NPRE) * RCHV, hl, D);
+            }
         }
     }
     if (ctail < D) r = fma_chunk<true>(vt, xb, ctail, hl, D, r);
@@ -473,12 +469,15 @@ __device__ __forceinline__ void router_body(const tlm_hip_moe_desc &d, const WsL
     }
 }
 
+template <int NPRE>
 __global__ __launch_bounds__(64) void k_moe_router(tlm_hip_moe_desc d, WsLayout L, const float *__restrict__ hptr,
                                                    uint8_t *ws, size_t tstride) {
     args_now(d.D, d.E, d.eps, d.router_w, d.ffn_norm, d.ds, d.expert_dt, d.shared_dt, d.shared_gate_inp, L.logits,
              L.xb, L.xe, L.xs, L.route, hptr, ws, tstride, gridDim.x);
-    router_body(d, L, hptr + (size_t)blockIdx.y * d.D, ws + (size_t)blockIdx.y * tstride, blockIdx.x);
+    router_body<NPRE>(d, L, hptr + (size_t)blockIdx.y * d.D, ws + (size_t)blockIdx.y * tstride, blockIdx.x);
 }
+/* chunks in flight from the start for rows of D values */
+inline int router_npre(int64_t D) { return D > 4 * RCHV ? 8 : 4; }
 
 /* Several routers over the same residual in one launch (a block's and its
  * lookahead hints'): blockIdx.y picks the router, each with its own
@@ -490,10 +489,11 @@ struct RouterSet {
     uint8_t *ws[MULTI_ROUTES];
     int groups[MULTI_ROUTES];
 };
+template <int NPRE>
 __global__ __launch_bounds__(64) void k_moe_router_multi(const RouterSet S, const float *__restrict__ h) {
     const int i = blockIdx.y;
     if ((int)blockIdx.x >= S.groups[i]) return;
-    router_body(S.d[i], S.L[i], h, S.ws[i], blockIdx.x);
+    router_body<NPRE>(S.d[i], S.L[i], h, S.ws[i], blockIdx.x);
 }
 
 inline int router_groups(const tlm_hip_moe_desc &d) {
@@ -1504,7 +1504,8 @@ static int moe_phase(const tlm_hip_moe_desc *d, int phase, float *h, int32_t *id
     const unsigned g2 = (unsigned)(d->k * (d->de / GUR) + (d->ds > 0 ? d->ds / TILE_ROWS : 0));
     const unsigned g3 = (unsigned)(d->D / DROWS);
     if (phase == 0 || phase == 1)
-        hipLaunchKernelGGL(k_moe_router, dim3(g1), dim3(64), lds1, s, dv, L, (const float *)h, w8, (size_t)0);
+        hipLaunchKernelGGL(router_npre(d->D) == 8 ? k_moe_router<8> : k_moe_router<4>, dim3(g1), dim3(64), lds1, s,
+                           dv, L, (const float *)h, w8, (size_t)0);
     if (msp) {
         const MoeSlots ms = *msp;
         if (phase == 0 || phase == 2)
@@ -1571,7 +1572,10 @@ int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, in
         lds = al256((size_t)d[i]->D * 8) > lds ? al256((size_t)d[i]->D * 8) : lds;
     }
     if (lds > 64 * 1024) return tlmh_seterr(TLM_HIP_EUNSUP, "moe routes: D exceeds the LDS staging limit");
-    hipLaunchKernelGGL(k_moe_router_multi, dim3((unsigned)g, (unsigned)n), dim3(64), lds, s, rs, h);
+    int64_t dmax = 0;
+    for (int i = 0; i < n; i++) dmax = d[i]->D > dmax ? d[i]->D : dmax;
+    hipLaunchKernelGGL(router_npre(dmax) == 8 ? k_moe_router_multi<8> : k_moe_router_multi<4>,
+                       dim3((unsigned)g, (unsigned)n), dim3(64), lds, s, rs, h);
     RouteDev r{};
     if (rd) {
         if (!rd->tab || !rd->slot_out || !rd->report || rd->n_slots <= 0)
