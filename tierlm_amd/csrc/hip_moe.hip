@@ -1109,6 +1109,7 @@ __global__ __launch_bounds__(256) void k_moe_route_host(const RouteSet S, uint32
                                                         const RouteDev rd) {
     __shared__ RouteLds s_route;
     __shared__ int s_bad;
+    __shared__ int32_t s_row[MAXE];
     const int i = blockIdx.x;
     const tlm_hip_moe_desc &d = S.d[i];
     const int q = threadIdx.x;
@@ -1117,13 +1118,30 @@ __global__ __launch_bounds__(256) void k_moe_route_host(const RouteSet S, uint32
     ExpTabLanes tab;
     tab.load();
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
-    route_group(d, (const GAS float *)(S.ws[i] + S.L[i].logits), R, []() {}, tab);
-    /* the routed experts' slots: one read of the table each (mapped host
-     * memory, system scope); any expert without a landed slot sends the
+    /* the layer's row of the slot table (mapped host memory, system scope),
+     * read while the logits arrive and the routing runs.  Safe that early:
+     * this launch was queued after the host replayed the earlier layers (no
+     * entry of this layer's experts can be cleared before its export), so an
+     * entry read here is at worst a load that lands a moment later (-1),
+     * which only hands the layer back */
+    int32_t rowv = -1;
+    int z;   /* 0, in a vector register: the loaded value stays per lane */
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    /* unconditional (a branch around it would make the routing wait for it);
+     * without a table the word read is the export's own area */
+    const int32_t *rp = dev ? rd.tab : (const int32_t *)host;
+    route_group(d, (const GAS float *)(S.ws[i] + S.L[i].logits), R, []() {}, tab, true, [&]() {
+        rowv = __hip_atomic_load(rp + (q < d.E ? q : 0) + z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    });
+    if (dev) {
+        if (q < d.E) s_row[q] = rowv;
+        __syncthreads();
+    }
+    /* the routed experts' slots; any expert without a landed slot sends the
      * whole layer back to the caller */
     int32_t v = -1;
     if (dev && q < d.k) {
-        v = __hip_atomic_load(rd.tab + R->ids[q], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        v = s_row[R->ids[q]];
         if (v < 0 || v >= rd.n_slots) s_bad = 1;
     }
     if (q < 32) {
