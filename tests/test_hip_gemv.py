@@ -148,10 +148,14 @@ def test_matvec_tiles_ranges(hip, dev, dt):
 
 @pytest.mark.parametrize("dt", INT)
 @pytest.mark.parametrize("rows,n", [(16, 256), (48, 512), (37, 768), (768, 2048), (2048, 768), (100, 4096),
-                                    (64, 8192)])
+                                    (64, 8192), (4096, 8192), (4100, 2048), (16400, 512)])
 def test_matvec_packed(hip, dev, dt, rows, n):
     """Packed tile layout == oracle, including a partial last tile and rows
-    longer than one chunk of blocks (Q8_0: 128 blocks, others 64)."""
+    longer than one chunk of blocks (Q8_0: 128 blocks, others 64), through the
+    model's launch: quarter tiles per group for few tiles, half tiles from 256
+    tiles on (4100 x 2048; 4096 x 8192, the Qwen3-235B-A22B o projection's
+    shape, two chunks of blocks per row for Q8_0), whole tiles from 1024
+    tiles on (16400 x 512)."""
     rng = np.random.default_rng(rows * 31 + n + dt)
     W = random_code_rows(rng, dt, rows, n)
     if rows <= 64:

@@ -297,47 +297,6 @@ template <> struct MvCfg<DT_Q8_0, true> {
 static bool mv_deep(int dt, int nb) { return dt == DT_Q8_0 && nb >= 64; }
 static int mv_nbc(int dt, int nb) { return mv_deep(dt, nb) ? MvCfg<DT_Q8_0, true>::NBC : MvCfg<DT_Q6_K, false>::NBC; }
 
-template <int DT, bool DEEP>
-__global__ __launch_bounds__(256) void k_mv_packed(const uint8_t *__restrict__ Wp, int64_t rows, int nb,
-                                                   const uint8_t *__restrict__ act, float *__restrict__ y) {
-    using F = Packed<DT>;
-    constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
-    constexpr int IPL = MvCfg<DT, DEEP>::IPL;                     /* items in flight per lane */
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int kind = dt_act_kind(DT);
-    const XLds X = stage_act(kind, act, nb, lds);
-    const int cap = nb < MvCfg<DT, DEEP>::NBC ? nb : MvCfg<DT, DEEP>::NBC;
-    const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * TILE_ROWS);
-    __syncthreads();
-
-    const int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS, t = blockIdx.x;
-    const int64_t units = T * nb * TILE_ROWS;
-    const int round_items = (GROUP_THREADS / F::LPI) * IPL;
-    float acc = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += cap) {
-        const int nbc = nb - b0 < cap ? nb - b0 : cap;
-        const int nitems = nbc * TILE_ROWS;
-        for (int base = 0; base < nitems; base += round_items) {
-            auto map = [&](int it, const uint8_t *&W, int64_t &un, int64_t &u, int &b, int &pk) {
-                const int g = base + it, bl = g / TILE_ROWS, i = g % TILE_ROWS;
-                W = Wp;
-                un = units;
-                b = b0 + bl;
-                u = ((int64_t)t * nb + b) * TILE_ROWS + i;
-                pk = g;
-            };
-            run_items<DT, IPL, MvCfg<DT, DEEP>::CLAMP>(nitems - base, map, [&]() { return X; }, park);
-        }
-        __syncthreads();
-        if (threadIdx.x < TILE_ROWS) acc = chain_park<AFF>(park, nbc, 0, TILE_ROWS, threadIdx.x, acc);
-        __syncthreads();
-    }
-    if (threadIdx.x < TILE_ROWS) {
-        const int64_t r = t * TILE_ROWS + threadIdx.x;
-        if (r < rows) y[r] = acc;
-    }
-}
-
 /* rmsnorm of x (when w is given) then the activation quantiser of kind,
  * written straight into the LDS layout that stage_act fills from a quantised
  * vector: r = 1 / sqrtf(mean(x^2) + eps) with the sum of squares in double
@@ -744,21 +703,12 @@ int launch_matvec_packed(int dt, const void *Wp, int64_t rows, int64_t n, const 
     if (packed_lds_bytes(dt, nb) > 64 * 1024)
         return tlmh_seterr(TLM_HIP_EUNSUP, "matvec_packed: n=%lld exceeds the staged-activation limit", (long long)n);
     if (n == 0) return launch_matvec_plain(dt, Wp, 0, act, y, 0, 0, rows, s);
-    int64_t T = (rows + TILE_ROWS - 1) / TILE_ROWS;
-    size_t lds = packed_lds_bytes(dt, nb);
-    dim3 g((unsigned)T), blk(256);
-    const uint8_t *w = (const uint8_t *)Wp, *a = (const uint8_t *)act;
-    switch (dt) {
-    case DT_Q8_0:
-        if (mv_deep(dt, nb)) hipLaunchKernelGGL((k_mv_packed<DT_Q8_0, true>), g, blk, lds, s, w, rows, nb, a, y);
-        else hipLaunchKernelGGL((k_mv_packed<DT_Q8_0, false>), g, blk, lds, s, w, rows, nb, a, y);
-        break;
-    case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed<DT_Q4_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
-    case DT_Q5_K: hipLaunchKernelGGL((k_mv_packed<DT_Q5_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
-    case DT_Q6_K: hipLaunchKernelGGL((k_mv_packed<DT_Q6_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
-    case DT_Q8_K: hipLaunchKernelGGL((k_mv_packed<DT_Q8_K, false>), g, blk, lds, s, w, rows, nb, a, y); break;
-    }
-    return tlmh_check(hipGetLastError(), "matvec_packed launch");
+    /* the model's segmented launch with one segment: the same kernel, the
+     * same rows-per-group rule */
+    float *ys[1] = {y};
+    const void *Ws[1] = {Wp};
+    const int64_t rs[1] = {rows};
+    return launch_mv_segs(dt, n, Ws, rs, ys, 1, 0, act, s, nullptr, nullptr);
 }
 
 int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows, float *const *y, int nseg, int accum,
@@ -794,7 +744,9 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
     const size_t lds = packed_lds_bytes(dt, nb);
     /* rows per group: whole tiles for matrices of many tiles (and for the
      * greedy keys, one per tile), else halves or quarters of tiles so that
-     * the launch spreads over the chip */
+     * the launch spreads over the chip (at the Qwen3-235B-A22B shape's
+     * 4352- and 8704-byte rows quarter or whole tiles were both slower than
+     * halves) */
     const int rpg = keys || end >= 1024 ? 16 : end >= 256 ? 8 : 4;
     const dim3 blk(256);
     const uint8_t *a = (const uint8_t *)act;
