@@ -32,6 +32,11 @@ Checks:
   (32 / 2 heads at D 2048), qk-norm - with 16 Q4_K experts top-8, over 1163
   positions (a 1100-token prompt and the first 63 greedy tokens), and the
   reference's 64 greedy tokens after the prompt;
+* C6D (oracle/make_c6d.sh, tests/golden/make_c6d_golden.sh): two leading
+  dense-FFN layers (first_k_dense_replace) then two MoE layers with a shared
+  expert, over 263 positions (a 200-token prompt and the first 63 greedy
+  tokens): top-10 logits bit for bit resident (graph replay and eager) and
+  through the slot cache, and the reference's 64 greedy tokens;
 * the split attention option (attn_split) on the three: the reference's
   greedy tokens, its top-1 at 99% or more of the teacher-forced positions;
 * the full Qwen3-235B-A22B geometry (D 4096, 64 / 4 heads x 128, 128 Q4_K
@@ -51,11 +56,13 @@ C1 = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
 C2S = os.path.join(ROOT, "oracle", "_ref", "c2s", "c2s.tlmm")
 C3S = os.path.join(ROOT, "oracle", "_ref", "c3s", "c3s.tlmm")
 C5S = os.path.join(ROOT, "oracle", "_ref", "c5s", "c5s.tlmm")
+C6D = os.path.join(ROOT, "oracle", "_ref", "c6d", "c6d.tlmm")
 GOLD = os.path.join(ROOT, "tests", "golden")
 needs_c1 = pytest.mark.skipif(not os.path.exists(C1), reason="oracle/_ref/c1 not built (oracle/make_c1.sh)")
 needs_c2s = pytest.mark.skipif(not os.path.exists(C2S), reason="oracle/_ref/c2s not built (oracle/make_c2s.sh)")
 needs_c3s = pytest.mark.skipif(not os.path.exists(C3S), reason="oracle/_ref/c3s not built (oracle/make_c3s.sh)")
 needs_c5s = pytest.mark.skipif(not os.path.exists(C5S), reason="oracle/_ref/c5s not built (oracle/make_c5s.sh)")
+needs_c6d = pytest.mark.skipif(not os.path.exists(C6D), reason="oracle/_ref/c6d not built (oracle/make_c6d.sh)")
 
 
 def prompt_tokens(vocab=4096, n=64):
@@ -197,6 +204,37 @@ def test_c5s_sixteen_query_heads_per_key_head(hip, max_ctx, slices):
         assert total == 1163 * 10
         m.reset()
         assert m.generate(prompt, 64) == gen
+    finally:
+        m.close()
+
+
+@needs_c6d
+@pytest.mark.parametrize("eager,budget", [(False, 0), (True, 0), (False, 1)])
+def test_c6d_dense_ffn_layers(hip, eager, budget):
+    """Two dense-FFN layers before the MoE layers (tlm_model.c:312-324,
+    946-964: rmsnorm, gate / up, silu(gate) * up, down added into h): every
+    position's top-10 logits teacher-forced and the reference's 64 greedy
+    tokens after the 200-token prompt - graph replay, eager launches, and the
+    experts through a cache of top_k slots (the dense layers before the
+    store's stack); dense layers route nothing."""
+    from tierlm_amd.model import Model
+    m = Model(C6D, max_ctx=512, eager=eager, expert_cache=budget)
+    try:
+        g = m.geom
+        assert (g.n_layers, g.d_model, g.n_heads, g.n_kv_heads, g.head_dim, g.n_experts, g.top_k, g.n_shared) == \
+            (4, 512, 8, 2, 64, 16, 4, 1)
+        gen = greedy_tokens("c6d_greedy.txt")
+        assert len(gen) == 64
+        prompt = prompt_tokens(2048, 200)
+        exact, total, worst = teacher_forced(m, "c6d_oracle.jsonl", prompt + gen[:63])
+        assert total == 263 * 10
+        ids, w = m.routes()
+        assert (ids[:2] == 0).all() and (w[:2] == 0).all() and (w[2:] > 0).all()
+        assert not m.prefill_batched()
+        m.reset()
+        assert m.generate(prompt, 64) == gen
+        if budget:
+            assert m.store_stats()["misses"] > 0
     finally:
         m.close()
 

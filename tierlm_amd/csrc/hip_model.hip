@@ -1313,6 +1313,11 @@ struct Layer {
     const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     DevMat q, k, v, o;
     tlm_hip_moe_desc moe{};
+    /* a dense-FFN layer (first_k_dense_replace / mlp_only_layers): gate, up
+     * [dffn x D], down [D x dffn]; no router, no experts */
+    bool dense = false;
+    DevMat dg, du, dd;
+    int64_t dffn = 0;
 };
 
 }  // namespace
@@ -1337,6 +1342,10 @@ struct tlm_hip_model {
     float *logits = nullptr;
     uint8_t *lm_act = nullptr;   /* the final norm's quantised activation, once per step for every lm_head group */
     uint8_t *moe_ws = nullptr;
+    float *dffn_buf = nullptr;   /* dense FFN layers: gate | up | silu(gate) * up, dffn_max each */
+    int64_t dffn_max = 0;
+    uint32_t dense_prefix = 0;   /* leading dense-FFN layers */
+    bool any_dense = false;
     int32_t *st = nullptr, *seq = nullptr, *ids = nullptr;   /* st[0] = position; seq[max_ctx + 1] tokens */
     unsigned long long *keys = nullptr;                      /* greedy key per lm_head tile */
     float *w = nullptr;
@@ -1606,8 +1615,13 @@ int finish(tlm_hip_model *M) {
     M->logits = (float *)M->dalloc((size_t)g.vocab * 4);
     M->lm_act = (uint8_t *)M->dalloc(act_bytes(DT_Q8_K, D) + act_bytes(DT_Q8_0, D));
     size_t ws = 0;
-    for (const Layer &Ly : M->L) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
+    for (const Layer &Ly : M->L)
+        if (!Ly.dense) ws = std::max(ws, tlm_hip_moe_workspace_bytes(&Ly.moe));
     M->moe_ws = (uint8_t *)M->dalloc(ws + 256);
+    if (M->any_dense) {
+        M->dffn_buf = (float *)M->dalloc((size_t)M->dffn_max * 3 * 4);
+        if (!M->dffn_buf) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the dense FFN");
+    }
     M->st = (int32_t *)M->dalloc(16);
     if (M->stats) {
         const size_t nst = (2 * (size_t)g.n_layers + 5) * 8;
@@ -1628,6 +1642,9 @@ int finish(tlm_hip_model *M) {
     if ((rc = tlmh_check(hipHostMalloc((void **)&M->host_tok, 64, hipHostMallocDefault), "model: pinned scratch")))
         return rc;
     if ((rc = tlmh_check(hipMemset(M->st, 0, 16), "model: position"))) return rc;
+    /* dense-FFN layers route nothing: their routing reads back as zeros */
+    if ((rc = tlmh_check(hipMemset(M->ids, 0, (size_t)g.n_layers * 32 * 4), "model: routing"))) return rc;
+    if ((rc = tlmh_check(hipMemset(M->w, 0, (size_t)g.n_layers * 32 * 4), "model: routing"))) return rc;
     return tlmh_check(hipStreamSynchronize(M->stream), "model: load");
 }
 
@@ -1647,6 +1664,10 @@ int open_expert_store(tlm_hip_model *M) {
         slot = std::max(slot, at);
     }
     if (slot == 0) return tlmh_seterr(TLM_HIP_EFORMAT, "model: no experts for the slot cache");
+    for (uint32_t l = M->dense_prefix; l < g.n_layers; l++)
+        if (M->L[l].dense)
+            return tlmh_seterr(TLM_HIP_EUNSUP, "model: with the slot cache, dense-FFN layers must come first (layer %u)",
+                               l);
     uint64_t budget = std::max<uint64_t>(M->xs_budget, (uint64_t)g.top_k * slot);
     uint64_t ns = budget / slot;
     ns = std::min<uint64_t>(ns, M->xs_src.size());
@@ -1674,7 +1695,9 @@ int open_expert_store(tlm_hip_model *M) {
     M->xopts.instinct_seen = M->instinct_seen.data();
     M->route_ids.assign((size_t)g.n_layers * g.top_k, 0);
     M->route_w.assign((size_t)g.n_layers * g.top_k, 0.0f);
-    const size_t ws = tlm_hip_moe_stack_workspace_bytes(M->descs.data(), (int)g.n_layers, &M->xopts);
+    /* the stack runs the MoE layers after the dense prefix */
+    const uint32_t K = M->dense_prefix;
+    const size_t ws = tlm_hip_moe_stack_workspace_bytes(M->descs.data() + K, (int)(g.n_layers - K), &M->xopts);
     M->stack_ws = (uint8_t *)M->dalloc(ws + 256);
     if (!M->stack_ws) return tlmh_seterr(TLM_HIP_ENOMEM, "model: out of device memory for the stack workspace");
     return TLM_HIP_OK;
@@ -1692,8 +1715,6 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
         if ((rc = read_packet(m, TLM_HIP_PK_DENSE, (int)l, 0, pk))) return rc;
         Layer &Ly = M->L[l];
         tlm_hip_tensor_ref t;
-        if (tlm_hip_dir_find(pk.payload(), pk.len, "ffn_gate", &t) == TLM_HIP_OK)
-            return tlmh_seterr(TLM_HIP_EUNSUP, "model: layer %u has a dense FFN", l);
         if ((rc = dev_vec(M, pk, "attn_norm", D, true, &Ly.attn_norm)) ||
             (rc = dev_vec(M, pk, "ffn_norm", D, true, &Ly.ffn_norm)) ||
             (rc = dev_vec(M, pk, "q_norm", hd, false, &Ly.q_norm)) ||
@@ -1703,6 +1724,24 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
             return rc;
         if (dt_act_kind(Ly.q.dt) != dt_act_kind(Ly.k.dt) || dt_act_kind(Ly.q.dt) != dt_act_kind(Ly.v.dt))
             return tlmh_seterr(TLM_HIP_EUNSUP, "model: q / k / v of layer %u take different activation kinds", l);
+        if (tlm_hip_dir_find(pk.payload(), pk.len, "ffn_gate", &t) == TLM_HIP_OK) {
+            /* a dense FFN (tlm_model.c:312-324): one SwiGLU block on ffn_norm's output */
+            const int64_t dffn = (int64_t)t.shape[0];
+            if (t.shape[1] != (uint64_t)D || dffn <= 0)
+                return tlmh_seterr(TLM_HIP_EFORMAT, "model: layer %u ffn_gate shape [%llu x %llu]", l,
+                                   (unsigned long long)t.shape[0], (unsigned long long)t.shape[1]);
+            if ((rc = dir_mat(M, pk, "ffn_gate", dffn, D, &Ly.dg)) || (rc = dir_mat(M, pk, "ffn_up", dffn, D, &Ly.du)) ||
+                (rc = dir_mat(M, pk, "ffn_down", D, dffn, &Ly.dd)))
+                return rc;
+            if (dt_act_kind(Ly.dg.dt) != dt_act_kind(Ly.du.dt))
+                return tlmh_seterr(TLM_HIP_EUNSUP, "model: gate / up of layer %u take different activation kinds", l);
+            Ly.dense = true;
+            Ly.dffn = dffn;
+            M->dffn_max = std::max(M->dffn_max, dffn);
+            if (M->dense_prefix == l) M->dense_prefix = l + 1;
+            M->any_dense = true;
+            continue;
+        }
         tlm_hip_moe_desc &d = Ly.moe;
         d.D = D;
         d.de = de;
@@ -1747,7 +1786,7 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
     for (int i = 0; i < tlm_hip_manifest_n_packets(m); i++) {
         const tlm_hip_packet_loc *loc = tlm_hip_manifest_packet(m, i);
         if (loc->type != TLM_HIP_PK_EXPERT) continue;
-        if (loc->layer >= g.n_layers || loc->id >= E)
+        if (loc->layer >= g.n_layers || loc->id >= E || M->L[loc->layer].dense)
             return tlmh_seterr(TLM_HIP_EFORMAT, "model: EXPERT packet %u:%u out of range", loc->layer, loc->id);
         heat_sum[loc->layer] += loc->heat;
         heat_cnt[loc->layer]++;
@@ -1804,6 +1843,7 @@ int load(tlm_hip_model *M, tlm_hip_manifest *m, const tlm_hip_model_opts *o) {
         }
     }
     for (uint32_t l = 0; l < g.n_layers; l++) {
+        if (M->L[l].dense) continue;   /* no experts to route (tlm_model.c:406, 621) */
         int live = 0;
         for (int64_t e = 0; e < E; e++) live += !masks[l][e];
         if (live < (int)g.top_k)   /* tlm_model.c:597-600 */
@@ -1899,6 +1939,48 @@ int enqueue_attention(tlm_hip_model *M, uint32_t l) {
     return rc;
 }
 
+/* silu(g) * u of a dense FFN (tlm_model.c:171, 955-956) */
+__global__ __launch_bounds__(256) void k_dense_swiglu(const float *__restrict__ g, const float *__restrict__ u,
+                                                      float *__restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        const float gv = g[i];
+        out[i] = gv / (1.0f + expf_ref(-gv)) * u[i];
+    }
+}
+
+/* layer l's dense FFN (moe()'s dense branch, tlm_model.c:946-964): gate | up
+ * in one launch whose groups each normalise and quantise h themselves (ffn_norm,
+ * as q | k | v do with attn_norm), silu(gate) * up, then down with the
+ * activation quantised in each group's prologue, added into h */
+int enqueue_dense_ffn(tlm_hip_model *M, uint32_t l) {
+    const tlm_hip_model_geom &g = M->g;
+    const int64_t D = g.d_model;
+    hipStream_t s = M->stream;
+    const Layer &Ly = M->L[l];
+    const int64_t F = Ly.dffn;
+    float *gb = M->dffn_buf, *ub = gb + M->dffn_max, *hb = ub + M->dffn_max;
+    const MvNorm fn{M->h, Ly.ffn_norm, g.norm_eps};
+    const void *W2[2] = {Ly.dg.p, Ly.du.p};
+    const int64_t R2[2] = {F, F};
+    float *const Y2[2] = {gb, ub};
+    int rc = TLM_HIP_OK;
+    if (Ly.dg.dt == Ly.du.dt) {
+        rc = launch_mv_segs(Ly.dg.dt, D, W2, R2, Y2, 2, 0, nullptr, s, &fn);
+    } else {
+        rc = launch_mv_segs(Ly.dg.dt, D, &W2[0], &R2[0], &Y2[0], 1, 0, nullptr, s, &fn);
+        if (!rc) rc = launch_mv_segs(Ly.du.dt, D, &W2[1], &R2[1], &Y2[1], 1, 0, nullptr, s, &fn);
+    }
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_dense_swiglu, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, s, gb, ub, hb, F);
+    if ((rc = tlmh_check(hipGetLastError(), "model: dense swiglu"))) return rc;
+    const MvNorm dn{hb, nullptr, 0.0f};
+    const void *Wd = Ly.dd.p;
+    const int64_t Rd = Ly.dd.rows;
+    float *const Yd = M->h;
+    return launch_mv_segs(Ly.dd.dt, F, &Wd, &Rd, &Yd, 1, 1, nullptr, s, &dn);
+}
+
 /* the step's end: final norm + lm_head with the greedy keys (tlm_model.c:
  * 1087-1095), then the argmax and the position's advance */
 int enqueue_tail(tlm_hip_model *M, bool want_logits) {
@@ -1952,8 +2034,10 @@ int enqueue_step(tlm_hip_model *M, bool want_logits) {
         rc = enqueue_attention(M, l);
         stamp(M, 2 + 2 * (size_t)l);
         /* moe(), tlm_model.c:940-1055 */
-        if (!rc) rc = launch_moe_layer(&Ly.moe, M->h, M->ids + (size_t)l * 32, M->w + (size_t)l * 32, M->moe_ws,
-                                       M->stream);
+        if (!rc)
+            rc = Ly.dense ? enqueue_dense_ffn(M, l)
+                          : launch_moe_layer(&Ly.moe, M->h, M->ids + (size_t)l * 32, M->w + (size_t)l * 32, M->moe_ws,
+                                             M->stream);
     }
     if (rc) return rc;
     stamp(M, 1 + 2 * L);
@@ -1974,14 +2058,31 @@ int step_cached(tlm_hip_model *M, bool want_logits) {
     stamp(M, 0);
     enqueue_embed(M);
     int rc = tlmh_check(hipGetLastError(), "model: embed");
+    /* the leading dense-FFN layers, then the MoE layers through the store
+     * (its layer numbers stay the model's; the per-layer state starts at K) */
+    const uint32_t K = M->dense_prefix;
+    for (uint32_t l = 0; l < K && !rc; l++) {
+        stamp(M, 1 + 2 * (size_t)l);
+        rc = enqueue_attention(M, l);
+        stamp(M, 2 + 2 * (size_t)l);
+        if (!rc) rc = enqueue_dense_ffn(M, l);
+    }
+    tlm_hip_stack_opts so = M->xopts;
+    if (so.layer_heat) so.layer_heat += K;
+    so.instinct += K;
+    so.instinct_seen += K;
     if (!rc)
-        rc = moe_stack_run(M->descs.data(), (int)L, M->xs, M->h, &M->xopts, M->route_ids.data(),
-                           M->route_w.data(), M->stack_ws, M->stream, [M](int l) {
-                               stamp(M, 1 + 2 * (size_t)l);
-                               const int r = enqueue_attention(M, (uint32_t)l);
-                               stamp(M, 2 + 2 * (size_t)l);
+        rc = moe_stack_run(M->descs.data() + K, (int)(L - K), M->xs, M->h, &so,
+                           M->route_ids.data() + (size_t)K * M->g.top_k, M->route_w.data() + (size_t)K * M->g.top_k,
+                           M->stack_ws, M->stream,
+                           [M, K](int l) {
+                               const uint32_t ml = K + (uint32_t)l;
+                               stamp(M, 1 + 2 * (size_t)ml);
+                               const int r = enqueue_attention(M, ml);
+                               stamp(M, 2 + 2 * (size_t)ml);
                                return r;
-                           });
+                           },
+                           (int)K);
     if (rc) return rc;
     stamp(M, 1 + 2 * L);
     rc = enqueue_tail(M, want_logits);
@@ -2040,6 +2141,7 @@ bool pf_supported(const tlm_hip_model *M) {
     if (g.d_model % 256 || ((int64_t)g.n_heads * g.head_dim) % 256 || g.d_model > 8192 ||
         (int64_t)g.n_heads * g.head_dim > 8192)
         return false;
+    if (M->any_dense) return false;   /* dense-FFN layers: one step per token */
     for (const Layer &Ly : M->L) {
         if (!pf_dense_ok(Ly.q) || !pf_dense_ok(Ly.k) || !pf_dense_ok(Ly.v) || !pf_dense_ok(Ly.o)) return false;
         const int edt = Ly.moe.expert_dt;

@@ -1112,7 +1112,7 @@ static void update_instinct(const tlm_hip_stack_opts *o, int l, const float *w, 
  * of route area `area` (hints routed hd[i].k wide), the breadth
  * interest-weighted (:863-874) */
 static void issue_hints(tlm_hip_store *s, const tlm_hip_stack_opts *o, const tlm_hip_moe_desc *descs, int l,
-                        const tlm_hip_moe_desc *hd, int n, const uint8_t *area) {
+                        const tlm_hip_moe_desc *hd, int n, const uint8_t *area, int layer0) {
     for (int i = 0; i < n; i++) {
         const int tl = l + 1 + i, hk = hd[i].k, top = descs[tl].k;
         const int32_t *hid = (const int32_t *)(area + ROUTE_BYTES * (1 + i));
@@ -1130,7 +1130,7 @@ static void issue_hints(tlm_hip_store *s, const tlm_hip_stack_opts *o, const tlm
             kk = top + (int)(W * (double)(hk - top) + 0.5);
             kk = std::min(kk, hd[i].E);
         }
-        tlm_hip_store_prefetch(s, tl, (const int *)hid, kk);
+        tlm_hip_store_prefetch(s, layer0 + tl, (const int *)hid, kk);
     }
 }
 
@@ -1146,8 +1146,8 @@ static int hint_descs(const tlm_hip_moe_desc *descs, int n_layers, int l, int de
 
 /* Whether the blocks can resolve their slots on the device: the slots share
  * one layout, and every layer's experts index the store's table. */
-static bool dev_resolvable(const tlm_hip_store *s, const tlm_hip_moe_desc *descs, int n_layers) {
-    if (!s->uniform || !s->tab_host || !s->rep_host || !s->res_dev || n_layers > s->tab_L) return false;
+static bool dev_resolvable(const tlm_hip_store *s, const tlm_hip_moe_desc *descs, int n_layers, int layer0) {
+    if (!s->uniform || !s->tab_host || !s->rep_host || !s->res_dev || layer0 + n_layers > s->tab_L) return false;
     for (int l = 0; l < n_layers; l++)
         if (descs[l].E > s->tab_E || descs[l].k > MOE_MAXK) return false;
     return true;
@@ -1176,7 +1176,7 @@ static bool dev_resolvable(const tlm_hip_store *s, const tlm_hip_moe_desc *descs
  * point on the stream, for whatever the caller enqueues next. */
 static int moe_stack_run_dev(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
                              const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace,
-                             hipStream_t st, const std::function<int(int)> &before) {
+                             hipStream_t st, const std::function<int(int)> &before, int layer0) {
     const int depth = stack_depth(o), lk = o ? o->lookahead_k : 0;
     size_t bsz, hsz;
     stack_layout(descs, n_layers, depth, lk, &bsz, &hsz);
@@ -1209,7 +1209,7 @@ static int moe_stack_run_dev(const tlm_hip_moe_desc *descs, int n_layers, tlm_hi
         const uint32_t seq = ++s->route_seq;
         s->route_n[area] = 1 + nh;
         RouteDev rd{};
-        rd.tab = s->tab_dev + (size_t)l * s->tab_E;
+        rd.tab = s->tab_dev + (size_t)(layer0 + l) * s->tab_E;
         rd.slot_out = s->res_dev + area * 32;
         rd.report = s->rep_dev + area;
         rd.n_slots = s->n_slots;
@@ -1233,12 +1233,12 @@ static int moe_stack_run_dev(const tlm_hip_moe_desc *descs, int n_layers, tlm_hi
         update_instinct(o, l, w, k);
         tlm_hip_expert_ref refs[MOE_MAXK];
         if (kept) {
-            rc = tlm_hip_store_acquire(s, l, ids, k, refs);
+            rc = tlm_hip_store_acquire(s, layer0 + l, ids, k, refs);
         } else {
-            rc = run_block(s, &descs[l], l, ids, w, h, blk[l & 1], refs, st);
+            rc = run_block(s, &descs[l], layer0 + l, ids, w, h, blk[l & 1], refs, st);
         }
         /* hints while this block's experts hold their references (:988-990) */
-        if (!rc) issue_hints(s, o, descs, l, hd, nh, ar);
+        if (!rc) issue_hints(s, o, descs, l, hd, nh, ar, layer0);
         for (int r = 0; r < k; r++) {
             if (l == n_layers - 1 || rc) tlm_hip_store_release(s, &refs[r], st);
             else release_retired(s, &refs[r]);
@@ -1259,7 +1259,7 @@ static int moe_stack_run_dev(const tlm_hip_moe_desc *descs, int n_layers, tlm_hi
  * arguments, and layer l + 1's attention is queued behind layer l's block. */
 int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
                   const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace, void *stream,
-                  const std::function<int(int)> &before) {
+                  const std::function<int(int)> &before, int layer0) {
     if (!descs || n_layers <= 0 || !s || !h || !workspace)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: bad arguments");
     if ((uintptr_t)workspace & 255u)
@@ -1270,8 +1270,8 @@ int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s,
     if (o && o->lookahead > 0 && o->lookahead_k > MOE_MAXK)
         return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: lookahead_k %d above %d", o->lookahead_k, MOE_MAXK);
     hipStream_t st = (hipStream_t)stream;
-    if (!(o && o->host_routes) && dev_resolvable(s, descs, n_layers))
-        return moe_stack_run_dev(descs, n_layers, s, h, o, ids_out, w_out, workspace, st, before);
+    if (!(o && o->host_routes) && dev_resolvable(s, descs, n_layers, layer0))
+        return moe_stack_run_dev(descs, n_layers, s, h, o, ids_out, w_out, workspace, st, before, layer0);
     const int depth = stack_depth(o), lk = o ? o->lookahead_k : 0;
     size_t bsz, hsz;
     stack_layout(descs, n_layers, depth, lk, &bsz, &hsz);
@@ -1308,11 +1308,11 @@ int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s,
         if (w_out) memcpy(w_out + (size_t)l * k, w, sizeof(float) * k);
         update_instinct(o, l, w, k);
         tlm_hip_expert_ref refs[MOE_MAXK];
-        rc = run_block(s, &descs[l], l, ids, w, h, blk[l & 1], refs, st);
+        rc = run_block(s, &descs[l], layer0 + l, ids, w, h, blk[l & 1], refs, st);
         /* the next layer's routing queued behind this block, before the host's bookkeeping */
         if (!rc && l + 1 < n_layers) rc = enqueue(l + 1, &seq);
         /* hints while this block's experts hold their references (:988-990) */
-        if (!rc) issue_hints(s, o, descs, l, hdl, hints_here, area);
+        if (!rc) issue_hints(s, o, descs, l, hdl, hints_here, area, layer0);
         for (int r = 0; r < k; r++) tlm_hip_store_release(s, &refs[r], stream);
     }
     if (!rc) tlm_hip_store_tick(s);
@@ -1327,7 +1327,7 @@ int tlm_hip_moe_stack_store(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip
     if (descs)
         for (int l = 0; l < n_layers; l++)
             if (!descs[l].experts) return tlmh_seterr(TLM_HIP_EINVAL, "moe_stack_store: layer %d has no expert table", l);
-    return moe_stack_run(descs, n_layers, s, h, o, ids_out, w_out, workspace, stream, {});
+    return moe_stack_run(descs, n_layers, s, h, o, ids_out, w_out, workspace, stream, {}, 0);
 }
 
 }  // extern "C"

@@ -341,9 +341,11 @@ int launch_moe_routes_host(const tlm_hip_moe_desc *const *d, void *const *ws, in
 int launch_publish_slot(int32_t *entry, int32_t v, hipStream_t s);
 /* tlm_hip_moe_stack_store's loop (hip_store.hip); before(l), when given,
  * enqueues what precedes layer l's router (a model's attention) and returns 0
- * or an error; descs' expert tables are not used */
+ * or an error; descs' expert tables are not used; descs[l] is the store's
+ * layer layer0 + l (a model whose first layers are dense FFNs), o's per-layer
+ * arrays start at descs[0]'s layer */
 int moe_stack_run(const tlm_hip_moe_desc *descs, int n_layers, tlm_hip_store *s, float *h,
                   const tlm_hip_stack_opts *o, int32_t *ids_out, float *w_out, void *workspace, void *stream,
-                  const std::function<int(int)> &before);
+                  const std::function<int(int)> &before, int layer0);
 
 #endif
