@@ -21,7 +21,10 @@ synthetic store (oracle/make_c1.sh) against the reference's own outputs
   A3B's attention geometry) `tierlm run` gives the reference's greedy tokens
   and `tierlm oracle` its top-10 text, and --stats reports the device
   cache's hits, misses and evictions and the device step's attention / MoE
-  split."""
+  split;
+* on C6D (oracle/make_c6d.sh), two dense-FFN layers before the MoE layers:
+  `tierlm oracle` gives the reference's top-10 text with every expert
+  resident, and `tierlm run` its greedy tokens through 4 slots."""
 import os
 import subprocess
 
@@ -34,6 +37,7 @@ TIERLM = os.path.join(ROOT, "oracle", "_ref", "dropin", "bin", "tierlm")
 C1 = os.path.join(ROOT, "oracle", "_ref", "c1", "c1.tlmm")
 GOLD = os.path.join(ROOT, "tests", "golden")
 C2S = os.path.join(ROOT, "oracle", "_ref", "c2s", "c2s.tlmm")
+C6D = os.path.join(ROOT, "oracle", "_ref", "c6d", "c6d.tlmm")
 needs = pytest.mark.skipif(not (os.path.exists(TIERLM) and os.path.exists(C1)),
                            reason="oracle/_ref/dropin (python3 oracle/dropin.py) or oracle/_ref/c1 not built")
 
@@ -157,3 +161,23 @@ def test_run_hip_slot_cache_c3s():
     assert r.stdout.split() == golden("c3s_greedy.txt").split()
     st = stats_fields(r.stderr)
     assert st["slots"] == 8 and st["misses"] > 0 and st["evictions"] > 0, r.stderr[-1500:]
+
+
+@pytest.mark.skipif(not (os.path.exists(TIERLM) and os.path.exists(C6D)), reason="oracle/_ref/dropin or c6d not built")
+def test_dense_ffn_layers_c6d():
+    """Two dense-FFN layers before the MoE layers: the reference's
+    teacher-forced top-10 text line for line with every expert in HBM, and
+    its 64 greedy tokens after the 200-token prompt through 4 slots."""
+    gen = golden("c6d_greedy.txt").split()
+    p = ",".join(map(str, prompt_ids(200, 2048)))
+    r = tierlm(["oracle", C6D, "--tokens", p + "," + ",".join(gen[:63]), "--cache", "1G", "--kernel", "hip"])
+    want = golden("c6d_oracle.jsonl").splitlines()
+    got = r.stdout.splitlines()
+    assert len(got) == len(want) == 263
+    bad = [i for i, (a, b) in enumerate(zip(got, want)) if a != b]
+    assert not bad, f"{len(bad)} positions differ, first {bad[0]}: {got[bad[0]]} vs {want[bad[0]]}"
+    r = tierlm(["run", C6D, "--tokens", p, "-n", "64", "--print-tokens", "--cache", "1", "--kernel", "hip",
+                "--stats"])
+    assert r.stdout.split() == gen
+    st = stats_fields(r.stderr)
+    assert st["slots"] == 4 and st["misses"] > 0, r.stderr[-1500:]
