@@ -209,16 +209,17 @@ def test_c5s_sixteen_query_heads_per_key_head(hip, max_ctx, slices):
 
 
 @needs_c6d
-@pytest.mark.parametrize("eager,budget", [(False, 0), (True, 0), (False, 1)])
-def test_c6d_dense_ffn_layers(hip, eager, budget):
+@pytest.mark.parametrize("eager,budget,chunk", [(False, 0, 0), (True, 0, 96), (False, 1, 0), (False, 1, 96)])
+def test_c6d_dense_ffn_layers(hip, eager, budget, chunk):
     """Two dense-FFN layers before the MoE layers (tlm_model.c:312-324,
     946-964: rmsnorm, gate / up, silu(gate) * up, down added into h): every
     position's top-10 logits teacher-forced and the reference's 64 greedy
-    tokens after the 200-token prompt - graph replay, eager launches, and the
-    experts through a cache of top_k slots (the dense layers before the
-    store's stack); dense layers route nothing."""
+    tokens after the 200-token prompt, run batched (one chunk, or three of
+    68) - graph replay, eager launches, and the experts through a cache of
+    top_k slots (the dense layers before the store's stack); dense layers
+    route nothing."""
     from tierlm_amd.model import Model
-    m = Model(C6D, max_ctx=512, eager=eager, expert_cache=budget)
+    m = Model(C6D, max_ctx=512, eager=eager, expert_cache=budget, prefill_chunk=chunk)
     try:
         g = m.geom
         assert (g.n_layers, g.d_model, g.n_heads, g.n_kv_heads, g.head_dim, g.n_experts, g.top_k, g.n_shared) == \
@@ -230,7 +231,10 @@ def test_c6d_dense_ffn_layers(hip, eager, budget):
         assert total == 263 * 10
         ids, w = m.routes()
         assert (ids[:2] == 0).all() and (w[:2] == 0).all() and (w[2:] > 0).all()
-        assert not m.prefill_batched()
+        assert m.prefill_batched()
+        m.reset()
+        lg = m.prefill(prompt)
+        assert int(np.argmax(lg)) == gen[0]
         m.reset()
         assert m.generate(prompt, 64) == gen
         if budget:

@@ -1343,6 +1343,7 @@ struct tlm_hip_model {
     uint8_t *lm_act = nullptr;   /* the final norm's quantised activation, once per step for every lm_head group */
     uint8_t *moe_ws = nullptr;
     float *dffn_buf = nullptr;   /* dense FFN layers: gate | up | silu(gate) * up, dffn_max each */
+    float *pf_ffn = nullptr;     /* the same for a prefill chunk, [cap][dffn_max] each */
     int64_t dffn_max = 0;
     uint32_t dense_prefix = 0;   /* leading dense-FFN layers */
     bool any_dense = false;
@@ -2141,9 +2142,13 @@ bool pf_supported(const tlm_hip_model *M) {
     if (g.d_model % 256 || ((int64_t)g.n_heads * g.head_dim) % 256 || g.d_model > 8192 ||
         (int64_t)g.n_heads * g.head_dim > 8192)
         return false;
-    if (M->any_dense) return false;   /* dense-FFN layers: one step per token */
     for (const Layer &Ly : M->L) {
         if (!pf_dense_ok(Ly.q) || !pf_dense_ok(Ly.k) || !pf_dense_ok(Ly.v) || !pf_dense_ok(Ly.o)) return false;
+        if (Ly.dense) {   /* gate / up / down as token matmuls */
+            if (!pf_dense_ok(Ly.dg) || !pf_dense_ok(Ly.du) || !pf_dense_ok(Ly.dd) || Ly.dffn % 256 || Ly.dffn > 65536)
+                return false;
+            continue;
+        }
         const int edt = Ly.moe.expert_dt;
         if ((edt != DT_Q4_K && edt != DT_Q5_K && edt != DT_Q6_K) || (!Ly.moe.experts && !M->xs)) return false;
         const int sdt = Ly.moe.shared_dt;
@@ -2170,10 +2175,12 @@ int pf_alloc(tlm_hip_model *M) {
     cap = cap >= 4 ? cap & ~3 : cap < 1 ? 1 : cap;
     size_t ws = 0;
     for (const Layer &Ly : M->L) {
+        if (Ly.dense) continue;
         const size_t b = moe_prefill_workspace_bytes(&Ly.moe, cap);
         ws = b > ws ? b : ws;
     }
-    const int64_t wmax = D > HQ ? D : HQ;
+    int64_t wmax = D > HQ ? D : HQ;
+    wmax = wmax > M->dffn_max ? wmax : M->dffn_max;
     M->pf_h = (float *)M->dalloc((size_t)cap * D * 4);
     M->pf_q = (float *)M->dalloc((size_t)cap * HQ * 4);
     M->pf_kx = (float *)M->dalloc((size_t)cap * KVD * 4);
@@ -2185,6 +2192,7 @@ int pf_alloc(tlm_hip_model *M) {
     M->pf_ws = (uint8_t *)M->dalloc(ws);
     M->pf_ids = (int32_t *)M->dalloc((size_t)cap * g.top_k * 4);
     M->pf_w = (float *)M->dalloc((size_t)cap * g.top_k * 4);
+    if (M->any_dense) M->pf_ffn = (float *)M->dalloc((size_t)cap * M->dffn_max * 3 * 4);
     bool host_ok = true;
     if (M->xs) {   /* the routing back on the host; an expert table per pass, at most one pass per expert */
         const size_t tab = (size_t)g.n_experts * 3 * g.n_experts * sizeof(void *);
@@ -2195,11 +2203,12 @@ int pf_alloc(tlm_hip_model *M) {
         host_ok = host_ok && M->pf_dev_tab;
     }
     if (!M->pf_h || !M->pf_q || !M->pf_kx || !M->pf_vx || !M->pf_att || !M->pf_y || !M->pf_scores || !M->pf_act ||
-        !M->pf_ws || !M->pf_ids || !M->pf_w || !host_ok) {
+        !M->pf_ws || !M->pf_ids || !M->pf_w || !host_ok || (M->any_dense && !M->pf_ffn)) {
         (void)hipGetLastError();
         for (void **p : {(void **)&M->pf_h, (void **)&M->pf_q, (void **)&M->pf_kx, (void **)&M->pf_vx,
                          (void **)&M->pf_att, (void **)&M->pf_y, (void **)&M->pf_scores, (void **)&M->pf_act,
-                         (void **)&M->pf_ws, (void **)&M->pf_ids, (void **)&M->pf_w, (void **)&M->pf_dev_tab}) {
+                         (void **)&M->pf_ws, (void **)&M->pf_ids, (void **)&M->pf_w, (void **)&M->pf_dev_tab,
+                         (void **)&M->pf_ffn}) {
             M->dfree(*p);
             *p = nullptr;
         }
@@ -2227,6 +2236,30 @@ int pf_matmul(tlm_hip_model *M, const DevMat &W, const float *x, int64_t n, cons
         *act_kind = rc ? -1 : kind;
     }
     if (!rc) rc = launch_tokmm(W.dt, W.p, W.rows, n, M->pf_act, nt, y, M->stream);
+    return rc;
+}
+
+/* Layer l's dense FFN for the chunk's nt tokens: the step's launches as
+ * token matmuls (each token's values the step's bits) */
+int pf_dense_ffn(tlm_hip_model *M, uint32_t l, int nt) {
+    const Layer &Ly = M->L[l];
+    const int64_t D = M->g.d_model, F = Ly.dffn;
+    float *gb = M->pf_ffn, *ub = gb + (size_t)nt * F, *hb = ub + (size_t)nt * F;
+    int ak = -1;
+    int rc = pf_matmul(M, Ly.dg, M->pf_h, D, Ly.ffn_norm, nt, gb, &ak);
+    if (!rc) rc = pf_matmul(M, Ly.du, M->pf_h, D, Ly.ffn_norm, nt, ub, &ak);
+    if (rc) return rc;
+    const int64_t cnt = (int64_t)nt * F;
+    hipLaunchKernelGGL(k_dense_swiglu, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, M->stream, gb, ub, hb, cnt);
+    if ((rc = tlmh_check(hipGetLastError(), "model prefill: dense swiglu"))) return rc;
+    ak = -1;
+    rc = pf_matmul(M, Ly.dd, hb, F, nullptr, nt, M->pf_y, &ak);
+    if (!rc) {
+        const int64_t c2 = (int64_t)nt * D;
+        hipLaunchKernelGGL(k_pf_add, dim3((unsigned)((c2 + NT * 4 - 1) / (NT * 4))), dim3(NT), 0, M->stream, M->pf_h,
+                           (const float *)M->pf_y, c2);
+        rc = tlmh_check(hipGetLastError(), "model prefill: dense residual");
+    }
     return rc;
 }
 
@@ -2345,6 +2378,10 @@ int prefill_batched(tlm_hip_model *M, int p0, int n, bool want_logits) {
                 rc = tlmh_check(hipGetLastError(), "model prefill: residual");
             }
             stamp(M, 2 + 2 * (size_t)l);
+            if (Ly.dense) {   /* the dense FFN, token by token's bits: gate, up, silu(gate) * up, down, + h */
+                if (!rc) rc = pf_dense_ffn(M, l, nt);
+                continue;
+            }
             if (!rc)
                 rc = M->xs ? pf_moe_cached(M, l, nt)
                            : launch_moe_prefill(&Ly.moe, M->pf_h, nt, M->pf_ids, M->pf_w, M->pf_ws, s);
