@@ -77,11 +77,12 @@ __global__ __launch_bounds__(NT) void k_pf_add(float *__restrict__ h, const floa
  * k_attn_pv: a group per (query head, PV_EW = 16 output elements), so a
  * head of width 128 spreads over 8 groups and 32 heads cover the chip's 256
  * CUs.  All four waves run the softmax in the reference's order - the
- * maximum over the context, e_t = e^(s_t - max), their sum in double, inv =
- * 1 / sum, p_t = e_t * inv (probabilities in LDS), e^x with its table held
- * in the lanes - then the P.V sums out += p_t * v_t[i] over ascending t:
+ * maximum over the context, e_t = e^(s_t - max) (kept in LDS), their sum in
+ * double, inv = 1 / sum, p_t = e_t * inv (formed by the producers as they
+ * read e_t), e^x with its table held in the lanes - then the P.V sums out +=
+ * p_t * v_t[i] over ascending t:
  * wave 0 holds the chains (lane i mod 16 runs element i's) and only adds,
- * one dependent add per position (about 4.5 clocks); waves 1-3, 12 lanes per
+ * one dependent add per position (about 6.5 clocks); waves 1-3, 12 lanes per
  * element, form the products p_t v_t[i] (the reference's rounded products)
  * into a ring of three LDS blocks of 48 value tiles, two blocks ahead of the
  * chains, with their value tiles PV_VPF blocks ahead in registers (the first
@@ -443,23 +444,30 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     float acc = 0.0f;
     for (int sb = 0; sb < T; sb += ATT_PSEG) {   /* uniform over the group */
         const int se = min(T, sb + ATT_PSEG);
-        if (nseg == 1) {   /* each thread scales the terms it stored: p = e * inv */
-            for (int t = tid; t < T; t += NT) s_p[t] = s_p[t] * inv_s;
-        } else {   /* every lane through every pass: e^x reads its table from the other lanes */
+        /* s_p holds the segment's terms e_t; the producers form p_t = e_t *
+         * inv as they read them.  One segment: the exp pass stored them */
+        if (nseg > 1) {   /* every lane through every pass: e^x reads its table from the other lanes */
             for (int t0 = sb; t0 < se; t0 += NT) {
                 const int t = t0 + tid;
-                const float p = expf_ref_with(S[min(t, se - 1)] - mx, tab) * inv_s;
-                if (t < se) s_p[t - sb] = p;
+                const float ex = expf_ref_with(S[min(t, se - 1)] - mx, tab);
+                if (t < se) s_p[t - sb] = ex;
             }
         }
         const int nbk = (se - sb + BT * 4 - 1) / (BT * 4);   /* blocks of the segment */
         const int q0 = sb >> 2;   /* the segment's first tile */
-        /* the probabilities of a producer lane's tiles of block blk (LDS reads
-         * shared by the lanes of a tile column), read a block ahead of their use */
+        /* the probabilities p_t = e_t * inv (tlm_model.c:710, 715) of a
+         * producer lane's tiles of block blk (LDS reads shared by the lanes of
+         * a tile column), read a block ahead of their use */
         auto pread = [&](int blk, f32x4 (&p)[TPL]) {
             const f32x4 *p4 = (const f32x4 *)s_p;
 #pragma unroll
-            for (int u = 0; u < TPL; u++) p[u] = p4[min(blk * BT + tc + TL * u, ATT_PSEG / 4 - 1)];
+            for (int u = 0; u < TPL; u++) {
+                const f32x4 ev = p4[min(blk * BT + tc + TL * u, ATT_PSEG / 4 - 1)];
+                p[u].x = ev.x * inv_s;
+                p[u].y = ev.y * inv_s;
+                p[u].z = ev.z * inv_s;
+                p[u].w = ev.w * inv_s;
+            }
         };
         auto produce = [&](int blk, const f32x4 (&p)[TPL], const f32x4 (&r)[TPL], int buf) {
             const int tl0 = blk * BT;   /* the block's first tile in the segment */
@@ -494,7 +502,7 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
                 for (int k = 0; k < VPF; k++) vload(q0, k, lastq, vq[k]);
             }
             f32x4 pc[TPL];
-            __syncthreads();   /* the segment's probabilities */
+            if (nseg > 1) __syncthreads();   /* the segment's terms (one segment: stored before the sum's barrier) */
             pread(0, pc);
             produce(0, pc, vq[0], 0);
             vload(q0, VPF, lastq, vq[0]);
@@ -532,7 +540,7 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
              * of its adds (the next block's first part during this block's last) */
             constexpr int SUB = 8, NPART = BT / SUB;
             static_assert(BT % SUB == 0, "whole parts");
-            __syncthreads();   /* the segment's probabilities */
+            if (nseg > 1) __syncthreads();   /* the segment's terms */
             __syncthreads();
             f32x4 cur[SUB];
             const bool chain = lane < EW;   /* lanes past EW stay out of the LDS reads and adds */
@@ -560,7 +568,10 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
 #pragma unroll
                     for (int u = 0; u < SUB; u++) cur[u] = nx[u];
                 }
-                __syncthreads();
+                /* the chain wave writes no LDS, and its reads in flight are
+                 * of the next block's buffer, which the next step does not
+                 * overwrite: a bare barrier, without draining them */
+                __builtin_amdgcn_s_barrier();
             };
             int b = 0;
             for (; b + VPF <= nbk; b += VPF) {
