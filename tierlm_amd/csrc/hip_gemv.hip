@@ -555,12 +555,49 @@ template <int DT, bool DEEP, int RPG>
 __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
     int64_t tile;
     int part;
-    mv_group_tile<RPG>(blockIdx.x, gridDim.x, tile, part);
+    /* every per-segment field is read at entry, in the launch's first
+     * scalar round trip, and passed through an empty asm so that the
+     * compiler cannot turn the select below back into a read at a
+     * computed offset (a second, dependent round trip) */
+    static_assert(MV_SEGS == 4, "segment select");
+    const uint8_t *Wv[MV_SEGS];
+    int64_t rv[MV_SEGS], te[MV_SEGS];
+    float *yv[MV_SEGS];
+#pragma unroll
+    for (int i = 0; i < MV_SEGS; i++) {
+        Wv[i] = sg.W[i];
+        rv[i] = sg.rows[i];
+        te[i] = sg.tile_end[i];
+        yv[i] = sg.y[i];
+    }
+    const float *nx = sg.nx, *nw = sg.nw;
+    unsigned long long *keys = sg.keys;
+    float eps = sg.eps;
+    int nseg = sg.n, accum = sg.accum, nbv = nb;
+    const uint8_t *actv = act;
+    unsigned ngrid = gridDim.x;
+    asm volatile("" : "+s"(Wv[0]), "+s"(Wv[1]), "+s"(Wv[2]), "+s"(Wv[3]), "+s"(rv[0]), "+s"(rv[1]), "+s"(rv[2]),
+                 "+s"(rv[3]), "+s"(te[0]), "+s"(te[1]), "+s"(te[2]), "+s"(te[3]), "+s"(yv[0]), "+s"(yv[1]),
+                 "+s"(yv[2]), "+s"(yv[3]), "+s"(nx), "+s"(nw), "+s"(keys), "+s"(eps), "+s"(nseg), "+s"(accum),
+                 "+s"(nbv), "+s"(actv), "+s"(ngrid));
+    mv_group_tile<RPG>(blockIdx.x, ngrid, tile, part);
+    /* the group's segment: the count of segment ends at or below its tile */
     int s = 0;
-    while (s + 1 < sg.n && tile >= sg.tile_end[s]) s++;
-    const MvTile tl{sg.W[s], sg.rows[s], tile - (s ? sg.tile_end[s - 1] : 0), part * RPG, sg.y[s], sg.nx,
-                    sg.nw, sg.eps, sg.accum, sg.keys};
-    mv_packed_tile<DT, DEEP, RPG>(tl, nb, act);
+#pragma unroll
+    for (int i = 0; i + 1 < MV_SEGS; i++) s += i + 1 < nseg && tile >= te[i] ? 1 : 0;
+    const uint8_t *W = Wv[0];
+    int64_t rows = rv[0], first = 0;
+    float *y = yv[0];
+#pragma unroll
+    for (int i = 1; i < MV_SEGS; i++)
+        if (s == i) {
+            W = Wv[i];
+            rows = rv[i];
+            first = te[i - 1];
+            y = yv[i];
+        }
+    const MvTile tl{W, rows, tile - first, part * RPG, y, nx, nw, eps, accum, keys};
+    mv_packed_tile<DT, DEEP, RPG>(tl, nbv, actv);
 }
 
 /* One launch for a whole job of matrices (mv_job / mv_exec,
