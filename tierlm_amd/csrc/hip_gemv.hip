@@ -525,14 +525,14 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
         __builtin_amdgcn_s_waitcnt(0);
     }
     const int64_t r = t * TILE_ROWS + i0 + threadIdx.x;
-    if (threadIdx.x < RPG && r < rows) y[r] = sg.accum ? y[r] + acc : acc;
+    if (threadIdx.x < RPG && r < rows) ((GAS float *)y)[r] = sg.accum ? ((GAS float *)y)[r] + acc : acc;
     if (RPG == TILE_ROWS && sg.keys && threadIdx.x < 64) {   /* lanes 0..15 hold the tile's rows */
         unsigned long long key = threadIdx.x < TILE_ROWS && r < rows ? argmax_key(acc, (uint32_t)r) : 0ull;
         for (int o = 8; o > 0; o >>= 1) {
             const unsigned long long other = __shfl_xor(key, o, 64);
             key = other > key ? other : key;
         }
-        if (threadIdx.x == 0) sg.keys[t] = key;
+        if (threadIdx.x == 0) ((GAS unsigned long long *)sg.keys)[t] = key;
     }
 }
 /* group g -> (tile, part): work-groups go to the 8 XCDs round-robin by id,

@@ -204,6 +204,12 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
                                                     float *__restrict__ kc, float *__restrict__ vc,
                                                     float *__restrict__ scores, int H, int KV, int max_ctx, int G,
                                                     const int32_t *__restrict__ st, float eps) {
+    /* the arguments the first loads need, in the launch's first scalar round
+     * trip (the compiler otherwise fetches them in batches where they are
+     * first used; eps is needed only after the first loads land) */
+    asm volatile("" : "+s"(has_qn), "+s"(has_kn), "+s"(H), "+s"(KV), "+s"(max_ctx), "+s"(G)
+                 : "s"(q), "s"(kx), "s"(vx), "s"(q_norm), "s"(k_norm), "s"(cs_all), "s"(sn_all), "s"(kc), "s"(vc),
+                   "s"(scores), "s"(st));
     constexpr int H4 = HD / 4, HALF = HD / 2, KS = HD + 4;
     constexpr int CF = ATT_CH * H4 / NT;            /* float4 of a chunk's K per thread */
     constexpr int QF = ATT_QMAX / 4 / NT;           /* float4 of the query heads per thread, at most */
@@ -231,6 +237,9 @@ __global__ __launch_bounds__(NT) void k_attn_scores(const float *__restrict__ q,
         qn[e] = q_norm[sub + 16 * e];
         kn[e] = k_norm[sub + 16 * e];
     }
+    /* those loads stay above the position's read and the slice test that
+     * follows it (the compiler would otherwise sink them below the branch) */
+    asm volatile("" ::: "memory");
     const int pos = st[0], T = pos + 1;
     const int L = att_slice_len(T, G), t0 = (int)blockIdx.y * L;
     if (t0 >= T) return;
