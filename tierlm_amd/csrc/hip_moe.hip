@@ -334,28 +334,35 @@ __device__ __forceinline__ void router_body(const tlm_hip_moe_desc &d, const WsL
     const GAS f32x4 *h4 = (const GAS f32x4 *)hptr, *n4 = (const GAS f32x4 *)d.ffn_norm;
     const int64_t nfull = D / RCHV, ctail = nfull * RCHV;
 
-    /* the first NPRE full chunks and the partial last chunk in flight before
-     * the norm */
-    float v[NPRE][RCH], vt[RCH];
-#pragma unroll
-    for (int c = 0; c < NPRE; c++)
-        if (nfull > c) load_chunk<false>(v[c], wr, c * RCHV, hl, D);
-    if (ctail < D) load_chunk<true>(vt, wr, ctail, hl, D);
-
     /* rmsnorm (src/lib/tlm_model.c:164-169): sum of squares in double, lane
      * then wave tree; x and the norm weights parked in LDS (16-byte copies) */
     LAS f32x4 *xb4 = (LAS f32x4 *)lds;
     LAS f32x4 *xw4 = xb4 + D / 4;
     constexpr int NV = 8;   /* 16-byte loads of h and of the weights per lane per batch */
     const int D4 = (int)(D / 4);
-    if (D4 <= 64 * NV) {
-        /* one batch (D <= 2048): normalise in registers, write x once */
-        f32x4 hv[NV], nv[NV];
+    const bool one = D4 <= 64 * NV;   /* D <= 2048: h and the norm weights in one batch */
+    /* one batch: h and the norm weights go out first (loads retire in issue
+     * order, so the norm then waits for them alone), branch-free (lanes past
+     * the row read its last vector), then the router rows */
+    f32x4 hv[NV], nv[NV];
+    if (one) {
 #pragma unroll
         for (int j = 0; j < NV; j++) {
-            const int cc = lane + 64 * j;
-            if (cc < D4) { hv[j] = h4[cc]; nv[j] = n4[cc]; }
+            const int cc = min(lane + 64 * j, D4 - 1);
+            hv[j] = h4[cc];
+            nv[j] = n4[cc];
         }
+    }
+    /* the first NPRE full chunks and the partial last chunk in flight
+     * during the norm */
+    float v[NPRE][RCH], vt[RCH];
+#pragma unroll
+    for (int c = 0; c < NPRE; c++)
+        if (nfull > c) load_chunk<false>(v[c], wr, c * RCHV, hl, D);
+    if (ctail < D) load_chunk<true>(vt, wr, ctail, hl, D);
+
+    if (one) {
+        /* normalise in registers, write x once */
         double ss = 0.0;
 #pragma unroll
         for (int j = 0; j < NV; j++)
