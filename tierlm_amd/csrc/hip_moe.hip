@@ -612,9 +612,11 @@ template <> struct GivenArgT<GIVEN> { using type = MoeGiven; };
 template <> struct GivenArgT<SLOTS> { using type = MoeSlots; };
 template <int MODE> using GivenArg = typename GivenArgT<MODE>::type;
 
-/* rows of a 16-row tile per routed gate/up group: half tiles, 768 groups at
- * Qwen3-30B-A3B shape, three to a compute unit (the register cap below) */
-constexpr int GUR = 8;
+/* rows of a 16-row tile per routed gate/up group: quarter tiles, 1536
+ * groups at the Qwen3-30B-A3B shape (3072 at Qwen3-235B-A22B's), so that
+ * while some groups of a compute unit route, others stream their weights (a
+ * compute unit's load queue, not HBM, paces each group's weight issue) */
+constexpr int GUR = 4;
 template <int EDT, int SDT, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_moe_gateup(tlm_hip_moe_desc d, WsLayout L, int32_t *ids_out, float *w_out,
                                                     uint8_t *ws, const GivenArg<MODE> gv) {
