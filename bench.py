@@ -49,6 +49,7 @@ HBM_PEAK_GBS = 8000.0
 # scaled by its reading for a 256 MiB device copy (factors 1.99980 and 1.0); the run and its
 # figures: profiles/moe_block_qwen3_30b_hbm_traffic.md
 GATEUP_TRAFFIC_BYTES = 20945811
+DENSE_TRAFFIC_BYTES = {}
 
 
 def log(msg):
@@ -784,6 +785,61 @@ def expert_gemv_bench(torch, dev, args, gen):
     return out, W, router_w, ffn_norm
 
 
+Q8_0 = 8
+# the decode step's dense Q8_0 matrices at the Qwen3-30B-A3B shape: q|k|v (32 + 4 + 4 heads x 128
+# rows of 2048), o (2048 rows of 4096), lm_head (151936 rows of 2048)
+DENSE_SHAPES = [("qkv", 5120, 2048), ("o", 2048, 4096), ("lm_head", 151936, 2048)]
+
+
+def dense_gemv_bench(torch, dev, layers, reps, gen):
+    """The decode step's dense Q8_0 GEMVs through tlm_hip_matvec_packed (the
+    step's segmented launch with one segment, activation given quantised):
+    per shape, random code bytes in the packed layout (`layers` copies of
+    q|k|v and o cycled, so no launch re-reads the last-level cache), a graph
+    of `reps` back-to-back launches, HIP events, best of 3."""
+    from tierlm_amd import quant as hq
+    out = {}
+    for name, rows, n in DENSE_SHAPES:
+        copies = 1 if name == "lm_head" else layers
+        pb = hq.packed_bytes(Q8_0, rows, n)
+        W = torch.empty((copies, pb), dtype=torch.uint8, device=dev).random_(0, 256, generator=gen)
+        act = hq.quantize_act(Q8_0, torch.randn(n, generator=gen, device=dev))
+        y = torch.empty(rows, dtype=torch.float32, device=dev)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            hq.matvec_packed(Q8_0, W[0], rows, n, act, y)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for t in range(reps):
+                hq.matvec_packed(Q8_0, W[t % copies], rows, n, act, y)
+        g.replay()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(3):
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            g.replay()
+            ev1.record()
+            ev1.synchronize()
+            us = ev0.elapsed_time(ev1) * 1e3 / reps
+            best = us if best is None else min(best, us)
+        del g, W
+        gbs = pb / (best * 1e-6) / 1e9
+        out[name] = {"rows": rows, "n": n, "bytes_per_launch": pb, "avg_launch_us": round(best, 3),
+                     "achieved_GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": DENSE_TRAFFIC_BYTES.get(name)}
+    log("bench: dense GEMVs per launch: " + ", ".join(
+        f"{k} {v['avg_launch_us']:.2f} us ({v['achieved_GBps']:.0f} GB/s)" for k, v in out.items()))
+    out["timing"] = (f"HIP events around a graph of {reps} back-to-back launches per shape, / {reps} (best of 3); "
+                     "random code bytes, activation quantised once")
+    out["traffic_source"] = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch of this leg, each scaled by its "
+                             "reading for a 256 MiB device copy")
+    return out
+
+
 def stream_read_peak(torch, dev, nbytes):
     """A plain streaming read (tlm_hip_stream_read) over nbytes of device
     memory, best of 5, HIP events."""
@@ -867,8 +923,10 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(2)
     c2 = prefill = prefill_q5k = slot_cache = None
+    dense = None
     if not args.no_c2:
         c2, W, router_w, ffn_norm = expert_gemv_bench(torch, dev, args, gen)
+        dense = dense_gemv_bench(torch, dev, args.layers, args.roofline_tokens, gen)
         if args.copy_check_mib > 0:
             nbytes = args.copy_check_mib << 20
             src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
@@ -926,7 +984,8 @@ def main():
     if c3 is None:   # --no-c3: the other legs only
         print(json.dumps({"metric": "decode tok/s batch-1, Qwen3-30B-A3B shape; expert GEMV HBM GB/s vs peak",
                           "value": None, "unit": "tok/s", "n_gpus": 1, "note": "--no-c3: whole-model legs skipped",
-                          "expert_gemv": c2, "cpu_baseline": cpu, "prefill": prefill, "prefill_q5k": prefill_q5k,
+                          "expert_gemv": c2, "dense_gemv": dense, "cpu_baseline": cpu, "prefill": prefill,
+                          "prefill_q5k": prefill_q5k,
                           "slot_cache": slot_cache, "c1_whole_step": c1, "stream_read": peak,
                           "qwen3_235b_a22b_slot_cache": c5, "qwen3_235b_a22b_model": c5m,
                           "qwen3_235b_a22b_model_q5k": c5q5}), flush=True)
@@ -956,6 +1015,7 @@ def main():
                          c3["achieved_GBps"] / peak["GBps"], 4),
                      "stream_read_kernel": peak["kernel"]},
         "expert_gemv": c2,
+        "dense_gemv": dense,
         "cpu_baseline": cpu,
         "prefill": prefill,
         "prefill_q5k": prefill_q5k,

@@ -642,7 +642,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             return;
         }
     }
-    const int r = (int)blockIdx.x / te, q = (int)blockIdx.x - r * te, t = q / SPT, i0 = (q % SPT) * GUR;
+    /* group -> (rank, tile, part): work-groups go to the 8 XCDs round-robin
+     * by id, so in each run of 8 SPT ids the parts of 8 (rank, tile) pairs go
+     * to one XCD each (ids g, g + 8, ... share the XCD and its L2, whose lines
+     * hold neighbouring rows of a tile and its scale plane); ids of a last
+     * incomplete run map straight */
+    const int g = (int)blockIdx.x, run = g / (8 * SPT), tpe = te / SPT;
+    const bool whole = (run + 1) * 8 * SPT <= nexp;
+    const int tau = whole ? run * 8 + g % 8 : g / SPT, part = whole ? (g / 8) % SPT : g % SPT;
+    const int r = tau / tpe, t = tau - r * tpe, i0 = part * GUR;
     if constexpr (MODE == SLOTS) {   /* one load for the slot, then the weight loads */
         const int v = ((const GAS int32_t *)gv.slot)[r];
         if (v < 0) return;   /* the layer went back to the caller */
