@@ -45,11 +45,18 @@ TOKEN_BYTES = K * EXPERT_BYTES           # 30,965,760 B per token-layer
 GATEUP_BYTES = K * 2 * MAT_BYTES         # 20,643,840 B per gate/up launch
 DOWN_BYTES = K * MAT_BYTES               # 10,321,920 B per down launch
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per gate/up launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (KiB per dispatch), each
-# scaled by its reading for a 256 MiB device copy (factors 1.99980 and 1.0); the run and its
-# figures: profiles/moe_block_qwen3_30b_hbm_traffic.md
-GATEUP_TRAFFIC_BYTES = 20945811
-DENSE_TRAFFIC_BYTES = {}
+# HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (KiB per dispatch) of the MoE-block
+# and dense-GEMV legs, each scaled by its reading for a 256 MiB device copy (factors 1.99982 and
+# 1.0); the runs and their figures: profiles/moe_block_qwen3_30b_hbm_traffic.md
+GATEUP_TRAFFIC_BYTES = 20868827
+ROUTER_TRAFFIC_BYTES = 1383201
+DOWN_TRAFFIC_BYTES = 10892562
+DENSE_TRAFFIC_BYTES = {"qkv": 11322400, "o": 9071845, "lm_head": 331416531}
+# the decode step's kernels at the Qwen3-30B-A3B shape: per layer q|k|v + o + router + gate/up +
+# down, then lm_head once (the attention launches' K / V reads are added at their algorithmic bytes:
+# they run only inside the model, which is not profiled under counters)
+STEP_LAYER_TRAFFIC_BYTES = (DENSE_TRAFFIC_BYTES["qkv"] + DENSE_TRAFFIC_BYTES["o"] + ROUTER_TRAFFIC_BYTES
+                            + GATEUP_TRAFFIC_BYTES + DOWN_TRAFFIC_BYTES)
 
 
 def log(msg):
@@ -1005,7 +1012,14 @@ def main():
                    "timing": "HIP events on the model's stream around exactly K steps (each a context rewind + "
                              "one replay of the captured step graph)"},
         "roofline": {"bound": "hbm", "achieved": round(c3["achieved_GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(c3["achieved_GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(c3["achieved_GBps"] / HBM_PEAK_GBS, 4),
+                     "traffic": int(48 * STEP_LAYER_TRAFFIC_BYTES + DENSE_TRAFFIC_BYTES["lm_head"]
+                                    + c3["kv_bytes_per_token_mean"]),
+                     "traffic_source": "the step's launches summed: per layer the q|k|v, o, router, gate/up and down "
+                                       "kernels' HBM bytes per dispatch (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
+                                       "the same kernels at the same shapes in the MoE-block and dense-GEMV legs, "
+                                       "scaled by a 256 MiB copy), 48 layers, plus lm_head's, plus the mean K / V "
+                                       "read at its algorithmic bytes",
                      "kernel": "the decode step (its kernels' algorithmic bytes / the step time)",
                      "bytes_per_step": int(c3["bytes_per_token"]),
                      "weights_per_step": c3["weights_per_token"],
