@@ -785,6 +785,11 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
      * 4352- and 8704-byte rows quarter or whole tiles were both slower than
      * halves) */
     const int rpg = keys || end >= 1024 ? 16 : end >= 256 ? 8 : 4;
+    /* whole-tile launches (lm_head) take the shallow Q8_0 tile: the deep one
+     * holds 16 items per lane (234 VGPRs, one group per compute unit), the
+     * shallow one 4 in two rounds with four groups per compute unit, which
+     * stream more (lm_head 151936 x 2048: ~25 us less per launch) */
+    const bool deep = mv_deep(dt, nb) && rpg < TILE_ROWS;
     const dim3 blk(256);
     const uint8_t *a = (const uint8_t *)act;
     auto go = [&](auto rpg_c) -> int {
@@ -792,7 +797,7 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
         const dim3 g((unsigned)(end * (TILE_ROWS / R)));
         switch (dt) {
         case DT_Q8_0:
-            if (mv_deep(dt, nb)) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, true, R>), g, blk, lds, s, sg, nb, a);
+            if (deep) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, true, R>), g, blk, lds, s, sg, nb, a);
             else hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, false, R>), g, blk, lds, s, sg, nb, a);
             break;
         case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q4_K, false, R>), g, blk, lds, s, sg, nb, a); break;
