@@ -281,21 +281,31 @@ __global__ void k_pack_f32(const uint8_t *__restrict__ src, size_t row_bytes, in
  * threads extend their row's float chain over the chunk in block order.
  * The activation is staged once per work-group (all blocks).  Items in
  * flight per lane (IPL) and blocks per chunk (NBC): a round of loads costs
- * one memory latency, so for wide Q8_0 rows (DEEP: at least 64 blocks) a
+ * one memory latency, so for wide Q8_0 rows (DEEP: at least 128 blocks in
+ * the segmented launch; the job kernel's whole tiles take it from 64) a
  * lane (5 registers per item) keeps 16 in flight, branch-free, and a chunk
  * of 128 blocks is one round - a 16-row tile of up to 4096 columns streams in
- * a single latency; narrower rows keep 4 per lane (a deep round would be
- * mostly dropped items). */
-template <int DT, bool DEEP> struct MvCfg {
+ * a single latency; rows of 64 to 127 blocks (MID) keep 8 per lane, a chunk
+ * of 64 blocks in one round; narrower rows keep 4 per lane (a deep round
+ * would be mostly dropped items).  A group of RPG rows of a tile scales the
+ * items per lane by RPG / 16. */
+enum { MV_SHALLOW = 0, MV_DEEP = 1, MV_MID = 2 };
+template <int DT, int V> struct MvCfg {
     static constexpr int IPL = 4, NBC = 64;
     static constexpr bool CLAMP = false;
 };
-template <> struct MvCfg<DT_Q8_0, true> {
+template <> struct MvCfg<DT_Q8_0, MV_DEEP> {
     static constexpr int IPL = 16, NBC = 128;
     static constexpr bool CLAMP = true;
 };
+/* rows of 64 blocks in one round: a chunk of 64 blocks is exactly one round
+ * (the deep tile's round of 128 would load every second item in vain) */
+template <> struct MvCfg<DT_Q8_0, MV_MID> {
+    static constexpr int IPL = 8, NBC = 64;
+    static constexpr bool CLAMP = true;
+};
 static bool mv_deep(int dt, int nb) { return dt == DT_Q8_0 && nb >= 64; }
-static int mv_nbc(int dt, int nb) { return mv_deep(dt, nb) ? MvCfg<DT_Q8_0, true>::NBC : MvCfg<DT_Q6_K, false>::NBC; }
+static int mv_nbc(int dt, int nb) { return mv_deep(dt, nb) ? MvCfg<DT_Q8_0, MV_DEEP>::NBC : MvCfg<DT_Q6_K, MV_SHALLOW>::NBC; }
 
 /* rmsnorm of x (when w is given) then the activation quantiser of kind,
  * written straight into the LDS layout that stage_act fills from a quantised
@@ -458,7 +468,7 @@ struct MvTile {
  * only some tens of GB/s, so a matrix of few tiles (the o projection's 128)
  * spreads its rows over more groups than tiles, each with fewer items in
  * flight per lane */
-template <int DT, bool DEEP, int RPG>
+template <int DT, int DEEP, int RPG>
 __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const uint8_t *__restrict__ act) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
@@ -551,7 +561,7 @@ __device__ __forceinline__ void mv_group_tile(int64_t g, int64_t ngroups, int64_
         part = (int)(g % SPT);
     }
 }
-template <int DT, bool DEEP, int RPG>
+template <int DT, int DEEP, int RPG>
 __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
     int64_t tile;
     int part;
@@ -628,13 +638,13 @@ __global__ __launch_bounds__(256) void k_mv_job(MvJob j) {
         const MvTile tl{g.W, g.rows, bid, 0, g.y, nullptr, nullptr, 0.0f, 0, nullptr};
         switch (g.dt) {
         case DT_Q8_0:
-            if (g.kind == JK_PACKED_DEEP) mv_packed_tile<DT_Q8_0, true, TILE_ROWS>(tl, nb, g.act);
-            else mv_packed_tile<DT_Q8_0, false, TILE_ROWS>(tl, nb, g.act);
+            if (g.kind == JK_PACKED_DEEP) mv_packed_tile<DT_Q8_0, MV_DEEP, TILE_ROWS>(tl, nb, g.act);
+            else mv_packed_tile<DT_Q8_0, MV_SHALLOW, TILE_ROWS>(tl, nb, g.act);
             break;
-        case DT_Q4_K: mv_packed_tile<DT_Q4_K, false, TILE_ROWS>(tl, nb, g.act); break;
-        case DT_Q5_K: mv_packed_tile<DT_Q5_K, false, TILE_ROWS>(tl, nb, g.act); break;
-        case DT_Q6_K: mv_packed_tile<DT_Q6_K, false, TILE_ROWS>(tl, nb, g.act); break;
-        case DT_Q8_K: mv_packed_tile<DT_Q8_K, false, TILE_ROWS>(tl, nb, g.act); break;
+        case DT_Q4_K: mv_packed_tile<DT_Q4_K, MV_SHALLOW, TILE_ROWS>(tl, nb, g.act); break;
+        case DT_Q5_K: mv_packed_tile<DT_Q5_K, MV_SHALLOW, TILE_ROWS>(tl, nb, g.act); break;
+        case DT_Q6_K: mv_packed_tile<DT_Q6_K, MV_SHALLOW, TILE_ROWS>(tl, nb, g.act); break;
+        case DT_Q8_K: mv_packed_tile<DT_Q8_K, MV_SHALLOW, TILE_ROWS>(tl, nb, g.act); break;
         }
     } else if (g.kind == JK_PLAIN) {
         switch (g.dt) {
@@ -785,11 +795,14 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
      * 4352- and 8704-byte rows quarter or whole tiles were both slower than
      * halves) */
     const int rpg = keys || end >= 1024 ? 16 : end >= 256 ? 8 : 4;
-    /* whole-tile launches (lm_head) take the shallow Q8_0 tile: the deep one
-     * holds 16 items per lane (234 VGPRs, one group per compute unit), the
-     * shallow one 4 in two rounds with four groups per compute unit, which
-     * stream more (lm_head 151936 x 2048: ~25 us less per launch) */
-    const bool deep = mv_deep(dt, nb) && rpg < TILE_ROWS;
+    /* Q8_0 rows of 64 to 127 blocks take the mid tile (one round of a
+     * 64-block chunk); wider rows the deep tile, except whole-tile launches
+     * (lm_head), for which the deep tile holds 16 items per lane (234 VGPRs,
+     * one group per compute unit) and the shallow one, 4 per lane in two
+     * rounds with four groups per compute unit, streams more (lm_head 151936
+     * x 2048: ~25 us less per launch than deep; the mid tile's one round
+     * then took the Qwen3-30B-A3B-shape decode from 381.9 to 383.4 tok/s) */
+    const int var = !mv_deep(dt, nb) ? MV_SHALLOW : nb < 128 ? MV_MID : rpg < TILE_ROWS ? MV_DEEP : MV_SHALLOW;
     const dim3 blk(256);
     const uint8_t *a = (const uint8_t *)act;
     auto go = [&](auto rpg_c) -> int {
@@ -797,13 +810,14 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
         const dim3 g((unsigned)(end * (TILE_ROWS / R)));
         switch (dt) {
         case DT_Q8_0:
-            if (deep) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, true, R>), g, blk, lds, s, sg, nb, a);
-            else hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, false, R>), g, blk, lds, s, sg, nb, a);
+            if (var == MV_DEEP) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_DEEP, R>), g, blk, lds, s, sg, nb, a);
+            else if (var == MV_MID) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_MID, R>), g, blk, lds, s, sg, nb, a);
+            else hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_SHALLOW, R>), g, blk, lds, s, sg, nb, a);
             break;
-        case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q4_K, false, R>), g, blk, lds, s, sg, nb, a); break;
-        case DT_Q5_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q5_K, false, R>), g, blk, lds, s, sg, nb, a); break;
-        case DT_Q6_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q6_K, false, R>), g, blk, lds, s, sg, nb, a); break;
-        case DT_Q8_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_K, false, R>), g, blk, lds, s, sg, nb, a); break;
+        case DT_Q4_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q4_K, MV_SHALLOW, R>), g, blk, lds, s, sg, nb, a); break;
+        case DT_Q5_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q5_K, MV_SHALLOW, R>), g, blk, lds, s, sg, nb, a); break;
+        case DT_Q6_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q6_K, MV_SHALLOW, R>), g, blk, lds, s, sg, nb, a); break;
+        case DT_Q8_K: hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_K, MV_SHALLOW, R>), g, blk, lds, s, sg, nb, a); break;
         default: return tlmh_seterr(TLM_HIP_EINVAL, "mv_segs: dtype %d", dt);
         }
         return tlmh_check(hipGetLastError(), "mv_segs launch");
