@@ -51,7 +51,7 @@ HBM_PEAK_GBS = 8000.0
 GATEUP_TRAFFIC_BYTES = 20868827
 ROUTER_TRAFFIC_BYTES = 1383201
 DOWN_TRAFFIC_BYTES = 10892562
-DENSE_TRAFFIC_BYTES = {"qkv": 11322400, "o": 9071845, "lm_head": 331416531}
+DENSE_TRAFFIC_BYTES = {"qkv": 11293705, "o": 9071845, "lm_head": 331328952}
 # the decode step's kernels at the Qwen3-30B-A3B shape: per layer q|k|v + o + router + gate/up +
 # down, then lm_head once (the attention launches' K / V reads are added at their algorithmic bytes:
 # they run only inside the model, which is not profiled under counters)
