@@ -281,14 +281,14 @@ __global__ void k_pack_f32(const uint8_t *__restrict__ src, size_t row_bytes, in
  * threads extend their row's float chain over the chunk in block order.
  * The activation is staged once per work-group (all blocks).  Items in
  * flight per lane (IPL) and blocks per chunk (NBC): a round of loads costs
- * one memory latency, so for wide Q8_0 rows (DEEP: at least 128 blocks in
- * the segmented launch; the job kernel's whole tiles take it from 64) a
- * lane (5 registers per item) keeps 16 in flight, branch-free, and a chunk
- * of 128 blocks is one round - a 16-row tile of up to 4096 columns streams in
- * a single latency; rows of 64 to 127 blocks (MID) keep 8 per lane, a chunk
- * of 64 blocks in one round; narrower rows keep 4 per lane (a deep round
- * would be mostly dropped items).  A group of RPG rows of a tile scales the
- * items per lane by RPG / 16. */
+ * one memory latency, so for wide Q8_0 rows (DEEP: at least 128 blocks, in
+ * groups of part of a tile) a lane (5 registers per item) keeps 16 in
+ * flight, branch-free, and a chunk of 128 blocks is one round - a 16-row
+ * tile of up to 4096 columns streams in a single latency; rows of 64 to 127
+ * blocks and whole-tile groups (MID) keep 8 per lane, a chunk of 64 blocks
+ * in one round; narrower rows keep 4 per lane (a deep round would be mostly
+ * dropped items).  A group of RPG rows of a tile scales the items per lane by
+ * RPG / 16. */
 enum { MV_SHALLOW = 0, MV_DEEP = 1, MV_MID = 2 };
 template <int DT, int V> struct MvCfg {
     static constexpr int IPL = 4, NBC = 64;
@@ -615,7 +615,7 @@ __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const 
  * layout and activation; segment s owns groups [first[s], first[s + 1]) and
  * every group runs its segment's body (a uniform switch): a 16-row tile of a
  * packed matrix, 4 plain rows of an integer format or 8 f32 rows. */
-enum { JK_PACKED = 0, JK_PACKED_DEEP = 1, JK_PLAIN = 2, JK_F32 = 3, JK_F32_UNALIGNED = 4 };
+enum { JK_PACKED = 0, JK_PACKED_MID = 1, JK_PLAIN = 2, JK_F32 = 3, JK_F32_UNALIGNED = 4 };
 struct JobSeg {
     const uint8_t *W, *act;
     float *y;
@@ -633,12 +633,12 @@ __global__ __launch_bounds__(256) void k_mv_job(MvJob j) {
     while (s + 1 < j.n && (int64_t)blockIdx.x >= j.s[s + 1].first) s++;
     const JobSeg &g = j.s[s];
     const int64_t bid = (int64_t)blockIdx.x - g.first;
-    if (g.kind == JK_PACKED || g.kind == JK_PACKED_DEEP) {
+    if (g.kind == JK_PACKED || g.kind == JK_PACKED_MID) {
         const int nb = (int)(g.n / dt_block_values(g.dt));
         const MvTile tl{g.W, g.rows, bid, 0, g.y, nullptr, nullptr, 0.0f, 0, nullptr};
         switch (g.dt) {
         case DT_Q8_0:
-            if (g.kind == JK_PACKED_DEEP) mv_packed_tile<DT_Q8_0, MV_DEEP, TILE_ROWS>(tl, nb, g.act);
+            if (g.kind == JK_PACKED_MID) mv_packed_tile<DT_Q8_0, MV_MID, TILE_ROWS>(tl, nb, g.act);
             else mv_packed_tile<DT_Q8_0, MV_SHALLOW, TILE_ROWS>(tl, nb, g.act);
             break;
         case DT_Q4_K: mv_packed_tile<DT_Q4_K, MV_SHALLOW, TILE_ROWS>(tl, nb, g.act); break;
@@ -795,14 +795,15 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
      * 4352- and 8704-byte rows quarter or whole tiles were both slower than
      * halves) */
     const int rpg = keys || end >= 1024 ? 16 : end >= 256 ? 8 : 4;
-    /* Q8_0 rows of 64 to 127 blocks take the mid tile (one round of a
-     * 64-block chunk); wider rows the deep tile, except whole-tile launches
-     * (lm_head), for which the deep tile holds 16 items per lane (234 VGPRs,
-     * one group per compute unit) and the shallow one, 4 per lane in two
-     * rounds with four groups per compute unit, streams more (lm_head 151936
-     * x 2048: ~25 us less per launch than deep; the mid tile's one round
-     * then took the Qwen3-30B-A3B-shape decode from 381.9 to 383.4 tok/s) */
-    const int var = !mv_deep(dt, nb) ? MV_SHALLOW : nb < 128 ? MV_MID : rpg < TILE_ROWS ? MV_DEEP : MV_SHALLOW;
+    /* Q8_0 rows of 64 blocks or more: the mid tile (one round per 64-block
+     * chunk) for rows under 128 blocks and for whole-tile launches (lm_head),
+     * else the deep tile (one round per 128-block chunk).  For lm_head the
+     * deep tile holds 16 items per lane (234 VGPRs, one group per compute
+     * unit); the shallow tile (4 per lane, two rounds per chunk, four groups
+     * per compute unit) took 151936 x 2048 from 103 to 80 us and the mid
+     * tile to 71 us (Qwen3-30B-A3B-shape decode 381.9 -> 383.4 tok/s), and
+     * 151936 x 4096 from 150 us in the shallow tile to 127 us (5.2 TB/s) */
+    const int var = !mv_deep(dt, nb) ? MV_SHALLOW : nb < 128 || rpg == TILE_ROWS ? MV_MID : MV_DEEP;
     const dim3 blk(256);
     const uint8_t *a = (const uint8_t *)act;
     auto go = [&](auto rpg_c) -> int {
@@ -857,7 +858,7 @@ int launch_mv_job(const tlm_hip_seg *segs, int nseg, hipStream_t s) {
             const int nb = (int)(g->n / bv);
             need = packed_lds_bytes(g->dt, nb);
             if (need <= 64 * 1024) {
-                kind = mv_deep(g->dt, nb) ? JK_PACKED_DEEP : JK_PACKED;
+                kind = mv_deep(g->dt, nb) ? JK_PACKED_MID : JK_PACKED;
                 ng = (g->rows + TILE_ROWS - 1) / TILE_ROWS;
             }
         } else if (fmt && ptrs && !g->packed &&
