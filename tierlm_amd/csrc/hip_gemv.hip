@@ -469,7 +469,8 @@ struct MvTile {
  * spreads its rows over more groups than tiles, each with fewer items in
  * flight per lane */
 template <int DT, int DEEP, int RPG>
-__device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const uint8_t *__restrict__ act) {
+__device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const uint8_t *__restrict__ act,
+                                               bool have_x = false) {
     using F = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
     constexpr int IPL0 = MvCfg<DT, DEEP>::IPL * RPG / TILE_ROWS;
@@ -482,7 +483,9 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     const int kind = dt_act_kind(DT);
     XLds X = xlds_at(kind, nb, lds);
     NormIn nin;
-    if (!sg.nx) {
+    if (have_x) {
+        /* the activation is in LDS from the group's previous tile */
+    } else if (!sg.nx) {
         stage_act(kind, act, nb, lds);
         /* its loads are all consumed; a wait the compiler can see keeps its
          * count from holding back the other path's first weight loads */
@@ -493,7 +496,7 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     }
     const int cap = nb < MvCfg<DT, DEEP>::NBC ? nb : MvCfg<DT, DEEP>::NBC;
     const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * RPG);
-    bool staged = !sg.nx;
+    bool staged = !sg.nx || have_x;
     /* the activation from rmsnorm once the first weight loads are out: the
      * empty asm keeps the norm's arithmetic (and so its wait for x) below
      * the weight loads, where the compiler would otherwise hoist it */
@@ -561,8 +564,9 @@ __device__ __forceinline__ void mv_group_tile(int64_t g, int64_t ngroups, int64_
         part = (int)(g % SPT);
     }
 }
-template <int DT, int DEEP, int RPG>
+template <int DT, int DEEP, int RPG, int TPG = 1>
 __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const uint8_t *__restrict__ act) {
+    static_assert(TPG == 1 || RPG == TILE_ROWS, "several tiles per group take whole tiles");
     int64_t tile;
     int part;
     /* every per-segment field is read at entry, in the launch's first
@@ -590,24 +594,39 @@ __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const 
                  "+s"(rv[3]), "+s"(te[0]), "+s"(te[1]), "+s"(te[2]), "+s"(te[3]), "+s"(yv[0]), "+s"(yv[1]),
                  "+s"(yv[2]), "+s"(yv[3]), "+s"(nx), "+s"(nw), "+s"(keys), "+s"(eps), "+s"(nseg), "+s"(accum),
                  "+s"(nbv), "+s"(actv), "+s"(ngrid));
-    mv_group_tile<RPG>(blockIdx.x, ngrid, tile, part);
-    /* the group's segment: the count of segment ends at or below its tile */
-    int s = 0;
+    /* TPG > 1: whole tiles, TPG neighbouring tiles per group (the
+     * activation staged once): fewer groups, each with less of its life
+     * spent on its start and the staging */
+    int64_t end = te[0];
 #pragma unroll
-    for (int i = 0; i + 1 < MV_SEGS; i++) s += i + 1 < nseg && tile >= te[i] ? 1 : 0;
-    const uint8_t *W = Wv[0];
-    int64_t rows = rv[0], first = 0;
-    float *y = yv[0];
+    for (int i = 1; i < MV_SEGS; i++) end = te[i] > end ? te[i] : end;
 #pragma unroll
-    for (int i = 1; i < MV_SEGS; i++)
-        if (s == i) {
-            W = Wv[i];
-            rows = rv[i];
-            first = te[i - 1];
-            y = yv[i];
+    for (int k = 0; k < TPG; k++) {
+        if constexpr (TPG > 1) {
+            tile = (int64_t)blockIdx.x * TPG + k;
+            part = 0;
+            if (tile >= end) break;
+        } else {
+            mv_group_tile<RPG>(blockIdx.x, ngrid, tile, part);
         }
-    const MvTile tl{W, rows, tile - first, part * RPG, y, nx, nw, eps, accum, keys};
-    mv_packed_tile<DT, DEEP, RPG>(tl, nbv, actv);
+        /* the group's segment: the count of segment ends at or below its tile */
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i + 1 < MV_SEGS; i++) s += i + 1 < nseg && tile >= te[i] ? 1 : 0;
+        const uint8_t *W = Wv[0];
+        int64_t rows = rv[0], first = 0;
+        float *y = yv[0];
+#pragma unroll
+        for (int i = 1; i < MV_SEGS; i++)
+            if (s == i) {
+                W = Wv[i];
+                rows = rv[i];
+                first = te[i - 1];
+                y = yv[i];
+            }
+        const MvTile tl{W, rows, tile - first, part * RPG, y, nx, nw, eps, accum, keys};
+        mv_packed_tile<DT, DEEP, RPG>(tl, nbv, actv, k > 0);
+    }
 }
 
 /* One launch for a whole job of matrices (mv_job / mv_exec,
@@ -812,6 +831,9 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
         switch (dt) {
         case DT_Q8_0:
             if (var == MV_DEEP) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_DEEP, R>), g, blk, lds, s, sg, nb, a);
+            else if (var == MV_MID && R == TILE_ROWS && nb < 128)   /* two tiles per group */
+                hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_MID, R, (R == TILE_ROWS ? 2 : 1)>),
+                                   dim3((unsigned)((end + 1) / 2)), blk, lds, s, sg, nb, a);
             else if (var == MV_MID) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_MID, R>), g, blk, lds, s, sg, nb, a);
             else hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_SHALLOW, R>), g, blk, lds, s, sg, nb, a);
             break;
