@@ -290,6 +290,7 @@ __global__ void k_pack_f32(const uint8_t *__restrict__ src, size_t row_bytes, in
  * dropped items).  A group of RPG rows of a tile scales the items per lane by
  * RPG / 16. */
 enum { MV_SHALLOW = 0, MV_DEEP = 1, MV_MID = 2 };
+constexpr int MV_EARLY_WORDS = 5;   /* a8 words per thread of an activation loaded early */
 template <int DT, int V> struct MvCfg {
     static constexpr int IPL = 4, NBC = 64;
     static constexpr bool CLAMP = false;
@@ -468,7 +469,7 @@ struct MvTile {
  * only some tens of GB/s, so a matrix of few tiles (the o projection's 128)
  * spreads its rows over more groups than tiles, each with fewer items in
  * flight per lane */
-template <int DT, int DEEP, int RPG>
+template <int DT, int DEEP, int RPG, bool EARLY = false>
 __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const uint8_t *__restrict__ act,
                                                bool have_x = false) {
     using F = Packed<DT>;
@@ -483,8 +484,22 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     const int kind = dt_act_kind(DT);
     XLds X = xlds_at(kind, nb, lds);
     NormIn nin;
+    /* EARLY (a given a8 activation of at most AWN words per thread, no
+     * norm): the activation goes into registers ahead of the weight loads
+     * and into LDS once they are out (loads retire in issue order: one round
+     * trip for both instead of the staging's own before the weights) */
+    constexpr int AWN = MV_EARLY_WORDS;
+    constexpr bool EARLY_OK = EARLY && DT == DT_Q8_0;
+    uint32_t aw[AWN];
     if (have_x) {
         /* the activation is in LDS from the group's previous tile */
+    } else if constexpr (EARLY_OK) {
+        const GAS uint32_t *ag = (const GAS uint32_t *)act;
+#pragma unroll
+        for (int j = 0; j < AWN; j++) {
+            const int k = (int)threadIdx.x + GROUP_THREADS * j;
+            aw[j] = ag[k < nb * 9 ? k : 0];
+        }
     } else if (!sg.nx) {
         stage_act(kind, act, nb, lds);
         /* its loads are all consumed; a wait the compiler can see keeps its
@@ -496,12 +511,26 @@ __device__ __forceinline__ void mv_packed_tile(const MvTile &sg, int nb, const u
     }
     const int cap = nb < MvCfg<DT, DEEP>::NBC ? nb : MvCfg<DT, DEEP>::NBC;
     const Park park = park_at(lds + ((stage_bytes(kind, nb) + 15) & ~(size_t)15), cap * RPG);
-    bool staged = !sg.nx || have_x;
+    bool staged = EARLY_OK ? have_x : !sg.nx || have_x;
     /* the activation from rmsnorm once the first weight loads are out: the
      * empty asm keeps the norm's arithmetic (and so its wait for x) below
      * the weight loads, where the compiler would otherwise hoist it */
     auto stage = [&]() {
-        if (!staged) {
+        if constexpr (EARLY_OK) {
+            if (staged) return X;
+            LAS uint32_t *q = (LAS uint32_t *)lds;
+            LAS float *d = (LAS float *)((LAS uint8_t *)lds + nb * 32);
+#pragma unroll
+            for (int j = 0; j < AWN; j++) {
+                const int k = (int)threadIdx.x + GROUP_THREADS * j, b = k / 9, w = k - b * 9;
+                if (k < nb * 9) {
+                    if (w == 0) d[b] = __uint_as_float(aw[j]);
+                    else q[b * 8 + (w - 1)] = aw[j];
+                }
+            }
+            __syncthreads();
+            staged = true;
+        } else if (!staged) {
 #pragma unroll
             for (int u = 0; u < 4; u++) asm volatile("" : "+v"(nin.xv[u]), "+v"(nin.wv[u])::"memory");
             stage_norm_act(kind, sg.nx, sg.nw, sg.eps, nb, lds, nin);
@@ -625,7 +654,7 @@ __global__ __launch_bounds__(256) void k_mv_packed_seg(MvSegs sg, int nb, const 
                 y = yv[i];
             }
         const MvTile tl{W, rows, tile - first, part * RPG, y, nx, nw, eps, accum, keys};
-        mv_packed_tile<DT, DEEP, RPG>(tl, nbv, actv, k > 0);
+        mv_packed_tile<DT, DEEP, RPG, (TPG > 1)>(tl, nbv, actv, k > 0);
     }
 }
 
@@ -831,7 +860,8 @@ int launch_mv_segs(int dt, int64_t n, const void *const *W, const int64_t *rows,
         switch (dt) {
         case DT_Q8_0:
             if (var == MV_DEEP) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_DEEP, R>), g, blk, lds, s, sg, nb, a);
-            else if (var == MV_MID && R == TILE_ROWS && nb < 128)   /* two tiles per group */
+            else if (var == MV_MID && R == TILE_ROWS && nb < 128 && !norm && nb * 9 <= MV_EARLY_WORDS * 256)
+                /* two tiles per group, the given activation loaded early */
                 hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_MID, R, (R == TILE_ROWS ? 2 : 1)>),
                                    dim3((unsigned)((end + 1) / 2)), blk, lds, s, sg, nb, a);
             else if (var == MV_MID) hipLaunchKernelGGL((k_mv_packed_seg<DT_Q8_0, MV_MID, R>), g, blk, lds, s, sg, nb, a);
