@@ -541,6 +541,24 @@ __device__ XLds wave_stage(int kind, const uint8_t *__restrict__ act, int nb, ui
     return xlds_at(kind, nb, area_g);
 }
 
+/* The wave-private activation copy of wave_stage, issued as direct-to-LDS
+ * loads (no registers held): a group can put it in flight before anything
+ * else and find it landed when its weights arrive.  Returns false (nothing
+ * issued) for an activation of more than 5 16-byte pieces per lane. */
+__device__ __forceinline__ bool wave_stage_issue(int kind, const uint8_t *__restrict__ act, int nb, uint8_t *area_g) {
+    const int lane = threadIdx.x & 63;
+    const int n16 = (int)((stage_bytes(kind, nb) + 15) / 16);
+    if (n16 > 64 * 5) return false;
+#pragma unroll
+    for (int j = 0; j < 5; j++) {
+        const int c = lane + 64 * j;
+        if (c < n16)
+            __builtin_amdgcn_global_load_lds((const void *)(act + (size_t)c * 16),
+                                             (LAS void *)(area_g + 64 * 16 * j), 16, 0, 0);
+    }
+    return true;
+}
+
 /* ======================================================================
  * K2: route + gate/up + SwiGLU
  * grid: k * de/16 expert tiles (rank-major), then ds/16 shared tiles
@@ -548,7 +566,8 @@ __device__ XLds wave_stage(int kind, const uint8_t *__restrict__ act, int nb, ui
  * ==================================================================== */
 template <int DT, int GR>
 __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const uint8_t *uW, const uint8_t *act,
-                            int64_t F, int64_t t, int i0, float *hh, uint8_t *lds, const ExpTabLanes &tab) {
+                            int64_t F, int64_t t, int i0, float *hh, uint8_t *lds, const ExpTabLanes &tab,
+                            bool issued = false) {
     using Fm = Packed<DT>;
     constexpr bool AFF = DT == DT_Q4_K || DT == DT_Q5_K;
     constexpr int IPL = (DT == DT_Q8_0 ? 8 : 4) * GR / TILE_ROWS;
@@ -577,7 +596,15 @@ __device__ void gateup_tile(const tlm_hip_moe_desc &d, const uint8_t *gW, const 
                 pk = g;
             };
             auto stage = [&]() {
-                if (!staged) { X = wave_stage(kind, act, nb, xarea); staged = true; }
+                if (!staged) {
+                    if (issued) {   /* landed by direct-to-LDS loads issued at the group's start */
+                        __builtin_amdgcn_s_waitcnt(0);
+                        wave_sync();
+                    } else {
+                        X = wave_stage(kind, act, nb, xarea);
+                    }
+                    staged = true;
+                }
                 return X;
             };
             run_items<DT, IPL>(nitems - base, map, stage, park);
@@ -647,6 +674,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
      * to one XCD each (ids g, g + 8, ... share the XCD and its L2, whose lines
      * hold neighbouring rows of a tile and its scale plane); ids of a last
      * incomplete run map straight */
+    /* the activation (the router's quantised xb) into each wave's copy
+     * before the slot, routing or tables are read */
+    constexpr int ekind = EDT == DT_Q8_0 ? DT_Q8_0 : DT_Q8_K;
+    const int enb = (int)(d.D / Packed<EDT>::BV);
+    const bool issued = wave_stage_issue(
+        ekind, ws + L.xe, enb, lds + ((stage_bytes(ekind, enb) + 15) & ~(size_t)15) * (threadIdx.x >> 6));
     const int g = (int)blockIdx.x, run = g / (8 * SPT), tpe = te / SPT;
     const bool whole = (run + 1) * 8 * SPT <= nexp;
     const int tau = whole ? run * 8 + g % 8 : g / SPT, part = whole ? (g / 8) % SPT : g % SPT;
@@ -656,7 +689,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         if (v < 0) return;   /* the layer went back to the caller */
         const uint8_t *base = gv.arena + (size_t)v * gv.slot_bytes;
         gateup_tile<EDT, GUR>(d, base + gv.off[0], base + gv.off[1], ws + L.xe, d.de, t, i0,
-                              (float *)(ws + L.hh) + (size_t)r * d.de, lds, tab);
+                              (float *)(ws + L.hh) + (size_t)r * d.de, lds, tab, issued);
         return;
     }
     if constexpr (MODE == GIVEN) {   /* routing and matrices given: the weight loads go out at once */
@@ -668,7 +701,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             if (w_out) w_out[q] = gv.w[q];
         }
         gateup_tile<EDT, GUR>(d, gv.p[3 * r], gv.p[3 * r + 1], ws + L.xe, d.de, t, i0,
-                              (float *)(ws + L.hh) + (size_t)r * d.de, lds, tab);
+                              (float *)(ws + L.hh) + (size_t)r * d.de, lds, tab, issued);
         return;
     }
     LAS RouteLds *R = (LAS RouteLds *)&s_route;
@@ -697,7 +730,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     }
     const int e = R->ids[r];
     float *hh = (float *)(ws + L.hh) + (size_t)r * d.de;
-    gateup_tile<EDT, GUR>(d, s_gate[e], s_up[e], ws + L.xe, d.de, t, i0, hh, lds, tab);
+    gateup_tile<EDT, GUR>(d, s_gate[e], s_up[e], ws + L.xe, d.de, t, i0, hh, lds, tab, issued);
 }
 
 /* ======================================================================
