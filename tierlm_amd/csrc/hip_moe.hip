@@ -686,7 +686,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int r = tau / tpe, t = tau - r * tpe, i0 = part * GUR;
     if constexpr (MODE == SLOTS) {   /* one load for the slot, then the weight loads */
         const int v = ((const GAS int32_t *)gv.slot)[r];
-        if (v < 0) return;   /* the layer went back to the caller */
+        if (v < 0) {   /* the layer went back to the caller; the LDS loads land first */
+            __builtin_amdgcn_s_waitcnt(0);
+            return;
+        }
         const uint8_t *base = gv.arena + (size_t)v * gv.slot_bytes;
         gateup_tile<EDT, GUR>(d, base + gv.off[0], base + gv.off[1], ws + L.xe, d.de, t, i0,
                               (float *)(ws + L.hh) + (size_t)r * d.de, lds, tab, issued);
