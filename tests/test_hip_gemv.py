@@ -148,14 +148,17 @@ def test_matvec_tiles_ranges(hip, dev, dt):
 
 @pytest.mark.parametrize("dt", INT)
 @pytest.mark.parametrize("rows,n", [(16, 256), (48, 512), (37, 768), (768, 2048), (2048, 768), (100, 4096),
-                                    (64, 8192), (4096, 8192), (4100, 2048), (16400, 512)])
+                                    (64, 8192), (4096, 8192), (4100, 2048), (16400, 512), (16400, 2048),
+                                    (16384, 4096)])
 def test_matvec_packed(hip, dev, dt, rows, n):
     """Packed tile layout == oracle, including a partial last tile and rows
     longer than one chunk of blocks (Q8_0: 128 blocks, others 64), through the
     model's launch: quarter tiles per group for few tiles, half tiles from 256
     tiles on (4100 x 2048; 4096 x 8192, the Qwen3-235B-A22B o projection's
     shape, two chunks of blocks per row for Q8_0), whole tiles from 1024
-    tiles on (16400 x 512)."""
+    tiles on (16400 x 512; for Q8_0 at 2048 columns two tiles per group, the
+    last group with one, and the activation loaded ahead of the weights; at
+    4096 columns two 64-block chunks per tile)."""
     rng = np.random.default_rng(rows * 31 + n + dt)
     W = random_code_rows(rng, dt, rows, n)
     if rows <= 64:
@@ -273,7 +276,7 @@ def test_mv_job_segments(hip, dev):
 
 def test_mv_job_one_launch_any_mix(hip, dev):
     """30 segments (more than one launch's 24): every format packed and plain,
-    the deep Q8_0 tile (2048 columns), f32 rows at an unaligned offset, a
+    the mid Q8_0 tile (2048 columns), f32 rows at an unaligned offset, a
     segment of zero rows; each equals its separate matvec bit for bit.  A
     segment with a bad dtype is NaN-filled and reported while the others run
     (tlm_matvec_rows' rule, src/lib/tlm_quant.c:1119-1127)."""
